@@ -1,0 +1,99 @@
+"""Exact sparse-attention top-k over a growing KV cache (reference certex/attention.py:1-114).
+
+KeyCache keeps one inner-product index per KV head; query head h reads KV head h // (n_heads /
+n_kv_heads). topk(q, keys, k) equals torch.topk(q @ keys.mT, k, dim=-1) with exact fp64 scores and,
+on equal scores, the lower key id first.
+"""
+
+import torch
+
+from .index import Index, _require
+
+_TILE = 128
+
+
+def _width(head_dim):
+    """The widest screening row that fits the head dimension (certex/attention.py:25-27)."""
+    return max(59, (head_dim + 5) // 64 * 64 - 5) if head_dim >= 59 else head_dim
+
+
+def _stride(n, k):
+    """An anchor stride between 1 and 16 that leaves about 16k anchor groups (attention.py:30-34)."""
+    s = n // (16 * k * _TILE)
+    return int(max(1, min(16, s)))
+
+
+def _keys(x):
+    """Keys or queries on the GPU as float16, or float32 when float16 would overflow
+    (certex/attention.py:37-41)."""
+    x = torch.as_tensor(x, device="cuda")
+    h = x.to(torch.float16)
+    return h if bool(torch.isfinite(h).all()) else x.to(torch.float32)
+
+
+class KeyCache:
+    """Exact top-k over the keys of a growing KV cache: one index per KV head (attention.py:44-106)."""
+
+    def __init__(self, n_kv_heads, head_dim, k=2048, capacity=None):
+        _require(n_kv_heads >= 1 and head_dim >= 1, "n_kv_heads and head_dim must be positive")
+        _require(1 <= k <= 2048, f"k must be between 1 and 2048, not {k}")
+        self.n_kv_heads, self.head_dim, self.k, self.capacity = int(n_kv_heads), int(head_dim), int(k), capacity
+        self.heads, self.dtype = None, None
+        self.size = 0
+
+    def append(self, keys):
+        """Append keys of shape (n_kv_heads, n, head_dim); ids continue from the keys before."""
+        K = _keys(keys)
+        _require(
+            K.ndim == 3 and K.shape[0] == self.n_kv_heads and K.shape[2] == self.head_dim,
+            f"keys must have shape ({self.n_kv_heads}, n, {self.head_dim}), not {tuple(K.shape)}",
+        )
+        if self.heads is None:
+            self.dtype = K.dtype
+            n = max(K.shape[1], int(self.capacity or 0))
+            self.heads = [
+                Index(
+                    self.head_dim,
+                    metric="ip",
+                    width=_width(self.head_dim),
+                    storage="device",
+                    capacity=self.capacity,
+                    anchor_stride=_stride(n, self.k),
+                )
+                for _ in range(self.n_kv_heads)
+            ]
+        for g, idx in enumerate(self.heads):
+            idx.add(K[g].to(self.dtype).contiguous())
+        self.size += K.shape[1]
+        return self
+
+    def topk(self, q, k=None, batch=2048):
+        """The exact top k keys of every query: q (n_heads, m, head_dim) or (n_heads, head_dim);
+        returns (scores, ids) of shape (n_heads, m, k) or (n_heads, k)."""
+        _require(self.heads is not None, "the cache is empty: append keys first")
+        k = self.k if k is None else int(k)
+        _require(1 <= k <= min(2048, self.size), f"k must be between 1 and {min(2048, self.size)}, not {k}")
+        Q = _keys(q)
+        single = Q.ndim == 2
+        if single:
+            Q = Q[:, None, :]
+        _require(
+            Q.ndim == 3 and Q.shape[2] == self.head_dim and Q.shape[0] % self.n_kv_heads == 0,
+            f"queries must have shape (n_heads, m, {self.head_dim}) with n_heads a multiple of {self.n_kv_heads}",
+        )
+        H, m, d = Q.shape
+        r = H // self.n_kv_heads
+        scores = torch.empty((H, m, k), dtype=torch.float32, device="cuda")
+        ids = torch.empty((H, m, k), dtype=torch.int64, device="cuda")
+        for g, idx in enumerate(self.heads):
+            D, I = idx.search(Q[g * r : (g + 1) * r].reshape(r * m, d).to(self.dtype), k=k, batch=batch)
+            scores[g * r : (g + 1) * r] = D.reshape(r, m, k)
+            ids[g * r : (g + 1) * r] = I.reshape(r, m, k)
+        return (scores[:, 0], ids[:, 0]) if single else (scores, ids)
+
+
+def topk(q, keys, k):
+    """The exact top k keys of every query in one call (certex/attention.py:109-114)."""
+    K = torch.as_tensor(keys)
+    _require(K.ndim == 3, "keys must have shape (n_kv_heads, n, head_dim)")
+    return KeyCache(K.shape[0], K.shape[2], k=k).append(K).topk(q, k)

@@ -1,0 +1,576 @@
+// Host orchestration of the exact k-NN index (MI355X build).
+//
+// Reference: cpp/src/neighbors/certex/certex.cu (build_from 641-703, extend_from 705-732,
+// remove 803-843, search_batch 885-1402, search_one_batch 1404-1443, search 1460-1508,
+// set_labels 1815-1840, index ctor / reserve 1844-1936). The pipeline of one batch here:
+//   encode queries -> anchor pass (int8 MFMA, best screen value per anchor group) -> threshold
+//   (k-th best group) -> screen (int8 MFMA, survivors into per-query buckets) -> one host read of
+//   the largest bucket (re-run with larger buckets on overflow, as the reference re-runs on
+//   segment overflow) -> fp64 exact scores and top-k by (score, id) -> output conversion.
+
+#include "certex_state.hpp"
+
+#include <algorithm>
+#include <functional>
+#include <new>
+
+namespace cuvs {
+
+resources::resources(void* stream) : s_(std::make_unique<detail::resources_state>())
+{
+  CERTEX_HIP_TRY(hipGetDevice(&s_->device));
+  if (stream != nullptr) {
+    s_->stream = static_cast<hipStream_t>(stream);
+  } else {
+    CERTEX_HIP_TRY(hipStreamCreateWithFlags(&s_->stream, hipStreamNonBlocking));
+    s_->owns_stream = true;
+  }
+  CERTEX_HIP_TRY(hipHostMalloc(&s_->host_small, 64, hipHostMallocDefault));
+}
+
+resources::~resources()
+{
+  if (s_) {
+    (void)hipStreamSynchronize(s_->stream);
+    for (auto& b : s_->slots) { b.release(); }
+    if (s_->host_small) { (void)hipHostFree(s_->host_small); }
+    if (s_->owns_stream) { (void)hipStreamDestroy(s_->stream); }
+  }
+}
+
+auto resources::stream() const -> void* { return s_->stream; }
+
+void resources::set_stream(void* stream)
+{
+  CERTEX_HIP_TRY(hipStreamSynchronize(s_->stream));
+  if (s_->owns_stream) {
+    CERTEX_HIP_TRY(hipStreamDestroy(s_->stream));
+    s_->owns_stream = false;
+  }
+  s_->stream = static_cast<hipStream_t>(stream);
+}
+
+auto resources::device() const -> int { return s_->device; }
+
+void resources::sync() const { CERTEX_HIP_TRY(hipStreamSynchronize(s_->stream)); }
+
+auto resources::state() const -> detail::resources_state& { return *s_; }
+
+}  // namespace cuvs
+
+namespace cuvs::neighbors::certex {
+
+namespace {
+
+thread_local bool t_stats_on = false;
+thread_local search_stats t_stats{};
+
+/** Event pairs around the kernels of the calling thread's searches while timing is on. */
+struct timing_state {
+  bool on = false;
+  struct mark {
+    int phase;
+    hipEvent_t start, stop;
+  };
+  std::vector<mark> marks;
+  std::vector<hipEvent_t> pool;
+  auto event() -> hipEvent_t
+  {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e;
+    CERTEX_HIP_TRY(hipEventCreate(&e));
+    return e;
+  }
+};
+thread_local timing_state t_timing;
+
+/** Run `launch` between two events of `phase` when timing is on. */
+template <typename F>
+void timed(int phase, hipStream_t stream, F&& launch)
+{
+  if (!t_timing.on) {
+    launch();
+    return;
+  }
+  hipEvent_t a = t_timing.event(), b = t_timing.event();
+  CERTEX_HIP_TRY(hipEventRecord(a, stream));
+  launch();
+  CERTEX_HIP_TRY(hipEventRecord(b, stream));
+  t_timing.marks.push_back({phase, a, b});
+}
+
+using certex_amd::metric_kind;
+using detail::index_state;
+using detail::vtype;
+
+auto to_kind(cuvs::distance::DistanceType m) -> metric_kind
+{
+  switch (m) {
+    case cuvs::distance::DistanceType::L2Expanded: return metric_kind::l2;
+    case cuvs::distance::DistanceType::InnerProduct: return metric_kind::inner;
+    case cuvs::distance::DistanceType::CosineExpanded: return metric_kind::cosine;
+  }
+  throw std::invalid_argument("certex supports L2Expanded, InnerProduct, and CosineExpanded");
+}
+
+auto is_int(vtype t) -> bool { return t == vtype::i8 || t == vtype::u8; }
+
+auto round_up(int64_t v, int64_t m) -> int64_t { return (v + m - 1) / m * m; }
+
+/** Grow the row arrays of an integer index to `cap` rows (the caller holds the writer lock). */
+void grow_int(cuvs::resources const& res, index_state& st, int64_t cap)
+{
+  if (cap <= st.capacity) { return; }
+  hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  cuvs::detail::device_buffer codes(size_t(cap) * st.row_bytes);
+  cuvs::detail::device_buffer rowc(size_t(cap) * sizeof(int32_t));
+  cuvs::detail::device_buffer labels;
+  if (st.size > 0) {
+    CERTEX_HIP_TRY(hipMemcpyAsync(codes.p, st.codes.p, size_t(st.size) * st.row_bytes,
+                                  hipMemcpyDeviceToDevice, stream));
+    CERTEX_HIP_TRY(hipMemcpyAsync(rowc.p, st.rowc.p, size_t(st.size) * sizeof(int32_t),
+                                  hipMemcpyDeviceToDevice, stream));
+  }
+  if (st.has_labels) {
+    labels.resize_discard(size_t(cap) * sizeof(int32_t));
+    certex_amd::fill_i32(labels.as<int32_t>(), cap, -1, stream);
+    if (st.size > 0) {
+      CERTEX_HIP_TRY(hipMemcpyAsync(labels.p, st.labels.p, size_t(st.size) * sizeof(int32_t),
+                                    hipMemcpyDeviceToDevice, stream));
+    }
+  }
+  CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  {
+    // searches in flight on other streams may still read the old arrays
+    std::unique_lock lk(st.rw);
+    CERTEX_HIP_TRY(hipDeviceSynchronize());
+    st.codes    = std::move(codes);
+    st.rowc     = std::move(rowc);
+    if (st.has_labels) { st.labels = std::move(labels); }
+    st.capacity = cap;
+  }
+}
+
+/** Encode rows [0, n) of a device or host matrix into stored rows first .. first + n - 1. */
+void append_int(cuvs::resources const& res, index_state& st, const uint8_t* x, int64_t n,
+                bool on_device, int64_t first)
+{
+  hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  const uint8_t flip = st.type == vtype::u8 ? 0x80 : 0;
+  if (on_device) {
+    certex_amd::encode_rows_i8(x, n, st.dim, st.row_bytes, flip, st.metric,
+                               st.codes.as<int8_t>() + first * st.row_bytes,
+                               st.rowc.as<int32_t>() + first, stream);
+    return;
+  }
+  // host rows: staged through device memory in chunks of at most 64 MB
+  const int64_t chunk = std::max<int64_t>(1, (int64_t(64) << 20) / std::max<int64_t>(1, st.dim));
+  cuvs::detail::device_buffer staging(size_t(std::min(chunk, n)) * st.dim);
+  for (int64_t r = 0; r < n; r += chunk) {
+    const int64_t m = std::min(chunk, n - r);
+    CERTEX_HIP_TRY(hipMemcpyAsync(staging.p, x + r * st.dim, size_t(m) * st.dim,
+                                  hipMemcpyHostToDevice, stream));
+    certex_amd::encode_rows_i8(staging.as<uint8_t>(), m, st.dim, st.row_bytes, flip, st.metric,
+                               st.codes.as<int8_t>() + (first + r) * st.row_bytes,
+                               st.rowc.as<int32_t>() + first + r, stream);
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  }
+}
+
+template <typename T>
+void check_type_supported(index_state const& st)
+{
+  if (!is_int(st.type)) {
+    throw std::invalid_argument(
+      "certex: float32 and float16 vectors are not supported by this build yet (int8 and uint8 "
+      "are)");
+  }
+}
+
+/** One batch of queries of an integer index (the caller holds the shared lock). */
+void search_batch_int(cuvs::resources const& res, index_state const& st, const uint8_t* queries,
+                      int64_t B, int k, int64_t q0, int64_t* neighbors, float* distances,
+                      certex_amd::filter_args fa)
+{
+  auto& rs           = res.state();
+  hipStream_t stream = rs.stream;
+  const int64_t size = st.size;
+  const int64_t nq_pad = round_up(B, certex_amd::kBlockQ);
+  const uint8_t flip   = st.type == vtype::u8 ? 0x80 : 0;
+  fa.q0                = q0;
+
+  auto* qcodes = static_cast<int8_t*>(rs.get(cuvs::detail::ws_qcodes, size_t(nq_pad) * st.row_bytes));
+  certex_amd::encode_queries_i8(queries, B, nq_pad, st.dim, st.row_bytes, flip, qcodes, stream);
+
+  // anchor pass: every anchor_stride-th stored row; the best screen value of every group of
+  // group_steps * 64 anchors, then the k-th best group is the threshold of the query
+  const int s            = std::max(1, st.anchor_stride);
+  const int64_t n_anchor = (size + s - 1) / s;
+  const int64_t a_steps  = certex_amd::screen_steps(n_anchor);
+  int64_t g              = std::max<int64_t>(1, a_steps / (64 * int64_t(k)));
+  while (nq_pad * ((a_steps + g - 1) / g) * 4 > (int64_t(1) << 30)) { g *= 2; }
+  const int64_t n_groups = (a_steps + g - 1) / g;
+
+  certex_amd::screen_args sa{};
+  sa.codes     = st.codes.as<int8_t>();
+  sa.rowc      = st.rowc.as<int32_t>();
+  sa.row_bytes = st.row_bytes;
+  sa.qcodes    = qcodes;
+  sa.nq        = B;
+  sa.nq_pad    = nq_pad;
+  sa.filter    = fa;
+
+  auto* theta = static_cast<int32_t*>(rs.get(cuvs::detail::ws_theta, size_t(nq_pad) * 4));
+  bool all_rows = n_groups < k;
+  if (!all_rows) {
+    auto* gmax = static_cast<int32_t*>(
+      rs.get(cuvs::detail::ws_gmax, size_t(nq_pad) * size_t(n_groups) * 4));
+    certex_amd::screen_args aa = sa;
+    aa.n_scan                  = n_anchor;
+    aa.row_stride              = s;
+    aa.chunk_steps             = int(g * std::max<int64_t>(1, 64 / g));
+    aa.gmax                    = gmax;
+    aa.n_groups                = n_groups;
+    aa.group_steps             = int(g);
+    timed(0, stream, [&] { certex_amd::anchors_i8(aa, stream); });
+    timed(1, stream,
+          [&] { certex_amd::threshold_i8(gmax, n_groups, B, nq_pad, k, theta, stream); });
+  }
+
+  auto* small = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_small, 64));
+  auto* count = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_count, size_t(nq_pad) * 4));
+  int64_t cap = rs.bucket_cap;
+  // a bucket larger than this holds a sizeable part of the index: score every row instead
+  const int64_t all_rows_above = std::max<int64_t>(1 << 16, size / 8);
+  uint32_t* rows               = nullptr;
+  while (!all_rows) {
+    if (size_t(nq_pad) * size_t(cap) * 4 > (size_t(1) << 32)) { throw batch_too_large(); }
+    rows = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_rows, size_t(nq_pad) * size_t(cap) * 4));
+    certex_amd::fill_u32(count, nq_pad, 0, stream);
+    sa.n_scan      = size;
+    sa.row_stride  = 1;
+    sa.theta       = theta;
+    sa.chunk_steps = 64;
+    sa.cand_count  = count;
+    sa.cand_rows   = rows;
+    sa.cap         = cap;
+    timed(2, stream, [&] { certex_amd::screen_i8(sa, stream); });
+    certex_amd::fill_u32(small, 1, 0, stream);
+    certex_amd::max_u32(count, B, small, stream);
+    CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, small, 4, hipMemcpyDeviceToHost, stream));
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+    const int64_t worst = *static_cast<uint32_t*>(rs.host_small);
+    if (worst <= cap) { break; }
+    if (worst > all_rows_above) {
+      all_rows = true;
+      break;
+    }
+    int64_t c = 1024;
+    while (c < worst) { c *= 2; }
+    cap           = c;
+    rs.bucket_cap = c;
+  }
+
+  if (t_stats_on) {
+    auto* sums = reinterpret_cast<unsigned long long*>(small + 4);
+    t_stats.queries += B;
+    if (all_rows) {
+      const int64_t live = size - st.n_removed;
+      t_stats.survivors += B * live;
+      t_stats.verified += B * live;
+    } else {
+      certex_amd::fill_u32(small + 4, 4, 0, stream);
+      certex_amd::sum_u32(count, B, int64_t(1) << 40, sums, stream);
+      certex_amd::sum_u32(count, B, cap, sums + 1, stream);
+      CERTEX_HIP_TRY(
+        hipMemcpyAsync(rs.host_small, sums, 16, hipMemcpyDeviceToHost, stream));
+      CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+      auto* h = static_cast<unsigned long long*>(rs.host_small);
+      t_stats.survivors += int64_t(h[0]);
+      t_stats.verified += int64_t(h[1]);
+    }
+  }
+
+  auto* best_score =
+    static_cast<double*>(rs.get(cuvs::detail::ws_best_score, size_t(B) * k * sizeof(double)));
+  auto* best_row =
+    static_cast<int64_t*>(rs.get(cuvs::detail::ws_best_row, size_t(B) * k * sizeof(int64_t)));
+  certex_amd::verify_args va{};
+  va.cand_count = count;
+  va.cand_rows  = rows;
+  va.cap        = cap;
+  va.all_rows   = all_rows;
+  va.n_rows     = size;
+  va.codes      = st.codes.as<int8_t>();
+  va.rowc       = st.rowc.as<int32_t>();
+  va.row_bytes  = st.row_bytes;
+  va.dim        = st.dim;
+  va.flip       = flip;
+  va.qcodes     = qcodes;
+  va.metric     = st.metric;
+  va.filter     = fa;
+  va.nq         = B;
+  va.k          = k;
+  va.best_score = best_score;
+  va.best_row   = best_row;
+  timed(3, stream, [&] { certex_amd::verify_topk_i8(va, stream); });
+  certex_amd::finish(best_score, best_row, B, k, st.metric, distances, neighbors, stream);
+}
+
+template <typename T>
+void search_impl(cuvs::resources const& res, search_params const& params, index<T> const& idx,
+                 matrix_view<const T> queries, int64_t* neighbors, float* distances, int64_t k,
+                 certex_amd::filter_args fa)
+{
+  index_state const& st = idx.state();
+  expects(queries.on_device, "certex: the queries must be in device memory");
+  expects(queries.cols == st.dim, "dimension mismatch");
+  expects(k >= 1 && k <= 2048, "certex returns at most 2048 neighbors per query");
+  expects(st.size >= k, "the index holds fewer than k vectors");
+  check_type_supported<T>(st);
+  const int64_t nq = queries.rows;
+  if (nq == 0) { return; }
+  if (t_stats_on) { res.sync(); }
+  const int64_t bs = std::max(1, params.batch_size);
+  std::function<void(int64_t, int64_t)> run = [&](int64_t b0, int64_t B) {
+    try {
+      search_batch_int(res, st, reinterpret_cast<const uint8_t*>(queries.data) + b0 * st.dim, B,
+                       int(k), b0, neighbors + b0 * k, distances + b0 * k, fa);
+    } catch (batch_too_large const&) {
+      if (B < 2) { throw; }
+      run(b0, B / 2);
+      run(b0 + B / 2, B - B / 2);
+    } catch (std::bad_alloc const&) {
+      if (B < 2) { throw; }
+      res.sync();
+      run(b0, B / 2);
+      run(b0 + B / 2, B - B / 2);
+    }
+  };
+  for (int64_t b0 = 0; b0 < nq; b0 += bs) {
+    std::shared_lock batch_view(st.rw);  // the rows of this batch stay fixed during updates
+    run(b0, std::min(bs, nq - b0));
+  }
+}
+
+}  // namespace
+
+void stats_begin()
+{
+  t_stats_on = true;
+  t_stats    = {};
+}
+
+auto stats_end() -> search_stats
+{
+  t_stats_on = false;
+  return t_stats;
+}
+
+void timing_begin()
+{
+  t_timing.on = true;
+  for (auto& m : t_timing.marks) {
+    t_timing.pool.push_back(m.start);
+    t_timing.pool.push_back(m.stop);
+  }
+  t_timing.marks.clear();
+}
+
+auto timing_end() -> kernel_times
+{
+  kernel_times out;
+  t_timing.on = false;
+  for (auto& m : t_timing.marks) {
+    CERTEX_HIP_TRY(hipEventSynchronize(m.stop));
+    float ms = 0;
+    CERTEX_HIP_TRY(hipEventElapsedTime(&ms, m.start, m.stop));
+    out.ms[m.phase] += ms;
+    out.launches[m.phase] += 1;
+    t_timing.pool.push_back(m.start);
+    t_timing.pool.push_back(m.stop);
+  }
+  t_timing.marks.clear();
+  return out;
+}
+
+template <typename T>
+index<T>::index(cuvs::resources const& res) : s_(std::make_unique<index_state>())
+{
+  s_->device = res.device();
+  s_->type   = detail::vtype_of<T>();
+}
+template <typename T>
+index<T>::index(index&&) noexcept = default;
+template <typename T>
+index<T>& index<T>::operator=(index&&) noexcept = default;
+template <typename T>
+index<T>::~index() = default;
+
+template <typename T>
+auto index<T>::size() const noexcept -> int64_t { return s_->size; }
+template <typename T>
+auto index<T>::dim() const noexcept -> int64_t { return s_->dim; }
+template <typename T>
+auto index<T>::capacity() const noexcept -> int64_t { return s_->capacity; }
+template <typename T>
+auto index<T>::n_removed() const noexcept -> int64_t { return s_->n_removed; }
+template <typename T>
+auto index<T>::width() const noexcept -> int { return s_->width; }
+template <typename T>
+auto index<T>::anchor_stride() const noexcept -> int { return s_->anchor_stride; }
+template <typename T>
+auto index<T>::metric() const noexcept -> cuvs::distance::DistanceType { return s_->dmetric; }
+template <typename T>
+auto index<T>::has_labels() const noexcept -> bool { return s_->has_labels; }
+template <typename T>
+auto index<T>::host_vectors() const noexcept -> bool { return s_->host_vectors; }
+template <typename T>
+auto index<T>::state() const -> detail::index_state& { return *s_; }
+
+template <typename T>
+auto build(cuvs::resources const& res, index_params const& params, matrix_view<const T> dataset)
+  -> index<T>
+{
+  index<T> out(res);
+  index_state& st = out.state();
+  st.metric       = to_kind(params.metric);
+  st.dmetric      = params.metric;
+  expects(!(st.metric == metric_kind::cosine && is_int(st.type)),
+          "certex: cosine distance needs float32 or float16 vectors");
+  expects(dataset.rows >= 1 && dataset.cols >= 1, "certex: the dataset is empty");
+  expects(params.anchor_stride >= 1, "certex: anchor_stride must be at least 1");
+  check_type_supported<T>(st);
+  expects(dataset.cols <= certex_amd::kMaxIntDim,
+          "certex: integer vectors of more than 256 coordinates are not supported by this build");
+  st.params        = params;
+  st.dim           = dataset.cols;
+  st.row_bytes     = certex_amd::int_row_bytes(st.dim);
+  st.width         = int(st.dim);
+  st.anchor_stride = params.anchor_stride;
+  st.host_vectors  = params.host_vectors;
+  std::lock_guard w(st.writer);
+  grow_int(res, st, dataset.rows);
+  append_int(res, st, reinterpret_cast<const uint8_t*>(dataset.data), dataset.rows,
+             dataset.on_device, 0);
+  res.sync();
+  st.size = dataset.rows;
+  return out;
+}
+
+template <typename T>
+void extend(cuvs::resources const& res, matrix_view<const T> new_vectors, index<T>* idx)
+{
+  index_state& st = idx->state();
+  expects(new_vectors.cols == st.dim, "dimension mismatch");
+  if (new_vectors.rows == 0) { return; }
+  std::lock_guard w(st.writer);
+  const int64_t need = st.size + new_vectors.rows;
+  if (need > st.capacity) { grow_int(res, st, std::max(need, 2 * st.capacity)); }
+  append_int(res, st, reinterpret_cast<const uint8_t*>(new_vectors.data), new_vectors.rows,
+             new_vectors.on_device, st.size);
+  res.sync();
+  std::unique_lock publish(st.rw);
+  st.size = need;
+}
+
+template <typename T>
+void reserve(cuvs::resources const& res, int64_t capacity, index<T>* idx)
+{
+  index_state& st = idx->state();
+  std::lock_guard w(st.writer);
+  grow_int(res, st, capacity);
+}
+
+template <typename T>
+void remove(cuvs::resources const& res, const int64_t* ids, int64_t n_ids, index<T>* idx)
+{
+  index_state& st = idx->state();
+  if (n_ids == 0) { return; }
+  std::lock_guard w(st.writer);
+  auto& rs           = res.state();
+  hipStream_t stream = rs.stream;
+  auto* counter      = static_cast<unsigned long long*>(rs.get(cuvs::detail::ws_small, 64));
+  std::unique_lock publish(st.rw);
+  CERTEX_HIP_TRY(hipDeviceSynchronize());
+  certex_amd::fill_u32(reinterpret_cast<uint32_t*>(counter), 2, 0, stream);
+  certex_amd::remove_rows_i8(ids, n_ids, st.size, st.rowc.as<int32_t>(), counter, stream);
+  CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, counter, 8, hipMemcpyDeviceToHost, stream));
+  CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  st.n_removed += int64_t(*static_cast<unsigned long long*>(rs.host_small));
+}
+
+template <typename T>
+void set_labels(cuvs::resources const& res, const int32_t* labels, int64_t n, index<T>* idx,
+                int64_t first)
+{
+  index_state& st = idx->state();
+  expects(first >= 0 && first + n <= st.size, "certex: labels beyond the vectors of the index");
+  std::lock_guard w(st.writer);
+  hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  std::unique_lock publish(st.rw);
+  if (!st.has_labels) {
+    CERTEX_HIP_TRY(hipDeviceSynchronize());
+    st.labels.resize_discard(size_t(std::max<int64_t>(st.capacity, 1)) * sizeof(int32_t));
+    certex_amd::fill_i32(st.labels.as<int32_t>(), st.capacity, -1, stream);
+    st.has_labels = true;
+  }
+  if (n > 0) {
+    CERTEX_HIP_TRY(hipMemcpyAsync(st.labels.as<int32_t>() + first, labels,
+                                  size_t(n) * sizeof(int32_t), hipMemcpyDeviceToDevice, stream));
+  }
+  CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+}
+
+template <typename T>
+void search(cuvs::resources const& res, search_params const& params, index<T> const& idx,
+            matrix_view<const T> queries, int64_t* neighbors, float* distances, int64_t k,
+            filter f)
+{
+  certex_amd::filter_args fa{};
+  if (f.type != filter::kind::none) {
+    expects(f.words != nullptr, "certex: a filter needs its words");
+    fa.kind      = f.type == filter::kind::bitset ? 1 : 2;
+    fa.words     = f.words;
+    fa.bitmap_ld = idx.size();
+  }
+  search_impl(res, params, idx, queries, neighbors, distances, k, fa);
+}
+
+template <typename T>
+void search(cuvs::resources const& res, search_params const& params, index<T> const& idx,
+            matrix_view<const T> queries, const int32_t* query_labels, int64_t* neighbors,
+            float* distances, int64_t k)
+{
+  expects(idx.has_labels(), "certex: the index has no labels");
+  certex_amd::filter_args fa{};
+  fa.kind         = 3;
+  fa.row_labels   = idx.state().labels.template as<int32_t>();
+  fa.query_labels = query_labels;
+  search_impl(res, params, idx, queries, neighbors, distances, k, fa);
+}
+
+#define CERTEX_INSTANTIATE(T)                                                                  \
+  template class index<T>;                                                                     \
+  template auto build<T>(cuvs::resources const&, index_params const&, matrix_view<const T>)    \
+    -> index<T>;                                                                               \
+  template void extend<T>(cuvs::resources const&, matrix_view<const T>, index<T>*);            \
+  template void reserve<T>(cuvs::resources const&, int64_t, index<T>*);                        \
+  template void remove<T>(cuvs::resources const&, const int64_t*, int64_t, index<T>*);         \
+  template void set_labels<T>(cuvs::resources const&, const int32_t*, int64_t, index<T>*,      \
+                              int64_t);                                                        \
+  template void search<T>(cuvs::resources const&, search_params const&, index<T> const&,       \
+                          matrix_view<const T>, int64_t*, float*, int64_t, filter);            \
+  template void search<T>(cuvs::resources const&, search_params const&, index<T> const&,       \
+                          matrix_view<const T>, const int32_t*, int64_t*, float*, int64_t);
+
+CERTEX_INSTANTIATE(float)
+CERTEX_INSTANTIATE(half_t)
+CERTEX_INSTANTIATE(int8_t)
+CERTEX_INSTANTIATE(uint8_t)
+
+}  // namespace cuvs::neighbors::certex

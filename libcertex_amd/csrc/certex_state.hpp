@@ -1,0 +1,163 @@
+// Internal state of the resources and of an index, shared by the C++ API and the C API.
+#pragma once
+
+#include <cuvs/neighbors/certex.hpp>
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <mutex>
+#include <shared_mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+
+#define CERTEX_HIP_TRY(call)                                                              \
+  do {                                                                                    \
+    const hipError_t e_ = (call);                                                         \
+    if (e_ != hipSuccess) {                                                               \
+      throw std::runtime_error(std::string("certex: HIP error: ") + hipGetErrorString(e_) + \
+                               " at " #call);                                             \
+    }                                                                                     \
+  } while (0)
+
+namespace cuvs::neighbors::certex {
+
+/** Thrown when a batch needs more scratch memory than allowed; the search halves the batch. */
+struct batch_too_large : std::runtime_error {
+  batch_too_large() : std::runtime_error("certex: the batch does not fit the scratch memory") {}
+};
+
+inline void expects(bool ok, const char* message)
+{
+  if (!ok) { throw std::invalid_argument(message); }
+}
+
+}  // namespace cuvs::neighbors::certex
+
+namespace cuvs::detail {
+
+/** Owned device memory. */
+struct device_buffer {
+  void* p      = nullptr;
+  size_t bytes = 0;
+  device_buffer() = default;
+  explicit device_buffer(size_t n) { resize_discard(n); }
+  device_buffer(device_buffer const&)            = delete;
+  device_buffer& operator=(device_buffer const&) = delete;
+  device_buffer(device_buffer&& o) noexcept : p(o.p), bytes(o.bytes)
+  {
+    o.p     = nullptr;
+    o.bytes = 0;
+  }
+  device_buffer& operator=(device_buffer&& o) noexcept
+  {
+    std::swap(p, o.p);
+    std::swap(bytes, o.bytes);
+    return *this;
+  }
+  ~device_buffer() { release(); }
+  void release()
+  {
+    if (p != nullptr) { (void)hipFree(p); }
+    p     = nullptr;
+    bytes = 0;
+  }
+  /** Reallocate to n bytes (contents lost). */
+  void resize_discard(size_t n)
+  {
+    release();
+    if (n > 0) {
+      const hipError_t e = hipMalloc(&p, n);
+      if (e != hipSuccess) {
+        (void)hipGetLastError();
+        p = nullptr;
+        throw std::bad_alloc();
+      }
+      bytes = n;
+    }
+  }
+  template <typename U>
+  U* as() const
+  {
+    return static_cast<U*>(p);
+  }
+};
+
+/** Slots of the scratch memory of a search. */
+enum ws_slot : int {
+  ws_qcodes = 0,
+  ws_gmax,
+  ws_theta,
+  ws_count,
+  ws_rows,
+  ws_small,
+  ws_best_score,
+  ws_best_row,
+  ws_staging,
+  ws_n_slots
+};
+
+struct resources_state {
+  int device          = 0;
+  hipStream_t stream  = nullptr;
+  bool owns_stream    = false;
+  int64_t bucket_cap  = 1024;  // survivors per query kept by the last searches
+  device_buffer slots[ws_n_slots];
+  void* host_small    = nullptr;  // pinned host words for counters read back by the host
+
+  /** Scratch slot of at least `bytes` bytes (grow-only; waits for the stream before growing). */
+  void* get(int slot, size_t bytes)
+  {
+    device_buffer& b = slots[slot];
+    if (b.bytes < bytes) {
+      CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+      b.resize_discard(bytes + bytes / 4);
+    }
+    return b.p;
+  }
+};
+
+}  // namespace cuvs::detail
+
+namespace cuvs::neighbors::certex::detail {
+
+enum class vtype : int { f32 = 0, f16 = 1, i8 = 2, u8 = 3 };
+
+template <typename T>
+constexpr vtype vtype_of();
+template <>
+constexpr vtype vtype_of<float>() { return vtype::f32; }
+template <>
+constexpr vtype vtype_of<half_t>() { return vtype::f16; }
+template <>
+constexpr vtype vtype_of<int8_t>() { return vtype::i8; }
+template <>
+constexpr vtype vtype_of<uint8_t>() { return vtype::u8; }
+
+struct index_state {
+  int device                            = 0;
+  vtype type                            = vtype::f32;
+  cuvs::distance::DistanceType dmetric  = cuvs::distance::DistanceType::L2Expanded;
+  certex_amd::metric_kind metric        = certex_amd::metric_kind::l2;
+  int64_t dim                           = 0;
+  int64_t size                          = 0;
+  int64_t capacity                      = 0;
+  int64_t n_removed                     = 0;
+  int row_bytes                         = 0;
+  int anchor_stride                     = 16;
+  int width                             = 0;
+  bool host_vectors                     = false;
+  bool has_labels                       = false;
+  index_params params{};
+  // integer vectors: int8 codes (the vectors themselves, uint8 shifted by -128) and row terms
+  cuvs::detail::device_buffer codes;
+  cuvs::detail::device_buffer rowc;
+  cuvs::detail::device_buffer labels;
+  mutable std::shared_mutex rw;  // searches: shared per batch; publication of updates: exclusive
+  std::mutex writer;             // one update at a time
+};
+
+}  // namespace cuvs::neighbors::certex::detail

@@ -1,0 +1,152 @@
+// Launchers of the gfx950 kernels of the exact k-NN search path. Every launcher takes plain device
+// pointers, sizes and the stream to queue on; none allocates or synchronises.
+//
+// The role of each launcher in the reference pipeline (cpp/src/neighbors/certex/certex.cu:885-1402):
+//   encode_rows_i8       encode_int8_rows / encode_rows        (detail/int8.cuh:30-77)
+//   encode_queries_i8    encode_int8_queries / encode_queries  (detail/int8.cuh:84-136)
+//   screen_i8 (anchors)  anchor_groups + select_k              (detail/kernels.hpp:125-135)
+//   threshold_i8         anchor_scores + anchor_threshold      (certex_kernels.cuh:276-370)
+//   screen_i8 (screen)   screen_int8 + survivor segments       (detail/screen_int8.cu:99-292)
+//   verify_topk          survivor_keys + sort + verify_rounds  (certex_kernels.cuh:458-515,
+//                                                               detail/verify.cuh:371-487)
+//   finish               finish<S>                             (certex.cu:224-250)
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace certex_amd {
+
+/** Row term of a removed or padding row: its screen value can never reach a threshold. */
+constexpr int32_t kDeadRow = -(1 << 30);
+/** Lowest threshold: keeps every live row (a live row's screen value exceeds -2^26). */
+constexpr int32_t kKeepAll = -(1 << 29);
+/** Threshold of a padding query: keeps nothing. */
+constexpr int32_t kKeepNone = 0x7fffffff;
+
+/** Rows of one screen step and queries of one screen workgroup. */
+constexpr int kStepRows  = 64;
+constexpr int kBlockQ    = 256;
+/** Widest integer row (bytes) that the MFMA screen instantiates. */
+constexpr int kMaxIntDim = 256;
+
+enum class metric_kind : int { l2 = 0, inner = 1, cosine = 2 };
+
+/** Bytes of a stored integer screening row of `dim` coordinates (a multiple of 64). */
+__host__ __device__ inline int int_row_bytes(int64_t dim) { return int((dim + 63) / 64 * 64); }
+
+// --- encoding -------------------------------------------------------------------------------
+
+/**
+ * codes[i, :] = x[i, :] ^ flip (flip = 0x80 turns uint8 into the int8 code x - 128, 0 keeps int8),
+ * zero padded to row_bytes; rowc[i] = the row term of the screen (l2: -floor(|x'|^2 / 2); inner:
+ * 128 * sum(x') for uint8, 0 for int8). Rows first .. first + n - 1 of the stored arrays.
+ */
+void encode_rows_i8(const uint8_t* x, int64_t n, int64_t dim, int row_bytes, uint8_t flip,
+                    metric_kind metric, int8_t* codes, int32_t* rowc, hipStream_t stream);
+
+/** qcodes[i] = q[i] ^ flip, zero padded, for i < nq; padding queries [nq, nq_pad) are zero. */
+void encode_queries_i8(const uint8_t* q, int64_t nq, int64_t nq_pad, int64_t dim, int row_bytes,
+                       uint8_t flip, int8_t* qcodes, hipStream_t stream);
+
+/**
+ * Tombstone rows by id: rowc[id] = kDeadRow for 0 <= id < size; counts the ids that were live into
+ * *newly_removed (ids out of range or repeated count once at most).
+ */
+void remove_rows_i8(const int64_t* ids, int64_t n, int64_t size, int32_t* rowc,
+                    unsigned long long* newly_removed, hipStream_t stream);
+
+void fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);
+void fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream);
+
+// --- screen -------------------------------------------------------------------------------
+
+struct filter_args {
+  int kind = 0;                     // 0 none, 1 bitset over rows, 2 bitmap per query, 3 labels
+  const uint32_t* words = nullptr;  // bitset / bitmap words
+  int64_t bitmap_ld = 0;            // bits per bitmap row (= index size when built)
+  int64_t q0 = 0;                   // first query of the batch (bitmap row, label offset)
+  const int32_t* row_labels = nullptr;
+  const int32_t* query_labels = nullptr;  // of all queries of the search
+};
+
+struct screen_args {
+  const int8_t* codes;   // stored rows [*, row_bytes]
+  const int32_t* rowc;   // row terms
+  int64_t n_scan;        // scanned rows: scan index i reads stored row i * row_stride
+  int row_stride;        // 1 for the screen, the anchor stride for the anchor pass
+  int row_bytes;         // 64 KS
+  const int8_t* qcodes;  // [nq_pad, row_bytes]
+  const int32_t* theta;  // [nq_pad] (screen only)
+  int64_t nq;            // live queries
+  int64_t nq_pad;        // multiple of kBlockQ
+  int chunk_steps;       // steps of kStepRows rows per workgroup
+  filter_args filter;
+  // screen: candidate buckets
+  uint32_t* cand_count = nullptr;  // [nq_pad]
+  uint32_t* cand_rows  = nullptr;  // [nq_pad, cap]
+  int64_t cap          = 0;
+  // anchors: group maxima [nq_pad, n_groups], a group = group_steps consecutive steps
+  int32_t* gmax    = nullptr;
+  int64_t n_groups = 0;
+  int group_steps  = 1;
+};
+
+/** Steps of kStepRows rows that cover n_scan rows. */
+__host__ __device__ inline int64_t screen_steps(int64_t n_scan) { return (n_scan + kStepRows - 1) / kStepRows; }
+
+/** Int8 MFMA pass that keeps (query, row) pairs whose screen value reaches the query threshold. */
+void screen_i8(const screen_args& a, hipStream_t stream);
+
+/** Int8 MFMA pass that records the best screen value of every group of anchors for every query. */
+void anchors_i8(const screen_args& a, hipStream_t stream);
+
+/**
+ * theta[q] = the k-th largest of gmax[q, 0 .. n_groups) (kKeepAll when n_groups < k, and never
+ * below kKeepAll); padding queries q >= nq get kKeepNone.
+ */
+void threshold_i8(const int32_t* gmax, int64_t n_groups, int64_t nq, int64_t nq_pad, int k,
+                  int32_t* theta, hipStream_t stream);
+
+/** *out = max(count[0 .. n)). */
+void max_u32(const uint32_t* count, int64_t n, uint32_t* out, hipStream_t stream);
+/** *out += sum(min(count[i], cap)) over i < n (64-bit). */
+void sum_u32(const uint32_t* count, int64_t n, int64_t cap, unsigned long long* out,
+             hipStream_t stream);
+
+// --- exact re-rank and top-k -----------------------------------------------------------------
+
+struct verify_args {
+  // candidates: the bucket of each query, or every row when all_rows
+  const uint32_t* cand_count;
+  const uint32_t* cand_rows;
+  int64_t cap;
+  bool all_rows;
+  int64_t n_rows;  // rows of the index (all_rows)
+  // vectors: integer codes (int path)
+  const int8_t* codes;
+  const int32_t* rowc;  // liveness (kDeadRow) for all_rows
+  int row_bytes;
+  int64_t dim;
+  uint8_t flip;
+  const int8_t* qcodes;
+  metric_kind metric;
+  filter_args filter;  // applied to all_rows candidates
+  int64_t nq;
+  int k;
+  double* best_score;  // [nq, k], smaller is better; +inf where missing
+  int64_t* best_row;   // [nq, k], -1 where missing
+};
+
+/** fp64 exact scores of the candidates of every query and their k best by (score, row). */
+void verify_topk_i8(const verify_args& a, hipStream_t stream);
+
+/**
+ * Output conversion: distances (l2: score; inner: -score = <q, x>; cosine: score + 1 = 1 - cos)
+ * as float32, -1 / +-inf for missing entries, and row -> id.
+ */
+void finish(const double* best_score, const int64_t* best_row, int64_t nq, int k,
+            metric_kind metric, float* distances, int64_t* neighbors, hipStream_t stream);
+
+}  // namespace certex_amd

@@ -1,0 +1,348 @@
+// Threshold selection, fp64 exact re-rank, per-query top-k and output conversion (gfx950).
+//
+// Reference contracts:
+//   threshold  anchor_threshold (certex_kernels.cuh:310-370): the k-th best anchor bounds the k-th
+//              neighbour; here the k-th largest of the per-group best screen values, found by an
+//              LDS radix select over the 32-bit keys (4 passes of 8 bits).
+//   re-rank    rounds_score / warp_score (detail/verify.cuh:186-218, certex_kernels.cuh:247-273):
+//              the exact score of every survivor in fp64 from the stored vectors.
+//   top-k      rounds_merge + segmented sort (detail/verify.cuh:240-364): here the survivors of a
+//              query sit in LDS and are ordered by the total order (score, row), so ties go to the
+//              lower id, which the reference does not guarantee.
+//   finish     certex.cu:224-250.
+
+#include "../kernels.hpp"
+
+#include <climits>
+#include <cmath>
+
+namespace certex_amd {
+namespace {
+
+constexpr int kThreads = 256;
+
+/** Inclusive prefix sum over the 256 threads of a block (4 waves). */
+__device__ inline int block_scan_incl(int v, int* wave_tot)
+{
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off);
+    if (lane >= off) { incl += t; }
+  }
+  if (lane == 63) { wave_tot[wave] = incl; }
+  __syncthreads();
+  int add = 0;
+  for (int w = 0; w < wave; ++w) { add += wave_tot[w]; }
+  __syncthreads();
+  return incl + add;
+}
+
+/** Order-preserving map of a signed 32-bit value onto an unsigned key (descending value). */
+__device__ inline uint32_t desc_key(int32_t v) { return ~(uint32_t(v) ^ 0x80000000u); }
+__device__ inline int32_t desc_value(uint32_t key) { return int32_t(~key ^ 0x80000000u); }
+
+__global__ __launch_bounds__(kThreads) void threshold_kernel(
+  const int32_t* gmax, int64_t n_groups, int64_t nq, int k, int32_t* theta)
+{
+  __shared__ int hist[256];
+  __shared__ int wave_tot[4];
+  __shared__ uint32_t sel_digit;
+  __shared__ int sel_rank;
+  const int64_t q = blockIdx.x;
+  const int tid   = threadIdx.x;
+  if (q >= nq) {
+    if (tid == 0) { theta[q] = kKeepNone; }
+    return;
+  }
+  if (n_groups < k) {
+    if (tid == 0) { theta[q] = kKeepAll; }
+    return;
+  }
+  const int32_t* v = gmax + q * n_groups;
+  uint32_t prefix = 0, mask = 0;
+  int rank = k;  // 1-based rank among ascending keys
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hist[tid] = 0;
+    __syncthreads();
+    for (int64_t e = tid; e < n_groups; e += kThreads) {
+      const uint32_t key = desc_key(v[e]);
+      if ((key & mask) == prefix) { atomicAdd(&hist[(key >> shift) & 255], 1); }
+    }
+    __syncthreads();
+    const int c    = hist[tid];
+    const int incl = block_scan_incl(c, wave_tot);
+    if (incl - c < rank && rank <= incl) {
+      sel_digit = uint32_t(tid);
+      sel_rank  = rank - (incl - c);
+    }
+    __syncthreads();
+    prefix |= sel_digit << shift;
+    mask |= 255u << shift;
+    rank = sel_rank;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const int32_t t = desc_value(prefix);
+    theta[q]        = t > kKeepAll ? t : kKeepAll;
+  }
+}
+
+__global__ void max_kernel(const uint32_t* c, int64_t n, uint32_t* out)
+{
+  uint32_t m = 0;
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    m = max(m, c[i]);
+  }
+  for (int off = 32; off; off >>= 1) { m = max(m, uint32_t(__shfl_xor(int(m), off))); }
+  if ((threadIdx.x & 63) == 0) { atomicMax(out, m); }
+}
+
+__global__ void sum_kernel(const uint32_t* c, int64_t n, int64_t cap, unsigned long long* out)
+{
+  unsigned long long s = 0;
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    s += c[i] < cap ? c[i] : uint64_t(cap);
+  }
+  for (int off = 32; off; off >>= 1) {
+    s += (unsigned long long)__shfl_xor((long long)s, off);
+  }
+  if ((threadIdx.x & 63) == 0) { atomicAdd(out, s); }
+}
+
+// ---- exact scores --------------------------------------------------------------------------
+
+/** Order-preserving map of a double onto a 64-bit key (ascending); -0 maps as +0. */
+__device__ inline uint64_t score_key(double s)
+{
+  const uint64_t b = __double_as_longlong(s + 0.0);
+  return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+__device__ inline double key_score(uint64_t k)
+{
+  const uint64_t b = (k >> 63) ? (k & 0x7fffffffffffffffull) : ~k;
+  return __longlong_as_double((long long)b);
+}
+
+__device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
+{
+  switch (f.kind) {
+    case 1: return (f.words[row >> 5] >> (row & 31)) & 1u;
+    case 2: {
+      const int64_t bit = (f.q0 + q) * f.bitmap_ld + row;
+      return (f.words[bit >> 5] >> (bit & 31)) & 1u;
+    }
+    case 3: return f.row_labels[row] == f.query_labels[f.q0 + q];
+    default: return true;
+  }
+}
+
+/**
+ * fp64 score of stored integer row `row` against the query codes in LDS: the coordinates in
+ * increasing order, accumulated by fused multiply-add (exact for 8-bit integers, where every
+ * partial sum is an integer below 2^53). l2: sum (q - x)^2; inner: -sum q x.
+ */
+__device__ inline double int_score(const int8_t* qv, const int8_t* xrow, int64_t dim, int bias,
+                                   metric_kind metric)
+{
+  double acc = 0;
+  int64_t j  = 0;
+  for (; j + 4 <= dim; j += 4) {
+    const int xw = *reinterpret_cast<const int*>(xrow + j);
+    const int qw = *reinterpret_cast<const int*>(qv + j);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int xc = int(int8_t(xw >> (8 * b))), qc = int(int8_t(qw >> (8 * b)));
+      if (metric == metric_kind::l2) {
+        const double t = double(qc - xc);
+        acc            = fma(t, t, acc);
+      } else {
+        acc = fma(double(qc + bias), double(xc + bias), acc);
+      }
+    }
+  }
+  for (; j < dim; ++j) {
+    const int xc = int(xrow[j]), qc = int(qv[j]);
+    if (metric == metric_kind::l2) {
+      const double t = double(qc - xc);
+      acc            = fma(t, t, acc);
+    } else {
+      acc = fma(double(qc + bias), double(xc + bias), acc);
+    }
+  }
+  return metric == metric_kind::l2 ? acc : -acc;
+}
+
+constexpr int kBuf = 4096;  // LDS candidates per query (keys 32 KB + rows 16 KB)
+
+/** Bitonic sort of key/row pairs [0, P) in LDS by (key, row); P a power of two. */
+__device__ inline void bitonic_sort(uint64_t* key, uint32_t* row, int P)
+{
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < (P >> 1); i += kThreads) {
+        const int lo  = 2 * i - (i & (stride - 1));
+        const int hi  = lo + stride;
+        const bool up = (lo & size) == 0;
+        const uint64_t ka = key[lo], kb = key[hi];
+        const uint32_t ra = row[lo], rb = row[hi];
+        const bool greater = ka > kb || (ka == kb && ra > rb);
+        if (greater == up) {
+          key[lo] = kb;
+          key[hi] = ka;
+          row[lo] = rb;
+          row[hi] = ra;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__device__ inline int pow2_at_least(int v)
+{
+  int p = 1;
+  while (p < v) { p <<= 1; }
+  return p;
+}
+
+__global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a)
+{
+  __shared__ uint64_t key[kBuf];
+  __shared__ uint32_t rid[kBuf];
+  __shared__ __attribute__((aligned(16))) int8_t qv[kMaxIntDim];
+  __shared__ int fill;
+
+  const int64_t q = blockIdx.x;
+  const int tid   = threadIdx.x;
+  const int k     = a.k;
+  for (int j = tid; j < a.row_bytes; j += kThreads) { qv[j] = a.qcodes[q * a.row_bytes + j]; }
+  const int bias = a.flip ? 128 : 0;
+
+  const int64_t n_cand =
+    a.all_rows ? a.n_rows : (a.cand_count[q] < a.cap ? int64_t(a.cand_count[q]) : a.cap);
+  const uint32_t* cand = a.cand_rows + q * a.cap;
+
+  int have = 0;  // entries [0, have) of the buffer hold the best candidates so far
+  if (tid == 0) { fill = 0; }
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < n_cand;) {
+    // fill the buffer beyond `have` with the next candidates (compacted by an LDS counter)
+    const int room  = kBuf - have;
+    const int64_t m = n_cand - c0 < room ? n_cand - c0 : room;
+    for (int64_t e = tid; e < m; e += kThreads) {
+      uint32_t r;
+      bool live;
+      if (a.all_rows) {
+        r    = uint32_t(c0 + e);
+        live = a.rowc[r] != kDeadRow && keeps(a.filter, q, r);
+      } else {
+        r    = cand[c0 + e];
+        live = true;
+      }
+      if (live) {
+        const double s =
+          int_score(qv, a.codes + int64_t(r) * a.row_bytes, a.dim, bias, a.metric);
+        const int slot = have + atomicAdd(&fill, 1);
+        key[slot]      = score_key(s);
+        rid[slot]      = r;
+      }
+    }
+    c0 += m;
+    __syncthreads();
+    have += fill;
+    __syncthreads();
+    if (tid == 0) { fill = 0; }
+    if (c0 < n_cand && have > k) {
+      // keep the k best: sort the buffer and drop the rest
+      const int P = pow2_at_least(have);
+      for (int j = have + tid; j < P; j += kThreads) {
+        key[j] = ~0ull;
+        rid[j] = ~0u;
+      }
+      __syncthreads();
+      bitonic_sort(key, rid, P);
+      have = k;
+    }
+    __syncthreads();
+  }
+  const int P = pow2_at_least(have > 1 ? have : 1);
+  for (int j = have + tid; j < P; j += kThreads) {
+    key[j] = ~0ull;
+    rid[j] = ~0u;
+  }
+  __syncthreads();
+  bitonic_sort(key, rid, P);
+  for (int j = tid; j < k; j += kThreads) {
+    if (j < have) {
+      a.best_score[q * k + j] = key_score(key[j]);
+      a.best_row[q * k + j]   = int64_t(rid[j]);
+    } else {
+      a.best_score[q * k + j] = INFINITY;
+      a.best_row[q * k + j]   = -1;
+    }
+  }
+}
+
+__global__ void finish_kernel(const double* best_score, const int64_t* best_row, int64_t n, int k,
+                              metric_kind metric, float* distances, int64_t* neighbors)
+{
+  const int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (t >= n * k) { return; }
+  const int64_t r = best_row[t];
+  const double s  = best_score[t];
+  float d;
+  if (r < 0) {
+    d = metric == metric_kind::inner ? -INFINITY : INFINITY;
+  } else if (metric == metric_kind::inner) {
+    d = float(-s);
+  } else if (metric == metric_kind::cosine) {
+    d = float(1.0 + s);
+  } else {
+    d = float(s);
+  }
+  distances[t] = d;
+  neighbors[t] = r;
+}
+
+}  // namespace
+
+void threshold_i8(const int32_t* gmax, int64_t n_groups, int64_t nq, int64_t nq_pad, int k,
+                  int32_t* theta, hipStream_t stream)
+{
+  if (nq_pad == 0) { return; }
+  threshold_kernel<<<unsigned(nq_pad), kThreads, 0, stream>>>(gmax, n_groups, nq, k, theta);
+}
+
+void max_u32(const uint32_t* count, int64_t n, uint32_t* out, hipStream_t stream)
+{
+  const int64_t blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+  if (blocks > 0) { max_kernel<<<unsigned(blocks), 256, 0, stream>>>(count, n, out); }
+}
+
+void sum_u32(const uint32_t* count, int64_t n, int64_t cap, unsigned long long* out,
+             hipStream_t stream)
+{
+  const int64_t blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
+  if (blocks > 0) { sum_kernel<<<unsigned(blocks), 256, 0, stream>>>(count, n, cap, out); }
+}
+
+void verify_topk_i8(const verify_args& a, hipStream_t stream)
+{
+  if (a.nq == 0) { return; }
+  verify_topk_i8_kernel<<<unsigned(a.nq), kThreads, 0, stream>>>(a);
+}
+
+void finish(const double* best_score, const int64_t* best_row, int64_t nq, int k,
+            metric_kind metric, float* distances, int64_t* neighbors, hipStream_t stream)
+{
+  const int64_t n = nq * k;
+  if (n == 0) { return; }
+  finish_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(best_score, best_row, nq, k, metric,
+                                                              distances, neighbors);
+}
+
+}  // namespace certex_amd

@@ -1,0 +1,421 @@
+"""certex.Index: exact k-nearest-neighbour search on the MI355X, over the C API.
+
+Mirrors the reference's Python interface (certex/index.py:191-548): the same classes, functions,
+argument names, defaults, validation and errors. Every call goes through libcertex_c.so's
+cuvsCertex* entry points on torch's current stream; arrays are converted here and the ids are
+kept here.
+"""
+
+import ctypes
+import threading
+
+import numpy as np
+import torch
+
+from . import _capi as C
+
+METRICS = ("l2", "cosine", "ip")
+_DTYPES = {torch.float32: "float32", torch.float16: "float16", torch.int8: "int8", torch.uint8: "uint8"}
+_TORCH = {v: k for k, v in _DTYPES.items()}
+_METRIC_C = {"l2": C.L2Expanded, "cosine": C.CosineExpanded, "ip": C.InnerProduct}
+_METRIC_PY = {v: k for k, v in _METRIC_C.items()}
+_PREFIX = {b"f4": "float32", b"f2": "float16", b"i1": "int8", b"u1": "uint8"}
+
+
+def row_len(m):
+    """Halves per screening row of width m: m + 1 lifted and 4 certificate coordinates, padded to
+    64 or 128n (reference certex/index.py:46-49, certex.cu:58-62)."""
+    L = m + 5
+    return 64 if L <= 64 else 128 * ((L + 127) // 128)
+
+
+def _to_torch(x):
+    """A torch view of numpy, torch or DLPack arrays, and the kind of the input (certex/index.py:52-63)."""
+    if isinstance(x, np.ndarray):
+        return torch.from_numpy(np.ascontiguousarray(x)), "numpy"
+    if isinstance(x, torch.Tensor):
+        return x, "torch"
+    if hasattr(x, "__dlpack__"):
+        return torch.from_dlpack(x), type(x).__module__.split(".")[0]
+    return torch.from_numpy(np.ascontiguousarray(np.asarray(x))), "numpy"
+
+
+def _require(ok, message):
+    """Reject a call with a ValueError (certex/index.py:66-69)."""
+    if not ok:
+        raise ValueError(message)
+
+
+def _back(t, kind):
+    """t in the array type of an input of this kind (certex/index.py:72-84)."""
+    if kind == "numpy":
+        return t.cpu().numpy()
+    if kind == "torch":
+        return t
+    try:
+        import importlib
+
+        return importlib.import_module(kind).from_dlpack(t)
+    except (ImportError, AttributeError, TypeError):
+        return t
+
+
+def _cast(t, dtype):
+    """t in the data type of the index; non-representable values are an error (index.py:87-96)."""
+    if t.dtype == dtype:
+        return t
+    if not dtype.is_floating_point:
+        lim = torch.iinfo(dtype)
+        f = t.double()
+        if not bool(((f == f.round()) & (f >= lim.min) & (f <= lim.max)).all()):
+            raise ValueError(f"the index holds {dtype} vectors: values must be integers in [{lim.min}, {lim.max}]")
+    return t.to(dtype)
+
+
+def _pack(mask):
+    """A boolean mask, flattened row-major, as bitset words: bit j of word i is entry 32 i + j
+    (certex/index.py:99-104). Returned as int32 words on the mask's device."""
+    b = mask.reshape(-1).to(dtype=torch.int64)
+    b = torch.nn.functional.pad(b, (0, (-b.numel()) % 32)).view(-1, 32)
+    w = (b << torch.arange(32, device=b.device)).sum(1)
+    return torch.where(w >= 2**31, w - 2**32, w).to(torch.int32).contiguous()
+
+
+def auto_width(X, metric, target=0.95, sample=200_000):
+    """Smallest tile-aligned width whose principal directions capture `target` of the variance
+    (certex/index.py:107-121)."""
+    X = _to_torch(X)[0]
+    d = X.shape[1]
+    S = X[torch.randperm(X.shape[0], device=X.device)[:sample]].float()
+    if metric != "ip":
+        S = S - S.mean(0)
+    ev = torch.linalg.eigvalsh(S.double().T @ S.double()).flip(0).clamp_min(0)
+    frac = torch.cumsum(ev, 0) / ev.sum().clamp_min(1e-300)
+    for L in [64, 128] + list(range(256, 4097, 128)):
+        m = L - 5
+        if m >= d or float(frac[m - 1]) >= target:
+            return min(m, d)
+    return d
+
+
+class search_stats:
+    """Counters of the searches of the calling thread inside the block: queries, certified
+    survivors and verified exact distances (certex/index.py:171-188).
+
+        with certex.search_stats() as st:
+            index.search(q)
+        st.survivors / st.queries
+    """
+
+    def __enter__(self):
+        C.check(C.lib().cuvsCertexStatsBegin())
+        self.queries = self.survivors = self.verified = 0
+        return self
+
+    def __exit__(self, *exc):
+        torch.cuda.current_stream().synchronize()
+        q, s, v = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+        C.check(C.lib().cuvsCertexStatsEnd(ctypes.byref(q), ctypes.byref(s), ctypes.byref(v)))
+        self.queries, self.survivors, self.verified = q.value, s.value, v.value
+        return False
+
+
+class _Core:
+    """One cuvsCertexIndex handle."""
+
+    def __init__(self):
+        self.h = ctypes.POINTER(C.IndexHandle)()
+        C.check(C.lib().cuvsCertexIndexCreate(ctypes.byref(self.h)))
+
+    def __del__(self):
+        try:
+            if self.h:
+                C.lib().cuvsCertexIndexDestroy(self.h)
+                self.h = None
+        except Exception:  # interpreter shutdown
+            pass
+
+    def _get(self, fn, ctype):
+        v = ctype()
+        C.check(getattr(C.lib(), fn)(self.h, ctypes.byref(v)))
+        return v.value
+
+    @property
+    def size(self):
+        return self._get("cuvsCertexIndexGetSize", ctypes.c_int64)
+
+    @property
+    def dim(self):
+        return self._get("cuvsCertexIndexGetDim", ctypes.c_int64)
+
+    @property
+    def n_removed(self):
+        return self._get("cuvsCertexIndexGetRemoved", ctypes.c_int64)
+
+    @property
+    def capacity(self):
+        return self._get("cuvsCertexIndexGetCapacity", ctypes.c_int64)
+
+    @property
+    def width(self):
+        return self._get("cuvsCertexIndexGetWidth", ctypes.c_int32)
+
+    @property
+    def metric(self):
+        return _METRIC_PY[self._get("cuvsCertexIndexGetMetric", ctypes.c_int)]
+
+    @property
+    def anchor_stride(self):
+        return self._get("cuvsCertexIndexGetAnchorStride", ctypes.c_int32)
+
+    @property
+    def has_labels(self):
+        return self._get("cuvsCertexIndexHasLabels", ctypes.c_bool)
+
+    @property
+    def dtype(self):
+        d = self.h.contents.dtype
+        return {(C.kDLFloat, 32): "float32", (C.kDLFloat, 16): "float16", (C.kDLInt, 8): "int8", (C.kDLUInt, 8): "uint8"}[
+            (d.code, d.bits)
+        ]
+
+
+class Index:
+    """Exact k-NN index: every search returns the exact k nearest stored vectors of every query,
+    ranked by the fp64 score and, on equal scores, by the lower id (certex/index.py:191-216).
+
+    metric: "l2" (squared Euclidean distances, ascending), "ip" (inner products, descending) or
+    "cosine" (cosine similarities, descending). width, storage, capacity, anchor_stride,
+    partition_labels, n_lists, local_projections and int8_rows have the reference's meaning; they
+    change the speed or the memory, never the results.
+    """
+
+    def __init__(
+        self,
+        dim,
+        metric="l2",
+        width="auto",
+        storage="device",
+        capacity=None,
+        anchor_stride=16,
+        partition_labels=True,
+        n_lists=0,
+        local_projections=False,
+        int8_rows=False,
+    ):
+        _require(metric in METRICS, f"metric must be one of {METRICS}, not {metric!r}")
+        _require(storage in ("device", "host"), f'storage must be "device" or "host", not {storage!r}')
+        self.d, self.metric, self.width, self.storage = dim, metric, width, storage
+        self.capacity, self.anchor_stride = capacity, anchor_stride
+        self.partition_labels = partition_labels
+        self.n_lists, self.local_projections, self.int8_rows = n_lists, local_projections, int8_rows
+        self.core = None
+        self._writer = threading.Lock()
+
+    @property
+    def ntotal(self):
+        return 0 if self.core is None else int(self.core.size - self.core.n_removed)
+
+    @property
+    def dtype(self):
+        return None if self.core is None else _TORCH[self.core.dtype]
+
+    def _vectors(self, x, device):
+        t, kind = _to_torch(x)
+        if t.ndim == 1:
+            t = t.reshape(1, -1)
+        _require(
+            t.ndim == 2 and t.shape[1] == self.d,
+            f"expected vectors of dimension {self.d} (a matrix (n, {self.d}) or one vector), "
+            f"got shape {tuple(t.shape)}",
+        )
+        if device or t.is_cuda:
+            t = t.cuda()
+        if self.core is not None:
+            t = _cast(t, self.dtype)
+        elif t.dtype not in _DTYPES or (self.metric == "cosine" and not t.dtype.is_floating_point):
+            t = t.float()
+        return t.contiguous(), kind
+
+    def add(self, x, labels=None):
+        """Add vectors, optionally with one non-negative label each; returns their ids
+        (certex/index.py:266-305)."""
+        X, kind = self._vectors(x, device=False)
+        if labels is not None:
+            labels = _to_torch(labels)[0].reshape(-1).to(device="cuda", dtype=torch.int32).contiguous()
+            _require(labels.shape[0] == X.shape[0] and int(labels.min()) >= 0, "one non-negative label per vector")
+        L = C.lib()
+        with self._writer:
+            if self.core is not None and self.core.has_labels:
+                _require(labels is not None, "this index is labeled: add labels with every addition")
+            if self.core is not None and labels is not None and not self.core.has_labels:
+                raise ValueError("labels must be given from the first addition on")
+            res = C.resources()
+            if self.core is None:
+                core = _Core()
+                p = ctypes.POINTER(C.IndexParams)()
+                C.check(L.cuvsCertexIndexParamsCreate(ctypes.byref(p)))
+                try:
+                    p.contents.metric = _METRIC_C[self.metric]
+                    p.contents.width = 0 if self.width == "auto" else int(self.width)
+                    p.contents.anchor_stride = int(self.anchor_stride)
+                    p.contents.host_vectors = self.storage == "host"
+                    p.contents.n_lists = int(self.n_lists)
+                    p.contents.local_projections = bool(self.local_projections)
+                    p.contents.int8_rows = bool(self.int8_rows)
+                    x = C.Borrowed(X)
+                    C.check(L.cuvsCertexBuild(res, p, x.ptr, core.h))
+                finally:
+                    C.check(L.cuvsCertexIndexParamsDestroy(p))
+                self.core = core
+                n0 = 0
+                if self.capacity is not None and self.capacity > X.shape[0]:
+                    C.check(L.cuvsCertexReserve(res, int(self.capacity), core.h))
+            else:
+                n0 = self.core.size
+                x = C.Borrowed(X)
+                C.check(L.cuvsCertexExtend(res, x.ptr, self.core.h))
+            if labels is not None:
+                lb = C.Borrowed(labels)
+                C.check(L.cuvsCertexSetLabels(res, lb.ptr, n0, self.core.h))
+                if self.partition_labels:
+                    C.check(L.cuvsCertexPartitionByLabels(res, self.core.h))
+        ids = torch.arange(n0, n0 + X.shape[0])
+        return _back(ids, kind)
+
+    def remove(self, ids):
+        """Remove vectors by id; they never appear in later results (certex/index.py:314-319)."""
+        _require(self.core is not None, "add vectors first")
+        t = _to_torch(ids)[0].reshape(-1).to(device="cuda", dtype=torch.int64).contiguous()
+        with self._writer:
+            b = C.Borrowed(t)
+            C.check(C.lib().cuvsCertexRemove(C.resources(), b.ptr, self.core.h))
+
+    def search(self, q, k=10, batch=2048, labels=None, filter=None, anchors=128, probe_lists=2):
+        """Exact k nearest neighbours of every query: (distances or similarities, ids), best first
+        (certex/index.py:320-351)."""
+        _require(self.core is not None, "the index is empty: add vectors first")
+        single = _to_torch(q)[0].ndim == 1
+        Q, kind = self._vectors(q, device=True)
+        nq = Q.shape[0]
+        _require(1 <= k <= 2048, f"k must be between 1 and 2048, not {k}")
+        _require(k <= self.core.size, f"k = {k} exceeds the {int(self.core.size)} vectors added to the index")
+        I = torch.empty((nq, k), dtype=torch.int64, device="cuda")
+        D = torch.empty((nq, k), dtype=torch.float32, device="cuda")
+        ql = words = None
+        ftype = C.NO_FILTER
+        if labels is not None:
+            _require(self.core.has_labels, "the index has no labels")
+            ql = _to_torch(labels)[0].reshape(-1).to(device="cuda", dtype=torch.int32).contiguous()
+            _require(ql.shape[0] == nq, "one label per query")
+        if filter is not None:
+            m = _to_torch(filter)[0].to(torch.bool)
+            _require(m.shape[-1] == self.core.size, "the filter needs one entry per id")
+            _require(m.ndim == 1 or (m.ndim == 2 and m.shape[0] == nq), "a mask over the ids, or one row per query")
+            words = _pack(m.cuda())
+            ftype = C.BITSET if m.ndim == 1 else C.BITMAP
+        if nq > 0:
+            L = C.lib()
+            sp = C.SearchParams(int(anchors), int(batch), int(probe_lists))
+            qb, ib, db = C.Borrowed(Q), C.Borrowed(I), C.Borrowed(D)
+            res = C.resources()
+            if ql is not None:
+                lb = C.Borrowed(ql)
+                C.check(L.cuvsCertexSearchWithLabels(res, ctypes.byref(sp), self.core.h, qb.ptr, lb.ptr, ib.ptr, db.ptr))
+            else:
+                wb = None
+                f = C.Filter(0, C.NO_FILTER)
+                if words is not None:
+                    wb = C.Borrowed(words, dtype_override=(C.kDLUInt, 32))
+                    f = C.Filter(ctypes.addressof(wb.m), ftype)
+                C.check(L.cuvsCertexSearch(res, ctypes.byref(sp), self.core.h, qb.ptr, ib.ptr, db.ptr, f))
+                del wb
+        if self.metric == "cosine":
+            D = 1 - D
+        if single:
+            D, I = D[0], I[0]
+        return _back(D, kind), _back(I, kind)
+
+    def save(self, path):
+        """Write the index to a file (certex/index.py:361-365)."""
+        _require(self.core is not None, "add vectors first")
+        C.check(C.lib().cuvsCertexSerialize(C.resources(), str(path).encode(), self.core.h))
+
+    def info(self):
+        c = self.core
+        return {
+            "metric": self.metric,
+            "width": None if c is None else c.width,
+            "dtype": None if c is None else c.dtype,
+            "storage": self.storage,
+            "ntotal": self.ntotal,
+        }
+
+
+def search(xb, xq=None, k=10, metric="l2", **index_options):
+    """The exact k nearest neighbours in one call (certex/index.py:422-447)."""
+    X, _ = _to_torch(xb)
+    _require(X.ndim == 2, "xb must be a matrix (n, dim)")
+    index_options.setdefault("storage", "device")
+    index = Index(dim=X.shape[1], metric=metric, **index_options)
+    index.add(X)
+    D, I = index.search(xb if xq is None else xq, k=k)
+    del index
+    return D, I
+
+
+def verify(xb, xq, I, metric="l2", sample=100, seed=0):
+    """Fraction of checked queries whose returned neighbours have exactly the k best fp64 scores
+    (certex/index.py:450-548): a random sample of queries (torch generator seeded with `seed`) is
+    searched exhaustively in float64; ties count as exact whichever tied vector was returned. Runs
+    with torch on the queries' device (the GPU when available)."""
+    _require(metric in METRICS, f"metric must be one of {METRICS}, not {metric!r}")
+    X, _ = _to_torch(xb)
+    Q, _ = _to_torch(xq)
+    ids, _ = _to_torch(I)
+    if Q.ndim == 1:
+        Q, ids = Q.reshape(1, -1), ids.reshape(1, -1)
+    _require(X.ndim == 2 and Q.ndim == 2 and Q.shape[1] == X.shape[1], "xb and xq need the same dimension")
+    _require(ids.shape[0] == Q.shape[0], "one row of ids per query")
+    dev = "cuda" if torch.cuda.is_available() else "cpu"
+    nq, k = ids.shape
+    pick = (
+        torch.arange(nq)
+        if sample is None or sample >= nq
+        else torch.randperm(nq, generator=torch.Generator().manual_seed(seed))[:sample]
+    )
+    Qs = Q[pick.to(Q.device)].to(dev).double()
+    got_ids = ids[pick.to(ids.device)].to(dev).long()
+    if metric == "cosine":
+        Qs = Qs / Qs.norm(dim=1, keepdim=True)
+
+    def coarse(q, rows):
+        if metric == "l2":
+            return (q * q).sum(1, keepdim=True) + (rows * rows).sum(1)[None] - 2.0 * q @ rows.T
+        if metric == "cosine":
+            rows = rows / rows.norm(dim=1, keepdim=True)
+        return -(q @ rows.T)
+
+    def exact(cand):
+        rows = X[cand.clamp_min(0).reshape(-1).to(X.device)].to(dev).double().reshape(*cand.shape, -1)
+        if metric == "l2":
+            s = ((Qs[:, None, :] - rows) ** 2).sum(-1)
+        else:
+            if metric == "cosine":
+                rows = rows / rows.norm(dim=-1, keepdim=True)
+            s = -(rows * Qs[:, None, :]).sum(-1)
+        return torch.where(cand >= 0, s, torch.full_like(s, float("inf")))
+
+    kc = min(k + 32, X.shape[0])
+    cv = torch.full((Qs.shape[0], kc), float("inf"), dtype=torch.float64, device=dev)
+    ci = torch.full((Qs.shape[0], kc), -1, dtype=torch.int64, device=dev)
+    chunk = max(1, (1 << 28) // (8 * X.shape[1]))
+    for i in range(0, X.shape[0], chunk):
+        s = coarse(Qs, X[i : i + chunk].to(dev).double())
+        idx = torch.arange(i, i + s.shape[1], device=dev).expand(s.shape[0], -1)
+        top = torch.topk(torch.cat([cv, s], 1), kc, dim=1, largest=False)
+        cv, ci = top.values, torch.gather(torch.cat([ci, idx], 1), 1, top.indices)
+    best = exact(ci).sort(1).values[:, :k]
+    got = exact(got_ids).sort(1).values
+    tol = 1e-9 * best.abs().amax(1, keepdim=True).clamp_min(1e-30)
+    return float(((got - best).abs() <= tol).all(1).float().mean())

@@ -1,0 +1,30 @@
+"""Seeded synthetic inputs of the configurations, shared by the tests and the bench."""
+
+import numpy as np
+
+
+def gaussian(n, d, seed, dtype=np.float32):
+    """i.i.d. N(0, 1) rows (config 1 shape: 100,000 x 128 fp32, seeds 11 / 12)."""
+    return np.random.default_rng(seed).standard_normal((n, d)).astype(dtype)
+
+
+def mixture_u8(n, d=128, n_centres=1000, seed=2, centre_seed=1, sigma=20.0, hi=80.0):
+    """Descriptor-like uint8 rows (config 2): a centre drawn uniformly from n_centres centres
+    U[0, hi]^d, plus N(0, sigma^2) per coordinate, rounded half-to-even and clipped to [0, 255]."""
+    centres = np.random.default_rng(centre_seed).uniform(0.0, hi, (n_centres, d))
+    rng = np.random.default_rng(seed)
+    out = np.empty((n, d), np.uint8)
+    step = 1 << 16
+    for i in range(0, n, step):
+        m = min(step, n - i)
+        c = rng.integers(0, n_centres, m)
+        v = centres[c] + rng.standard_normal((m, d)) * sigma
+        out[i : i + m] = np.clip(np.rint(v), 0, 255).astype(np.uint8)
+    return out
+
+
+def uniform_int(n, d, seed, dtype=np.uint8, lo=None, hi=None):
+    info = np.iinfo(dtype)
+    lo = info.min if lo is None else lo
+    hi = info.max if hi is None else hi
+    return np.random.default_rng(seed).integers(lo, hi + 1, (n, d)).astype(dtype)
