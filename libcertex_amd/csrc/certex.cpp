@@ -199,7 +199,7 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const u
   auto& rs           = res.state();
   hipStream_t stream = rs.stream;
   const int64_t size = st.size;
-  const int64_t nq_pad = round_up(B, certex_amd::kBlockQ);
+  const int64_t nq_pad = certex_amd::pad_queries(B);
   const uint8_t flip   = st.type == vtype::u8 ? 0x80 : 0;
   fa.q0                = q0;
 
@@ -232,7 +232,7 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const u
     certex_amd::screen_args aa = sa;
     aa.n_scan                  = n_anchor;
     aa.row_stride              = s;
-    aa.chunk_steps             = int(g * std::max<int64_t>(1, 64 / g));
+    aa.chunk_steps             = int(4 * g * std::max<int64_t>(1, 16 / g));
     aa.gmax                    = gmax;
     aa.n_groups                = n_groups;
     aa.group_steps             = int(g);
@@ -254,7 +254,7 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const u
     sa.n_scan      = size;
     sa.row_stride  = 1;
     sa.theta       = theta;
-    sa.chunk_steps = 64;
+    sa.chunk_steps = 128;
     sa.cand_count  = count;
     sa.cand_rows   = rows;
     sa.cap         = cap;

@@ -25,16 +25,26 @@ constexpr int32_t kKeepAll = -(1 << 29);
 /** Threshold of a padding query: keeps nothing. */
 constexpr int32_t kKeepNone = 0x7fffffff;
 
-/** Rows of one screen step and queries of one screen workgroup. */
+/** Rows of one screen step. */
 constexpr int kStepRows  = 64;
-constexpr int kBlockQ    = 256;
 /** Widest integer row (bytes) that the MFMA screen instantiates. */
 constexpr int kMaxIntDim = 256;
 
+/** Queries per screen workgroup for a batch of nq queries (512, or 128 for small batches). */
+__host__ __device__ inline int query_block(int64_t nq) { return nq > 128 ? 512 : 128; }
+/** Padded query count of a batch: a multiple of its query block. */
+__host__ __device__ inline int64_t pad_queries(int64_t nq)
+{
+  const int qb = query_block(nq);
+  return (nq + qb - 1) / qb * qb;
+}
+/** Query block of a padded batch (the kernels' view of query_block). */
+__host__ __device__ inline int screen_block_queries(int64_t nq_pad) { return nq_pad % 512 == 0 ? 512 : 128; }
+
 enum class metric_kind : int { l2 = 0, inner = 1, cosine = 2 };
 
-/** Bytes of a stored integer screening row of `dim` coordinates (a multiple of 64). */
-__host__ __device__ inline int int_row_bytes(int64_t dim) { return int((dim + 63) / 64 * 64); }
+/** Bytes of a stored integer screening row of `dim` coordinates: 128 or 256 (zero padded). */
+__host__ __device__ inline int int_row_bytes(int64_t dim) { return dim <= 128 ? 128 : 256; }
 
 // --- encoding -------------------------------------------------------------------------------
 
@@ -80,8 +90,9 @@ struct screen_args {
   const int8_t* qcodes;  // [nq_pad, row_bytes]
   const int32_t* theta;  // [nq_pad] (screen only)
   int64_t nq;            // live queries
-  int64_t nq_pad;        // multiple of kBlockQ
-  int chunk_steps;       // steps of kStepRows rows per workgroup
+  int64_t nq_pad;        // pad_queries(nq)
+  int chunk_steps;       // steps of kStepRows rows per workgroup: 4 waves x a whole number of
+                         // anchor groups
   filter_args filter;
   // screen: candidate buckets
   uint32_t* cand_count = nullptr;  // [nq_pad]

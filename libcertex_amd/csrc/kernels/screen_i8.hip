@@ -10,15 +10,23 @@
 // rounding-error term exists, and the certified test of the reference degenerates to the exact
 // integer comparison acc >= theta(q).
 //
-// Layout of one MFMA tile (v_mfma_i32_16x16x64_i8): operand A holds 16 stored rows, operand B
-// holds 16 queries, so lane l owns query (l % 16) and rows 4 (l / 16) + r, r = 0..3, of the tile.
-// The row term enters as the C operand (four consecutive rows = one 16-byte LDS read), and the
-// per-query test is a max over the lane's 16 accumulators of a step and one compare.
+// MFMA tile (v_mfma_i32_16x16x64_i8): operand A holds 16 stored rows, operand B holds 16 queries,
+// so lane l owns query (l % 16) and rows 4 (l / 16) + r, r = 0..3. The row term enters as the C
+// operand (four consecutive rows = one 16-byte load), and the per-query test is a max over the
+// lane's 16 accumulators of a 64-row step and one compare per query tile.
 //
-// Work decomposition: a workgroup (4 waves) keeps 256 queries resident in registers (64 per
-// wave) and streams a chunk of stored rows through double-buffered LDS, 64 rows per step. Block
-// b runs on XCD b % 8; the chunk index is derived so that all query blocks of one chunk run on one
-// XCD at about the same time, and the chunk is read from HBM once per pass into that XCD's L2.
+// Work decomposition:
+// - a workgroup holds QB queries (512, or 128 for small batches) in LDS for its whole life, rows
+//   stored with the 16-byte chunks XOR-swizzled by (row & 7) so that the ds_read_b128 of a query
+//   tile is free of bank conflicts;
+// - each of its 4 waves streams its own contiguous quarter of a chunk of stored rows straight
+//   from HBM/L2 into registers, 64 rows (one step) at a time, and runs the step against all QB
+//   queries in groups of 64, reading the next group's query fragments from LDS while the current
+//   group's MFMAs run; no barrier in the main loop;
+// - block b runs on XCD b % 8, and the chunk index is derived so that the query blocks of one
+//   chunk run on one XCD together: a chunk is read from HBM about once per pass into that L2.
+// Survivors are compacted with a ballot + mbcnt rank and one LDS reservation per round into a
+// per-workgroup list, flushed to the per-query buckets at the end.
 
 #include "../kernels.hpp"
 
@@ -29,20 +37,14 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves  = 4;
-constexpr int kQT     = 4;  // 16-query tiles per wave
-constexpr int kBT     = 4;  // 16-row tiles per step
 constexpr int kHitCap = 1024;
 
+/** 16-byte chunk slot of chunk c of row r (conflict-free ds_read_b128 of 16 rows x 1 chunk). */
 template <int KS>
-struct lds_layout {
-  static constexpr int kRowBytes  = 64 * KS;
-  // 16 bytes of padding per row: the 16 lanes of a ds_read_b128 quarter-wave that read rows
-  // 0..15 at one column start in 16 distinct 4-bank groups.
-  static constexpr int kPitch     = kRowBytes + 16;
-  static constexpr int kRowsBytes = kStepRows * kPitch;
-  static constexpr int kBufBytes  = kRowsBytes + kStepRows * 4;
-};
+__device__ __forceinline__ int slot(int r, int c)
+{
+  return KS == 2 ? (c ^ (r & 7)) : (c ^ (r & 15));
+}
 
 __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
 {
@@ -57,11 +59,15 @@ __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
   }
 }
 
-template <int KS, bool ANCHORS, bool FILT>
+template <int KS, int QB, bool ANCHORS, bool FILT>
 __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 {
-  using L = lds_layout<KS>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * L::kBufBytes];
+  constexpr int ROWB = 64 * KS;
+  constexpr int NG   = QB / 64;  // groups of 64 queries
+  static_assert(NG % 2 == 0, "query groups are processed in pairs");
+  __shared__ __attribute__((aligned(16))) uint8_t qlds[QB * ROWB];
+  __shared__ int thl[ANCHORS ? 1 : QB];
+  __shared__ int gml[ANCHORS ? 4 * QB : 1];
   __shared__ uint32_t hit_q[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t hit_row[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t n_hits;
@@ -72,197 +78,206 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 
   const int64_t n_steps  = screen_steps(a.n_scan);
   const int64_t n_chunks = (n_steps + a.chunk_steps - 1) / a.chunk_steps;
-  const int n_qb         = int(a.nq_pad / kBlockQ);
+  const int n_qb         = int(a.nq_pad / QB);
   const uint32_t b       = blockIdx.x;
   const uint32_t i       = b >> 3;
   const int qb           = int(i % uint32_t(n_qb));
   const int64_t chunk    = int64_t(i / uint32_t(n_qb)) * 8 + (b & 7);
   if (chunk >= n_chunks) { return; }
-  const int64_t s0 = chunk * a.chunk_steps;
-  const int64_t s1 = s0 + a.chunk_steps < n_steps ? s0 + a.chunk_steps : n_steps;
+  const int64_t q0 = int64_t(qb) * QB;
+  // this wave's steps: a contiguous quarter of the chunk (a whole number of anchor groups)
+  const int64_t quarter = a.chunk_steps / 4;
+  const int64_t w0      = chunk * a.chunk_steps + wave * quarter;
+  const int64_t w1      = w0 + quarter < n_steps ? w0 + quarter : n_steps;
 
   if (tid == 0) { n_hits = 0; }
-
-  // resident queries (B operands) and their thresholds
-  const int64_t qw = int64_t(qb) * kBlockQ + wave * 64;
-  v4i qf[kQT][KS];
-  int th[kQT];
-#pragma unroll
-  for (int qt = 0; qt < kQT; ++qt) {
-    const int64_t q   = qw + qt * 16 + (lane & 15);
-    const int8_t* src = a.qcodes + q * L::kRowBytes + (lane >> 4) * 16;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) { qf[qt][ks] = *reinterpret_cast<const v4i*>(src + ks * 64); }
-    th[qt] = ANCHORS ? 0 : a.theta[q];
+  for (int e = tid; e < QB * (ROWB / 16); e += 256) {
+    const int r = e / (ROWB / 16), c = e % (ROWB / 16);
+    const v4i v = *reinterpret_cast<const v4i*>(a.qcodes + (q0 + r) * ROWB + 16 * c);
+    *reinterpret_cast<v4i*>(qlds + r * ROWB + 16 * slot<KS>(r, c)) = v;
   }
-
-  // global -> LDS staging: thread t moves 16 KS bytes of row t / 4 and, for t % 4 == 0, its term
-  v4i pre[KS];
-  int prc = 0;
-  auto load_step = [&](int64_t s) {
-    const int64_t r = s * kStepRows + (tid >> 2);
-    if (r < a.n_scan) {
-      const int64_t row = r * a.row_stride;
-      const int8_t* src = a.codes + row * L::kRowBytes + (tid & 3) * 16 * KS;
-#pragma unroll
-      for (int c = 0; c < KS; ++c) { pre[c] = *reinterpret_cast<const v4i*>(src + 16 * c); }
-      prc = (tid & 3) == 0 ? a.rowc[row] : 0;
-    } else {
-#pragma unroll
-      for (int c = 0; c < KS; ++c) { pre[c] = v4i{0, 0, 0, 0}; }
-      prc = kDeadRow;
-    }
-  };
-  auto store_step = [&](int buf) {
-    uint8_t* base = smem + buf * L::kBufBytes;
-    uint8_t* dst  = base + (tid >> 2) * L::kPitch + (tid & 3) * 16 * KS;
-#pragma unroll
-    for (int c = 0; c < KS; ++c) { *reinterpret_cast<v4i*>(dst + 16 * c) = pre[c]; }
-    if ((tid & 3) == 0) { reinterpret_cast<int32_t*>(base + L::kRowsBytes)[tid >> 2] = prc; }
-  };
-
-  load_step(s0);
-  store_step(0);
+  if constexpr (ANCHORS) {
+    for (int e = tid; e < 4 * QB; e += 256) { gml[e] = INT_MIN; }
+  } else {
+    for (int e = tid; e < QB; e += 256) { thl[e] = a.theta[q0 + e]; }
+  }
   __syncthreads();
 
-  int gm[kQT];
+  v4i av[4][KS], cc[4];
+  auto load_rows = [&](int64_t s) {
 #pragma unroll
-  for (int qt = 0; qt < kQT; ++qt) { gm[qt] = INT_MIN; }
+    for (int bt = 0; bt < 4; ++bt) {
+      int64_t r = s * kStepRows + bt * 16 + (lane & 15);
+      r         = r < a.n_scan ? r : 0;  // rows past the end read row 0; their term kills them
+      const int8_t* src = a.codes + r * a.row_stride * ROWB + (lane >> 4) * 16;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) { av[bt][ks] = *reinterpret_cast<const v4i*>(src + 64 * ks); }
+      const int64_t r4 = s * kStepRows + bt * 16 + (lane >> 4) * 4;
+      if (a.row_stride == 1 && r4 + 3 < a.n_scan) {
+        cc[bt] = *reinterpret_cast<const v4i*>(a.rowc + r4);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          cc[bt][j] = r4 + j < a.n_scan ? a.rowc[(r4 + j) * a.row_stride] : kDeadRow;
+        }
+      }
+    }
+  };
+  auto read_queries = [&](int g, v4i (&bf)[4][KS], int (&th)[4]) {
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) {
+      const int r = g * 64 + qt * 16 + (lane & 15);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        bf[qt][ks] =
+          *reinterpret_cast<const v4i*>(qlds + r * ROWB + 16 * slot<KS>(r, (lane >> 4) + 4 * ks));
+      }
+      th[qt] = ANCHORS ? 0 : thl[r];
+    }
+  };
 
-  for (int64_t s = s0; s < s1; ++s) {
-    const int buf   = int(s - s0) & 1;
-    const bool more = s + 1 < s1;
-    if (more) { load_step(s + 1); }
-
-    const uint8_t* base = smem + buf * L::kBufBytes;
-    v4i acc[kBT][kQT];
+  int64_t row0 = 0;  // scan index of (bt = 0, r = 0) of this lane in the current step
+  auto group = [&](int g, const v4i (&bf)[4][KS], const int (&th)[4]) {
+    v4i acc[4][4];
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int bt = 0; bt < kBT; ++bt) {
-      const uint8_t* rp = base + (bt * 16 + (lane & 15)) * L::kPitch + (lane >> 4) * 16;
-      v4i av[KS];
+    for (int bt = 0; bt < 4; ++bt) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) { av[ks] = *reinterpret_cast<const v4i*>(rp + ks * 64); }
-      const v4i c = *reinterpret_cast<const v4i*>(base + L::kRowsBytes +
-                                                   (bt * 16 + (lane >> 4) * 4) * 4);
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
-        v4i t = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[0], qf[qt][0], c, 0, 0, 0);
+      for (int qt = 0; qt < 4; ++qt) {
+        v4i t = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[bt][0], bf[qt][0], cc[bt], 0, 0, 0);
 #pragma unroll
         for (int ks = 1; ks < KS; ++ks) {
-          t = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[ks], qf[qt][ks], t, 0, 0, 0);
+          t = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[bt][ks], bf[qt][ks], t, 0, 0, 0);
         }
         acc[bt][qt] = t;
       }
     }
+    __builtin_amdgcn_s_setprio(0);
 
-    const int64_t row0 = s * kStepRows + (lane >> 4) * 4;  // scan index of (bt = 0, r = 0)
-    if constexpr (!ANCHORS) {
-      bool hit = false;
+    if constexpr (ANCHORS) {
 #pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
-        int m = acc[0][qt][0];
-#pragma unroll
-        for (int bt = 0; bt < kBT; ++bt) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) { m = max(m, acc[bt][qt][r]); }
-        }
-        hit |= m >= th[qt];
-      }
-      if (__any(hit)) {
-        // compaction: per-lane hit masks, a wave prefix sum of their popcounts, one LDS
-        // reservation per wave and query tile
-#pragma unroll
-        for (int qt = 0; qt < kQT; ++qt) {
-          const int qloc = wave * 64 + qt * 16 + (lane & 15);
-          uint32_t bits  = 0;
-#pragma unroll
-          for (int bt = 0; bt < kBT; ++bt) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              bits |= uint32_t(acc[bt][qt][r] >= th[qt]) << (bt * 4 + r);
-            }
-          }
-          if constexpr (FILT) {
-            uint32_t scan = bits;
-            while (scan) {
-              const int j = __builtin_ctz(scan);
-              scan &= scan - 1;
-              const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
-              if (!keeps(a.filter, int64_t(qb) * kBlockQ + qloc, row)) { bits &= ~(1u << j); }
-            }
-          }
-          const int cnt = __builtin_popcount(bits);
-          int incl      = cnt;
-#pragma unroll
-          for (int off = 1; off < 64; off <<= 1) {
-            const int t = __shfl_up(incl, off);
-            if (lane >= off) { incl += t; }
-          }
-          const int total = __shfl(incl, 63);
-          if (total == 0) { continue; }
-          uint32_t pos = 0;
-          if (lane == 0) { pos = atomicAdd(&n_hits, uint32_t(total)); }
-          pos = uint32_t(__shfl(int(pos), 0)) + uint32_t(incl - cnt);
-          while (bits) {
-            const int j = __builtin_ctz(bits);
-            bits &= bits - 1;
-            const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
-            if (pos < kHitCap) {
-              hit_q[pos]   = uint32_t(qloc);
-              hit_row[pos] = row;
-            } else {  // LDS list full: straight to the global bucket
-              const int64_t q     = int64_t(qb) * kBlockQ + qloc;
-              const uint32_t slot = atomicAdd(a.cand_count + q, 1u);
-              if (slot < a.cap) { a.cand_rows[q * a.cap + slot] = row; }
-            }
-            ++pos;
-          }
-        }
-      }
-    } else {
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
+      for (int qt = 0; qt < 4; ++qt) {
         int m = INT_MIN;
 #pragma unroll
-        for (int bt = 0; bt < kBT; ++bt) {
+        for (int bt = 0; bt < 4; ++bt) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             int v = acc[bt][qt][r];
             if constexpr (FILT) {
               const int64_t idx = row0 + bt * 16 + r;
               if (idx < a.n_scan &&
-                  !keeps(a.filter, qw + qt * 16 + (lane & 15), uint32_t(idx * a.row_stride))) {
+                  !keeps(a.filter, q0 + g * 64 + qt * 16 + (lane & 15),
+                         uint32_t(idx * a.row_stride))) {
                 v = INT_MIN;
               }
             }
             m = max(m, v);
           }
         }
-        m      = max(m, __shfl_xor(m, 16));
-        m      = max(m, __shfl_xor(m, 32));
-        gm[qt] = max(gm[qt], m);
-      }
-      if ((s + 1) % a.group_steps == 0 || s + 1 == n_steps) {
-        const int64_t g = s / a.group_steps;
+        m = max(m, __shfl_xor(m, 16));
+        m = max(m, __shfl_xor(m, 32));
         if (lane < 16) {
+          int* p = gml + wave * QB + g * 64 + qt * 16 + lane;
+          *p     = max(*p, m);
+        }
+      }
+    } else {
+      int mq[4];
+      bool hit = false;
 #pragma unroll
-          for (int qt = 0; qt < kQT; ++qt) {
-            a.gmax[(qw + qt * 16 + lane) * a.n_groups + g] = gm[qt];
+      for (int qt = 0; qt < 4; ++qt) {
+        int m = acc[0][qt][0];
+#pragma unroll
+        for (int bt = 0; bt < 4; ++bt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) { m = max(m, acc[bt][qt][r]); }
+        }
+        mq[qt] = m;
+        hit |= m >= th[qt];
+      }
+      if (__builtin_expect(__any(hit), 0)) {
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) {
+          if (!__any(mq[qt] >= th[qt])) { continue; }
+          uint32_t bits = 0;
+#pragma unroll
+          for (int bt = 0; bt < 4; ++bt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              bits |= uint32_t(acc[bt][qt][r] >= th[qt]) << (bt * 4 + r);
+            }
+          }
+          const uint32_t qloc = uint32_t(g * 64 + qt * 16 + (lane & 15));
+          if constexpr (FILT) {
+            uint32_t scan = bits;
+            while (scan) {
+              const int j = __builtin_ctz(scan);
+              scan &= scan - 1;
+              const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
+              if (!keeps(a.filter, q0 + qloc, row)) { bits &= ~(1u << j); }
+            }
+          }
+          // compaction: one round per survivor of the busiest lane; ballot, rank by mbcnt,
+          // one LDS reservation per round
+          while (true) {
+            const uint64_t mask = __ballot(bits != 0);
+            if (mask == 0) { break; }
+            const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
+              uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0u));
+            const int leader = __builtin_ctzll(mask);
+            uint32_t base    = 0;
+            if (lane == leader) { base = atomicAdd(&n_hits, uint32_t(__builtin_popcountll(mask))); }
+            base = __builtin_amdgcn_readlane(base, leader);
+            if (bits) {
+              const int j = __builtin_ctz(bits);
+              bits &= bits - 1;
+              const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
+              const uint32_t pos = base + rank;
+              if (pos < uint32_t(kHitCap)) {
+                hit_q[pos]   = qloc;
+                hit_row[pos] = row;
+              } else {  // LDS list full: straight to the global bucket
+                const int64_t q     = q0 + qloc;
+                const uint32_t slot = atomicAdd(a.cand_count + q, 1u);
+                if (slot < a.cap) { a.cand_rows[q * a.cap + slot] = row; }
+              }
+            }
           }
         }
-#pragma unroll
-        for (int qt = 0; qt < kQT; ++qt) { gm[qt] = INT_MIN; }
       }
     }
+  };
 
-    if (more) { store_step(buf ^ 1); }
-    __syncthreads();
+  v4i b0[4][KS], b1[4][KS];
+  int t0[4], t1[4];
+  read_queries(0, b0, t0);
+  for (int64_t s = w0; s < w1; ++s) {
+    load_rows(s);
+    row0 = s * kStepRows + (lane >> 4) * 4;
+#pragma unroll 1
+    for (int g = 0; g < NG; g += 2) {
+      read_queries(g + 1, b1, t1);
+      group(g, b0, t0);
+      read_queries(g + 2 < NG ? g + 2 : 0, b0, t0);
+      group(g + 1, b1, t1);
+    }
+    if constexpr (ANCHORS) {
+      // end of an anchor group (group_steps steps, aligned to the wave's range)
+      if ((s + 1) % a.group_steps == 0 || s + 1 == n_steps) {
+        const int64_t grp = s / a.group_steps;
+        for (int e = lane; e < QB; e += 64) {
+          a.gmax[(q0 + e) * a.n_groups + grp] = gml[wave * QB + e];
+          gml[wave * QB + e]                  = INT_MIN;
+        }
+      }
+    }
   }
 
   if constexpr (!ANCHORS) {
+    __syncthreads();
     const uint32_t nh = n_hits < uint32_t(kHitCap) ? n_hits : uint32_t(kHitCap);
     for (uint32_t e = tid; e < nh; e += 256) {
-      const int64_t q     = int64_t(qb) * kBlockQ + hit_q[e];
+      const int64_t q     = q0 + hit_q[e];
       const uint32_t slot = atomicAdd(a.cand_count + q, 1u);
       if (slot < a.cap) { a.cand_rows[q * a.cap + slot] = hit_row[e]; }
     }
@@ -272,19 +287,24 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 template <bool ANCHORS, bool FILT>
 void launch(const screen_args& a, hipStream_t stream)
 {
+  const int qb_size      = screen_block_queries(a.nq_pad);
   const int64_t n_steps  = screen_steps(a.n_scan);
   const int64_t n_chunks = (n_steps + a.chunk_steps - 1) / a.chunk_steps;
-  const int64_t n_qb     = a.nq_pad / kBlockQ;
+  const int64_t n_qb     = a.nq_pad / qb_size;
   const int64_t blocks   = 8 * n_qb * ((n_chunks + 7) / 8);
   if (n_steps == 0 || n_qb == 0) { return; }
   const dim3 grid{unsigned(blocks)};
-  switch (a.row_bytes / 64) {
-    case 1: screen_kernel<1, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a); break;
-    case 2: screen_kernel<2, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a); break;
-    case 3: screen_kernel<3, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a); break;
-    case 4: screen_kernel<4, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a); break;
-    default: break;  // the host rejects wider rows before any launch
+  const int ks = a.row_bytes / 64;
+  if (ks == 2 && qb_size == 512) {
+    screen_kernel<2, 512, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
+  } else if (ks == 2) {
+    screen_kernel<2, 128, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
+  } else if (ks == 4 && qb_size == 512) {
+    screen_kernel<4, 512, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
+  } else if (ks == 4) {
+    screen_kernel<4, 128, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
   }
+  // other row widths are rejected by the host before any launch
 }
 
 }  // namespace
