@@ -19,7 +19,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 SOURCES = [
-    "kernels/screen_i8.hip",
+    "kernels/screen.hip",
     "kernels/select.hip",
     "kernels/encode.hip",
     "certex.cpp",

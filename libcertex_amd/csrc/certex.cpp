@@ -118,44 +118,50 @@ auto to_kind(cuvs::distance::DistanceType m) -> metric_kind
 }
 
 auto is_int(vtype t) -> bool { return t == vtype::i8 || t == vtype::u8; }
+auto elem_of(vtype t) -> certex_amd::elem
+{
+  return t == vtype::f32 ? certex_amd::elem::f32 : certex_amd::elem::f16;
+}
+auto elem_size(vtype t) -> size_t { return t == vtype::f32 ? 4 : (t == vtype::f16 ? 2 : 1); }
 
-auto round_up(int64_t v, int64_t m) -> int64_t { return (v + m - 1) / m * m; }
-
-/** Grow the row arrays of an integer index to `cap` rows (the caller holds the writer lock). */
-void grow_int(cuvs::resources const& res, index_state& st, int64_t cap)
+/** Grow every per-row array to `cap` rows (the caller holds the writer lock). */
+void grow(cuvs::resources const& res, index_state& st, int64_t cap)
 {
   if (cap <= st.capacity) { return; }
   hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  const size_t vbytes = is_int(st.type) ? 0 : size_t(st.dim) * elem_size(st.type);
   cuvs::detail::device_buffer codes(size_t(cap) * st.row_bytes);
-  cuvs::detail::device_buffer rowc(size_t(cap) * sizeof(int32_t));
+  cuvs::detail::device_buffer rowc(size_t(cap) * 4);
+  cuvs::detail::device_buffer vectors(size_t(cap) * vbytes);
   cuvs::detail::device_buffer labels;
-  if (st.size > 0) {
-    CERTEX_HIP_TRY(hipMemcpyAsync(codes.p, st.codes.p, size_t(st.size) * st.row_bytes,
-                                  hipMemcpyDeviceToDevice, stream));
-    CERTEX_HIP_TRY(hipMemcpyAsync(rowc.p, st.rowc.p, size_t(st.size) * sizeof(int32_t),
-                                  hipMemcpyDeviceToDevice, stream));
-  }
+  auto copy = [&](cuvs::detail::device_buffer& dst, cuvs::detail::device_buffer const& src,
+                  size_t bytes) {
+    if (bytes > 0) {
+      CERTEX_HIP_TRY(hipMemcpyAsync(dst.p, src.p, bytes, hipMemcpyDeviceToDevice, stream));
+    }
+  };
+  copy(codes, st.codes, size_t(st.size) * st.row_bytes);
+  copy(rowc, st.rowc, size_t(st.size) * 4);
+  copy(vectors, st.vectors, size_t(st.size) * vbytes);
   if (st.has_labels) {
     labels.resize_discard(size_t(cap) * sizeof(int32_t));
     certex_amd::fill_i32(labels.as<int32_t>(), cap, -1, stream);
-    if (st.size > 0) {
-      CERTEX_HIP_TRY(hipMemcpyAsync(labels.p, st.labels.p, size_t(st.size) * sizeof(int32_t),
-                                    hipMemcpyDeviceToDevice, stream));
-    }
+    copy(labels, st.labels, size_t(st.size) * sizeof(int32_t));
   }
   CERTEX_HIP_TRY(hipStreamSynchronize(stream));
   {
     // searches in flight on other streams may still read the old arrays
     std::unique_lock lk(st.rw);
     CERTEX_HIP_TRY(hipDeviceSynchronize());
-    st.codes    = std::move(codes);
-    st.rowc     = std::move(rowc);
+    st.codes   = std::move(codes);
+    st.rowc    = std::move(rowc);
+    st.vectors = std::move(vectors);
     if (st.has_labels) { st.labels = std::move(labels); }
     st.capacity = cap;
   }
 }
 
-/** Encode rows [0, n) of a device or host matrix into stored rows first .. first + n - 1. */
+/** Encode integer rows [0, n) of a device or host matrix into stored rows first, first + 1, ... */
 void append_int(cuvs::resources const& res, index_state& st, const uint8_t* x, int64_t n,
                 bool on_device, int64_t first)
 {
@@ -181,119 +187,166 @@ void append_int(cuvs::resources const& res, index_state& st, const uint8_t* x, i
   }
 }
 
-template <typename T>
-void check_type_supported(index_state const& st)
+/** Copy float rows [0, n) into the stored vectors first, ... and encode their screening rows. */
+void append_float(cuvs::resources const& res, index_state& st, const void* x, int64_t n,
+                  bool on_device, int64_t first)
 {
-  if (!is_int(st.type)) {
-    throw std::invalid_argument(
-      "certex: float32 and float16 vectors are not supported by this build yet (int8 and uint8 "
-      "are)");
-  }
+  hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  const size_t rb    = size_t(st.dim) * elem_size(st.type);
+  char* dst          = st.vectors.as<char>() + size_t(first) * rb;
+  CERTEX_HIP_TRY(hipMemcpyAsync(dst, x, size_t(n) * rb,
+                                on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                stream));
+  certex_amd::encode_rows_f16(dst, elem_of(st.type), n, st.dim, st.halves, st.normalize,
+                              st.center.as<double>(), 1.0 / st.alpha, st.metric, st.gamma,
+                              st.codes.as<uint16_t>() + size_t(first) * st.halves,
+                              st.rowc.as<float>() + first, st.maxima.as<double>(), stream);
 }
 
-/** One batch of queries of an integer index (the caller holds the shared lock). */
-void search_batch_int(cuvs::resources const& res, index_state const& st, const uint8_t* queries,
-                      int64_t B, int k, int64_t q0, int64_t* neighbors, float* distances,
-                      certex_amd::filter_args fa)
+/**
+ * Anchor grouping: the anchor pass records one best value per group of group_steps * 64 anchors;
+ * groups stay numerous enough for a good k-th value while the [nq_pad, n_groups] table stays
+ * under 1 GB.
+ */
+struct anchor_plan {
+  int stride;
+  int64_t n_anchor, n_groups;
+  int64_t group_steps;
+};
+auto plan_anchors(index_state const& st, int64_t size, int64_t nq_pad, int k) -> anchor_plan
+{
+  anchor_plan p{};
+  p.stride       = std::max(1, st.anchor_stride);
+  p.n_anchor     = (size + p.stride - 1) / p.stride;
+  const int64_t steps = certex_amd::screen_steps(p.n_anchor);
+  int64_t g      = std::max<int64_t>(1, steps / (64 * int64_t(k)));
+  while (nq_pad * ((steps + g - 1) / g) * 4 > (int64_t(1) << 30)) { g *= 2; }
+  p.group_steps = g;
+  p.n_groups    = (steps + g - 1) / g;
+  return p;
+}
+
+/**
+ * Screen pass into per-query buckets, re-run with larger buckets while one overflows (the
+ * reference re-runs on segment overflow, certex.cu:1208-1269). Returns false when some query
+ * keeps so many rows that scoring every row is cheaper (all_rows).
+ */
+template <typename F>
+bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, int64_t size,
+                         certex_amd::screen_args& sa, F&& screen, uint32_t*& count,
+                         uint32_t*& rows, int64_t& cap)
 {
   auto& rs           = res.state();
   hipStream_t stream = rs.stream;
-  const int64_t size = st.size;
+  auto* small        = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_small, 64));
+  count              = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_count, size_t(nq_pad) * 4));
+  cap                = rs.bucket_cap;
+  const int64_t all_rows_above = std::max<int64_t>(1 << 16, size / 8);
+  while (true) {
+    if (size_t(nq_pad) * size_t(cap) * 4 > (size_t(1) << 32)) { throw batch_too_large(); }
+    rows = static_cast<uint32_t*>(
+      rs.get(cuvs::detail::ws_rows, size_t(nq_pad) * size_t(cap) * 4));
+    certex_amd::fill_u32(count, nq_pad, 0, stream);
+    sa.n_scan      = size;
+    sa.row_stride  = 1;
+    sa.chunk_steps = 128;
+    sa.cand_count  = count;
+    sa.cand_rows   = rows;
+    sa.cap         = cap;
+    timed(2, stream, [&] { screen(sa, stream); });
+    certex_amd::fill_u32(small, 1, 0, stream);
+    certex_amd::max_u32(count, B, small, stream);
+    CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, small, 4, hipMemcpyDeviceToHost, stream));
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+    const int64_t worst = *static_cast<uint32_t*>(rs.host_small);
+    if (worst <= cap) { return true; }
+    if (worst > all_rows_above) { return false; }
+    int64_t c = 1024;
+    while (c < worst) { c *= 2; }
+    cap           = c;
+    rs.bucket_cap = c;
+  }
+}
+
+void count_stats(cuvs::resources const& res, index_state const& st, int64_t B, bool all_rows,
+                 const uint32_t* count, int64_t cap)
+{
+  if (!t_stats_on) { return; }
+  auto& rs           = res.state();
+  hipStream_t stream = rs.stream;
+  t_stats.queries += B;
+  if (all_rows) {
+    const int64_t live = st.size - st.n_removed;
+    t_stats.survivors += B * live;
+    t_stats.verified += B * live;
+    return;
+  }
+  auto* small = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_small, 64));
+  auto* sums  = reinterpret_cast<unsigned long long*>(small + 4);
+  certex_amd::fill_u32(small + 4, 4, 0, stream);
+  certex_amd::sum_u32(count, B, int64_t(1) << 40, sums, stream);
+  certex_amd::sum_u32(count, B, cap, sums + 1, stream);
+  CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, sums, 16, hipMemcpyDeviceToHost, stream));
+  CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  auto* h = static_cast<unsigned long long*>(rs.host_small);
+  t_stats.survivors += int64_t(h[0]);
+  t_stats.verified += int64_t(h[1]);
+}
+
+/** One batch of queries of an integer index (the caller holds the shared lock). */
+void search_batch_int(cuvs::resources const& res, index_state const& st, const void* queries,
+                      int64_t B, int k, int64_t q0, int64_t* neighbors, float* distances,
+                      certex_amd::filter_args fa, int)
+{
+  auto& rs             = res.state();
+  hipStream_t stream   = rs.stream;
+  const int64_t size   = st.size;
   const int64_t nq_pad = certex_amd::pad_queries(B);
   const uint8_t flip   = st.type == vtype::u8 ? 0x80 : 0;
   fa.q0                = q0;
 
-  auto* qcodes = static_cast<int8_t*>(rs.get(cuvs::detail::ws_qcodes, size_t(nq_pad) * st.row_bytes));
-  certex_amd::encode_queries_i8(queries, B, nq_pad, st.dim, st.row_bytes, flip, qcodes, stream);
+  auto* qcodes =
+    static_cast<int8_t*>(rs.get(cuvs::detail::ws_qcodes, size_t(nq_pad) * st.row_bytes));
+  certex_amd::encode_queries_i8(static_cast<const uint8_t*>(queries), B, nq_pad, st.dim,
+                                st.row_bytes, flip, qcodes, stream);
 
   // anchor pass: every anchor_stride-th stored row; the best screen value of every group of
-  // group_steps * 64 anchors, then the k-th best group is the threshold of the query
-  const int s            = std::max(1, st.anchor_stride);
-  const int64_t n_anchor = (size + s - 1) / s;
-  const int64_t a_steps  = certex_amd::screen_steps(n_anchor);
-  int64_t g              = std::max<int64_t>(1, a_steps / (64 * int64_t(k)));
-  while (nq_pad * ((a_steps + g - 1) / g) * 4 > (int64_t(1) << 30)) { g *= 2; }
-  const int64_t n_groups = (a_steps + g - 1) / g;
-
+  // anchors, then the k-th best group is the threshold of the query
+  const anchor_plan ap = plan_anchors(st, size, nq_pad, k);
   certex_amd::screen_args sa{};
   sa.codes     = st.codes.as<int8_t>();
-  sa.rowc      = st.rowc.as<int32_t>();
+  sa.rowc      = st.rowc.p;
   sa.row_bytes = st.row_bytes;
   sa.qcodes    = qcodes;
   sa.nq        = B;
   sa.nq_pad    = nq_pad;
   sa.filter    = fa;
 
-  auto* theta = static_cast<int32_t*>(rs.get(cuvs::detail::ws_theta, size_t(nq_pad) * 4));
-  bool all_rows = n_groups < k;
+  auto* theta   = static_cast<int32_t*>(rs.get(cuvs::detail::ws_theta, size_t(nq_pad) * 4));
+  bool all_rows = ap.n_groups < k;
   if (!all_rows) {
     auto* gmax = static_cast<int32_t*>(
-      rs.get(cuvs::detail::ws_gmax, size_t(nq_pad) * size_t(n_groups) * 4));
+      rs.get(cuvs::detail::ws_gmax, size_t(nq_pad) * size_t(ap.n_groups) * 4));
     certex_amd::screen_args aa = sa;
-    aa.n_scan                  = n_anchor;
-    aa.row_stride              = s;
-    aa.chunk_steps             = int(4 * g * std::max<int64_t>(1, 16 / g));
+    aa.n_scan                  = ap.n_anchor;
+    aa.row_stride              = ap.stride;
+    aa.chunk_steps             = int(4 * ap.group_steps * std::max<int64_t>(1, 16 / ap.group_steps));
     aa.gmax                    = gmax;
-    aa.n_groups                = n_groups;
-    aa.group_steps             = int(g);
+    aa.n_groups                = ap.n_groups;
+    aa.group_steps             = int(ap.group_steps);
     timed(0, stream, [&] { certex_amd::anchors_i8(aa, stream); });
     timed(1, stream,
-          [&] { certex_amd::threshold_i8(gmax, n_groups, B, nq_pad, k, theta, stream); });
+          [&] { certex_amd::threshold_i8(gmax, ap.n_groups, B, nq_pad, k, theta, stream); });
   }
 
-  auto* small = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_small, 64));
-  auto* count = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_count, size_t(nq_pad) * 4));
-  int64_t cap = rs.bucket_cap;
-  // a bucket larger than this holds a sizeable part of the index: score every row instead
-  const int64_t all_rows_above = std::max<int64_t>(1 << 16, size / 8);
-  uint32_t* rows               = nullptr;
-  while (!all_rows) {
-    if (size_t(nq_pad) * size_t(cap) * 4 > (size_t(1) << 32)) { throw batch_too_large(); }
-    rows = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_rows, size_t(nq_pad) * size_t(cap) * 4));
-    certex_amd::fill_u32(count, nq_pad, 0, stream);
-    sa.n_scan      = size;
-    sa.row_stride  = 1;
-    sa.theta       = theta;
-    sa.chunk_steps = 128;
-    sa.cand_count  = count;
-    sa.cand_rows   = rows;
-    sa.cap         = cap;
-    timed(2, stream, [&] { certex_amd::screen_i8(sa, stream); });
-    certex_amd::fill_u32(small, 1, 0, stream);
-    certex_amd::max_u32(count, B, small, stream);
-    CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, small, 4, hipMemcpyDeviceToHost, stream));
-    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
-    const int64_t worst = *static_cast<uint32_t*>(rs.host_small);
-    if (worst <= cap) { break; }
-    if (worst > all_rows_above) {
-      all_rows = true;
-      break;
-    }
-    int64_t c = 1024;
-    while (c < worst) { c *= 2; }
-    cap           = c;
-    rs.bucket_cap = c;
+  uint32_t *count = nullptr, *rows = nullptr;
+  int64_t cap = 0;
+  if (!all_rows) {
+    sa.theta = theta;
+    all_rows = !screen_into_buckets(res, B, nq_pad, size, sa, certex_amd::screen_i8, count, rows,
+                                    cap);
   }
-
-  if (t_stats_on) {
-    auto* sums = reinterpret_cast<unsigned long long*>(small + 4);
-    t_stats.queries += B;
-    if (all_rows) {
-      const int64_t live = size - st.n_removed;
-      t_stats.survivors += B * live;
-      t_stats.verified += B * live;
-    } else {
-      certex_amd::fill_u32(small + 4, 4, 0, stream);
-      certex_amd::sum_u32(count, B, int64_t(1) << 40, sums, stream);
-      certex_amd::sum_u32(count, B, cap, sums + 1, stream);
-      CERTEX_HIP_TRY(
-        hipMemcpyAsync(rs.host_small, sums, 16, hipMemcpyDeviceToHost, stream));
-      CERTEX_HIP_TRY(hipStreamSynchronize(stream));
-      auto* h = static_cast<unsigned long long*>(rs.host_small);
-      t_stats.survivors += int64_t(h[0]);
-      t_stats.verified += int64_t(h[1]);
-    }
-  }
+  count_stats(res, st, B, all_rows, count, cap);
 
   auto* best_score =
     static_cast<double*>(rs.get(cuvs::detail::ws_best_score, size_t(B) * k * sizeof(double)));
@@ -321,6 +374,105 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const u
   certex_amd::finish(best_score, best_row, B, k, st.metric, distances, neighbors, stream);
 }
 
+/** One batch of queries of a float index (the caller holds the shared lock). */
+void search_batch_float(cuvs::resources const& res, index_state const& st, const void* queries,
+                        int64_t B, int k, int64_t q0, int64_t* neighbors, float* distances,
+                        certex_amd::filter_args fa, int anchors)
+{
+  auto& rs             = res.state();
+  hipStream_t stream   = rs.stream;
+  const int64_t size   = st.size;
+  const int64_t nq_pad = certex_amd::pad_queries(B);
+  const auto t         = elem_of(st.type);
+  fa.q0                = q0;
+
+  auto* qrows =
+    static_cast<uint16_t*>(rs.get(cuvs::detail::ws_qcodes, size_t(nq_pad) * st.row_bytes));
+  auto* qscal = static_cast<double*>(rs.get(cuvs::detail::ws_qscal, size_t(nq_pad) * 3 * 8));
+  certex_amd::encode_queries_f16(queries, t, B, nq_pad, st.dim, st.halves, st.normalize,
+                                 st.center.as<double>(), 1.0 / st.alpha, qrows, qscal, stream);
+
+  const anchor_plan ap = plan_anchors(st, size, nq_pad, k);
+  certex_amd::screen_args sa{};
+  sa.codes     = st.codes.as<int8_t>();
+  sa.rowc      = st.rowc.p;
+  sa.row_bytes = st.row_bytes;
+  sa.qcodes    = reinterpret_cast<const int8_t*>(qrows);
+  sa.nq        = B;
+  sa.nq_pad    = nq_pad;
+  sa.filter    = fa;
+
+  auto* theta   = static_cast<float*>(rs.get(cuvs::detail::ws_theta, size_t(nq_pad) * 4));
+  bool all_rows = ap.n_groups < k;
+  if (!all_rows) {
+    auto* gmax = static_cast<float*>(
+      rs.get(cuvs::detail::ws_gmax, size_t(nq_pad) * size_t(ap.n_groups) * 4));
+    auto* grow = static_cast<uint32_t*>(
+      rs.get(cuvs::detail::ws_grow, size_t(nq_pad) * size_t(ap.n_groups) * 4));
+    certex_amd::screen_args aa = sa;
+    aa.n_scan                  = ap.n_anchor;
+    aa.row_stride              = ap.stride;
+    aa.chunk_steps             = int(4 * ap.group_steps * std::max<int64_t>(1, 16 / ap.group_steps));
+    aa.gmax                    = gmax;
+    aa.grow                    = grow;
+    aa.n_groups                = ap.n_groups;
+    aa.group_steps             = int(ap.group_steps);
+    timed(0, stream, [&] { certex_amd::anchors_f16(aa, stream); });
+    certex_amd::threshold_f_args ta{};
+    ta.gmax      = gmax;
+    ta.grow      = grow;
+    ta.n_groups  = ap.n_groups;
+    ta.nq        = B;
+    ta.nq_pad    = nq_pad;
+    ta.k         = k;
+    ta.per_query = std::max(std::max(anchors, 2 * k), k);
+    ta.vectors   = st.vectors.p;
+    ta.queries   = queries;
+    ta.t         = t;
+    ta.dim       = st.dim;
+    ta.metric    = st.metric;
+    ta.qscal     = qscal;
+    ta.maxima    = st.maxima.as<double>();
+    ta.alpha2    = st.alpha * st.alpha;
+    ta.gamma     = st.gamma;
+    ta.theta     = theta;
+    timed(1, stream, [&] { certex_amd::threshold_f16(ta, stream); });
+  }
+
+  uint32_t *count = nullptr, *rows = nullptr;
+  int64_t cap = 0;
+  if (!all_rows) {
+    sa.theta = theta;
+    all_rows = !screen_into_buckets(res, B, nq_pad, size, sa, certex_amd::screen_f16, count,
+                                    rows, cap);
+  }
+  count_stats(res, st, B, all_rows, count, cap);
+
+  auto* best_score =
+    static_cast<double*>(rs.get(cuvs::detail::ws_best_score, size_t(B) * k * sizeof(double)));
+  auto* best_row =
+    static_cast<int64_t*>(rs.get(cuvs::detail::ws_best_row, size_t(B) * k * sizeof(int64_t)));
+  certex_amd::verify_f_args va{};
+  va.cand_count = count;
+  va.cand_rows  = rows;
+  va.cap        = cap;
+  va.all_rows   = all_rows;
+  va.n_rows     = size;
+  va.vectors    = st.vectors.p;
+  va.rowc       = st.rowc.as<float>();
+  va.queries    = queries;
+  va.t          = t;
+  va.dim        = st.dim;
+  va.metric     = st.metric;
+  va.filter     = fa;
+  va.nq         = B;
+  va.k          = k;
+  va.best_score = best_score;
+  va.best_row   = best_row;
+  timed(3, stream, [&] { certex_amd::verify_topk_f(va, stream); });
+  certex_amd::finish(best_score, best_row, B, k, st.metric, distances, neighbors, stream);
+}
+
 template <typename T>
 void search_impl(cuvs::resources const& res, search_params const& params, index<T> const& idx,
                  matrix_view<const T> queries, int64_t* neighbors, float* distances, int64_t k,
@@ -331,15 +483,16 @@ void search_impl(cuvs::resources const& res, search_params const& params, index<
   expects(queries.cols == st.dim, "dimension mismatch");
   expects(k >= 1 && k <= 2048, "certex returns at most 2048 neighbors per query");
   expects(st.size >= k, "the index holds fewer than k vectors");
-  check_type_supported<T>(st);
   const int64_t nq = queries.rows;
   if (nq == 0) { return; }
   if (t_stats_on) { res.sync(); }
-  const int64_t bs = std::max(1, params.batch_size);
+  const int64_t bs   = std::max(1, params.batch_size);
+  const size_t qrow  = size_t(st.dim) * sizeof(T);
+  auto batch         = is_int(st.type) ? search_batch_int : search_batch_float;
   std::function<void(int64_t, int64_t)> run = [&](int64_t b0, int64_t B) {
     try {
-      search_batch_int(res, st, reinterpret_cast<const uint8_t*>(queries.data) + b0 * st.dim, B,
-                       int(k), b0, neighbors + b0 * k, distances + b0 * k, fa);
+      batch(res, st, reinterpret_cast<const char*>(queries.data) + size_t(b0) * qrow, B, int(k),
+            b0, neighbors + b0 * k, distances + b0 * k, fa, params.anchors);
     } catch (batch_too_large const&) {
       if (B < 2) { throw; }
       run(b0, B / 2);
@@ -444,21 +597,70 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
           "certex: cosine distance needs float32 or float16 vectors");
   expects(dataset.rows >= 1 && dataset.cols >= 1, "certex: the dataset is empty");
   expects(params.anchor_stride >= 1, "certex: anchor_stride must be at least 1");
-  check_type_supported<T>(st);
-  expects(dataset.cols <= certex_amd::kMaxIntDim,
-          "certex: integer vectors of more than 256 coordinates are not supported by this build");
   st.params        = params;
   st.dim           = dataset.cols;
-  st.row_bytes     = certex_amd::int_row_bytes(st.dim);
-  st.width         = int(st.dim);
   st.anchor_stride = params.anchor_stride;
   st.host_vectors  = params.host_vectors;
   std::lock_guard w(st.writer);
-  grow_int(res, st, dataset.rows);
-  append_int(res, st, reinterpret_cast<const uint8_t*>(dataset.data), dataset.rows,
-             dataset.on_device, 0);
+  if (is_int(st.type)) {
+    expects(dataset.cols <= certex_amd::kMaxIntDim,
+            "certex: integer vectors of more than 256 coordinates are not supported by this build");
+    st.row_bytes = certex_amd::int_row_bytes(st.dim);
+    st.width     = int(st.dim);
+    grow(res, st, dataset.rows);
+    append_int(res, st, reinterpret_cast<const uint8_t*>(dataset.data), dataset.rows,
+               dataset.on_device, 0);
+    res.sync();
+    st.size = dataset.rows;
+    return out;
+  }
+  expects(dataset.cols <= 128,
+          "certex: float vectors of more than 128 coordinates are not supported by this build yet");
+  hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  st.halves          = certex_amd::f16_row_halves(st.dim);
+  st.row_bytes       = 2 * st.halves;
+  st.width           = int(st.dim);
+  st.normalize       = st.metric == metric_kind::cosine;
+  // fp32 accumulation of halves + 1 terms; a factor 2 covers truncating accumulation
+  st.gamma = 2.0 * double(st.halves + 1) * std::ldexp(1.0, -24);
+  grow(res, st, dataset.rows);
+  const int64_t n = dataset.rows;
+  const auto t    = elem_of(st.type);
+  // the vectors, then the center (mean; none for inner products) and the scale alpha that puts
+  // every screening row within norm 64
+  const size_t rb = size_t(st.dim) * sizeof(T);
+  CERTEX_HIP_TRY(hipMemcpyAsync(st.vectors.p, dataset.data, size_t(n) * rb,
+                                dataset.on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                stream));
+  st.center.resize_discard(size_t(st.dim) * sizeof(double));
+  st.maxima.resize_discard(2 * sizeof(double));
+  CERTEX_HIP_TRY(hipMemsetAsync(st.center.p, 0, size_t(st.dim) * sizeof(double), stream));
+  CERTEX_HIP_TRY(hipMemsetAsync(st.maxima.p, 0, 2 * sizeof(double), stream));
+  if (st.metric != metric_kind::inner) {
+    certex_amd::column_sums(st.vectors.p, t, n, st.dim, st.normalize, st.center.as<double>(),
+                            stream);
+    std::vector<double> c(size_t(st.dim));
+    CERTEX_HIP_TRY(hipMemcpyAsync(c.data(), st.center.p, c.size() * sizeof(double),
+                                  hipMemcpyDeviceToHost, stream));
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+    for (auto& v : c) { v /= double(n); }
+    CERTEX_HIP_TRY(hipMemcpyAsync(st.center.p, c.data(), c.size() * sizeof(double),
+                                  hipMemcpyHostToDevice, stream));
+  }
+  double* scratch = st.maxima.as<double>();  // max |x - c| lands in maxima[0] first
+  certex_amd::max_norm(st.vectors.p, t, n, st.dim, st.normalize, st.center.as<double>(), scratch,
+                       stream);
+  double max_norm = 0;
+  CERTEX_HIP_TRY(hipMemcpyAsync(&max_norm, scratch, sizeof(double), hipMemcpyDeviceToHost, stream));
+  CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  st.alpha = max_norm > 0 ? max_norm / 64.0 : 1.0;
+  CERTEX_HIP_TRY(hipMemsetAsync(st.maxima.p, 0, 2 * sizeof(double), stream));
+  certex_amd::encode_rows_f16(st.vectors.p, t, n, st.dim, st.halves, st.normalize,
+                              st.center.as<double>(), 1.0 / st.alpha, st.metric, st.gamma,
+                              st.codes.as<uint16_t>(), st.rowc.as<float>(), st.maxima.as<double>(),
+                              stream);
   res.sync();
-  st.size = dataset.rows;
+  st.size = n;
   return out;
 }
 
@@ -470,9 +672,13 @@ void extend(cuvs::resources const& res, matrix_view<const T> new_vectors, index<
   if (new_vectors.rows == 0) { return; }
   std::lock_guard w(st.writer);
   const int64_t need = st.size + new_vectors.rows;
-  if (need > st.capacity) { grow_int(res, st, std::max(need, 2 * st.capacity)); }
-  append_int(res, st, reinterpret_cast<const uint8_t*>(new_vectors.data), new_vectors.rows,
-             new_vectors.on_device, st.size);
+  if (need > st.capacity) { grow(res, st, std::max(need, 2 * st.capacity)); }
+  if (is_int(st.type)) {
+    append_int(res, st, reinterpret_cast<const uint8_t*>(new_vectors.data), new_vectors.rows,
+               new_vectors.on_device, st.size);
+  } else {
+    append_float(res, st, new_vectors.data, new_vectors.rows, new_vectors.on_device, st.size);
+  }
   res.sync();
   std::unique_lock publish(st.rw);
   st.size = need;
@@ -483,7 +689,7 @@ void reserve(cuvs::resources const& res, int64_t capacity, index<T>* idx)
 {
   index_state& st = idx->state();
   std::lock_guard w(st.writer);
-  grow_int(res, st, capacity);
+  grow(res, st, capacity);
 }
 
 template <typename T>
@@ -498,7 +704,11 @@ void remove(cuvs::resources const& res, const int64_t* ids, int64_t n_ids, index
   std::unique_lock publish(st.rw);
   CERTEX_HIP_TRY(hipDeviceSynchronize());
   certex_amd::fill_u32(reinterpret_cast<uint32_t*>(counter), 2, 0, stream);
-  certex_amd::remove_rows_i8(ids, n_ids, st.size, st.rowc.as<int32_t>(), counter, stream);
+  if (is_int(st.type)) {
+    certex_amd::remove_rows_i8(ids, n_ids, st.size, st.rowc.as<int32_t>(), counter, stream);
+  } else {
+    certex_amd::remove_rows_f16(ids, n_ids, st.size, st.rowc.as<float>(), counter, stream);
+  }
   CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, counter, 8, hipMemcpyDeviceToHost, stream));
   CERTEX_HIP_TRY(hipStreamSynchronize(stream));
   st.n_removed += int64_t(*static_cast<unsigned long long*>(rs.host_small));

@@ -97,6 +97,8 @@ enum ws_slot : int {
   ws_best_score,
   ws_best_row,
   ws_staging,
+  ws_qscal,
+  ws_grow,
   ws_n_slots
 };
 
@@ -152,10 +154,19 @@ struct index_state {
   bool host_vectors                     = false;
   bool has_labels                       = false;
   index_params params{};
-  // integer vectors: int8 codes (the vectors themselves, uint8 shifted by -128) and row terms
+  // screening rows and their terms. Integer vectors: int8 codes (the vectors themselves, uint8
+  // shifted by -128) and int32 terms. Float vectors: fp16 rows of (x - center) / alpha and fp32
+  // terms; the vectors as given are kept in `vectors` for the exact scores.
   cuvs::detail::device_buffer codes;
   cuvs::detail::device_buffer rowc;
   cuvs::detail::device_buffer labels;
+  cuvs::detail::device_buffer vectors;  // float vectors [capacity, dim]
+  cuvs::detail::device_buffer center;   // double [dim]
+  cuvs::detail::device_buffer maxima;   // double [2]: max |fp16(Z)|, max |Z - fp16(Z)|
+  double alpha   = 1.0;
+  double gamma   = 0.0;  // fp32 accumulation error factor of a screening product
+  int halves     = 0;    // fp16 row length
+  bool normalize = false;
   mutable std::shared_mutex rw;  // searches: shared per batch; publication of updates: exclusive
   std::mutex writer;             // one update at a time
 };

@@ -82,13 +82,13 @@ struct filter_args {
 };
 
 struct screen_args {
-  const int8_t* codes;   // stored rows [*, row_bytes]
-  const int32_t* rowc;   // row terms
+  const int8_t* codes;   // stored rows [*, row_bytes]: int8 codes or fp16 values
+  const void* rowc;      // row terms: int32 (int8 rows) or float (fp16 rows)
   int64_t n_scan;        // scanned rows: scan index i reads stored row i * row_stride
   int row_stride;        // 1 for the screen, the anchor stride for the anchor pass
   int row_bytes;         // 64 KS
   const int8_t* qcodes;  // [nq_pad, row_bytes]
-  const int32_t* theta;  // [nq_pad] (screen only)
+  const void* theta;     // [nq_pad] int32 or float (screen only)
   int64_t nq;            // live queries
   int64_t nq_pad;        // pad_queries(nq)
   int chunk_steps;       // steps of kStepRows rows per workgroup: 4 waves x a whole number of
@@ -98,8 +98,10 @@ struct screen_args {
   uint32_t* cand_count = nullptr;  // [nq_pad]
   uint32_t* cand_rows  = nullptr;  // [nq_pad, cap]
   int64_t cap          = 0;
-  // anchors: group maxima [nq_pad, n_groups], a group = group_steps consecutive steps
-  int32_t* gmax    = nullptr;
+  // anchors: group maxima [nq_pad, n_groups] (int32 or float), a group = group_steps steps;
+  // fp16 rows also record the stored row of each maximum in grow
+  void* gmax       = nullptr;
+  uint32_t* grow   = nullptr;
   int64_t n_groups = 0;
   int group_steps  = 1;
 };
@@ -112,6 +114,10 @@ void screen_i8(const screen_args& a, hipStream_t stream);
 
 /** Int8 MFMA pass that records the best screen value of every group of anchors for every query. */
 void anchors_i8(const screen_args& a, hipStream_t stream);
+
+/** The same two passes over fp16 rows (f32 accumulation, certified threshold). */
+void screen_f16(const screen_args& a, hipStream_t stream);
+void anchors_f16(const screen_args& a, hipStream_t stream);
 
 /**
  * theta[q] = the k-th largest of gmax[q, 0 .. n_groups) (kKeepAll when n_groups < k, and never
@@ -152,6 +158,93 @@ struct verify_args {
 
 /** fp64 exact scores of the candidates of every query and their k best by (score, row). */
 void verify_topk_i8(const verify_args& a, hipStream_t stream);
+
+// --- float vectors (float32 / float16) ------------------------------------------------------
+
+enum class elem : int { f32 = 0, f16 = 1 };
+
+/** Row length (halves) of the fp16 screening rows for dimension dim: 64 or 128. */
+__host__ __device__ inline int f16_row_halves(int64_t dim) { return dim <= 64 ? 64 : 128; }
+
+/**
+ * sums[j] += sum over rows of x[i, j] (x normalised to unit length when `normalize`), in fp64;
+ * the center of the screening rows is sums / n.
+ */
+void column_sums(const void* x, elem t, int64_t n, int64_t dim, bool normalize, double* sums,
+                 hipStream_t stream);
+/** *out = max(*out, max over rows of |x_i - center|) (x normalised when `normalize`). */
+void max_norm(const void* x, elem t, int64_t n, int64_t dim, bool normalize, const double* center,
+              double* out, hipStream_t stream);
+
+/**
+ * fp16 screening rows: Z = (x - center) / alpha (x normalised when `normalize`), rows[i] =
+ * fp16(Z) with subnormal results set to 0, zero padded to `halves`; rowc[i] = the row term
+ * rounded up (l2 / cosine: -(|Z|^2 / 2)(1 - 2 gamma - slack); inner: 0); maxima[0] and [1] are
+ * raised to the row's |fp16(Z)| and |Z - fp16(Z)| (upper bounds). Rows whose |Z| exceeds the
+ * fp16-safe bound get zeros and rowc = +inf (always a candidate).
+ */
+void encode_rows_f16(const void* x, elem t, int64_t n, int64_t dim, int halves, bool normalize,
+                     const double* center, double inv_alpha, metric_kind metric, double gamma,
+                     uint16_t* rows, float* rowc, double* maxima, hipStream_t stream);
+
+/**
+ * Query rows the same way; qscal[3 i + 0..2] = |W|^2, |fp16(W)| and |W - fp16(W)| (upper bounds,
+ * |W|^2 a lower bound) for i < nq; padding queries are zero.
+ */
+void encode_queries_f16(const void* q, elem t, int64_t nq, int64_t nq_pad, int64_t dim,
+                        int halves, bool normalize, const double* center, double inv_alpha,
+                        uint16_t* qrows, double* qscal, hipStream_t stream);
+
+/** Float tombstones: rowc[id] = -inf; counts the ids that were live. */
+void remove_rows_f16(const int64_t* ids, int64_t n, int64_t size, float* rowc,
+                     unsigned long long* newly_removed, hipStream_t stream);
+
+struct threshold_f_args {
+  const float* gmax;     // [nq_pad, n_groups]
+  const uint32_t* grow;  // [nq_pad, n_groups]
+  int64_t n_groups;
+  int64_t nq, nq_pad;
+  int k;
+  int per_query;         // anchors scored exactly per query (>= k)
+  const void* vectors;   // original vectors [*, dim]
+  const void* queries;   // original queries of the batch [nq, dim]
+  elem t;
+  int64_t dim;
+  metric_kind metric;
+  const double* qscal;   // [nq_pad, 3]
+  const double* maxima;  // [2]
+  double alpha2;         // alpha^2
+  double gamma;
+  float* theta;          // [nq_pad]
+};
+/**
+ * theta[q] for fp16 rows: the k-th smallest exact fp64 score among the best anchors of the
+ * per_query best groups gives U >= the k-th neighbour's score; theta is the screen value below
+ * which no pair can have a score <= U (rounded down). -FLT_MAX (keep every live row) with fewer
+ * than k valid anchors; +inf for padding queries.
+ */
+void threshold_f16(const threshold_f_args& a, hipStream_t stream);
+
+struct verify_f_args {
+  const uint32_t* cand_count;
+  const uint32_t* cand_rows;
+  int64_t cap;
+  bool all_rows;
+  int64_t n_rows;
+  const void* vectors;  // original vectors [*, dim]
+  const float* rowc;    // liveness (-inf) for all_rows
+  const void* queries;  // original queries of the batch
+  elem t;
+  int64_t dim;
+  metric_kind metric;
+  filter_args filter;
+  int64_t nq;
+  int k;
+  double* best_score;
+  int64_t* best_row;
+};
+/** fp64 exact scores (the canonical order of the oracle) and top-k by (score, row). */
+void verify_topk_f(const verify_f_args& a, hipStream_t stream);
 
 /**
  * Output conversion: distances (l2: score; inner: -score = <q, x>; cosine: score + 1 = 1 - cos)

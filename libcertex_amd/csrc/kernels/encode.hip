@@ -10,6 +10,11 @@
 namespace certex_amd {
 namespace {
 
+inline unsigned blocks_for(int64_t n, int block = 256)
+{
+  return unsigned((n + block - 1) / block);
+}
+
 __global__ void encode_rows_kernel(const uint8_t* x, int64_t n, int64_t dim, int row_bytes,
                                    uint8_t flip, metric_kind metric, int8_t* codes, int32_t* rowc)
 {
@@ -60,12 +65,202 @@ __global__ void fill_kernel(T* p, int64_t n, T v)
   }
 }
 
-inline unsigned blocks_for(int64_t n, int block = 256)
+// ---- float vectors ---------------------------------------------------------------------------
+
+__device__ inline double coord(const void* p, elem t, int64_t i)
 {
-  return unsigned((n + block - 1) / block);
+  return t == elem::f32 ? double(static_cast<const float*>(p)[i])
+                        : double(static_cast<const _Float16*>(p)[i]);
+}
+
+/** Euclidean norm of row i (1 when zero) for unit normalisation, fp64 in coordinate order. */
+__device__ inline double row_norm(const void* x, elem t, int64_t i, int64_t dim)
+{
+  double s = 0;
+  for (int64_t j = 0; j < dim; ++j) {
+    const double v = coord(x, t, i * dim + j);
+    s              = fma(v, v, s);
+  }
+  return s > 0 ? sqrt(s) : 1.0;
+}
+
+__device__ inline void atomic_max_pos(double* p, double v)
+{
+  // non-negative doubles order like their bit patterns
+  atomicMax(reinterpret_cast<unsigned long long*>(p), (unsigned long long)__double_as_longlong(v));
+}
+
+/** Upper bound of sqrt(s) for a non-negative fp64 sum s accumulated over `terms` terms. */
+__device__ inline double sqrt_up(double s, int64_t terms)
+{
+  return sqrt(s * (1.0 + 4e-16 * double(terms + 4))) * (1.0 + 4e-16);
+}
+
+__global__ void column_sums_kernel(const void* x, elem t, int64_t n, int64_t dim, bool normalize,
+                                   int64_t rows_per_block, double* sums)
+{
+  __shared__ double nrm[512];
+  const int64_t r0 = blockIdx.x * rows_per_block;
+  const int64_t r1 = r0 + rows_per_block < n ? r0 + rows_per_block : n;
+  for (int64_t i = r0 + threadIdx.x; i < r1; i += blockDim.x) {
+    nrm[i - r0] = normalize ? row_norm(x, t, i, dim) : 1.0;
+  }
+  __syncthreads();
+  for (int64_t j = threadIdx.x; j < dim; j += blockDim.x) {
+    double s = 0;
+    for (int64_t i = r0; i < r1; ++i) { s += coord(x, t, i * dim + j) / nrm[i - r0]; }
+    atomicAdd(sums + j, s);
+  }
+}
+
+__global__ void max_norm_kernel(const void* x, elem t, int64_t n, int64_t dim, bool normalize,
+                                const double* center, double* out)
+{
+  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (i >= n) { return; }
+  const double nrm = normalize ? row_norm(x, t, i, dim) : 1.0;
+  double s         = 0;
+  for (int64_t j = 0; j < dim; ++j) {
+    const double v = coord(x, t, i * dim + j) / nrm - center[j];
+    s              = fma(v, v, s);
+  }
+  atomic_max_pos(out, sqrt_up(s, dim));
+}
+
+constexpr double kF16Safe = 4096.0;  // |Z| above this: the row is always a candidate
+
+/** fp16 value of z (round to nearest), 0 for results below the smallest normal fp16. */
+__device__ inline _Float16 to_f16(double z)
+{
+  const _Float16 h = _Float16(float(z));
+  return fabs(double(h)) < 6.103515625e-05 ? _Float16(0.0f) : h;
+}
+
+__global__ void encode_rows_f16_kernel(const void* x, elem t, int64_t n, int64_t dim, int halves,
+                                       bool normalize, const double* center, double inv_alpha,
+                                       metric_kind metric, double gamma, uint16_t* rows,
+                                       float* rowc, double* maxima)
+{
+  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (i >= n) { return; }
+  _Float16* dst    = reinterpret_cast<_Float16*>(rows + i * halves);
+  const double nrm = normalize ? row_norm(x, t, i, dim) : 1.0;
+  double a = 0;
+  for (int64_t j = 0; j < dim; ++j) {
+    const double z = (coord(x, t, i * dim + j) / nrm - center[j]) * inv_alpha;
+    a              = fma(z, z, a);
+  }
+  if (!(sqrt(a) <= kF16Safe)) {
+    for (int j = 0; j < halves; ++j) { dst[j] = _Float16(0.0f); }
+    rowc[i] = INFINITY;
+    return;
+  }
+  double nz = 0, ez = 0;
+  for (int64_t j = 0; j < dim; ++j) {
+    const double z = (coord(x, t, i * dim + j) / nrm - center[j]) * inv_alpha;
+    const _Float16 h = to_f16(z);
+    const double e   = z - double(h);  // exact (Sterbenz, or h = 0)
+    dst[j]           = h;
+    nz               = fma(double(h), double(h), nz);
+    ez               = fma(e, e, ez);
+  }
+  for (int64_t j = dim; j < halves; ++j) { dst[j] = _Float16(0.0f); }
+  if (metric == metric_kind::inner) {
+    rowc[i] = 0.0f;
+  } else {
+    // row term rounded up: the fp32 accumulation error of this term is folded in (factor 1 - 2g)
+    const double c = -(a * (1.0 - 1e-13) / 2.0) * (1.0 - 2.0 * gamma - 1e-10);
+    float f        = float(c);
+    if (double(f) < c) { f = nextafterf(f, INFINITY); }
+    rowc[i] = f;
+  }
+  atomic_max_pos(maxima + 0, sqrt_up(nz, dim));
+  atomic_max_pos(maxima + 1, sqrt_up(ez, dim));
+}
+
+__global__ void encode_queries_f16_kernel(const void* q, elem t, int64_t nq, int64_t nq_pad,
+                                          int64_t dim, int halves, bool normalize,
+                                          const double* center, double inv_alpha, uint16_t* qrows,
+                                          double* qscal)
+{
+  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (i >= nq_pad) { return; }
+  _Float16* dst = reinterpret_cast<_Float16*>(qrows + i * halves);
+  if (i >= nq) {
+    for (int j = 0; j < halves; ++j) { dst[j] = _Float16(0.0f); }
+    qscal[3 * i] = qscal[3 * i + 1] = qscal[3 * i + 2] = 0.0;
+    return;
+  }
+  const double nrm = normalize ? row_norm(q, t, i, dim) : 1.0;
+  double a = 0, nw = 0, ew = 0;
+  for (int64_t j = 0; j < dim; ++j) {
+    const double w   = (coord(q, t, i * dim + j) / nrm - center[j]) * inv_alpha;
+    const _Float16 h = to_f16(w);
+    const double e   = w - double(h);
+    dst[j]           = h;
+    a                = fma(w, w, a);
+    nw               = fma(double(h), double(h), nw);
+    ew               = fma(e, e, ew);
+  }
+  for (int64_t j = dim; j < halves; ++j) { dst[j] = _Float16(0.0f); }
+  qscal[3 * i]     = a * (1.0 - 1e-13);
+  qscal[3 * i + 1] = sqrt_up(nw, dim);
+  qscal[3 * i + 2] = sqrt_up(ew, dim);
+}
+
+__global__ void remove_f_kernel(const int64_t* ids, int64_t n, int64_t size, float* rowc,
+                                unsigned long long* newly)
+{
+  const int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (t >= n) { return; }
+  const int64_t id = ids[t];
+  if (id < 0 || id >= size) { return; }
+  const int old = atomicExch(reinterpret_cast<int*>(rowc + id), __float_as_int(-INFINITY));
+  if (old != __float_as_int(-INFINITY)) { atomicAdd(newly, 1ull); }
 }
 
 }  // namespace
+
+void column_sums(const void* x, elem t, int64_t n, int64_t dim, bool normalize, double* sums,
+                 hipStream_t stream)
+{
+  if (n == 0) { return; }
+  const int64_t rows_per_block = 512;
+  const unsigned blocks        = unsigned((n + rows_per_block - 1) / rows_per_block);
+  column_sums_kernel<<<blocks, 128, 0, stream>>>(x, t, n, dim, normalize, rows_per_block, sums);
+}
+
+void max_norm(const void* x, elem t, int64_t n, int64_t dim, bool normalize, const double* center,
+              double* out, hipStream_t stream)
+{
+  if (n == 0) { return; }
+  max_norm_kernel<<<blocks_for(n), 256, 0, stream>>>(x, t, n, dim, normalize, center, out);
+}
+
+void encode_rows_f16(const void* x, elem t, int64_t n, int64_t dim, int halves, bool normalize,
+                     const double* center, double inv_alpha, metric_kind metric, double gamma,
+                     uint16_t* rows, float* rowc, double* maxima, hipStream_t stream)
+{
+  if (n == 0) { return; }
+  encode_rows_f16_kernel<<<blocks_for(n), 256, 0, stream>>>(
+    x, t, n, dim, halves, normalize, center, inv_alpha, metric, gamma, rows, rowc, maxima);
+}
+
+void encode_queries_f16(const void* q, elem t, int64_t nq, int64_t nq_pad, int64_t dim,
+                        int halves, bool normalize, const double* center, double inv_alpha,
+                        uint16_t* qrows, double* qscal, hipStream_t stream)
+{
+  if (nq_pad == 0) { return; }
+  encode_queries_f16_kernel<<<blocks_for(nq_pad), 256, 0, stream>>>(
+    q, t, nq, nq_pad, dim, halves, normalize, center, inv_alpha, qrows, qscal);
+}
+
+void remove_rows_f16(const int64_t* ids, int64_t n, int64_t size, float* rowc,
+                     unsigned long long* newly_removed, hipStream_t stream)
+{
+  if (n == 0) { return; }
+  remove_f_kernel<<<blocks_for(n), 256, 0, stream>>>(ids, n, size, rowc, newly_removed);
+}
 
 void encode_rows_i8(const uint8_t* x, int64_t n, int64_t dim, int row_bytes, uint8_t flip,
                     metric_kind metric, int8_t* codes, int32_t* rowc, hipStream_t stream)

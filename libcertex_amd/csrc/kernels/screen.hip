@@ -1,43 +1,80 @@
-// Int8 MFMA screen of the exact k-NN path for integer vectors (gfx950).
+// MFMA screens of the exact k-NN path (gfx950): int8 rows (exact) and fp16 rows (certified).
 //
-// Reference contract: detail/screen_int8.cu:99-292 (int8 codes, int32 accumulation, fp32
-// Cauchy-Schwarz epilogue) and the anchor-group pass of detail/kernels.hpp:125-135. This kernel
-// is built differently: the stored int8 code of a uint8 coordinate is x - 128 (x ^ 0x80), so the
-// int32 MFMA accumulator holds the exact value
+// Reference contract: detail/screen_int8.cu:99-292 and detail/screen_sm80.cu:117-379 (screen a
+// batch of queries against every stored row, keep the pairs that pass the query's threshold) and
+// the anchor-group pass of detail/kernels.hpp:125-135.
+//
+// int8 rows. The stored int8 code of a uint8 coordinate is x - 128 (x ^ 0x80), so the int32
+// accumulator holds the exact value
 //     acc(q, x) = <q', x'> + rowc(x),   rowc = -floor(|x'|^2 / 2)   (l2)
 //                                      rowc = 128 sum(x')          (inner product of uint8)
-// and the squared distance is |q'|^2 - 2 acc + (|x'|^2 mod 2). A larger acc is a closer row, no
-// rounding-error term exists, and the certified test of the reference degenerates to the exact
-// integer comparison acc >= theta(q).
+// and the squared distance is |q'|^2 - 2 acc + (|x'|^2 mod 2): a larger acc is a closer row and
+// the test acc >= theta(q) is exact.
+// fp16 rows. Rows hold fp16(Z) for Z = (x - c) / alpha; the fp32 accumulator holds
+// <fp16(W), fp16(Z)> + rowc(x) with rowc ~ -|Z|^2 / 2 (l2, cosine) or 0 (inner product). The host
+// folds the rounding error of both operands and of the fp32 accumulation into theta(q) and rowc,
+// so that acc >= theta(q) holds for every pair whose exact score passes the threshold.
 //
-// MFMA tile (v_mfma_i32_16x16x64_i8): operand A holds 16 stored rows, operand B holds 16 queries,
-// so lane l owns query (l % 16) and rows 4 (l / 16) + r, r = 0..3. The row term enters as the C
-// operand (four consecutive rows = one 16-byte load), and the per-query test is a max over the
-// lane's 16 accumulators of a 64-row step and one compare per query tile.
+// MFMA tile: operand A holds 16 stored rows, operand B holds 16 queries (one 16-byte fragment per
+// lane per 64-byte K step: v_mfma_i32_16x16x64_i8 or v_mfma_f32_16x16x32_f16), so lane l owns
+// query (l % 16) and rows 4 (l / 16) + r, r = 0..3. The row term enters as the C operand (four
+// consecutive rows = one 16-byte load); the per-query test is a max over the lane's 16
+// accumulators of a 64-row step and one compare per query tile.
 //
 // Work decomposition:
 // - a workgroup holds QB queries (512, or 128 for small batches) in LDS for its whole life, rows
-//   stored with the 16-byte chunks XOR-swizzled by (row & 7) so that the ds_read_b128 of a query
+//   stored with their 16-byte chunks XOR-swizzled by the row so that the ds_read_b128 of a query
 //   tile is free of bank conflicts;
 // - each of its 4 waves streams its own contiguous quarter of a chunk of stored rows straight
 //   from HBM/L2 into registers, 64 rows (one step) at a time, and runs the step against all QB
 //   queries in groups of 64, reading the next group's query fragments from LDS while the current
 //   group's MFMAs run; no barrier in the main loop;
-// - block b runs on XCD b % 8, and the chunk index is derived so that the query blocks of one
-//   chunk run on one XCD together: a chunk is read from HBM about once per pass into that L2.
+// - block b runs on XCD b % 8 and the chunk index is derived so that the query blocks of one chunk
+//   run on one XCD together: a chunk is read from HBM about once per pass into that XCD's L2.
 // Survivors are compacted with a ballot + mbcnt rank and one LDS reservation per round into a
 // per-workgroup list, flushed to the per-query buckets at the end.
 
 #include "../kernels.hpp"
 
 #include <climits>
+#include <cmath>
 
 namespace certex_amd {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 constexpr int kHitCap = 1024;
+
+struct int8_rows {
+  using acc_t  = v4i;
+  using frag_t = v4i;
+  using val_t  = int;
+  static constexpr bool kArgmax = false;
+  __device__ static acc_t mfma(frag_t a, frag_t b, acc_t c)
+  {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  }
+  __device__ static val_t lowest() { return INT_MIN; }
+  __device__ static val_t dead() { return kDeadRow; }
+  __device__ static val_t vmax(val_t a, val_t b) { return max(a, b); }
+};
+
+struct f16_rows {
+  using acc_t  = v4f;
+  using frag_t = v8h;
+  using val_t  = float;
+  static constexpr bool kArgmax = true;  // the float threshold scores the best anchor exactly
+  __device__ static acc_t mfma(frag_t a, frag_t b, acc_t c)
+  {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static val_t lowest() { return -INFINITY; }
+  __device__ static val_t dead() { return -INFINITY; }
+  __device__ static val_t vmax(val_t a, val_t b) { return fmaxf(a, b); }
+};
 
 /** 16-byte chunk slot of chunk c of row r (conflict-free ds_read_b128 of 16 rows x 1 chunk). */
 template <int KS>
@@ -59,18 +96,27 @@ __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
   }
 }
 
-template <int KS, int QB, bool ANCHORS, bool FILT>
+template <typename R, int KS, int QB, bool ANCHORS, bool FILT>
 __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 {
-  constexpr int ROWB = 64 * KS;
-  constexpr int NG   = QB / 64;  // groups of 64 queries
+  using acc_t  = typename R::acc_t;
+  using frag_t = typename R::frag_t;
+  using val_t  = typename R::val_t;
+  constexpr int ROWB   = 64 * KS;
+  constexpr int NG     = QB / 64;  // groups of 64 queries
+  constexpr bool ARGMX = ANCHORS && R::kArgmax;
   static_assert(NG % 2 == 0, "query groups are processed in pairs");
   __shared__ __attribute__((aligned(16))) uint8_t qlds[QB * ROWB];
-  __shared__ int thl[ANCHORS ? 1 : QB];
-  __shared__ int gml[ANCHORS ? 4 * QB : 1];
+  __shared__ val_t thl[ANCHORS ? 1 : QB];
+  __shared__ val_t gml[ANCHORS ? 4 * QB : 1];
+  __shared__ uint32_t gmr[ARGMX ? 4 * QB : 1];
   __shared__ uint32_t hit_q[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t hit_row[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t n_hits;
+
+  const val_t* rowc  = static_cast<const val_t*>(a.rowc);
+  const val_t* theta = static_cast<const val_t*>(a.theta);
+  val_t* gmax        = static_cast<val_t*>(a.gmax);
 
   const int tid  = threadIdx.x;
   const int lane = tid & 63;
@@ -97,13 +143,17 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     *reinterpret_cast<v4i*>(qlds + r * ROWB + 16 * slot<KS>(r, c)) = v;
   }
   if constexpr (ANCHORS) {
-    for (int e = tid; e < 4 * QB; e += 256) { gml[e] = INT_MIN; }
+    for (int e = tid; e < 4 * QB; e += 256) {
+      gml[e] = R::lowest();
+      if constexpr (ARGMX) { gmr[e] = 0xffffffffu; }
+    }
   } else {
-    for (int e = tid; e < QB; e += 256) { thl[e] = a.theta[q0 + e]; }
+    for (int e = tid; e < QB; e += 256) { thl[e] = theta[q0 + e]; }
   }
   __syncthreads();
 
-  v4i av[4][KS], cc[4];
+  frag_t av[4][KS];
+  acc_t cc[4];
   auto load_rows = [&](int64_t s) {
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
@@ -111,44 +161,44 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
       r         = r < a.n_scan ? r : 0;  // rows past the end read row 0; their term kills them
       const int8_t* src = a.codes + r * a.row_stride * ROWB + (lane >> 4) * 16;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) { av[bt][ks] = *reinterpret_cast<const v4i*>(src + 64 * ks); }
+      for (int ks = 0; ks < KS; ++ks) {
+        av[bt][ks] = *reinterpret_cast<const frag_t*>(src + 64 * ks);
+      }
       const int64_t r4 = s * kStepRows + bt * 16 + (lane >> 4) * 4;
       if (a.row_stride == 1 && r4 + 3 < a.n_scan) {
-        cc[bt] = *reinterpret_cast<const v4i*>(a.rowc + r4);
+        cc[bt] = *reinterpret_cast<const acc_t*>(rowc + r4);
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          cc[bt][j] = r4 + j < a.n_scan ? a.rowc[(r4 + j) * a.row_stride] : kDeadRow;
+          cc[bt][j] = r4 + j < a.n_scan ? rowc[(r4 + j) * a.row_stride] : R::dead();
         }
       }
     }
   };
-  auto read_queries = [&](int g, v4i (&bf)[4][KS], int (&th)[4]) {
+  auto read_queries = [&](int g, frag_t (&bf)[4][KS], val_t (&th)[4]) {
 #pragma unroll
     for (int qt = 0; qt < 4; ++qt) {
       const int r = g * 64 + qt * 16 + (lane & 15);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        bf[qt][ks] =
-          *reinterpret_cast<const v4i*>(qlds + r * ROWB + 16 * slot<KS>(r, (lane >> 4) + 4 * ks));
+        bf[qt][ks] = *reinterpret_cast<const frag_t*>(qlds + r * ROWB +
+                                                      16 * slot<KS>(r, (lane >> 4) + 4 * ks));
       }
-      th[qt] = ANCHORS ? 0 : thl[r];
+      th[qt] = ANCHORS ? val_t(0) : thl[r];
     }
   };
 
   int64_t row0 = 0;  // scan index of (bt = 0, r = 0) of this lane in the current step
-  auto group = [&](int g, const v4i (&bf)[4][KS], const int (&th)[4]) {
-    v4i acc[4][4];
+  auto group = [&](int g, const frag_t (&bf)[4][KS], const val_t (&th)[4]) {
+    acc_t acc[4][4];
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
 #pragma unroll
       for (int qt = 0; qt < 4; ++qt) {
-        v4i t = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[bt][0], bf[qt][0], cc[bt], 0, 0, 0);
+        acc_t t = R::mfma(av[bt][0], bf[qt][0], cc[bt]);
 #pragma unroll
-        for (int ks = 1; ks < KS; ++ks) {
-          t = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[bt][ks], bf[qt][ks], t, 0, 0, 0);
-        }
+        for (int ks = 1; ks < KS; ++ks) { t = R::mfma(av[bt][ks], bf[qt][ks], t); }
         acc[bt][qt] = t;
       }
     }
@@ -157,40 +207,69 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     if constexpr (ANCHORS) {
 #pragma unroll
       for (int qt = 0; qt < 4; ++qt) {
-        int m = INT_MIN;
+        val_t m    = R::lowest();
+        uint32_t j = 0;
 #pragma unroll
         for (int bt = 0; bt < 4; ++bt) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            int v = acc[bt][qt][r];
+            val_t v = acc[bt][qt][r];
             if constexpr (FILT) {
               const int64_t idx = row0 + bt * 16 + r;
               if (idx < a.n_scan &&
                   !keeps(a.filter, q0 + g * 64 + qt * 16 + (lane & 15),
                          uint32_t(idx * a.row_stride))) {
-                v = INT_MIN;
+                v = R::lowest();
               }
             }
-            m = max(m, v);
+            if constexpr (ARGMX) {
+              if (v > m) {
+                m = v;
+                j = uint32_t(bt * 16 + r);
+              }
+            } else {
+              m = R::vmax(m, v);
+            }
           }
         }
-        m = max(m, __shfl_xor(m, 16));
-        m = max(m, __shfl_xor(m, 32));
-        if (lane < 16) {
-          int* p = gml + wave * QB + g * 64 + qt * 16 + lane;
-          *p     = max(*p, m);
+        if constexpr (ARGMX) {
+          // best (value, row) of the query over the 64 rows of the step; ties to the lower row
+          uint32_t row = uint32_t((row0 + j) * a.row_stride);
+#pragma unroll
+          for (int off = 16; off <= 32; off <<= 1) {
+            const val_t om     = __shfl_xor(m, off);
+            const uint32_t orw = uint32_t(__shfl_xor(int(row), off));
+            if (om > m || (om == m && orw < row)) {
+              m   = om;
+              row = orw;
+            }
+          }
+          if (lane < 16) {
+            const int e = wave * QB + g * 64 + qt * 16 + lane;
+            if (m > gml[e] || (m == gml[e] && row < gmr[e])) {
+              gml[e] = m;
+              gmr[e] = row;
+            }
+          }
+        } else {
+          m = R::vmax(m, __shfl_xor(m, 16));
+          m = R::vmax(m, __shfl_xor(m, 32));
+          if (lane < 16) {
+            val_t* p = gml + wave * QB + g * 64 + qt * 16 + lane;
+            *p       = R::vmax(*p, m);
+          }
         }
       }
     } else {
-      int mq[4];
+      val_t mq[4];
       bool hit = false;
 #pragma unroll
       for (int qt = 0; qt < 4; ++qt) {
-        int m = acc[0][qt][0];
+        val_t m = acc[0][qt][0];
 #pragma unroll
         for (int bt = 0; bt < 4; ++bt) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) { m = max(m, acc[bt][qt][r]); }
+          for (int r = 0; r < 4; ++r) { m = R::vmax(m, acc[bt][qt][r]); }
         }
         mq[qt] = m;
         hit |= m >= th[qt];
@@ -237,9 +316,9 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
                 hit_q[pos]   = qloc;
                 hit_row[pos] = row;
               } else {  // LDS list full: straight to the global bucket
-                const int64_t q     = q0 + qloc;
-                const uint32_t slot = atomicAdd(a.cand_count + q, 1u);
-                if (slot < a.cap) { a.cand_rows[q * a.cap + slot] = row; }
+                const int64_t q       = q0 + qloc;
+                const uint32_t bslot  = atomicAdd(a.cand_count + q, 1u);
+                if (bslot < a.cap) { a.cand_rows[q * a.cap + bslot] = row; }
               }
             }
           }
@@ -248,8 +327,8 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     }
   };
 
-  v4i b0[4][KS], b1[4][KS];
-  int t0[4], t1[4];
+  frag_t b0[4][KS], b1[4][KS];
+  val_t t0[4], t1[4];
   read_queries(0, b0, t0);
   for (int64_t s = w0; s < w1; ++s) {
     load_rows(s);
@@ -266,8 +345,12 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
       if ((s + 1) % a.group_steps == 0 || s + 1 == n_steps) {
         const int64_t grp = s / a.group_steps;
         for (int e = lane; e < QB; e += 64) {
-          a.gmax[(q0 + e) * a.n_groups + grp] = gml[wave * QB + e];
-          gml[wave * QB + e]                  = INT_MIN;
+          gmax[(q0 + e) * a.n_groups + grp] = gml[wave * QB + e];
+          gml[wave * QB + e]                = R::lowest();
+          if constexpr (ARGMX) {
+            a.grow[(q0 + e) * a.n_groups + grp] = gmr[wave * QB + e];
+            gmr[wave * QB + e]                  = 0xffffffffu;
+          }
         }
       }
     }
@@ -277,14 +360,14 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     __syncthreads();
     const uint32_t nh = n_hits < uint32_t(kHitCap) ? n_hits : uint32_t(kHitCap);
     for (uint32_t e = tid; e < nh; e += 256) {
-      const int64_t q     = q0 + hit_q[e];
-      const uint32_t slot = atomicAdd(a.cand_count + q, 1u);
-      if (slot < a.cap) { a.cand_rows[q * a.cap + slot] = hit_row[e]; }
+      const int64_t q      = q0 + hit_q[e];
+      const uint32_t bslot = atomicAdd(a.cand_count + q, 1u);
+      if (bslot < a.cap) { a.cand_rows[q * a.cap + bslot] = hit_row[e]; }
     }
   }
 }
 
-template <bool ANCHORS, bool FILT>
+template <typename R, bool ANCHORS, bool FILT>
 void launch(const screen_args& a, hipStream_t stream)
 {
   const int qb_size      = screen_block_queries(a.nq_pad);
@@ -296,13 +379,13 @@ void launch(const screen_args& a, hipStream_t stream)
   const dim3 grid{unsigned(blocks)};
   const int ks = a.row_bytes / 64;
   if (ks == 2 && qb_size == 512) {
-    screen_kernel<2, 512, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
+    screen_kernel<R, 2, 512, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
   } else if (ks == 2) {
-    screen_kernel<2, 128, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
+    screen_kernel<R, 2, 128, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
   } else if (ks == 4 && qb_size == 512) {
-    screen_kernel<4, 512, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
+    screen_kernel<R, 4, 512, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
   } else if (ks == 4) {
-    screen_kernel<4, 128, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
+    screen_kernel<R, 4, 128, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
   }
   // other row widths are rejected by the host before any launch
 }
@@ -312,18 +395,36 @@ void launch(const screen_args& a, hipStream_t stream)
 void screen_i8(const screen_args& a, hipStream_t stream)
 {
   if (a.filter.kind != 0) {
-    launch<false, true>(a, stream);
+    launch<int8_rows, false, true>(a, stream);
   } else {
-    launch<false, false>(a, stream);
+    launch<int8_rows, false, false>(a, stream);
   }
 }
 
 void anchors_i8(const screen_args& a, hipStream_t stream)
 {
   if (a.filter.kind != 0) {
-    launch<true, true>(a, stream);
+    launch<int8_rows, true, true>(a, stream);
   } else {
-    launch<true, false>(a, stream);
+    launch<int8_rows, true, false>(a, stream);
+  }
+}
+
+void screen_f16(const screen_args& a, hipStream_t stream)
+{
+  if (a.filter.kind != 0) {
+    launch<f16_rows, false, true>(a, stream);
+  } else {
+    launch<f16_rows, false, false>(a, stream);
+  }
+}
+
+void anchors_f16(const screen_args& a, hipStream_t stream)
+{
+  if (a.filter.kind != 0) {
+    launch<f16_rows, true, true>(a, stream);
+  } else {
+    launch<f16_rows, true, false>(a, stream);
   }
 }
 

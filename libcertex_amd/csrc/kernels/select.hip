@@ -13,6 +13,7 @@
 
 #include "../kernels.hpp"
 
+#include <cfloat>
 #include <climits>
 #include <cmath>
 
@@ -287,6 +288,226 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a)
   }
 }
 
+
+// ---- float vectors ---------------------------------------------------------------------------
+
+__device__ inline double fcoord(const void* p, elem t, int64_t i)
+{
+  return t == elem::f32 ? double(static_cast<const float*>(p)[i])
+                        : double(static_cast<const _Float16*>(p)[i]);
+}
+
+/**
+ * Exact score of stored row x against the query whose coordinates sit in LDS as doubles, in the
+ * oracle's canonical order (coordinates ascending, fused multiply-adds): l2 sum (q - x)^2, inner
+ * -sum q x, cosine -sum q x / sqrt(sum q^2 sum x^2).
+ */
+__device__ inline double float_score(const double* qv, const void* vectors, elem t, int64_t row,
+                                     int64_t dim, metric_kind metric)
+{
+  double acc = 0, qq = 0, xx = 0;
+  const int64_t base = row * dim;
+  for (int64_t j = 0; j < dim; ++j) {
+    const double a = qv[j], b = fcoord(vectors, t, base + j);
+    if (metric == metric_kind::l2) {
+      const double d = a - b;
+      acc            = fma(d, d, acc);
+    } else {
+      acc = fma(a, b, acc);
+      if (metric == metric_kind::cosine) {
+        qq = fma(a, a, qq);
+        xx = fma(b, b, xx);
+      }
+    }
+  }
+  if (metric == metric_kind::l2) { return acc; }
+  if (metric == metric_kind::inner) { return -acc; }
+  return -acc / sqrt(qq * xx);
+}
+
+/** Order-preserving map of a float onto an unsigned key (ascending). */
+__device__ inline uint32_t fkey(float f)
+{
+  const uint32_t b = __float_as_uint(f + 0.0f);
+  return (b >> 31) ? ~b : (b | 0x80000000u);
+}
+
+constexpr int kMaxFloatDim = 4096;
+
+__global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_args a)
+{
+  __shared__ uint64_t key[kBuf];
+  __shared__ uint32_t rid[kBuf];
+  __shared__ double qv[kMaxFloatDim];
+  __shared__ int hist[256];
+  __shared__ int wave_tot[4];
+  __shared__ uint32_t sel_digit;
+  __shared__ int sel_rank;
+  __shared__ int cnt;
+
+  const int64_t q = blockIdx.x;
+  const int tid   = threadIdx.x;
+  if (q >= a.nq) {
+    if (tid == 0) { a.theta[q] = INFINITY; }
+    return;
+  }
+  const float* v    = a.gmax + q * a.n_groups;
+  const uint32_t* r = a.grow + q * a.n_groups;
+  // valid groups: a finite or +inf best value (all anchors removed or filtered: -inf)
+  if (tid == 0) { cnt = 0; }
+  __syncthreads();
+  int local = 0;
+  for (int64_t e = tid; e < a.n_groups; e += kThreads) { local += v[e] > -INFINITY ? 1 : 0; }
+  atomicAdd(&cnt, local);
+  __syncthreads();
+  const int n_valid = cnt;
+  if (n_valid < a.k) {
+    // keep every live row: removed rows (screen value -inf) still fail
+    if (tid == 0) { a.theta[q] = -FLT_MAX; }
+    return;
+  }
+  const int P = a.per_query < n_valid ? a.per_query : n_valid;
+  // the P-th largest value: radix select over descending keys (~fkey)
+  uint32_t prefix = 0, mask = 0;
+  int rank = P;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hist[tid] = 0;
+    __syncthreads();
+    for (int64_t e = tid; e < a.n_groups; e += kThreads) {
+      if (!(v[e] > -INFINITY)) { continue; }
+      const uint32_t k = ~fkey(v[e]);
+      if ((k & mask) == prefix) { atomicAdd(&hist[(k >> shift) & 255], 1); }
+    }
+    __syncthreads();
+    const int c    = hist[tid];
+    const int incl = block_scan_incl(c, wave_tot);
+    if (incl - c < rank && rank <= incl) {
+      sel_digit = uint32_t(tid);
+      sel_rank  = rank - (incl - c);
+    }
+    __syncthreads();
+    prefix |= sel_digit << shift;
+    mask |= 255u << shift;
+    rank = sel_rank;
+    __syncthreads();
+  }
+  // exact scores of the anchors of the groups at or above it (at most kBuf)
+  for (int64_t j = tid; j < a.dim; j += kThreads) { qv[j] = fcoord(a.queries, a.t, q * a.dim + j); }
+  if (tid == 0) { cnt = 0; }
+  __syncthreads();
+  for (int64_t e = tid; e < a.n_groups; e += kThreads) {
+    if (!(v[e] > -INFINITY) || ~fkey(v[e]) > prefix) { continue; }
+    const int slot = atomicAdd(&cnt, 1);
+    if (slot < kBuf) { rid[slot] = r[e]; }
+  }
+  __syncthreads();
+  const int m = cnt < kBuf ? cnt : kBuf;
+  for (int e = tid; e < m; e += kThreads) {
+    key[e] = score_key(float_score(qv, a.vectors, a.t, rid[e], a.dim, a.metric));
+  }
+  const int Pw = pow2_at_least(m);
+  for (int e = m + tid; e < Pw; e += kThreads) {
+    key[e] = ~0ull;
+    rid[e] = ~0u;
+  }
+  __syncthreads();
+  bitonic_sort(key, rid, Pw);
+  if (tid == 0) {
+    const double U  = key_score(key[a.k - 1]);  // k distinct anchors: U bounds the k-th score
+    const double aq = a.qscal[3 * q], nw = a.qscal[3 * q + 1], ew = a.qscal[3 * q + 2];
+    const double nz = a.maxima[0], ez = a.maxima[1];
+    const double cross = ew * nz + nw * ez + ew * ez;  // operand rounding, all pairs
+    const double accum = a.gamma * nw * nz;            // fp32 accumulation of the products
+    double th, scale;
+    if (a.metric == metric_kind::inner) {
+      th    = -U / a.alpha2;
+      scale = fabs(th);
+    } else {
+      const double u = a.metric == metric_kind::cosine ? (2.0 + 2.0 * U) : U;
+      const double ua = u / a.alpha2;
+      th              = (aq - ua) / 2.0;
+      scale           = fabs(aq) + fabs(ua);
+    }
+    const double t = th - accum - cross - 1e-10 * scale - 1e-30;
+    float f        = float(t);
+    if (double(f) > t) { f = nextafterf(f, -INFINITY); }
+    a.theta[q] = f > -FLT_MAX ? f : -FLT_MAX;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a)
+{
+  __shared__ uint64_t key[kBuf];
+  __shared__ uint32_t rid[kBuf];
+  __shared__ double qv[kMaxFloatDim];
+  __shared__ int fill;
+
+  const int64_t q = blockIdx.x;
+  const int tid   = threadIdx.x;
+  const int k     = a.k;
+  for (int64_t j = tid; j < a.dim; j += kThreads) { qv[j] = fcoord(a.queries, a.t, q * a.dim + j); }
+
+  const int64_t n_cand =
+    a.all_rows ? a.n_rows : (a.cand_count[q] < a.cap ? int64_t(a.cand_count[q]) : a.cap);
+  const uint32_t* cand = a.cand_rows + q * a.cap;
+  int have             = 0;
+  if (tid == 0) { fill = 0; }
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < n_cand;) {
+    const int room  = kBuf - have;
+    const int64_t m = n_cand - c0 < room ? n_cand - c0 : room;
+    for (int64_t e = tid; e < m; e += kThreads) {
+      uint32_t r;
+      bool live;
+      if (a.all_rows) {
+        r    = uint32_t(c0 + e);
+        live = a.rowc[r] != -INFINITY && keeps(a.filter, q, r);
+      } else {
+        r    = cand[c0 + e];
+        live = true;
+      }
+      if (live) {
+        const double s = float_score(qv, a.vectors, a.t, r, a.dim, a.metric);
+        const int slot = have + atomicAdd(&fill, 1);
+        key[slot]      = score_key(s);
+        rid[slot]      = r;
+      }
+    }
+    c0 += m;
+    __syncthreads();
+    have += fill;
+    __syncthreads();
+    if (tid == 0) { fill = 0; }
+    if (c0 < n_cand && have > k) {
+      const int P = pow2_at_least(have);
+      for (int j = have + tid; j < P; j += kThreads) {
+        key[j] = ~0ull;
+        rid[j] = ~0u;
+      }
+      __syncthreads();
+      bitonic_sort(key, rid, P);
+      have = k;
+    }
+    __syncthreads();
+  }
+  const int P = pow2_at_least(have > 1 ? have : 1);
+  for (int j = have + tid; j < P; j += kThreads) {
+    key[j] = ~0ull;
+    rid[j] = ~0u;
+  }
+  __syncthreads();
+  bitonic_sort(key, rid, P);
+  for (int j = tid; j < k; j += kThreads) {
+    if (j < have) {
+      a.best_score[q * k + j] = key_score(key[j]);
+      a.best_row[q * k + j]   = int64_t(rid[j]);
+    } else {
+      a.best_score[q * k + j] = INFINITY;
+      a.best_row[q * k + j]   = -1;
+    }
+  }
+}
+
 __global__ void finish_kernel(const double* best_score, const int64_t* best_row, int64_t n, int k,
                               metric_kind metric, float* distances, int64_t* neighbors)
 {
@@ -334,6 +555,18 @@ void verify_topk_i8(const verify_args& a, hipStream_t stream)
 {
   if (a.nq == 0) { return; }
   verify_topk_i8_kernel<<<unsigned(a.nq), kThreads, 0, stream>>>(a);
+}
+
+void threshold_f16(const threshold_f_args& a, hipStream_t stream)
+{
+  if (a.nq_pad == 0) { return; }
+  threshold_f16_kernel<<<unsigned(a.nq_pad), kThreads, 0, stream>>>(a);
+}
+
+void verify_topk_f(const verify_f_args& a, hipStream_t stream)
+{
+  if (a.nq == 0) { return; }
+  verify_topk_f_kernel<<<unsigned(a.nq), kThreads, 0, stream>>>(a);
 }
 
 void finish(const double* best_score, const int64_t* best_row, int64_t nq, int k,
