@@ -25,8 +25,12 @@ def _stride(n, k):
 
 def _keys(x):
     """Keys or queries on the GPU as float16, or float32 when float16 would overflow
-    (certex/attention.py:37-41)."""
+    (certex/attention.py:37-41). bfloat16 inputs become float32, which holds them exactly, so that
+    the top k is exact for the values given (float16 would round bfloat16 values below its normal
+    range)."""
     x = torch.as_tensor(x, device="cuda")
+    if x.dtype == torch.bfloat16:
+        return x.to(torch.float32)
     h = x.to(torch.float16)
     return h if bool(torch.isfinite(h).all()) else x.to(torch.float32)
 
