@@ -178,4 +178,16 @@ void search(cuvs::resources const& res, search_params const& params, index<T> co
             matrix_view<const T> queries, const int32_t* query_labels, int64_t* neighbors,
             float* distances, int64_t k);
 
+/**
+ * Save the index, its vectors and every quantity a search reads (reference
+ * certex_serialize.cu:42-150). The file starts with the NumPy descriptor of the vector type padded
+ * to 4 bytes ("<f4", "<f2", "|i1", "|u1"), the magic 0x43455258 and the format version.
+ */
+template <typename T>
+void serialize(cuvs::resources const& res, std::string const& filename, index<T> const& idx);
+
+/** Load an index saved by serialize into `idx` (reference certex_serialize.cu:152-243). */
+template <typename T>
+void deserialize(cuvs::resources const& res, std::string const& filename, index<T>* idx);
+
 }  // namespace cuvs::neighbors::certex

@@ -8,6 +8,7 @@
 
 #include <cstring>
 #include <exception>
+#include <fstream>
 #include <string>
 
 namespace {
@@ -414,11 +415,27 @@ cuvsError_t cuvsCertexSearchWithLabels(cuvsResources_t res,
 cuvsError_t cuvsCertexSerialize(cuvsResources_t res, const char* filename, cuvsCertexIndex_t index)
 {
   return translate([=] {
-    (void)res_of(res);
-    (void)filename;
-    (void)index;
-    throw std::invalid_argument("certex: serialization is not supported by this build yet");
+    auto& r = res_of(res);
+    certex::expects(filename != nullptr, "certex: NULL file name");
+    dispatch(index->dtype, [&](auto tag) {
+      certex::serialize<decltype(tag)>(r, std::string(filename), *as_index<decltype(tag)>(*index));
+    });
   });
+}
+
+/** The vector type of a saved index from its leading NumPy descriptor (certex.cpp:146-158). */
+static DLDataType dtype_of_file(const char* filename)
+{
+  std::ifstream is(filename, std::ios::binary);
+  certex::expects(is.good(), "certex: cannot open the index file");
+  char prefix[4] = {};
+  is.read(prefix, 4);
+  const std::string d(prefix + 1, 2);
+  if (d == "f4") { return {kDLFloat, 32, 1}; }
+  if (d == "f2") { return {kDLFloat, 16, 1}; }
+  if (d == "i1") { return {kDLInt, 8, 1}; }
+  if (d == "u1") { return {kDLUInt, 8, 1}; }
+  throw std::invalid_argument("certex: not a CertEx index file");
 }
 
 cuvsError_t cuvsCertexDeserialize(cuvsResources_t res,
@@ -426,10 +443,22 @@ cuvsError_t cuvsCertexDeserialize(cuvsResources_t res,
                                   cuvsCertexIndex_t index)
 {
   return translate([=] {
-    (void)res_of(res);
-    (void)filename;
+    auto& r = res_of(res);
+    certex::expects(filename != nullptr, "certex: NULL file name");
     certex::expects(index->addr == 0, "certex: the index handle already holds an index");
-    throw std::invalid_argument("certex: serialization is not supported by this build yet");
+    const DLDataType dtype = dtype_of_file(filename);
+    dispatch(dtype, [&](auto tag) {
+      using T = decltype(tag);
+      auto* p = new certex::index<T>(r);
+      try {
+        certex::deserialize<T>(r, std::string(filename), p);
+      } catch (...) {
+        delete p;
+        throw;
+      }
+      index->dtype = dtype;
+      index->addr  = reinterpret_cast<uintptr_t>(p);
+    });
   });
 }
 

@@ -11,6 +11,8 @@
 #include "certex_state.hpp"
 
 #include <algorithm>
+#include <cstring>
+#include <fstream>
 #include <functional>
 #include <new>
 
@@ -764,6 +766,151 @@ void search(cuvs::resources const& res, search_params const& params, index<T> co
   search_impl(res, params, idx, queries, neighbors, distances, k, fa);
 }
 
+
+namespace {
+
+constexpr uint32_t kMagic         = 0x43455258;  // "CERX"
+constexpr uint32_t kFormatVersion = 100;         // this build's layout of the stored arrays
+
+template <typename T>
+auto dtype_prefix() -> std::string
+{
+  std::string s;
+  if constexpr (std::is_same_v<T, float>) {
+    s = "<f4";
+  } else if constexpr (std::is_same_v<T, half_t>) {
+    s = "<f2";
+  } else if constexpr (std::is_same_v<T, int8_t>) {
+    s = "|i1";
+  } else {
+    s = "|u1";
+  }
+  s.resize(4, '\0');
+  return s;
+}
+
+template <typename V>
+void put(std::ostream& os, V v)
+{
+  os.write(reinterpret_cast<const char*>(&v), sizeof(V));
+}
+template <typename V>
+auto get(std::istream& is) -> V
+{
+  V v{};
+  is.read(reinterpret_cast<char*>(&v), sizeof(V));
+  expects(bool(is), "certex: the index file is truncated");
+  return v;
+}
+
+void put_device(std::ostream& os, cuvs::resources const& res, const void* p, size_t bytes)
+{
+  std::vector<char> h(bytes);
+  if (bytes > 0) {
+    CERTEX_HIP_TRY(hipMemcpyAsync(h.data(), p, bytes, hipMemcpyDeviceToHost,
+                                  static_cast<hipStream_t>(res.stream())));
+    res.sync();
+  }
+  os.write(h.data(), std::streamsize(bytes));
+}
+void get_device(std::istream& is, cuvs::resources const& res, void* p, size_t bytes)
+{
+  std::vector<char> h(bytes);
+  is.read(h.data(), std::streamsize(bytes));
+  expects(bool(is) || bytes == 0, "certex: the index file is truncated");
+  if (bytes > 0) {
+    CERTEX_HIP_TRY(hipMemcpyAsync(p, h.data(), bytes, hipMemcpyHostToDevice,
+                                  static_cast<hipStream_t>(res.stream())));
+    res.sync();
+  }
+}
+
+}  // namespace
+
+template <typename T>
+void serialize(cuvs::resources const& res, std::string const& filename, index<T> const& idx)
+{
+  index_state const& st = idx.state();
+  std::shared_lock view(st.rw);
+  std::ofstream os(filename, std::ios::binary);
+  expects(os.good(), "certex: cannot open the index file for writing");
+  os << dtype_prefix<T>();
+  put(os, kMagic);
+  put(os, kFormatVersion);
+  put(os, int32_t(st.dmetric));
+  put(os, int64_t(st.dim));
+  put(os, int32_t(st.width));
+  put(os, int32_t(st.anchor_stride));
+  put(os, uint8_t(st.host_vectors));
+  put(os, int64_t(st.size));
+  put(os, int64_t(st.n_removed));
+  put(os, uint8_t(st.has_labels));
+  put(os, int32_t(st.row_bytes));
+  put(os, st.alpha);
+  put(os, st.gamma);
+  put(os, int32_t(st.halves));
+  put(os, uint8_t(st.normalize));
+  const size_t n = size_t(st.size);
+  put_device(os, res, st.codes.p, n * st.row_bytes);
+  put_device(os, res, st.rowc.p, n * 4);
+  if (!is_int(st.type)) {
+    put_device(os, res, st.vectors.p, n * size_t(st.dim) * elem_size(st.type));
+    put_device(os, res, st.center.p, size_t(st.dim) * sizeof(double));
+    put_device(os, res, st.maxima.p, 2 * sizeof(double));
+  }
+  if (st.has_labels) { put_device(os, res, st.labels.p, n * sizeof(int32_t)); }
+  expects(os.good(), "certex: writing the index file failed");
+}
+
+template <typename T>
+void deserialize(cuvs::resources const& res, std::string const& filename, index<T>* idx)
+{
+  index_state& st = idx->state();
+  std::ifstream is(filename, std::ios::binary);
+  expects(is.good(), "certex: cannot open the index file");
+  char prefix[4] = {};
+  is.read(prefix, 4);
+  expects(bool(is) && std::memcmp(prefix, dtype_prefix<T>().data(), 4) == 0,
+          "certex: the file holds vectors of another type");
+  expects(get<uint32_t>(is) == kMagic, "certex: not a CertEx index file");
+  expects(get<uint32_t>(is) == kFormatVersion,
+          "certex: the index file was written by another version of the library");
+  std::lock_guard w(st.writer);
+  st.dmetric       = static_cast<cuvs::distance::DistanceType>(get<int32_t>(is));
+  st.metric        = to_kind(st.dmetric);
+  st.dim           = get<int64_t>(is);
+  st.width         = get<int32_t>(is);
+  st.anchor_stride = get<int32_t>(is);
+  st.host_vectors  = get<uint8_t>(is) != 0;
+  const int64_t n  = get<int64_t>(is);
+  st.n_removed     = get<int64_t>(is);
+  const bool labels = get<uint8_t>(is) != 0;
+  st.row_bytes     = get<int32_t>(is);
+  st.alpha         = get<double>(is);
+  st.gamma         = get<double>(is);
+  st.halves        = get<int32_t>(is);
+  st.normalize     = get<uint8_t>(is) != 0;
+  expects(st.dim >= 1 && n >= 0 && st.row_bytes > 0, "certex: corrupt index file");
+  st.size     = 0;
+  st.capacity = 0;
+  grow(res, st, std::max<int64_t>(n, 1));
+  get_device(is, res, st.codes.p, size_t(n) * st.row_bytes);
+  get_device(is, res, st.rowc.p, size_t(n) * 4);
+  if (!is_int(st.type)) {
+    st.center.resize_discard(size_t(st.dim) * sizeof(double));
+    st.maxima.resize_discard(2 * sizeof(double));
+    get_device(is, res, st.vectors.p, size_t(n) * size_t(st.dim) * elem_size(st.type));
+    get_device(is, res, st.center.p, size_t(st.dim) * sizeof(double));
+    get_device(is, res, st.maxima.p, 2 * sizeof(double));
+  }
+  if (labels) {
+    st.labels.resize_discard(size_t(st.capacity) * sizeof(int32_t));
+    get_device(is, res, st.labels.p, size_t(n) * sizeof(int32_t));
+    st.has_labels = true;
+  }
+  st.size = n;
+}
+
 #define CERTEX_INSTANTIATE(T)                                                                  \
   template class index<T>;                                                                     \
   template auto build<T>(cuvs::resources const&, index_params const&, matrix_view<const T>)    \
@@ -776,7 +923,9 @@ void search(cuvs::resources const& res, search_params const& params, index<T> co
   template void search<T>(cuvs::resources const&, search_params const&, index<T> const&,       \
                           matrix_view<const T>, int64_t*, float*, int64_t, filter);            \
   template void search<T>(cuvs::resources const&, search_params const&, index<T> const&,       \
-                          matrix_view<const T>, const int32_t*, int64_t*, float*, int64_t);
+                          matrix_view<const T>, const int32_t*, int64_t*, float*, int64_t);    \
+  template void serialize<T>(cuvs::resources const&, std::string const&, index<T> const&);     \
+  template void deserialize<T>(cuvs::resources const&, std::string const&, index<T>*);
 
 CERTEX_INSTANTIATE(float)
 CERTEX_INSTANTIATE(half_t)

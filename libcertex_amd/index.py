@@ -337,9 +337,21 @@ class Index:
         return _back(D, kind), _back(I, kind)
 
     def save(self, path):
-        """Write the index to a file (certex/index.py:361-365)."""
+        """Write the index to a file; load() restores it without rebuilding (certex/index.py:361-365)."""
         _require(self.core is not None, "add vectors first")
         C.check(C.lib().cuvsCertexSerialize(C.resources(), str(path).encode(), self.core.h))
+
+    @classmethod
+    def load(cls, path):
+        """An index saved by save() (certex/index.py:367-385)."""
+        with open(path, "rb") as f:
+            prefix = f.read(4)
+        _require(prefix[1:3] in _PREFIX, "not a certex index file")
+        core = _Core()
+        C.check(C.lib().cuvsCertexDeserialize(C.resources(), str(path).encode(), core.h))
+        idx = cls(core.dim, metric=core.metric, anchor_stride=core.anchor_stride)
+        idx.core = core
+        return idx
 
     def info(self):
         c = self.core
