@@ -20,6 +20,7 @@ ARCH = "gfx950"
 
 SOURCES = [
     "kernels/screen.hip",
+    "kernels/screen_wide.hip",
     "kernels/select.hip",
     "kernels/encode.hip",
     "certex.cpp",

@@ -386,6 +386,7 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   const int64_t size   = st.size;
   const int64_t nq_pad = certex_amd::pad_queries(B);
   const auto t         = elem_of(st.type);
+  const bool wide      = st.halves > 128;  // the K-loop screen
   fa.q0                = q0;
 
   auto* qrows =
@@ -414,12 +415,15 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
     certex_amd::screen_args aa = sa;
     aa.n_scan                  = ap.n_anchor;
     aa.row_stride              = ap.stride;
-    aa.chunk_steps             = int(4 * ap.group_steps * std::max<int64_t>(1, 16 / ap.group_steps));
+    aa.chunk_steps = int(wide ? 8 * ap.group_steps * std::max<int64_t>(1, 4 / ap.group_steps)
+                              : 4 * ap.group_steps * std::max<int64_t>(1, 16 / ap.group_steps));
     aa.gmax                    = gmax;
     aa.grow                    = grow;
     aa.n_groups                = ap.n_groups;
     aa.group_steps             = int(ap.group_steps);
-    timed(0, stream, [&] { certex_amd::anchors_f16(aa, stream); });
+    timed(0, stream, [&] {
+      (wide ? certex_amd::anchors_f16_wide : certex_amd::anchors_f16)(aa, stream);
+    });
     certex_amd::threshold_f_args ta{};
     ta.gmax      = gmax;
     ta.grow      = grow;
@@ -445,8 +449,9 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   int64_t cap = 0;
   if (!all_rows) {
     sa.theta = theta;
-    all_rows = !screen_into_buckets(res, B, nq_pad, size, sa, certex_amd::screen_f16, count,
-                                    rows, cap);
+    all_rows = !screen_into_buckets(res, B, nq_pad, size, sa,
+                                    wide ? certex_amd::screen_f16_wide : certex_amd::screen_f16,
+                                    count, rows, cap);
   }
   count_stats(res, st, B, all_rows, count, cap);
 
@@ -616,8 +621,8 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
     st.size = dataset.rows;
     return out;
   }
-  expects(dataset.cols <= 128,
-          "certex: float vectors of more than 128 coordinates are not supported by this build yet");
+  expects(dataset.cols <= certex_amd::kMaxF16Halves,
+          "certex: float vectors of more than 2048 coordinates are not supported by this build");
   hipStream_t stream = static_cast<hipStream_t>(res.stream());
   st.halves          = certex_amd::f16_row_halves(st.dim);
   st.row_bytes       = 2 * st.halves;

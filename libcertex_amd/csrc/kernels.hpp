@@ -118,6 +118,12 @@ void anchors_i8(const screen_args& a, hipStream_t stream);
 /** The same two passes over fp16 rows (f32 accumulation, certified threshold). */
 void screen_f16(const screen_args& a, hipStream_t stream);
 void anchors_f16(const screen_args& a, hipStream_t stream);
+/**
+ * The fp16 passes for rows of more than 128 halves (a multiple of 128, at most kMaxF16Halves):
+ * a K loop, workgroups of 8 waves; chunk_steps is a multiple of 8 (8 group_steps for anchors).
+ */
+void screen_f16_wide(const screen_args& a, hipStream_t stream);
+void anchors_f16_wide(const screen_args& a, hipStream_t stream);
 
 /**
  * theta[q] = the k-th largest of gmax[q, 0 .. n_groups) (kKeepAll when n_groups < k, and never
@@ -163,8 +169,21 @@ void verify_topk_i8(const verify_args& a, hipStream_t stream);
 
 enum class elem : int { f32 = 0, f16 = 1 };
 
-/** Row length (halves) of the fp16 screening rows for dimension dim: 64 or 128. */
-__host__ __device__ inline int f16_row_halves(int64_t dim) { return dim <= 64 ? 64 : 128; }
+/** Widest fp16 screening row (halves) of the screens. */
+constexpr int kMaxF16Halves = 2048;
+/**
+ * Row length (halves) of the fp16 screening rows for dimension dim: 64, 128, or dim rounded up
+ * to a multiple of 128 (rows of more than 128 halves use the K-loop screen).
+ */
+__host__ __device__ inline int f16_row_halves(int64_t dim)
+{
+  return dim <= 64 ? 64 : int((dim + 127) / 128 * 128);
+}
+/** Waves of a screen workgroup: 8 for the K-loop screen of wide fp16 rows, 4 otherwise. */
+__host__ __device__ inline int screen_waves(bool f16, int row_bytes)
+{
+  return f16 && row_bytes > 256 ? 8 : 4;
+}
 
 /**
  * sums[j] += sum over rows of x[i, j] (x normalised to unit length when `normalize`), in fp64;

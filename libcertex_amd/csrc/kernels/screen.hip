@@ -34,66 +34,18 @@
 // Survivors are compacted with a ballot + mbcnt rank and one LDS reservation per round into a
 // per-workgroup list, flushed to the per-query buckets at the end.
 
-#include "../kernels.hpp"
-
-#include <climits>
-#include <cmath>
+#include "screen_common.hpp"
 
 namespace certex_amd {
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-
-constexpr int kHitCap = 1024;
-
-struct int8_rows {
-  using acc_t  = v4i;
-  using frag_t = v4i;
-  using val_t  = int;
-  static constexpr bool kArgmax = false;
-  __device__ static acc_t mfma(frag_t a, frag_t b, acc_t c)
-  {
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-  }
-  __device__ static val_t lowest() { return INT_MIN; }
-  __device__ static val_t dead() { return kDeadRow; }
-  __device__ static val_t vmax(val_t a, val_t b) { return max(a, b); }
-};
-
-struct f16_rows {
-  using acc_t  = v4f;
-  using frag_t = v8h;
-  using val_t  = float;
-  static constexpr bool kArgmax = true;  // the float threshold scores the best anchor exactly
-  __device__ static acc_t mfma(frag_t a, frag_t b, acc_t c)
-  {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-  __device__ static val_t lowest() { return -INFINITY; }
-  __device__ static val_t dead() { return -INFINITY; }
-  __device__ static val_t vmax(val_t a, val_t b) { return fmaxf(a, b); }
-};
+using namespace screen_detail;
 
 /** 16-byte chunk slot of chunk c of row r (conflict-free ds_read_b128 of 16 rows x 1 chunk). */
 template <int KS>
 __device__ __forceinline__ int slot(int r, int c)
 {
   return KS == 2 ? (c ^ (r & 7)) : (c ^ (r & 15));
-}
-
-__device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
-{
-  switch (f.kind) {
-    case 1: return (f.words[row >> 5] >> (row & 31)) & 1u;
-    case 2: {
-      const int64_t bit = (f.q0 + q) * f.bitmap_ld + row;
-      return (f.words[bit >> 5] >> (bit & 31)) & 1u;
-    }
-    case 3: return f.row_labels[row] == f.query_labels[f.q0 + q];
-    default: return true;
-  }
 }
 
 template <typename R, int KS, int QB, bool ANCHORS, bool FILT>
@@ -113,6 +65,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   __shared__ uint32_t hit_q[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t hit_row[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t n_hits;
+  const hit_list hits{hit_q, hit_row, &n_hits};
 
   const val_t* rowc  = static_cast<const val_t*>(a.rowc);
   const val_t* theta = static_cast<const val_t*>(a.theta);
@@ -131,6 +84,10 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   const int64_t chunk    = int64_t(i / uint32_t(n_qb)) * 8 + (b & 7);
   if (chunk >= n_chunks) { return; }
   const int64_t q0 = int64_t(qb) * QB;
+  // groups of 64 queries holding a live query, rounded up to a pair (the last query block of a
+  // batch is partly padding)
+  const int64_t live = a.nq - q0;
+  const int ng       = live >= QB ? NG : int(((live + 63) / 64 + 1) & ~int64_t(1));
   // this wave's steps: a contiguous quarter of the chunk (a whole number of anchor groups)
   const int64_t quarter = a.chunk_steps / 4;
   const int64_t w0      = chunk * a.chunk_steps + wave * quarter;
@@ -207,58 +164,9 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     if constexpr (ANCHORS) {
 #pragma unroll
       for (int qt = 0; qt < 4; ++qt) {
-        val_t m    = R::lowest();
-        uint32_t j = 0;
-#pragma unroll
-        for (int bt = 0; bt < 4; ++bt) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            val_t v = acc[bt][qt][r];
-            if constexpr (FILT) {
-              const int64_t idx = row0 + bt * 16 + r;
-              if (idx < a.n_scan &&
-                  !keeps(a.filter, q0 + g * 64 + qt * 16 + (lane & 15),
-                         uint32_t(idx * a.row_stride))) {
-                v = R::lowest();
-              }
-            }
-            if constexpr (ARGMX) {
-              if (v > m) {
-                m = v;
-                j = uint32_t(bt * 16 + r);
-              }
-            } else {
-              m = R::vmax(m, v);
-            }
-          }
-        }
-        if constexpr (ARGMX) {
-          // best (value, row) of the query over the 64 rows of the step; ties to the lower row
-          uint32_t row = uint32_t((row0 + j) * a.row_stride);
-#pragma unroll
-          for (int off = 16; off <= 32; off <<= 1) {
-            const val_t om     = __shfl_xor(m, off);
-            const uint32_t orw = uint32_t(__shfl_xor(int(row), off));
-            if (om > m || (om == m && orw < row)) {
-              m   = om;
-              row = orw;
-            }
-          }
-          if (lane < 16) {
-            const int e = wave * QB + g * 64 + qt * 16 + lane;
-            if (m > gml[e] || (m == gml[e] && row < gmr[e])) {
-              gml[e] = m;
-              gmr[e] = row;
-            }
-          }
-        } else {
-          m = R::vmax(m, __shfl_xor(m, 16));
-          m = R::vmax(m, __shfl_xor(m, 32));
-          if (lane < 16) {
-            val_t* p = gml + wave * QB + g * 64 + qt * 16 + lane;
-            *p       = R::vmax(*p, m);
-          }
-        }
+        const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
+        anchor_tile<R, FILT>(col, row0, q0 + g * 64 + qt * 16 + (lane & 15),
+                             wave * QB + g * 64 + qt * 16 + lane, a, gml, gmr);
       }
     } else {
       val_t mq[4];
@@ -287,41 +195,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
             }
           }
           const uint32_t qloc = uint32_t(g * 64 + qt * 16 + (lane & 15));
-          if constexpr (FILT) {
-            uint32_t scan = bits;
-            while (scan) {
-              const int j = __builtin_ctz(scan);
-              scan &= scan - 1;
-              const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
-              if (!keeps(a.filter, q0 + qloc, row)) { bits &= ~(1u << j); }
-            }
-          }
-          // compaction: one round per survivor of the busiest lane; ballot, rank by mbcnt,
-          // one LDS reservation per round
-          while (true) {
-            const uint64_t mask = __ballot(bits != 0);
-            if (mask == 0) { break; }
-            const uint32_t rank = __builtin_amdgcn_mbcnt_hi(
-              uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0u));
-            const int leader = __builtin_ctzll(mask);
-            uint32_t base    = 0;
-            if (lane == leader) { base = atomicAdd(&n_hits, uint32_t(__builtin_popcountll(mask))); }
-            base = __builtin_amdgcn_readlane(base, leader);
-            if (bits) {
-              const int j = __builtin_ctz(bits);
-              bits &= bits - 1;
-              const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
-              const uint32_t pos = base + rank;
-              if (pos < uint32_t(kHitCap)) {
-                hit_q[pos]   = qloc;
-                hit_row[pos] = row;
-              } else {  // LDS list full: straight to the global bucket
-                const int64_t q       = q0 + qloc;
-                const uint32_t bslot  = atomicAdd(a.cand_count + q, 1u);
-                if (bslot < a.cap) { a.cand_rows[q * a.cap + bslot] = row; }
-              }
-            }
-          }
+          push_hits<FILT>(bits, qloc, row0, q0, a, hits);
         }
       }
     }
@@ -334,10 +208,10 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     load_rows(s);
     row0 = s * kStepRows + (lane >> 4) * 4;
 #pragma unroll 1
-    for (int g = 0; g < NG; g += 2) {
+    for (int g = 0; g < ng; g += 2) {
       read_queries(g + 1, b1, t1);
       group(g, b0, t0);
-      read_queries(g + 2 < NG ? g + 2 : 0, b0, t0);
+      read_queries(g + 2 < ng ? g + 2 : 0, b0, t0);
       group(g + 1, b1, t1);
     }
     if constexpr (ANCHORS) {
@@ -358,12 +232,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 
   if constexpr (!ANCHORS) {
     __syncthreads();
-    const uint32_t nh = n_hits < uint32_t(kHitCap) ? n_hits : uint32_t(kHitCap);
-    for (uint32_t e = tid; e < nh; e += 256) {
-      const int64_t q      = q0 + hit_q[e];
-      const uint32_t bslot = atomicAdd(a.cand_count + q, 1u);
-      if (bslot < a.cap) { a.cand_rows[q * a.cap + bslot] = hit_row[e]; }
-    }
+    flush_hits(q0, a, hits);
   }
 }
 

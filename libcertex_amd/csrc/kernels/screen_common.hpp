@@ -1,0 +1,189 @@
+// Pieces shared by the MFMA screens (screen.hip: rows of up to 256 bytes with the queries of a
+// workgroup resident in LDS; screen_wide.hip: fp16 rows of more than 128 halves, K loop).
+//
+// MFMA tile: operand A holds 16 stored rows and operand B 16 queries, so lane l owns query l % 16
+// and rows 4 (l / 16) + r, r = 0..3, of the tile. A step is 64 rows = 4 row tiles (bt); bit
+// bt * 4 + r of a lane's survivor mask marks row row0 + bt * 16 + r, with row0 = the step's first
+// row + 4 (l / 16).
+#pragma once
+
+#include "../kernels.hpp"
+
+#include <climits>
+#include <cmath>
+
+namespace certex_amd::screen_detail {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+/** Survivors a workgroup gathers in LDS before it flushes them to the per-query buckets. */
+constexpr int kHitCap = 1024;
+
+struct int8_rows {
+  using acc_t  = v4i;
+  using frag_t = v4i;
+  using val_t  = int;
+  static constexpr bool kArgmax = false;
+  __device__ static acc_t mfma(frag_t a, frag_t b, acc_t c)
+  {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  }
+  __device__ static val_t lowest() { return INT_MIN; }
+  __device__ static val_t dead() { return kDeadRow; }
+  __device__ static val_t vmax(val_t a, val_t b) { return max(a, b); }
+};
+
+struct f16_rows {
+  using acc_t  = v4f;
+  using frag_t = v8h;
+  using val_t  = float;
+  static constexpr bool kArgmax = true;  // the float threshold scores the best anchor exactly
+  __device__ static acc_t mfma(frag_t a, frag_t b, acc_t c)
+  {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static val_t lowest() { return -INFINITY; }
+  __device__ static val_t dead() { return -INFINITY; }
+  __device__ static val_t vmax(val_t a, val_t b) { return fmaxf(a, b); }
+};
+
+/** Filter test of a pair (query q of the batch, stored row). */
+__device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
+{
+  switch (f.kind) {
+    case 1: return (f.words[row >> 5] >> (row & 31)) & 1u;
+    case 2: {
+      const int64_t bit = (f.q0 + q) * f.bitmap_ld + row;
+      return (f.words[bit >> 5] >> (bit & 31)) & 1u;
+    }
+    case 3: return f.row_labels[row] == f.query_labels[f.q0 + q];
+    default: return true;
+  }
+}
+
+/** LDS survivor list of a workgroup. */
+struct hit_list {
+  uint32_t* q;
+  uint32_t* row;
+  uint32_t* n;
+};
+
+/**
+ * Appends the survivors of one 16-query tile of a step to the workgroup's list: `bits` is this
+ * lane's survivor mask, `qloc` its query within the workgroup. One round per survivor of the
+ * busiest lane: ballot, rank by mbcnt, one LDS reservation per round; a full list spills straight
+ * into the global bucket. Every lane of the wave must call it.
+ */
+template <bool FILT>
+__device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t row0, int64_t q0,
+                                          const screen_args& a, hit_list h)
+{
+  if constexpr (FILT) {
+    uint32_t scan = bits;
+    while (scan) {
+      const int j = __builtin_ctz(scan);
+      scan &= scan - 1;
+      const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
+      if (!keeps(a.filter, q0 + qloc, row)) { bits &= ~(1u << j); }
+    }
+  }
+  const int lane = threadIdx.x & 63;
+  while (true) {
+    const uint64_t mask = __ballot(bits != 0);
+    if (mask == 0) { break; }
+    const uint32_t rank =
+      __builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0u));
+    const int leader = __builtin_ctzll(mask);
+    uint32_t base    = 0;
+    if (lane == leader) { base = atomicAdd(h.n, uint32_t(__builtin_popcountll(mask))); }
+    base = __builtin_amdgcn_readlane(base, leader);
+    if (bits) {
+      const int j = __builtin_ctz(bits);
+      bits &= bits - 1;
+      const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
+      const uint32_t pos = base + rank;
+      if (pos < uint32_t(kHitCap)) {
+        h.q[pos]   = qloc;
+        h.row[pos] = row;
+      } else {
+        const int64_t q      = q0 + qloc;
+        const uint32_t bslot = atomicAdd(a.cand_count + q, 1u);
+        if (bslot < a.cap) { a.cand_rows[q * a.cap + bslot] = row; }
+      }
+    }
+  }
+}
+
+/** Flushes the workgroup's LDS survivor list to the per-query buckets (after a barrier). */
+__device__ inline void flush_hits(int64_t q0, const screen_args& a, hit_list h)
+{
+  const uint32_t nh = *h.n < uint32_t(kHitCap) ? *h.n : uint32_t(kHitCap);
+  for (uint32_t e = threadIdx.x; e < nh; e += blockDim.x) {
+    const int64_t q      = q0 + h.q[e];
+    const uint32_t bslot = atomicAdd(a.cand_count + q, 1u);
+    if (bslot < a.cap) { a.cand_rows[q * a.cap + bslot] = h.row[e]; }
+  }
+}
+
+/**
+ * Anchor pass, one 16-query tile of a 64-row step: folds the best screen value of this lane's
+ * query over the step (and, for fp16 rows, the stored row holding it, ties to the lower row) into
+ * the wave's running group maximum gml[e] / gmr[e] (e = the query's slot). `col[bt]` holds the
+ * tile's accumulators of row tile bt. Scan indices at or past n_scan are padding.
+ */
+template <typename R, bool FILT>
+__device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], int64_t row0,
+                                            int64_t q, int e, const screen_args& a,
+                                            typename R::val_t* gml, uint32_t* gmr)
+{
+  using val_t         = typename R::val_t;
+  constexpr bool ARGX = R::kArgmax;
+  const int lane      = threadIdx.x & 63;
+  val_t m             = R::lowest();
+  uint32_t j          = 0;
+#pragma unroll
+  for (int bt = 0; bt < 4; ++bt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      val_t v = col[bt][r];
+      if constexpr (FILT) {
+        const int64_t idx = row0 + bt * 16 + r;
+        if (idx < a.n_scan && !keeps(a.filter, q, uint32_t(idx * a.row_stride))) {
+          v = R::lowest();
+        }
+      }
+      if constexpr (ARGX) {
+        if (v > m) {
+          m = v;
+          j = uint32_t(bt * 16 + r);
+        }
+      } else {
+        m = R::vmax(m, v);
+      }
+    }
+  }
+  if constexpr (ARGX) {
+    uint32_t row = uint32_t((row0 + j) * a.row_stride);
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+      const val_t om     = __shfl_xor(m, off);
+      const uint32_t orw = uint32_t(__shfl_xor(int(row), off));
+      if (om > m || (om == m && orw < row)) {
+        m   = om;
+        row = orw;
+      }
+    }
+    if (lane < 16 && (m > gml[e] || (m == gml[e] && row < gmr[e]))) {
+      gml[e] = m;
+      gmr[e] = row;
+    }
+  } else {
+    m = R::vmax(m, __shfl_xor(m, 16));
+    m = R::vmax(m, __shfl_xor(m, 32));
+    if (lane < 16) { gml[e] = R::vmax(gml[e], m); }
+  }
+}
+
+}  // namespace certex_amd::screen_detail

@@ -1,0 +1,317 @@
+// fp16 certified screen for rows of more than 128 halves (gfx950): a K loop over the coordinates.
+//
+// Reference contract: detail/screen_sm80.cu:117-379 and detail/screen_sm90.cu:594-785 (fp16 MMA,
+// fp32 accumulation, keep a pair iff its screen value reaches the query threshold) and the anchor
+// pass of detail/kernels.hpp:125-135. The certificate is the one of screen.hip: the row term
+// enters as the accumulator's initial value and the host folds every rounding error into the
+// row term and the threshold, so the test needs no per-pair arithmetic.
+//
+// Work decomposition:
+// - a workgroup of 8 waves holds QB = 16 QT queries (all their halves) in LDS for its whole life,
+//   16-byte chunks XOR-swizzled by the query (chunk c of query r sits in slot c ^ (r & 15)), so
+//   the ds_read_b128 of a 16-query fragment is free of bank conflicts;
+// - each wave streams its own contiguous eighth of a chunk of stored rows, 64 rows per step, and
+//   runs the K loop in chunks of 64 halves; the next chunk's row fragments are loaded into a
+//   second register set while the MFMAs of the current chunk run. No barrier in the main loop.
+// - within a 64-half chunk, lane group g = lane / 16 supplies halves 16 g .. 16 g + 7 to the first
+//   v_mfma_f32_16x16x32_f16 and 16 g + 8 .. 16 g + 15 to the second, in both operands (a
+//   permutation of the summation order), so a lane's row fragment is 32 contiguous bytes and the
+//   four lane groups read whole 128-byte lines;
+// - block b runs on XCD b % 8; the query blocks of one row chunk run on one XCD together.
+// Survivors go through the ballot + mbcnt compaction of screen_common.hpp.
+
+#include "screen_common.hpp"
+
+#include <stdexcept>
+
+namespace certex_amd {
+namespace {
+
+using namespace screen_detail;
+
+constexpr int kWideWaves = 8;
+
+/** Pointers into global memory, so that loads through them stay global (never flat) loads. */
+typedef const __attribute__((address_space(1))) int8_t* gbytes;
+
+__device__ __forceinline__ v8h gload(gbytes p)
+{
+  return *reinterpret_cast<const __attribute__((address_space(1))) v8h*>(p);
+}
+
+template <int QT, bool ANCHORS, bool FILT>
+__global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_args a)
+{
+  using R      = f16_rows;
+  using acc_t  = v4f;
+  using frag_t = v8h;
+  constexpr int QB = 16 * QT;
+  extern __shared__ __attribute__((aligned(16))) uint8_t qlds[];  // [QB][H] halves, swizzled
+  __shared__ float thl[ANCHORS ? 1 : QB];
+  __shared__ float gml[ANCHORS ? kWideWaves * QB : 1];
+  __shared__ uint32_t gmr[ANCHORS ? kWideWaves * QB : 1];
+  __shared__ uint32_t hit_q[ANCHORS ? 1 : kHitCap];
+  __shared__ uint32_t hit_row[ANCHORS ? 1 : kHitCap];
+  __shared__ uint32_t n_hits;
+  const hit_list hits{hit_q, hit_row, &n_hits};
+
+  const float* rowc  = static_cast<const float*>(a.rowc);
+  const float* theta = static_cast<const float*>(a.theta);
+  float* gmax        = static_cast<float*>(a.gmax);
+
+  const int tid   = threadIdx.x;
+  const int lane  = tid & 63;
+  const int wave  = tid >> 6;
+  const int H     = a.row_bytes / 2;  // halves per row, a multiple of 128
+  const int NC    = H / 64;           // K chunks, even
+  const int RB    = a.row_bytes;      // bytes per row (stored rows and LDS query rows)
+
+  const int64_t n_steps  = screen_steps(a.n_scan);
+  const int64_t n_chunks = (n_steps + a.chunk_steps - 1) / a.chunk_steps;
+  const int n_qb         = int((a.nq + QB - 1) / QB);
+  const uint32_t b       = blockIdx.x;
+  const uint32_t i       = b >> 3;
+  const int qb           = int(i % uint32_t(n_qb));
+  const int64_t chunk    = int64_t(i / uint32_t(n_qb)) * 8 + (b & 7);
+  if (chunk >= n_chunks) { return; }
+  const int64_t q0     = int64_t(qb) * QB;
+  const int64_t eighth = a.chunk_steps / kWideWaves;  // whole anchor groups
+  const int64_t w0     = chunk * a.chunk_steps + wave * eighth;
+  const int64_t w1     = w0 + eighth < n_steps ? w0 + eighth : n_steps;
+
+  if (tid == 0) { n_hits = 0; }
+  const int cpr = RB / 16;  // 16-byte chunks per row
+  for (int e = tid; e < QB * cpr; e += 64 * kWideWaves) {
+    const int r = e / cpr, c = e % cpr;
+    v4i v       = {0, 0, 0, 0};
+    if (q0 + r < a.nq) { v = *reinterpret_cast<const v4i*>(a.qcodes + (q0 + r) * RB + 16 * c); }
+    *reinterpret_cast<v4i*>(qlds + r * RB + 16 * (c ^ (r & 15))) = v;
+  }
+  if constexpr (ANCHORS) {
+    for (int e = tid; e < kWideWaves * QB; e += 64 * kWideWaves) {
+      gml[e] = R::lowest();
+      gmr[e] = 0xffffffffu;
+    }
+  } else {
+    for (int e = tid; e < QB; e += 64 * kWideWaves) {
+      // a padding query keeps nothing: no value compares >= NaN (not even a +inf row term)
+      thl[e] = q0 + e < a.nq ? theta[q0 + e] : __builtin_nanf("");
+    }
+  }
+  __syncthreads();
+
+  frag_t av[2][4][2];  // [buffer][row tile][first / second MFMA of the chunk]
+  acc_t cc[4];
+  // Every load of the main loop is unconditional (indices are clamped instead), so that the
+  // compiler's wait counts see one straight path and the prefetches stay in flight.
+  const gbytes codes = (gbytes)a.codes;
+  auto bases = [&](int64_t s, gbytes (&P)[4]) {
+#pragma unroll
+    for (int bt = 0; bt < 4; ++bt) {
+      int64_t r = s * kStepRows + bt * 16 + (lane & 15);
+      r         = r < a.n_scan ? r : 0;  // rows past the end read row 0; their term kills them
+      P[bt]     = codes + r * a.row_stride * RB + (lane >> 4) * 32;
+    }
+  };
+  auto load_chunk = [&](const gbytes (&P)[4], int64_t off, frag_t (&A)[4][2]) {
+#pragma unroll
+    for (int bt = 0; bt < 4; ++bt) {
+      A[bt][0] = gload(P[bt] + off);
+      A[bt][1] = gload(P[bt] + off + 16);
+    }
+  };
+  auto load_terms = [&](int64_t s) {
+#pragma unroll
+    for (int bt = 0; bt < 4; ++bt) {
+      const int64_t r4 = s * kStepRows + bt * 16 + (lane >> 4) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool ok  = r4 + j < a.n_scan;
+        const float v  = rowc[(ok ? r4 + j : 0) * a.row_stride];
+        cc[bt][j]      = ok ? v : R::dead();
+      }
+    }
+  };
+
+  acc_t acc[4][QT];
+  auto compute = [&](int c, const frag_t (&A)[4][2]) {
+    const uint8_t* qbase = qlds + (lane & 15) * RB;
+    const int c0         = c * 8 + (lane >> 4) * 2;  // this lane's first 16-byte chunk
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int r         = qt * 16 + (lane & 15);
+      const uint8_t* qrow = qbase + qt * 16 * RB;
+      const frag_t b0     = *reinterpret_cast<const frag_t*>(qrow + 16 * ((c0) ^ (r & 15)));
+      const frag_t b1     = *reinterpret_cast<const frag_t*>(qrow + 16 * ((c0 + 1) ^ (r & 15)));
+#pragma unroll
+      for (int bt = 0; bt < 4; ++bt) {
+        acc[bt][qt] = R::mfma(A[bt][0], b0, acc[bt][qt]);
+        acc[bt][qt] = R::mfma(A[bt][1], b1, acc[bt][qt]);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  gbytes P[4];
+  gbytes PN[4];
+  bases(w0, P);
+  load_chunk(P, 0, av[0]);
+  load_terms(w0);
+  for (int64_t s = w0; s < w1; ++s) {
+#pragma unroll
+    for (int bt = 0; bt < 4; ++bt) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = cc[bt]; }
+    }
+    // the next step's rows and terms (the last step reloads its own)
+    const int64_t sn = s + 1 < w1 ? s + 1 : s;
+    bases(sn, PN);
+    load_terms(sn);
+#pragma unroll 1
+    for (int c = 0; c < NC; c += 2) {
+      load_chunk(P, int64_t(c + 1) * 128, av[1]);
+      compute(c, av[0]);
+      const bool last = c + 2 >= NC;
+      gbytes Q[4];
+#pragma unroll
+      for (int bt = 0; bt < 4; ++bt) { Q[bt] = last ? PN[bt] : P[bt] + int64_t(c + 2) * 128; }
+      load_chunk(Q, 0, av[0]);
+      compute(c + 1, av[1]);
+    }
+#pragma unroll
+    for (int bt = 0; bt < 4; ++bt) { P[bt] = PN[bt]; }
+
+    const int64_t row0 = s * kStepRows + (lane >> 4) * 4;
+    if constexpr (ANCHORS) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
+        anchor_tile<R, FILT>(col, row0, q0 + qt * 16 + (lane & 15), wave * QB + qt * 16 + lane, a,
+                             gml, gmr);
+      }
+      // end of an anchor group (group_steps steps, aligned to the wave's range)
+      if ((s + 1) % a.group_steps == 0 || s + 1 == n_steps) {
+        const int64_t grp = s / a.group_steps;
+        for (int e = lane; e < QB; e += 64) {
+          if (q0 + e < a.nq) {
+            gmax[(q0 + e) * a.n_groups + grp]   = gml[wave * QB + e];
+            a.grow[(q0 + e) * a.n_groups + grp] = gmr[wave * QB + e];
+          }
+          gml[wave * QB + e] = R::lowest();
+          gmr[wave * QB + e] = 0xffffffffu;
+        }
+      }
+    } else {
+      float mq[QT];
+      bool hit = false;
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        float m = acc[0][qt][0];
+#pragma unroll
+        for (int bt = 0; bt < 4; ++bt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) { m = fmaxf(m, acc[bt][qt][r]); }
+        }
+        mq[qt] = m;
+        hit |= m >= thl[qt * 16 + (lane & 15)];
+      }
+      if (__builtin_expect(__any(hit), 0)) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const float th = thl[qt * 16 + (lane & 15)];
+          if (!__any(mq[qt] >= th)) { continue; }
+          uint32_t bits = 0;
+#pragma unroll
+          for (int bt = 0; bt < 4; ++bt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              bits |= uint32_t(acc[bt][qt][r] >= th) << (bt * 4 + r);
+            }
+          }
+          push_hits<FILT>(bits, uint32_t(qt * 16 + (lane & 15)), row0, q0, a, hits);
+        }
+      }
+    }
+  }
+
+  if constexpr (!ANCHORS) {
+    __syncthreads();
+    flush_hits(q0, a, hits);
+  }
+}
+
+template <int QT, bool ANCHORS, bool FILT>
+void launch_qt(const screen_args& a, dim3 grid, size_t lds, hipStream_t stream)
+{
+  auto* k = &screen_wide_kernel<QT, ANCHORS, FILT>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess) {
+    (void)hipGetLastError();
+    throw std::runtime_error("certex: the wide screen cannot reserve its LDS");
+  }
+  k<<<grid, 64 * kWideWaves, lds, stream>>>(a);
+}
+
+/**
+ * Query tiles of a workgroup for rows of `row_bytes`: the largest of 6, 4, 2 whose queries and
+ * static arrays fit the LDS of a workgroup (0: none fits).
+ */
+int wide_query_tiles(int row_bytes)
+{
+  static const int max_lds = [] {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      return 65536;
+    }
+    return v;
+  }();
+  const int fixed = 2 * kHitCap * 4 + kWideWaves * 16 * 6 * 8 + 1024;  // static arrays, margin
+  for (int qt : {6, 4, 2}) {
+    if (16 * qt * row_bytes + fixed <= max_lds) { return qt; }
+  }
+  return 0;
+}
+
+template <bool ANCHORS, bool FILT>
+void launch(const screen_args& a, hipStream_t stream)
+{
+  const int qt           = wide_query_tiles(a.row_bytes);
+  const int qb           = 16 * qt;
+  const int64_t n_steps  = screen_steps(a.n_scan);
+  const int64_t n_chunks = (n_steps + a.chunk_steps - 1) / a.chunk_steps;
+  const int64_t n_qb     = (a.nq + qb - 1) / qb;
+  if (n_steps == 0 || n_qb == 0) { return; }
+  if (qt == 0) { throw std::invalid_argument("certex: the fp16 rows are too wide for the LDS"); }
+  const dim3 grid{unsigned(8 * n_qb * ((n_chunks + 7) / 8))};
+  const size_t lds = size_t(qb) * size_t(a.row_bytes);
+  switch (qt) {
+    case 6: launch_qt<6, ANCHORS, FILT>(a, grid, lds, stream); break;
+    case 4: launch_qt<4, ANCHORS, FILT>(a, grid, lds, stream); break;
+    default: launch_qt<2, ANCHORS, FILT>(a, grid, lds, stream); break;
+  }
+}
+
+}  // namespace
+
+void screen_f16_wide(const screen_args& a, hipStream_t stream)
+{
+  if (a.filter.kind != 0) {
+    launch<false, true>(a, stream);
+  } else {
+    launch<false, false>(a, stream);
+  }
+}
+
+void anchors_f16_wide(const screen_args& a, hipStream_t stream)
+{
+  if (a.filter.kind != 0) {
+    launch<true, true>(a, stream);
+  } else {
+    launch<true, false>(a, stream);
+  }
+}
+
+}  // namespace certex_amd

@@ -28,3 +28,22 @@ def uniform_int(n, d, seed, dtype=np.uint8, lo=None, hi=None):
     lo = info.min if lo is None else lo
     hi = info.max if hi is None else hi
     return np.random.default_rng(seed).integers(lo, hi + 1, (n, d)).astype(dtype)
+
+
+def powerlaw_unit(n, d, seed, basis_seed=31, dtype=np.float32, chunk=1 << 15):
+    """Embedding-like rows (config 3): Gaussian with covariance eigenvalues lambda_i ~ 1 / i
+    (i = 1..d) in a random orthogonal basis (seeded by basis_seed), then L2-normalised."""
+    q, _ = np.linalg.qr(np.random.default_rng(basis_seed).standard_normal((d, d)))
+    m = (np.sqrt(1.0 / np.arange(1, d + 1))[:, None] * q.T).astype(np.float32)
+    rng = np.random.default_rng(seed)
+    out = np.empty((n, d), dtype)
+    for i in range(0, n, chunk):
+        r = min(chunk, n - i)
+        x = rng.standard_normal((r, d), dtype=np.float32) @ m
+        out[i : i + r] = (x / np.linalg.norm(x, axis=1, keepdims=True)).astype(dtype)
+    return out
+
+
+def labels(n, n_classes, seed):
+    """uint32-valued labels uniform over n_classes (stored as int32, as the index takes them)."""
+    return np.random.default_rng(seed).integers(0, n_classes, n).astype(np.int32)

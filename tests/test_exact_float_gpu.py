@@ -124,3 +124,58 @@ def test_config1_shape(gpu):
     Q = data.gaussian(1_000, 128, 12)
     D, I, _ = run(X, Q, 10)
     check(X, Q, 10, "l2", D, I)
+
+
+# --- rows of more than 128 halves: the K-loop screen ------------------------------------------
+
+
+@pytest.mark.parametrize("d", [129, 200, 256, 384, 768])
+def test_wide_dims_l2(gpu, d):
+    X, Q = correlated(6_007, d, 211, seed=d)
+    D, I, _ = run(X, Q, 10)
+    check(X, Q, 10, "l2", D, I)
+
+
+@pytest.mark.parametrize("metric", ["ip", "cosine"])
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_wide_metrics(gpu, metric, dtype):
+    X, Q = correlated(8_000, 300, 150, seed=3)
+    X, Q = X.astype(dtype), Q.astype(dtype)
+    D, I, _ = run(X, Q, 25, metric)
+    check(X, Q, 25, metric, D, I)
+
+
+def test_wide_largest_rows(gpu):
+    """1,000 and 2,048 coordinates: fewer queries per workgroup (the LDS holds whole queries)."""
+    for d in (1000, 2048):
+        X, Q = correlated(3_000, d, 70, seed=d)
+        D, I, _ = run(X, Q, 7)
+        check(X, Q, 7, "l2", D, I)
+
+
+def test_wide_remove_filter_ties(gpu):
+    X, Q = correlated(12_000, 256, 97, seed=21)
+    X = np.concatenate([X, X[:500]])  # exact duplicates: ties go to the lower id
+    idx = certex.Index(256)
+    idx.add(torch.from_numpy(X).cuda())
+    gone = np.arange(0, 12_500, 7)
+    idx.remove(torch.from_numpy(gone))
+    removed = np.zeros(len(X), np.uint8)
+    removed[gone] = 1
+    keep = np.random.default_rng(2).random(len(X)) < 0.3
+    D, I = idx.search(torch.from_numpy(Q).cuda(), k=12, filter=torch.from_numpy(keep))
+    check(X, Q, 12, "l2", D.cpu().numpy(), I.cpu().numpy(), removed=(removed | ~keep).astype(np.uint8))
+
+
+def test_config3_shape_labels(gpu):
+    """Config 3's kind of data at reduced size: power-law spectrum embeddings, L2-normalised,
+    768 coordinates, cosine, k = 100, one of 16 labels per vector and per query; the batch is
+    ragged (1,000 queries in batches of 384)."""
+    X = data.powerlaw_unit(60_000, 768, seed=41)
+    Q = data.powerlaw_unit(1_000, 768, seed=42)
+    lx, lq = data.labels(len(X), 16, 43), data.labels(len(Q), 16, 44)
+    idx = certex.Index(768, metric="cosine")
+    idx.add(torch.from_numpy(X).cuda(), labels=torch.from_numpy(lx))
+    D, I = idx.search(torch.from_numpy(Q).cuda(), k=100, batch=384, labels=torch.from_numpy(lq))
+    torch.cuda.synchronize()
+    check(X, Q, 100, "cosine", D.cpu().numpy(), I.cpu().numpy(), row_labels=lx, query_labels=lq)
