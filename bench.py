@@ -24,6 +24,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 P_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA peak, 10^12 ops/s
+P_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA peak
 HBM_GBS = 8000.0
 
 
@@ -39,17 +40,132 @@ def mixture_u8(n, d, n_centres, centres, seed, device):
     return out
 
 
+def powerlaw_unit(n, d, seed, basis, device):
+    """Config 3 rows: Gaussian with covariance eigenvalues ~ 1 / i in the orthogonal basis, then
+    L2-normalised (torch generator seeded `seed`)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    out = torch.empty((n, d), dtype=torch.float32, device=device)
+    step = 1 << 17
+    for i in range(0, n, step):
+        m = min(step, n - i)
+        x = torch.randn((m, d), generator=g, device=device) @ basis
+        out[i : i + m] = x / x.norm(dim=1, keepdim=True)
+    return out
+
+
+def timed_steps(step, steps, warmup):
+    """Runs warmup + steps calls of step(); returns (ms per step, kernel ms per phase, launches)."""
+    from libcertex_amd import _capi as C
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    L = C.lib()
+    C.check(L.cuvsCertexTimingBegin())
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (ctypes.c_double * 4)()
+    launches = (ctypes.c_int64 * 4)()
+    C.check(L.cuvsCertexTimingEnd(ms, launches))
+    return (t1 - t0) * 1000.0 / steps, list(ms), list(launches)
+
+
+PHASES = ("anchors", "threshold", "screen", "verify_topk")
+
+
+def bench_config3(args):
+    """Config 3: exact 100-NN, cosine, 1,000,000 x 768 fp32 power-law embeddings, 10,000 queries,
+    one of 16 labels per vector and per query (label-filtered search), fp16 MFMA screen."""
+    import libcertex_amd as certex
+
+    dev = torch.device("cuda:0")
+    n, d, nq, k = args.n or 1_000_000, args.dim or 768, args.nq, args.k or 100
+    qm, _ = torch.linalg.qr(torch.randn((d, d), generator=torch.Generator().manual_seed(31), dtype=torch.float64))
+    basis = (torch.sqrt(1.0 / torch.arange(1, d + 1, dtype=torch.float64))[:, None] * qm.T).float().to(dev)
+    X = powerlaw_unit(n, d, 32, basis, dev)
+    Q = powerlaw_unit(nq, d, 33, basis, dev)
+    gl = torch.Generator(device=dev).manual_seed(34)
+    lx = torch.randint(0, 16, (n,), generator=gl, device=dev, dtype=torch.int32)
+    lq = torch.randint(0, 16, (nq,), generator=gl, device=dev, dtype=torch.int32)
+    idx = certex.Index(d, metric="cosine")
+    idx.add(X, labels=lx)
+    torch.cuda.synchronize()
+    batch = args.batch or 2048
+
+    def step():
+        return idx.search(Q, k=k, batch=batch, labels=lq)
+
+    ms_step, ms, launches = timed_steps(step, args.steps, args.warmup)
+    with certex.search_stats() as st:
+        D, I = step()
+    torch.cuda.synchronize()
+    halves = (d + 127) // 128 * 128
+    screen_ms = ms[2] / max(1, launches[2])
+    flops_per_launch = 2.0 * n * halves * nq / max(1, launches[2] // args.steps)
+    achieved = flops_per_launch / (screen_ms / 1000.0) / 1e12
+    cpu = None
+    if not args.no_cpu:
+        import numpy as np
+
+        import oracle
+
+        cq = args.cpu_queries
+        t0 = time.perf_counter()
+        s_cpu, i_cpu = oracle.knn(X.cpu().numpy(), Q[:cq].cpu().numpy(), k, "cosine",
+                                  row_labels=lx.cpu().numpy(), query_labels=lq[:cq].cpu().numpy())
+        tc = time.perf_counter() - t0
+        agree = bool(np.array_equal(i_cpu, I[:cq].cpu().numpy()))
+        cpu = {"value": round(cq / tc, 3), "unit": "queries/s", "cores": oracle.threads(), "kind": "port",
+               "sample": f"first {cq} of the {nq} queries, exhaustive fp64 over all {n} rows with the label "
+               f"filter (oracle/oracle.c, OpenMP), {tc:.1f} s; ids equal to the GPU's: {agree}"}
+    return {
+        "metric": "exact 100-NN queries/sec, 1M x 768 fp32 cosine, 16 labels, 1 MI355X",
+        "value": round(nq / (ms_step / 1000.0), 1),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 screen, f64 re-rank",
+        "data": "synthetic (config 3 power-law embeddings, torch generators seeded 31/32/33/34)",
+        "config": {
+            "workload": f"config 3: exact {k}-NN, cosine, base {n} x {d} fp32, {nq} queries, 16 labels",
+            "n": n, "dim": d, "n_queries": nq, "k": k, "batch": batch,
+            "phase_ms_per_step": {p: round(ms[i] / args.steps, 4) for i, p in enumerate(PHASES)},
+            "launches_per_step": {p: launches[i] // args.steps for i, p in enumerate(PHASES)},
+            "survivors_per_query": round(st.survivors / max(1, st.queries), 2),
+            "verified_per_query": round(st.verified / max(1, st.queries), 2),
+        },
+        "roofline": {
+            "bound": "mfma", "kernel": "screen_wide_kernel (fp16 MFMA screen, label filter)",
+            "achieved": round(achieved, 2), "peak": P_FP16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / P_FP16_TFLOPS, 4), "traffic": None,
+            "avg_launch_ms": round(screen_ms, 4), "flops_per_launch": flops_per_launch,
+        },
+        "cpu_baseline": cpu,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3),
+                    help="2: the headline (10M x 128 uint8); 3: 1M x 768 fp32 cosine with labels")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--n", type=int, default=10_000_000)
+    ap.add_argument("--n", type=int, default=0, help="rows (default: the config's)")
     ap.add_argument("--nq", type=int, default=10_000)
-    ap.add_argument("--dim", type=int, default=128)
-    ap.add_argument("--k", type=int, default=10)
-    ap.add_argument("--batch", type=int, default=10_000)
-    ap.add_argument("--cpu-queries", type=int, default=64)
+    ap.add_argument("--dim", type=int, default=0)
+    ap.add_argument("--k", type=int, default=0)
+    ap.add_argument("--batch", type=int, default=0)
+    ap.add_argument("--cpu-queries", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -66,7 +182,13 @@ def main():
     C.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    n, d, nq, k = args.n, args.dim, args.nq, args.k
+    if args.config == 3:
+        args.cpu_queries = args.cpu_queries or 16
+        print(json.dumps(bench_config3(args)), flush=True)
+        return
+    args.cpu_queries = args.cpu_queries or 64
+    args.batch = args.batch or 10_000
+    n, d, nq, k = args.n or 10_000_000, args.dim or 128, args.nq, args.k or 10
     centres = torch.rand((1000, d), generator=torch.Generator().manual_seed(1), dtype=torch.float64) * 80.0
     centres = centres.float().to(dev)
     X = mixture_u8(n, d, 1000, centres, 2, dev)

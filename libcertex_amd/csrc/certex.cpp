@@ -236,7 +236,7 @@ auto plan_anchors(index_state const& st, int64_t size, int64_t nq_pad, int k) ->
 template <typename F>
 bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, int64_t size,
                          certex_amd::screen_args& sa, F&& screen, uint32_t*& count,
-                         uint32_t*& rows, int64_t& cap)
+                         uint32_t*& rows, int64_t& cap, float** vals = nullptr)
 {
   auto& rs           = res.state();
   hipStream_t stream = rs.stream;
@@ -248,6 +248,11 @@ bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, 
     if (size_t(nq_pad) * size_t(cap) * 4 > (size_t(1) << 32)) { throw batch_too_large(); }
     rows = static_cast<uint32_t*>(
       rs.get(cuvs::detail::ws_rows, size_t(nq_pad) * size_t(cap) * 4));
+    if (vals != nullptr) {
+      *vals = static_cast<float*>(
+        rs.get(cuvs::detail::ws_vals, size_t(nq_pad) * size_t(cap) * 4));
+      sa.cand_vals = *vals;
+    }
     certex_amd::fill_u32(count, nq_pad, 0, stream);
     sa.n_scan      = size;
     sa.row_stride  = 1;
@@ -270,8 +275,12 @@ bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, 
   }
 }
 
+/**
+ * Adds the batch's queries and survivors to the thread's counts; `verified` too unless the verify
+ * kernel counts the rows it scores itself (verified_by_kernel).
+ */
 void count_stats(cuvs::resources const& res, index_state const& st, int64_t B, bool all_rows,
-                 const uint32_t* count, int64_t cap)
+                 const uint32_t* count, int64_t cap, bool verified_by_kernel = false)
 {
   if (!t_stats_on) { return; }
   auto& rs           = res.state();
@@ -280,7 +289,7 @@ void count_stats(cuvs::resources const& res, index_state const& st, int64_t B, b
   if (all_rows) {
     const int64_t live = st.size - st.n_removed;
     t_stats.survivors += B * live;
-    t_stats.verified += B * live;
+    if (!verified_by_kernel) { t_stats.verified += B * live; }
     return;
   }
   auto* small = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_small, 64));
@@ -292,7 +301,7 @@ void count_stats(cuvs::resources const& res, index_state const& st, int64_t B, b
   CERTEX_HIP_TRY(hipStreamSynchronize(stream));
   auto* h = static_cast<unsigned long long*>(rs.host_small);
   t_stats.survivors += int64_t(h[0]);
-  t_stats.verified += int64_t(h[1]);
+  if (!verified_by_kernel) { t_stats.verified += int64_t(h[1]); }
 }
 
 /** One batch of queries of an integer index (the caller holds the shared lock). */
@@ -446,14 +455,15 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   }
 
   uint32_t *count = nullptr, *rows = nullptr;
+  float* vals = nullptr;
   int64_t cap = 0;
   if (!all_rows) {
     sa.theta = theta;
     all_rows = !screen_into_buckets(res, B, nq_pad, size, sa,
                                     wide ? certex_amd::screen_f16_wide : certex_amd::screen_f16,
-                                    count, rows, cap);
+                                    count, rows, cap, &vals);
   }
-  count_stats(res, st, B, all_rows, count, cap);
+  count_stats(res, st, B, all_rows, count, cap, true);
 
   auto* best_score =
     static_cast<double*>(rs.get(cuvs::detail::ws_best_score, size_t(B) * k * sizeof(double)));
@@ -462,10 +472,15 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   certex_amd::verify_f_args va{};
   va.cand_count = count;
   va.cand_rows  = rows;
+  va.cand_vals  = vals;
   va.cap        = cap;
   va.all_rows   = all_rows;
   va.n_rows     = size;
   va.vectors    = st.vectors.p;
+  va.qscal      = qscal;
+  va.maxima     = st.maxima.as<double>();
+  va.alpha2     = st.alpha * st.alpha;
+  va.gamma      = st.gamma;
   va.rowc       = st.rowc.as<float>();
   va.queries    = queries;
   va.t          = t;
@@ -476,7 +491,19 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   va.k          = k;
   va.best_score = best_score;
   va.best_row   = best_row;
+  unsigned long long* scored = nullptr;
+  if (t_stats_on) {
+    auto* small = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_small, 64));
+    scored      = reinterpret_cast<unsigned long long*>(small + 8);
+    certex_amd::fill_u32(small + 8, 2, 0, stream);
+  }
+  va.scored = scored;
   timed(3, stream, [&] { certex_amd::verify_topk_f(va, stream); });
+  if (scored != nullptr) {
+    CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, scored, 8, hipMemcpyDeviceToHost, stream));
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+    t_stats.verified += int64_t(*static_cast<unsigned long long*>(rs.host_small));
+  }
   certex_amd::finish(best_score, best_row, B, k, st.metric, distances, neighbors, stream);
 }
 

@@ -99,6 +99,7 @@ enum ws_slot : int {
   ws_staging,
   ws_qscal,
   ws_grow,
+  ws_vals,
   ws_n_slots
 };
 

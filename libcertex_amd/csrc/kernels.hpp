@@ -97,6 +97,7 @@ struct screen_args {
   // screen: candidate buckets
   uint32_t* cand_count = nullptr;  // [nq_pad]
   uint32_t* cand_rows  = nullptr;  // [nq_pad, cap]
+  float* cand_vals     = nullptr;  // [nq_pad, cap] screen values (fp16 rows only)
   int64_t cap          = 0;
   // anchors: group maxima [nq_pad, n_groups] (int32 or float), a group = group_steps steps;
   // fp16 rows also record the stored row of each maximum in grow
@@ -247,6 +248,7 @@ void threshold_f16(const threshold_f_args& a, hipStream_t stream);
 struct verify_f_args {
   const uint32_t* cand_count;
   const uint32_t* cand_rows;
+  const float* cand_vals;  // screen values of the candidates (ordered verification), or null
   int64_t cap;
   bool all_rows;
   int64_t n_rows;
@@ -259,10 +261,19 @@ struct verify_f_args {
   filter_args filter;
   int64_t nq;
   int k;
+  // the certificate of the screen (lower bounds from screen values): as in threshold_f_args
+  const double* qscal;
+  const double* maxima;
+  double alpha2;
+  double gamma;
+  unsigned long long* scored;  // optional: += the rows scored exactly (the stats' verified count)
   double* best_score;
   int64_t* best_row;
 };
-/** fp64 exact scores (the canonical order of the oracle) and top-k by (score, row). */
+/**
+ * fp64 exact scores (the canonical order of the oracle) and top-k by (score, row); with screen
+ * values, only the candidates whose certified lower bound can reach the top k are scored.
+ */
 void verify_topk_f(const verify_f_args& a, hipStream_t stream);
 
 /**

@@ -64,8 +64,9 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   __shared__ uint32_t gmr[ARGMX ? 4 * QB : 1];
   __shared__ uint32_t hit_q[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t hit_row[ANCHORS ? 1 : kHitCap];
+  __shared__ float hit_val[ANCHORS || !R::kValues ? 1 : kHitCap];
   __shared__ uint32_t n_hits;
-  const hit_list hits{hit_q, hit_row, &n_hits};
+  const hit_list hits{hit_q, hit_row, hit_val, &n_hits};
 
   const val_t* rowc  = static_cast<const val_t*>(a.rowc);
   const val_t* theta = static_cast<const val_t*>(a.theta);
@@ -195,7 +196,11 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
             }
           }
           const uint32_t qloc = uint32_t(g * 64 + qt * 16 + (lane & 15));
-          push_hits<FILT>(bits, qloc, row0, q0, a, hits);
+          const val_t v16[16] = {acc[0][qt][0], acc[0][qt][1], acc[0][qt][2], acc[0][qt][3],
+                                 acc[1][qt][0], acc[1][qt][1], acc[1][qt][2], acc[1][qt][3],
+                                 acc[2][qt][0], acc[2][qt][1], acc[2][qt][2], acc[2][qt][3],
+                                 acc[3][qt][0], acc[3][qt][1], acc[3][qt][2], acc[3][qt][3]};
+          push_hits<FILT, R::kValues>(bits, qloc, row0, q0, a, hits, v16);
         }
       }
     }
@@ -232,7 +237,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 
   if constexpr (!ANCHORS) {
     __syncthreads();
-    flush_hits(q0, a, hits);
+    flush_hits<R::kValues>(q0, a, hits);
   }
 }
 

@@ -26,6 +26,7 @@ struct int8_rows {
   using frag_t = v4i;
   using val_t  = int;
   static constexpr bool kArgmax = false;
+  static constexpr bool kValues = false;  // survivors carry no screen value (verify scores all)
   __device__ static acc_t mfma(frag_t a, frag_t b, acc_t c)
   {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -40,6 +41,7 @@ struct f16_rows {
   using frag_t = v8h;
   using val_t  = float;
   static constexpr bool kArgmax = true;  // the float threshold scores the best anchor exactly
+  static constexpr bool kValues = true;  // survivors carry their screen value (ordered verify)
   __device__ static acc_t mfma(frag_t a, frag_t b, acc_t c)
   {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -63,10 +65,11 @@ __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
   }
 }
 
-/** LDS survivor list of a workgroup. */
+/** LDS survivor list of a workgroup (val: the screen values, when the rows carry them). */
 struct hit_list {
   uint32_t* q;
   uint32_t* row;
+  float* val;
   uint32_t* n;
 };
 
@@ -76,9 +79,9 @@ struct hit_list {
  * busiest lane: ballot, rank by mbcnt, one LDS reservation per round; a full list spills straight
  * into the global bucket. Every lane of the wave must call it.
  */
-template <bool FILT>
+template <bool FILT, bool VALS, typename V>
 __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t row0, int64_t q0,
-                                          const screen_args& a, hit_list h)
+                                          const screen_args& a, hit_list h, const V (&v)[16])
 {
   if constexpr (FILT) {
     uint32_t scan = bits;
@@ -104,26 +107,39 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
       bits &= bits - 1;
       const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
       const uint32_t pos = base + rank;
+      float val          = 0.0f;
+      if constexpr (VALS) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) { val = t == j ? float(v[t]) : val; }
+      }
       if (pos < uint32_t(kHitCap)) {
         h.q[pos]   = qloc;
         h.row[pos] = row;
+        if constexpr (VALS) { h.val[pos] = val; }
       } else {
         const int64_t q      = q0 + qloc;
         const uint32_t bslot = atomicAdd(a.cand_count + q, 1u);
-        if (bslot < a.cap) { a.cand_rows[q * a.cap + bslot] = row; }
+        if (bslot < a.cap) {
+          a.cand_rows[q * a.cap + bslot] = row;
+          if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = val; }
+        }
       }
     }
   }
 }
 
 /** Flushes the workgroup's LDS survivor list to the per-query buckets (after a barrier). */
+template <bool VALS>
 __device__ inline void flush_hits(int64_t q0, const screen_args& a, hit_list h)
 {
   const uint32_t nh = *h.n < uint32_t(kHitCap) ? *h.n : uint32_t(kHitCap);
   for (uint32_t e = threadIdx.x; e < nh; e += blockDim.x) {
     const int64_t q      = q0 + h.q[e];
     const uint32_t bslot = atomicAdd(a.cand_count + q, 1u);
-    if (bslot < a.cap) { a.cand_rows[q * a.cap + bslot] = h.row[e]; }
+    if (bslot < a.cap) {
+      a.cand_rows[q * a.cap + bslot] = h.row[e];
+      if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = h.val[e]; }
+    }
   }
 }
 

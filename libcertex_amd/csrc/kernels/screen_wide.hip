@@ -52,8 +52,9 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
   __shared__ uint32_t gmr[ANCHORS ? kWideWaves * QB : 1];
   __shared__ uint32_t hit_q[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t hit_row[ANCHORS ? 1 : kHitCap];
+  __shared__ float hit_val[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t n_hits;
-  const hit_list hits{hit_q, hit_row, &n_hits};
+  const hit_list hits{hit_q, hit_row, hit_val, &n_hits};
 
   const float* rowc  = static_cast<const float*>(a.rowc);
   const float* theta = static_cast<const float*>(a.theta);
@@ -229,7 +230,11 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
               bits |= uint32_t(acc[bt][qt][r] >= th) << (bt * 4 + r);
             }
           }
-          push_hits<FILT>(bits, uint32_t(qt * 16 + (lane & 15)), row0, q0, a, hits);
+          const float v16[16] = {acc[0][qt][0], acc[0][qt][1], acc[0][qt][2], acc[0][qt][3],
+                                 acc[1][qt][0], acc[1][qt][1], acc[1][qt][2], acc[1][qt][3],
+                                 acc[2][qt][0], acc[2][qt][1], acc[2][qt][2], acc[2][qt][3],
+                                 acc[3][qt][0], acc[3][qt][1], acc[3][qt][2], acc[3][qt][3]};
+          push_hits<FILT, true>(bits, uint32_t(qt * 16 + (lane & 15)), row0, q0, a, hits, v16);
         }
       }
     }
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
 
   if constexpr (!ANCHORS) {
     __syncthreads();
-    flush_hits(q0, a, hits);
+    flush_hits<true>(q0, a, hits);
   }
 }
 
@@ -268,7 +273,7 @@ int wide_query_tiles(int row_bytes)
     }
     return v;
   }();
-  const int fixed = 2 * kHitCap * 4 + kWideWaves * 16 * 6 * 8 + 1024;  // static arrays, margin
+  const int fixed = 3 * kHitCap * 4 + 16 * 6 * 4 + 512;  // static arrays of the screen, margin
   for (int qt : {6, 4, 2}) {
     if (16 * qt * row_bytes + fixed <= max_lds) { return qt; }
   }

@@ -298,16 +298,18 @@ __device__ inline double fcoord(const void* p, elem t, int64_t i)
 }
 
 /**
- * Exact score of stored row x against the query whose coordinates sit in LDS as doubles, in the
- * oracle's canonical order (coordinates ascending, fused multiply-adds): l2 sum (q - x)^2, inner
- * -sum q x, cosine -sum q x / sqrt(sum q^2 sum x^2).
+ * Exact fp64 score of stored row `row` against the query whose coordinates sit in LDS as doubles,
+ * computed by one wave in the oracle's canonical order: lane l accumulates coordinates l, l + 64,
+ * ... with fused multiply-adds, and the 64 partial sums are combined by the xor butterfly (every
+ * lane returns the same bits). l2: sum (q - x)^2; inner: -sum q x; cosine: -sum q x /
+ * sqrt(sum q^2 sum x^2). The row's coordinates are read by the 64 lanes together (coalesced).
  */
-__device__ inline double float_score(const double* qv, const void* vectors, elem t, int64_t row,
-                                     int64_t dim, metric_kind metric)
+__device__ inline double wave_score(const double* qv, const void* vectors, elem t, int64_t row,
+                                    int64_t dim, metric_kind metric, int lane)
 {
   double acc = 0, qq = 0, xx = 0;
   const int64_t base = row * dim;
-  for (int64_t j = 0; j < dim; ++j) {
+  for (int64_t j = lane; j < dim; j += 64) {
     const double a = qv[j], b = fcoord(vectors, t, base + j);
     if (metric == metric_kind::l2) {
       const double d = a - b;
@@ -318,6 +320,14 @@ __device__ inline double float_score(const double* qv, const void* vectors, elem
         qq = fma(a, a, qq);
         xx = fma(b, b, xx);
       }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off; off >>= 1) {
+    acc += __shfl_xor(acc, off);
+    if (metric == metric_kind::cosine) {
+      qq += __shfl_xor(qq, off);
+      xx += __shfl_xor(xx, off);
     }
   }
   if (metric == metric_kind::l2) { return acc; }
@@ -332,7 +342,7 @@ __device__ inline uint32_t fkey(float f)
   return (b >> 31) ? ~b : (b | 0x80000000u);
 }
 
-constexpr int kMaxFloatDim = 4096;
+constexpr int kMaxFloatDim = kMaxF16Halves;  // widest float vector
 
 __global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_args a)
 {
@@ -402,8 +412,9 @@ __global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_arg
   }
   __syncthreads();
   const int m = cnt < kBuf ? cnt : kBuf;
-  for (int e = tid; e < m; e += kThreads) {
-    key[e] = score_key(float_score(qv, a.vectors, a.t, rid[e], a.dim, a.metric));
+  for (int e = tid >> 6; e < m; e += kThreads / 64) {
+    const double sc = wave_score(qv, a.vectors, a.t, rid[e], a.dim, a.metric, tid & 63);
+    if ((tid & 63) == 0) { key[e] = score_key(sc); }
   }
   const int Pw = pow2_at_least(m);
   for (int e = m + tid; e < Pw; e += kThreads) {
@@ -435,68 +446,176 @@ __global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_arg
   }
 }
 
+/**
+ * A lower bound of the exact score of a pair whose fp16 screen value is v: the inverse of the
+ * threshold map of threshold_f16_kernel (a pair with score s has v >= t(s), where t(U) is the
+ * threshold before rounding), with 20 times its relative slack and a margin for the fp64 rounding
+ * of this expression. C = the query's cross and accumulation terms; aq = |W|^2 (lower bound).
+ */
+__device__ inline double screen_lower_bound(float v, double aq, double C, double alpha2,
+                                            metric_kind metric)
+{
+  const double R = double(v) + C + 1e-30;
+  if (metric == metric_kind::inner) {
+    // t(U) = -U / alpha2 - C - 1e-10 |U / alpha2| - 1e-30
+    return -alpha2 * (R + 2e-9 * fabs(R)) - 1e-12 * alpha2 * (fabs(R) + 1e-300);
+  }
+  // l2 on the (unit) vectors: t(U) = (aq - U / alpha2) / 2 - C - 1e-10 (aq + U / alpha2) - 1e-30
+  const double y  = (aq * (1.0 - 2e-9) - 2.0 * R) / (1.0 + 2e-9);
+  const double lb = alpha2 * y - 1e-12 * alpha2 * (fabs(aq) + 2.0 * fabs(R) + 1e-300);
+  if (metric == metric_kind::cosine) { return (lb - 2.0) / 2.0 - 1e-12 * (fabs(lb) + 2.0); }
+  return lb;
+}
+
+/**
+ * The rank-th smallest (1-based) of the 32-bit keys key_of(e), e < n: an LDS radix select over
+ * four 8-bit digits. Every thread of the block calls it and gets the same key.
+ */
+template <typename F>
+__device__ uint32_t radix_select(int64_t n, int rank, F key_of, int* hist, int* wave_tot,
+                                 uint32_t* sel_digit, int* sel_rank)
+{
+  const int tid   = threadIdx.x;
+  uint32_t prefix = 0, mask = 0;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hist[tid] = 0;
+    __syncthreads();
+    for (int64_t e = tid; e < n; e += kThreads) {
+      const uint32_t kk = key_of(e);
+      if ((kk & mask) == prefix) { atomicAdd(&hist[(kk >> shift) & 255], 1); }
+    }
+    __syncthreads();
+    const int c    = hist[tid];
+    const int incl = block_scan_incl(c, wave_tot);
+    if (incl - c < rank && rank <= incl) {
+      *sel_digit = uint32_t(tid);
+      *sel_rank  = rank - (incl - c);
+    }
+    __syncthreads();
+    prefix |= *sel_digit << shift;
+    mask |= 255u << shift;
+    rank = *sel_rank;
+    __syncthreads();
+  }
+  return prefix;
+}
+
+/**
+ * Exact re-rank of one query's survivors, one block per query. With screen values (fp16 rows),
+ * the verification is ordered (the reference's verify_rounds, detail/verify.cuh:371-487): first
+ * the k survivors with the largest screen values are scored, which bounds the k-th neighbour's
+ * score by U; then only the survivors whose screen lower bound does not exceed U are scored
+ * (U tightens as better rows arrive). Scores use one wave per row; the best k by (score, row)
+ * stay in LDS.
+ */
 __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a)
 {
   __shared__ uint64_t key[kBuf];
   __shared__ uint32_t rid[kBuf];
   __shared__ double qv[kMaxFloatDim];
+  __shared__ int hist[256];
+  __shared__ int wave_tot[4];
+  __shared__ uint32_t sel_digit;
+  __shared__ int sel_rank;
   __shared__ int fill;
 
   const int64_t q = blockIdx.x;
   const int tid   = threadIdx.x;
+  const int lane  = tid & 63;
+  const int wave  = tid >> 6;
   const int k     = a.k;
   for (int64_t j = tid; j < a.dim; j += kThreads) { qv[j] = fcoord(a.queries, a.t, q * a.dim + j); }
 
   const int64_t n_cand =
     a.all_rows ? a.n_rows : (a.cand_count[q] < a.cap ? int64_t(a.cand_count[q]) : a.cap);
   const uint32_t* cand = a.cand_rows + q * a.cap;
-  int have             = 0;
-  if (tid == 0) { fill = 0; }
-  __syncthreads();
+  const float* vals    = (a.all_rows || a.cand_vals == nullptr) ? nullptr : a.cand_vals + q * a.cap;
+
+  int64_t n_scored = 0;
+  auto score_rows  = [&](int from, int to) {
+    n_scored += to - from;
+    for (int e = from + wave; e < to; e += kThreads / 64) {
+      const double sc = wave_score(qv, a.vectors, a.t, rid[e], a.dim, a.metric, lane);
+      if (lane == 0) { key[e] = score_key(sc); }
+    }
+  };
+  int have = 0;  // entries [0, have) of key / rid are scored
+  auto keep_best = [&]() {
+    const int P = pow2_at_least(have > 1 ? have : 1);
+    for (int j = have + tid; j < P; j += kThreads) {
+      key[j] = ~0ull;
+      rid[j] = ~0u;
+    }
+    __syncthreads();
+    bitonic_sort(key, rid, P);
+    have = have < k ? have : k;
+  };
+
+  // phase A: the survivors whose screen value is at least the k-th largest (descending keys)
+  bool ordered = vals != nullptr && n_cand > k;
+  uint32_t tk  = 0;
+  double U = INFINITY, aq = 0, C = 0;
+  if (ordered) {
+    tk = radix_select(n_cand, k, [&](int64_t e) { return ~fkey(vals[e]); }, hist, wave_tot,
+                      &sel_digit, &sel_rank);
+    if (tid == 0) { fill = 0; }
+    __syncthreads();
+    for (int64_t e = tid; e < n_cand; e += kThreads) {
+      if (~fkey(vals[e]) <= tk) {
+        const int slot = atomicAdd(&fill, 1);
+        if (slot < kBuf) { rid[slot] = cand[e]; }
+      }
+    }
+    __syncthreads();
+    const int c = fill;
+    __syncthreads();
+    if (c <= kBuf) {
+      have = c;
+      score_rows(0, c);
+      __syncthreads();
+      keep_best();
+      U                = key_score(key[k - 1]);  // k distinct live rows: bounds the k-th score
+      const double nw  = a.qscal[3 * q + 1], ew = a.qscal[3 * q + 2];
+      const double nz  = a.maxima[0], ez = a.maxima[1];
+      aq               = a.qscal[3 * q];
+      C                = a.gamma * nw * nz + ew * nz + nw * ez + ew * ez;
+    } else {
+      ordered = false;  // more ties at the k-th screen value than the buffer holds: score all
+    }
+  }
+
+  // phase B: the rest (everything when not ordered), in buffer-sized chunks
   for (int64_t c0 = 0; c0 < n_cand;) {
     const int room  = kBuf - have;
     const int64_t m = n_cand - c0 < room ? n_cand - c0 : room;
+    if (tid == 0) { fill = 0; }
+    __syncthreads();
     for (int64_t e = tid; e < m; e += kThreads) {
+      const int64_t idx = c0 + e;
       uint32_t r;
-      bool live;
+      bool take;
       if (a.all_rows) {
-        r    = uint32_t(c0 + e);
-        live = a.rowc[r] != -INFINITY && keeps(a.filter, q, r);
+        r    = uint32_t(idx);
+        take = a.rowc[r] != -INFINITY && keeps(a.filter, q, r);
       } else {
-        r    = cand[c0 + e];
-        live = true;
+        r    = cand[idx];
+        take = !ordered || (~fkey(vals[idx]) > tk &&
+                            screen_lower_bound(vals[idx], aq, C, a.alpha2, a.metric) <= U);
       }
-      if (live) {
-        const double s = float_score(qv, a.vectors, a.t, r, a.dim, a.metric);
-        const int slot = have + atomicAdd(&fill, 1);
-        key[slot]      = score_key(s);
-        rid[slot]      = r;
-      }
+      if (take) { rid[have + atomicAdd(&fill, 1)] = r; }
     }
+    __syncthreads();
+    const int added = fill;
+    score_rows(have, have + added);
+    have += added;
     c0 += m;
     __syncthreads();
-    have += fill;
-    __syncthreads();
-    if (tid == 0) { fill = 0; }
-    if (c0 < n_cand && have > k) {
-      const int P = pow2_at_least(have);
-      for (int j = have + tid; j < P; j += kThreads) {
-        key[j] = ~0ull;
-        rid[j] = ~0u;
-      }
-      __syncthreads();
-      bitonic_sort(key, rid, P);
-      have = k;
+    if (have > k && c0 < n_cand) {
+      keep_best();
+      if (ordered) { U = key_score(key[k - 1]); }
     }
-    __syncthreads();
   }
-  const int P = pow2_at_least(have > 1 ? have : 1);
-  for (int j = have + tid; j < P; j += kThreads) {
-    key[j] = ~0ull;
-    rid[j] = ~0u;
-  }
-  __syncthreads();
-  bitonic_sort(key, rid, P);
+  keep_best();
   for (int j = tid; j < k; j += kThreads) {
     if (j < have) {
       a.best_score[q * k + j] = key_score(key[j]);
@@ -506,6 +625,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
       a.best_row[q * k + j]   = -1;
     }
   }
+  if (a.scored != nullptr && tid == 0) { atomicAdd(a.scored, (unsigned long long)n_scored); }
 }
 
 __global__ void finish_kernel(const double* best_score, const int64_t* best_row, int64_t n, int k,

@@ -9,7 +9,11 @@
  *   l2      score = sum_j (q_j - x_j)^2                       (smaller is better)
  *   inner   score = -sum_j q_j x_j                            (index.py:532, -(rows * Qs).sum)
  *   cosine  score = -sum_j q_j x_j / sqrt(sum q^2 * sum x^2)  (index.py:527-532 normalises both)
- * evaluated in fp64 over the coordinates in increasing order with fused multiply-adds, and ranked
+ * evaluated in fp64 in a fixed order that a 64-lane wave reproduces bit for bit: coordinate j goes
+ * to partial sum j mod 64, each partial accumulates its coordinates in increasing order with fused
+ * multiply-adds, and the 64 partials are combined by a butterfly (for off = 32, 16, ..., 1:
+ * p[i] = p[i] + p[i ^ off]). The reference sums per warp lane and combines by shuffles the same
+ * way (warp_score, 32 lanes). Results are ranked
  * by the total order (score, id): ties go to the lower id, as in the only tie-break of the
  * reference (certex_shards.cu:154-157). Filters follow the reference semantics: a bitset over ids,
  * a bitmap of one row of bits per query (certex.h:176-182), or equal labels (certex.hpp:702-705);
@@ -52,26 +56,45 @@ static double coord(const void* p, int dt, int64_t i)
   }
 }
 
-/** The exact score of query row q against stored row x (see the header). */
-double oracle_score(const void* q, const void* x, int dt, int64_t d, int metric)
+enum { LANES = 64 };
+
+/** Butterfly combination of 64 partial sums (every lane of a wave ends with this value). */
+static double combine(double* p)
 {
-  double acc = 0, qq = 0, xx = 0;
-  for (int64_t j = 0; j < d; ++j) {
-    const double a = coord(q, dt, j), b = coord(x, dt, j);
-    if (metric == M_L2) {
-      const double t = a - b;
-      acc            = fma(t, t, acc);
-    } else {
-      acc = fma(a, b, acc);
-      if (metric == M_COSINE) {
-        qq = fma(a, a, qq);
-        xx = fma(b, b, xx);
+  for (int off = LANES / 2; off; off >>= 1) {
+    for (int i = 0; i < LANES; ++i) {
+      if (!(i & off)) {
+        const double v = p[i] + p[i | off];
+        p[i]           = v;
+        p[i | off]     = v;
       }
     }
   }
-  if (metric == M_L2) { return acc; }
-  if (metric == M_INNER) { return -acc; }
-  return -acc / sqrt(qq * xx);
+  return p[0];
+}
+
+/** The exact score of query row q against stored row x (see the header). */
+double oracle_score(const void* q, const void* x, int dt, int64_t d, int metric)
+{
+  double acc[LANES] = {0}, qq[LANES] = {0}, xx[LANES] = {0};
+  for (int64_t j = 0; j < d; ++j) {
+    const double a = coord(q, dt, j), b = coord(x, dt, j);
+    const int l    = (int)(j % LANES);
+    if (metric == M_L2) {
+      const double t = a - b;
+      acc[l]         = fma(t, t, acc[l]);
+    } else {
+      acc[l] = fma(a, b, acc[l]);
+      if (metric == M_COSINE) {
+        qq[l] = fma(a, a, qq[l]);
+        xx[l] = fma(b, b, xx[l]);
+      }
+    }
+  }
+  const double s = combine(acc);
+  if (metric == M_L2) { return s; }
+  if (metric == M_INNER) { return -s; }
+  return -s / sqrt(combine(qq) * combine(xx));
 }
 
 static int elem_size(int dt) { return dt == DT_F32 ? 4 : (dt == DT_F16 ? 2 : 1); }
