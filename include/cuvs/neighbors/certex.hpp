@@ -132,6 +132,8 @@ class index {
   [[nodiscard]] auto anchor_stride() const noexcept -> int;
   [[nodiscard]] auto metric() const noexcept -> cuvs::distance::DistanceType;
   [[nodiscard]] auto has_labels() const noexcept -> bool;
+  /** Vectors covered by the label partition (0: none; later additions are not). */
+  [[nodiscard]] auto n_partitioned() const noexcept -> int64_t;
   [[nodiscard]] auto host_vectors() const noexcept -> bool;
   [[nodiscard]] auto state() const -> detail::index_state&;
 
@@ -160,6 +162,14 @@ void remove(cuvs::resources const& res, const int64_t* ids, int64_t n_ids, index
 template <typename T>
 void set_labels(cuvs::resources const& res, const int32_t* labels, int64_t n, index<T>* idx,
                 int64_t first = 0);
+
+/**
+ * Copy the screening rows into label order (reference certex.hpp:607-619, certex.cu:1542-1606),
+ * a speed option of label search: each label's queries then screen only that label's rows, and
+ * the rows added later go through the label filter. Needs labels; results do not change.
+ */
+template <typename T>
+void partition_by_labels(cuvs::resources const& res, index<T>* idx);
 
 /**
  * Exact k nearest neighbours of every query (reference certex.hpp:602-705): queries [nq, dim] in

@@ -23,6 +23,7 @@ SOURCES = [
     "kernels/screen_wide.hip",
     "kernels/select.hip",
     "kernels/encode.hip",
+    "kernels/partition.hip",
     "certex.cpp",
     "c_api.cpp",
 ]

@@ -331,10 +331,9 @@ cuvsError_t cuvsCertexSetLabels(cuvsResources_t res,
 cuvsError_t cuvsCertexPartitionByLabels(cuvsResources_t res, cuvsCertexIndex_t index)
 {
   return translate([=] {
-    (void)res_of(res);
+    auto& r = res_of(res);
     dispatch(index->dtype, [&](auto tag) {
-      certex::expects(as_index<decltype(tag)>(*index)->has_labels(),
-                      "certex: the index has no labels");
+      certex::partition_by_labels<decltype(tag)>(r, as_index<decltype(tag)>(*index));
     });
   });
 }

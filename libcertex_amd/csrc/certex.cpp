@@ -229,6 +229,97 @@ auto plan_anchors(index_state const& st, int64_t size, int64_t nq_pad, int k) ->
 }
 
 /**
+ * Routing of one label-sorted batch over the label partition (reference route_plan,
+ * certex.cu:1669-1712): per label, its queries against its partition rows, as two group tables
+ * (the anchor pass and the screen tile the groups differently); the rows added after the
+ * partition (the tail) are screened with the label filter.
+ */
+struct route_plan {
+  const certex_amd::screen_group* anchor_groups = nullptr;
+  const certex_amd::screen_group* screen_groups = nullptr;
+  int n_route          = 0;
+  int64_t anchor_tiles = 0, screen_tiles = 0;
+  int anchor_chunk     = 0;
+  int64_t part_groups  = 0;  // anchor group columns of the partition (the tail's follow)
+  anchor_plan ap{};
+};
+
+constexpr int kScreenChunk = 128;  // steps per screen workgroup chunk
+
+auto anchor_chunk_steps(bool wide, int64_t g) -> int
+{
+  return int(wide ? 8 * g * std::max<int64_t>(1, 4 / g) : 4 * g * std::max<int64_t>(1, 16 / g));
+}
+
+/** Anchor pass: every anchor of the index, or the partition's (routed) and the tail's. */
+template <typename F>
+void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan const& ap,
+                 route_plan const* route, F&& launch, hipStream_t stream)
+{
+  aa.row_stride  = ap.stride;
+  aa.n_groups    = ap.n_groups;
+  aa.group_steps = int(ap.group_steps);
+  if (route == nullptr) {
+    aa.n_scan = ap.n_anchor;
+    launch(aa, stream);
+    return;
+  }
+  // columns of labels with fewer groups stay at the lowest value (no anchor)
+  if (is_int(st.type)) {
+    certex_amd::fill_i32(static_cast<int32_t*>(aa.gmax), aa.nq_pad * ap.n_groups, INT32_MIN,
+                         stream);
+  } else {
+    certex_amd::fill_u32(static_cast<uint32_t*>(aa.gmax), aa.nq_pad * ap.n_groups, 0xff800000u,
+                         stream);
+  }
+  certex_amd::screen_args r = aa;
+  r.codes                   = st.part_codes.as<int8_t>();
+  r.rowc                    = st.part_rowc.p;
+  r.row_ids                 = st.part_ids.as<int32_t>();
+  r.groups                  = route->anchor_groups;
+  r.n_route                 = route->n_route;
+  r.n_tiles                 = route->anchor_tiles;
+  r.filter.kind             = 0;  // every row of a group carries the group's label
+  if (r.n_tiles > 0) { launch(r, stream); }
+  const int64_t tail = st.size - st.n_part;
+  if (tail > 0) {
+    certex_amd::screen_args t = aa;
+    t.row_base                = st.n_part;
+    t.n_scan                  = (tail + ap.stride - 1) / ap.stride;
+    t.grp_base                = route->part_groups;
+    launch(t, stream);
+  }
+}
+
+/** Screen pass: every row, or the partition's (routed) and the tail's (label filter). */
+template <typename F>
+auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
+{
+  return [&st, route, launch](certex_amd::screen_args& sa, hipStream_t stream) {
+    if (route == nullptr) {
+      launch(sa, stream);
+      return;
+    }
+    certex_amd::screen_args r = sa;
+    r.codes                   = st.part_codes.as<int8_t>();
+    r.rowc                    = st.part_rowc.p;
+    r.row_ids                 = st.part_ids.as<int32_t>();
+    r.groups                  = route->screen_groups;
+    r.n_route                 = route->n_route;
+    r.n_tiles                 = route->screen_tiles;
+    r.filter.kind             = 0;
+    if (r.n_tiles > 0) { launch(r, stream); }
+    const int64_t tail = st.size - st.n_part;
+    if (tail > 0) {
+      certex_amd::screen_args t = sa;
+      t.row_base                = st.n_part;
+      t.n_scan                  = tail;
+      launch(t, stream);
+    }
+  };
+}
+
+/**
  * Screen pass into per-query buckets, re-run with larger buckets while one overflows (the
  * reference re-runs on segment overflow, certex.cu:1208-1269). Returns false when some query
  * keeps so many rows that scoring every row is cheaper (all_rows).
@@ -256,7 +347,7 @@ bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, 
     certex_amd::fill_u32(count, nq_pad, 0, stream);
     sa.n_scan      = size;
     sa.row_stride  = 1;
-    sa.chunk_steps = 128;
+    sa.chunk_steps = kScreenChunk;
     sa.cand_count  = count;
     sa.cand_rows   = rows;
     sa.cap         = cap;
@@ -307,7 +398,7 @@ void count_stats(cuvs::resources const& res, index_state const& st, int64_t B, b
 /** One batch of queries of an integer index (the caller holds the shared lock). */
 void search_batch_int(cuvs::resources const& res, index_state const& st, const void* queries,
                       int64_t B, int k, int64_t q0, int64_t* neighbors, float* distances,
-                      certex_amd::filter_args fa, int)
+                      certex_amd::filter_args fa, int, route_plan const* route)
 {
   auto& rs             = res.state();
   hipStream_t stream   = rs.stream;
@@ -323,7 +414,7 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
 
   // anchor pass: every anchor_stride-th stored row; the best screen value of every group of
   // anchors, then the k-th best group is the threshold of the query
-  const anchor_plan ap = plan_anchors(st, size, nq_pad, k);
+  const anchor_plan ap = route ? route->ap : plan_anchors(st, size, nq_pad, k);
   certex_amd::screen_args sa{};
   sa.codes     = st.codes.as<int8_t>();
   sa.rowc      = st.rowc.p;
@@ -339,13 +430,9 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
     auto* gmax = static_cast<int32_t*>(
       rs.get(cuvs::detail::ws_gmax, size_t(nq_pad) * size_t(ap.n_groups) * 4));
     certex_amd::screen_args aa = sa;
-    aa.n_scan                  = ap.n_anchor;
-    aa.row_stride              = ap.stride;
-    aa.chunk_steps             = int(4 * ap.group_steps * std::max<int64_t>(1, 16 / ap.group_steps));
+    aa.chunk_steps             = anchor_chunk_steps(false, ap.group_steps);
     aa.gmax                    = gmax;
-    aa.n_groups                = ap.n_groups;
-    aa.group_steps             = int(ap.group_steps);
-    timed(0, stream, [&] { certex_amd::anchors_i8(aa, stream); });
+    timed(0, stream, [&] { anchor_pass(st, aa, ap, route, certex_amd::anchors_i8, stream); });
     timed(1, stream,
           [&] { certex_amd::threshold_i8(gmax, ap.n_groups, B, nq_pad, k, theta, stream); });
   }
@@ -354,7 +441,8 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
   int64_t cap = 0;
   if (!all_rows) {
     sa.theta = theta;
-    all_rows = !screen_into_buckets(res, B, nq_pad, size, sa, certex_amd::screen_i8, count, rows,
+    all_rows = !screen_into_buckets(res, B, nq_pad, size, sa,
+                                    screen_pass(st, route, certex_amd::screen_i8), count, rows,
                                     cap);
   }
   count_stats(res, st, B, all_rows, count, cap);
@@ -388,7 +476,7 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
 /** One batch of queries of a float index (the caller holds the shared lock). */
 void search_batch_float(cuvs::resources const& res, index_state const& st, const void* queries,
                         int64_t B, int k, int64_t q0, int64_t* neighbors, float* distances,
-                        certex_amd::filter_args fa, int anchors)
+                        certex_amd::filter_args fa, int anchors, route_plan const* route)
 {
   auto& rs             = res.state();
   hipStream_t stream   = rs.stream;
@@ -404,7 +492,7 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   certex_amd::encode_queries_f16(queries, t, B, nq_pad, st.dim, st.halves, st.normalize,
                                  st.center.as<double>(), 1.0 / st.alpha, qrows, qscal, stream);
 
-  const anchor_plan ap = plan_anchors(st, size, nq_pad, k);
+  const anchor_plan ap = route ? route->ap : plan_anchors(st, size, nq_pad, k);
   certex_amd::screen_args sa{};
   sa.codes     = st.codes.as<int8_t>();
   sa.rowc      = st.rowc.p;
@@ -422,16 +510,12 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
     auto* grow = static_cast<uint32_t*>(
       rs.get(cuvs::detail::ws_grow, size_t(nq_pad) * size_t(ap.n_groups) * 4));
     certex_amd::screen_args aa = sa;
-    aa.n_scan                  = ap.n_anchor;
-    aa.row_stride              = ap.stride;
-    aa.chunk_steps = int(wide ? 8 * ap.group_steps * std::max<int64_t>(1, 4 / ap.group_steps)
-                              : 4 * ap.group_steps * std::max<int64_t>(1, 16 / ap.group_steps));
+    aa.chunk_steps             = anchor_chunk_steps(wide, ap.group_steps);
     aa.gmax                    = gmax;
     aa.grow                    = grow;
-    aa.n_groups                = ap.n_groups;
-    aa.group_steps             = int(ap.group_steps);
     timed(0, stream, [&] {
-      (wide ? certex_amd::anchors_f16_wide : certex_amd::anchors_f16)(aa, stream);
+      anchor_pass(st, aa, ap, route,
+                  wide ? certex_amd::anchors_f16_wide : certex_amd::anchors_f16, stream);
     });
     certex_amd::threshold_f_args ta{};
     ta.gmax      = gmax;
@@ -459,9 +543,10 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   int64_t cap = 0;
   if (!all_rows) {
     sa.theta = theta;
-    all_rows = !screen_into_buckets(res, B, nq_pad, size, sa,
-                                    wide ? certex_amd::screen_f16_wide : certex_amd::screen_f16,
-                                    count, rows, cap, &vals);
+    all_rows = !screen_into_buckets(
+      res, B, nq_pad, size, sa,
+      screen_pass(st, route, wide ? certex_amd::screen_f16_wide : certex_amd::screen_f16), count,
+      rows, cap, &vals);
   }
   count_stats(res, st, B, all_rows, count, cap, true);
 
@@ -507,6 +592,114 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   certex_amd::finish(best_score, best_row, B, k, st.metric, distances, neighbors, stream);
 }
 
+using batch_fn = void (*)(cuvs::resources const&, index_state const&, const void*, int64_t, int,
+                          int64_t, int64_t*, float*, certex_amd::filter_args, int,
+                          route_plan const*);
+
+/**
+ * Label search of one batch over the label partition (reference search_by_labels,
+ * certex.cu:1613-1735): the queries in label order (stable), one routed group per label that has
+ * partition rows, the tail through the label filter, and the results back in query order.
+ */
+void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn batch,
+                  const char* queries, size_t qrow, int64_t B, int k, const int32_t* qlabels,
+                  int64_t* neighbors, float* distances, certex_amd::filter_args fa, int anchors)
+{
+  auto& rs           = res.state();
+  hipStream_t stream = rs.stream;
+  std::vector<int32_t> lab(static_cast<size_t>(B)), order(static_cast<size_t>(B)),
+    sorted(static_cast<size_t>(B));
+  CERTEX_HIP_TRY(hipMemcpyAsync(lab.data(), qlabels, size_t(B) * 4, hipMemcpyDeviceToHost, stream));
+  CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  for (int64_t i = 0; i < B; ++i) { order[size_t(i)] = int32_t(i); }
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int32_t a, int32_t b) { return lab[size_t(a)] < lab[size_t(b)]; });
+
+  const int64_t nq_pad = certex_amd::pad_queries(B);
+  const bool f16       = !is_int(st.type);
+  const bool wide      = f16 && st.row_bytes > 256;
+  const int qb         = certex_amd::screen_query_block(f16, st.row_bytes, nq_pad);
+  const auto& off      = st.part_offsets;
+  std::vector<certex_amd::screen_group> ga, gs;
+  int64_t max_nx = 0;
+  for (int64_t i = 0; i < B;) {
+    const int32_t l = lab[size_t(order[size_t(i)])];
+    int64_t j       = i;
+    while (j < B && lab[size_t(order[size_t(j)])] == l) { sorted[size_t(j++)] = l; }
+    if (l >= 0 && int64_t(l) + 1 < int64_t(off.size()) && off[size_t(l) + 1] > off[size_t(l)]) {
+      certex_amd::screen_group g{i, j - i, off[size_t(l)], off[size_t(l) + 1] - off[size_t(l)], 0};
+      ga.push_back(g);
+      gs.push_back(g);
+      max_nx = std::max(max_nx, g.nx);
+    }
+    i = j;
+  }
+  // a label's anchors must form at least k groups of 64 for a threshold: below the index's
+  // stride, a denser one (a query whose label still has fewer groups keeps all of its rows)
+  const int stride = int(std::max<int64_t>(
+    1, std::min<int64_t>(std::max(1, st.anchor_stride), max_nx / (64 * int64_t(k)))));
+  int64_t max_steps = 0;
+  for (auto const& e : ga) {
+    max_steps = std::max(max_steps, certex_amd::screen_steps((e.nx + stride - 1) / stride));
+  }
+  // anchor groups: per label as plan_anchors sizes them for the largest label; the tail's
+  // columns follow the partition's
+  route_plan route;
+  const int64_t tail_steps = certex_amd::screen_steps((st.size - st.n_part + stride - 1) / stride);
+  int64_t g = std::max<int64_t>(1, max_steps / (64 * int64_t(k)));
+  while (true) {
+    route.part_groups = (max_steps + g - 1) / g;
+    route.ap.n_groups = route.part_groups + (tail_steps + g - 1) / g;
+    if (nq_pad * route.ap.n_groups * 4 <= (int64_t(1) << 30)) { break; }
+    g *= 2;
+  }
+  route.ap.stride      = stride;
+  route.ap.n_anchor    = 0;
+  route.ap.group_steps = g;
+  route.anchor_chunk   = anchor_chunk_steps(wide, g);
+  for (auto& e : ga) {
+    e.tile0 = route.anchor_tiles;
+    route.anchor_tiles += certex_amd::screen_group_tiles(e.nq, (e.nx + stride - 1) / stride, qb,
+                                                         route.anchor_chunk);
+  }
+  for (auto& e : gs) {
+    e.tile0 = route.screen_tiles;
+    route.screen_tiles += certex_amd::screen_group_tiles(e.nq, e.nx, qb, kScreenChunk);
+  }
+  route.n_route = int(gs.size());
+
+  // device copies: order, sorted labels, the two group tables
+  const size_t lab_bytes = (size_t(B) * 4 + 15) / 16 * 16;
+  const size_t tab_bytes = std::max<size_t>(1, gs.size()) * sizeof(certex_amd::screen_group);
+  char* dev = static_cast<char*>(rs.get(cuvs::detail::ws_route, 2 * lab_bytes + 2 * tab_bytes));
+  auto* d_order  = reinterpret_cast<int32_t*>(dev);
+  auto* d_sorted = reinterpret_cast<int32_t*>(dev + lab_bytes);
+  auto* d_ga     = reinterpret_cast<certex_amd::screen_group*>(dev + 2 * lab_bytes);
+  auto* d_gs     = reinterpret_cast<certex_amd::screen_group*>(dev + 2 * lab_bytes + tab_bytes);
+  CERTEX_HIP_TRY(hipMemcpyAsync(d_order, order.data(), size_t(B) * 4, hipMemcpyHostToDevice, stream));
+  CERTEX_HIP_TRY(
+    hipMemcpyAsync(d_sorted, sorted.data(), size_t(B) * 4, hipMemcpyHostToDevice, stream));
+  if (!gs.empty()) {
+    CERTEX_HIP_TRY(hipMemcpyAsync(d_ga, ga.data(), ga.size() * sizeof(ga[0]),
+                                  hipMemcpyHostToDevice, stream));
+    CERTEX_HIP_TRY(hipMemcpyAsync(d_gs, gs.data(), gs.size() * sizeof(gs[0]),
+                                  hipMemcpyHostToDevice, stream));
+  }
+  route.anchor_groups = d_ga;
+  route.screen_groups = d_gs;
+
+  auto* q_sorted = rs.get(cuvs::detail::ws_route_q, size_t(B) * qrow);
+  certex_amd::gather_rows(queries, d_order, B, int64_t(qrow), q_sorted, stream);
+  auto* out   = static_cast<char*>(rs.get(cuvs::detail::ws_route_out, size_t(B) * k * 12));
+  auto* nb_s  = reinterpret_cast<int64_t*>(out);
+  auto* ds_s  = reinterpret_cast<float*>(out + size_t(B) * k * 8);
+  fa.query_labels = d_sorted;  // the label filter of the tail, in the sorted order
+  batch(res, st, q_sorted, B, k, 0, nb_s, ds_s, fa, anchors, &route);
+  certex_amd::scatter_rows(nb_s, d_order, B, int64_t(k) * 8, neighbors, stream);
+  certex_amd::scatter_rows(ds_s, d_order, B, int64_t(k) * 4, distances, stream);
+  CERTEX_HIP_TRY(hipStreamSynchronize(stream));  // the host tables above go out of scope
+}
+
 template <typename T>
 void search_impl(cuvs::resources const& res, search_params const& params, index<T> const& idx,
                  matrix_view<const T> queries, int64_t* neighbors, float* distances, int64_t k,
@@ -522,11 +715,17 @@ void search_impl(cuvs::resources const& res, search_params const& params, index<
   if (t_stats_on) { res.sync(); }
   const int64_t bs   = std::max(1, params.batch_size);
   const size_t qrow  = size_t(st.dim) * sizeof(T);
-  auto batch         = is_int(st.type) ? search_batch_int : search_batch_float;
+  const batch_fn batch = is_int(st.type) ? search_batch_int : search_batch_float;
   std::function<void(int64_t, int64_t)> run = [&](int64_t b0, int64_t B) {
     try {
-      batch(res, st, reinterpret_cast<const char*>(queries.data) + size_t(b0) * qrow, B, int(k),
-            b0, neighbors + b0 * k, distances + b0 * k, fa, params.anchors);
+      const char* q = reinterpret_cast<const char*>(queries.data) + size_t(b0) * qrow;
+      if (fa.kind == 3 && st.n_part > 0) {
+        routed_batch(res, st, batch, q, qrow, B, int(k), fa.query_labels + b0, neighbors + b0 * k,
+                     distances + b0 * k, fa, params.anchors);
+      } else {
+        batch(res, st, q, B, int(k), b0, neighbors + b0 * k, distances + b0 * k, fa,
+              params.anchors, nullptr);
+      }
     } catch (batch_too_large const&) {
       if (B < 2) { throw; }
       run(b0, B / 2);
@@ -614,6 +813,8 @@ template <typename T>
 auto index<T>::metric() const noexcept -> cuvs::distance::DistanceType { return s_->dmetric; }
 template <typename T>
 auto index<T>::has_labels() const noexcept -> bool { return s_->has_labels; }
+template <typename T>
+auto index<T>::n_partitioned() const noexcept -> int64_t { return s_->n_part; }
 template <typename T>
 auto index<T>::host_vectors() const noexcept -> bool { return s_->host_vectors; }
 template <typename T>
@@ -738,10 +939,13 @@ void remove(cuvs::resources const& res, const int64_t* ids, int64_t n_ids, index
   std::unique_lock publish(st.rw);
   CERTEX_HIP_TRY(hipDeviceSynchronize());
   certex_amd::fill_u32(reinterpret_cast<uint32_t*>(counter), 2, 0, stream);
+  const auto* ppos = st.part_pos.as<int32_t>();
   if (is_int(st.type)) {
-    certex_amd::remove_rows_i8(ids, n_ids, st.size, st.rowc.as<int32_t>(), counter, stream);
+    certex_amd::remove_rows_i8(ids, n_ids, st.size, st.rowc.as<int32_t>(), counter, stream, ppos,
+                               st.n_part, st.part_rowc.as<int32_t>());
   } else {
-    certex_amd::remove_rows_f16(ids, n_ids, st.size, st.rowc.as<float>(), counter, stream);
+    certex_amd::remove_rows_f16(ids, n_ids, st.size, st.rowc.as<float>(), counter, stream, ppos,
+                                st.n_part, st.part_rowc.as<float>());
   }
   CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, counter, 8, hipMemcpyDeviceToHost, stream));
   CERTEX_HIP_TRY(hipStreamSynchronize(stream));
@@ -768,6 +972,51 @@ void set_labels(cuvs::resources const& res, const int32_t* labels, int64_t n, in
                                   size_t(n) * sizeof(int32_t), hipMemcpyDeviceToDevice, stream));
   }
   CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  if (n > 0 && first < st.n_part) { st.n_part = 0; }  // the partition no longer matches
+}
+
+template <typename T>
+void partition_by_labels(cuvs::resources const& res, index<T>* idx)
+{
+  index_state& st = idx->state();
+  expects(st.has_labels, "certex: the index has no labels");
+  std::lock_guard w(st.writer);
+  const int64_t n = st.size;
+  expects(n < (int64_t(1) << 31), "certex: at most 2^31 - 1 vectors per partition");
+  hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  using cuvs::detail::device_buffer;
+  device_buffer keys(size_t(n) * 4), ids_tmp(size_t(n) * 4), ids(size_t(n) * 4),
+    pos(size_t(n) * 4), codes(size_t(n) * st.row_bytes), rowc(size_t(n) * 4);
+  std::vector<int64_t> offsets;
+  if (n > 0) {
+    const size_t tb = certex_amd::sort_by_label_temp_bytes(n);
+    device_buffer temp(std::max<size_t>(tb, 16));
+    CERTEX_HIP_TRY(certex_amd::sort_by_label(st.labels.as<int32_t>(), n, ids_tmp.as<int32_t>(),
+                                             keys.as<int32_t>(), ids.as<int32_t>(), temp.p, tb,
+                                             stream));
+    int32_t max_label = -1;
+    CERTEX_HIP_TRY(hipMemcpyAsync(&max_label, keys.as<int32_t>() + n - 1, 4,
+                                  hipMemcpyDeviceToHost, stream));
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+    const int64_t n_labels = int64_t(max_label) + 1;  // unlabeled rows (-1) sort first
+    device_buffer offs(size_t(n_labels + 1) * 8);
+    certex_amd::label_offsets(keys.as<int32_t>(), n, n_labels, offs.as<int64_t>(), stream);
+    offsets.resize(size_t(n_labels + 1));
+    CERTEX_HIP_TRY(hipMemcpyAsync(offsets.data(), offs.p, offsets.size() * 8,
+                                  hipMemcpyDeviceToHost, stream));
+    certex_amd::gather_rows(st.codes.p, ids.as<int32_t>(), n, st.row_bytes, codes.p, stream);
+    certex_amd::gather_rows(st.rowc.p, ids.as<int32_t>(), n, 4, rowc.p, stream);
+    certex_amd::invert_ids(ids.as<int32_t>(), n, pos.as<int32_t>(), stream);
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  }
+  std::unique_lock publish(st.rw);
+  CERTEX_HIP_TRY(hipDeviceSynchronize());  // searches on other streams may read the old copy
+  st.part_codes   = std::move(codes);
+  st.part_rowc    = std::move(rowc);
+  st.part_ids     = std::move(ids);
+  st.part_pos     = std::move(pos);
+  st.part_offsets = std::move(offsets);
+  st.n_part       = n;
 }
 
 template <typename T>
@@ -952,6 +1201,7 @@ void deserialize(cuvs::resources const& res, std::string const& filename, index<
   template void remove<T>(cuvs::resources const&, const int64_t*, int64_t, index<T>*);         \
   template void set_labels<T>(cuvs::resources const&, const int32_t*, int64_t, index<T>*,      \
                               int64_t);                                                        \
+  template void partition_by_labels<T>(cuvs::resources const&, index<T>*);                     \
   template void search<T>(cuvs::resources const&, search_params const&, index<T> const&,       \
                           matrix_view<const T>, int64_t*, float*, int64_t, filter);            \
   template void search<T>(cuvs::resources const&, search_params const&, index<T> const&,       \

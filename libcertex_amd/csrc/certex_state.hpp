@@ -100,6 +100,9 @@ enum ws_slot : int {
   ws_qscal,
   ws_grow,
   ws_vals,
+  ws_route,       // label routing of a batch: order, sorted labels, group tables
+  ws_route_q,     // the batch's queries in label order
+  ws_route_out,   // results in label order before they return to query order
   ws_n_slots
 };
 
@@ -168,6 +171,15 @@ struct index_state {
   double gamma   = 0.0;  // fp32 accumulation error factor of a screening product
   int halves     = 0;    // fp16 row length
   bool normalize = false;
+  // label partition (a speed option of label search): the screening rows and row terms of the
+  // ids [0, n_part) in label order; part_ids[i] = id of partition row i, part_pos[id] = its row;
+  // the rows of label l are [part_offsets[l], part_offsets[l + 1])
+  int64_t n_part = 0;
+  cuvs::detail::device_buffer part_codes;
+  cuvs::detail::device_buffer part_rowc;
+  cuvs::detail::device_buffer part_ids;
+  cuvs::detail::device_buffer part_pos;
+  std::vector<int64_t> part_offsets;
   mutable std::shared_mutex rw;  // searches: shared per batch; publication of updates: exclusive
   std::mutex writer;             // one update at a time
 };

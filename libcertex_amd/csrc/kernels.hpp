@@ -65,7 +65,9 @@ void encode_queries_i8(const uint8_t* q, int64_t nq, int64_t nq_pad, int64_t dim
  * *newly_removed (ids out of range or repeated count once at most).
  */
 void remove_rows_i8(const int64_t* ids, int64_t n, int64_t size, int32_t* rowc,
-                    unsigned long long* newly_removed, hipStream_t stream);
+                    unsigned long long* newly_removed, hipStream_t stream,
+                    const int32_t* part_pos = nullptr, int64_t n_part = 0,
+                    int32_t* part_rowc = nullptr);
 
 void fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);
 void fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream);
@@ -81,11 +83,29 @@ struct filter_args {
   const int32_t* query_labels = nullptr;  // of all queries of the search
 };
 
+/**
+ * One routed pairing of a label-partitioned search: the queries [q0, q0 + nq) of the (label
+ * sorted) batch against the stored rows [x0, x0 + nx) of the partition; its workgroups are
+ * tile0 .. tile0 + ceil(nq / QB) * chunks - 1 of the launch.
+ */
+struct screen_group {
+  int64_t q0, nq;
+  int64_t x0, nx;
+  int64_t tile0;
+};
+
 struct screen_args {
   const int8_t* codes;   // stored rows [*, row_bytes]: int8 codes or fp16 values
   const void* rowc;      // row terms: int32 (int8 rows) or float (fp16 rows)
-  int64_t n_scan;        // scanned rows: scan index i reads stored row i * row_stride
+  int64_t n_scan;        // scanned rows: scan index i reads stored row row_base + i * row_stride
+  int64_t row_base = 0;  // first stored row of the pass
   int row_stride;        // 1 for the screen, the anchor stride for the anchor pass
+  // routed pass (label partition): the workgroups follow the group table (n_scan and row_base
+  // come from each group); the survivors' stored rows map to ids through row_ids
+  const screen_group* groups = nullptr;
+  int n_route                = 0;
+  int64_t n_tiles            = 0;  // workgroups of a routed launch
+  const int32_t* row_ids     = nullptr;
   int row_bytes;         // 64 KS
   const int8_t* qcodes;  // [nq_pad, row_bytes]
   const void* theta;     // [nq_pad] int32 or float (screen only)
@@ -104,8 +124,18 @@ struct screen_args {
   void* gmax       = nullptr;
   uint32_t* grow   = nullptr;
   int64_t n_groups = 0;
+  int64_t grp_base = 0;  // first group column of the pass
   int group_steps  = 1;
 };
+
+/** Queries per workgroup of the screen kernels for a batch padded to nq_pad. */
+int screen_query_block(bool f16, int row_bytes, int64_t nq_pad);
+/** Workgroups of one routed group: query blocks x row chunks. */
+inline int64_t screen_group_tiles(int64_t nq, int64_t n_scan, int qb, int chunk_steps)
+{
+  const int64_t steps = (n_scan + kStepRows - 1) / kStepRows;
+  return (nq + qb - 1) / qb * ((steps + chunk_steps - 1) / chunk_steps);
+}
 
 /** Steps of kStepRows rows that cover n_scan rows. */
 __host__ __device__ inline int64_t screen_steps(int64_t n_scan) { return (n_scan + kStepRows - 1) / kStepRows; }
@@ -215,9 +245,14 @@ void encode_queries_f16(const void* q, elem t, int64_t nq, int64_t nq_pad, int64
                         int halves, bool normalize, const double* center, double inv_alpha,
                         uint16_t* qrows, double* qscal, hipStream_t stream);
 
-/** Float tombstones: rowc[id] = -inf; counts the ids that were live. */
+/**
+ * Float tombstones: rowc[id] = -inf; counts the ids that were live. With a label partition, the
+ * partition's copy of the row term (part_rowc[part_pos[id]], id < n_part) is tombstoned too.
+ */
 void remove_rows_f16(const int64_t* ids, int64_t n, int64_t size, float* rowc,
-                     unsigned long long* newly_removed, hipStream_t stream);
+                     unsigned long long* newly_removed, hipStream_t stream,
+                     const int32_t* part_pos = nullptr, int64_t n_part = 0,
+                     float* part_rowc = nullptr);
 
 struct threshold_f_args {
   const float* gmax;     // [nq_pad, n_groups]
@@ -275,6 +310,28 @@ struct verify_f_args {
  * values, only the candidates whose certified lower bound can reach the top k are scored.
  */
 void verify_topk_f(const verify_f_args& a, hipStream_t stream);
+
+// --- label partition and routing ------------------------------------------------------------
+
+/** Temporary bytes of sort_by_label for n rows. */
+size_t sort_by_label_temp_bytes(int64_t n);
+/**
+ * Stable sort of the ids 0 .. n-1 by label (unlabeled -1 first): keys_out = sorted labels,
+ * ids_out = ids in label order (ascending within a label). n < 2^31.
+ */
+hipError_t sort_by_label(const int32_t* labels, int64_t n, int32_t* ids_scratch, int32_t* keys_out,
+                         int32_t* ids_out, void* temp, size_t temp_bytes, hipStream_t stream);
+/** offsets[l] = first position of label >= l in keys_sorted, l = 0 .. n_labels. */
+void label_offsets(const int32_t* keys_sorted, int64_t n, int64_t n_labels, int64_t* offsets,
+                   hipStream_t stream);
+/** dst row i = src row ids[i] (rows of row_bytes bytes). */
+void gather_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes, void* dst,
+                 hipStream_t stream);
+/** dst row ids[i] = src row i. */
+void scatter_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes, void* dst,
+                  hipStream_t stream);
+/** pos[ids[i]] = i. */
+void invert_ids(const int32_t* ids, int64_t n, int32_t* pos, hipStream_t stream);
 
 /**
  * Output conversion: distances (l2: score; inner: -score = <q, x>; cosine: score + 1 = 1 - cos)

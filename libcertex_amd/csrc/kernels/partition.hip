@@ -1,0 +1,148 @@
+// Label partition of the screening rows and the per-batch routing moves (gfx950).
+//
+// Reference contract: partition_by_labels (certex.cu:1542-1606: a stable sort of the ids by
+// label, the start of every label, the rows copied in label order) and the query permutation of
+// search_by_labels (certex.cu:1613-1735: the batch in label order, results back in query order).
+// The sort is hipCUB's radix sort over (label, id) pairs, stable, so the ids of one label stay
+// ascending; unlabeled rows (-1) sort first and match no query.
+
+#include "../kernels.hpp"
+
+#include <hipcub/hipcub.hpp>
+
+namespace certex_amd {
+namespace {
+
+inline unsigned blocks_for(int64_t n, int64_t cap = int64_t(1) << 20)
+{
+  const int64_t b = (n + 255) / 256;
+  return unsigned(b < cap ? b : cap);
+}
+
+__global__ void iota_kernel(int32_t* p, int64_t n)
+{
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    p[i] = int32_t(i);
+  }
+}
+
+/** offsets[l] = the first sorted position whose label is >= l, for l = 0 .. n_labels. */
+__global__ void label_offsets_kernel(const int32_t* keys, int64_t n, int64_t n_labels,
+                                     int64_t* offsets)
+{
+  const int64_t l = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (l > n_labels) { return; }
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (keys[mid] < l) {
+      lo = mid + 1;
+    } else {
+      hi = mid;
+    }
+  }
+  offsets[l] = lo;
+}
+
+/** dst row i = src row ids[i], rows of `units` 16-byte units. */
+__global__ void gather_units_kernel(const int4* src, const int32_t* ids, int64_t n, int64_t units,
+                                    int4* dst)
+{
+  const int64_t total = n * units;
+  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < total;
+       t += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t i = t / units, u = t % units;
+    dst[t]          = src[int64_t(ids[i]) * units + u];
+  }
+}
+
+/** dst row i = src row ids[i], rows of `bytes` bytes (any length). */
+__global__ void gather_bytes_kernel(const uint8_t* src, const int32_t* ids, int64_t n,
+                                    int64_t bytes, uint8_t* dst)
+{
+  const int64_t total = n * bytes;
+  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < total;
+       t += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t i = t / bytes, b = t % bytes;
+    dst[t]          = src[int64_t(ids[i]) * bytes + b];
+  }
+}
+
+/** dst row ids[i] = src row i, rows of `bytes` bytes. */
+__global__ void scatter_bytes_kernel(const uint8_t* src, const int32_t* ids, int64_t n,
+                                     int64_t bytes, uint8_t* dst)
+{
+  const int64_t total = n * bytes;
+  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < total;
+       t += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t i = t / bytes, b = t % bytes;
+    dst[int64_t(ids[i]) * bytes + b] = src[t];
+  }
+}
+
+/** pos[ids[i]] = i. */
+__global__ void invert_kernel(const int32_t* ids, int64_t n, int32_t* pos)
+{
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    pos[ids[i]] = int32_t(i);
+  }
+}
+
+}  // namespace
+
+size_t sort_by_label_temp_bytes(int64_t n)
+{
+  size_t bytes = 0;
+  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, static_cast<const int32_t*>(nullptr),
+                                           static_cast<int32_t*>(nullptr),
+                                           static_cast<const int32_t*>(nullptr),
+                                           static_cast<int32_t*>(nullptr), int(n), 0, 32);
+  return bytes;
+}
+
+hipError_t sort_by_label(const int32_t* labels, int64_t n, int32_t* ids_scratch, int32_t* keys_out,
+                         int32_t* ids_out, void* temp, size_t temp_bytes, hipStream_t stream)
+{
+  if (n == 0) { return hipSuccess; }
+  iota_kernel<<<blocks_for(n), 256, 0, stream>>>(ids_scratch, n);
+  return hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, labels, keys_out, ids_scratch,
+                                            ids_out, int(n), 0, 32, stream);
+}
+
+void label_offsets(const int32_t* keys_sorted, int64_t n, int64_t n_labels, int64_t* offsets,
+                   hipStream_t stream)
+{
+  label_offsets_kernel<<<unsigned((n_labels + 1 + 255) / 256), 256, 0, stream>>>(
+    keys_sorted, n, n_labels, offsets);
+}
+
+void gather_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes, void* dst,
+                 hipStream_t stream)
+{
+  if (n == 0 || row_bytes == 0) { return; }
+  if (row_bytes % 16 == 0) {
+    gather_units_kernel<<<blocks_for(n * (row_bytes / 16)), 256, 0, stream>>>(
+      static_cast<const int4*>(src), ids, n, row_bytes / 16, static_cast<int4*>(dst));
+  } else {
+    gather_bytes_kernel<<<blocks_for(n * row_bytes), 256, 0, stream>>>(
+      static_cast<const uint8_t*>(src), ids, n, row_bytes, static_cast<uint8_t*>(dst));
+  }
+}
+
+void scatter_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes, void* dst,
+                  hipStream_t stream)
+{
+  if (n == 0 || row_bytes == 0) { return; }
+  scatter_bytes_kernel<<<blocks_for(n * row_bytes), 256, 0, stream>>>(
+    static_cast<const uint8_t*>(src), ids, n, row_bytes, static_cast<uint8_t*>(dst));
+}
+
+void invert_ids(const int32_t* ids, int64_t n, int32_t* pos, hipStream_t stream)
+{
+  if (n == 0) { return; }
+  invert_kernel<<<blocks_for(n), 256, 0, stream>>>(ids, n, pos);
+}
+
+}  // namespace certex_amd

@@ -76,28 +76,24 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   const int lane = tid & 63;
   const int wave = tid >> 6;
 
-  const int64_t n_steps  = screen_steps(a.n_scan);
-  const int64_t n_chunks = (n_steps + a.chunk_steps - 1) / a.chunk_steps;
-  const int n_qb         = int(a.nq_pad / QB);
-  const uint32_t b       = blockIdx.x;
-  const uint32_t i       = b >> 3;
-  const int qb           = int(i % uint32_t(n_qb));
-  const int64_t chunk    = int64_t(i / uint32_t(n_qb)) * 8 + (b & 7);
-  if (chunk >= n_chunks) { return; }
-  const int64_t q0 = int64_t(qb) * QB;
+  const screen_work w = work_of<QB>(a, blockIdx.x);
+  if (!w.valid) { return; }
+  const int64_t n_steps = screen_steps(w.n_scan);
+  const int64_t q0      = w.q0;
   // groups of 64 queries holding a live query, rounded up to a pair (the last query block of a
-  // batch is partly padding)
-  const int64_t live = a.nq - q0;
+  // batch or of a routed group is partly padding)
+  const int64_t live = w.q_end - q0;
   const int ng       = live >= QB ? NG : int(((live + 63) / 64 + 1) & ~int64_t(1));
   // this wave's steps: a contiguous quarter of the chunk (a whole number of anchor groups)
   const int64_t quarter = a.chunk_steps / 4;
-  const int64_t w0      = chunk * a.chunk_steps + wave * quarter;
+  const int64_t w0      = w.chunk * a.chunk_steps + wave * quarter;
   const int64_t w1      = w0 + quarter < n_steps ? w0 + quarter : n_steps;
 
   if (tid == 0) { n_hits = 0; }
   for (int e = tid; e < QB * (ROWB / 16); e += 256) {
     const int r = e / (ROWB / 16), c = e % (ROWB / 16);
-    const v4i v = *reinterpret_cast<const v4i*>(a.qcodes + (q0 + r) * ROWB + 16 * c);
+    v4i v       = {0, 0, 0, 0};
+    if (q0 + r < w.q_end) { v = *reinterpret_cast<const v4i*>(a.qcodes + (q0 + r) * ROWB + 16 * c); }
     *reinterpret_cast<v4i*>(qlds + r * ROWB + 16 * slot<KS>(r, c)) = v;
   }
   if constexpr (ANCHORS) {
@@ -106,7 +102,9 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
       if constexpr (ARGMX) { gmr[e] = 0xffffffffu; }
     }
   } else {
-    for (int e = tid; e < QB; e += 256) { thl[e] = theta[q0 + e]; }
+    for (int e = tid; e < QB; e += 256) {
+      thl[e] = q0 + e < w.q_end ? theta[q0 + e] : R::keep_none();
+    }
   }
   __syncthreads();
 
@@ -116,19 +114,19 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
       int64_t r = s * kStepRows + bt * 16 + (lane & 15);
-      r         = r < a.n_scan ? r : 0;  // rows past the end read row 0; their term kills them
-      const int8_t* src = a.codes + r * a.row_stride * ROWB + (lane >> 4) * 16;
+      r         = r < w.n_scan ? r : 0;  // rows past the end read row 0; their term kills them
+      const int8_t* src = a.codes + (w.base + r * a.row_stride) * ROWB + (lane >> 4) * 16;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         av[bt][ks] = *reinterpret_cast<const frag_t*>(src + 64 * ks);
       }
       const int64_t r4 = s * kStepRows + bt * 16 + (lane >> 4) * 4;
-      if (a.row_stride == 1 && r4 + 3 < a.n_scan) {
-        cc[bt] = *reinterpret_cast<const acc_t*>(rowc + r4);
+      if (a.row_stride == 1 && r4 + 3 < w.n_scan) {
+        cc[bt] = *reinterpret_cast<const acc_t*>(rowc + w.base + r4);
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          cc[bt][j] = r4 + j < a.n_scan ? rowc[(r4 + j) * a.row_stride] : R::dead();
+          cc[bt][j] = r4 + j < w.n_scan ? rowc[w.base + (r4 + j) * a.row_stride] : R::dead();
         }
       }
     }
@@ -167,7 +165,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
       for (int qt = 0; qt < 4; ++qt) {
         const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
         anchor_tile<R, FILT>(col, row0, q0 + g * 64 + qt * 16 + (lane & 15),
-                             wave * QB + g * 64 + qt * 16 + lane, a, gml, gmr);
+                             wave * QB + g * 64 + qt * 16 + lane, a, w, gml, gmr);
       }
     } else {
       val_t mq[4];
@@ -200,7 +198,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
                                  acc[1][qt][0], acc[1][qt][1], acc[1][qt][2], acc[1][qt][3],
                                  acc[2][qt][0], acc[2][qt][1], acc[2][qt][2], acc[2][qt][3],
                                  acc[3][qt][0], acc[3][qt][1], acc[3][qt][2], acc[3][qt][3]};
-          push_hits<FILT, R::kValues>(bits, qloc, row0, q0, a, hits, v16);
+          push_hits<FILT, R::kValues>(bits, qloc, w.base + row0, q0, a, hits, v16);
         }
       }
     }
@@ -222,14 +220,14 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     if constexpr (ANCHORS) {
       // end of an anchor group (group_steps steps, aligned to the wave's range)
       if ((s + 1) % a.group_steps == 0 || s + 1 == n_steps) {
-        const int64_t grp = s / a.group_steps;
+        const int64_t grp = a.grp_base + s / a.group_steps;
         for (int e = lane; e < QB; e += 64) {
-          gmax[(q0 + e) * a.n_groups + grp] = gml[wave * QB + e];
-          gml[wave * QB + e]                = R::lowest();
-          if constexpr (ARGMX) {
-            a.grow[(q0 + e) * a.n_groups + grp] = gmr[wave * QB + e];
-            gmr[wave * QB + e]                  = 0xffffffffu;
+          if (q0 + e < w.q_end) {
+            gmax[(q0 + e) * a.n_groups + grp] = gml[wave * QB + e];
+            if constexpr (ARGMX) { a.grow[(q0 + e) * a.n_groups + grp] = gmr[wave * QB + e]; }
           }
+          gml[wave * QB + e] = R::lowest();
+          if constexpr (ARGMX) { gmr[wave * QB + e] = 0xffffffffu; }
         }
       }
     }
@@ -244,12 +242,17 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 template <typename R, bool ANCHORS, bool FILT>
 void launch(const screen_args& a, hipStream_t stream)
 {
-  const int qb_size      = screen_block_queries(a.nq_pad);
-  const int64_t n_steps  = screen_steps(a.n_scan);
-  const int64_t n_chunks = (n_steps + a.chunk_steps - 1) / a.chunk_steps;
-  const int64_t n_qb     = a.nq_pad / qb_size;
-  const int64_t blocks   = 8 * n_qb * ((n_chunks + 7) / 8);
-  if (n_steps == 0 || n_qb == 0) { return; }
+  const int qb_size = screen_block_queries(a.nq_pad);
+  int64_t blocks    = 0;
+  if (a.groups != nullptr) {
+    blocks = a.n_tiles;
+  } else {
+    const int64_t n_steps  = screen_steps(a.n_scan);
+    const int64_t n_chunks = (n_steps + a.chunk_steps - 1) / a.chunk_steps;
+    const int64_t n_qb     = (a.nq + qb_size - 1) / qb_size;
+    blocks                 = n_steps == 0 ? 0 : 8 * n_qb * ((n_chunks + 7) / 8);
+  }
+  if (blocks == 0) { return; }
   const dim3 grid{unsigned(blocks)};
   const int ks = a.row_bytes / 64;
   if (ks == 2 && qb_size == 512) {
@@ -265,6 +268,13 @@ void launch(const screen_args& a, hipStream_t stream)
 }
 
 }  // namespace
+
+int wide_block_queries(int row_bytes);  // screen_wide.hip
+
+int screen_query_block(bool f16, int row_bytes, int64_t nq_pad)
+{
+  return f16 && row_bytes > 256 ? wide_block_queries(row_bytes) : screen_block_queries(nq_pad);
+}
 
 void screen_i8(const screen_args& a, hipStream_t stream)
 {

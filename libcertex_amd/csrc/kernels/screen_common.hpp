@@ -33,6 +33,7 @@ struct int8_rows {
   }
   __device__ static val_t lowest() { return INT_MIN; }
   __device__ static val_t dead() { return kDeadRow; }
+  __device__ static val_t keep_none() { return kKeepNone; }  // no screen value reaches it
   __device__ static val_t vmax(val_t a, val_t b) { return max(a, b); }
 };
 
@@ -48,8 +49,69 @@ struct f16_rows {
   }
   __device__ static val_t lowest() { return -INFINITY; }
   __device__ static val_t dead() { return -INFINITY; }
+  __device__ static val_t keep_none() { return __builtin_nanf(""); }  // no value compares >= NaN
   __device__ static val_t vmax(val_t a, val_t b) { return fmaxf(a, b); }
 };
+
+/** The share of one workgroup of a screen launch. */
+struct screen_work {
+  int64_t q0;      // first query of the block
+  int64_t q_end;   // queries [q0, q_end) are live (others in the block are padding)
+  int64_t chunk;   // row chunk: scan steps [chunk * chunk_steps, (chunk + 1) * chunk_steps)
+  int64_t n_scan;  // scan indices of the pass
+  int64_t base;    // stored row of scan index i: base + i * row_stride
+  bool valid;
+};
+
+/**
+ * Work of block b. Plain launches: block b runs on XCD b % 8 and the query blocks of one row
+ * chunk are consecutive on one XCD (chunk = (b / 8 / n_qb) * 8 + b % 8). Routed launches: the
+ * group whose tiles hold b (binary search over tile0), then query block and chunk within it.
+ */
+template <int QB>
+__device__ inline screen_work work_of(const screen_args& a, uint32_t b)
+{
+  screen_work w;
+  if (a.groups == nullptr) {
+    const int64_t n_steps  = screen_steps(a.n_scan);
+    const int64_t n_chunks = (n_steps + a.chunk_steps - 1) / a.chunk_steps;
+    const uint32_t n_qb    = uint32_t((a.nq + QB - 1) / QB);
+    const uint32_t i       = b >> 3;
+    w.q0                   = int64_t(i % n_qb) * QB;
+    w.q_end                = a.nq;
+    w.chunk                = int64_t(i / n_qb) * 8 + (b & 7);
+    w.n_scan               = a.n_scan;
+    w.base                 = a.row_base;
+    w.valid                = w.chunk < n_chunks;
+    return w;
+  }
+  int lo = 0, hi = a.n_route - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (a.groups[mid].tile0 <= int64_t(b)) {
+      lo = mid;
+    } else {
+      hi = mid - 1;
+    }
+  }
+  const screen_group g = a.groups[lo];
+  const int64_t t      = int64_t(b) - g.tile0;
+  const int64_t n_qb   = (g.nq + QB - 1) / QB;
+  w.q0                 = g.q0 + (t % n_qb) * QB;
+  w.q_end              = g.q0 + g.nq;
+  w.chunk              = t / n_qb;
+  w.n_scan             = (g.nx + a.row_stride - 1) / a.row_stride;
+  w.base               = g.x0;
+  const int64_t steps  = screen_steps(w.n_scan);
+  w.valid              = t >= 0 && w.chunk < (steps + a.chunk_steps - 1) / a.chunk_steps;
+  return w;
+}
+
+/** Id of stored row r (the partition's rows map through row_ids). */
+__device__ inline uint32_t row_id(const screen_args& a, int64_t r)
+{
+  return a.row_ids != nullptr ? uint32_t(a.row_ids[r]) : uint32_t(r);
+}
 
 /** Filter test of a pair (query q of the batch, stored row). */
 __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
@@ -75,7 +137,7 @@ struct hit_list {
 
 /**
  * Appends the survivors of one 16-query tile of a step to the workgroup's list: `bits` is this
- * lane's survivor mask, `qloc` its query within the workgroup. One round per survivor of the
+ * lane's survivor mask, `qloc` its query within the workgroup, row0 the stored row of its bit 0. One round per survivor of the
  * busiest lane: ballot, rank by mbcnt, one LDS reservation per round; a full list spills straight
  * into the global bucket. Every lane of the wave must call it.
  */
@@ -88,8 +150,9 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
     while (scan) {
       const int j = __builtin_ctz(scan);
       scan &= scan - 1;
-      const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
-      if (!keeps(a.filter, q0 + qloc, row)) { bits &= ~(1u << j); }
+      if (!keeps(a.filter, q0 + qloc, row_id(a, row0 + (j >> 2) * 16 + (j & 3)))) {
+        bits &= ~(1u << j);
+      }
     }
   }
   const int lane = threadIdx.x & 63;
@@ -105,7 +168,7 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
     if (bits) {
       const int j = __builtin_ctz(bits);
       bits &= bits - 1;
-      const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
+      const uint32_t row = row_id(a, row0 + (j >> 2) * 16 + (j & 3));
       const uint32_t pos = base + rank;
       float val          = 0.0f;
       if constexpr (VALS) {
@@ -147,12 +210,14 @@ __device__ inline void flush_hits(int64_t q0, const screen_args& a, hit_list h)
  * Anchor pass, one 16-query tile of a 64-row step: folds the best screen value of this lane's
  * query over the step (and, for fp16 rows, the stored row holding it, ties to the lower row) into
  * the wave's running group maximum gml[e] / gmr[e] (e = the query's slot). `col[bt]` holds the
- * tile's accumulators of row tile bt. Scan indices at or past n_scan are padding.
+ * tile's accumulators of row tile bt; row0 is the scan index of its bit 0. Scan indices at or past
+ * the work's n_scan are padding.
  */
 template <typename R, bool FILT>
 __device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], int64_t row0,
                                             int64_t q, int e, const screen_args& a,
-                                            typename R::val_t* gml, uint32_t* gmr)
+                                            const screen_work& w, typename R::val_t* gml,
+                                            uint32_t* gmr)
 {
   using val_t         = typename R::val_t;
   constexpr bool ARGX = R::kArgmax;
@@ -166,7 +231,7 @@ __device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], i
       val_t v = col[bt][r];
       if constexpr (FILT) {
         const int64_t idx = row0 + bt * 16 + r;
-        if (idx < a.n_scan && !keeps(a.filter, q, uint32_t(idx * a.row_stride))) {
+        if (idx < w.n_scan && !keeps(a.filter, q, row_id(a, w.base + idx * a.row_stride))) {
           v = R::lowest();
         }
       }
@@ -181,7 +246,7 @@ __device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], i
     }
   }
   if constexpr (ARGX) {
-    uint32_t row = uint32_t((row0 + j) * a.row_stride);
+    uint32_t row = row_id(a, w.base + (row0 + j) * a.row_stride);
 #pragma unroll
     for (int off = 16; off <= 32; off <<= 1) {
       const val_t om     = __shfl_xor(m, off);

@@ -67,25 +67,20 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
   const int NC    = H / 64;           // K chunks, even
   const int RB    = a.row_bytes;      // bytes per row (stored rows and LDS query rows)
 
-  const int64_t n_steps  = screen_steps(a.n_scan);
-  const int64_t n_chunks = (n_steps + a.chunk_steps - 1) / a.chunk_steps;
-  const int n_qb         = int((a.nq + QB - 1) / QB);
-  const uint32_t b       = blockIdx.x;
-  const uint32_t i       = b >> 3;
-  const int qb           = int(i % uint32_t(n_qb));
-  const int64_t chunk    = int64_t(i / uint32_t(n_qb)) * 8 + (b & 7);
-  if (chunk >= n_chunks) { return; }
-  const int64_t q0     = int64_t(qb) * QB;
-  const int64_t eighth = a.chunk_steps / kWideWaves;  // whole anchor groups
-  const int64_t w0     = chunk * a.chunk_steps + wave * eighth;
-  const int64_t w1     = w0 + eighth < n_steps ? w0 + eighth : n_steps;
+  const screen_work w = work_of<QB>(a, blockIdx.x);
+  if (!w.valid) { return; }
+  const int64_t n_steps = screen_steps(w.n_scan);
+  const int64_t q0      = w.q0;
+  const int64_t eighth  = a.chunk_steps / kWideWaves;  // whole anchor groups
+  const int64_t w0      = w.chunk * a.chunk_steps + wave * eighth;
+  const int64_t w1      = w0 + eighth < n_steps ? w0 + eighth : n_steps;
 
   if (tid == 0) { n_hits = 0; }
   const int cpr = RB / 16;  // 16-byte chunks per row
   for (int e = tid; e < QB * cpr; e += 64 * kWideWaves) {
     const int r = e / cpr, c = e % cpr;
     v4i v       = {0, 0, 0, 0};
-    if (q0 + r < a.nq) { v = *reinterpret_cast<const v4i*>(a.qcodes + (q0 + r) * RB + 16 * c); }
+    if (q0 + r < w.q_end) { v = *reinterpret_cast<const v4i*>(a.qcodes + (q0 + r) * RB + 16 * c); }
     *reinterpret_cast<v4i*>(qlds + r * RB + 16 * (c ^ (r & 15))) = v;
   }
   if constexpr (ANCHORS) {
@@ -96,7 +91,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
   } else {
     for (int e = tid; e < QB; e += 64 * kWideWaves) {
       // a padding query keeps nothing: no value compares >= NaN (not even a +inf row term)
-      thl[e] = q0 + e < a.nq ? theta[q0 + e] : __builtin_nanf("");
+      thl[e] = q0 + e < w.q_end ? theta[q0 + e] : R::keep_none();
     }
   }
   __syncthreads();
@@ -110,8 +105,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
       int64_t r = s * kStepRows + bt * 16 + (lane & 15);
-      r         = r < a.n_scan ? r : 0;  // rows past the end read row 0; their term kills them
-      P[bt]     = codes + r * a.row_stride * RB + (lane >> 4) * 32;
+      r         = r < w.n_scan ? r : 0;  // rows past the end read row 0; their term kills them
+      P[bt]     = codes + (w.base + r * a.row_stride) * RB + (lane >> 4) * 32;
     }
   };
   auto load_chunk = [&](const gbytes (&P)[4], int64_t off, frag_t (&A)[4][2]) {
@@ -127,8 +122,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
       const int64_t r4 = s * kStepRows + bt * 16 + (lane >> 4) * 4;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const bool ok  = r4 + j < a.n_scan;
-        const float v  = rowc[(ok ? r4 + j : 0) * a.row_stride];
+        const bool ok  = r4 + j < w.n_scan;
+        const float v  = rowc[w.base + (ok ? r4 + j : 0) * a.row_stride];
         cc[bt][j]      = ok ? v : R::dead();
       }
     }
@@ -189,13 +184,13 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
       for (int qt = 0; qt < QT; ++qt) {
         const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
         anchor_tile<R, FILT>(col, row0, q0 + qt * 16 + (lane & 15), wave * QB + qt * 16 + lane, a,
-                             gml, gmr);
+                             w, gml, gmr);
       }
       // end of an anchor group (group_steps steps, aligned to the wave's range)
       if ((s + 1) % a.group_steps == 0 || s + 1 == n_steps) {
-        const int64_t grp = s / a.group_steps;
+        const int64_t grp = a.grp_base + s / a.group_steps;
         for (int e = lane; e < QB; e += 64) {
-          if (q0 + e < a.nq) {
+          if (q0 + e < w.q_end) {
             gmax[(q0 + e) * a.n_groups + grp]   = gml[wave * QB + e];
             a.grow[(q0 + e) * a.n_groups + grp] = gmr[wave * QB + e];
           }
@@ -234,7 +229,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
                                  acc[1][qt][0], acc[1][qt][1], acc[1][qt][2], acc[1][qt][3],
                                  acc[2][qt][0], acc[2][qt][1], acc[2][qt][2], acc[2][qt][3],
                                  acc[3][qt][0], acc[3][qt][1], acc[3][qt][2], acc[3][qt][3]};
-          push_hits<FILT, true>(bits, uint32_t(qt * 16 + (lane & 15)), row0, q0, a, hits, v16);
+          push_hits<FILT, true>(bits, uint32_t(qt * 16 + (lane & 15)), w.base + row0, q0, a, hits,
+                                v16);
         }
       }
     }
@@ -283,14 +279,20 @@ int wide_query_tiles(int row_bytes)
 template <bool ANCHORS, bool FILT>
 void launch(const screen_args& a, hipStream_t stream)
 {
-  const int qt           = wide_query_tiles(a.row_bytes);
-  const int qb           = 16 * qt;
-  const int64_t n_steps  = screen_steps(a.n_scan);
-  const int64_t n_chunks = (n_steps + a.chunk_steps - 1) / a.chunk_steps;
-  const int64_t n_qb     = (a.nq + qb - 1) / qb;
-  if (n_steps == 0 || n_qb == 0) { return; }
+  const int qt = wide_query_tiles(a.row_bytes);
+  const int qb = 16 * qt;
   if (qt == 0) { throw std::invalid_argument("certex: the fp16 rows are too wide for the LDS"); }
-  const dim3 grid{unsigned(8 * n_qb * ((n_chunks + 7) / 8))};
+  int64_t blocks = 0;
+  if (a.groups != nullptr) {
+    blocks = a.n_tiles;
+  } else {
+    const int64_t n_steps  = screen_steps(a.n_scan);
+    const int64_t n_chunks = (n_steps + a.chunk_steps - 1) / a.chunk_steps;
+    const int64_t n_qb     = (a.nq + qb - 1) / qb;
+    blocks                 = n_steps == 0 ? 0 : 8 * n_qb * ((n_chunks + 7) / 8);
+  }
+  if (blocks == 0) { return; }
+  const dim3 grid{unsigned(blocks)};
   const size_t lds = size_t(qb) * size_t(a.row_bytes);
   switch (qt) {
     case 6: launch_qt<6, ANCHORS, FILT>(a, grid, lds, stream); break;
@@ -300,6 +302,8 @@ void launch(const screen_args& a, hipStream_t stream)
 }
 
 }  // namespace
+
+int wide_block_queries(int row_bytes) { return 16 * wide_query_tiles(row_bytes); }
 
 void screen_f16_wide(const screen_args& a, hipStream_t stream)
 {

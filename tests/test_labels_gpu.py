@@ -1,0 +1,113 @@
+"""Label search over the label partition (routed) against the CPU oracle.
+
+The partition is a speed option (reference certex.cu:1542-1735): every label's queries screen only
+that label's rows, the rows added after the partition go through the label filter, and results
+must stay bit-exact: ids equal to the oracle's exhaustive fp64 search among the rows of the
+query's label, ties to the lower id. Cases follow the reference's label tests
+(tests/test_exact.py label cases, ann_certex.cuh label matrix): skewed and missing labels,
+queries whose label has no rows, additions and removals after the partition, ragged batches.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import libcertex_amd as certex
+import oracle
+from tests import data
+
+pytestmark = pytest.mark.gpu
+
+
+def check(X, Q, k, metric, D, I, **okw):
+    s, i = oracle.knn(X, Q, k, metric, **okw)
+    np.testing.assert_array_equal(I, i)
+    d = oracle.distances(s, i, metric)
+    if metric == "cosine":
+        d = np.where(i >= 0, np.float32(1) - d, -np.inf).astype(np.float32)
+    np.testing.assert_array_equal(D, d)
+
+
+def search(idx, Q, k, ql, batch=2048):
+    D, I = idx.search(torch.from_numpy(Q).cuda(), k=k, batch=batch, labels=torch.from_numpy(ql))
+    torch.cuda.synchronize()
+    return D.cpu().numpy(), I.cpu().numpy()
+
+
+def skewed_labels(n, seed, n_classes=16):
+    """Labels with a skewed histogram: class c has weight 2^-c / ..., class 5 is never used."""
+    w = 0.5 ** np.arange(n_classes)
+    w[5] = 0
+    return np.random.default_rng(seed).choice(n_classes, n, p=w / w.sum()).astype(np.int32)
+
+
+@pytest.mark.parametrize("dtype", [np.uint8, np.int8])
+def test_integer_routed(gpu, dtype):
+    X = data.mixture_u8(40_000, seed=61) if dtype == np.uint8 else data.uniform_int(40_000, 96, 61, np.int8)
+    Q = data.mixture_u8(700, seed=62) if dtype == np.uint8 else data.uniform_int(700, 96, 62, np.int8)
+    lx, lq = skewed_labels(len(X), 63), data.labels(len(Q), 18, 64)  # labels 16, 17 and 5: no rows
+    idx = certex.Index(X.shape[1])
+    idx.add(torch.from_numpy(X).cuda(), labels=torch.from_numpy(lx))
+    assert idx.core is not None
+    for batch in (2048, 150):
+        D, I = search(idx, Q, 10, lq, batch)
+        check(X, Q, 10, "l2", D, I, row_labels=lx, query_labels=lq)
+
+
+@pytest.mark.parametrize("metric,d", [("l2", 64), ("cosine", 64), ("ip", 300), ("cosine", 768)])
+def test_float_routed(gpu, metric, d):
+    X = data.powerlaw_unit(30_000, d, seed=65) * np.float32(1.0 if metric != "ip" else 3.0)
+    Q = data.powerlaw_unit(400, d, seed=66)
+    lx, lq = data.labels(len(X), 16, 67), data.labels(len(Q), 16, 68)
+    idx = certex.Index(d, metric=metric)
+    idx.add(torch.from_numpy(X).cuda(), labels=torch.from_numpy(lx))
+    D, I = search(idx, Q, 50, lq, batch=256)
+    check(X, Q, 50, metric, D, I, row_labels=lx, query_labels=lq)
+
+
+def test_tail_after_partition_and_removals(gpu):
+    """Rows added after the partition (the tail) go through the label filter; removals reach the
+    partition's copy of the rows."""
+    X = data.mixture_u8(50_000, seed=71)
+    Q = data.mixture_u8(300, seed=72)
+    lx, lq = data.labels(len(X), 8, 73), data.labels(len(Q), 8, 74)
+    idx = certex.Index(128)
+    idx.add(torch.from_numpy(X[:30_000]).cuda(), labels=torch.from_numpy(lx[:30_000]))
+    idx.partition_labels = False  # the next rows stay outside the partition
+    idx.add(torch.from_numpy(X[30_000:]).cuda(), labels=torch.from_numpy(lx[30_000:]))
+    _, nn = oracle.knn(X, Q, 1, "l2", row_labels=lx, query_labels=lq)
+    gone = np.unique(np.concatenate([nn[:, 0], np.arange(0, 50_000, 97)]))
+    idx.remove(torch.from_numpy(gone))
+    removed = np.zeros(len(X), np.uint8)
+    removed[gone] = 1
+    D, I = search(idx, Q, 10, lq)
+    check(X, Q, 10, "l2", D, I, removed=removed, row_labels=lx, query_labels=lq)
+
+
+def test_float_tail_wide(gpu):
+    X = data.powerlaw_unit(20_000, 256, seed=75)
+    Q = data.powerlaw_unit(200, 256, seed=76)
+    lx, lq = data.labels(len(X), 4, 77), data.labels(len(Q), 4, 78)
+    idx = certex.Index(256, metric="cosine")
+    idx.add(torch.from_numpy(X[:15_000]).cuda(), labels=torch.from_numpy(lx[:15_000]))
+    idx.partition_labels = False
+    idx.add(torch.from_numpy(X[15_000:]).cuda(), labels=torch.from_numpy(lx[15_000:]))
+    idx.remove(torch.arange(0, 20_000, 5))
+    removed = np.zeros(len(X), np.uint8)
+    removed[::5] = 1
+    D, I = search(idx, Q, 20, lq)
+    check(X, Q, 20, "cosine", D, I, removed=removed, row_labels=lx, query_labels=lq)
+
+
+def test_rare_label_fewer_than_k(gpu):
+    """A label with fewer rows than k: its queries get its rows, then -1 / +inf."""
+    X = data.mixture_u8(10_000, seed=79)
+    Q = data.mixture_u8(40, seed=80)
+    lx = np.zeros(len(X), np.int32)
+    lx[[5, 500, 9_999]] = 3
+    lq = np.array([3, 0] * 20, np.int32)
+    idx = certex.Index(128)
+    idx.add(torch.from_numpy(X).cuda(), labels=torch.from_numpy(lx))
+    D, I = search(idx, Q, 8, lq)
+    assert (I[0::2, 3:] == -1).all()
+    check(X, Q, 8, "l2", D, I, row_labels=lx, query_labels=lq)
