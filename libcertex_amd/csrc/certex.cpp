@@ -245,6 +245,7 @@ struct route_plan {
 };
 
 constexpr int kScreenChunk = 128;  // steps per screen workgroup chunk
+constexpr int kRoutedChunk = 32;   // steps per chunk of a routed screen (labels hold fewer rows)
 
 auto anchor_chunk_steps(bool wide, int64_t g) -> int
 {
@@ -275,7 +276,6 @@ void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan 
   certex_amd::screen_args r = aa;
   r.codes                   = st.part_codes.as<int8_t>();
   r.rowc                    = st.part_rowc.p;
-  r.row_ids                 = st.part_ids.as<int32_t>();
   r.groups                  = route->anchor_groups;
   r.n_route                 = route->n_route;
   r.n_tiles                 = route->anchor_tiles;
@@ -303,10 +303,10 @@ auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
     certex_amd::screen_args r = sa;
     r.codes                   = st.part_codes.as<int8_t>();
     r.rowc                    = st.part_rowc.p;
-    r.row_ids                 = st.part_ids.as<int32_t>();
     r.groups                  = route->screen_groups;
     r.n_route                 = route->n_route;
     r.n_tiles                 = route->screen_tiles;
+    r.chunk_steps             = kRoutedChunk;
     r.filter.kind             = 0;
     if (r.n_tiles > 0) { launch(r, stream); }
     const int64_t tail = st.size - st.n_part;
@@ -467,6 +467,10 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
   va.filter     = fa;
   va.nq         = B;
   va.k          = k;
+  if (route != nullptr) {
+    va.part_ids = st.part_ids.as<int32_t>();
+    va.n_part   = st.n_part;
+  }
   va.best_score = best_score;
   va.best_row   = best_row;
   timed(3, stream, [&] { certex_amd::verify_topk_i8(va, stream); });
@@ -535,6 +539,10 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
     ta.alpha2    = st.alpha * st.alpha;
     ta.gamma     = st.gamma;
     ta.theta     = theta;
+    if (route != nullptr) {
+      ta.part_ids = st.part_ids.as<int32_t>();
+      ta.n_part   = st.n_part;
+    }
     timed(1, stream, [&] { certex_amd::threshold_f16(ta, stream); });
   }
 
@@ -583,6 +591,10 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
     certex_amd::fill_u32(small + 8, 2, 0, stream);
   }
   va.scored = scored;
+  if (route != nullptr) {
+    va.part_ids = st.part_ids.as<int32_t>();
+    va.n_part   = st.n_part;
+  }
   timed(3, stream, [&] { certex_amd::verify_topk_f(va, stream); });
   if (scored != nullptr) {
     CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, scored, 8, hipMemcpyDeviceToHost, stream));
@@ -664,7 +676,7 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   }
   for (auto& e : gs) {
     e.tile0 = route.screen_tiles;
-    route.screen_tiles += certex_amd::screen_group_tiles(e.nq, e.nx, qb, kScreenChunk);
+    route.screen_tiles += certex_amd::screen_group_tiles(e.nq, e.nx, qb, kRoutedChunk);
   }
   route.n_route = int(gs.size());
 

@@ -101,11 +101,12 @@ struct screen_args {
   int64_t row_base = 0;  // first stored row of the pass
   int row_stride;        // 1 for the screen, the anchor stride for the anchor pass
   // routed pass (label partition): the workgroups follow the group table (n_scan and row_base
-  // come from each group); the survivors' stored rows map to ids through row_ids
+  // come from each group). Survivors and anchors are recorded as stored rows: a routed pass over
+  // the partition records partition rows (below n_part), the tail pass records ids (n_part and
+  // above); the exact-score kernels map partition rows to ids (part_ids)
   const screen_group* groups = nullptr;
   int n_route                = 0;
   int64_t n_tiles            = 0;  // workgroups of a routed launch
-  const int32_t* row_ids     = nullptr;
   int row_bytes;         // 64 KS
   const int8_t* qcodes;  // [nq_pad, row_bytes]
   const void* theta;     // [nq_pad] int32 or float (screen only)
@@ -189,6 +190,9 @@ struct verify_args {
   filter_args filter;  // applied to all_rows candidates
   int64_t nq;
   int k;
+  // routed searches: candidate rows below n_part are partition rows, id = part_ids[row]
+  const int32_t* part_ids = nullptr;
+  int64_t n_part          = 0;
   double* best_score;  // [nq, k], smaller is better; +inf where missing
   int64_t* best_row;   // [nq, k], -1 where missing
 };
@@ -270,6 +274,8 @@ struct threshold_f_args {
   const double* maxima;  // [2]
   double alpha2;         // alpha^2
   double gamma;
+  const int32_t* part_ids = nullptr;  // routed: anchor rows below n_part are partition rows
+  int64_t n_part          = 0;
   float* theta;          // [nq_pad]
 };
 /**
@@ -302,6 +308,8 @@ struct verify_f_args {
   double alpha2;
   double gamma;
   unsigned long long* scored;  // optional: += the rows scored exactly (the stats' verified count)
+  const int32_t* part_ids = nullptr;  // routed: candidate rows below n_part are partition rows
+  int64_t n_part          = 0;
   double* best_score;
   int64_t* best_row;
 };

@@ -66,7 +66,6 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   __shared__ uint32_t hit_row[ANCHORS ? 1 : kHitCap];
   __shared__ float hit_val[ANCHORS || !R::kValues ? 1 : kHitCap];
   __shared__ uint32_t n_hits;
-  const hit_list hits{hit_q, hit_row, hit_val, &n_hits};
 
   const val_t* rowc  = static_cast<const val_t*>(a.rowc);
   const val_t* theta = static_cast<const val_t*>(a.theta);
@@ -110,24 +109,43 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 
   frag_t av[4][KS];
   acc_t cc[4];
+  // the screen reads consecutive rows (stride 1), the anchor pass every row_stride-th
+  const int64_t stride = ANCHORS ? a.row_stride : 1;
+  // a step whose 64 rows all exist: straight-line loads, so that the steady-state loop has one
+  // path for the compiler's wait counts
   auto load_rows = [&](int64_t s) {
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
-      int64_t r = s * kStepRows + bt * 16 + (lane & 15);
-      r         = r < w.n_scan ? r : 0;  // rows past the end read row 0; their term kills them
-      const int8_t* src = a.codes + (w.base + r * a.row_stride) * ROWB + (lane >> 4) * 16;
+      const int64_t r   = s * kStepRows + bt * 16 + (lane & 15);
+      const int8_t* src = a.codes + (w.base + r * stride) * ROWB + (lane >> 4) * 16;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         av[bt][ks] = *reinterpret_cast<const frag_t*>(src + 64 * ks);
       }
       const int64_t r4 = s * kStepRows + bt * 16 + (lane >> 4) * 4;
-      if (a.row_stride == 1 && r4 + 3 < w.n_scan) {
-        cc[bt] = *reinterpret_cast<const acc_t*>(rowc + w.base + r4);
-      } else {
+      if constexpr (ANCHORS) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          cc[bt][j] = r4 + j < w.n_scan ? rowc[w.base + (r4 + j) * a.row_stride] : R::dead();
-        }
+        for (int j = 0; j < 4; ++j) { cc[bt][j] = rowc[w.base + (r4 + j) * stride]; }
+      } else {
+        cc[bt] = *reinterpret_cast<const acc_t*>(rowc + w.base + r4);
+      }
+    }
+  };
+  // the last step of a scan whose length is not a multiple of 64
+  auto load_rows_tail = [&](int64_t s) {
+#pragma unroll
+    for (int bt = 0; bt < 4; ++bt) {
+      int64_t r = s * kStepRows + bt * 16 + (lane & 15);
+      r         = r < w.n_scan ? r : 0;  // rows past the end read row 0; their term kills them
+      const int8_t* src = a.codes + (w.base + r * stride) * ROWB + (lane >> 4) * 16;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        av[bt][ks] = *reinterpret_cast<const frag_t*>(src + 64 * ks);
+      }
+      const int64_t r4 = s * kStepRows + bt * 16 + (lane >> 4) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        cc[bt][j] = r4 + j < w.n_scan ? rowc[w.base + (r4 + j) * stride] : R::dead();
       }
     }
   };
@@ -198,7 +216,8 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
                                  acc[1][qt][0], acc[1][qt][1], acc[1][qt][2], acc[1][qt][3],
                                  acc[2][qt][0], acc[2][qt][1], acc[2][qt][2], acc[2][qt][3],
                                  acc[3][qt][0], acc[3][qt][1], acc[3][qt][2], acc[3][qt][3]};
-          push_hits<FILT, R::kValues>(bits, qloc, w.base + row0, q0, a, hits, v16);
+          push_hits<FILT, R::kValues>(bits, qloc, w.base + row0, q0, a, hit_q, hit_row, hit_val,
+                                      &n_hits, v16);
         }
       }
     }
@@ -207,8 +226,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   frag_t b0[4][KS], b1[4][KS];
   val_t t0[4], t1[4];
   read_queries(0, b0, t0);
-  for (int64_t s = w0; s < w1; ++s) {
-    load_rows(s);
+  auto step = [&](int64_t s) {
     row0 = s * kStepRows + (lane >> 4) * 4;
 #pragma unroll 1
     for (int g = 0; g < ng; g += 2) {
@@ -231,11 +249,21 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
         }
       }
     }
+  };
+  const int64_t full = w.n_scan / kStepRows;  // steps whose rows all exist
+  const int64_t w1f  = w1 < full ? w1 : full;
+  for (int64_t s = w0; s < w1f; ++s) {
+    load_rows(s);
+    step(s);
+  }
+  if (w0 <= full && full < w1) {  // the scan's last, partial step, when it is this wave's
+    load_rows_tail(full);
+    step(full);
   }
 
   if constexpr (!ANCHORS) {
     __syncthreads();
-    flush_hits<R::kValues>(q0, a, hits);
+    flush_hits<R::kValues>(q0, a, hit_q, hit_row, hit_val, &n_hits);
   }
 }
 

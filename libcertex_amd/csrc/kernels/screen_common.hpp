@@ -107,12 +107,6 @@ __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
   return w;
 }
 
-/** Id of stored row r (the partition's rows map through row_ids). */
-__device__ inline uint32_t row_id(const screen_args& a, int64_t r)
-{
-  return a.row_ids != nullptr ? uint32_t(a.row_ids[r]) : uint32_t(r);
-}
-
 /** Filter test of a pair (query q of the batch, stored row). */
 __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
 {
@@ -127,13 +121,11 @@ __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
   }
 }
 
-/** LDS survivor list of a workgroup (val: the screen values, when the rows carry them). */
-struct hit_list {
-  uint32_t* q;
-  uint32_t* row;
-  float* val;
-  uint32_t* n;
-};
+/**
+ * LDS survivor list of a workgroup: hit_q / hit_row / hit_val (the screen values, when the rows
+ * carry them) of kHitCap entries and the count n_hits, passed as separate pointers (a struct of
+ * LDS addresses can end up as a constant initializer, which the backend rejects).
+ */
 
 /**
  * Appends the survivors of one 16-query tile of a step to the workgroup's list: `bits` is this
@@ -143,14 +135,16 @@ struct hit_list {
  */
 template <bool FILT, bool VALS, typename V>
 __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t row0, int64_t q0,
-                                          const screen_args& a, hit_list h, const V (&v)[16])
+                                          const screen_args& a, uint32_t* hit_q,
+                                          uint32_t* hit_row, float* hit_val, uint32_t* n_hits,
+                                          const V (&v)[16])
 {
   if constexpr (FILT) {
     uint32_t scan = bits;
     while (scan) {
       const int j = __builtin_ctz(scan);
       scan &= scan - 1;
-      if (!keeps(a.filter, q0 + qloc, row_id(a, row0 + (j >> 2) * 16 + (j & 3)))) {
+      if (!keeps(a.filter, q0 + qloc, uint32_t(row0 + (j >> 2) * 16 + (j & 3)))) {
         bits &= ~(1u << j);
       }
     }
@@ -163,12 +157,12 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
       __builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0u));
     const int leader = __builtin_ctzll(mask);
     uint32_t base    = 0;
-    if (lane == leader) { base = atomicAdd(h.n, uint32_t(__builtin_popcountll(mask))); }
+    if (lane == leader) { base = atomicAdd(n_hits, uint32_t(__builtin_popcountll(mask))); }
     base = __builtin_amdgcn_readlane(base, leader);
     if (bits) {
       const int j = __builtin_ctz(bits);
       bits &= bits - 1;
-      const uint32_t row = row_id(a, row0 + (j >> 2) * 16 + (j & 3));
+      const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
       const uint32_t pos = base + rank;
       float val          = 0.0f;
       if constexpr (VALS) {
@@ -176,9 +170,9 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
         for (int t = 0; t < 16; ++t) { val = t == j ? float(v[t]) : val; }
       }
       if (pos < uint32_t(kHitCap)) {
-        h.q[pos]   = qloc;
-        h.row[pos] = row;
-        if constexpr (VALS) { h.val[pos] = val; }
+        hit_q[pos]   = qloc;
+        hit_row[pos] = row;
+        if constexpr (VALS) { hit_val[pos] = val; }
       } else {
         const int64_t q      = q0 + qloc;
         const uint32_t bslot = atomicAdd(a.cand_count + q, 1u);
@@ -193,15 +187,17 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
 
 /** Flushes the workgroup's LDS survivor list to the per-query buckets (after a barrier). */
 template <bool VALS>
-__device__ inline void flush_hits(int64_t q0, const screen_args& a, hit_list h)
+__device__ inline void flush_hits(int64_t q0, const screen_args& a, const uint32_t* hit_q,
+                                  const uint32_t* hit_row, const float* hit_val,
+                                  const uint32_t* n_hits)
 {
-  const uint32_t nh = *h.n < uint32_t(kHitCap) ? *h.n : uint32_t(kHitCap);
+  const uint32_t nh = *n_hits < uint32_t(kHitCap) ? *n_hits : uint32_t(kHitCap);
   for (uint32_t e = threadIdx.x; e < nh; e += blockDim.x) {
-    const int64_t q      = q0 + h.q[e];
+    const int64_t q      = q0 + hit_q[e];
     const uint32_t bslot = atomicAdd(a.cand_count + q, 1u);
     if (bslot < a.cap) {
-      a.cand_rows[q * a.cap + bslot] = h.row[e];
-      if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = h.val[e]; }
+      a.cand_rows[q * a.cap + bslot] = hit_row[e];
+      if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = hit_val[e]; }
     }
   }
 }
@@ -231,7 +227,7 @@ __device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], i
       val_t v = col[bt][r];
       if constexpr (FILT) {
         const int64_t idx = row0 + bt * 16 + r;
-        if (idx < w.n_scan && !keeps(a.filter, q, row_id(a, w.base + idx * a.row_stride))) {
+        if (idx < w.n_scan && !keeps(a.filter, q, uint32_t(w.base + idx * a.row_stride))) {
           v = R::lowest();
         }
       }
@@ -246,7 +242,7 @@ __device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], i
     }
   }
   if constexpr (ARGX) {
-    uint32_t row = row_id(a, w.base + (row0 + j) * a.row_stride);
+    uint32_t row = uint32_t(w.base + (row0 + j) * a.row_stride);
 #pragma unroll
     for (int off = 16; off <= 32; off <<= 1) {
       const val_t om     = __shfl_xor(m, off);

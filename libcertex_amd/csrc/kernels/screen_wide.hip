@@ -54,7 +54,6 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
   __shared__ uint32_t hit_row[ANCHORS ? 1 : kHitCap];
   __shared__ float hit_val[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t n_hits;
-  const hit_list hits{hit_q, hit_row, hit_val, &n_hits};
 
   const float* rowc  = static_cast<const float*>(a.rowc);
   const float* theta = static_cast<const float*>(a.theta);
@@ -229,8 +228,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
                                  acc[1][qt][0], acc[1][qt][1], acc[1][qt][2], acc[1][qt][3],
                                  acc[2][qt][0], acc[2][qt][1], acc[2][qt][2], acc[2][qt][3],
                                  acc[3][qt][0], acc[3][qt][1], acc[3][qt][2], acc[3][qt][3]};
-          push_hits<FILT, true>(bits, uint32_t(qt * 16 + (lane & 15)), w.base + row0, q0, a, hits,
-                                v16);
+          push_hits<FILT, true>(bits, uint32_t(qt * 16 + (lane & 15)), w.base + row0, q0, a, hit_q,
+                                hit_row, hit_val, &n_hits, v16);
         }
       }
     }
@@ -238,7 +237,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
 
   if constexpr (!ANCHORS) {
     __syncthreads();
-    flush_hits<true>(q0, a, hits);
+    flush_hits<true>(q0, a, hit_q, hit_row, hit_val, &n_hits);
   }
 }
 

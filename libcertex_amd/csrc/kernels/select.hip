@@ -242,6 +242,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a)
         live = a.rowc[r] != kDeadRow && keeps(a.filter, q, r);
       } else {
         r    = cand[c0 + e];
+        r    = (a.part_ids != nullptr && r < a.n_part) ? uint32_t(a.part_ids[r]) : r;
         live = true;
       }
       if (live) {
@@ -298,41 +299,97 @@ __device__ inline double fcoord(const void* p, elem t, int64_t i)
 }
 
 /**
- * Exact fp64 score of stored row `row` against the query whose coordinates sit in LDS as doubles,
+ * Exact fp64 scores of NR stored rows against the query whose coordinates sit in LDS as doubles,
  * computed by one wave in the oracle's canonical order: lane l accumulates coordinates l, l + 64,
  * ... with fused multiply-adds, and the 64 partial sums are combined by the xor butterfly (every
  * lane returns the same bits). l2: sum (q - x)^2; inner: -sum q x; cosine: -sum q x /
- * sqrt(sum q^2 sum x^2). The row's coordinates are read by the 64 lanes together (coalesced).
+ * sqrt(sum q^2 sum x^2). The 64 lanes read a row's coordinates together (coalesced), 4 per lane
+ * and row at a time, so that 4 NR loads per lane are in flight.
  */
-__device__ inline double wave_score(const double* qv, const void* vectors, elem t, int64_t row,
-                                    int64_t dim, metric_kind metric, int lane)
+template <int NR>
+__device__ inline void wave_scores(const double* qv, const void* vectors, elem t,
+                                   const int64_t (&rows)[NR], int64_t dim, metric_kind metric,
+                                   int lane, double (&out)[NR])
 {
-  double acc = 0, qq = 0, xx = 0;
-  const int64_t base = row * dim;
-  for (int64_t j = lane; j < dim; j += 64) {
-    const double a = qv[j], b = fcoord(vectors, t, base + j);
-    if (metric == metric_kind::l2) {
-      const double d = a - b;
-      acc            = fma(d, d, acc);
-    } else {
-      acc = fma(a, b, acc);
-      if (metric == metric_kind::cosine) {
-        qq = fma(a, a, qq);
-        xx = fma(b, b, xx);
+  constexpr int U = 4;
+  double acc[NR], xx[NR], qq = 0;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) { acc[r] = xx[r] = 0; }
+  for (int64_t j0 = lane; j0 < dim; j0 += 64 * U) {
+    double b[NR][U];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t j = j0 + 64 * u;
+        b[r][u]         = j < dim ? fcoord(vectors, t, rows[r] * dim + j) : 0.0;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = j0 + 64 * u;
+      if (j >= dim) { break; }
+      const double a = qv[j];
+      if (metric == metric_kind::cosine) { qq = fma(a, a, qq); }
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        if (metric == metric_kind::l2) {
+          const double d = a - b[r][u];
+          acc[r]         = fma(d, d, acc[r]);
+        } else {
+          acc[r] = fma(a, b[r][u], acc[r]);
+          if (metric == metric_kind::cosine) { xx[r] = fma(b[r][u], b[r][u], xx[r]); }
+        }
       }
     }
   }
 #pragma unroll
   for (int off = 32; off; off >>= 1) {
-    acc += __shfl_xor(acc, off);
-    if (metric == metric_kind::cosine) {
-      qq += __shfl_xor(qq, off);
-      xx += __shfl_xor(xx, off);
+    if (metric == metric_kind::cosine) { qq += __shfl_xor(qq, off); }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      acc[r] += __shfl_xor(acc[r], off);
+      if (metric == metric_kind::cosine) { xx[r] += __shfl_xor(xx[r], off); }
     }
   }
-  if (metric == metric_kind::l2) { return acc; }
-  if (metric == metric_kind::inner) { return -acc; }
-  return -acc / sqrt(qq * xx);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    if (metric == metric_kind::l2) {
+      out[r] = acc[r];
+    } else if (metric == metric_kind::inner) {
+      out[r] = -acc[r];
+    } else {
+      out[r] = -acc[r] / sqrt(qq * xx[r]);
+    }
+  }
+}
+
+/**
+ * Scores rid[from, to) into key[] (ordered keys), two rows per wave at a time; every thread of
+ * the block calls it.
+ */
+__device__ inline void score_rows(const double* qv, const void* vectors, elem t, int64_t dim,
+                                  metric_kind metric, const uint32_t* rid, uint64_t* key, int from,
+                                  int to)
+{
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int e = from + 2 * wave; e < to; e += 2 * (kThreads / 64)) {
+    const int64_t rows[2] = {int64_t(rid[e]), int64_t(rid[e + 1 < to ? e + 1 : e])};
+    double sc[2];
+    wave_scores<2>(qv, vectors, t, rows, dim, metric, lane, sc);
+    if (lane == 0) {
+      key[e] = score_key(sc[0]);
+      if (e + 1 < to) { key[e + 1] = score_key(sc[1]); }
+    }
+  }
+}
+
+/** LDS entries of the candidate buffers: a power of two between lo and kBuf covering want. */
+inline int buffer_entries(int want, int lo)
+{
+  int p = lo;
+  while (p < want && p < kBuf) { p <<= 1; }
+  return p;
 }
 
 /** Order-preserving map of a float onto an unsigned key (ascending). */
@@ -344,11 +401,12 @@ __device__ inline uint32_t fkey(float f)
 
 constexpr int kMaxFloatDim = kMaxF16Halves;  // widest float vector
 
-__global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_args a)
+__global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_args a, int cap)
 {
-  __shared__ uint64_t key[kBuf];
-  __shared__ uint32_t rid[kBuf];
-  __shared__ double qv[kMaxFloatDim];
+  extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
+  auto* key = reinterpret_cast<uint64_t*>(dyn);                 // [cap]
+  auto* rid = reinterpret_cast<uint32_t*>(dyn + size_t(cap) * 8);  // [cap]
+  auto* qv  = reinterpret_cast<double*>(dyn + size_t(cap) * 12);  // [dim]
   __shared__ int hist[256];
   __shared__ int wave_tot[4];
   __shared__ uint32_t sel_digit;
@@ -401,21 +459,21 @@ __global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_arg
     rank = sel_rank;
     __syncthreads();
   }
-  // exact scores of the anchors of the groups at or above it (at most kBuf)
+  // exact scores of the anchors of the groups at or above it (at most cap)
   for (int64_t j = tid; j < a.dim; j += kThreads) { qv[j] = fcoord(a.queries, a.t, q * a.dim + j); }
   if (tid == 0) { cnt = 0; }
   __syncthreads();
   for (int64_t e = tid; e < a.n_groups; e += kThreads) {
     if (!(v[e] > -INFINITY) || ~fkey(v[e]) > prefix) { continue; }
     const int slot = atomicAdd(&cnt, 1);
-    if (slot < kBuf) { rid[slot] = r[e]; }
+    if (slot < cap) {
+      const uint32_t row = r[e];
+      rid[slot] = (a.part_ids != nullptr && row < a.n_part) ? uint32_t(a.part_ids[row]) : row;
+    }
   }
   __syncthreads();
-  const int m = cnt < kBuf ? cnt : kBuf;
-  for (int e = tid >> 6; e < m; e += kThreads / 64) {
-    const double sc = wave_score(qv, a.vectors, a.t, rid[e], a.dim, a.metric, tid & 63);
-    if ((tid & 63) == 0) { key[e] = score_key(sc); }
-  }
+  const int m = cnt < cap ? cnt : cap;
+  score_rows(qv, a.vectors, a.t, a.dim, a.metric, rid, key, 0, m);
   const int Pw = pow2_at_least(m);
   for (int e = m + tid; e < Pw; e += kThreads) {
     key[e] = ~0ull;
@@ -508,11 +566,12 @@ __device__ uint32_t radix_select(int64_t n, int rank, F key_of, int* hist, int* 
  * (U tightens as better rows arrive). Scores use one wave per row; the best k by (score, row)
  * stay in LDS.
  */
-__global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a)
+__global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a, int cap)
 {
-  __shared__ uint64_t key[kBuf];
-  __shared__ uint32_t rid[kBuf];
-  __shared__ double qv[kMaxFloatDim];
+  extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
+  auto* key = reinterpret_cast<uint64_t*>(dyn);                 // [cap]
+  auto* rid = reinterpret_cast<uint32_t*>(dyn + size_t(cap) * 8);  // [cap]
+  auto* qv  = reinterpret_cast<double*>(dyn + size_t(cap) * 12);  // [dim]
   __shared__ int hist[256];
   __shared__ int wave_tot[4];
   __shared__ uint32_t sel_digit;
@@ -531,13 +590,13 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
   const uint32_t* cand = a.cand_rows + q * a.cap;
   const float* vals    = (a.all_rows || a.cand_vals == nullptr) ? nullptr : a.cand_vals + q * a.cap;
 
+  auto to_id = [&](uint32_t r) {
+    return (a.part_ids != nullptr && r < a.n_part) ? uint32_t(a.part_ids[r]) : r;
+  };
   int64_t n_scored = 0;
-  auto score_rows  = [&](int from, int to) {
+  auto score       = [&](int from, int to) {
     n_scored += to - from;
-    for (int e = from + wave; e < to; e += kThreads / 64) {
-      const double sc = wave_score(qv, a.vectors, a.t, rid[e], a.dim, a.metric, lane);
-      if (lane == 0) { key[e] = score_key(sc); }
-    }
+    score_rows(qv, a.vectors, a.t, a.dim, a.metric, rid, key, from, to);
   };
   int have = 0;  // entries [0, have) of key / rid are scored
   auto keep_best = [&]() {
@@ -563,15 +622,15 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
     for (int64_t e = tid; e < n_cand; e += kThreads) {
       if (~fkey(vals[e]) <= tk) {
         const int slot = atomicAdd(&fill, 1);
-        if (slot < kBuf) { rid[slot] = cand[e]; }
+        if (slot < cap) { rid[slot] = to_id(cand[e]); }
       }
     }
     __syncthreads();
     const int c = fill;
     __syncthreads();
-    if (c <= kBuf) {
+    if (c <= cap) {
       have = c;
-      score_rows(0, c);
+      score(0, c);
       __syncthreads();
       keep_best();
       U                = key_score(key[k - 1]);  // k distinct live rows: bounds the k-th score
@@ -586,7 +645,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
 
   // phase B: the rest (everything when not ordered), in buffer-sized chunks
   for (int64_t c0 = 0; c0 < n_cand;) {
-    const int room  = kBuf - have;
+    const int room  = cap - have;
     const int64_t m = n_cand - c0 < room ? n_cand - c0 : room;
     if (tid == 0) { fill = 0; }
     __syncthreads();
@@ -598,7 +657,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
         r    = uint32_t(idx);
         take = a.rowc[r] != -INFINITY && keeps(a.filter, q, r);
       } else {
-        r    = cand[idx];
+        r    = to_id(cand[idx]);
         take = !ordered || (~fkey(vals[idx]) > tk &&
                             screen_lower_bound(vals[idx], aq, C, a.alpha2, a.metric) <= U);
       }
@@ -606,7 +665,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
     }
     __syncthreads();
     const int added = fill;
-    score_rows(have, have + added);
+    score(have, have + added);
     have += added;
     c0 += m;
     __syncthreads();
@@ -677,16 +736,32 @@ void verify_topk_i8(const verify_args& a, hipStream_t stream)
   verify_topk_i8_kernel<<<unsigned(a.nq), kThreads, 0, stream>>>(a);
 }
 
+/** Launches a kernel with `bytes` of dynamic LDS (raising the kernel's limit when needed). */
+template <typename K, typename... Args>
+void launch_dyn(K kernel, unsigned blocks, size_t bytes, hipStream_t stream, Args... args)
+{
+  if (bytes > 65536 && hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           int(bytes)) != hipSuccess) {
+    (void)hipGetLastError();
+  }
+  kernel<<<blocks, kThreads, bytes, stream>>>(args...);
+}
+
 void threshold_f16(const threshold_f_args& a, hipStream_t stream)
 {
   if (a.nq_pad == 0) { return; }
-  threshold_f16_kernel<<<unsigned(a.nq_pad), kThreads, 0, stream>>>(a);
+  const int cap = buffer_entries(a.per_query, 256);
+  launch_dyn(threshold_f16_kernel, unsigned(a.nq_pad), size_t(cap) * 12 + size_t(a.dim) * 8,
+             stream, a, cap);
 }
 
 void verify_topk_f(const verify_f_args& a, hipStream_t stream)
 {
   if (a.nq == 0) { return; }
-  verify_topk_f_kernel<<<unsigned(a.nq), kThreads, 0, stream>>>(a);
+  const int cap = buffer_entries(4 * a.k, 1024);
+  launch_dyn(verify_topk_f_kernel, unsigned(a.nq), size_t(cap) * 12 + size_t(a.dim) * 8, stream,
+             a, cap);
 }
 
 void finish(const double* best_score, const int64_t* best_row, int64_t nq, int k,
