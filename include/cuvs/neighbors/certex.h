@@ -145,6 +145,12 @@ CUVS_EXPORT cuvsError_t cuvsCertexIndexGetMetric(cuvsCertexIndex_t index,
 CUVS_EXPORT cuvsError_t cuvsCertexIndexGetAnchorStride(cuvsCertexIndex_t index, int32_t* stride);
 /** Whether labels were set (core.cpp has_labels). */
 CUVS_EXPORT cuvsError_t cuvsCertexIndexHasLabels(cuvsCertexIndex_t index, bool* has_labels);
+/**
+ * Vectors covered by the label partition (0 when none); the ones added later go through the
+ * label filter (reference index::n_partitioned, certex.hpp:421-425).
+ */
+CUVS_EXPORT cuvsError_t cuvsCertexIndexGetPartitioned(cuvsCertexIndex_t index,
+                                                      int64_t* n_partitioned);
 /** Grow the capacity to at least `capacity` rows (core.cpp reserve). */
 CUVS_EXPORT cuvsError_t cuvsCertexReserve(cuvsResources_t res,
                                           int64_t capacity,

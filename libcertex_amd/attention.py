@@ -9,17 +9,16 @@ import torch
 
 from .index import Index, _require
 
-_TILE = 128
-
-
 def _width(head_dim):
     """The widest screening row that fits the head dimension (certex/attention.py:25-27)."""
     return max(59, (head_dim + 5) // 64 * 64 - 5) if head_dim >= 59 else head_dim
 
 
 def _stride(n, k):
-    """An anchor stride between 1 and 16 that leaves about 16k anchor groups (attention.py:30-34)."""
-    s = n // (16 * k * _TILE)
+    """An anchor stride between 1 and 16 (the reference picks one from n and k,
+    certex/attention.py:30-34): here it leaves about 4k groups of 4 anchors, so that the k-th best
+    group stays close to the k-th best key while the anchor pass reads a fraction of the keys."""
+    s = n // (16 * k)
     return int(max(1, min(16, s)))
 
 
@@ -36,13 +35,21 @@ def _keys(x):
 
 
 class KeyCache:
-    """Exact top-k over the keys of a growing KV cache: one index per KV head (attention.py:44-106)."""
+    """Exact top-k over the keys of a growing KV cache (attention.py:44-106).
+
+    The reference keeps one index per KV head. Here all heads share one inner-product index whose
+    keys carry their head as a label, so that one label-routed search serves every query head of
+    a step (each query head screens only its KV head's keys, in one launch per phase). Keys
+    appended after the label partition are screened through the label filter; the partition is
+    rebuilt when they exceed a sixteenth of the cache.
+    """
 
     def __init__(self, n_kv_heads, head_dim, k=2048, capacity=None):
         _require(n_kv_heads >= 1 and head_dim >= 1, "n_kv_heads and head_dim must be positive")
         _require(1 <= k <= 2048, f"k must be between 1 and 2048, not {k}")
         self.n_kv_heads, self.head_dim, self.k, self.capacity = int(n_kv_heads), int(head_dim), int(k), capacity
-        self.heads, self.dtype = None, None
+        self.index, self.dtype = None, None
+        self.local = None  # key id within its head, per id of the shared index
         self.size = 0
 
     def append(self, keys):
@@ -52,29 +59,38 @@ class KeyCache:
             K.ndim == 3 and K.shape[0] == self.n_kv_heads and K.shape[2] == self.head_dim,
             f"keys must have shape ({self.n_kv_heads}, n, {self.head_dim}), not {tuple(K.shape)}",
         )
-        if self.heads is None:
+        n = K.shape[1]
+        if n == 0:
+            return self
+        if self.index is None:
             self.dtype = K.dtype
-            n = max(K.shape[1], int(self.capacity or 0))
-            self.heads = [
-                Index(
-                    self.head_dim,
-                    metric="ip",
-                    width=_width(self.head_dim),
-                    storage="device",
-                    capacity=self.capacity,
-                    anchor_stride=_stride(n, self.k),
-                )
-                for _ in range(self.n_kv_heads)
-            ]
-        for g, idx in enumerate(self.heads):
-            idx.add(K[g].to(self.dtype).contiguous())
-        self.size += K.shape[1]
+            cap = max(n, int(self.capacity or 0))
+            self.index = Index(
+                self.head_dim,
+                metric="ip",
+                width=_width(self.head_dim),
+                storage="device",
+                capacity=cap * self.n_kv_heads,
+                anchor_stride=_stride(cap, self.k),
+                partition_labels=False,
+            )
+        heads = torch.arange(self.n_kv_heads, device="cuda", dtype=torch.int32)
+        self.index.add(
+            K.to(self.dtype).reshape(self.n_kv_heads * n, self.head_dim).contiguous(),
+            labels=heads.repeat_interleave(n),
+        )
+        local = torch.arange(self.size, self.size + n, device="cuda", dtype=torch.int64).repeat(self.n_kv_heads)
+        self.local = local if self.local is None else torch.cat([self.local, local])
+        self.size += n
+        core = self.index.core
+        if (core.size - core.n_partitioned) * 16 > core.size:
+            self.index.partition()
         return self
 
-    def topk(self, q, k=None, batch=2048):
+    def topk(self, q, k=None, batch=None):
         """The exact top k keys of every query: q (n_heads, m, head_dim) or (n_heads, head_dim);
         returns (scores, ids) of shape (n_heads, m, k) or (n_heads, k)."""
-        _require(self.heads is not None, "the cache is empty: append keys first")
+        _require(self.index is not None, "the cache is empty: append keys first")
         k = self.k if k is None else int(k)
         _require(1 <= k <= min(2048, self.size), f"k must be between 1 and {min(2048, self.size)}, not {k}")
         Q = _keys(q)
@@ -87,12 +103,12 @@ class KeyCache:
         )
         H, m, d = Q.shape
         r = H // self.n_kv_heads
-        scores = torch.empty((H, m, k), dtype=torch.float32, device="cuda")
-        ids = torch.empty((H, m, k), dtype=torch.int64, device="cuda")
-        for g, idx in enumerate(self.heads):
-            D, I = idx.search(Q[g * r : (g + 1) * r].reshape(r * m, d).to(self.dtype), k=k, batch=batch)
-            scores[g * r : (g + 1) * r] = D.reshape(r, m, k)
-            ids[g * r : (g + 1) * r] = I.reshape(r, m, k)
+        labels = (torch.arange(H, device="cuda", dtype=torch.int32) // r).repeat_interleave(m)
+        D, I = self.index.search(
+            Q.to(self.dtype).reshape(H * m, d), k=k, batch=batch or max(2048, H * m), labels=labels
+        )
+        scores = D.reshape(H, m, k)
+        ids = self.local[I].reshape(H, m, k)
         return (scores[:, 0], ids[:, 0]) if single else (scores, ids)
 
 

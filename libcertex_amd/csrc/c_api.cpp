@@ -509,6 +509,15 @@ cuvsError_t cuvsCertexIndexHasLabels(cuvsCertexIndex_t index, bool* has_labels)
   });
 }
 
+cuvsError_t cuvsCertexIndexGetPartitioned(cuvsCertexIndex_t index, int64_t* n_partitioned)
+{
+  return translate([=] {
+    dispatch(index->dtype, [&](auto tag) {
+      *n_partitioned = as_index<decltype(tag)>(*index)->n_partitioned();
+    });
+  });
+}
+
 cuvsError_t cuvsCertexReserve(cuvsResources_t res, int64_t capacity, cuvsCertexIndex_t index)
 {
   return translate([=] {

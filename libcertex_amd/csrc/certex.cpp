@@ -206,25 +206,49 @@ void append_float(cuvs::resources const& res, index_state& st, const void* x, in
 }
 
 /**
- * Anchor grouping: the anchor pass records one best value per group of group_steps * 64 anchors;
- * groups stay numerous enough for a good k-th value while the [nq_pad, n_groups] table stays
+ * Anchor grouping: the anchor pass records one best value per group of group_steps * 64 anchors
+ * (coarse), or per group of 4 anchors (fine) when k is large next to the anchor steps, so that
+ * the k-th best group stays close to the k-th best anchor; the [nq_pad, n_groups] table stays
  * under 1 GB.
  */
 struct anchor_plan {
   int stride;
   int64_t n_anchor, n_groups;
   int64_t group_steps;
+  bool fine = false;
 };
+constexpr int64_t kTableBytes = int64_t(1) << 30;
+
+/** Coarse groups when there are at least 64 k anchor steps; fine groups otherwise. */
+void size_groups(anchor_plan& p, int64_t max_anchors, int64_t tail_anchors, int64_t nq_pad, int k,
+                 int64_t* part_groups)
+{
+  const int64_t steps      = certex_amd::screen_steps(max_anchors);
+  const int64_t tail_steps = certex_amd::screen_steps(tail_anchors);
+  const int64_t q          = certex_amd::kFineGroup;
+  const int64_t fine_cols  = (max_anchors + q - 1) / q + (tail_anchors + q - 1) / q;
+  if (steps < 64 * int64_t(k) && nq_pad * fine_cols * 4 <= kTableBytes) {
+    p.fine        = true;
+    p.group_steps = 1;
+    p.n_groups    = fine_cols;
+    *part_groups  = (max_anchors + q - 1) / q;
+    return;
+  }
+  int64_t g = std::max<int64_t>(1, steps / (64 * int64_t(k)));
+  while (nq_pad * ((steps + g - 1) / g + (tail_steps + g - 1) / g) * 4 > kTableBytes) { g *= 2; }
+  p.fine        = false;
+  p.group_steps = g;
+  *part_groups  = (steps + g - 1) / g;
+  p.n_groups    = *part_groups + (tail_steps + g - 1) / g;
+}
+
 auto plan_anchors(index_state const& st, int64_t size, int64_t nq_pad, int k) -> anchor_plan
 {
   anchor_plan p{};
-  p.stride       = std::max(1, st.anchor_stride);
-  p.n_anchor     = (size + p.stride - 1) / p.stride;
-  const int64_t steps = certex_amd::screen_steps(p.n_anchor);
-  int64_t g      = std::max<int64_t>(1, steps / (64 * int64_t(k)));
-  while (nq_pad * ((steps + g - 1) / g) * 4 > (int64_t(1) << 30)) { g *= 2; }
-  p.group_steps = g;
-  p.n_groups    = (steps + g - 1) / g;
+  p.stride   = std::max(1, st.anchor_stride);
+  p.n_anchor = (size + p.stride - 1) / p.stride;
+  int64_t part = 0;
+  size_groups(p, p.n_anchor, 0, nq_pad, k, &part);
   return p;
 }
 
@@ -240,16 +264,47 @@ struct route_plan {
   int n_route          = 0;
   int64_t anchor_tiles = 0, screen_tiles = 0;
   int anchor_chunk     = 0;
+  int screen_chunk     = 0;
   int64_t part_groups  = 0;  // anchor group columns of the partition (the tail's follow)
   anchor_plan ap{};
 };
 
-constexpr int kScreenChunk = 128;  // steps per screen workgroup chunk
-constexpr int kRoutedChunk = 32;   // steps per chunk of a routed screen (labels hold fewer rows)
+constexpr int kScreenChunk = 128;      // most steps per screen workgroup
+constexpr int kRoutedChunk = 32;       // most steps per workgroup of a routed screen
+constexpr int64_t kMinTiles = 2048;    // workgroups a launch should have (8 per CU)
 
 auto anchor_chunk_steps(bool wide, int64_t g) -> int
 {
   return int(wide ? 8 * g * std::max<int64_t>(1, 4 / g) : 4 * g * std::max<int64_t>(1, 16 / g));
+}
+
+/**
+ * Steps per workgroup: the largest of cap, cap / 2, ... (multiples of unit) that still gives the
+ * launch kMinTiles workgroups; small batches and short scans split into smaller chunks so that
+ * every CU gets work.
+ */
+template <typename F>
+auto pick_chunk(int64_t unit, int64_t cap, F&& tiles) -> int
+{
+  int64_t c = std::max(unit, cap / unit * unit);
+  while (c > unit && tiles(c) < kMinTiles) { c = std::max(unit, c / 2 / unit * unit); }
+  return int(c);
+}
+
+/** Chunk of a plain (unrouted) pass over n_scan scan indices. */
+auto plain_chunk(index_state const& st, int64_t nq, int64_t nq_pad, int64_t n_scan, int64_t unit,
+                 int64_t cap) -> int
+{
+  const bool f16      = !is_int(st.type);
+  const int64_t qb    = certex_amd::screen_query_block(f16, st.row_bytes, nq_pad);
+  const int64_t n_qb  = (nq + qb - 1) / qb;
+  const int64_t steps = certex_amd::screen_steps(n_scan);
+  return pick_chunk(unit, cap, [&](int64_t c) { return n_qb * ((steps + c - 1) / c); });
+}
+
+auto waves_of(index_state const& st) -> int64_t
+{
+  return certex_amd::screen_waves(!is_int(st.type), st.row_bytes);
 }
 
 /** Anchor pass: every anchor of the index, or the partition's (routed) and the tail's. */
@@ -260,8 +315,12 @@ void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan 
   aa.row_stride  = ap.stride;
   aa.n_groups    = ap.n_groups;
   aa.group_steps = int(ap.group_steps);
+  aa.fine        = ap.fine;
+  const int64_t unit = waves_of(st) * ap.group_steps;
+  const int64_t cap  = anchor_chunk_steps(waves_of(st) == 8, ap.group_steps);
   if (route == nullptr) {
-    aa.n_scan = ap.n_anchor;
+    aa.n_scan      = ap.n_anchor;
+    aa.chunk_steps = plain_chunk(st, aa.nq, aa.nq_pad, aa.n_scan, unit, cap);
     launch(aa, stream);
     return;
   }
@@ -279,6 +338,7 @@ void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan 
   r.groups                  = route->anchor_groups;
   r.n_route                 = route->n_route;
   r.n_tiles                 = route->anchor_tiles;
+  r.chunk_steps             = route->anchor_chunk;
   r.filter.kind             = 0;  // every row of a group carries the group's label
   if (r.n_tiles > 0) { launch(r, stream); }
   const int64_t tail = st.size - st.n_part;
@@ -287,6 +347,7 @@ void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan 
     t.row_base                = st.n_part;
     t.n_scan                  = (tail + ap.stride - 1) / ap.stride;
     t.grp_base                = route->part_groups;
+    t.chunk_steps             = plain_chunk(st, t.nq, t.nq_pad, t.n_scan, unit, cap);
     launch(t, stream);
   }
 }
@@ -297,6 +358,7 @@ auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
 {
   return [&st, route, launch](certex_amd::screen_args& sa, hipStream_t stream) {
     if (route == nullptr) {
+      sa.chunk_steps = plain_chunk(st, sa.nq, sa.nq_pad, sa.n_scan, waves_of(st), kScreenChunk);
       launch(sa, stream);
       return;
     }
@@ -306,7 +368,7 @@ auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
     r.groups                  = route->screen_groups;
     r.n_route                 = route->n_route;
     r.n_tiles                 = route->screen_tiles;
-    r.chunk_steps             = kRoutedChunk;
+    r.chunk_steps             = route->screen_chunk;
     r.filter.kind             = 0;
     if (r.n_tiles > 0) { launch(r, stream); }
     const int64_t tail = st.size - st.n_part;
@@ -314,6 +376,7 @@ auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
       certex_amd::screen_args t = sa;
       t.row_base                = st.n_part;
       t.n_scan                  = tail;
+      t.chunk_steps = plain_chunk(st, t.nq, t.nq_pad, t.n_scan, waves_of(st), kScreenChunk);
       launch(t, stream);
     }
   };
@@ -347,7 +410,6 @@ bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, 
     certex_amd::fill_u32(count, nq_pad, 0, stream);
     sa.n_scan      = size;
     sa.row_stride  = 1;
-    sa.chunk_steps = kScreenChunk;
     sa.cand_count  = count;
     sa.cand_rows   = rows;
     sa.cap         = cap;
@@ -430,7 +492,6 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
     auto* gmax = static_cast<int32_t*>(
       rs.get(cuvs::detail::ws_gmax, size_t(nq_pad) * size_t(ap.n_groups) * 4));
     certex_amd::screen_args aa = sa;
-    aa.chunk_steps             = anchor_chunk_steps(false, ap.group_steps);
     aa.gmax                    = gmax;
     timed(0, stream, [&] { anchor_pass(st, aa, ap, route, certex_amd::anchors_i8, stream); });
     timed(1, stream,
@@ -514,7 +575,6 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
     auto* grow = static_cast<uint32_t*>(
       rs.get(cuvs::detail::ws_grow, size_t(nq_pad) * size_t(ap.n_groups) * 4));
     certex_amd::screen_args aa = sa;
-    aa.chunk_steps             = anchor_chunk_steps(wide, ap.group_steps);
     aa.gmax                    = gmax;
     aa.grow                    = grow;
     timed(0, stream, [&] {
@@ -528,7 +588,7 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
     ta.nq        = B;
     ta.nq_pad    = nq_pad;
     ta.k         = k;
-    ta.per_query = std::max(std::max(anchors, 2 * k), k);
+    ta.per_query = std::max(anchors, k + std::max(k / 4, 16));
     ta.vectors   = st.vectors.p;
     ta.queries   = queries;
     ta.t         = t;
@@ -646,29 +706,32 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
     }
     i = j;
   }
-  // a label's anchors must form at least k groups of 64 for a threshold: below the index's
-  // stride, a denser one (a query whose label still has fewer groups keeps all of its rows)
+  // the largest label's anchors should form at least 4 k fine groups: below the index's stride,
+  // a denser one (a query whose label still has fewer than k groups keeps all of its rows)
   const int stride = int(std::max<int64_t>(
-    1, std::min<int64_t>(std::max(1, st.anchor_stride), max_nx / (64 * int64_t(k)))));
-  int64_t max_steps = 0;
-  for (auto const& e : ga) {
-    max_steps = std::max(max_steps, certex_amd::screen_steps((e.nx + stride - 1) / stride));
-  }
+    1, std::min<int64_t>(std::max(1, st.anchor_stride),
+                         max_nx / (4 * certex_amd::kFineGroup * int64_t(k)))));
   // anchor groups: per label as plan_anchors sizes them for the largest label; the tail's
   // columns follow the partition's
   route_plan route;
-  const int64_t tail_steps = certex_amd::screen_steps((st.size - st.n_part + stride - 1) / stride);
-  int64_t g = std::max<int64_t>(1, max_steps / (64 * int64_t(k)));
-  while (true) {
-    route.part_groups = (max_steps + g - 1) / g;
-    route.ap.n_groups = route.part_groups + (tail_steps + g - 1) / g;
-    if (nq_pad * route.ap.n_groups * 4 <= (int64_t(1) << 30)) { break; }
-    g *= 2;
-  }
-  route.ap.stride      = stride;
-  route.ap.n_anchor    = 0;
-  route.ap.group_steps = g;
-  route.anchor_chunk   = anchor_chunk_steps(wide, g);
+  route.ap.stride   = stride;
+  route.ap.n_anchor = 0;
+  size_groups(route.ap, (max_nx + stride - 1) / stride,
+              (st.size - st.n_part + stride - 1) / stride, nq_pad, k, &route.part_groups);
+  const int64_t waves = waves_of(st);
+  route.anchor_chunk  = pick_chunk(
+    waves * route.ap.group_steps, anchor_chunk_steps(wide, route.ap.group_steps), [&](int64_t c) {
+      int64_t t = 0;
+      for (auto const& e : ga) {
+        t += certex_amd::screen_group_tiles(e.nq, (e.nx + stride - 1) / stride, qb, int(c));
+      }
+      return t;
+    });
+  route.screen_chunk = pick_chunk(waves, kRoutedChunk, [&](int64_t c) {
+    int64_t t = 0;
+    for (auto const& e : gs) { t += certex_amd::screen_group_tiles(e.nq, e.nx, qb, int(c)); }
+    return t;
+  });
   for (auto& e : ga) {
     e.tile0 = route.anchor_tiles;
     route.anchor_tiles += certex_amd::screen_group_tiles(e.nq, (e.nx + stride - 1) / stride, qb,
@@ -676,7 +739,7 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   }
   for (auto& e : gs) {
     e.tile0 = route.screen_tiles;
-    route.screen_tiles += certex_amd::screen_group_tiles(e.nq, e.nx, qb, kRoutedChunk);
+    route.screen_tiles += certex_amd::screen_group_tiles(e.nq, e.nx, qb, route.screen_chunk);
   }
   route.n_route = int(gs.size());
 

@@ -127,7 +127,13 @@ struct screen_args {
   int64_t n_groups = 0;
   int64_t grp_base = 0;  // first group column of the pass
   int group_steps  = 1;
+  // fine groups: a group is 4 consecutive anchors (column grp_base + scan index / 4) instead of
+  // group_steps steps, for searches whose k is large next to the number of anchor steps
+  bool fine = false;
 };
+
+/** Anchors per fine group. */
+constexpr int kFineGroup = 4;
 
 /** Queries per workgroup of the screen kernels for a batch padded to nq_pad. */
 int screen_query_block(bool f16, int row_bytes, int64_t nq_pad);

@@ -179,11 +179,20 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     __builtin_amdgcn_s_setprio(0);
 
     if constexpr (ANCHORS) {
+      if (a.fine) {
 #pragma unroll
-      for (int qt = 0; qt < 4; ++qt) {
-        const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
-        anchor_tile<R, FILT>(col, row0, q0 + g * 64 + qt * 16 + (lane & 15),
-                             wave * QB + g * 64 + qt * 16 + lane, a, w, gml, gmr);
+        for (int qt = 0; qt < 4; ++qt) {
+          const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
+          const int64_t q    = q0 + g * 64 + qt * 16 + (lane & 15);
+          anchor_tile_fine<R, FILT>(col, row0, q, q < w.q_end, a, w, gmax);
+        }
+      } else {
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) {
+          const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
+          anchor_tile<R, FILT>(col, row0, q0 + g * 64 + qt * 16 + (lane & 15),
+                               wave * QB + g * 64 + qt * 16 + lane, a, w, gml, gmr);
+        }
       }
     } else {
       val_t mq[4];
@@ -237,7 +246,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     }
     if constexpr (ANCHORS) {
       // end of an anchor group (group_steps steps, aligned to the wave's range)
-      if ((s + 1) % a.group_steps == 0 || s + 1 == n_steps) {
+      if (!a.fine && ((s + 1) % a.group_steps == 0 || s + 1 == n_steps)) {
         const int64_t grp = a.grp_base + s / a.group_steps;
         for (int e = lane; e < QB; e += 64) {
           if (q0 + e < w.q_end) {
@@ -263,7 +272,8 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 
   if constexpr (!ANCHORS) {
     __syncthreads();
-    flush_hits<R::kValues>(q0, a, hit_q, hit_row, hit_val, &n_hits);
+    flush_hits<R::kValues>(q0, QB, a, hit_q, hit_row, hit_val, &n_hits,
+                           reinterpret_cast<uint32_t*>(qlds));
   }
 }
 

@@ -159,23 +159,35 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
     uint32_t base    = 0;
     if (lane == leader) { base = atomicAdd(n_hits, uint32_t(__builtin_popcountll(mask))); }
     base = __builtin_amdgcn_readlane(base, leader);
-    if (bits) {
-      const int j = __builtin_ctz(bits);
-      bits &= bits - 1;
-      const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
-      const uint32_t pos = base + rank;
-      float val          = 0.0f;
-      if constexpr (VALS) {
+    const bool had     = bits != 0;
+    const int j        = had ? __builtin_ctz(bits) : 0;
+    bits &= bits - 1;
+    const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
+    const uint32_t pos = base + rank;
+    float val          = 0.0f;
+    if constexpr (VALS) {
 #pragma unroll
-        for (int t = 0; t < 16; ++t) { val = t == j ? float(v[t]) : val; }
+      for (int t = 0; t < 16; ++t) { val = t == j ? float(v[t]) : val; }
+    }
+    if (had && pos < uint32_t(kHitCap)) {
+      hit_q[pos]   = qloc;
+      hit_row[pos] = row;
+      if constexpr (VALS) { hit_val[pos] = val; }
+    }
+    // a full list: straight to the global bucket, one atomic per query of the round (the 4 lanes
+    // l, l ^ 16, l ^ 32, l ^ 48 hold the same query)
+    const uint64_t spill = __ballot(had && pos >= uint32_t(kHitCap));
+    if (spill != 0) {
+      const uint64_t same = spill & (0x0001000100010001ull << (lane & 15));
+      const int first     = same ? __builtin_ctzll(same) : lane;
+      uint32_t at         = 0;
+      if (same && lane == first) {
+        at = atomicAdd(a.cand_count + q0 + qloc, uint32_t(__builtin_popcountll(same)));
       }
-      if (pos < uint32_t(kHitCap)) {
-        hit_q[pos]   = qloc;
-        hit_row[pos] = row;
-        if constexpr (VALS) { hit_val[pos] = val; }
-      } else {
+      at = uint32_t(__shfl(int(at), first));
+      if ((spill >> lane) & 1) {
         const int64_t q      = q0 + qloc;
-        const uint32_t bslot = atomicAdd(a.cand_count + q, 1u);
+        const uint32_t bslot = at + uint32_t(__builtin_popcountll(same & ((1ull << lane) - 1)));
         if (bslot < a.cap) {
           a.cand_rows[q * a.cap + bslot] = row;
           if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = val; }
@@ -185,17 +197,33 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
   }
 }
 
-/** Flushes the workgroup's LDS survivor list to the per-query buckets (after a barrier). */
+/**
+ * Flushes the workgroup's LDS survivor list to the per-query buckets (after a barrier, once the
+ * queries in LDS are no longer read): each survivor's rank among its query's survivors comes
+ * from an LDS counter, then one global atomic per query reserves the query's slots. `scratch`
+ * holds qb + kHitCap words of LDS (the query rows' space).
+ */
 template <bool VALS>
-__device__ inline void flush_hits(int64_t q0, const screen_args& a, const uint32_t* hit_q,
+__device__ inline void flush_hits(int64_t q0, int qb, const screen_args& a, const uint32_t* hit_q,
                                   const uint32_t* hit_row, const float* hit_val,
-                                  const uint32_t* n_hits)
+                                  const uint32_t* n_hits, uint32_t* scratch)
 {
+  uint32_t* cnt     = scratch;       // [qb] survivors per query, then their first slot
+  uint32_t* rank    = scratch + qb;  // [kHitCap]
   const uint32_t nh = *n_hits < uint32_t(kHitCap) ? *n_hits : uint32_t(kHitCap);
+  for (int e = threadIdx.x; e < qb; e += blockDim.x) { cnt[e] = 0; }
+  __syncthreads();
+  for (uint32_t e = threadIdx.x; e < nh; e += blockDim.x) { rank[e] = atomicAdd(&cnt[hit_q[e]], 1u); }
+  __syncthreads();
+  for (int e = threadIdx.x; e < qb; e += blockDim.x) {
+    if (cnt[e] != 0) { cnt[e] = atomicAdd(a.cand_count + q0 + e, cnt[e]); }
+  }
+  __syncthreads();
   for (uint32_t e = threadIdx.x; e < nh; e += blockDim.x) {
-    const int64_t q      = q0 + hit_q[e];
-    const uint32_t bslot = atomicAdd(a.cand_count + q, 1u);
+    const uint32_t ql    = hit_q[e];
+    const uint32_t bslot = cnt[ql] + rank[e];
     if (bslot < a.cap) {
+      const int64_t q                = q0 + ql;
       a.cand_rows[q * a.cap + bslot] = hit_row[e];
       if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = hit_val[e]; }
     }
@@ -260,6 +288,46 @@ __device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], i
     m = R::vmax(m, __shfl_xor(m, 16));
     m = R::vmax(m, __shfl_xor(m, 32));
     if (lane < 16) { gml[e] = R::vmax(gml[e], m); }
+  }
+}
+
+/**
+ * Anchor pass with fine groups, one 16-query tile of a 64-row step: each lane writes, for each of
+ * its 4 row tiles, the best screen value of its 4 consecutive anchors (and, for fp16 rows, the
+ * stored row holding it, ties to the lower row) straight to the group table: group column
+ * grp_base + (scan index of the first of the 4) / 4. row0 is the scan index of the lane's bit 0;
+ * q the lane's query (written only when live).
+ */
+template <typename R, bool FILT>
+__device__ __forceinline__ void anchor_tile_fine(const typename R::acc_t (&col)[4], int64_t row0,
+                                                 int64_t q, bool live, const screen_args& a,
+                                                 const screen_work& w, typename R::val_t* gmax)
+{
+  using val_t = typename R::val_t;
+#pragma unroll
+  for (int bt = 0; bt < 4; ++bt) {
+    const int64_t first = row0 + bt * 16;  // scan index of the group's first anchor
+    val_t m             = R::lowest();
+    uint32_t row        = 0xffffffffu;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      val_t v           = col[bt][r];
+      const int64_t idx = first + r;
+      if constexpr (FILT) {
+        if (idx < w.n_scan && !keeps(a.filter, q, uint32_t(w.base + idx * a.row_stride))) {
+          v = R::lowest();
+        }
+      }
+      if (v > m) {  // strict: ties keep the lower row
+        m   = v;
+        row = uint32_t(w.base + idx * a.row_stride);
+      }
+    }
+    if (live && first < w.n_scan) {
+      const int64_t e = q * a.n_groups + a.grp_base + first / kFineGroup;
+      gmax[e]         = m;
+      if constexpr (R::kArgmax) { a.grow[e] = row; }
+    }
   }
 }
 

@@ -179,14 +179,23 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
 
     const int64_t row0 = s * kStepRows + (lane >> 4) * 4;
     if constexpr (ANCHORS) {
+      if (a.fine) {
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
-        anchor_tile<R, FILT>(col, row0, q0 + qt * 16 + (lane & 15), wave * QB + qt * 16 + lane, a,
-                             w, gml, gmr);
+        for (int qt = 0; qt < QT; ++qt) {
+          const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
+          const int64_t q    = q0 + qt * 16 + (lane & 15);
+          anchor_tile_fine<R, FILT>(col, row0, q, q < w.q_end, a, w, gmax);
+        }
+      } else {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
+          anchor_tile<R, FILT>(col, row0, q0 + qt * 16 + (lane & 15), wave * QB + qt * 16 + lane,
+                               a, w, gml, gmr);
+        }
       }
       // end of an anchor group (group_steps steps, aligned to the wave's range)
-      if ((s + 1) % a.group_steps == 0 || s + 1 == n_steps) {
+      if (!a.fine && ((s + 1) % a.group_steps == 0 || s + 1 == n_steps)) {
         const int64_t grp = a.grp_base + s / a.group_steps;
         for (int e = lane; e < QB; e += 64) {
           if (q0 + e < w.q_end) {
@@ -237,7 +246,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
 
   if constexpr (!ANCHORS) {
     __syncthreads();
-    flush_hits<true>(q0, a, hit_q, hit_row, hit_val, &n_hits);
+    flush_hits<true>(q0, QB, a, hit_q, hit_row, hit_val, &n_hits,
+                     reinterpret_cast<uint32_t*>(qlds));
   }
 }
 

@@ -299,90 +299,137 @@ __device__ inline double fcoord(const void* p, elem t, int64_t i)
 }
 
 /**
- * Exact fp64 scores of NR stored rows against the query whose coordinates sit in LDS as doubles,
- * computed by one wave in the oracle's canonical order: lane l accumulates coordinates l, l + 64,
- * ... with fused multiply-adds, and the 64 partial sums are combined by the xor butterfly (every
- * lane returns the same bits). l2: sum (q - x)^2; inner: -sum q x; cosine: -sum q x /
- * sqrt(sum q^2 sum x^2). The 64 lanes read a row's coordinates together (coalesced), 4 per lane
- * and row at a time, so that 4 NR loads per lane are in flight.
+ * Exact fp64 scores of stored rows against the query whose coordinates sit in LDS as doubles, in
+ * the oracle's canonical order: 64 partial sums, partial p accumulating coordinates p, p + 64, ...
+ * in increasing order with fused multiply-adds, combined by the xor butterfly (for off = 32 .. 1:
+ * p[i] + p[i ^ off]). A row is scored by L lanes of a wave (a slot): lane g of the slot keeps the
+ * 64 / L partials g, g + L, ..., so the butterfly levels off >= L combine partials inside a lane
+ * and the levels below L cross lanes; every lane of the slot ends with the same bits. With L < 64
+ * a wave scores 64 / L rows at once (short rows keep more loads in flight), NR rows per slot.
+ * l2: sum (q - x)^2; inner: -sum q x; cosine: -sum q x / sqrt(sum q^2 sum x^2).
  */
-template <int NR>
-__device__ inline void wave_scores(const double* qv, const void* vectors, elem t,
+template <int L, int NR>
+__device__ inline void slot_scores(const double* qv, const void* vectors, elem t,
                                    const int64_t (&rows)[NR], int64_t dim, metric_kind metric,
-                                   int lane, double (&out)[NR])
+                                   int g, double (&out)[NR])
 {
-  constexpr int U = 4;
-  double acc[NR], xx[NR], qq = 0;
+  constexpr int P = 64 / L;               // partials per lane
+  constexpr int U = P >= 4 ? 1 : 4 / P;   // 64-coordinate rounds per iteration: 4 loads per row
+  double acc[NR][P], xx[NR][P], qq[P];
 #pragma unroll
-  for (int r = 0; r < NR; ++r) { acc[r] = xx[r] = 0; }
-  for (int64_t j0 = lane; j0 < dim; j0 += 64 * U) {
-    double b[NR][U];
+  for (int u = 0; u < P; ++u) {
+    qq[u] = 0;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) { acc[r][u] = xx[r][u] = 0; }
+  }
+  for (int64_t j0 = g; j0 < dim; j0 += 64 * U) {
+    double b[NR][U][P];
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t j = j0 + 64 * u;
-        b[r][u]         = j < dim ? fcoord(vectors, t, rows[r] * dim + j) : 0.0;
+      for (int v = 0; v < U; ++v) {
+#pragma unroll
+        for (int u = 0; u < P; ++u) {
+          const int64_t j = j0 + 64 * v + L * u;
+          b[r][v][u]      = j < dim ? fcoord(vectors, t, rows[r] * dim + j) : 0.0;
+        }
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t j = j0 + 64 * u;
-      if (j >= dim) { break; }
-      const double a = qv[j];
-      if (metric == metric_kind::cosine) { qq = fma(a, a, qq); }
+    for (int v = 0; v < U; ++v) {
 #pragma unroll
-      for (int r = 0; r < NR; ++r) {
-        if (metric == metric_kind::l2) {
-          const double d = a - b[r][u];
-          acc[r]         = fma(d, d, acc[r]);
-        } else {
-          acc[r] = fma(a, b[r][u], acc[r]);
-          if (metric == metric_kind::cosine) { xx[r] = fma(b[r][u], b[r][u], xx[r]); }
+      for (int u = 0; u < P; ++u) {
+        const int64_t j = j0 + 64 * v + L * u;
+        if (j < dim) {
+          const double a = qv[j];
+          if (metric == metric_kind::cosine) { qq[u] = fma(a, a, qq[u]); }
+#pragma unroll
+          for (int r = 0; r < NR; ++r) {
+            const double x = b[r][v][u];
+            if (metric == metric_kind::l2) {
+              const double d = a - x;
+              acc[r][u]      = fma(d, d, acc[r][u]);
+            } else {
+              acc[r][u] = fma(a, x, acc[r][u]);
+              if (metric == metric_kind::cosine) { xx[r][u] = fma(x, x, xx[r][u]); }
+            }
+          }
         }
       }
     }
   }
+  // butterfly levels inside the lane (off = 32 .. L): partial u pairs with u ^ (off / L)
 #pragma unroll
-  for (int off = 32; off; off >>= 1) {
-    if (metric == metric_kind::cosine) { qq += __shfl_xor(qq, off); }
+  for (int h = P / 2; h >= 1; h >>= 1) {
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      if (u & h) { continue; }
+      qq[u] += qq[u | h];
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        acc[r][u] += acc[r][u | h];
+        xx[r][u] += xx[r][u | h];
+      }
+    }
+  }
+  // levels off < L across the lanes of the slot
+#pragma unroll
+  for (int off = L / 2; off; off >>= 1) {
+    if (metric == metric_kind::cosine) { qq[0] += __shfl_xor(qq[0], off); }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      acc[r] += __shfl_xor(acc[r], off);
-      if (metric == metric_kind::cosine) { xx[r] += __shfl_xor(xx[r], off); }
+      acc[r][0] += __shfl_xor(acc[r][0], off);
+      if (metric == metric_kind::cosine) { xx[r][0] += __shfl_xor(xx[r][0], off); }
     }
   }
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     if (metric == metric_kind::l2) {
-      out[r] = acc[r];
+      out[r] = acc[r][0];
     } else if (metric == metric_kind::inner) {
-      out[r] = -acc[r];
+      out[r] = -acc[r][0];
     } else {
-      out[r] = -acc[r] / sqrt(qq * xx[r]);
+      out[r] = -acc[r][0] / sqrt(qq[0] * xx[r][0]);
+    }
+  }
+}
+
+/** Scores rid[from, to) into key[] (ordered keys) with slots of L lanes, NR rows per slot. */
+template <int L>
+__device__ inline void score_rows_l(const double* qv, const void* vectors, elem t, int64_t dim,
+                                    metric_kind metric, const uint32_t* rid, uint64_t* key,
+                                    int from, int to)
+{
+  constexpr int NR   = 2;
+  constexpr int PER  = (64 / L) * NR;  // rows per wave at a time
+  const int lane     = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g        = lane % L;
+  const int slot     = lane / L;
+  for (int e0 = from + wave * PER; e0 < to; e0 += PER * (kThreads / 64)) {
+    int64_t rows[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int e = e0 + slot * NR + r;
+      rows[r]     = int64_t(rid[e < to ? e : to - 1]);
+    }
+    double sc[NR];
+    slot_scores<L, NR>(qv, vectors, t, rows, dim, metric, g, sc);
+    if (g == 0) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        const int e = e0 + slot * NR + r;
+        if (e < to) { key[e] = score_key(sc[r]); }
+      }
     }
   }
 }
 
 /**
- * Scores rid[from, to) into key[] (ordered keys), two rows per wave at a time; every thread of
- * the block calls it.
+ * Lanes per scored row for vectors of `dim` coordinates: 16 up to 128 coordinates, 32 up to 256,
+ * whole waves above (the kernels that score rows are instantiated per width, so that each keeps
+ * the registers and occupancy of its own width).
  */
-__device__ inline void score_rows(const double* qv, const void* vectors, elem t, int64_t dim,
-                                  metric_kind metric, const uint32_t* rid, uint64_t* key, int from,
-                                  int to)
-{
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int e = from + 2 * wave; e < to; e += 2 * (kThreads / 64)) {
-    const int64_t rows[2] = {int64_t(rid[e]), int64_t(rid[e + 1 < to ? e + 1 : e])};
-    double sc[2];
-    wave_scores<2>(qv, vectors, t, rows, dim, metric, lane, sc);
-    if (lane == 0) {
-      key[e] = score_key(sc[0]);
-      if (e + 1 < to) { key[e + 1] = score_key(sc[1]); }
-    }
-  }
-}
+inline int score_lanes(int64_t dim) { return dim <= 128 ? 16 : (dim <= 256 ? 32 : 64); }
 
 /** LDS entries of the candidate buffers: a power of two between lo and kBuf covering want. */
 inline int buffer_entries(int want, int lo)
@@ -401,6 +448,7 @@ __device__ inline uint32_t fkey(float f)
 
 constexpr int kMaxFloatDim = kMaxF16Halves;  // widest float vector
 
+template <int L>
 __global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_args a, int cap)
 {
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
@@ -473,7 +521,7 @@ __global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_arg
   }
   __syncthreads();
   const int m = cnt < cap ? cnt : cap;
-  score_rows(qv, a.vectors, a.t, a.dim, a.metric, rid, key, 0, m);
+  score_rows_l<L>(qv, a.vectors, a.t, a.dim, a.metric, rid, key, 0, m);
   const int Pw = pow2_at_least(m);
   for (int e = m + tid; e < Pw; e += kThreads) {
     key[e] = ~0ull;
@@ -566,6 +614,7 @@ __device__ uint32_t radix_select(int64_t n, int rank, F key_of, int* hist, int* 
  * (U tightens as better rows arrive). Scores use one wave per row; the best k by (score, row)
  * stay in LDS.
  */
+template <int L>
 __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a, int cap)
 {
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
@@ -596,7 +645,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
   int64_t n_scored = 0;
   auto score       = [&](int from, int to) {
     n_scored += to - from;
-    score_rows(qv, a.vectors, a.t, a.dim, a.metric, rid, key, from, to);
+    score_rows_l<L>(qv, a.vectors, a.t, a.dim, a.metric, rid, key, from, to);
   };
   int have = 0;  // entries [0, have) of key / rid are scored
   auto keep_best = [&]() {
@@ -751,17 +800,27 @@ void launch_dyn(K kernel, unsigned blocks, size_t bytes, hipStream_t stream, Arg
 void threshold_f16(const threshold_f_args& a, hipStream_t stream)
 {
   if (a.nq_pad == 0) { return; }
-  const int cap = buffer_entries(a.per_query, 256);
-  launch_dyn(threshold_f16_kernel, unsigned(a.nq_pad), size_t(cap) * 12 + size_t(a.dim) * 8,
-             stream, a, cap);
+  const int cap       = buffer_entries(a.per_query, 256);
+  const size_t bytes  = size_t(cap) * 12 + size_t(a.dim) * 8;
+  const unsigned grid = unsigned(a.nq_pad);
+  switch (score_lanes(a.dim)) {
+    case 16: launch_dyn(threshold_f16_kernel<16>, grid, bytes, stream, a, cap); break;
+    case 32: launch_dyn(threshold_f16_kernel<32>, grid, bytes, stream, a, cap); break;
+    default: launch_dyn(threshold_f16_kernel<64>, grid, bytes, stream, a, cap); break;
+  }
 }
 
 void verify_topk_f(const verify_f_args& a, hipStream_t stream)
 {
   if (a.nq == 0) { return; }
-  const int cap = buffer_entries(4 * a.k, 1024);
-  launch_dyn(verify_topk_f_kernel, unsigned(a.nq), size_t(cap) * 12 + size_t(a.dim) * 8, stream,
-             a, cap);
+  const int cap       = buffer_entries(4 * a.k, 1024);
+  const size_t bytes  = size_t(cap) * 12 + size_t(a.dim) * 8;
+  const unsigned grid = unsigned(a.nq);
+  switch (score_lanes(a.dim)) {
+    case 16: launch_dyn(verify_topk_f_kernel<16>, grid, bytes, stream, a, cap); break;
+    case 32: launch_dyn(verify_topk_f_kernel<32>, grid, bytes, stream, a, cap); break;
+    default: launch_dyn(verify_topk_f_kernel<64>, grid, bytes, stream, a, cap); break;
+  }
 }
 
 void finish(const double* best_score, const int64_t* best_row, int64_t nq, int k,

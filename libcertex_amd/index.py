@@ -173,6 +173,10 @@ class _Core:
         return self._get("cuvsCertexIndexHasLabels", ctypes.c_bool)
 
     @property
+    def n_partitioned(self):
+        return self._get("cuvsCertexIndexGetPartitioned", ctypes.c_int64)
+
+    @property
     def dtype(self):
         d = self.h.contents.dtype
         return {(C.kDLFloat, 32): "float32", (C.kDLFloat, 16): "float16", (C.kDLInt, 8): "int8", (C.kDLUInt, 8): "uint8"}[
@@ -282,6 +286,14 @@ class Index:
                     C.check(L.cuvsCertexPartitionByLabels(res, self.core.h))
         ids = torch.arange(n0, n0 + X.shape[0])
         return _back(ids, kind)
+
+    def partition(self):
+        """Copy the screening rows into label order now (reference index.partition_by_labels): each
+        label's queries then screen only that label's rows; vectors added later go through the
+        label filter until the next partition. Results do not change."""
+        _require(self.core is not None and self.core.has_labels, "add labeled vectors first")
+        with self._writer:
+            C.check(C.lib().cuvsCertexPartitionByLabels(C.resources(), self.core.h))
 
     def remove(self, ids):
         """Remove vectors by id; they never appear in later results (certex/index.py:314-319)."""
