@@ -24,6 +24,19 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 P_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA peak, 10^12 ops/s
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "screen_i8_c2_traffic.txt")
+
+
+def screen_traffic():
+    """HBM bytes per screen launch at config 2, from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (calibrated against a plain copy); None when it is missing."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
 P_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA peak
 HBM_GBS = 8000.0
 
@@ -370,7 +383,8 @@ def main():
             "peak": P_INT8_TOPS,
             "unit": "TOP/s",
             "frac": round(achieved / P_INT8_TOPS, 4),
-            "traffic": None,
+            # measured only for the default workload (profiles/screen_i8_c2_traffic.txt)
+            "traffic": screen_traffic() if (n, d, nq, args.batch) == (10_000_000, 128, 10_000, 10_000) else None,
             "avg_launch_ms": round(screen_ms, 4),
             "ops_per_launch": ops_per_launch,
         },

@@ -15,25 +15,44 @@ inline unsigned blocks_for(int64_t n, int block = 256)
   return unsigned((n + block - 1) / block);
 }
 
+/**
+ * One thread per 16-byte chunk of a stored row (row_bytes / 16 = 8 or 16 consecutive lanes per
+ * row), so that the reads of the input rows and the writes of the codes are coalesced; the
+ * chunks' partial norms and sums meet by shuffles within the row's lanes.
+ */
 __global__ void encode_rows_kernel(const uint8_t* x, int64_t n, int64_t dim, int row_bytes,
                                    uint8_t flip, metric_kind metric, int8_t* codes, int32_t* rowc)
 {
-  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
-  if (i >= n) { return; }
-  const uint8_t* src = x + i * dim;
-  int8_t* dst        = codes + i * row_bytes;
+  const int cpr   = row_bytes / 16;  // a power of two that divides 64
+  const int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  const int64_t r = t / cpr;
+  const int c     = int(t % cpr);
   int norm = 0, sum = 0;
-  for (int64_t j = 0; j < dim; ++j) {
-    const int c = int(int8_t(src[j] ^ flip));
-    dst[j]      = int8_t(c);
-    norm += c * c;
-    sum += c;
+  if (r < n) {
+    uint8_t v[16];
+    const int64_t j0 = int64_t(c) * 16;
+    if (dim % 16 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && j0 < dim) {
+      *reinterpret_cast<int4*>(v) = *reinterpret_cast<const int4*>(x + r * dim + j0);
+    } else {
+#pragma unroll
+      for (int b = 0; b < 16; ++b) { v[b] = j0 + b < dim ? x[r * dim + j0 + b] : uint8_t(0); }
+    }
+    int8_t out[16];
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      const int code = j0 + b < dim ? int(int8_t(v[b] ^ flip)) : 0;
+      out[b]         = int8_t(code);
+      norm += code * code;
+      sum += code;
+    }
+    *reinterpret_cast<int4*>(codes + r * row_bytes + j0) = *reinterpret_cast<const int4*>(out);
   }
-  for (int64_t j = dim; j < row_bytes; ++j) { dst[j] = 0; }
-  if (metric == metric_kind::l2) {
-    rowc[i] = -(norm >> 1);
-  } else {
-    rowc[i] = flip ? 128 * sum : 0;
+  for (int off = 1; off < cpr; off <<= 1) {
+    norm += __shfl_xor(norm, off);
+    sum += __shfl_xor(sum, off);
+  }
+  if (r < n && c == 0) {
+    rowc[r] = metric == metric_kind::l2 ? -(norm >> 1) : (flip ? 128 * sum : 0);
   }
 }
 
@@ -272,8 +291,8 @@ void encode_rows_i8(const uint8_t* x, int64_t n, int64_t dim, int row_bytes, uin
                     metric_kind metric, int8_t* codes, int32_t* rowc, hipStream_t stream)
 {
   if (n == 0) { return; }
-  encode_rows_kernel<<<blocks_for(n), 256, 0, stream>>>(x, n, dim, row_bytes, flip, metric, codes,
-                                                        rowc);
+  encode_rows_kernel<<<blocks_for(n * (row_bytes / 16)), 256, 0, stream>>>(x, n, dim, row_bytes,
+                                                                          flip, metric, codes, rowc);
 }
 
 void encode_queries_i8(const uint8_t* q, int64_t nq, int64_t nq_pad, int64_t dim, int row_bytes,
