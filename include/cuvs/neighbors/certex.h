@@ -147,7 +147,7 @@ CUVS_EXPORT cuvsError_t cuvsCertexIndexGetAnchorStride(cuvsCertexIndex_t index, 
 CUVS_EXPORT cuvsError_t cuvsCertexIndexHasLabels(cuvsCertexIndex_t index, bool* has_labels);
 /**
  * Vectors covered by the label partition (0 when none); the ones added later go through the
- * label filter (reference index::n_partitioned, certex.hpp:421-425).
+ * label filter (reference index::n_partitioned, certex.hpp:301-306).
  */
 CUVS_EXPORT cuvsError_t cuvsCertexIndexGetPartitioned(cuvsCertexIndex_t index,
                                                       int64_t* n_partitioned);

@@ -164,7 +164,7 @@ void set_labels(cuvs::resources const& res, const int32_t* labels, int64_t n, in
                 int64_t first = 0);
 
 /**
- * Copy the screening rows into label order (reference certex.hpp:607-619, certex.cu:1542-1606),
+ * Copy the screening rows into label order (reference certex.hpp:601-624, certex.cu:1542-1606),
  * a speed option of label search: each label's queries then screen only that label's rows, and
  * the rows added later go through the label filter. Needs labels; results do not change.
  */
