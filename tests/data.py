@@ -47,3 +47,20 @@ def powerlaw_unit(n, d, seed, basis_seed=31, dtype=np.float32, chunk=1 << 15):
 def labels(n, n_classes, seed):
     """uint32-valued labels uniform over n_classes (stored as int32, as the index takes them)."""
     return np.random.default_rng(seed).integers(0, n_classes, n).astype(np.int32)
+
+
+def mixture_u8_cuda(n, d=128, n_centres=1000, seed=2, centre_seed=1, sigma=20.0, hi=80.0, chunk=1 << 22):
+    """The config 2 / config 5 generator on the GPU (torch generators): for large n. Centres come
+    from a CPU generator seeded centre_seed, rows from a CUDA generator seeded seed."""
+    import torch
+
+    centres = (torch.rand((n_centres, d), generator=torch.Generator().manual_seed(centre_seed), dtype=torch.float64) * hi)
+    centres = centres.float().cuda()
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    out = torch.empty((n, d), dtype=torch.uint8, device="cuda")
+    for i in range(0, n, chunk):
+        m = min(chunk, n - i)
+        c = torch.randint(0, n_centres, (m,), generator=g, device="cuda")
+        v = centres[c] + torch.randn((m, d), generator=g, device="cuda") * sigma
+        out[i : i + m] = v.round().clamp_(0, 255).to(torch.uint8)
+    return out
