@@ -151,6 +151,13 @@ CUVS_EXPORT cuvsError_t cuvsCertexIndexHasLabels(cuvsCertexIndex_t index, bool* 
  */
 CUVS_EXPORT cuvsError_t cuvsCertexIndexGetPartitioned(cuvsCertexIndex_t index,
                                                       int64_t* n_partitioned);
+/**
+ * Number of k-means lists (0 when none), and the vectors they cover: those of the build, stored
+ * in list order (reference index::n_lists / list_offsets, certex.hpp:321-334).
+ */
+CUVS_EXPORT cuvsError_t cuvsCertexIndexGetLists(cuvsCertexIndex_t index,
+                                                int32_t* n_lists,
+                                                int64_t* n_listed);
 /** Grow the capacity to at least `capacity` rows (core.cpp reserve). */
 CUVS_EXPORT cuvsError_t cuvsCertexReserve(cuvsResources_t res,
                                           int64_t capacity,

@@ -12,6 +12,7 @@
 #include <cstdint>
 #include <memory>
 #include <string>
+#include <vector>
 
 namespace cuvs {
 
@@ -134,6 +135,13 @@ class index {
   [[nodiscard]] auto has_labels() const noexcept -> bool;
   /** Vectors covered by the label partition (0: none; later additions are not). */
   [[nodiscard]] auto n_partitioned() const noexcept -> int64_t;
+  /**
+   * k-means lists (index_params::n_lists; reference certex.hpp:321-334): the stored rows
+   * [list_offsets()[j], list_offsets()[j + 1]) hold the vectors of list j, which covers the
+   * vectors of the build; later vectors follow in insertion order. 0 lists: rows are ids.
+   */
+  [[nodiscard]] auto n_lists() const noexcept -> int;
+  [[nodiscard]] auto list_offsets() const noexcept -> std::vector<int64_t> const&;
   [[nodiscard]] auto host_vectors() const noexcept -> bool;
   [[nodiscard]] auto state() const -> detail::index_state&;
 

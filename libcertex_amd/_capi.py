@@ -147,6 +147,7 @@ def lib():
                     "cuvsCertexIndexGetAnchorStride": [P(IndexHandle), P(i32)],
                     "cuvsCertexIndexHasLabels": [P(IndexHandle), P(ctypes.c_bool)],
                     "cuvsCertexIndexGetPartitioned": [P(IndexHandle), P(i64)],
+                    "cuvsCertexIndexGetLists": [P(IndexHandle), P(i32), P(i64)],
                     "cuvsCertexReserve": [ctypes.c_size_t, i64, P(IndexHandle)],
                     "cuvsCertexStatsBegin": [],
                     "cuvsCertexStatsEnd": [P(i64), P(i64), P(i64)],

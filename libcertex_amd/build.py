@@ -24,6 +24,7 @@ SOURCES = [
     "kernels/select.hip",
     "kernels/encode.hip",
     "kernels/partition.hip",
+    "kernels/lists.hip",
     "certex.cpp",
     "c_api.cpp",
 ]

@@ -518,6 +518,17 @@ cuvsError_t cuvsCertexIndexGetPartitioned(cuvsCertexIndex_t index, int64_t* n_pa
   });
 }
 
+cuvsError_t cuvsCertexIndexGetLists(cuvsCertexIndex_t index, int32_t* n_lists, int64_t* n_listed)
+{
+  return translate([=] {
+    dispatch(index->dtype, [&](auto tag) {
+      auto const* idx = as_index<decltype(tag)>(*index);
+      *n_lists        = idx->n_lists();
+      *n_listed       = idx->n_lists() > 0 ? idx->list_offsets().back() : 0;
+    });
+  });
+}
+
 cuvsError_t cuvsCertexReserve(cuvsResources_t res, int64_t capacity, cuvsCertexIndex_t index)
 {
   return translate([=] {

@@ -15,6 +15,7 @@
 #include <fstream>
 #include <functional>
 #include <new>
+#include <thread>
 
 namespace cuvs {
 
@@ -307,13 +308,16 @@ auto waves_of(index_state const& st) -> int64_t
   return certex_amd::screen_waves(!is_int(st.type), st.row_bytes);
 }
 
-/** Anchor pass: every anchor of the index, or the partition's (routed) and the tail's. */
+/**
+ * Anchor pass: every anchor of the index, or the partition's (routed) and the tail's, into the
+ * columns [0, ap.n_groups) of a group table of row_len columns.
+ */
 template <typename F>
 void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan const& ap,
-                 route_plan const* route, F&& launch, hipStream_t stream)
+                 int64_t row_len, route_plan const* route, F&& launch, hipStream_t stream)
 {
   aa.row_stride  = ap.stride;
-  aa.n_groups    = ap.n_groups;
+  aa.n_groups    = row_len;
   aa.group_steps = int(ap.group_steps);
   aa.fine        = ap.fine;
   const int64_t unit = waves_of(st) * ap.group_steps;
@@ -333,18 +337,18 @@ void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan 
                          stream);
   }
   certex_amd::screen_args r = aa;
-  r.codes                   = st.part_codes.as<int8_t>();
-  r.rowc                    = st.part_rowc.p;
+  r.codes                   = st.label_part.codes.as<int8_t>();
+  r.rowc                    = st.label_part.rowc.p;
   r.groups                  = route->anchor_groups;
   r.n_route                 = route->n_route;
   r.n_tiles                 = route->anchor_tiles;
   r.chunk_steps             = route->anchor_chunk;
   r.filter.kind             = 0;  // every row of a group carries the group's label
   if (r.n_tiles > 0) { launch(r, stream); }
-  const int64_t tail = st.size - st.n_part;
+  const int64_t tail = st.size - st.label_part.n;
   if (tail > 0) {
     certex_amd::screen_args t = aa;
-    t.row_base                = st.n_part;
+    t.row_base                = st.label_part.n;
     t.n_scan                  = (tail + ap.stride - 1) / ap.stride;
     t.grp_base                = route->part_groups;
     t.chunk_steps             = plain_chunk(st, t.nq, t.nq_pad, t.n_scan, unit, cap);
@@ -363,18 +367,18 @@ auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
       return;
     }
     certex_amd::screen_args r = sa;
-    r.codes                   = st.part_codes.as<int8_t>();
-    r.rowc                    = st.part_rowc.p;
+    r.codes                   = st.label_part.codes.as<int8_t>();
+    r.rowc                    = st.label_part.rowc.p;
     r.groups                  = route->screen_groups;
     r.n_route                 = route->n_route;
     r.n_tiles                 = route->screen_tiles;
     r.chunk_steps             = route->screen_chunk;
     r.filter.kind             = 0;
     if (r.n_tiles > 0) { launch(r, stream); }
-    const int64_t tail = st.size - st.n_part;
+    const int64_t tail = st.size - st.label_part.n;
     if (tail > 0) {
       certex_amd::screen_args t = sa;
-      t.row_base                = st.n_part;
+      t.row_base                = st.label_part.n;
       t.n_scan                  = tail;
       t.chunk_steps = plain_chunk(st, t.nq, t.nq_pad, t.n_scan, waves_of(st), kScreenChunk);
       launch(t, stream);
@@ -457,10 +461,218 @@ void count_stats(cuvs::resources const& res, index_state const& st, int64_t B, b
   if (!verified_by_kernel) { t_stats.verified += int64_t(h[1]); }
 }
 
+/**
+ * The list probe of one batch (reference probe_lists, lists.cuh:351-460): the p nearest lists of
+ * every query, and more of its nearest (up to kMaxProbe) while they hold fewer than kProbeRows * k
+ * rows. Every (query, list) pair scans all rows of the list as fine anchor groups of 4, written to
+ * the query's row of the group table; the pairs are grouped by list so that the rows of a list are
+ * read once for all of its queries.
+ */
+struct probe_plan {
+  int64_t n_pairs = 0;
+  int64_t nq_pad  = 0;
+  int64_t cols    = 0;     // table columns of the probe: those of the query with the most
+  bool enough     = true;  // every query met kProbeRows * k rows
+  std::vector<int32_t> pair_q, pair_col;  // per pair, in list order
+  std::vector<certex_amd::screen_group> groups;
+  int64_t tiles = 0;
+  int chunk     = 0;
+};
+constexpr int64_t kProbeRows = 16;
+
+/** Plans the probe from the encoded query rows; false when the index has no lists to probe. */
+bool plan_probe(cuvs::resources const& res, index_state const& st, const void* qrows, int64_t B,
+                int k, int p, probe_plan& pp)
+{
+  auto& rs           = res.state();
+  hipStream_t stream = rs.stream;
+  const bool f16     = !is_int(st.type);
+  const int L        = st.n_lists;
+  const int Lp       = certex_amd::pad_centers(L);
+  const int pmax     = std::min(L, certex_amd::kMaxProbe);
+  p                  = std::min(p, pmax);
+  auto* dist  = static_cast<float*>(rs.get(cuvs::detail::ws_probe_dist, size_t(B) * Lp * 4));
+  auto* lists = static_cast<int32_t*>(rs.get(cuvs::detail::ws_probe, size_t(B) * pmax * 4));
+  certex_amd::center_distances(qrows, f16, B, st.row_bytes, st.centers_q.p, st.cterm.as<float>(),
+                               Lp, dist, stream);
+  certex_amd::nearest_lists(dist, B, L, Lp, pmax, lists, stream);
+  std::vector<int32_t> h(size_t(B) * pmax);
+  CERTEX_HIP_TRY(hipMemcpyAsync(h.data(), lists, h.size() * 4, hipMemcpyDeviceToHost, stream));
+  CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  const auto& off    = st.list_offsets;
+  const int64_t want = kProbeRows * k;
+  auto list_rows     = [&](int32_t j) { return off[size_t(j) + 1] - off[size_t(j)]; };
+  std::vector<int32_t> taken(static_cast<size_t>(B));
+  std::vector<int64_t> start(static_cast<size_t>(L) + 1, 0);
+  for (int64_t q = 0; q < B; ++q) {
+    int64_t rows = 0, cols = 0;
+    int t        = 0;
+    for (; t < pmax; ++t) {
+      const int32_t j = h[size_t(q * pmax + t)];
+      if (j < 0 || (t >= p && rows >= want)) { break; }
+      rows += list_rows(j);
+      cols += (list_rows(j) + certex_amd::kFineGroup - 1) / certex_amd::kFineGroup;
+      ++start[size_t(j) + 1];
+    }
+    taken[size_t(q)] = t;
+    pp.cols          = std::max(pp.cols, cols);
+    pp.enough        = pp.enough && rows >= want;
+  }
+  for (int j = 0; j < L; ++j) { start[size_t(j) + 1] += start[size_t(j)]; }
+  pp.n_pairs = start[size_t(L)];
+  pp.nq_pad  = certex_amd::pad_queries(pp.n_pairs);
+  pp.pair_q.resize(size_t(pp.n_pairs));
+  pp.pair_col.resize(size_t(pp.n_pairs));
+  {
+    std::vector<int64_t> fill(start.begin(), start.end() - 1);
+    for (int64_t q = 0; q < B; ++q) {
+      int64_t col = 0;
+      for (int t = 0; t < taken[size_t(q)]; ++t) {
+        const int32_t j   = h[size_t(q * pmax + t)];
+        const int64_t s   = fill[size_t(j)]++;
+        pp.pair_q[size_t(s)]   = int32_t(q);
+        pp.pair_col[size_t(s)] = int32_t(col);
+        col += (list_rows(j) + certex_amd::kFineGroup - 1) / certex_amd::kFineGroup;
+      }
+    }
+  }
+  for (int j = 0; j < L; ++j) {
+    const int64_t nq = start[size_t(j) + 1] - start[size_t(j)];
+    if (nq > 0 && list_rows(j) > 0) {
+      pp.groups.push_back({start[size_t(j)], nq, off[size_t(j)], list_rows(j), 0});
+    }
+  }
+  if (pp.groups.empty()) { return false; }
+  const bool wide     = f16 && st.row_bytes > 256;
+  const int qb        = certex_amd::screen_query_block(f16, st.row_bytes, pp.nq_pad);
+  const int64_t waves = waves_of(st);
+  pp.chunk = pick_chunk(waves, anchor_chunk_steps(wide, 1), [&](int64_t c) {
+    int64_t t = 0;
+    for (auto const& g : pp.groups) { t += certex_amd::screen_group_tiles(g.nq, g.nx, qb, int(c)); }
+    return t;
+  });
+  for (auto& g : pp.groups) {
+    g.tile0 = pp.tiles;
+    pp.tiles += certex_amd::screen_group_tiles(g.nq, g.nx, qb, pp.chunk);
+  }
+  return true;
+}
+
+/** The probe's launch into the columns col0 + ... of a group table of row_len columns. */
+template <typename F>
+void probe_pass(cuvs::resources const& res, index_state const& st, certex_amd::screen_args aa,
+                probe_plan const& pp, int64_t col0, int64_t row_len, F&& launch)
+{
+  auto& rs           = res.state();
+  hipStream_t stream = rs.stream;
+  // device tables: pair query, pair column, groups
+  const size_t pair_bytes = (size_t(pp.n_pairs) * 4 + 15) / 16 * 16;
+  const size_t grp_bytes  = pp.groups.size() * sizeof(certex_amd::screen_group);
+  std::vector<char> host(2 * pair_bytes + grp_bytes);
+  std::memcpy(host.data(), pp.pair_q.data(), size_t(pp.n_pairs) * 4);
+  auto* hc = reinterpret_cast<int32_t*>(host.data() + pair_bytes);
+  for (int64_t i = 0; i < pp.n_pairs; ++i) { hc[i] = int32_t(col0 + pp.pair_col[size_t(i)]); }
+  std::memcpy(host.data() + 2 * pair_bytes, pp.groups.data(), grp_bytes);
+  char* dev = static_cast<char*>(rs.get(cuvs::detail::ws_probe, host.size()));
+  CERTEX_HIP_TRY(hipMemcpyAsync(dev, host.data(), host.size(), hipMemcpyHostToDevice, stream));
+  const auto* d_q = reinterpret_cast<const int32_t*>(dev);
+  auto* rows      = rs.get(cuvs::detail::ws_probe_rows, size_t(pp.nq_pad) * st.row_bytes);
+  certex_amd::gather_rows(aa.qcodes, d_q, pp.n_pairs, st.row_bytes, rows, stream);
+  certex_amd::screen_args r = aa;
+  r.codes       = st.codes.as<int8_t>();
+  r.rowc        = st.rowc.p;
+  r.qcodes      = static_cast<const int8_t*>(rows);
+  r.nq          = pp.n_pairs;
+  r.nq_pad      = pp.nq_pad;
+  r.groups      = reinterpret_cast<const certex_amd::screen_group*>(dev + 2 * pair_bytes);
+  r.n_route     = int(pp.groups.size());
+  r.n_tiles     = pp.tiles;
+  r.chunk_steps = pp.chunk;
+  r.row_stride  = 1;
+  r.row_base    = 0;
+  r.fine        = true;
+  r.group_steps = 1;
+  r.grp_base    = 0;
+  r.n_groups    = row_len;
+  r.out_row     = d_q;
+  r.out_col     = reinterpret_cast<const int32_t*>(dev + pair_bytes);
+  launch(r, stream);
+  CERTEX_HIP_TRY(hipStreamSynchronize(stream));  // the host tables go out of scope
+}
+
+/**
+ * The group table of a batch: the anchors' groups, or the list probe's groups over the listed rows
+ * and the anchors' over the rows added after the lists (columns of the anchors first). No stored
+ * row may sit in two groups: the k-th best group must stand for k distinct rows. Without enough
+ * rows in some query's probed lists the batch uses the anchors alone.
+ */
+struct table_plan {
+  anchor_plan ap{};
+  bool anchors        = true;
+  int64_t anchor_base = 0;  // the anchors cover the stored rows [anchor_base, size)
+  probe_plan pp;
+  int64_t n_groups = 0;
+};
+
+auto plan_table(cuvs::resources const& res, index_state const& st, const void* qrows, int64_t B,
+                int64_t nq_pad, int k, search_params const& params,
+                certex_amd::filter_args const& fa, route_plan const* route) -> table_plan
+{
+  table_plan tp;
+  if (route != nullptr) {
+    tp.ap       = route->ap;
+    tp.n_groups = tp.ap.n_groups;
+    return tp;
+  }
+  bool probe = st.n_lists > 0 && params.probe_lists > 0 && (fa.kind == 0 || fa.kind == 1) &&
+               plan_probe(res, st, qrows, B, k, params.probe_lists, tp.pp) && tp.pp.enough;
+  if (probe) {
+    const int64_t tail = st.size - st.n_listed;
+    tp.anchors         = tail > 0;
+    tp.anchor_base     = st.n_listed;
+    if (tp.anchors) { tp.ap = plan_anchors(st, tail, nq_pad, k); }
+    const int64_t acols = tp.anchors ? tp.ap.n_groups : 0;
+    probe = nq_pad * (acols + tp.pp.cols) * 4 <= kTableBytes;
+  }
+  if (!probe) {  // anchors over every row
+    tp.pp          = probe_plan{};
+    tp.anchors     = true;
+    tp.anchor_base = 0;
+    tp.ap          = plan_anchors(st, st.size, nq_pad, k);
+  }
+  tp.n_groups = (tp.anchors ? tp.ap.n_groups : 0) + tp.pp.cols;
+  return tp;
+}
+
+/** Fills the group table (lowest values) where the probe leaves columns unwritten, then the passes. */
+template <typename F>
+void table_pass(cuvs::resources const& res, index_state const& st, certex_amd::screen_args aa,
+                table_plan const& tp, route_plan const* route, F&& launch)
+{
+  hipStream_t stream = res.state().stream;
+  if (tp.pp.n_pairs > 0) {
+    if (is_int(st.type)) {
+      certex_amd::fill_i32(static_cast<int32_t*>(aa.gmax), aa.nq_pad * tp.n_groups, INT32_MIN,
+                           stream);
+    } else {
+      certex_amd::fill_u32(static_cast<uint32_t*>(aa.gmax), aa.nq_pad * tp.n_groups, 0xff800000u,
+                           stream);
+    }
+  }
+  if (tp.anchors) {
+    aa.row_base = tp.anchor_base;
+    anchor_pass(st, aa, tp.ap, tp.n_groups, route, launch, stream);
+  }
+  if (tp.pp.n_pairs > 0) {
+    probe_pass(res, st, aa, tp.pp, tp.anchors ? tp.ap.n_groups : 0, tp.n_groups, launch);
+  }
+}
+
 /** One batch of queries of an integer index (the caller holds the shared lock). */
 void search_batch_int(cuvs::resources const& res, index_state const& st, const void* queries,
                       int64_t B, int k, int64_t q0, int64_t* neighbors, float* distances,
-                      certex_amd::filter_args fa, int, route_plan const* route)
+                      certex_amd::filter_args fa, search_params const& params,
+                      route_plan const* route)
 {
   auto& rs             = res.state();
   hipStream_t stream   = rs.stream;
@@ -468,15 +680,17 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
   const int64_t nq_pad = certex_amd::pad_queries(B);
   const uint8_t flip   = st.type == vtype::u8 ? 0x80 : 0;
   fa.q0                = q0;
+  fa.row_ids           = st.row_ids.as<int32_t>();
+  fa.n_listed          = st.n_listed;
 
   auto* qcodes =
     static_cast<int8_t*>(rs.get(cuvs::detail::ws_qcodes, size_t(nq_pad) * st.row_bytes));
   certex_amd::encode_queries_i8(static_cast<const uint8_t*>(queries), B, nq_pad, st.dim,
                                 st.row_bytes, flip, qcodes, stream);
 
-  // anchor pass: every anchor_stride-th stored row; the best screen value of every group of
-  // anchors, then the k-th best group is the threshold of the query
-  const anchor_plan ap = route ? route->ap : plan_anchors(st, size, nq_pad, k);
+  // group table: the best screen value of every group of anchors (every anchor_stride-th stored
+  // row) and of the probed lists' rows; the k-th best group is the threshold of the query
+  const table_plan tp = plan_table(res, st, qcodes, B, nq_pad, k, params, fa, route);
   certex_amd::screen_args sa{};
   sa.codes     = st.codes.as<int8_t>();
   sa.rowc      = st.rowc.p;
@@ -487,15 +701,15 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
   sa.filter    = fa;
 
   auto* theta   = static_cast<int32_t*>(rs.get(cuvs::detail::ws_theta, size_t(nq_pad) * 4));
-  bool all_rows = ap.n_groups < k;
+  bool all_rows = tp.n_groups < k;
   if (!all_rows) {
     auto* gmax = static_cast<int32_t*>(
-      rs.get(cuvs::detail::ws_gmax, size_t(nq_pad) * size_t(ap.n_groups) * 4));
+      rs.get(cuvs::detail::ws_gmax, size_t(nq_pad) * size_t(tp.n_groups) * 4));
     certex_amd::screen_args aa = sa;
     aa.gmax                    = gmax;
-    timed(0, stream, [&] { anchor_pass(st, aa, ap, route, certex_amd::anchors_i8, stream); });
+    timed(0, stream, [&] { table_pass(res, st, aa, tp, route, certex_amd::anchors_i8); });
     timed(1, stream,
-          [&] { certex_amd::threshold_i8(gmax, ap.n_groups, B, nq_pad, k, theta, stream); });
+          [&] { certex_amd::threshold_i8(gmax, tp.n_groups, B, nq_pad, k, theta, stream); });
   }
 
   uint32_t *count = nullptr, *rows = nullptr;
@@ -529,8 +743,9 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
   va.nq         = B;
   va.k          = k;
   if (route != nullptr) {
-    va.part_ids = st.part_ids.as<int32_t>();
-    va.n_part   = st.n_part;
+    va.part_ids   = st.label_part.ids.as<int32_t>();
+    va.n_part     = st.label_part.n;
+    va.part_codes = st.label_part.codes.as<int8_t>();
   }
   va.best_score = best_score;
   va.best_row   = best_row;
@@ -541,7 +756,8 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
 /** One batch of queries of a float index (the caller holds the shared lock). */
 void search_batch_float(cuvs::resources const& res, index_state const& st, const void* queries,
                         int64_t B, int k, int64_t q0, int64_t* neighbors, float* distances,
-                        certex_amd::filter_args fa, int anchors, route_plan const* route)
+                        certex_amd::filter_args fa, search_params const& params,
+                        route_plan const* route)
 {
   auto& rs             = res.state();
   hipStream_t stream   = rs.stream;
@@ -550,6 +766,8 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   const auto t         = elem_of(st.type);
   const bool wide      = st.halves > 128;  // the K-loop screen
   fa.q0                = q0;
+  fa.row_ids           = st.row_ids.as<int32_t>();
+  fa.n_listed          = st.n_listed;
 
   auto* qrows =
     static_cast<uint16_t*>(rs.get(cuvs::detail::ws_qcodes, size_t(nq_pad) * st.row_bytes));
@@ -557,7 +775,7 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   certex_amd::encode_queries_f16(queries, t, B, nq_pad, st.dim, st.halves, st.normalize,
                                  st.center.as<double>(), 1.0 / st.alpha, qrows, qscal, stream);
 
-  const anchor_plan ap = route ? route->ap : plan_anchors(st, size, nq_pad, k);
+  const table_plan tp = plan_table(res, st, qrows, B, nq_pad, k, params, fa, route);
   certex_amd::screen_args sa{};
   sa.codes     = st.codes.as<int8_t>();
   sa.rowc      = st.rowc.p;
@@ -568,27 +786,29 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   sa.filter    = fa;
 
   auto* theta   = static_cast<float*>(rs.get(cuvs::detail::ws_theta, size_t(nq_pad) * 4));
-  bool all_rows = ap.n_groups < k;
+  bool all_rows = tp.n_groups < k;
   if (!all_rows) {
     auto* gmax = static_cast<float*>(
-      rs.get(cuvs::detail::ws_gmax, size_t(nq_pad) * size_t(ap.n_groups) * 4));
+      rs.get(cuvs::detail::ws_gmax, size_t(nq_pad) * size_t(tp.n_groups) * 4));
     auto* grow = static_cast<uint32_t*>(
-      rs.get(cuvs::detail::ws_grow, size_t(nq_pad) * size_t(ap.n_groups) * 4));
+      rs.get(cuvs::detail::ws_grow, size_t(nq_pad) * size_t(tp.n_groups) * 4));
     certex_amd::screen_args aa = sa;
     aa.gmax                    = gmax;
     aa.grow                    = grow;
     timed(0, stream, [&] {
-      anchor_pass(st, aa, ap, route,
-                  wide ? certex_amd::anchors_f16_wide : certex_amd::anchors_f16, stream);
+      table_pass(res, st, aa, tp, route,
+                 wide ? certex_amd::anchors_f16_wide : certex_amd::anchors_f16);
     });
     certex_amd::threshold_f_args ta{};
     ta.gmax      = gmax;
     ta.grow      = grow;
-    ta.n_groups  = ap.n_groups;
+    ta.n_groups  = tp.n_groups;
     ta.nq        = B;
     ta.nq_pad    = nq_pad;
     ta.k         = k;
-    ta.per_query = std::max(anchors, k + std::max(k / 4, 16));
+    ta.per_query = std::max(params.anchors, k + std::max(k / 4, 16));
+    ta.row_ids   = st.row_ids.as<int32_t>();
+    ta.n_listed  = st.n_listed;
     ta.vectors   = st.vectors.p;
     ta.queries   = queries;
     ta.t         = t;
@@ -600,8 +820,8 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
     ta.gamma     = st.gamma;
     ta.theta     = theta;
     if (route != nullptr) {
-      ta.part_ids = st.part_ids.as<int32_t>();
-      ta.n_part   = st.n_part;
+      ta.part_ids = st.label_part.ids.as<int32_t>();
+      ta.n_part   = st.label_part.n;
     }
     timed(1, stream, [&] { certex_amd::threshold_f16(ta, stream); });
   }
@@ -652,8 +872,8 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   }
   va.scored = scored;
   if (route != nullptr) {
-    va.part_ids = st.part_ids.as<int32_t>();
-    va.n_part   = st.n_part;
+    va.part_ids = st.label_part.ids.as<int32_t>();
+    va.n_part   = st.label_part.n;
   }
   timed(3, stream, [&] { certex_amd::verify_topk_f(va, stream); });
   if (scored != nullptr) {
@@ -665,8 +885,8 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
 }
 
 using batch_fn = void (*)(cuvs::resources const&, index_state const&, const void*, int64_t, int,
-                          int64_t, int64_t*, float*, certex_amd::filter_args, int,
-                          route_plan const*);
+                          int64_t, int64_t*, float*, certex_amd::filter_args,
+                          search_params const&, route_plan const*);
 
 /**
  * Label search of one batch over the label partition (reference search_by_labels,
@@ -675,7 +895,8 @@ using batch_fn = void (*)(cuvs::resources const&, index_state const&, const void
  */
 void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn batch,
                   const char* queries, size_t qrow, int64_t B, int k, const int32_t* qlabels,
-                  int64_t* neighbors, float* distances, certex_amd::filter_args fa, int anchors)
+                  int64_t* neighbors, float* distances, certex_amd::filter_args fa,
+                  search_params const& params)
 {
   auto& rs           = res.state();
   hipStream_t stream = rs.stream;
@@ -691,7 +912,7 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   const bool f16       = !is_int(st.type);
   const bool wide      = f16 && st.row_bytes > 256;
   const int qb         = certex_amd::screen_query_block(f16, st.row_bytes, nq_pad);
-  const auto& off      = st.part_offsets;
+  const auto& off      = st.label_part.offsets;
   std::vector<certex_amd::screen_group> ga, gs;
   int64_t max_nx = 0;
   for (int64_t i = 0; i < B;) {
@@ -717,7 +938,7 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   route.ap.stride   = stride;
   route.ap.n_anchor = 0;
   size_groups(route.ap, (max_nx + stride - 1) / stride,
-              (st.size - st.n_part + stride - 1) / stride, nq_pad, k, &route.part_groups);
+              (st.size - st.label_part.n + stride - 1) / stride, nq_pad, k, &route.part_groups);
   const int64_t waves = waves_of(st);
   route.anchor_chunk  = pick_chunk(
     waves * route.ap.group_steps, anchor_chunk_steps(wide, route.ap.group_steps), [&](int64_t c) {
@@ -769,7 +990,7 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   auto* nb_s  = reinterpret_cast<int64_t*>(out);
   auto* ds_s  = reinterpret_cast<float*>(out + size_t(B) * k * 8);
   fa.query_labels = d_sorted;  // the label filter of the tail, in the sorted order
-  batch(res, st, q_sorted, B, k, 0, nb_s, ds_s, fa, anchors, &route);
+  batch(res, st, q_sorted, B, k, 0, nb_s, ds_s, fa, params, &route);
   certex_amd::scatter_rows(nb_s, d_order, B, int64_t(k) * 8, neighbors, stream);
   certex_amd::scatter_rows(ds_s, d_order, B, int64_t(k) * 4, distances, stream);
   CERTEX_HIP_TRY(hipStreamSynchronize(stream));  // the host tables above go out of scope
@@ -794,12 +1015,12 @@ void search_impl(cuvs::resources const& res, search_params const& params, index<
   std::function<void(int64_t, int64_t)> run = [&](int64_t b0, int64_t B) {
     try {
       const char* q = reinterpret_cast<const char*>(queries.data) + size_t(b0) * qrow;
-      if (fa.kind == 3 && st.n_part > 0) {
+      if (fa.kind == 3 && st.label_part.n > 0) {
         routed_batch(res, st, batch, q, qrow, B, int(k), fa.query_labels + b0, neighbors + b0 * k,
-                     distances + b0 * k, fa, params.anchors);
+                     distances + b0 * k, fa, params);
       } else {
-        batch(res, st, q, B, int(k), b0, neighbors + b0 * k, distances + b0 * k, fa,
-              params.anchors, nullptr);
+        batch(res, st, q, B, int(k), b0, neighbors + b0 * k, distances + b0 * k, fa, params,
+              nullptr);
       }
     } catch (batch_too_large const&) {
       if (B < 2) { throw; }
@@ -889,11 +1110,159 @@ auto index<T>::metric() const noexcept -> cuvs::distance::DistanceType { return 
 template <typename T>
 auto index<T>::has_labels() const noexcept -> bool { return s_->has_labels; }
 template <typename T>
-auto index<T>::n_partitioned() const noexcept -> int64_t { return s_->n_part; }
+auto index<T>::n_partitioned() const noexcept -> int64_t { return s_->label_part.n; }
+template <typename T>
+auto index<T>::n_lists() const noexcept -> int { return s_->n_lists; }
+template <typename T>
+auto index<T>::list_offsets() const noexcept -> std::vector<int64_t> const&
+{
+  return s_->list_offsets;
+}
 template <typename T>
 auto index<T>::host_vectors() const noexcept -> bool { return s_->host_vectors; }
 template <typename T>
 auto index<T>::state() const -> detail::index_state& { return *s_; }
+
+constexpr int kKmeansRounds = 10;
+
+/**
+ * k-means lists of the stored rows [0, n) (reference fit_lists, lists.cuh:137-210): centers from
+ * an evenly strided sample of the screening rows (kKmeansRounds Lloyd rounds from sample rows
+ * spread evenly over it), every row's nearest center, and a stable sort of the ids by list, which
+ * gives row_ids, id_rows and the list offsets. The caller then stores the rows in that order.
+ */
+void fit_lists(cuvs::resources const& res, index_state& st, int64_t n)
+{
+  using cuvs::detail::device_buffer;
+  hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  const int L        = st.params.n_lists;
+  const bool f16     = !is_int(st.type);
+  const int width    = f16 ? st.halves : st.row_bytes;
+  const int Lp       = certex_amd::pad_centers(L);
+  const int64_t s    = std::max<int64_t>(L, std::min<int64_t>(n, st.params.kmeans_sample));
+  const int64_t step = std::max<int64_t>(1, n / s);
+  const int64_t cnt  = std::min<int64_t>(s, (n + step - 1) / step);
+  device_buffer centers(size_t(L) * width * 4), centers_q(size_t(Lp) * st.row_bytes),
+    cterm(size_t(Lp) * 4), assign(size_t(n) * 4);
+  {
+    device_buffer sids(size_t(cnt) * 4), sample(size_t(cnt) * st.row_bytes);
+    device_buffer sums(size_t(L) * width * 4), counts(size_t(L) * 4), init_d(size_t(L) * 4);
+    certex_amd::strided_ids(sids.as<int32_t>(), cnt, step, stream);
+    certex_amd::gather_rows(st.codes.p, sids.as<int32_t>(), cnt, st.row_bytes, sample.p, stream);
+    std::vector<int32_t> init(static_cast<size_t>(L));
+    for (int c = 0; c < L; ++c) { init[size_t(c)] = int32_t(int64_t(c) * cnt / L); }
+    CERTEX_HIP_TRY(
+      hipMemcpyAsync(init_d.p, init.data(), init.size() * 4, hipMemcpyHostToDevice, stream));
+    certex_amd::rows_to_centers(sample.p, f16, init_d.as<int32_t>(), L, width,
+                                centers.as<float>(), stream);
+    certex_amd::finish_centers(nullptr, nullptr, L, Lp, width, f16, centers.as<float>(),
+                               centers_q.p, cterm.as<float>(), stream);
+    for (int it = 0; it < kKmeansRounds; ++it) {
+      certex_amd::nearest_centers(sample.p, f16, cnt, st.row_bytes, centers_q.p,
+                                  cterm.as<float>(), Lp, assign.as<int32_t>(), stream);
+      certex_amd::fill_u32(sums.as<uint32_t>(), int64_t(L) * width, 0, stream);
+      certex_amd::fill_u32(counts.as<uint32_t>(), L, 0, stream);
+      certex_amd::center_sums(sample.p, f16, cnt, width, assign.as<int32_t>(), L,
+                              sums.as<float>(), counts.as<unsigned int>(), stream);
+      certex_amd::finish_centers(sums.as<float>(), counts.as<unsigned int>(), L, Lp, width, f16,
+                                 centers.as<float>(), centers_q.p, cterm.as<float>(), stream);
+    }
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  }
+  // the list of every row, then the ids in list order (stable: ascending ids within a list)
+  certex_amd::nearest_centers(st.codes.p, f16, n, st.row_bytes, centers_q.p, cterm.as<float>(),
+                              Lp, assign.as<int32_t>(), stream);
+  device_buffer keys(size_t(n) * 4), ids_tmp(size_t(n) * 4), row_ids(size_t(n) * 4),
+    id_rows(size_t(n) * 4), offs(size_t(L + 1) * 8);
+  const size_t tb = certex_amd::sort_by_label_temp_bytes(n);
+  {
+    device_buffer temp(std::max<size_t>(tb, 16));
+    CERTEX_HIP_TRY(certex_amd::sort_by_label(assign.as<int32_t>(), n, ids_tmp.as<int32_t>(),
+                                             keys.as<int32_t>(), row_ids.as<int32_t>(), temp.p,
+                                             tb, stream));
+    certex_amd::label_offsets(keys.as<int32_t>(), n, L, offs.as<int64_t>(), stream);
+    certex_amd::invert_ids(row_ids.as<int32_t>(), n, id_rows.as<int32_t>(), stream);
+    st.list_offsets.assign(size_t(L) + 1, 0);
+    CERTEX_HIP_TRY(hipMemcpyAsync(st.list_offsets.data(), offs.p, st.list_offsets.size() * 8,
+                                  hipMemcpyDeviceToHost, stream));
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  }
+  st.n_lists    = L;
+  st.list_width = width;
+  st.centers    = std::move(centers);
+  st.centers_q  = std::move(centers_q);
+  st.cterm      = std::move(cterm);
+  st.row_ids    = std::move(row_ids);
+  st.id_rows    = std::move(id_rows);
+}
+
+/**
+ * Stores the screening rows [0, n) in list order (reference permuted(), lists.cuh:88-100):
+ * stored row r is encoded again from the vector of id row_ids[r], read from the stored vectors
+ * (float) or from the integer source x (device or host).
+ */
+void store_in_lists(cuvs::resources const& res, index_state& st, int64_t n, const void* x,
+                    bool on_device)
+{
+  hipStream_t stream  = static_cast<hipStream_t>(res.stream());
+  const auto* row_ids = st.row_ids.as<int32_t>();
+  if (!is_int(st.type)) {
+    const size_t rb     = size_t(st.dim) * elem_size(st.type);
+    const int64_t chunk = std::max<int64_t>(1, (int64_t(64) << 20) / int64_t(rb));
+    cuvs::detail::device_buffer staging(size_t(std::min(chunk, n)) * rb);
+    for (int64_t r = 0; r < n; r += chunk) {
+      const int64_t m = std::min(chunk, n - r);
+      certex_amd::gather_rows(st.vectors.p, row_ids + r, m, int64_t(rb), staging.p, stream);
+      certex_amd::encode_rows_f16(staging.p, elem_of(st.type), m, st.dim, st.halves, st.normalize,
+                                  st.center.as<double>(), 1.0 / st.alpha, st.metric, st.gamma,
+                                  st.codes.as<uint16_t>() + size_t(r) * st.halves,
+                                  st.rowc.as<float>() + r, st.maxima.as<double>(), stream);
+    }
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+    st.n_listed = n;
+    return;
+  }
+  const uint8_t flip  = st.type == vtype::u8 ? 0x80 : 0;
+  const int64_t d     = st.dim;
+  const int64_t chunk = std::max<int64_t>(1, (int64_t(64) << 20) / d);
+  cuvs::detail::device_buffer staging(size_t(std::min(chunk, n)) * d);
+  std::vector<int32_t> h_ids;
+  std::vector<uint8_t> h_rows;
+  if (!on_device) {
+    h_ids.resize(size_t(n));
+    h_rows.resize(size_t(std::min(chunk, n)) * d);
+    CERTEX_HIP_TRY(
+      hipMemcpyAsync(h_ids.data(), row_ids, size_t(n) * 4, hipMemcpyDeviceToHost, stream));
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  }
+  const auto* src = static_cast<const uint8_t*>(x);
+  for (int64_t r = 0; r < n; r += chunk) {
+    const int64_t m = std::min(chunk, n - r);
+    if (on_device) {
+      certex_amd::gather_rows(src, row_ids + r, m, d, staging.p, stream);
+    } else {
+      // host rows gathered by host threads, then one copy
+      const int threads = int(std::max(1u, std::min(16u, std::thread::hardware_concurrency())));
+      std::vector<std::thread> pool;
+      for (int t = 0; t < threads; ++t) {
+        pool.emplace_back([&, t] {
+          for (int64_t i = t; i < m; i += threads) {
+            std::memcpy(h_rows.data() + i * d, src + int64_t(h_ids[size_t(r + i)]) * d,
+                        size_t(d));
+          }
+        });
+      }
+      for (auto& th : pool) { th.join(); }
+      CERTEX_HIP_TRY(hipMemcpyAsync(staging.p, h_rows.data(), size_t(m) * d,
+                                    hipMemcpyHostToDevice, stream));
+    }
+    certex_amd::encode_rows_i8(staging.as<uint8_t>(), m, d, st.row_bytes, flip, st.metric,
+                               st.codes.as<int8_t>() + r * st.row_bytes,
+                               st.rowc.as<int32_t>() + r, stream);
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  }
+  st.n_listed = n;
+}
 
 template <typename T>
 auto build(cuvs::resources const& res, index_params const& params, matrix_view<const T> dataset)
@@ -907,6 +1276,11 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
           "certex: cosine distance needs float32 or float16 vectors");
   expects(dataset.rows >= 1 && dataset.cols >= 1, "certex: the dataset is empty");
   expects(params.anchor_stride >= 1, "certex: anchor_stride must be at least 1");
+  expects(params.n_lists >= 0 && params.n_lists <= dataset.rows,
+          "certex: n_lists must lie in [0, number of vectors]");
+  expects(params.n_lists <= certex_amd::kMaxLists, "certex: at most 16384 lists");
+  expects(params.n_lists == 0 || dataset.rows < (int64_t(1) << 31),
+          "certex: at most 2^31 - 1 vectors in an index with lists");
   st.params        = params;
   st.dim           = dataset.cols;
   st.anchor_stride = params.anchor_stride;
@@ -921,6 +1295,10 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
     append_int(res, st, reinterpret_cast<const uint8_t*>(dataset.data), dataset.rows,
                dataset.on_device, 0);
     res.sync();
+    if (params.n_lists > 0) {  // the rows in list order; ids stay the input order
+      fit_lists(res, st, dataset.rows);
+      store_in_lists(res, st, dataset.rows, dataset.data, dataset.on_device);
+    }
     st.size = dataset.rows;
     return out;
   }
@@ -970,6 +1348,10 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
                               st.codes.as<uint16_t>(), st.rowc.as<float>(), st.maxima.as<double>(),
                               stream);
   res.sync();
+  if (params.n_lists > 0) {  // the rows in list order; ids and stored vectors stay the input order
+    fit_lists(res, st, n);
+    store_in_lists(res, st, n, nullptr, true);
+  }
   st.size = n;
   return out;
 }
@@ -1014,13 +1396,16 @@ void remove(cuvs::resources const& res, const int64_t* ids, int64_t n_ids, index
   std::unique_lock publish(st.rw);
   CERTEX_HIP_TRY(hipDeviceSynchronize());
   certex_amd::fill_u32(reinterpret_cast<uint32_t*>(counter), 2, 0, stream);
-  const auto* ppos = st.part_pos.as<int32_t>();
+  certex_amd::row_places at;
+  at.list_pos  = st.id_rows.as<int32_t>();
+  at.n_listed  = st.n_listed;
+  at.part_pos  = st.label_part.pos.as<int32_t>();
+  at.n_part    = st.label_part.n;
+  at.part_rowc = st.label_part.rowc.p;
   if (is_int(st.type)) {
-    certex_amd::remove_rows_i8(ids, n_ids, st.size, st.rowc.as<int32_t>(), counter, stream, ppos,
-                               st.n_part, st.part_rowc.as<int32_t>());
+    certex_amd::remove_rows_i8(ids, n_ids, st.size, st.rowc.as<int32_t>(), counter, at, stream);
   } else {
-    certex_amd::remove_rows_f16(ids, n_ids, st.size, st.rowc.as<float>(), counter, stream, ppos,
-                                st.n_part, st.part_rowc.as<float>());
+    certex_amd::remove_rows_f16(ids, n_ids, st.size, st.rowc.as<float>(), counter, at, stream);
   }
   CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, counter, 8, hipMemcpyDeviceToHost, stream));
   CERTEX_HIP_TRY(hipStreamSynchronize(stream));
@@ -1047,7 +1432,7 @@ void set_labels(cuvs::resources const& res, const int32_t* labels, int64_t n, in
                                   size_t(n) * sizeof(int32_t), hipMemcpyDeviceToDevice, stream));
   }
   CERTEX_HIP_TRY(hipStreamSynchronize(stream));
-  if (n > 0 && first < st.n_part) { st.n_part = 0; }  // the partition no longer matches
+  if (n > 0 && first < st.label_part.n) { st.label_part.n = 0; }  // the partition no longer matches
 }
 
 template <typename T>
@@ -1079,19 +1464,26 @@ void partition_by_labels(cuvs::resources const& res, index<T>* idx)
     offsets.resize(size_t(n_labels + 1));
     CERTEX_HIP_TRY(hipMemcpyAsync(offsets.data(), offs.p, offsets.size() * 8,
                                   hipMemcpyDeviceToHost, stream));
-    certex_amd::gather_rows(st.codes.p, ids.as<int32_t>(), n, st.row_bytes, codes.p, stream);
-    certex_amd::gather_rows(st.rowc.p, ids.as<int32_t>(), n, 4, rowc.p, stream);
+    // the stored row of every id (they differ in an index with lists)
+    const int32_t* from = ids.as<int32_t>();
+    if (st.n_listed > 0) {
+      certex_amd::stored_rows(ids.as<int32_t>(), n, st.id_rows.as<int32_t>(), st.n_listed,
+                              ids_tmp.as<int32_t>(), stream);
+      from = ids_tmp.as<int32_t>();
+    }
+    certex_amd::gather_rows(st.codes.p, from, n, st.row_bytes, codes.p, stream);
+    certex_amd::gather_rows(st.rowc.p, from, n, 4, rowc.p, stream);
     certex_amd::invert_ids(ids.as<int32_t>(), n, pos.as<int32_t>(), stream);
     CERTEX_HIP_TRY(hipStreamSynchronize(stream));
   }
   std::unique_lock publish(st.rw);
   CERTEX_HIP_TRY(hipDeviceSynchronize());  // searches on other streams may read the old copy
-  st.part_codes   = std::move(codes);
-  st.part_rowc    = std::move(rowc);
-  st.part_ids     = std::move(ids);
-  st.part_pos     = std::move(pos);
-  st.part_offsets = std::move(offsets);
-  st.n_part       = n;
+  st.label_part.codes   = std::move(codes);
+  st.label_part.rowc    = std::move(rowc);
+  st.label_part.ids     = std::move(ids);
+  st.label_part.pos     = std::move(pos);
+  st.label_part.offsets = std::move(offsets);
+  st.label_part.n       = n;
 }
 
 template <typename T>
@@ -1126,7 +1518,7 @@ void search(cuvs::resources const& res, search_params const& params, index<T> co
 namespace {
 
 constexpr uint32_t kMagic         = 0x43455258;  // "CERX"
-constexpr uint32_t kFormatVersion = 100;         // this build's layout of the stored arrays
+constexpr uint32_t kFormatVersion = 101;         // this build's layout of the stored arrays
 
 template <typename T>
 auto dtype_prefix() -> std::string
@@ -1215,6 +1607,15 @@ void serialize(cuvs::resources const& res, std::string const& filename, index<T>
     put_device(os, res, st.maxima.p, 2 * sizeof(double));
   }
   if (st.has_labels) { put_device(os, res, st.labels.p, n * sizeof(int32_t)); }
+  put(os, int32_t(st.n_lists));
+  if (st.n_lists > 0) {
+    put(os, int64_t(st.n_listed));
+    put(os, int32_t(st.list_width));
+    os.write(reinterpret_cast<const char*>(st.list_offsets.data()),
+             std::streamsize(st.list_offsets.size() * 8));
+    put_device(os, res, st.row_ids.p, size_t(st.n_listed) * 4);
+    put_device(os, res, st.centers.p, size_t(st.n_lists) * st.list_width * 4);
+  }
   expects(os.good(), "certex: writing the index file failed");
 }
 
@@ -1263,6 +1664,32 @@ void deserialize(cuvs::resources const& res, std::string const& filename, index<
     st.labels.resize_discard(size_t(st.capacity) * sizeof(int32_t));
     get_device(is, res, st.labels.p, size_t(n) * sizeof(int32_t));
     st.has_labels = true;
+  }
+  const int32_t L = get<int32_t>(is);
+  expects(L >= 0 && L <= certex_amd::kMaxLists, "certex: corrupt index file");
+  if (L > 0) {
+    st.n_listed   = get<int64_t>(is);
+    st.list_width = get<int32_t>(is);
+    expects(st.n_listed >= 0 && st.n_listed <= n && st.list_width > 0,
+            "certex: corrupt index file");
+    st.list_offsets.assign(size_t(L) + 1, 0);
+    is.read(reinterpret_cast<char*>(st.list_offsets.data()), std::streamsize((L + 1) * 8));
+    expects(bool(is), "certex: the index file is truncated");
+    const int Lp = certex_amd::pad_centers(L);
+    st.row_ids.resize_discard(size_t(std::max<int64_t>(st.n_listed, 1)) * 4);
+    st.id_rows.resize_discard(size_t(std::max<int64_t>(st.n_listed, 1)) * 4);
+    st.centers.resize_discard(size_t(L) * st.list_width * 4);
+    st.centers_q.resize_discard(size_t(Lp) * st.row_bytes);
+    st.cterm.resize_discard(size_t(Lp) * 4);
+    get_device(is, res, st.row_ids.p, size_t(st.n_listed) * 4);
+    get_device(is, res, st.centers.p, size_t(L) * st.list_width * 4);
+    hipStream_t stream = static_cast<hipStream_t>(res.stream());
+    certex_amd::invert_ids(st.row_ids.as<int32_t>(), st.n_listed, st.id_rows.as<int32_t>(), stream);
+    certex_amd::finish_centers(nullptr, nullptr, L, Lp, st.list_width, !is_int(st.type),
+                               st.centers.as<float>(), st.centers_q.p, st.cterm.as<float>(),
+                               stream);
+    res.sync();
+    st.n_lists = L;
   }
   st.size = n;
 }

@@ -103,6 +103,9 @@ enum ws_slot : int {
   ws_route,       // label routing of a batch: order, sorted labels, group tables
   ws_route_q,     // the batch's queries in label order
   ws_route_out,   // results in label order before they return to query order
+  ws_probe_dist,  // list probe: center distances of the batch's queries
+  ws_probe,       // list probe: nearest lists, pair tables
+  ws_probe_rows,  // list probe: the query row of every (query, list) pair
   ws_n_slots
 };
 
@@ -143,6 +146,20 @@ constexpr vtype vtype_of<int8_t>() { return vtype::i8; }
 template <>
 constexpr vtype vtype_of<uint8_t>() { return vtype::u8; }
 
+/**
+ * A copy of the screening rows and row terms of the ids [0, n) ordered by a key (label or list):
+ * ids[i] = id of partition row i, pos[id] = its partition row; the rows of key j are
+ * [offsets[j], offsets[j + 1]).
+ */
+struct row_partition {
+  int64_t n = 0;
+  cuvs::detail::device_buffer codes;
+  cuvs::detail::device_buffer rowc;
+  cuvs::detail::device_buffer ids;
+  cuvs::detail::device_buffer pos;
+  std::vector<int64_t> offsets;
+};
+
 struct index_state {
   int device                            = 0;
   vtype type                            = vtype::f32;
@@ -171,15 +188,21 @@ struct index_state {
   double gamma   = 0.0;  // fp32 accumulation error factor of a screening product
   int halves     = 0;    // fp16 row length
   bool normalize = false;
-  // label partition (a speed option of label search): the screening rows and row terms of the
-  // ids [0, n_part) in label order; part_ids[i] = id of partition row i, part_pos[id] = its row;
-  // the rows of label l are [part_offsets[l], part_offsets[l + 1])
-  int64_t n_part = 0;
-  cuvs::detail::device_buffer part_codes;
-  cuvs::detail::device_buffer part_rowc;
-  cuvs::detail::device_buffer part_ids;
-  cuvs::detail::device_buffer part_pos;
-  std::vector<int64_t> part_offsets;
+  // label partition (a speed option of label search): a copy of the rows in label order
+  row_partition label_part;
+  // k-means lists (a speed option of every search: the rows of the nearest lists of a query bound
+  // its threshold). The stored rows [0, n_listed) are in list order: list j holds the rows
+  // [list_offsets[j], list_offsets[j + 1]); row_ids[row] = its id, id_rows[id] = its row. Rows
+  // added later are their own ids.
+  int n_lists      = 0;
+  int64_t n_listed = 0;
+  cuvs::detail::device_buffer row_ids;
+  cuvs::detail::device_buffer id_rows;
+  cuvs::detail::device_buffer centers;    // float [n_lists, list_width]
+  cuvs::detail::device_buffer centers_q;  // the centers in the rows' type [pad_centers, row_bytes]
+  cuvs::detail::device_buffer cterm;      // float [pad_centers]: |centers_q|^2 / 2
+  std::vector<int64_t> list_offsets;
+  int list_width = 0;  // elements of a screening row: row_bytes (int8) or halves (fp16)
   mutable std::shared_mutex rw;  // searches: shared per batch; publication of updates: exclusive
   std::mutex writer;             // one update at a time
 };

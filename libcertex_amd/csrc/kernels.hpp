@@ -61,13 +61,25 @@ void encode_queries_i8(const uint8_t* q, int64_t nq, int64_t nq_pad, int64_t dim
                        uint8_t flip, int8_t* qcodes, hipStream_t stream);
 
 /**
- * Tombstone rows by id: rowc[id] = kDeadRow for 0 <= id < size; counts the ids that were live into
- * *newly_removed (ids out of range or repeated count once at most).
+ * Tombstones of ids and where their rows are stored: with lists the ids below n_listed live in
+ * stored row list_pos[id]; with a label partition the ids below n_part also have the copy
+ * part_rowc[part_pos[id]].
+ */
+struct row_places {
+  const int32_t* list_pos = nullptr;
+  int64_t n_listed        = 0;
+  const int32_t* part_pos = nullptr;
+  int64_t n_part          = 0;
+  void* part_rowc         = nullptr;
+};
+
+/**
+ * Tombstone rows by id: the row term of the id's stored row becomes kDeadRow for 0 <= id < size;
+ * counts the ids that were live into *newly_removed (ids out of range or repeated count once at
+ * most).
  */
 void remove_rows_i8(const int64_t* ids, int64_t n, int64_t size, int32_t* rowc,
-                    unsigned long long* newly_removed, hipStream_t stream,
-                    const int32_t* part_pos = nullptr, int64_t n_part = 0,
-                    int32_t* part_rowc = nullptr);
+                    unsigned long long* newly_removed, const row_places& at, hipStream_t stream);
 
 void fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);
 void fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream);
@@ -81,7 +93,18 @@ struct filter_args {
   int64_t q0 = 0;                   // first query of the batch (bitmap row, label offset)
   const int32_t* row_labels = nullptr;
   const int32_t* query_labels = nullptr;  // of all queries of the search
+  // an index with lists stores the rows [0, n_listed) in list order: stored row r < n_listed holds
+  // the id row_ids[r], later rows are their own ids. Filters test ids; the exact-score kernels
+  // report ids.
+  const int32_t* row_ids = nullptr;
+  int64_t n_listed       = 0;
 };
+
+/** The id held by stored row `row`. */
+__host__ __device__ inline uint32_t listed_id(const filter_args& f, uint32_t row)
+{
+  return row < f.n_listed ? uint32_t(f.row_ids[row]) : row;
+}
 
 /**
  * One routed pairing of a label-partitioned search: the queries [q0, q0 + nq) of the (label
@@ -130,6 +153,10 @@ struct screen_args {
   // fine groups: a group is 4 consecutive anchors (column grp_base + scan index / 4) instead of
   // group_steps steps, for searches whose k is large next to the number of anchor steps
   bool fine = false;
+  // fine groups of the list probe: query q of the launch writes its groups to row out_row[q] of the
+  // table, from column out_col[q] on (null: row q, column grp_base)
+  const int32_t* out_row = nullptr;
+  const int32_t* out_col = nullptr;
 };
 
 /** Anchors per fine group. */
@@ -196,9 +223,11 @@ struct verify_args {
   filter_args filter;  // applied to all_rows candidates
   int64_t nq;
   int k;
-  // routed searches: candidate rows below n_part are partition rows, id = part_ids[row]
-  const int32_t* part_ids = nullptr;
-  int64_t n_part          = 0;
+  // routed searches: candidate rows below n_part are partition rows, id = part_ids[row], codes in
+  // part_codes; the other rows are stored rows (filter.row_ids maps them to ids)
+  const int32_t* part_ids  = nullptr;
+  int64_t n_part           = 0;
+  const int8_t* part_codes = nullptr;
   double* best_score;  // [nq, k], smaller is better; +inf where missing
   int64_t* best_row;   // [nq, k], -1 where missing
 };
@@ -255,14 +284,9 @@ void encode_queries_f16(const void* q, elem t, int64_t nq, int64_t nq_pad, int64
                         int halves, bool normalize, const double* center, double inv_alpha,
                         uint16_t* qrows, double* qscal, hipStream_t stream);
 
-/**
- * Float tombstones: rowc[id] = -inf; counts the ids that were live. With a label partition, the
- * partition's copy of the row term (part_rowc[part_pos[id]], id < n_part) is tombstoned too.
- */
+/** Float tombstones (row term -inf) of ids, as remove_rows_i8. */
 void remove_rows_f16(const int64_t* ids, int64_t n, int64_t size, float* rowc,
-                     unsigned long long* newly_removed, hipStream_t stream,
-                     const int32_t* part_pos = nullptr, int64_t n_part = 0,
-                     float* part_rowc = nullptr);
+                     unsigned long long* newly_removed, const row_places& at, hipStream_t stream);
 
 struct threshold_f_args {
   const float* gmax;     // [nq_pad, n_groups]
@@ -282,6 +306,8 @@ struct threshold_f_args {
   double gamma;
   const int32_t* part_ids = nullptr;  // routed: anchor rows below n_part are partition rows
   int64_t n_part          = 0;
+  const int32_t* row_ids  = nullptr;  // lists: stored rows below n_listed hold ids row_ids[row]
+  int64_t n_listed        = 0;
   float* theta;          // [nq_pad]
 };
 /**
@@ -346,6 +372,46 @@ void scatter_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_by
                   hipStream_t stream);
 /** pos[ids[i]] = i. */
 void invert_ids(const int32_t* ids, int64_t n, int32_t* pos, hipStream_t stream);
+
+/** out[i] = i * step for i < n. */
+void strided_ids(int32_t* out, int64_t n, int64_t step, hipStream_t stream);
+/** out[i] = the stored row of id ids[i] (id_rows[id] for id < n_listed, else id). */
+void stored_rows(const int32_t* ids, int64_t n, const int32_t* id_rows, int64_t n_listed,
+                 int32_t* out, hipStream_t stream);
+
+// --- k-means lists (screening coordinates, squared L2) --------------------------------------
+
+/** Most lists an index may have, and most lists a query probes. */
+constexpr int kMaxLists = 16384;
+constexpr int kMaxProbe = 8;
+/** Centers are stored padded to a multiple of 64 (padding: zero rows, cterm = +inf). */
+__host__ __device__ inline int pad_centers(int n) { return (n + 63) / 64 * 64; }
+/**
+ * out[i] = the center nearest to screening row i (int8 codes or fp16 rows of row_bytes bytes);
+ * centers_q = the centers in the rows' type [n_centers_pad, row_bytes], cterm = |center|^2 / 2.
+ */
+void nearest_centers(const void* rows, bool f16, int64_t n, int row_bytes, const void* centers_q,
+                     const float* cterm, int n_centers_pad, int32_t* out, hipStream_t stream);
+/** dist[i, c] = cterm[c] - <row i, center c> for all padded centers (row stride n_centers_pad). */
+void center_distances(const void* rows, bool f16, int64_t n, int row_bytes,
+                      const void* centers_q, const float* cterm, int n_centers_pad, float* dist,
+                      hipStream_t stream);
+/** lists[q, 0 .. p) = the p nearest of the n_lists centers of dist row q (ld floats), p <= 8. */
+void nearest_lists(const float* dist, int64_t nq, int n_lists, int ld, int p, int32_t* lists,
+                   hipStream_t stream);
+/** sums[assign[i]] += row i; counts[assign[i]] += 1 (float atomics; width elements per row). */
+void center_sums(const void* rows, bool f16, int64_t n, int width, const int32_t* assign,
+                 int n_centers, float* sums, unsigned int* counts, hipStream_t stream);
+/**
+ * centers = sums / counts where counts > 0 (counts may be null: keep the centers); then their copy
+ * in the rows' type (centers_q) and cterm, for the n_centers_pad padded centers.
+ */
+void finish_centers(const float* sums, const unsigned int* counts, int n_centers,
+                    int n_centers_pad, int width, bool f16, float* centers, void* centers_q,
+                    float* cterm, hipStream_t stream);
+/** centers[c] = rows[ids[c]] as floats. */
+void rows_to_centers(const void* rows, bool f16, const int32_t* ids, int n_centers, int width,
+                     float* centers, hipStream_t stream);
 
 /**
  * Output conversion: distances (l2: score; inner: -score = <q, x>; cosine: score + 1 = 1 - cos)

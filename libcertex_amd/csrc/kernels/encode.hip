@@ -65,16 +65,20 @@ __global__ void encode_queries_kernel(const uint8_t* q, int64_t nq, int64_t nq_p
   qcodes[t]       = (i < nq && j < dim) ? int8_t(q[i * dim + j] ^ flip) : int8_t(0);
 }
 
+__device__ inline int64_t stored_row(const row_places& at, int64_t id)
+{
+  return id < at.n_listed ? int64_t(at.list_pos[id]) : id;
+}
+
 __global__ void remove_kernel(const int64_t* ids, int64_t n, int64_t size, int32_t* rowc,
-                              unsigned long long* newly, const int32_t* part_pos, int64_t n_part,
-                              int32_t* part_rowc)
+                              unsigned long long* newly, row_places at)
 {
   const int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
   if (t >= n) { return; }
   const int64_t id = ids[t];
   if (id < 0 || id >= size) { return; }
-  if (id < n_part) { part_rowc[part_pos[id]] = kDeadRow; }
-  if (atomicExch(rowc + id, kDeadRow) != kDeadRow) { atomicAdd(newly, 1ull); }
+  if (id < at.n_part) { static_cast<int32_t*>(at.part_rowc)[at.part_pos[id]] = kDeadRow; }
+  if (atomicExch(rowc + stored_row(at, id), kDeadRow) != kDeadRow) { atomicAdd(newly, 1ull); }
 }
 
 template <typename T>
@@ -230,15 +234,15 @@ __global__ void encode_queries_f16_kernel(const void* q, elem t, int64_t nq, int
 }
 
 __global__ void remove_f_kernel(const int64_t* ids, int64_t n, int64_t size, float* rowc,
-                                unsigned long long* newly, const int32_t* part_pos,
-                                int64_t n_part, float* part_rowc)
+                                unsigned long long* newly, row_places at)
 {
   const int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
   if (t >= n) { return; }
   const int64_t id = ids[t];
   if (id < 0 || id >= size) { return; }
-  if (id < n_part) { part_rowc[part_pos[id]] = -INFINITY; }
-  const int old = atomicExch(reinterpret_cast<int*>(rowc + id), __float_as_int(-INFINITY));
+  if (id < at.n_part) { static_cast<float*>(at.part_rowc)[at.part_pos[id]] = -INFINITY; }
+  const int old = atomicExch(reinterpret_cast<int*>(rowc + stored_row(at, id)),
+                             __float_as_int(-INFINITY));
   if (old != __float_as_int(-INFINITY)) { atomicAdd(newly, 1ull); }
 }
 
@@ -279,12 +283,10 @@ void encode_queries_f16(const void* q, elem t, int64_t nq, int64_t nq_pad, int64
 }
 
 void remove_rows_f16(const int64_t* ids, int64_t n, int64_t size, float* rowc,
-                     unsigned long long* newly_removed, hipStream_t stream,
-                     const int32_t* part_pos, int64_t n_part, float* part_rowc)
+                     unsigned long long* newly_removed, const row_places& at, hipStream_t stream)
 {
   if (n == 0) { return; }
-  remove_f_kernel<<<blocks_for(n), 256, 0, stream>>>(ids, n, size, rowc, newly_removed, part_pos,
-                                                     n_part, part_rowc);
+  remove_f_kernel<<<blocks_for(n), 256, 0, stream>>>(ids, n, size, rowc, newly_removed, at);
 }
 
 void encode_rows_i8(const uint8_t* x, int64_t n, int64_t dim, int row_bytes, uint8_t flip,
@@ -305,12 +307,10 @@ void encode_queries_i8(const uint8_t* q, int64_t nq, int64_t nq_pad, int64_t dim
 }
 
 void remove_rows_i8(const int64_t* ids, int64_t n, int64_t size, int32_t* rowc,
-                    unsigned long long* newly_removed, hipStream_t stream,
-                    const int32_t* part_pos, int64_t n_part, int32_t* part_rowc)
+                    unsigned long long* newly_removed, const row_places& at, hipStream_t stream)
 {
   if (n == 0) { return; }
-  remove_kernel<<<blocks_for(n), 256, 0, stream>>>(ids, n, size, rowc, newly_removed, part_pos,
-                                                   n_part, part_rowc);
+  remove_kernel<<<blocks_for(n), 256, 0, stream>>>(ids, n, size, rowc, newly_removed, at);
 }
 
 void fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream)

@@ -90,7 +90,38 @@ __global__ void invert_kernel(const int32_t* ids, int64_t n, int32_t* pos)
   }
 }
 
+/** out[i] = i * step. */
+__global__ void strided_kernel(int32_t* out, int64_t n, int64_t step)
+{
+  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (i < n) { out[i] = int32_t(i * step); }
+}
+
+/** out[i] = the stored row of id ids[i]: id_rows[id] below n_listed, else the id itself. */
+__global__ void stored_rows_kernel(const int32_t* ids, int64_t n, const int32_t* id_rows,
+                                   int64_t n_listed, int32_t* out)
+{
+  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (i >= n) { return; }
+  const int32_t id = ids[i];
+  out[i]           = id < n_listed ? id_rows[id] : id;
+}
+
 }  // namespace
+
+void strided_ids(int32_t* out, int64_t n, int64_t step, hipStream_t stream)
+{
+  if (n == 0) { return; }
+  strided_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(out, n, step);
+}
+
+void stored_rows(const int32_t* ids, int64_t n, const int32_t* id_rows, int64_t n_listed,
+                 int32_t* out, hipStream_t stream)
+{
+  if (n == 0) { return; }
+  stored_rows_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(ids, n, id_rows, n_listed,
+                                                                    out);
+}
 
 size_t sort_by_label_temp_bytes(int64_t n)
 {

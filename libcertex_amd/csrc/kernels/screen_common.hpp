@@ -110,6 +110,8 @@ __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
 /** Filter test of a pair (query q of the batch, stored row). */
 __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
 {
+  if (f.kind == 0) { return true; }
+  row = listed_id(f, row);
   switch (f.kind) {
     case 1: return (f.words[row >> 5] >> (row & 31)) & 1u;
     case 2: {
@@ -324,7 +326,9 @@ __device__ __forceinline__ void anchor_tile_fine(const typename R::acc_t (&col)[
       }
     }
     if (live && first < w.n_scan) {
-      const int64_t e = q * a.n_groups + a.grp_base + first / kFineGroup;
+      const int64_t orow = a.out_row != nullptr ? int64_t(a.out_row[q]) : q;
+      const int64_t ocol = a.out_col != nullptr ? int64_t(a.out_col[q]) : a.grp_base;
+      const int64_t e    = orow * a.n_groups + ocol + first / kFineGroup;
       gmax[e]         = m;
       if constexpr (R::kArgmax) { a.grow[e] = row; }
     }

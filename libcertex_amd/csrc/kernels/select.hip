@@ -130,6 +130,8 @@ __device__ inline double key_score(uint64_t k)
 
 __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
 {
+  if (f.kind == 0) { return true; }
+  row = listed_id(f, row);
   switch (f.kind) {
     case 1: return (f.words[row >> 5] >> (row & 31)) & 1u;
     case 2: {
@@ -235,22 +237,29 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a)
     const int room  = kBuf - have;
     const int64_t m = n_cand - c0 < room ? n_cand - c0 : room;
     for (int64_t e = tid; e < m; e += kThreads) {
+      // the candidate's stored row (or partition row), then its id
       uint32_t r;
       bool live;
+      const int8_t* base = a.codes;
       if (a.all_rows) {
         r    = uint32_t(c0 + e);
         live = a.rowc[r] != kDeadRow && keeps(a.filter, q, r);
       } else {
         r    = cand[c0 + e];
-        r    = (a.part_ids != nullptr && r < a.n_part) ? uint32_t(a.part_ids[r]) : r;
         live = true;
       }
+      uint32_t id;
+      if (!a.all_rows && a.part_ids != nullptr && r < a.n_part) {
+        base = a.part_codes;
+        id   = uint32_t(a.part_ids[r]);
+      } else {
+        id = listed_id(a.filter, r);
+      }
       if (live) {
-        const double s =
-          int_score(qv, a.codes + int64_t(r) * a.row_bytes, a.dim, bias, a.metric);
+        const double s = int_score(qv, base + int64_t(r) * a.row_bytes, a.dim, bias, a.metric);
         const int slot = have + atomicAdd(&fill, 1);
         key[slot]      = score_key(s);
-        rid[slot]      = r;
+        rid[slot]      = id;
       }
     }
     c0 += m;
@@ -516,7 +525,9 @@ __global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_arg
     const int slot = atomicAdd(&cnt, 1);
     if (slot < cap) {
       const uint32_t row = r[e];
-      rid[slot] = (a.part_ids != nullptr && row < a.n_part) ? uint32_t(a.part_ids[row]) : row;
+      rid[slot]          = (a.part_ids != nullptr && row < a.n_part) ? uint32_t(a.part_ids[row])
+                           : row < a.n_listed                        ? uint32_t(a.row_ids[row])
+                                                                     : row;
     }
   }
   __syncthreads();
@@ -640,7 +651,8 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
   const float* vals    = (a.all_rows || a.cand_vals == nullptr) ? nullptr : a.cand_vals + q * a.cap;
 
   auto to_id = [&](uint32_t r) {
-    return (a.part_ids != nullptr && r < a.n_part) ? uint32_t(a.part_ids[r]) : r;
+    return (a.part_ids != nullptr && r < a.n_part) ? uint32_t(a.part_ids[r])
+                                                   : listed_id(a.filter, r);
   };
   int64_t n_scored = 0;
   auto score       = [&](int from, int to) {
@@ -705,6 +717,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
       if (a.all_rows) {
         r    = uint32_t(idx);
         take = a.rowc[r] != -INFINITY && keeps(a.filter, q, r);
+        r    = listed_id(a.filter, r);
       } else {
         r    = to_id(cand[idx]);
         take = !ordered || (~fkey(vals[idx]) > tk &&

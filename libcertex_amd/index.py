@@ -177,6 +177,13 @@ class _Core:
         return self._get("cuvsCertexIndexGetPartitioned", ctypes.c_int64)
 
     @property
+    def lists(self):
+        """(number of k-means lists, vectors they cover)."""
+        n, m = ctypes.c_int32(), ctypes.c_int64()
+        C.check(C.lib().cuvsCertexIndexGetLists(self.h, ctypes.byref(n), ctypes.byref(m)))
+        return n.value, m.value
+
+    @property
     def dtype(self):
         d = self.h.contents.dtype
         return {(C.kDLFloat, 32): "float32", (C.kDLFloat, 16): "float16", (C.kDLInt, 8): "int8", (C.kDLUInt, 8): "uint8"}[
@@ -373,6 +380,7 @@ class Index:
             "dtype": None if c is None else c.dtype,
             "storage": self.storage,
             "ntotal": self.ntotal,
+            "n_lists": 0 if c is None else c.lists[0],
         }
 
 
