@@ -249,8 +249,10 @@ def bench_config5(args):
     """Config 5: exact 10-NN, L2, 1,000,000,000 x 128 uint8 (the config 2 mixture, 128 GB of codes
     resident in HBM), 10,000 queries; while the timed searches run, another thread extends the
     index by 1,000,000 rows and removes 1,000,000 random ids. Afterwards 16 queries are checked
-    against a GPU fp64 brute force over the live set (exact for 8-bit data). The k-means lists of
-    the config only order the scan in the reference (a speed option); they are not built here."""
+    against a GPU fp64 brute force over the live set (exact for 8-bit data). The config's 4,096
+    k-means lists (a speed option: the rows stored in list order, each query's nearest lists probed
+    first) need the whole base in one build: it is generated into host memory (128 GB) and built
+    from there; --lists 0 builds by chunks without lists instead."""
     import threading
 
     import libcertex_amd as certex
@@ -264,9 +266,24 @@ def bench_config5(args):
     def rows(i, m):  # chunk i of the base, regenerated on demand (seed 100 + i); the new rows: i = -1
         return mixture_u8(m, d, 1000, centres, 100 + i if i >= 0 else 99, dev)
 
-    idx = certex.Index(d, metric="l2", capacity=n + n_new)
-    for c in range(0, n, chunk):
-        idx.add(rows(c // chunk, min(chunk, n - c)))
+    n_lists = 4096 if args.lists < 0 else args.lists
+    idx = certex.Index(d, metric="l2", capacity=n + n_new, n_lists=n_lists)
+    t_build = time.perf_counter()
+    if n_lists > 0:
+        X = torch.empty((n, d), dtype=torch.uint8)  # host memory: the base for one build
+        for c in range(0, n, chunk):
+            X[c : c + min(chunk, n - c)] = rows(c // chunk, min(chunk, n - c)).cpu()
+            if (c // chunk) % 10 == 9:
+                print(f"# generated {c + chunk} rows", file=sys.stderr, flush=True)
+        t_build = time.perf_counter()
+        idx.add(X)
+        del X
+    else:
+        for c in range(0, n, chunk):
+            idx.add(rows(c // chunk, min(chunk, n - c)))
+    torch.cuda.synchronize()
+    t_build = time.perf_counter() - t_build
+    print(f"# built {n} rows with {n_lists} lists in {t_build:.1f} s", file=sys.stderr, flush=True)
     Q = mixture_u8(nq, d, 1000, centres, 3, dev)
     new = rows(-1, n_new)
     gone = torch.randint(0, n, (n_gone,), generator=torch.Generator(device=dev).manual_seed(4), device=dev)
@@ -274,7 +291,7 @@ def bench_config5(args):
     batch = args.batch or 10_000
 
     def step():
-        return idx.search(Q, k=k, batch=batch)
+        return idx.search(Q, k=k, batch=batch, probe_lists=args.probe)
 
     errors = []
 
@@ -340,6 +357,9 @@ def bench_config5(args):
         "config": {
             "workload": f"config 5: exact {k}-NN, L2, base {n} x {d} uint8, {nq} queries, +{n_new} rows and "
             f"-{n_gone} random ids during the timed searches",
+            "n_lists": n_lists,
+            "probe_lists": args.probe if n_lists else 0,
+            "build_s": round(t_build, 1),
             "phase_ms_per_step": {p: round(ms[i] / args.steps, 4) for i, p in enumerate(PHASES)},
             "ids_equal_to_brute_force_16_queries": agree,
         },
@@ -368,6 +388,8 @@ def main():
     ap.add_argument("--batch", type=int, default=0)
     ap.add_argument("--cpu-queries", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--lists", type=int, default=-1, help="k-means lists (default: the config's; 0: none)")
+    ap.add_argument("--probe", type=int, default=2, help="lists probed per query")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -403,12 +425,15 @@ def main():
     Q = mixture_u8(nq, d, 1000, centres, 3, dev)
     torch.cuda.synchronize()
 
-    idx = certex.Index(d, metric="l2")
+    n_lists = max(0, args.lists)
+    idx = certex.Index(d, metric="l2", n_lists=n_lists)
+    t_build = time.perf_counter()
     idx.add(X)
     torch.cuda.synchronize()
+    t_build = time.perf_counter() - t_build
 
     def step():
-        return idx.search(Q, k=k, batch=args.batch)
+        return idx.search(Q, k=k, batch=args.batch, probe_lists=args.probe)
 
     for _ in range(args.warmup):
         step()
@@ -483,6 +508,9 @@ def main():
             "k": k,
             "batch": args.batch,
             "anchor_stride": 16,
+            "n_lists": n_lists,
+            "probe_lists": args.probe if n_lists else 0,
+            "build_s": round(t_build, 2),
             "screen": "int8 MFMA (exact), re-rank fp64",
             "phase_ms_per_step": phase_ms,
             "survivors_per_query": round(st.survivors / max(1, st.queries), 2),

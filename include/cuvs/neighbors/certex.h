@@ -158,7 +158,10 @@ CUVS_EXPORT cuvsError_t cuvsCertexIndexGetPartitioned(cuvsCertexIndex_t index,
 CUVS_EXPORT cuvsError_t cuvsCertexIndexGetLists(cuvsCertexIndex_t index,
                                                 int32_t* n_lists,
                                                 int64_t* n_listed);
-/** Grow the capacity to at least `capacity` rows (core.cpp reserve). */
+/**
+ * Grow the capacity to at least `capacity` rows (core.cpp reserve). On a handle that holds no
+ * index yet, the next cuvsCertexBuild allocates that capacity (this build's addition).
+ */
 CUVS_EXPORT cuvsError_t cuvsCertexReserve(cuvsResources_t res,
                                           int64_t capacity,
                                           cuvsCertexIndex_t index);

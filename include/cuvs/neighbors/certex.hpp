@@ -65,6 +65,9 @@ struct index_params {
   int64_t kmeans_sample              = 1000000;
   bool local_projections             = false;
   bool int8_rows                     = false;
+  /** Rows allocated by the build (0: the dataset's); this build's addition. Later additions up
+   * to it need no reallocation, which briefly holds two copies of the stored rows. */
+  int64_t capacity = 0;
 };
 
 /** Parameters of a search (reference certex.hpp:96-107). */

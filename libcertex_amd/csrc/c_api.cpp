@@ -9,6 +9,8 @@
 #include <cstring>
 #include <exception>
 #include <fstream>
+#include <map>
+#include <mutex>
 #include <string>
 
 namespace {
@@ -241,10 +243,27 @@ cuvsError_t cuvsCertexIndexCreate(cuvsCertexIndex_t* index)
   return translate([=] { *index = new cuvsCertexIndex{}; });
 }
 
+namespace {
+// capacities reserved on handles that hold no index yet: the next build allocates them
+std::mutex g_pending_mutex;
+std::map<cuvsCertexIndex_t, int64_t> g_pending_capacity;
+
+auto take_pending_capacity(cuvsCertexIndex_t index) -> int64_t
+{
+  std::lock_guard lk(g_pending_mutex);
+  auto it = g_pending_capacity.find(index);
+  if (it == g_pending_capacity.end()) { return 0; }
+  const int64_t c = it->second;
+  g_pending_capacity.erase(it);
+  return c;
+}
+}  // namespace
+
 cuvsError_t cuvsCertexIndexDestroy(cuvsCertexIndex_t index)
 {
   return translate([=] {
     if (index == nullptr) { return; }
+    (void)take_pending_capacity(index);
     if (index->addr != 0) {
       dispatch(index->dtype, [&](auto tag) {
         delete reinterpret_cast<certex::index<decltype(tag)>*>(index->addr);
@@ -277,8 +296,9 @@ cuvsError_t cuvsCertexBuild(cuvsResources_t res,
     certex::expects(index != nullptr && params != nullptr && dataset != nullptr,
                     "certex: NULL argument");
     certex::expects(index->addr == 0, "certex: the index handle already holds an index");
-    auto& r      = res_of(res);
-    const auto p = to_cpp(*params);
+    auto& r    = res_of(res);
+    auto p     = to_cpp(*params);
+    p.capacity = take_pending_capacity(index);
     dispatch(dataset->dl_tensor.dtype, [&](auto tag) {
       using T = decltype(tag);
       auto* out =
@@ -532,6 +552,12 @@ cuvsError_t cuvsCertexIndexGetLists(cuvsCertexIndex_t index, int32_t* n_lists, i
 cuvsError_t cuvsCertexReserve(cuvsResources_t res, int64_t capacity, cuvsCertexIndex_t index)
 {
   return translate([=] {
+    certex::expects(index != nullptr, "certex: NULL argument");
+    if (index->addr == 0) {  // no index yet: the next build allocates the capacity
+      std::lock_guard lk(g_pending_mutex);
+      g_pending_capacity[index] = capacity;
+      return;
+    }
     auto& r = res_of(res);
     dispatch(index->dtype, [&](auto tag) {
       certex::reserve<decltype(tag)>(r, capacity, as_index<decltype(tag)>(*index));

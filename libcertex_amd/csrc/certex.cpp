@@ -475,10 +475,12 @@ struct probe_plan {
   bool enough     = true;  // every query met kProbeRows * k rows
   std::vector<int32_t> pair_q, pair_col;  // per pair, in list order
   std::vector<certex_amd::screen_group> groups;
-  int64_t tiles = 0;
-  int chunk     = 0;
+  int64_t group_steps = 0;  // 0: groups of 4 rows; else groups of group_steps steps
+  int64_t tiles       = 0;
+  int chunk           = 0;
 };
-constexpr int64_t kProbeRows = 16;
+constexpr int64_t kProbeRows       = 16;
+constexpr int64_t kProbeTableBytes = int64_t(256) << 20;
 
 /** Plans the probe from the encoded query rows; false when the index has no lists to probe. */
 bool plan_probe(cuvs::resources const& res, index_state const& st, const void* qrows, int64_t B,
@@ -505,19 +507,43 @@ bool plan_probe(cuvs::resources const& res, index_state const& st, const void* q
   std::vector<int32_t> taken(static_cast<size_t>(B));
   std::vector<int64_t> start(static_cast<size_t>(L) + 1, 0);
   for (int64_t q = 0; q < B; ++q) {
-    int64_t rows = 0, cols = 0;
+    int64_t rows = 0;
     int t        = 0;
     for (; t < pmax; ++t) {
       const int32_t j = h[size_t(q * pmax + t)];
       if (j < 0 || (t >= p && rows >= want)) { break; }
       rows += list_rows(j);
-      cols += (list_rows(j) + certex_amd::kFineGroup - 1) / certex_amd::kFineGroup;
       ++start[size_t(j) + 1];
     }
     taken[size_t(q)] = t;
-    pp.cols          = std::max(pp.cols, cols);
     pp.enough        = pp.enough && rows >= want;
   }
+  // groups of 4 rows while the probe's table stays within kProbeTableBytes, else of g steps (64 g
+  // rows), g a power of two; every query should keep 4 k groups
+  auto list_cols = [&](int32_t j, int64_t g) {
+    return g == 0 ? (list_rows(j) + certex_amd::kFineGroup - 1) / certex_amd::kFineGroup
+                  : (certex_amd::screen_steps(list_rows(j)) + g - 1) / g;
+  };
+  auto widest = [&](int64_t g, int64_t* narrowest) {
+    int64_t most = 0, least = INT64_MAX;
+    for (int64_t q = 0; q < B; ++q) {
+      int64_t c = 0;
+      for (int t = 0; t < taken[size_t(q)]; ++t) { c += list_cols(h[size_t(q * pmax + t)], g); }
+      most  = std::max(most, c);
+      least = std::min(least, c);
+    }
+    *narrowest = least;
+    return most;
+  };
+  const int64_t nq_pad = certex_amd::pad_queries(B);
+  int64_t g = 0, least = 0;
+  pp.cols   = widest(0, &least);
+  while (nq_pad * pp.cols * 4 > kProbeTableBytes) {
+    g       = g == 0 ? 1 : 2 * g;
+    pp.cols = widest(g, &least);
+  }
+  pp.group_steps = g;
+  pp.enough      = pp.enough && least >= 4 * int64_t(k);
   for (int j = 0; j < L; ++j) { start[size_t(j) + 1] += start[size_t(j)]; }
   pp.n_pairs = start[size_t(L)];
   pp.nq_pad  = certex_amd::pad_queries(pp.n_pairs);
@@ -532,7 +558,7 @@ bool plan_probe(cuvs::resources const& res, index_state const& st, const void* q
         const int64_t s   = fill[size_t(j)]++;
         pp.pair_q[size_t(s)]   = int32_t(q);
         pp.pair_col[size_t(s)] = int32_t(col);
-        col += (list_rows(j) + certex_amd::kFineGroup - 1) / certex_amd::kFineGroup;
+        col += list_cols(j, g);
       }
     }
   }
@@ -546,14 +572,15 @@ bool plan_probe(cuvs::resources const& res, index_state const& st, const void* q
   const bool wide     = f16 && st.row_bytes > 256;
   const int qb        = certex_amd::screen_query_block(f16, st.row_bytes, pp.nq_pad);
   const int64_t waves = waves_of(st);
-  pp.chunk = pick_chunk(waves, anchor_chunk_steps(wide, 1), [&](int64_t c) {
+  const int64_t gs    = std::max<int64_t>(1, g);
+  pp.chunk = pick_chunk(waves * gs, anchor_chunk_steps(wide, gs), [&](int64_t c) {
     int64_t t = 0;
-    for (auto const& g : pp.groups) { t += certex_amd::screen_group_tiles(g.nq, g.nx, qb, int(c)); }
+    for (auto const& e : pp.groups) { t += certex_amd::screen_group_tiles(e.nq, e.nx, qb, int(c)); }
     return t;
   });
-  for (auto& g : pp.groups) {
-    g.tile0 = pp.tiles;
-    pp.tiles += certex_amd::screen_group_tiles(g.nq, g.nx, qb, pp.chunk);
+  for (auto& e : pp.groups) {
+    e.tile0 = pp.tiles;
+    pp.tiles += certex_amd::screen_group_tiles(e.nq, e.nx, qb, pp.chunk);
   }
   return true;
 }
@@ -590,8 +617,8 @@ void probe_pass(cuvs::resources const& res, index_state const& st, certex_amd::s
   r.chunk_steps = pp.chunk;
   r.row_stride  = 1;
   r.row_base    = 0;
-  r.fine        = true;
-  r.group_steps = 1;
+  r.fine        = pp.group_steps == 0;
+  r.group_steps = int(std::max<int64_t>(1, pp.group_steps));
   r.grp_base    = 0;
   r.n_groups    = row_len;
   r.out_row     = d_q;
@@ -1291,7 +1318,7 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
             "certex: integer vectors of more than 256 coordinates are not supported by this build");
     st.row_bytes = certex_amd::int_row_bytes(st.dim);
     st.width     = int(st.dim);
-    grow(res, st, dataset.rows);
+    grow(res, st, std::max(dataset.rows, params.capacity));
     append_int(res, st, reinterpret_cast<const uint8_t*>(dataset.data), dataset.rows,
                dataset.on_device, 0);
     res.sync();
@@ -1311,7 +1338,7 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
   st.normalize       = st.metric == metric_kind::cosine;
   // fp32 accumulation of halves + 1 terms; a factor 2 covers truncating accumulation
   st.gamma = 2.0 * double(st.halves + 1) * std::ldexp(1.0, -24);
-  grow(res, st, dataset.rows);
+  grow(res, st, std::max(dataset.rows, params.capacity));
   const int64_t n = dataset.rows;
   const auto t    = elem_of(st.type);
   // the vectors, then the center (mean; none for inner products) and the scale alpha that puts

@@ -153,8 +153,8 @@ struct screen_args {
   // fine groups: a group is 4 consecutive anchors (column grp_base + scan index / 4) instead of
   // group_steps steps, for searches whose k is large next to the number of anchor steps
   bool fine = false;
-  // fine groups of the list probe: query q of the launch writes its groups to row out_row[q] of the
-  // table, from column out_col[q] on (null: row q, column grp_base)
+  // list probe: query q of the launch writes its groups to row out_row[q] of the table, from column
+  // out_col[q] on (null: row q, column grp_base)
   const int32_t* out_row = nullptr;
   const int32_t* out_col = nullptr;
 };

@@ -247,11 +247,11 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     if constexpr (ANCHORS) {
       // end of an anchor group (group_steps steps, aligned to the wave's range)
       if (!a.fine && ((s + 1) % a.group_steps == 0 || s + 1 == n_steps)) {
-        const int64_t grp = a.grp_base + s / a.group_steps;
         for (int e = lane; e < QB; e += 64) {
           if (q0 + e < w.q_end) {
-            gmax[(q0 + e) * a.n_groups + grp] = gml[wave * QB + e];
-            if constexpr (ARGMX) { a.grow[(q0 + e) * a.n_groups + grp] = gmr[wave * QB + e]; }
+            const int64_t t = table_entry(a, q0 + e, s / a.group_steps);
+            gmax[t]         = gml[wave * QB + e];
+            if constexpr (ARGMX) { a.grow[t] = gmr[wave * QB + e]; }
           }
           gml[wave * QB + e] = R::lowest();
           if constexpr (ARGMX) { gmr[wave * QB + e] = 0xffffffffu; }

@@ -107,6 +107,17 @@ __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
   return w;
 }
 
+/**
+ * Group table entry of group `col` of the pass for launch query q: row q from column grp_base, or
+ * (list probe) row out_row[q] from column out_col[q].
+ */
+__device__ inline int64_t table_entry(const screen_args& a, int64_t q, int64_t col)
+{
+  const int64_t row  = a.out_row != nullptr ? int64_t(a.out_row[q]) : q;
+  const int64_t base = a.out_col != nullptr ? int64_t(a.out_col[q]) : a.grp_base;
+  return row * a.n_groups + base + col;
+}
+
 /** Filter test of a pair (query q of the batch, stored row). */
 __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
 {
@@ -326,9 +337,7 @@ __device__ __forceinline__ void anchor_tile_fine(const typename R::acc_t (&col)[
       }
     }
     if (live && first < w.n_scan) {
-      const int64_t orow = a.out_row != nullptr ? int64_t(a.out_row[q]) : q;
-      const int64_t ocol = a.out_col != nullptr ? int64_t(a.out_col[q]) : a.grp_base;
-      const int64_t e    = orow * a.n_groups + ocol + first / kFineGroup;
+      const int64_t e = table_entry(a, q, first / kFineGroup);
       gmax[e]         = m;
       if constexpr (R::kArgmax) { a.grow[e] = row; }
     }

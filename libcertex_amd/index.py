@@ -274,14 +274,14 @@ class Index:
                     p.contents.n_lists = int(self.n_lists)
                     p.contents.local_projections = bool(self.local_projections)
                     p.contents.int8_rows = bool(self.int8_rows)
+                    if self.capacity is not None and self.capacity > X.shape[0]:
+                        C.check(L.cuvsCertexReserve(res, int(self.capacity), core.h))  # for the build
                     x = C.Borrowed(X)
                     C.check(L.cuvsCertexBuild(res, p, x.ptr, core.h))
                 finally:
                     C.check(L.cuvsCertexIndexParamsDestroy(p))
                 self.core = core
                 n0 = 0
-                if self.capacity is not None and self.capacity > X.shape[0]:
-                    C.check(L.cuvsCertexReserve(res, int(self.capacity), core.h))
             else:
                 n0 = self.core.size
                 x = C.Borrowed(X)

@@ -72,10 +72,11 @@ def test_float_lists(gpu, metric, d, n_lists):
 def test_lists_extend_remove_filter(gpu):
     """Additions after the build follow the lists; removals and filters reach rows in list order."""
     X, Q = data.mixture_u8(50_000, seed=87), data.mixture_u8(400, seed=88)
-    idx = certex.Index(128, n_lists=256)
+    idx = certex.Index(128, n_lists=256, capacity=60_000)
     idx.add(torch.from_numpy(X[:35_000]).cuda())
+    assert idx.core.capacity == 60_000  # allocated by the build
     idx.add(torch.from_numpy(X[35_000:]).cuda())
-    assert idx.core.lists == (256, 35_000)
+    assert idx.core.lists == (256, 35_000) and idx.core.capacity == 60_000
     _, nn = oracle.knn(X, Q, 1, "l2")
     gone = np.unique(np.concatenate([nn[:, 0], np.arange(0, 50_000, 89)]))
     idx.remove(torch.from_numpy(gone))
@@ -161,3 +162,16 @@ def test_probe_lowers_survivors(gpu):
         counts[probe] = st.survivors
         check(X, Q[:64], 10, "l2", D[:64], I[:64])
     assert counts[2] <= counts[0]
+
+
+@pytest.mark.parametrize("metric", ["l2", "cosine"])
+def test_probe_coarse_groups(gpu, metric):
+    """Lists too long for groups of 4 rows in the probe's table: groups of whole steps instead."""
+    if metric == "l2":
+        X, Q = data.mixture_u8(1_000_000, seed=108), data.mixture_u8(1_000, seed=109)
+    else:
+        X, Q = data.powerlaw_unit(800_000, 64, seed=108), data.powerlaw_unit(1_000, 64, seed=109)
+    idx = certex.Index(X.shape[1], metric=metric, n_lists=2)
+    idx.add(torch.from_numpy(X).cuda())
+    D, I = search(idx, Q, 10, probe_lists=1)
+    check(X, Q[:64], 10, metric, D[:64], I[:64])
