@@ -212,12 +212,141 @@ __device__ inline int pow2_at_least(int v)
   return p;
 }
 
+/**
+ * The rank-th smallest (1-based, rank <= n) (key, row) pair of key/row[0, n) in LDS, the pairs
+ * being distinct: an LDS radix select over the eight 8-bit digits of the key and, when several
+ * pairs share the selected key and `with_row`, over the four digits of the row among them. Every
+ * thread of the block calls it and gets the same pair. Scratch: hist[256], wave_tot[4], and three
+ * LDS words.
+ */
+__device__ inline void select_pair(const uint64_t* key, const uint32_t* row, int n, int rank,
+                                   bool with_row, int* hist, int* wave_tot, uint32_t* sel_digit,
+                                   int* sel_rank, int* sel_count, uint64_t* out_key,
+                                   uint32_t* out_row)
+{
+  const int tid   = threadIdx.x;
+  uint64_t prefix = 0, mask = 0;
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    hist[tid] = 0;
+    __syncthreads();
+    for (int e = tid; e < n; e += kThreads) {
+      const uint64_t kk = key[e];
+      if ((kk & mask) == prefix) { atomicAdd(&hist[int(kk >> shift) & 255], 1); }
+    }
+    __syncthreads();
+    const int c    = hist[tid];
+    const int incl = block_scan_incl(c, wave_tot);
+    if (incl - c < rank && rank <= incl) {
+      *sel_digit = uint32_t(tid);
+      *sel_rank  = rank - (incl - c);
+      *sel_count = c;
+    }
+    __syncthreads();
+    prefix |= uint64_t(*sel_digit) << shift;
+    mask |= uint64_t(255) << shift;
+    rank = *sel_rank;
+    __syncthreads();
+  }
+  *out_key = prefix;
+  if (!with_row) { return; }
+  const int same = *sel_count;  // pairs whose key is the selected one
+  uint32_t rp = 0, rm = 0;
+  if (same == 1) {
+    for (int e = tid; e < n; e += kThreads) {
+      if (key[e] == prefix) { *sel_digit = row[e]; }
+    }
+    __syncthreads();
+    rp = *sel_digit;
+    __syncthreads();
+  } else {
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      hist[tid] = 0;
+      __syncthreads();
+      for (int e = tid; e < n; e += kThreads) {
+        const uint32_t rr = row[e];
+        if (key[e] == prefix && (rr & rm) == rp) { atomicAdd(&hist[(rr >> shift) & 255], 1); }
+      }
+      __syncthreads();
+      const int c    = hist[tid];
+      const int incl = block_scan_incl(c, wave_tot);
+      if (incl - c < rank && rank <= incl) {
+        *sel_digit = uint32_t(tid);
+        *sel_rank  = rank - (incl - c);
+      }
+      __syncthreads();
+      rp |= *sel_digit << shift;
+      rm |= 255u << shift;
+      rank = *sel_rank;
+      __syncthreads();
+    }
+  }
+  *out_row = rp;
+}
+
+/** Pair counts up to which a bitonic sort replaces the radix select (fewer barriers). */
+constexpr int kSortBelow = 512;
+
+/**
+ * Keeps the k best (key, row) pairs of [0, n), k <= n <= kBuf, in [0, k) of the same arrays (in
+ * order after a sort of few pairs, else in no particular order), and returns the k-th smallest
+ * key (which bounds the k-th score). With the select, each thread holds its at most
+ * kBuf / kThreads pairs in registers while the kept ones are rewritten.
+ */
+__device__ inline uint64_t keep_k_best(uint64_t* key, uint32_t* row, int n, int k, int* hist,
+                                       int* wave_tot, uint32_t* sel_digit, int* sel_rank,
+                                       int* sel_count, int* fill)
+{
+  constexpr int kPer = kBuf / kThreads;
+  if (n <= kSortBelow) {  // few pairs: one bitonic sort costs fewer barriers than the select
+    const int P = pow2_at_least(n);
+    for (int j = n + threadIdx.x; j < P; j += kThreads) {
+      key[j] = ~0ull;
+      row[j] = ~0u;
+    }
+    __syncthreads();
+    bitonic_sort(key, row, P);
+    return key[k - 1];
+  }
+  __shared__ uint64_t kth_key;
+  __shared__ uint32_t kth_row;
+  select_pair(key, row, n, k, n > k, hist, wave_tot, sel_digit, sel_rank, sel_count, &kth_key,
+              &kth_row);
+  const uint64_t K = kth_key;
+  if (n == k) { return K; }
+  const uint32_t R = kth_row;
+  uint64_t kk[kPer];
+  uint32_t rr[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = threadIdx.x + i * kThreads;
+    kk[i]       = e < n ? key[e] : ~0ull;
+    rr[i]       = e < n ? row[e] : ~0u;
+  }
+  if (threadIdx.x == 0) { *fill = 0; }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = threadIdx.x + i * kThreads;
+    if (e < n && (kk[i] < K || (kk[i] == K && rr[i] <= R))) {
+      const int s = atomicAdd(fill, 1);
+      key[s]      = kk[i];
+      row[s]      = rr[i];
+    }
+  }
+  __syncthreads();
+  return K;
+}
+
 __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a)
 {
   __shared__ uint64_t key[kBuf];
   __shared__ uint32_t rid[kBuf];
   __shared__ __attribute__((aligned(16))) int8_t qv[kMaxIntDim];
   __shared__ int fill;
+  __shared__ int hist[256];
+  __shared__ int wave_tot[4];
+  __shared__ uint32_t sel_digit;
+  __shared__ int sel_rank, sel_count, kept;
 
   const int64_t q = blockIdx.x;
   const int tid   = threadIdx.x;
@@ -267,18 +396,16 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a)
     have += fill;
     __syncthreads();
     if (tid == 0) { fill = 0; }
-    if (c0 < n_cand && have > k) {
-      // keep the k best: sort the buffer and drop the rest
-      const int P = pow2_at_least(have);
-      for (int j = have + tid; j < P; j += kThreads) {
-        key[j] = ~0ull;
-        rid[j] = ~0u;
-      }
-      __syncthreads();
-      bitonic_sort(key, rid, P);
+    if (c0 < n_cand && have > k) {  // keep the k best, drop the rest
+      (void)keep_k_best(key, rid, have, k, hist, wave_tot, &sel_digit, &sel_rank, &sel_count,
+                        &kept);
       have = k;
     }
     __syncthreads();
+  }
+  if (have > k) {
+    (void)keep_k_best(key, rid, have, k, hist, wave_tot, &sel_digit, &sel_rank, &sel_count, &kept);
+    have = k;
   }
   const int P = pow2_at_least(have > 1 ? have : 1);
   for (int j = have + tid; j < P; j += kThreads) {
@@ -533,15 +660,26 @@ __global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_arg
   __syncthreads();
   const int m = cnt < cap ? cnt : cap;
   score_rows_l<L>(qv, a.vectors, a.t, a.dim, a.metric, rid, key, 0, m);
-  const int Pw = pow2_at_least(m);
-  for (int e = m + tid; e < Pw; e += kThreads) {
-    key[e] = ~0ull;
-    rid[e] = ~0u;
-  }
   __syncthreads();
-  bitonic_sort(key, rid, Pw);
+  __shared__ uint64_t kth_key;
+  __shared__ uint32_t kth_row;
+  __shared__ int sel_count;
+  if (m <= kSortBelow) {
+    const int Pw = pow2_at_least(m);
+    for (int e = m + tid; e < Pw; e += kThreads) {
+      key[e] = ~0ull;
+      rid[e] = ~0u;
+    }
+    __syncthreads();
+    bitonic_sort(key, rid, Pw);
+    if (tid == 0) { kth_key = key[a.k - 1]; }
+    __syncthreads();
+  } else {
+    select_pair(key, rid, m, a.k, false, hist, wave_tot, &sel_digit, &sel_rank, &sel_count,
+                &kth_key, &kth_row);
+  }
   if (tid == 0) {
-    const double U  = key_score(key[a.k - 1]);  // k distinct anchors: U bounds the k-th score
+    const double U  = key_score(kth_key);  // k distinct anchors: U bounds the k-th score
     const double aq = a.qscal[3 * q], nw = a.qscal[3 * q + 1], ew = a.qscal[3 * q + 2];
     const double nz = a.maxima[0], ez = a.maxima[1];
     const double cross = ew * nz + nw * ez + ew * ez;  // operand rounding, all pairs
@@ -636,12 +774,11 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
   __shared__ int wave_tot[4];
   __shared__ uint32_t sel_digit;
   __shared__ int sel_rank;
+  __shared__ int sel_count;
   __shared__ int fill;
 
   const int64_t q = blockIdx.x;
   const int tid   = threadIdx.x;
-  const int lane  = tid & 63;
-  const int wave  = tid >> 6;
   const int k     = a.k;
   for (int64_t j = tid; j < a.dim; j += kThreads) { qv[j] = fcoord(a.queries, a.t, q * a.dim + j); }
 
@@ -660,15 +797,13 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
     score_rows_l<L>(qv, a.vectors, a.t, a.dim, a.metric, rid, key, from, to);
   };
   int have = 0;  // entries [0, have) of key / rid are scored
+  // the k best so far move to [0, k) (unordered); the k-th key bounds the k-th score
+  uint64_t kth = ~0ull;
   auto keep_best = [&]() {
-    const int P = pow2_at_least(have > 1 ? have : 1);
-    for (int j = have + tid; j < P; j += kThreads) {
-      key[j] = ~0ull;
-      rid[j] = ~0u;
-    }
-    __syncthreads();
-    bitonic_sort(key, rid, P);
-    have = have < k ? have : k;
+    if (have < k) { return; }
+    kth  = keep_k_best(key, rid, have, k, hist, wave_tot, &sel_digit, &sel_rank, &sel_count,
+                       &fill);
+    have = k;
   };
 
   // phase A: the survivors whose screen value is at least the k-th largest (descending keys)
@@ -694,7 +829,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
       score(0, c);
       __syncthreads();
       keep_best();
-      U                = key_score(key[k - 1]);  // k distinct live rows: bounds the k-th score
+      U                = key_score(kth);  // k distinct live rows: bounds the k-th score
       const double nw  = a.qscal[3 * q + 1], ew = a.qscal[3 * q + 2];
       const double nz  = a.maxima[0], ez = a.maxima[1];
       aq               = a.qscal[3 * q];
@@ -733,10 +868,19 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
     __syncthreads();
     if (have > k && c0 < n_cand) {
       keep_best();
-      if (ordered) { U = key_score(key[k - 1]); }
+      if (ordered) { U = key_score(kth); }
     }
   }
   keep_best();
+  {  // the final k in (score, row) order
+    const int P = pow2_at_least(have > 1 ? have : 1);
+    for (int j = have + tid; j < P; j += kThreads) {
+      key[j] = ~0ull;
+      rid[j] = ~0u;
+    }
+    __syncthreads();
+    bitonic_sort(key, rid, P);
+  }
   for (int j = tid; j < k; j += kThreads) {
     if (j < have) {
       a.best_score[q * k + j] = key_score(key[j]);
