@@ -435,22 +435,70 @@ __device__ inline double fcoord(const void* p, elem t, int64_t i)
 }
 
 /**
+ * Coordinates j .. j + P - 1 of a stored row as doubles (zero past dim): one vector load when
+ * `aligned` (dim a multiple of P, so that j is too), else one coordinate at a time.
+ */
+template <int P>
+__device__ inline void load_coords(const void* vectors, elem t, int64_t row, int64_t dim,
+                                   int64_t j, bool aligned, double (&b)[P])
+{
+  if (aligned) {
+    if (j >= dim) {
+#pragma unroll
+      for (int u = 0; u < P; ++u) { b[u] = 0.0; }
+      return;
+    }
+    const int64_t i = row * dim + j;
+    if (t == elem::f32) {
+      const float* x = static_cast<const float*>(vectors) + i;
+      if constexpr (P == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(x);
+        b[0] = v.x, b[1] = v.y, b[2] = v.z, b[3] = v.w;
+      } else if constexpr (P == 2) {
+        const float2 v = *reinterpret_cast<const float2*>(x);
+        b[0] = v.x, b[1] = v.y;
+      } else {
+        b[0] = x[0];
+      }
+    } else {
+      const _Float16* x = static_cast<const _Float16*>(vectors) + i;
+      if constexpr (P == 4) {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        const h4 v = *reinterpret_cast<const h4*>(x);
+        b[0] = double(v[0]), b[1] = double(v[1]), b[2] = double(v[2]), b[3] = double(v[3]);
+      } else if constexpr (P == 2) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 v = *reinterpret_cast<const h2*>(x);
+        b[0] = double(v[0]), b[1] = double(v[1]);
+      } else {
+        b[0] = double(x[0]);
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int u = 0; u < P; ++u) { b[u] = j + u < dim ? fcoord(vectors, t, row * dim + j + u) : 0.0; }
+}
+
+/**
  * Exact fp64 scores of stored rows against the query whose coordinates sit in LDS as doubles, in
  * the oracle's canonical order: 64 partial sums, partial p accumulating coordinates p, p + 64, ...
  * in increasing order with fused multiply-adds, combined by the xor butterfly (for off = 32 .. 1:
  * p[i] + p[i ^ off]). A row is scored by L lanes of a wave (a slot): lane g of the slot keeps the
- * 64 / L partials g, g + L, ..., so the butterfly levels off >= L combine partials inside a lane
- * and the levels below L cross lanes; every lane of the slot ends with the same bits. With L < 64
- * a wave scores 64 / L rows at once (short rows keep more loads in flight), NR rows per slot.
- * l2: sum (q - x)^2; inner: -sum q x; cosine: -sum q x / sqrt(sum q^2 sum x^2).
+ * P = 64 / L consecutive partials P g .. P g + P - 1, read with one vector load per 64
+ * coordinates; the butterfly levels off >= P pair lane g with lane g ^ (off / P) and the levels
+ * below P combine partials inside a lane, so every lane of the slot ends with the same bits. With
+ * L < 64 a wave scores 64 / L rows at once, NR rows per slot, U 64-coordinate blocks per
+ * iteration. l2: sum (q - x)^2; inner: -sum q x; cosine: -sum q x / sqrt(sum q^2 sum x^2).
  */
 template <int L, int NR>
 __device__ inline void slot_scores(const double* qv, const void* vectors, elem t,
                                    const int64_t (&rows)[NR], int64_t dim, metric_kind metric,
                                    int g, double (&out)[NR])
 {
-  constexpr int P = 64 / L;               // partials per lane
-  constexpr int U = P >= 4 ? 1 : 4 / P;   // 64-coordinate rounds per iteration: 4 loads per row
+  constexpr int P = 64 / L;            // partials per lane
+  constexpr int U = P == 1 ? 4 : 2;    // 64-coordinate blocks per iteration
+  const bool aligned = dim % P == 0;
   double acc[NR][P], xx[NR][P], qq[P];
 #pragma unroll
   for (int u = 0; u < P; ++u) {
@@ -458,24 +506,20 @@ __device__ inline void slot_scores(const double* qv, const void* vectors, elem t
 #pragma unroll
     for (int r = 0; r < NR; ++r) { acc[r][u] = xx[r][u] = 0; }
   }
-  for (int64_t j0 = g; j0 < dim; j0 += 64 * U) {
+  for (int64_t j0 = int64_t(P) * g; j0 < dim; j0 += 64 * U) {
     double b[NR][U][P];
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
 #pragma unroll
       for (int v = 0; v < U; ++v) {
-#pragma unroll
-        for (int u = 0; u < P; ++u) {
-          const int64_t j = j0 + 64 * v + L * u;
-          b[r][v][u]      = j < dim ? fcoord(vectors, t, rows[r] * dim + j) : 0.0;
-        }
+        load_coords<P>(vectors, t, rows[r], dim, j0 + 64 * v, aligned, b[r][v]);
       }
     }
 #pragma unroll
     for (int v = 0; v < U; ++v) {
 #pragma unroll
       for (int u = 0; u < P; ++u) {
-        const int64_t j = j0 + 64 * v + L * u;
+        const int64_t j = j0 + 64 * v + u;
         if (j < dim) {
           const double a = qv[j];
           if (metric == metric_kind::cosine) { qq[u] = fma(a, a, qq[u]); }
@@ -494,7 +538,20 @@ __device__ inline void slot_scores(const double* qv, const void* vectors, elem t
       }
     }
   }
-  // butterfly levels inside the lane (off = 32 .. L): partial u pairs with u ^ (off / L)
+  // butterfly levels off = 32 .. P across the lanes of the slot: partner lane g ^ (off / P)
+#pragma unroll
+  for (int lx = 32 / P; lx >= 1; lx >>= 1) {
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      if (metric == metric_kind::cosine) { qq[u] += __shfl_xor(qq[u], lx); }
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        acc[r][u] += __shfl_xor(acc[r][u], lx);
+        if (metric == metric_kind::cosine) { xx[r][u] += __shfl_xor(xx[r][u], lx); }
+      }
+    }
+  }
+  // levels off < P inside the lane: partial u pairs with u ^ off
 #pragma unroll
   for (int h = P / 2; h >= 1; h >>= 1) {
 #pragma unroll
@@ -506,16 +563,6 @@ __device__ inline void slot_scores(const double* qv, const void* vectors, elem t
         acc[r][u] += acc[r][u | h];
         xx[r][u] += xx[r][u | h];
       }
-    }
-  }
-  // levels off < L across the lanes of the slot
-#pragma unroll
-  for (int off = L / 2; off; off >>= 1) {
-    if (metric == metric_kind::cosine) { qq[0] += __shfl_xor(qq[0], off); }
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      acc[r][0] += __shfl_xor(acc[r][0], off);
-      if (metric == metric_kind::cosine) { xx[r][0] += __shfl_xor(xx[r][0], off); }
     }
   }
 #pragma unroll
