@@ -497,7 +497,7 @@ __device__ inline void slot_scores(const double* qv, const void* vectors, elem t
                                    int g, double (&out)[NR])
 {
   constexpr int P = 64 / L;            // partials per lane
-  constexpr int U = P == 1 ? 4 : 2;    // 64-coordinate blocks per iteration
+  constexpr int U = 2;                 // 64-coordinate blocks per iteration (measured best)
   const bool aligned = dim % P == 0;
   double acc[NR][P], xx[NR][P], qq[P];
 #pragma unroll
@@ -583,7 +583,7 @@ __device__ inline void score_rows_l(const double* qv, const void* vectors, elem 
                                     metric_kind metric, const uint32_t* rid, uint64_t* key,
                                     int from, int to)
 {
-  constexpr int NR   = 2;
+  constexpr int NR   = L == 16 ? 1 : 2;  // rows per slot (measured best at configs 3 and 4)
   constexpr int PER  = (64 / L) * NR;  // rows per wave at a time
   const int lane     = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g        = lane % L;
@@ -613,6 +613,14 @@ __device__ inline void score_rows_l(const double* qv, const void* vectors, elem 
  * the registers and occupancy of its own width).
  */
 inline int score_lanes(int64_t dim) { return dim <= 128 ? 16 : (dim <= 256 ? 32 : 64); }
+
+/** The smallest power of two >= v (host side). */
+inline int pow2_ge(int v)
+{
+  int p = 1;
+  while (p < v) { p <<= 1; }
+  return p;
+}
 
 /** LDS entries of the candidate buffers: a power of two between lo and kBuf covering want. */
 inline int buffer_entries(int want, int lo)
@@ -1004,7 +1012,10 @@ void launch_dyn(K kernel, unsigned blocks, size_t bytes, hipStream_t stream, Arg
 void threshold_f16(const threshold_f_args& a, hipStream_t stream)
 {
   if (a.nq_pad == 0) { return; }
-  const int cap       = buffer_entries(a.per_query, 256);
+  // per_query entries rounded up to 256 (at least 512, the largest bitonic sort here): less LDS
+  // per block than a power of two, so more blocks share a CU
+  const int want      = a.per_query < kBuf ? a.per_query : kBuf;
+  const int cap       = want <= 512 ? 512 : (want + 255) / 256 * 256;
   const size_t bytes  = size_t(cap) * 12 + size_t(a.dim) * 8;
   const unsigned grid = unsigned(a.nq_pad);
   switch (score_lanes(a.dim)) {
@@ -1017,7 +1028,11 @@ void threshold_f16(const threshold_f_args& a, hipStream_t stream)
 void verify_topk_f(const verify_f_args& a, hipStream_t stream)
 {
   if (a.nq == 0) { return; }
-  const int cap       = buffer_entries(4 * a.k, 1024);
+  // room for k scored rows plus a chunk of k / 2 more (at least the final sort's power of two):
+  // less LDS per block than 4 k, so more blocks share a CU
+  int cap = (3 * a.k / 2 + 255) / 256 * 256;
+  cap     = cap > pow2_ge(a.k) ? cap : pow2_ge(a.k);
+  cap     = cap > 1024 ? (cap < kBuf ? cap : kBuf) : 1024;
   const size_t bytes  = size_t(cap) * 12 + size_t(a.dim) * 8;
   const unsigned grid = unsigned(a.nq);
   switch (score_lanes(a.dim)) {
