@@ -337,11 +337,12 @@ __device__ inline uint64_t keep_k_best(uint64_t* key, uint32_t* row, int n, int 
   return K;
 }
 
-__global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a)
+__global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a, int cap)
 {
-  __shared__ uint64_t key[kBuf];
-  __shared__ uint32_t rid[kBuf];
-  __shared__ __attribute__((aligned(16))) int8_t qv[kMaxIntDim];
+  extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
+  auto* key = reinterpret_cast<uint64_t*>(dyn);                    // [cap]
+  auto* rid = reinterpret_cast<uint32_t*>(dyn + size_t(cap) * 8);  // [cap]
+  auto* qv  = reinterpret_cast<int8_t*>(dyn + size_t(cap) * 12);   // [row_bytes]
   __shared__ int fill;
   __shared__ int hist[256];
   __shared__ int wave_tot[4];
@@ -363,7 +364,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a)
   __syncthreads();
   for (int64_t c0 = 0; c0 < n_cand;) {
     // fill the buffer beyond `have` with the next candidates (compacted by an LDS counter)
-    const int room  = kBuf - have;
+    const int room  = cap - have;
     const int64_t m = n_cand - c0 < room ? n_cand - c0 : room;
     for (int64_t e = tid; e < m; e += kThreads) {
       // the candidate's stored row (or partition row), then its id
@@ -994,7 +995,12 @@ void sum_u32(const uint32_t* count, int64_t n, int64_t cap, unsigned long long* 
 void verify_topk_i8(const verify_args& a, hipStream_t stream)
 {
   if (a.nq == 0) { return; }
-  verify_topk_i8_kernel<<<unsigned(a.nq), kThreads, 0, stream>>>(a);
+  // room for 2 k candidates (at least 1,024): small k keeps the block's LDS small, so that many
+  // blocks share a CU
+  int cap = pow2_ge(2 * a.k);
+  cap     = cap > 1024 ? (cap < kBuf ? cap : kBuf) : 1024;
+  const size_t bytes = size_t(cap) * 12 + kMaxIntDim;
+  verify_topk_i8_kernel<<<unsigned(a.nq), kThreads, bytes, stream>>>(a, cap);
 }
 
 /** Launches a kernel with `bytes` of dynamic LDS (raising the kernel's limit when needed). */
