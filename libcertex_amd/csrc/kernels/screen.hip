@@ -89,7 +89,9 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   const int64_t w1      = w0 + quarter < n_steps ? w0 + quarter : n_steps;
 
   if (tid == 0) { n_hits = 0; }
-  for (int e = tid; e < QB * (ROWB / 16); e += 256) {
+  // only the groups that run are staged (a routed group's block is often mostly padding)
+  const int qlive = ng * 64;
+  for (int e = tid; e < qlive * (ROWB / 16); e += 256) {
     const int r = e / (ROWB / 16), c = e % (ROWB / 16);
     v4i v       = {0, 0, 0, 0};
     if (q0 + r < w.q_end) { v = *reinterpret_cast<const v4i*>(a.qcodes + (q0 + r) * ROWB + 16 * c); }
@@ -97,11 +99,12 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   }
   if constexpr (ANCHORS) {
     for (int e = tid; e < 4 * QB; e += 256) {
+      if (e % QB >= qlive) { continue; }
       gml[e] = R::lowest();
       if constexpr (ARGMX) { gmr[e] = 0xffffffffu; }
     }
   } else {
-    for (int e = tid; e < QB; e += 256) {
+    for (int e = tid; e < qlive; e += 256) {
       thl[e] = q0 + e < w.q_end ? theta[q0 + e] : R::keep_none();
     }
   }
