@@ -136,6 +136,11 @@ void grow(cuvs::resources const& res, index_state& st, int64_t cap)
   cuvs::detail::device_buffer codes(size_t(cap) * st.row_bytes);
   cuvs::detail::device_buffer rowc(size_t(cap) * 4);
   cuvs::detail::device_buffer vectors(size_t(cap) * vbytes);
+  const int64_t s       = std::max(1, st.anchor_stride);
+  const int64_t a_cap   = (cap + s - 1) / s;
+  const int64_t a_size  = (st.size + s - 1) / s;
+  cuvs::detail::device_buffer anchor_codes(size_t(a_cap) * st.row_bytes);
+  cuvs::detail::device_buffer anchor_rowc(size_t(a_cap) * 4);
   cuvs::detail::device_buffer labels;
   auto copy = [&](cuvs::detail::device_buffer& dst, cuvs::detail::device_buffer const& src,
                   size_t bytes) {
@@ -146,6 +151,8 @@ void grow(cuvs::resources const& res, index_state& st, int64_t cap)
   copy(codes, st.codes, size_t(st.size) * st.row_bytes);
   copy(rowc, st.rowc, size_t(st.size) * 4);
   copy(vectors, st.vectors, size_t(st.size) * vbytes);
+  copy(anchor_codes, st.anchor_codes, size_t(a_size) * st.row_bytes);
+  copy(anchor_rowc, st.anchor_rowc, size_t(a_size) * 4);
   if (st.has_labels) {
     labels.resize_discard(size_t(cap) * sizeof(int32_t));
     certex_amd::fill_i32(labels.as<int32_t>(), cap, -1, stream);
@@ -156,12 +163,24 @@ void grow(cuvs::resources const& res, index_state& st, int64_t cap)
     // searches in flight on other streams may still read the old arrays
     std::unique_lock lk(st.rw);
     CERTEX_HIP_TRY(hipDeviceSynchronize());
-    st.codes   = std::move(codes);
-    st.rowc    = std::move(rowc);
-    st.vectors = std::move(vectors);
+    st.codes        = std::move(codes);
+    st.rowc         = std::move(rowc);
+    st.vectors      = std::move(vectors);
+    st.anchor_codes = std::move(anchor_codes);
+    st.anchor_rowc  = std::move(anchor_rowc);
     if (st.has_labels) { st.labels = std::move(labels); }
     st.capacity = cap;
   }
+}
+
+/** The anchor copy of the ids [first, end): anchors ceil(first / s) .. ceil(end / s) - 1. */
+void refresh_anchors(cuvs::resources const& res, index_state& st, int64_t first, int64_t end)
+{
+  const int64_t s = std::max(1, st.anchor_stride);
+  certex_amd::gather_anchors(st.codes.p, st.rowc.p, st.row_bytes, s, (first + s - 1) / s,
+                             (end + s - 1) / s, st.row_ids.as<int32_t>(), st.n_listed,
+                             st.anchor_codes.p, st.anchor_rowc.p,
+                             static_cast<hipStream_t>(res.stream()));
 }
 
 /** Encode integer rows [0, n) of a device or host matrix into stored rows first, first + 1, ... */
@@ -214,6 +233,7 @@ void append_float(cuvs::resources const& res, index_state& st, const void* x, in
  */
 struct anchor_plan {
   int stride;
+  int64_t first = 0;  // plain passes: the first anchor of the anchor copy that the pass covers
   int64_t n_anchor, n_groups;
   int64_t group_steps;
   bool fine = false;
@@ -243,11 +263,13 @@ void size_groups(anchor_plan& p, int64_t max_anchors, int64_t tail_anchors, int6
   p.n_groups    = *part_groups + (tail_steps + g - 1) / g;
 }
 
-auto plan_anchors(index_state const& st, int64_t size, int64_t nq_pad, int k) -> anchor_plan
+/** The anchors of the anchor copy from anchor `first` on. */
+auto plan_anchors(index_state const& st, int64_t first, int64_t nq_pad, int k) -> anchor_plan
 {
   anchor_plan p{};
   p.stride   = std::max(1, st.anchor_stride);
-  p.n_anchor = (size + p.stride - 1) / p.stride;
+  p.first    = first;
+  p.n_anchor = (st.size + p.stride - 1) / p.stride - first;
   int64_t part = 0;
   size_groups(p, p.n_anchor, 0, nq_pad, k, &part);
   return p;
@@ -322,7 +344,12 @@ void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan 
   aa.fine        = ap.fine;
   const int64_t unit = waves_of(st) * ap.group_steps;
   const int64_t cap  = anchor_chunk_steps(waves_of(st) == 8, ap.group_steps);
-  if (route == nullptr) {
+  if (route == nullptr) {  // the anchor copy, consecutive rows
+    aa.codes       = st.anchor_codes.as<int8_t>();
+    aa.rowc        = st.anchor_rowc.p;
+    aa.row_stride  = 1;
+    aa.row_base    = ap.first;
+    aa.id_scale    = ap.stride;
     aa.n_scan      = ap.n_anchor;
     aa.chunk_steps = plain_chunk(st, aa.nq, aa.nq_pad, aa.n_scan, unit, cap);
     launch(aa, stream);
@@ -635,8 +662,7 @@ void probe_pass(cuvs::resources const& res, index_state const& st, certex_amd::s
  */
 struct table_plan {
   anchor_plan ap{};
-  bool anchors        = true;
-  int64_t anchor_base = 0;  // the anchors cover the stored rows [anchor_base, size)
+  bool anchors = true;
   probe_plan pp;
   int64_t n_groups = 0;
 };
@@ -653,19 +679,18 @@ auto plan_table(cuvs::resources const& res, index_state const& st, const void* q
   }
   bool probe = st.n_lists > 0 && params.probe_lists > 0 && (fa.kind == 0 || fa.kind == 1) &&
                plan_probe(res, st, qrows, B, k, params.probe_lists, tp.pp) && tp.pp.enough;
-  if (probe) {
-    const int64_t tail = st.size - st.n_listed;
-    tp.anchors         = tail > 0;
-    tp.anchor_base     = st.n_listed;
-    if (tp.anchors) { tp.ap = plan_anchors(st, tail, nq_pad, k); }
+  if (probe) {  // the anchors of the ids added after the lists (the first id >= n_listed on)
+    const int64_t s     = std::max(1, st.anchor_stride);
+    const int64_t first = (st.n_listed + s - 1) / s;
+    tp.anchors          = first < (st.size + s - 1) / s;
+    if (tp.anchors) { tp.ap = plan_anchors(st, first, nq_pad, k); }
     const int64_t acols = tp.anchors ? tp.ap.n_groups : 0;
     probe = nq_pad * (acols + tp.pp.cols) * 4 <= kTableBytes;
   }
   if (!probe) {  // anchors over every row
-    tp.pp          = probe_plan{};
-    tp.anchors     = true;
-    tp.anchor_base = 0;
-    tp.ap          = plan_anchors(st, st.size, nq_pad, k);
+    tp.pp      = probe_plan{};
+    tp.anchors = true;
+    tp.ap      = plan_anchors(st, 0, nq_pad, k);
   }
   tp.n_groups = (tp.anchors ? tp.ap.n_groups : 0) + tp.pp.cols;
   return tp;
@@ -686,10 +711,7 @@ void table_pass(cuvs::resources const& res, index_state const& st, certex_amd::s
                            stream);
     }
   }
-  if (tp.anchors) {
-    aa.row_base = tp.anchor_base;
-    anchor_pass(st, aa, tp.ap, tp.n_groups, route, launch, stream);
-  }
+  if (tp.anchors) { anchor_pass(st, aa, tp.ap, tp.n_groups, route, launch, stream); }
   if (tp.pp.n_pairs > 0) {
     probe_pass(res, st, aa, tp.pp, tp.anchors ? tp.ap.n_groups : 0, tp.n_groups, launch);
   }
@@ -836,6 +858,10 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
     ta.per_query = std::max(params.anchors, k + std::max(k / 4, 16));
     ta.row_ids   = st.row_ids.as<int32_t>();
     ta.n_listed  = st.n_listed;
+    if (route == nullptr && tp.anchors) {  // columns of the anchor copy hold anchor indices
+      ta.id_cols  = tp.ap.n_groups;
+      ta.id_scale = tp.ap.stride;
+    }
     ta.vectors   = st.vectors.p;
     ta.queries   = queries;
     ta.t         = t;
@@ -1326,6 +1352,8 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
       fit_lists(res, st, dataset.rows);
       store_in_lists(res, st, dataset.rows, dataset.data, dataset.on_device);
     }
+    refresh_anchors(res, st, 0, dataset.rows);
+    res.sync();
     st.size = dataset.rows;
     return out;
   }
@@ -1379,6 +1407,8 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
     fit_lists(res, st, n);
     store_in_lists(res, st, n, nullptr, true);
   }
+  refresh_anchors(res, st, 0, n);
+  res.sync();
   st.size = n;
   return out;
 }
@@ -1398,6 +1428,7 @@ void extend(cuvs::resources const& res, matrix_view<const T> new_vectors, index<
   } else {
     append_float(res, st, new_vectors.data, new_vectors.rows, new_vectors.on_device, st.size);
   }
+  refresh_anchors(res, st, st.size, need);  // anchors of the new ids only: searches read the others
   res.sync();
   std::unique_lock publish(st.rw);
   st.size = need;
@@ -1429,6 +1460,9 @@ void remove(cuvs::resources const& res, const int64_t* ids, int64_t n_ids, index
   at.part_pos  = st.label_part.pos.as<int32_t>();
   at.n_part    = st.label_part.n;
   at.part_rowc = st.label_part.rowc.p;
+  at.anchor_rowc   = st.anchor_rowc.p;
+  at.anchor_stride = std::max(1, st.anchor_stride);
+  at.n_anchor      = (st.size + at.anchor_stride - 1) / at.anchor_stride;
   if (is_int(st.type)) {
     certex_amd::remove_rows_i8(ids, n_ids, st.size, st.rowc.as<int32_t>(), counter, at, stream);
   } else {
@@ -1718,6 +1752,8 @@ void deserialize(cuvs::resources const& res, std::string const& filename, index<
     res.sync();
     st.n_lists = L;
   }
+  refresh_anchors(res, st, 0, n);
+  res.sync();
   st.size = n;
 }
 

@@ -182,6 +182,11 @@ struct index_state {
   cuvs::detail::device_buffer rowc;
   cuvs::detail::device_buffer labels;
   cuvs::detail::device_buffer vectors;  // float vectors [capacity, dim]
+  // the anchor copy: anchor j holds the screening row and term of id j * anchor_stride, so that
+  // the anchor pass reads consecutive rows whose groups mix rows from all over the index (the
+  // stored rows may be in list order)
+  cuvs::detail::device_buffer anchor_codes;
+  cuvs::detail::device_buffer anchor_rowc;
   cuvs::detail::device_buffer center;   // double [dim]
   cuvs::detail::device_buffer maxima;   // double [2]: max |fp16(Z)|, max |Z - fp16(Z)|
   double alpha   = 1.0;

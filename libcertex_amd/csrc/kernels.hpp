@@ -71,6 +71,10 @@ struct row_places {
   const int32_t* part_pos = nullptr;
   int64_t n_part          = 0;
   void* part_rowc         = nullptr;
+  // the anchor copy: the ids j * anchor_stride (j < n_anchor) also have the term anchor_rowc[j]
+  void* anchor_rowc     = nullptr;
+  int64_t anchor_stride = 0;
+  int64_t n_anchor      = 0;
 };
 
 /**
@@ -153,6 +157,9 @@ struct screen_args {
   // fine groups: a group is 4 consecutive anchors (column grp_base + scan index / 4) instead of
   // group_steps steps, for searches whose k is large next to the number of anchor steps
   bool fine = false;
+  // a pass over the anchor copy: stored row r of the pass is anchor r, the vector of id
+  // r * id_scale (0: the rows are stored rows of the index)
+  int64_t id_scale = 0;
   // list probe: query q of the launch writes its groups to row out_row[q] of the table, from column
   // out_col[q] on (null: row q, column grp_base)
   const int32_t* out_row = nullptr;
@@ -308,6 +315,8 @@ struct threshold_f_args {
   int64_t n_part          = 0;
   const int32_t* row_ids  = nullptr;  // lists: stored rows below n_listed hold ids row_ids[row]
   int64_t n_listed        = 0;
+  int64_t id_cols         = 0;  // columns [0, id_cols) hold anchors of the anchor copy: id = row * id_scale
+  int64_t id_scale        = 0;
   float* theta;          // [nq_pad]
 };
 /**
@@ -375,6 +384,13 @@ void invert_ids(const int32_t* ids, int64_t n, int32_t* pos, hipStream_t stream)
 
 /** out[i] = i * step for i < n. */
 void strided_ids(int32_t* out, int64_t n, int64_t step, hipStream_t stream);
+/**
+ * The anchor copy: anchors j0 .. j1 - 1 (the ids j * stride) get the codes and row term of their
+ * stored rows (id_rows[id] below n_listed, else the id itself).
+ */
+void gather_anchors(const void* codes, const void* rowc, int row_bytes, int64_t stride, int64_t j0,
+                    int64_t j1, const int32_t* id_rows, int64_t n_listed, void* anchor_codes,
+                    void* anchor_rowc, hipStream_t stream);
 /** out[i] = the stored row of id ids[i] (id_rows[id] for id < n_listed, else id). */
 void stored_rows(const int32_t* ids, int64_t n, const int32_t* id_rows, int64_t n_listed,
                  int32_t* out, hipStream_t stream);

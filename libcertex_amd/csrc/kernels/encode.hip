@@ -78,6 +78,9 @@ __global__ void remove_kernel(const int64_t* ids, int64_t n, int64_t size, int32
   const int64_t id = ids[t];
   if (id < 0 || id >= size) { return; }
   if (id < at.n_part) { static_cast<int32_t*>(at.part_rowc)[at.part_pos[id]] = kDeadRow; }
+  if (at.anchor_stride > 0 && id % at.anchor_stride == 0 && id / at.anchor_stride < at.n_anchor) {
+    static_cast<int32_t*>(at.anchor_rowc)[id / at.anchor_stride] = kDeadRow;
+  }
   if (atomicExch(rowc + stored_row(at, id), kDeadRow) != kDeadRow) { atomicAdd(newly, 1ull); }
 }
 
@@ -241,6 +244,9 @@ __global__ void remove_f_kernel(const int64_t* ids, int64_t n, int64_t size, flo
   const int64_t id = ids[t];
   if (id < 0 || id >= size) { return; }
   if (id < at.n_part) { static_cast<float*>(at.part_rowc)[at.part_pos[id]] = -INFINITY; }
+  if (at.anchor_stride > 0 && id % at.anchor_stride == 0 && id / at.anchor_stride < at.n_anchor) {
+    static_cast<float*>(at.anchor_rowc)[id / at.anchor_stride] = -INFINITY;
+  }
   const int old = atomicExch(reinterpret_cast<int*>(rowc + stored_row(at, id)),
                              __float_as_int(-INFINITY));
   if (old != __float_as_int(-INFINITY)) { atomicAdd(newly, 1ull); }

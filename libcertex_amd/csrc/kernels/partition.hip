@@ -90,6 +90,21 @@ __global__ void invert_kernel(const int32_t* ids, int64_t n, int32_t* pos)
   }
 }
 
+/** Anchor j0 + t / units: one 16-byte unit of its codes (and its term with the first unit). */
+__global__ void gather_anchors_kernel(const int4* codes, const uint32_t* rowc, int64_t units,
+                                      int64_t stride, int64_t j0, int64_t n, const int32_t* id_rows,
+                                      int64_t n_listed, int4* anchor_codes, uint32_t* anchor_rowc)
+{
+  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < n * units;
+       t += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t j   = j0 + t / units, u = t % units;
+    const int64_t id  = j * stride;
+    const int64_t row = id < n_listed ? int64_t(id_rows[id]) : id;
+    anchor_codes[j * units + u] = codes[row * units + u];
+    if (u == 0) { anchor_rowc[j] = rowc[row]; }
+  }
+}
+
 /** out[i] = i * step. */
 __global__ void strided_kernel(int32_t* out, int64_t n, int64_t step)
 {
@@ -108,6 +123,18 @@ __global__ void stored_rows_kernel(const int32_t* ids, int64_t n, const int32_t*
 }
 
 }  // namespace
+
+void gather_anchors(const void* codes, const void* rowc, int row_bytes, int64_t stride, int64_t j0,
+                    int64_t j1, const int32_t* id_rows, int64_t n_listed, void* anchor_codes,
+                    void* anchor_rowc, hipStream_t stream)
+{
+  if (j1 <= j0) { return; }
+  const int64_t units = row_bytes / 16;
+  gather_anchors_kernel<<<blocks_for((j1 - j0) * units), 256, 0, stream>>>(
+    static_cast<const int4*>(codes), static_cast<const uint32_t*>(rowc), units, stride, j0,
+    j1 - j0, id_rows, n_listed, static_cast<int4*>(anchor_codes),
+    static_cast<uint32_t*>(anchor_rowc));
+}
 
 void strided_ids(int32_t* out, int64_t n, int64_t step, hipStream_t stream)
 {

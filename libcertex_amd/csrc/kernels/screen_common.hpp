@@ -118,20 +118,33 @@ __device__ inline int64_t table_entry(const screen_args& a, int64_t q, int64_t c
   return row * a.n_groups + base + col;
 }
 
+/** Filter test of a pair (query q of the batch, id). */
+__device__ inline bool keeps_id(const filter_args& f, int64_t q, uint32_t id)
+{
+  switch (f.kind) {
+    case 1: return (f.words[id >> 5] >> (id & 31)) & 1u;
+    case 2: {
+      const int64_t bit = (f.q0 + q) * f.bitmap_ld + id;
+      return (f.words[bit >> 5] >> (bit & 31)) & 1u;
+    }
+    case 3: return f.row_labels[id] == f.query_labels[f.q0 + q];
+    default: return true;
+  }
+}
+
 /** Filter test of a pair (query q of the batch, stored row). */
 __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
 {
   if (f.kind == 0) { return true; }
-  row = listed_id(f, row);
-  switch (f.kind) {
-    case 1: return (f.words[row >> 5] >> (row & 31)) & 1u;
-    case 2: {
-      const int64_t bit = (f.q0 + q) * f.bitmap_ld + row;
-      return (f.words[bit >> 5] >> (bit & 31)) & 1u;
-    }
-    case 3: return f.row_labels[row] == f.query_labels[f.q0 + q];
-    default: return true;
-  }
+  return keeps_id(f, q, listed_id(f, row));
+}
+
+/** Filter test of a pair (query q, row of the pass): anchors of the anchor copy carry their id. */
+__device__ inline bool keeps_row(const screen_args& a, int64_t q, uint32_t row)
+{
+  if (a.filter.kind == 0) { return true; }
+  return a.id_scale > 0 ? keeps_id(a.filter, q, uint32_t(row * a.id_scale))
+                        : keeps(a.filter, q, row);
 }
 
 /**
@@ -268,7 +281,7 @@ __device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], i
       val_t v = col[bt][r];
       if constexpr (FILT) {
         const int64_t idx = row0 + bt * 16 + r;
-        if (idx < w.n_scan && !keeps(a.filter, q, uint32_t(w.base + idx * a.row_stride))) {
+        if (idx < w.n_scan && !keeps_row(a, q, uint32_t(w.base + idx * a.row_stride))) {
           v = R::lowest();
         }
       }
@@ -327,7 +340,7 @@ __device__ __forceinline__ void anchor_tile_fine(const typename R::acc_t (&col)[
       val_t v           = col[bt][r];
       const int64_t idx = first + r;
       if constexpr (FILT) {
-        if (idx < w.n_scan && !keeps(a.filter, q, uint32_t(w.base + idx * a.row_stride))) {
+        if (idx < w.n_scan && !keeps_row(a, q, uint32_t(w.base + idx * a.row_stride))) {
           v = R::lowest();
         }
       }

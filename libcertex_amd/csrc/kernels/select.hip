@@ -708,7 +708,8 @@ __global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_arg
     const int slot = atomicAdd(&cnt, 1);
     if (slot < cap) {
       const uint32_t row = r[e];
-      rid[slot]          = (a.part_ids != nullptr && row < a.n_part) ? uint32_t(a.part_ids[row])
+      rid[slot]          = e < a.id_cols                             ? uint32_t(row * a.id_scale)
+                           : (a.part_ids != nullptr && row < a.n_part) ? uint32_t(a.part_ids[row])
                            : row < a.n_listed                        ? uint32_t(a.row_ids[row])
                                                                      : row;
     }
