@@ -517,7 +517,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "screen_kernel<2,false,false> (int8 MFMA screen)",
+            "kernel": "screen_kernel<int8_rows,2,512,false,false,8,2> (int8 MFMA screen, 128-row steps)",
             "achieved": round(achieved, 2),
             "peak": P_INT8_TOPS,
             "unit": "TOP/s",

@@ -22,6 +22,9 @@
 // accumulators of a 64-row step and one compare per query tile.
 //
 // Work decomposition:
+// - a step is BT row tiles (16 BT rows) and a query group QT query tiles (16 QT queries): the
+//   int8 screen runs BT = 8 against QT = 2, so that each query fragment read from LDS feeds 8 row
+//   tiles (4 in the other passes, BT = QT = 4), which halves the LDS reads per MFMA;
 // - a workgroup holds QB queries (512, or 128 for small batches) in LDS for its whole life, rows
 //   stored with their 16-byte chunks XOR-swizzled by the row so that the ds_read_b128 of a query
 //   tile is free of bank conflicts;
@@ -48,16 +51,22 @@ __device__ __forceinline__ int slot(int r, int c)
   return KS == 2 ? (c ^ (r & 7)) : (c ^ (r & 15));
 }
 
-template <typename R, int KS, int QB, bool ANCHORS, bool FILT>
+template <typename R, int KS, int QB, bool ANCHORS, bool FILT, int BT, int QT>
 __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 {
   using acc_t  = typename R::acc_t;
   using frag_t = typename R::frag_t;
   using val_t  = typename R::val_t;
   constexpr int ROWB   = 64 * KS;
-  constexpr int NG     = QB / 64;  // groups of 64 queries
+  constexpr int GQ     = 16 * QT;        // queries of a group
+  constexpr int NG     = QB / GQ;        // groups of the workgroup
+  constexpr int TR     = 16 * BT;        // rows of a step
+  constexpr int SPT    = TR / kStepRows; // chunk steps (kStepRows rows) per step
   constexpr bool ARGMX = ANCHORS && R::kArgmax;
   static_assert(NG % 2 == 0, "query groups are processed in pairs");
+  static_assert(BT * 4 <= 32, "a lane's survivor mask of one query tile is 32 bits");
+  static_assert(!ANCHORS || (BT == 4 && QT == 4), "the anchor pass runs 64-row steps");
+  static_assert(!R::kValues || BT == 4, "screen values travel for 16 rows per query tile");
   __shared__ __attribute__((aligned(16))) uint8_t qlds[QB * ROWB];
   __shared__ val_t thl[ANCHORS ? 1 : QB];
   __shared__ val_t gml[ANCHORS ? 4 * QB : 1];
@@ -77,26 +86,23 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 
   const screen_work w = work_of<QB>(a, blockIdx.x);
   if (!w.valid) { return; }
-  const int64_t n_steps = screen_steps(w.n_scan);
+  const int64_t n_steps = screen_steps(w.n_scan);  // chunk steps
   const int64_t q0      = w.q0;
-  // groups of 64 queries holding a live query, rounded up to a pair (the last query block of a
-  // batch or of a routed group is partly padding)
+  // groups holding a live query, rounded up to a pair (the last query block of a batch or of a
+  // routed group is partly padding)
   const int64_t live = w.q_end - q0;
-  const int ng       = live >= QB ? NG : int(((live + 63) / 64 + 1) & ~int64_t(1));
-  // this wave's steps: a contiguous quarter of the chunk (a whole number of anchor groups)
+  const int ng       = live >= QB ? NG : int(((live + GQ - 1) / GQ + 1) & ~int64_t(1));
+  // this wave's chunk steps: a contiguous quarter of the chunk (a whole number of anchor groups,
+  // and of steps: the launcher picks BT > 4 only for chunks of whole steps per wave)
   const int64_t quarter = a.chunk_steps / 4;
   const int64_t w0      = w.chunk * a.chunk_steps + wave * quarter;
   const int64_t w1      = w0 + quarter < n_steps ? w0 + quarter : n_steps;
 
   if (tid == 0) { n_hits = 0; }
   // only the groups that run are staged (a routed group's block is often mostly padding)
-  const int qlive = ng * 64;
-  for (int e = tid; e < qlive * (ROWB / 16); e += 256) {
-    const int r = e / (ROWB / 16), c = e % (ROWB / 16);
-    v4i v       = {0, 0, 0, 0};
-    if (q0 + r < w.q_end) { v = *reinterpret_cast<const v4i*>(a.qcodes + (q0 + r) * ROWB + 16 * c); }
-    *reinterpret_cast<v4i*>(qlds + r * ROWB + 16 * slot<KS>(r, c)) = v;
-  }
+  const int qlive = ng * GQ;
+  stage_queries<ROWB, 256>(a.qcodes, q0, w.q_end, qlive, qlds,
+                           [](int r, int c) { return slot<KS>(r, c); });
   if constexpr (ANCHORS) {
     for (int e = tid; e < 4 * QB; e += 256) {
       if (e % QB >= qlive) { continue; }
@@ -110,22 +116,22 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   }
   __syncthreads();
 
-  frag_t av[4][KS];
-  acc_t cc[4];
+  frag_t av[BT][KS];
+  acc_t cc[BT];
   // the screen reads consecutive rows (stride 1), the anchor pass every row_stride-th
   const int64_t stride = ANCHORS ? a.row_stride : 1;
-  // a step whose 64 rows all exist: straight-line loads, so that the steady-state loop has one
+  // a step whose rows all exist: straight-line loads, so that the steady-state loop has one
   // path for the compiler's wait counts
   auto load_rows = [&](int64_t s) {
 #pragma unroll
-    for (int bt = 0; bt < 4; ++bt) {
-      const int64_t r   = s * kStepRows + bt * 16 + (lane & 15);
+    for (int bt = 0; bt < BT; ++bt) {
+      const int64_t r   = s * TR + bt * 16 + (lane & 15);
       const int8_t* src = a.codes + (w.base + r * stride) * ROWB + (lane >> 4) * 16;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         av[bt][ks] = *reinterpret_cast<const frag_t*>(src + 64 * ks);
       }
-      const int64_t r4 = s * kStepRows + bt * 16 + (lane >> 4) * 4;
+      const int64_t r4 = s * TR + bt * 16 + (lane >> 4) * 4;
       if constexpr (ANCHORS) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) { cc[bt][j] = rowc[w.base + (r4 + j) * stride]; }
@@ -134,28 +140,28 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
       }
     }
   };
-  // the last step of a scan whose length is not a multiple of 64
+  // the last step of a scan whose length is not a multiple of TR
   auto load_rows_tail = [&](int64_t s) {
 #pragma unroll
-    for (int bt = 0; bt < 4; ++bt) {
-      int64_t r = s * kStepRows + bt * 16 + (lane & 15);
+    for (int bt = 0; bt < BT; ++bt) {
+      int64_t r = s * TR + bt * 16 + (lane & 15);
       r         = r < w.n_scan ? r : 0;  // rows past the end read row 0; their term kills them
       const int8_t* src = a.codes + (w.base + r * stride) * ROWB + (lane >> 4) * 16;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         av[bt][ks] = *reinterpret_cast<const frag_t*>(src + 64 * ks);
       }
-      const int64_t r4 = s * kStepRows + bt * 16 + (lane >> 4) * 4;
+      const int64_t r4 = s * TR + bt * 16 + (lane >> 4) * 4;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         cc[bt][j] = r4 + j < w.n_scan ? rowc[w.base + (r4 + j) * stride] : R::dead();
       }
     }
   };
-  auto read_queries = [&](int g, frag_t (&bf)[4][KS], val_t (&th)[4]) {
+  auto read_queries = [&](int g, frag_t (&bf)[QT][KS], val_t (&th)[QT]) {
 #pragma unroll
-    for (int qt = 0; qt < 4; ++qt) {
-      const int r = g * 64 + qt * 16 + (lane & 15);
+    for (int qt = 0; qt < QT; ++qt) {
+      const int r = g * GQ + qt * 16 + (lane & 15);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         bf[qt][ks] = *reinterpret_cast<const frag_t*>(qlds + r * ROWB +
@@ -166,13 +172,13 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   };
 
   int64_t row0 = 0;  // scan index of (bt = 0, r = 0) of this lane in the current step
-  auto group = [&](int g, const frag_t (&bf)[4][KS], const val_t (&th)[4]) {
-    acc_t acc[4][4];
+  auto group = [&](int g, const frag_t (&bf)[QT][KS], const val_t (&th)[QT]) {
+    acc_t acc[BT][QT];
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int bt = 0; bt < 4; ++bt) {
+    for (int bt = 0; bt < BT; ++bt) {
 #pragma unroll
-      for (int qt = 0; qt < 4; ++qt) {
+      for (int qt = 0; qt < QT; ++qt) {
         acc_t t = R::mfma(av[bt][0], bf[qt][0], cc[bt]);
 #pragma unroll
         for (int ks = 1; ks < KS; ++ks) { t = R::mfma(av[bt][ks], bf[qt][ks], t); }
@@ -198,13 +204,13 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
         }
       }
     } else {
-      val_t mq[4];
+      val_t mq[QT];
       bool hit = false;
 #pragma unroll
-      for (int qt = 0; qt < 4; ++qt) {
+      for (int qt = 0; qt < QT; ++qt) {
         val_t m = acc[0][qt][0];
 #pragma unroll
-        for (int bt = 0; bt < 4; ++bt) {
+        for (int bt = 0; bt < BT; ++bt) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) { m = R::vmax(m, acc[bt][qt][r]); }
         }
@@ -213,21 +219,25 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
       }
       if (__builtin_expect(__any(hit), 0)) {
 #pragma unroll
-        for (int qt = 0; qt < 4; ++qt) {
+        for (int qt = 0; qt < QT; ++qt) {
           if (!__any(mq[qt] >= th[qt])) { continue; }
           uint32_t bits = 0;
 #pragma unroll
-          for (int bt = 0; bt < 4; ++bt) {
+          for (int bt = 0; bt < BT; ++bt) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               bits |= uint32_t(acc[bt][qt][r] >= th[qt]) << (bt * 4 + r);
             }
           }
-          const uint32_t qloc = uint32_t(g * 64 + qt * 16 + (lane & 15));
-          const val_t v16[16] = {acc[0][qt][0], acc[0][qt][1], acc[0][qt][2], acc[0][qt][3],
-                                 acc[1][qt][0], acc[1][qt][1], acc[1][qt][2], acc[1][qt][3],
-                                 acc[2][qt][0], acc[2][qt][1], acc[2][qt][2], acc[2][qt][3],
-                                 acc[3][qt][0], acc[3][qt][1], acc[3][qt][2], acc[3][qt][3]};
+          const uint32_t qloc = uint32_t(g * GQ + qt * 16 + (lane & 15));
+          val_t v16[16]       = {};
+          if constexpr (R::kValues) {
+#pragma unroll
+            for (int bt = 0; bt < 4; ++bt) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) { v16[bt * 4 + r] = acc[bt][qt][r]; }
+            }
+          }
           push_hits<FILT, R::kValues>(bits, qloc, w.base + row0, q0, a, hit_q, hit_row, hit_val,
                                       &n_hits, v16);
         }
@@ -235,11 +245,11 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     }
   };
 
-  frag_t b0[4][KS], b1[4][KS];
-  val_t t0[4], t1[4];
+  frag_t b0[QT][KS], b1[QT][KS];
+  val_t t0[QT], t1[QT];
   read_queries(0, b0, t0);
   auto step = [&](int64_t s) {
-    row0 = s * kStepRows + (lane >> 4) * 4;
+    row0 = s * TR + (lane >> 4) * 4;
 #pragma unroll 1
     for (int g = 0; g < ng; g += 2) {
       read_queries(g + 1, b1, t1);
@@ -262,13 +272,16 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
       }
     }
   };
-  const int64_t full = w.n_scan / kStepRows;  // steps whose rows all exist
-  const int64_t w1f  = w1 < full ? w1 : full;
-  for (int64_t s = w0; s < w1f; ++s) {
+  // this wave's steps [s0, s1): its chunk steps hold whole steps
+  const int64_t s0   = w0 / SPT;
+  const int64_t s1   = (w1 + SPT - 1) / SPT;
+  const int64_t full = w.n_scan / TR;  // steps whose rows all exist
+  const int64_t s1f  = s1 < full ? s1 : full;
+  for (int64_t s = s0; s < s1f; ++s) {
     load_rows(s);
     step(s);
   }
-  if (w0 <= full && full < w1) {  // the scan's last, partial step, when it is this wave's
+  if (s0 <= full && full < s1) {  // the scan's last, partial step, when it is this wave's
     load_rows_tail(full);
     step(full);
   }
@@ -296,14 +309,21 @@ void launch(const screen_args& a, hipStream_t stream)
   if (blocks == 0) { return; }
   const dim3 grid{unsigned(blocks)};
   const int ks = a.row_bytes / 64;
+  if constexpr (!ANCHORS && !R::kValues) {
+    // steps of 128 rows when every wave's share of a chunk is whole steps
+    if (ks == 2 && qb_size == 512 && (a.chunk_steps / 4) % 2 == 0) {
+      screen_kernel<R, 2, 512, ANCHORS, FILT, 8, 2><<<grid, 256, 0, stream>>>(a);
+      return;
+    }
+  }
   if (ks == 2 && qb_size == 512) {
-    screen_kernel<R, 2, 512, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
+    screen_kernel<R, 2, 512, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(a);
   } else if (ks == 2) {
-    screen_kernel<R, 2, 128, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
+    screen_kernel<R, 2, 128, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(a);
   } else if (ks == 4 && qb_size == 512) {
-    screen_kernel<R, 4, 512, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
+    screen_kernel<R, 4, 512, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(a);
   } else if (ks == 4) {
-    screen_kernel<R, 4, 128, ANCHORS, FILT><<<grid, 256, 0, stream>>>(a);
+    screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(a);
   }
   // other row widths are rejected by the host before any launch
 }

@@ -2,7 +2,7 @@
 // workgroup resident in LDS; screen_wide.hip: fp16 rows of more than 128 halves, K loop).
 //
 // MFMA tile: operand A holds 16 stored rows and operand B 16 queries, so lane l owns query l % 16
-// and rows 4 (l / 16) + r, r = 0..3, of the tile. A step is 64 rows = 4 row tiles (bt); bit
+// and rows 4 (l / 16) + r, r = 0..3, of the tile. A step is 4 or 8 row tiles (bt); bit
 // bt * 4 + r of a lane's survivor mask marks row row0 + bt * 16 + r, with row0 = the step's first
 // row + 4 (l / 16).
 #pragma once
@@ -108,6 +108,39 @@ __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
 }
 
 /**
+ * Copies the query rows [q0, q0 + n) of qcodes (ROWB bytes each) into LDS, 16-byte chunk c of row
+ * r at slot(r, c); rows at or past q_end are zero. Each thread issues a batch of 8 loads before
+ * their LDS stores, so a batch costs one memory latency (a load-store loop would wait once per
+ * chunk).
+ */
+template <int ROWB, int NT, typename Slot>
+__device__ inline void stage_queries(const int8_t* qcodes, int64_t q0, int64_t q_end, int n,
+                                     uint8_t* lds, Slot slot)
+{
+  constexpr int BATCH = 8;
+  constexpr int CPR   = ROWB / 16;  // chunks per row
+  const int total     = n * CPR;
+  for (int e0 = 0; e0 < total; e0 += NT * BATCH) {
+    v4i v[BATCH];
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+      const int e = e0 + i * NT + int(threadIdx.x);
+      const int r = e / CPR, c = e % CPR;
+      v[i]        = v4i{0, 0, 0, 0};
+      if (e < total && q0 + r < q_end) {
+        v[i] = *reinterpret_cast<const v4i*>(qcodes + (q0 + r) * ROWB + 16 * c);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+      const int e = e0 + i * NT + int(threadIdx.x);
+      const int r = e / CPR, c = e % CPR;
+      if (e < total) { *reinterpret_cast<v4i*>(lds + r * ROWB + 16 * slot(r, c)) = v[i]; }
+    }
+  }
+}
+
+/**
  * Group table entry of group `col` of the pass for launch query q: row q from column grp_base, or
  * (list probe) row out_row[q] from column out_col[q].
  */
@@ -155,9 +188,10 @@ __device__ inline bool keeps_row(const screen_args& a, int64_t q, uint32_t row)
 
 /**
  * Appends the survivors of one 16-query tile of a step to the workgroup's list: `bits` is this
- * lane's survivor mask, `qloc` its query within the workgroup, row0 the stored row of its bit 0. One round per survivor of the
- * busiest lane: ballot, rank by mbcnt, one LDS reservation per round; a full list spills straight
- * into the global bucket. Every lane of the wave must call it.
+ * lane's survivor mask (up to 8 row tiles), `qloc` its query within the workgroup, row0 the
+ * stored row of its bit 0, v the screen values of bits 0..15 (used when VALS). One round per
+ * survivor of the busiest lane: ballot, rank by mbcnt, one LDS reservation per round; a full list
+ * spills straight into the global bucket. Every lane of the wave must call it.
  */
 template <bool FILT, bool VALS, typename V>
 __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t row0, int64_t q0,
