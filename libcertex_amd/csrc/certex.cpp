@@ -606,8 +606,8 @@ bool plan_probe(cuvs::resources const& res, index_state const& st, const void* q
     return t;
   });
   for (auto& e : pp.groups) {
-    e.tile0 = pp.tiles;
-    pp.tiles += certex_amd::screen_group_tiles(e.nq, e.nx, qb, pp.chunk);
+    e.tile0  = certex_amd::screen_group_tile0(pp.tiles, e.nq, qb);
+    pp.tiles = e.tile0 + certex_amd::screen_group_tiles(e.nq, e.nx, qb, pp.chunk);
   }
   return true;
 }
@@ -1007,13 +1007,13 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
     return t;
   });
   for (auto& e : ga) {
-    e.tile0 = route.anchor_tiles;
-    route.anchor_tiles += certex_amd::screen_group_tiles(e.nq, (e.nx + stride - 1) / stride, qb,
-                                                         route.anchor_chunk);
+    e.tile0            = certex_amd::screen_group_tile0(route.anchor_tiles, e.nq, qb);
+    route.anchor_tiles = e.tile0 + certex_amd::screen_group_tiles(
+                                     e.nq, (e.nx + stride - 1) / stride, qb, route.anchor_chunk);
   }
   for (auto& e : gs) {
-    e.tile0 = route.screen_tiles;
-    route.screen_tiles += certex_amd::screen_group_tiles(e.nq, e.nx, qb, route.screen_chunk);
+    e.tile0            = certex_amd::screen_group_tile0(route.screen_tiles, e.nq, qb);
+    route.screen_tiles = e.tile0 + certex_amd::screen_group_tiles(e.nq, e.nx, qb, route.screen_chunk);
   }
   route.n_route = int(gs.size());
 

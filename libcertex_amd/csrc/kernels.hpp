@@ -171,11 +171,25 @@ constexpr int kFineGroup = 4;
 
 /** Queries per workgroup of the screen kernels for a batch padded to nq_pad. */
 int screen_query_block(bool f16, int row_bytes, int64_t nq_pad);
-/** Workgroups of one routed group: query blocks x row chunks. */
+/**
+ * Workgroups of one routed group: query blocks x row chunks. A group of several query blocks
+ * takes its chunks in octets (8 n_qb workgroups per octet, the last octet padded with workgroups
+ * that exit at once), so that the query blocks of one chunk run on one XCD, as in plain launches.
+ */
 inline int64_t screen_group_tiles(int64_t nq, int64_t n_scan, int qb, int chunk_steps)
 {
-  const int64_t steps = (n_scan + kStepRows - 1) / kStepRows;
-  return (nq + qb - 1) / qb * ((steps + chunk_steps - 1) / chunk_steps);
+  const int64_t steps    = (n_scan + kStepRows - 1) / kStepRows;
+  const int64_t n_chunks = (steps + chunk_steps - 1) / chunk_steps;
+  const int64_t n_qb     = (nq + qb - 1) / qb;
+  return n_qb > 1 ? 8 * n_qb * ((n_chunks + 7) / 8) : n_chunks;
+}
+/**
+ * First workgroup of a routed group that follows `tiles` workgroups: a multiple of 8 for a group
+ * of several query blocks (workgroup b runs on XCD b % 8), else `tiles`.
+ */
+inline int64_t screen_group_tile0(int64_t tiles, int64_t nq, int qb)
+{
+  return (nq + qb - 1) / qb > 1 ? (tiles + 7) / 8 * 8 : tiles;
 }
 
 /** Steps of kStepRows rows that cover n_scan rows. */

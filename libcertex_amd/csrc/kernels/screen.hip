@@ -101,8 +101,8 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   if (tid == 0) { n_hits = 0; }
   // only the groups that run are staged (a routed group's block is often mostly padding)
   const int qlive = ng * GQ;
-  stage_queries<ROWB, 256>(a.qcodes, q0, w.q_end, qlive, qlds,
-                           [](int r, int c) { return slot<KS>(r, c); });
+  stage_queries<256>(a.qcodes, ROWB, q0, w.q_end, qlive, qlds,
+                     [](int r, int c) { return slot<KS>(r, c); });
   if constexpr (ANCHORS) {
     for (int e = tid; e < 4 * QB; e += 256) {
       if (e % QB >= qlive) { continue; }

@@ -66,7 +66,9 @@ struct screen_work {
 /**
  * Work of block b. Plain launches: block b runs on XCD b % 8 and the query blocks of one row
  * chunk are consecutive on one XCD (chunk = (b / 8 / n_qb) * 8 + b % 8). Routed launches: the
- * group whose tiles hold b (binary search over tile0), then query block and chunk within it.
+ * group whose tiles hold b (binary search over tile0), then query block and chunk within it, in
+ * the same XCD order when the group has several query blocks (its tile0 is then a multiple of 8,
+ * screen_group_tile0). Blocks past a group's chunks (octet padding, alignment gaps) are invalid.
  */
 template <int QB>
 __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
@@ -97,9 +99,10 @@ __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
   const screen_group g = a.groups[lo];
   const int64_t t      = int64_t(b) - g.tile0;
   const int64_t n_qb   = (g.nq + QB - 1) / QB;
-  w.q0                 = g.q0 + (t % n_qb) * QB;
+  const int64_t i      = t >> 3;
+  w.q0                 = g.q0 + (n_qb > 1 ? i % n_qb : 0) * QB;
   w.q_end              = g.q0 + g.nq;
-  w.chunk              = t / n_qb;
+  w.chunk              = n_qb > 1 ? (i / n_qb) * 8 + (t & 7) : t;
   w.n_scan             = (g.nx + a.row_stride - 1) / a.row_stride;
   w.base               = g.x0;
   const int64_t steps  = screen_steps(w.n_scan);
@@ -109,16 +112,16 @@ __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
 
 /**
  * Copies the query rows [q0, q0 + n) of qcodes (ROWB bytes each) into LDS, 16-byte chunk c of row
- * r at slot(r, c); rows at or past q_end are zero. Each thread issues a batch of 8 loads before
+ * r at slot(r, c); rows at or past q_end are zero. NT threads (the workgroup) take part. Each thread issues a batch of 8 loads before
  * their LDS stores, so a batch costs one memory latency (a load-store loop would wait once per
  * chunk).
  */
-template <int ROWB, int NT, typename Slot>
-__device__ inline void stage_queries(const int8_t* qcodes, int64_t q0, int64_t q_end, int n,
-                                     uint8_t* lds, Slot slot)
+template <int NT, typename Slot>
+__device__ __forceinline__ void stage_queries(const int8_t* qcodes, int ROWB, int64_t q0,
+                                              int64_t q_end, int n, uint8_t* lds, Slot slot)
 {
   constexpr int BATCH = 8;
-  constexpr int CPR   = ROWB / 16;  // chunks per row
+  const int CPR       = ROWB / 16;  // chunks per row
   const int total     = n * CPR;
   for (int e0 = 0; e0 < total; e0 += NT * BATCH) {
     v4i v[BATCH];

@@ -75,13 +75,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
   const int64_t w1      = w0 + eighth < n_steps ? w0 + eighth : n_steps;
 
   if (tid == 0) { n_hits = 0; }
-  const int cpr = RB / 16;  // 16-byte chunks per row
-  for (int e = tid; e < QB * cpr; e += 64 * kWideWaves) {
-    const int r = e / cpr, c = e % cpr;
-    v4i v       = {0, 0, 0, 0};
-    if (q0 + r < w.q_end) { v = *reinterpret_cast<const v4i*>(a.qcodes + (q0 + r) * RB + 16 * c); }
-    *reinterpret_cast<v4i*>(qlds + r * RB + 16 * (c ^ (r & 15))) = v;
-  }
+  stage_queries<64 * kWideWaves>(a.qcodes, RB, q0, w.q_end, QB, qlds,
+                                 [](int r, int c) { return c ^ (r & 15); });
   if constexpr (ANCHORS) {
     for (int e = tid; e < kWideWaves * QB; e += 64 * kWideWaves) {
       gml[e] = R::lowest();
