@@ -239,7 +239,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
             }
           }
           push_hits<FILT, R::kValues>(bits, qloc, w.base + row0, q0, a, hit_q, hit_row, hit_val,
-                                      &n_hits, v16);
+                                      &n_hits, uint32_t(kHitCap), v16);
         }
       }
     }
@@ -288,7 +288,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 
   if constexpr (!ANCHORS) {
     __syncthreads();
-    flush_hits<R::kValues>(q0, QB, a, hit_q, hit_row, hit_val, &n_hits,
+    flush_hits<R::kValues>(q0, QB, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(kHitCap),
                            reinterpret_cast<uint32_t*>(qlds));
   }
 }

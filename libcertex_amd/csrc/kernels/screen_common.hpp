@@ -185,22 +185,24 @@ __device__ inline bool keeps_row(const screen_args& a, int64_t q, uint32_t row)
 
 /**
  * LDS survivor list of a workgroup: hit_q / hit_row / hit_val (the screen values, when the rows
- * carry them) of kHitCap entries and the count n_hits, passed as separate pointers (a struct of
- * LDS addresses can end up as a constant initializer, which the backend rejects).
+ * carry them) of `cap` entries (kHitCap, or what the K-loop screen's LDS leaves) and the count
+ * n_hits, passed as separate pointers (a struct of LDS addresses can end up as a constant
+ * initializer, which the backend rejects).
  */
 
 /**
  * Appends the survivors of one 16-query tile of a step to the workgroup's list: `bits` is this
  * lane's survivor mask (up to 8 row tiles), `qloc` its query within the workgroup, row0 the
  * stored row of its bit 0, v the screen values of bits 0..15 (used when VALS). One round per
- * survivor of the busiest lane: ballot, rank by mbcnt, one LDS reservation per round; a full list
- * spills straight into the global bucket. Every lane of the wave must call it.
+ * survivor of the busiest lane: ballot, rank by mbcnt, one LDS reservation per round; once the
+ * list holds `cap` entries, survivors spill straight into the global bucket (one global atomic
+ * per query and round, which waits for its reply). Every lane of the wave must call it.
  */
 template <bool FILT, bool VALS, typename V>
 __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t row0, int64_t q0,
                                           const screen_args& a, uint32_t* hit_q,
                                           uint32_t* hit_row, float* hit_val, uint32_t* n_hits,
-                                          const V (&v)[16])
+                                          uint32_t cap, const V (&v)[16])
 {
   if constexpr (FILT) {
     uint32_t scan = bits;
@@ -232,14 +234,14 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
 #pragma unroll
       for (int t = 0; t < 16; ++t) { val = t == j ? float(v[t]) : val; }
     }
-    if (had && pos < uint32_t(kHitCap)) {
+    if (had && pos < cap) {
       hit_q[pos]   = qloc;
       hit_row[pos] = row;
       if constexpr (VALS) { hit_val[pos] = val; }
     }
     // a full list: straight to the global bucket, one atomic per query of the round (the 4 lanes
     // l, l ^ 16, l ^ 32, l ^ 48 hold the same query)
-    const uint64_t spill = __ballot(had && pos >= uint32_t(kHitCap));
+    const uint64_t spill = __ballot(had && pos >= cap);
     if (spill != 0) {
       const uint64_t same = spill & (0x0001000100010001ull << (lane & 15));
       const int first     = same ? __builtin_ctzll(same) : lane;
@@ -264,16 +266,16 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
  * Flushes the workgroup's LDS survivor list to the per-query buckets (after a barrier, once the
  * queries in LDS are no longer read): each survivor's rank among its query's survivors comes
  * from an LDS counter, then one global atomic per query reserves the query's slots. `scratch`
- * holds qb + kHitCap words of LDS (the query rows' space).
+ * holds qb + cap words of LDS (the query rows' space).
  */
 template <bool VALS>
 __device__ inline void flush_hits(int64_t q0, int qb, const screen_args& a, const uint32_t* hit_q,
                                   const uint32_t* hit_row, const float* hit_val,
-                                  const uint32_t* n_hits, uint32_t* scratch)
+                                  const uint32_t* n_hits, uint32_t cap, uint32_t* scratch)
 {
   uint32_t* cnt     = scratch;       // [qb] survivors per query, then their first slot
-  uint32_t* rank    = scratch + qb;  // [kHitCap]
-  const uint32_t nh = *n_hits < uint32_t(kHitCap) ? *n_hits : uint32_t(kHitCap);
+  uint32_t* rank    = scratch + qb;  // [cap]
+  const uint32_t nh = *n_hits < cap ? *n_hits : cap;
   for (int e = threadIdx.x; e < qb; e += blockDim.x) { cnt[e] = 0; }
   __syncthreads();
   for (uint32_t e = threadIdx.x; e < nh; e += blockDim.x) { rank[e] = atomicAdd(&cnt[hit_q[e]], 1u); }

@@ -22,6 +22,7 @@
 
 #include "screen_common.hpp"
 
+#include <algorithm>
 #include <stdexcept>
 
 namespace certex_amd {
@@ -40,20 +41,21 @@ __device__ __forceinline__ v8h gload(gbytes p)
 }
 
 template <int QT, bool ANCHORS, bool FILT>
-__global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_args a)
+__global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_args a, int hc)
 {
   using R      = f16_rows;
   using acc_t  = v4f;
   using frag_t = v8h;
   constexpr int QB = 16 * QT;
-  extern __shared__ __attribute__((aligned(16))) uint8_t qlds[];  // [QB][H] halves, swizzled
+  // dynamic LDS: the queries [QB][H] halves (swizzled), then the survivor list of hc entries
+  extern __shared__ __attribute__((aligned(16))) uint8_t qlds[];
   __shared__ float thl[ANCHORS ? 1 : QB];
   __shared__ float gml[ANCHORS ? kWideWaves * QB : 1];
   __shared__ uint32_t gmr[ANCHORS ? kWideWaves * QB : 1];
-  __shared__ uint32_t hit_q[ANCHORS ? 1 : kHitCap];
-  __shared__ uint32_t hit_row[ANCHORS ? 1 : kHitCap];
-  __shared__ float hit_val[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t n_hits;
+  uint32_t* hit_q   = reinterpret_cast<uint32_t*>(qlds + QB * a.row_bytes);
+  uint32_t* hit_row = hit_q + hc;
+  float* hit_val    = reinterpret_cast<float*>(hit_row + hc);
 
   const float* rowc  = static_cast<const float*>(a.rowc);
   const float* theta = static_cast<const float*>(a.theta);
@@ -92,22 +94,28 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
 
   frag_t av[2][4][2];  // [buffer][row tile][first / second MFMA of the chunk]
   acc_t cc[4];
-  // Every load of the main loop is unconditional (indices are clamped instead), so that the
-  // compiler's wait counts see one straight path and the prefetches stay in flight.
-  const gbytes codes = (gbytes)a.codes;
-  auto bases = [&](int64_t s, gbytes (&P)[4]) {
+  // Row addresses: the rows of step s start at the uniform address step_base(s); lane l reads
+  // row bt * 16 + (l & 15) of the step (clamped to the pass's last row, whose term is dead past
+  // the end) at a 32-bit offset O[bt]. The loads then take the scalar-base + vector-offset form
+  // and a lane keeps 4 offsets per step instead of 4 pointers (64-bit pointers for this and the
+  // next step pushed the kernel past 256 VGPRs). Every load of the main loop is unconditional,
+  // so that the compiler's wait counts see one straight path and the prefetches stay in flight.
+  const gbytes codes     = (gbytes)a.codes;
+  const int64_t row_step = int64_t(a.row_stride) * RB;  // bytes between consecutive scan rows
+  auto step_base = [&](int64_t s) { return codes + (w.base + s * kStepRows * a.row_stride) * RB; };
+  auto offsets   = [&](int64_t s, uint32_t (&O)[4]) {
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
       int64_t r = s * kStepRows + bt * 16 + (lane & 15);
-      r         = r < w.n_scan ? r : 0;  // rows past the end read row 0; their term kills them
-      P[bt]     = codes + (w.base + r * a.row_stride) * RB + (lane >> 4) * 32;
+      r         = r < w.n_scan ? r : w.n_scan - 1;
+      O[bt]     = uint32_t((r - s * kStepRows) * row_step + (lane >> 4) * 32);
     }
   };
-  auto load_chunk = [&](const gbytes (&P)[4], int64_t off, frag_t (&A)[4][2]) {
+  auto load_chunk = [&](gbytes base, const uint32_t (&O)[4], int64_t off, frag_t (&A)[4][2]) {
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
-      A[bt][0] = gload(P[bt] + off);
-      A[bt][1] = gload(P[bt] + off + 16);
+      A[bt][0] = gload(base + off + O[bt]);
+      A[bt][1] = gload(base + off + 16 + O[bt]);
     }
   };
   auto load_terms = [&](int64_t s) {
@@ -143,34 +151,42 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
     __builtin_amdgcn_s_setprio(0);
   };
 
-  gbytes P[4];
-  gbytes PN[4];
-  bases(w0, P);
-  load_chunk(P, 0, av[0]);
-  load_terms(w0);
+  // offsets(s) needs a step that exists (s * 64 < n_scan): a wave whose share of the last chunk
+  // is empty (w0 >= n_steps) loads nothing
+  gbytes B = step_base(w0);
+  uint32_t O[4] = {0, 0, 0, 0};
+  if (w0 < w1) {
+    offsets(w0, O);
+    load_chunk(B, O, 0, av[0]);
+    load_terms(w0);
+  }
   for (int64_t s = w0; s < w1; ++s) {
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = cc[bt]; }
     }
-    // the next step's rows and terms (the last step reloads its own)
-    const int64_t sn = s + 1 < w1 ? s + 1 : s;
-    bases(sn, PN);
-    load_terms(sn);
 #pragma unroll 1
-    for (int c = 0; c < NC; c += 2) {
-      load_chunk(P, int64_t(c + 1) * 128, av[1]);
+    for (int c = 0; c < NC - 2; c += 2) {
+      load_chunk(B, O, int64_t(c + 1) * 128, av[1]);
       compute(c, av[0]);
-      const bool last = c + 2 >= NC;
-      gbytes Q[4];
-#pragma unroll
-      for (int bt = 0; bt < 4; ++bt) { Q[bt] = last ? PN[bt] : P[bt] + int64_t(c + 2) * 128; }
-      load_chunk(Q, 0, av[0]);
+      load_chunk(B, O, int64_t(c + 2) * 128, av[0]);
       compute(c + 1, av[1]);
     }
+    // the last two chunks; the next step's terms and first chunk are loaded meanwhile (the last
+    // step reloads its own); loaded this late, they hold no registers during the K loop
+    const int64_t sn = s + 1 < w1 ? s + 1 : s;
+    const gbytes BN  = step_base(sn);
+    uint32_t ON[4];
+    offsets(sn, ON);
+    load_terms(sn);
+    load_chunk(B, O, int64_t(NC - 1) * 128, av[1]);
+    compute(NC - 2, av[0]);
+    load_chunk(BN, ON, 0, av[0]);
+    compute(NC - 1, av[1]);
+    B = BN;
 #pragma unroll
-    for (int bt = 0; bt < 4; ++bt) { P[bt] = PN[bt]; }
+    for (int bt = 0; bt < 4; ++bt) { O[bt] = ON[bt]; }
 
     const int64_t row0 = s * kStepRows + (lane >> 4) * 4;
     if constexpr (ANCHORS) {
@@ -233,7 +249,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
                                  acc[2][qt][0], acc[2][qt][1], acc[2][qt][2], acc[2][qt][3],
                                  acc[3][qt][0], acc[3][qt][1], acc[3][qt][2], acc[3][qt][3]};
           push_hits<FILT, true>(bits, uint32_t(qt * 16 + (lane & 15)), w.base + row0, q0, a, hit_q,
-                                hit_row, hit_val, &n_hits, v16);
+                                hit_row, hit_val, &n_hits, uint32_t(hc), v16);
         }
       }
     }
@@ -241,13 +257,13 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
 
   if constexpr (!ANCHORS) {
     __syncthreads();
-    flush_hits<true>(q0, QB, a, hit_q, hit_row, hit_val, &n_hits,
+    flush_hits<true>(q0, QB, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(hc),
                      reinterpret_cast<uint32_t*>(qlds));
   }
 }
 
 template <int QT, bool ANCHORS, bool FILT>
-void launch_qt(const screen_args& a, dim3 grid, size_t lds, hipStream_t stream)
+void launch_qt(const screen_args& a, dim3 grid, size_t lds, int hc, hipStream_t stream)
 {
   auto* k = &screen_wide_kernel<QT, ANCHORS, FILT>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(k),
@@ -255,29 +271,55 @@ void launch_qt(const screen_args& a, dim3 grid, size_t lds, hipStream_t stream)
     (void)hipGetLastError();
     throw std::runtime_error("certex: the wide screen cannot reserve its LDS");
   }
-  k<<<grid, 64 * kWideWaves, lds, stream>>>(a);
+  k<<<grid, 64 * kWideWaves, lds, stream>>>(a, hc);
 }
 
-/**
- * Query tiles of a workgroup for rows of `row_bytes`: the largest of 6, 4, 2 whose queries and
- * static arrays fit the LDS of a workgroup (0: none fits).
- */
-int wide_query_tiles(int row_bytes)
+/** LDS bytes a workgroup may use. */
+int max_lds()
 {
-  static const int max_lds = [] {
-    int dev = 0, v = 0;
+  static const int v = [] {
+    int dev = 0, r = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) {
+        hipDeviceGetAttribute(&r, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) {
       (void)hipGetLastError();
       return 65536;
     }
-    return v;
+    return r;
   }();
-  const int fixed = 3 * kHitCap * 4 + 16 * 6 * 4 + 512;  // static arrays of the screen, margin
-  for (int qt : {6, 4, 2}) {
-    if (16 * qt * row_bytes + fixed <= max_lds) { return qt; }
+  return v;
+}
+
+/** Static LDS of the screen (thresholds, count) and a margin. */
+constexpr int kWideFixed = 16 * 6 * 4 + 512;
+/** Survivor list entries of the K-loop screen: at least this many, or the query tiles shrink. */
+constexpr int kWideMinHits = 4096;
+/** Most survivor list entries (hit_q, hit_row, hit_val: 12 bytes each). */
+constexpr int kWideMaxHits = 8192;
+
+/**
+ * Query tiles of a workgroup for rows of `row_bytes`: the largest of 6, 4, 2 whose queries and a
+ * survivor list of kWideMinHits entries fit the LDS, else the largest whose queries and 1,024
+ * entries fit (0: none fits). A survivor that finds the list full waits for a global atomic, so
+ * the fp16 screens, which keep thousands of rows per query, trade query tiles for list entries.
+ */
+int wide_query_tiles(int row_bytes)
+{
+  for (int min_hits : {kWideMinHits, kHitCap}) {
+    for (int qt : {6, 4, 2}) {
+      if (16 * qt * row_bytes + 12 * min_hits + kWideFixed <= max_lds()) { return qt; }
+    }
   }
   return 0;
+}
+
+/** Survivor list entries of a screen workgroup of qt query tiles over rows of row_bytes. */
+int wide_hit_cap(int qt, int row_bytes)
+{
+  const int qbytes = 16 * qt * row_bytes;
+  int hc           = (max_lds() - qbytes - kWideFixed) / 12;
+  hc               = std::min(hc, kWideMaxHits);
+  hc               = std::min(hc, qbytes / 4 - 16 * qt);  // the flush ranks in the queries' space
+  return hc / 64 * 64;
 }
 
 template <bool ANCHORS, bool FILT>
@@ -297,11 +339,12 @@ void launch(const screen_args& a, hipStream_t stream)
   }
   if (blocks == 0) { return; }
   const dim3 grid{unsigned(blocks)};
-  const size_t lds = size_t(qb) * size_t(a.row_bytes);
+  const int hc     = ANCHORS ? 0 : wide_hit_cap(qt, a.row_bytes);
+  const size_t lds = size_t(qb) * size_t(a.row_bytes) + size_t(hc) * 12;
   switch (qt) {
-    case 6: launch_qt<6, ANCHORS, FILT>(a, grid, lds, stream); break;
-    case 4: launch_qt<4, ANCHORS, FILT>(a, grid, lds, stream); break;
-    default: launch_qt<2, ANCHORS, FILT>(a, grid, lds, stream); break;
+    case 6: launch_qt<6, ANCHORS, FILT>(a, grid, lds, hc, stream); break;
+    case 4: launch_qt<4, ANCHORS, FILT>(a, grid, lds, hc, stream); break;
+    default: launch_qt<2, ANCHORS, FILT>(a, grid, lds, hc, stream); break;
   }
 }
 
