@@ -90,6 +90,34 @@ def timed_steps(step, steps, warmup):
 PHASES = ("anchors", "threshold", "screen", "verify_topk")
 
 
+def hbm_roofline(kernel, bytes_per_launch, ms_per_launch, what):
+    """Roofline of an HBM-bound phase: algorithmic bytes per launch (stated in `what`) over the
+    launch's average duration (HIP events of the library), against 8 TB/s."""
+    gbs = bytes_per_launch / (ms_per_launch / 1000.0) / 1e9 if ms_per_launch > 0 else 0.0
+    return {"bound": "hbm", "kernel": kernel, "achieved": round(gbs, 1), "peak": HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_GBS, 4), "bytes_per_launch": int(bytes_per_launch),
+            "avg_launch_ms": round(ms_per_launch, 4), "bytes": what}
+
+
+def float_phase_rooflines(ms, launches, steps, st, nq, d, k, elem):
+    """Threshold and verify rooflines of a float search (one batch per step): the threshold scores
+    max(128, k + max(k / 4, 16)) anchors per query exactly; the verify reads every survivor's
+    bucket entry (row and screen value) and the vectors of the rows it scores."""
+    per_query = max(128, k + max(k // 4, 16))
+    t_ms = ms[1] / max(1, launches[1])
+    v_ms = ms[3] / max(1, launches[3])
+    per_launch = max(1, launches[3] // steps)
+    return {
+        "threshold": hbm_roofline(
+            "threshold_f16_kernel", nq * (per_query * d * elem + d * elem) / per_launch, t_ms,
+            f"{per_query} anchor vectors of {d} x {elem} B and the query, per query"),
+        "verify_topk": hbm_roofline(
+            "verify_topk_f_kernel", (st.verified * d * elem + st.survivors * 8 + nq * d * elem) / per_launch,
+            v_ms, f"{st.verified / max(1, st.queries):.1f} scored vectors of {d} x {elem} B and "
+            f"{st.survivors / max(1, st.queries):.1f} bucket entries of 8 B, per query"),
+    }
+
+
 def bench_config3(args):
     """Config 3: exact 100-NN, cosine, 1,000,000 x 768 fp32 power-law embeddings, 10,000 queries,
     one of 16 labels per vector and per query (label-filtered search), fp16 MFMA screen."""
@@ -158,6 +186,7 @@ def bench_config3(args):
             "launches_per_step": {p: launches[i] // args.steps for i, p in enumerate(PHASES)},
             "survivors_per_query": round(st.survivors / max(1, st.queries), 2),
             "verified_per_query": round(st.verified / max(1, st.queries), 2),
+            "phase_rooflines": float_phase_rooflines(ms, launches, args.steps, st, nq, d, k, 4),
         },
         "roofline": {
             "bound": "mfma", "kernel": "screen_wide_kernel (fp16 MFMA screen, label-routed)",
@@ -219,6 +248,12 @@ def bench_config4(args):
                "sample": f"first {cq} queries of query head 0 against KV head 0 ({head0.shape[0]} keys), "
                f"exhaustive fp64 (oracle/oracle.c, OpenMP), {tc:.1f} s; ids equal to the GPU's: {agree}"}
     n_q = H * m
+    # screen roofline per step: every query against the keys of its KV head (fp16 rows of 128
+    # halves); the cache holds n + 256 (warmup + i + 1) keys per head in timed step i
+    keys_avg = n + grow * (args.warmup + (args.steps + 1) / 2.0)
+    flops_per_step = 2.0 * n_q * keys_avg * ((d + 127) // 128 * 128)
+    screen_ms_step = ms[2] / args.steps
+    achieved = flops_per_step / (screen_ms_step / 1000.0) / 1e12
     return {
         "metric": "exact top-2048 attention queries/sec, 8 KV heads x 131k keys, GQA 4:1, 1 MI355X",
         "value": round(n_q / (ms_step / 1000.0), 1),
@@ -239,8 +274,14 @@ def bench_config4(args):
             "launches_per_step": {p: launches[i] // args.steps for i, p in enumerate(PHASES)},
             "survivors_per_query": round(st.survivors / max(1, st.queries), 2),
             "verified_per_query": round(st.verified / max(1, st.queries), 2),
+            "phase_rooflines": float_phase_rooflines(ms, launches, args.steps, st, n_q, d, k, 4),
         },
-        "roofline": None,
+        "roofline": {
+            "bound": "mfma", "kernel": "screen_kernel<f16_rows,4,...> (fp16 MFMA screen, label-routed, + tail)",
+            "achieved": round(achieved, 2), "peak": P_FP16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / P_FP16_TFLOPS, 4), "traffic": None,
+            "screen_ms_per_step": round(screen_ms_step, 4), "flops_per_step": flops_per_step,
+        },
         "cpu_baseline": cpu,
     }
 
@@ -509,6 +550,13 @@ def main():
 
     # roofline of the screen: 2 N d int8 ops per query
     screen_ms = ms[2] / max(1, launches[2])
+    # the verify: every survivor's bucket entry (4 B) and its 128-byte code row, and the queries
+    row_b = 128 if d <= 128 else 256
+    verify_bytes = (st.survivors * (4 + row_b) + nq * row_b) / max(1, launches[3] // args.steps)
+    phase_roofs = {"verify_topk": hbm_roofline(
+        "verify_topk_i8_kernel", verify_bytes, ms[3] / max(1, launches[3]),
+        f"{st.survivors / max(1, st.queries):.1f} survivors x ({row_b} B code row + 4 B bucket "
+        f"entry), plus the query, per query")}
     batches = (nq + args.batch - 1) // args.batch
     ops_per_launch = 2.0 * n * d * nq / batches
     achieved = ops_per_launch / (screen_ms / 1000.0) / 1e12
@@ -565,6 +613,7 @@ def main():
             "screen": "int8 MFMA (exact), re-rank fp64",
             "phase_ms_per_step": phase_ms,
             "survivors_per_query": round(st.survivors / max(1, st.queries), 2),
+            "phase_rooflines": phase_roofs,
         },
         "roofline": {
             "bound": "mfma",
