@@ -438,18 +438,32 @@ bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, 
         rs.get(cuvs::detail::ws_vals, size_t(nq_pad) * size_t(cap) * 4));
       sa.cand_vals = *vals;
     }
+    // survivors past the workgroups' LDS lists: a pool of the buckets' size, once a search of
+    // these resources has overflowed them (the first such search took the slower atomic path)
+    sa.spill_q = nullptr, sa.spill_row = nullptr, sa.spill_val = nullptr, sa.spill_pool = 0;
+    if (rs.spill_pool) {
+      const size_t e = size_t(nq_pad) * size_t(cap);
+      sa.spill_q     = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_spill_q, e * 4));
+      sa.spill_row   = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_spill_row, e * 4));
+      if (vals != nullptr) {
+        sa.spill_val = static_cast<float*>(rs.get(cuvs::detail::ws_spill_val, e * 4));
+      }
+      sa.spill_pool = int64_t(e);
+    }
     certex_amd::fill_u32(count, nq_pad, 0, stream);
+    certex_amd::fill_u32(small, 2, 0, stream);
+    sa.spill_need  = small + 1;
     sa.n_scan      = size;
     sa.row_stride  = 1;
     sa.cand_count  = count;
     sa.cand_rows   = rows;
     sa.cap         = cap;
     timed(2, stream, [&] { screen(sa, stream); });
-    certex_amd::fill_u32(small, 1, 0, stream);
     certex_amd::max_u32(count, B, small, stream);
-    CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, small, 4, hipMemcpyDeviceToHost, stream));
+    CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, small, 8, hipMemcpyDeviceToHost, stream));
     CERTEX_HIP_TRY(hipStreamSynchronize(stream));
-    const int64_t worst = *static_cast<uint32_t*>(rs.host_small);
+    const int64_t worst = static_cast<uint32_t*>(rs.host_small)[0];
+    if (static_cast<uint32_t*>(rs.host_small)[1] > 0) { rs.spill_pool = true; }
     if (worst <= cap) { return true; }
     if (worst > all_rows_above) { return false; }
     int64_t c = 1024;

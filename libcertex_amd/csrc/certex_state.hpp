@@ -106,6 +106,9 @@ enum ws_slot : int {
   ws_probe_dist,  // list probe: center distances of the batch's queries
   ws_probe,       // list probe: nearest lists, pair tables
   ws_probe_rows,  // list probe: the query row of every (query, list) pair
+  ws_spill_q,     // screen spill pool: query of each entry
+  ws_spill_row,   // screen spill pool: row of each entry
+  ws_spill_val,   // screen spill pool: screen value of each entry (fp16 rows)
   ws_n_slots
 };
 
@@ -114,6 +117,7 @@ struct resources_state {
   hipStream_t stream  = nullptr;
   bool owns_stream    = false;
   int64_t bucket_cap  = 1024;  // survivors per query kept by the last searches
+  bool spill_pool     = false;  // a screen's LDS survivor lists overflowed: provide a spill pool
   device_buffer slots[ws_n_slots];
   void* host_small    = nullptr;  // pinned host words for counters read back by the host
 

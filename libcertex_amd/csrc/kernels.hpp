@@ -147,6 +147,18 @@ struct screen_args {
   uint32_t* cand_rows  = nullptr;  // [nq_pad, cap]
   float* cand_vals     = nullptr;  // [nq_pad, cap] screen values (fp16 rows only)
   int64_t cap          = 0;
+  // screen: survivors past a workgroup's LDS list go to the workgroup's own region of a pool of
+  // spill_pool entries (query within the block, row, and screen value for fp16 rows), with plain
+  // stores; the launcher splits the pool evenly among its workgroups (spill_cap each), and the
+  // workgroup's flush moves its region into the buckets. Survivors past the region take a global
+  // atomic each. spill_need (device word) gets the largest count past the LDS list of any
+  // workgroup, so that the host knows whether to provide a pool.
+  uint32_t* spill_q   = nullptr;
+  uint32_t* spill_row = nullptr;
+  float* spill_val    = nullptr;
+  int64_t spill_pool  = 0;
+  int64_t spill_cap   = 0;  // set by the launcher
+  uint32_t* spill_need = nullptr;
   // anchors: group maxima [nq_pad, n_groups] (int32 or float), a group = group_steps steps;
   // fp16 rows also record the stored row of each maximum in grow
   void* gmax       = nullptr;

@@ -308,22 +308,24 @@ void launch(const screen_args& a, hipStream_t stream)
   }
   if (blocks == 0) { return; }
   const dim3 grid{unsigned(blocks)};
-  const int ks = a.row_bytes / 64;
+  const int ks  = a.row_bytes / 64;
+  screen_args b = a;
+  b.spill_cap   = !ANCHORS && a.spill_q != nullptr ? a.spill_pool / blocks : 0;
   if constexpr (!ANCHORS && !R::kValues) {
     // steps of 128 rows when every wave's share of a chunk is whole steps
     if (ks == 2 && qb_size == 512 && (a.chunk_steps / 4) % 2 == 0) {
-      screen_kernel<R, 2, 512, ANCHORS, FILT, 8, 2><<<grid, 256, 0, stream>>>(a);
+      screen_kernel<R, 2, 512, ANCHORS, FILT, 8, 2><<<grid, 256, 0, stream>>>(b);
       return;
     }
   }
   if (ks == 2 && qb_size == 512) {
-    screen_kernel<R, 2, 512, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(a);
+    screen_kernel<R, 2, 512, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(b);
   } else if (ks == 2) {
-    screen_kernel<R, 2, 128, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(a);
+    screen_kernel<R, 2, 128, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(b);
   } else if (ks == 4 && qb_size == 512) {
-    screen_kernel<R, 4, 512, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(a);
+    screen_kernel<R, 4, 512, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(b);
   } else if (ks == 4) {
-    screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(a);
+    screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(b);
   }
   // other row widths are rejected by the host before any launch
 }

@@ -239,9 +239,17 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
       hit_row[pos] = row;
       if constexpr (VALS) { hit_val[pos] = val; }
     }
-    // a full list: straight to the global bucket, one atomic per query of the round (the 4 lanes
-    // l, l ^ 16, l ^ 32, l ^ 48 hold the same query)
-    const uint64_t spill = __ballot(had && pos >= cap);
+    // a full list: the workgroup's spill region (plain stores, moved to the buckets by the flush)
+    const uint32_t spos = pos - cap;
+    if (had && pos >= cap && spos < a.spill_cap) {
+      const int64_t e = int64_t(blockIdx.x) * a.spill_cap + spos;
+      a.spill_q[e]    = qloc;
+      a.spill_row[e]  = row;
+      if constexpr (VALS) { a.spill_val[e] = val; }
+    }
+    // a full region too: straight to the global bucket, one atomic per query of the round (the 4
+    // lanes l, l ^ 16, l ^ 32, l ^ 48 hold the same query)
+    const uint64_t spill = __ballot(had && pos >= cap && spos >= a.spill_cap);
     if (spill != 0) {
       const uint64_t same = spill & (0x0001000100010001ull << (lane & 15));
       const int first     = same ? __builtin_ctzll(same) : lane;
@@ -263,22 +271,34 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
 }
 
 /**
- * Flushes the workgroup's LDS survivor list to the per-query buckets (after a barrier, once the
- * queries in LDS are no longer read): each survivor's rank among its query's survivors comes
- * from an LDS counter, then one global atomic per query reserves the query's slots. `scratch`
- * holds qb + cap words of LDS (the query rows' space).
+ * Flushes the workgroup's survivors to the per-query buckets (after a barrier, once the queries in
+ * LDS are no longer read): the LDS list (the first `cap` of n_hits) and the entries of its spill
+ * region past it. Each LDS entry's rank among its query's survivors comes from an LDS counter
+ * (cnt), the region's entries follow the query's LDS entries (cursor cur); then one global atomic
+ * per query reserves the query's slots. `scratch` holds 2 qb + cap words of LDS (the query rows'
+ * space). Records the workgroup's count past the LDS list in spill_need.
  */
 template <bool VALS>
 __device__ inline void flush_hits(int64_t q0, int qb, const screen_args& a, const uint32_t* hit_q,
                                   const uint32_t* hit_row, const float* hit_val,
                                   const uint32_t* n_hits, uint32_t cap, uint32_t* scratch)
 {
-  uint32_t* cnt     = scratch;       // [qb] survivors per query, then their first slot
-  uint32_t* rank    = scratch + qb;  // [cap]
-  const uint32_t nh = *n_hits < cap ? *n_hits : cap;
+  uint32_t* cnt        = scratch;           // [qb] survivors per query, then their first slot
+  uint32_t* cur        = scratch + qb;      // [qb] the next rank of a region entry per query
+  uint32_t* rank       = scratch + 2 * qb;  // [cap]
+  const uint32_t total = *n_hits;
+  const uint32_t nh    = total < cap ? total : cap;
+  const uint32_t past  = total - nh;
+  const uint32_t ns    = past < uint32_t(a.spill_cap) ? past : uint32_t(a.spill_cap);
+  const int64_t region = int64_t(blockIdx.x) * a.spill_cap;
+  if (threadIdx.x == 0 && past > 0 && a.spill_need != nullptr) { atomicMax(a.spill_need, past); }
   for (int e = threadIdx.x; e < qb; e += blockDim.x) { cnt[e] = 0; }
   __syncthreads();
   for (uint32_t e = threadIdx.x; e < nh; e += blockDim.x) { rank[e] = atomicAdd(&cnt[hit_q[e]], 1u); }
+  __syncthreads();
+  for (int e = threadIdx.x; e < qb; e += blockDim.x) { cur[e] = cnt[e]; }
+  __syncthreads();
+  for (uint32_t e = threadIdx.x; e < ns; e += blockDim.x) { atomicAdd(&cnt[a.spill_q[region + e]], 1u); }
   __syncthreads();
   for (int e = threadIdx.x; e < qb; e += blockDim.x) {
     if (cnt[e] != 0) { cnt[e] = atomicAdd(a.cand_count + q0 + e, cnt[e]); }
@@ -291,6 +311,15 @@ __device__ inline void flush_hits(int64_t q0, int qb, const screen_args& a, cons
       const int64_t q                = q0 + ql;
       a.cand_rows[q * a.cap + bslot] = hit_row[e];
       if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = hit_val[e]; }
+    }
+  }
+  for (uint32_t e = threadIdx.x; e < ns; e += blockDim.x) {
+    const uint32_t ql    = a.spill_q[region + e];
+    const uint32_t bslot = cnt[ql] + atomicAdd(&cur[ql], 1u);
+    if (bslot < a.cap) {
+      const int64_t q                = q0 + ql;
+      a.cand_rows[q * a.cap + bslot] = a.spill_row[region + e];
+      if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = a.spill_val[region + e]; }
     }
   }
 }

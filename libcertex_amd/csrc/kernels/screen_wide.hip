@@ -318,7 +318,7 @@ int wide_hit_cap(int qt, int row_bytes)
   const int qbytes = 16 * qt * row_bytes;
   int hc           = (max_lds() - qbytes - kWideFixed) / 12;
   hc               = std::min(hc, kWideMaxHits);
-  hc               = std::min(hc, qbytes / 4 - 16 * qt);  // the flush ranks in the queries' space
+  hc               = std::min(hc, qbytes / 4 - 32 * qt);  // the flush ranks in the queries' space
   return hc / 64 * 64;
 }
 
@@ -341,10 +341,12 @@ void launch(const screen_args& a, hipStream_t stream)
   const dim3 grid{unsigned(blocks)};
   const int hc     = ANCHORS ? 0 : wide_hit_cap(qt, a.row_bytes);
   const size_t lds = size_t(qb) * size_t(a.row_bytes) + size_t(hc) * 12;
+  screen_args b    = a;
+  b.spill_cap      = !ANCHORS && a.spill_q != nullptr ? a.spill_pool / blocks : 0;
   switch (qt) {
-    case 6: launch_qt<6, ANCHORS, FILT>(a, grid, lds, hc, stream); break;
-    case 4: launch_qt<4, ANCHORS, FILT>(a, grid, lds, hc, stream); break;
-    default: launch_qt<2, ANCHORS, FILT>(a, grid, lds, hc, stream); break;
+    case 6: launch_qt<6, ANCHORS, FILT>(b, grid, lds, hc, stream); break;
+    case 4: launch_qt<4, ANCHORS, FILT>(b, grid, lds, hc, stream); break;
+    default: launch_qt<2, ANCHORS, FILT>(b, grid, lds, hc, stream); break;
   }
 }
 

@@ -179,3 +179,21 @@ def test_config3_shape_labels(gpu):
     D, I = idx.search(torch.from_numpy(Q).cuda(), k=100, batch=384, labels=torch.from_numpy(lq))
     torch.cuda.synchronize()
     check(X, Q, 100, "cosine", D.cpu().numpy(), I.cpu().numpy(), row_labels=lx, query_labels=lq)
+
+
+@pytest.mark.parametrize("d", [100, 300])
+def test_many_survivors_spill(gpu, d):
+    """A quarter of the rows repeat one row near every query (narrow screen at d = 100, K-loop
+    screen at d = 300): thousands of survivors per workgroup pass its LDS list. Repeated searches
+    (the later ones with the spill pool) must equal the oracle."""
+    rng = np.random.default_rng(d)
+    X = rng.standard_normal((30_000, d)).astype(np.float32)
+    base = rng.standard_normal(d).astype(np.float32)
+    X[rng.permutation(30_000)[:7_500]] = base
+    Q = (base + 0.01 * rng.standard_normal((48, d))).astype(np.float32)
+    idx = certex.Index(d, metric="l2")
+    idx.add(torch.from_numpy(X).cuda())
+    for _ in range(3):
+        D, I = idx.search(torch.from_numpy(Q).cuda(), k=50)
+        torch.cuda.synchronize()
+        check(X, Q, 50, "l2", D.cpu().numpy(), I.cpu().numpy())

@@ -184,3 +184,23 @@ def test_c2_shape_subset_parity(gpu):
         best = torch.topk(torch.cat([best, s], 1), 10, dim=1, largest=False).values
     kth = best[:, 9].cpu().numpy()
     np.testing.assert_array_equal(exact[:, 9].cpu().numpy(), kth)
+
+
+def test_many_survivors_spill(gpu):
+    """A quarter of the rows are one repeated row near every query: each screen workgroup keeps
+    thousands of survivors, past its LDS list. The first search of the resources moves them with a
+    global atomic each and asks for a spill pool; the later ones write the workgroups' spill regions.
+    Every search must equal the oracle (ties to the lower id)."""
+    rng = np.random.default_rng(5)
+    X = rng.integers(0, 256, (40_000, 128)).astype(np.uint8)
+    base = rng.integers(0, 256, 128).astype(np.uint8)
+    X[rng.permutation(40_000)[:10_000]] = base
+    Q = np.clip(base.astype(np.int32) + rng.integers(-2, 3, (64, 128)), 0, 255).astype(np.uint8)
+    idx = certex.Index(128, metric="l2")
+    idx.add(torch.from_numpy(X).cuda())
+    s, i = oracle.knn(X, Q, 100, "l2")
+    for _ in range(3):
+        D, I = idx.search(torch.from_numpy(Q).cuda(), k=100)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(I.cpu().numpy(), i)
+        np.testing.assert_array_equal(D.cpu().numpy(), oracle.distances(s, i, "l2"))
