@@ -143,40 +143,48 @@ __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
   }
 }
 
+typedef int v4i_t __attribute__((ext_vector_type(4)));
+
 /**
- * fp64 score of stored integer row `row` against the query codes in LDS: the coordinates in
- * increasing order, accumulated by fused multiply-add (exact for 8-bit integers, where every
- * partial sum is an integer below 2^53). l2: sum (q - x)^2; inner: -sum q x.
+ * Exact score of stored integer row `xrow` (row_bytes bytes, 16-byte aligned) against the query
+ * codes in LDS, in int32. The codes are int8 (uint8 coordinates shifted by -128, bias = 128) and
+ * zero past dim in both. For 8-bit data every fp64 partial sum of the oracle is an exact integer,
+ * so this exact integer converts to the same double:
+ *   l2:    sum (q - x)^2 = |q|^2 + |x|^2 - 2 <q, x>            (at most 255^2 * 256 < 2^31)
+ *   inner: -sum (q + bias)(x + bias) = -(<q, x> + bias (sum q + sum x) + bias^2 dim)
+ * qq = |q|^2 and qs = sum q of the query codes. Each 16-byte load feeds twelve v_dot4_i32_i8.
  */
-__device__ inline double int_score(const int8_t* qv, const int8_t* xrow, int64_t dim, int bias,
-                                   metric_kind metric)
+__device__ inline double int_score(const int8_t* qv, const int8_t* xrow, int row_bytes,
+                                   int64_t dim, int bias, int qq, int qs, metric_kind metric)
 {
-  double acc = 0;
-  int64_t j  = 0;
-  for (; j + 4 <= dim; j += 4) {
-    const int xw = *reinterpret_cast<const int*>(xrow + j);
-    const int qw = *reinterpret_cast<const int*>(qv + j);
+  int qx = 0, xx = 0, xs = 0;
+  for (int j = 0; j < row_bytes; j += 16) {
+    const v4i_t x  = *reinterpret_cast<const v4i_t*>(xrow + j);
+    const v4i_t qw = *reinterpret_cast<const v4i_t*>(qv + j);
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const int xc = int(int8_t(xw >> (8 * b))), qc = int(int8_t(qw >> (8 * b)));
-      if (metric == metric_kind::l2) {
-        const double t = double(qc - xc);
-        acc            = fma(t, t, acc);
-      } else {
-        acc = fma(double(qc + bias), double(xc + bias), acc);
-      }
+      qx = __builtin_amdgcn_sdot4(qw[b], x[b], qx, false);
+      xx = __builtin_amdgcn_sdot4(x[b], x[b], xx, false);
+      xs = __builtin_amdgcn_sdot4(x[b], 0x01010101, xs, false);
     }
   }
-  for (; j < dim; ++j) {
-    const int xc = int(xrow[j]), qc = int(qv[j]);
-    if (metric == metric_kind::l2) {
-      const double t = double(qc - xc);
-      acc            = fma(t, t, acc);
-    } else {
-      acc = fma(double(qc + bias), double(xc + bias), acc);
+  if (metric == metric_kind::l2) { return double(qq + xx - 2 * qx); }
+  return -double(int64_t(qx) + int64_t(bias) * (qs + xs) + int64_t(bias) * bias * dim);
+}
+
+/** |q|^2 and sum q of the query codes in LDS (row_bytes bytes, zero past dim). */
+__device__ inline void query_sums(const int8_t* qv, int row_bytes, int& qq, int& qs)
+{
+  qq = 0;
+  qs = 0;
+  for (int j = 0; j < row_bytes; j += 16) {
+    const v4i_t qw = *reinterpret_cast<const v4i_t*>(qv + j);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      qq = __builtin_amdgcn_sdot4(qw[b], qw[b], qq, false);
+      qs = __builtin_amdgcn_sdot4(qw[b], 0x01010101, qs, false);
     }
   }
-  return metric == metric_kind::l2 ? acc : -acc;
 }
 
 constexpr int kBuf = 4096;  // LDS candidates per query (keys 32 KB + rows 16 KB)
@@ -354,6 +362,9 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a,
   const int k     = a.k;
   for (int j = tid; j < a.row_bytes; j += kThreads) { qv[j] = a.qcodes[q * a.row_bytes + j]; }
   const int bias = a.flip ? 128 : 0;
+  __syncthreads();  // the query codes are in LDS
+  int qq, qs;
+  query_sums(qv, a.row_bytes, qq, qs);
 
   const int64_t n_cand =
     a.all_rows ? a.n_rows : (a.cand_count[q] < a.cap ? int64_t(a.cand_count[q]) : a.cap);
@@ -386,7 +397,8 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a,
         id = listed_id(a.filter, r);
       }
       if (live) {
-        const double s = int_score(qv, base + int64_t(r) * a.row_bytes, a.dim, bias, a.metric);
+        const double s =
+          int_score(qv, base + int64_t(r) * a.row_bytes, a.row_bytes, a.dim, bias, qq, qs, a.metric);
         const int slot = have + atomicAdd(&fill, 1);
         key[slot]      = score_key(s);
         rid[slot]      = id;
