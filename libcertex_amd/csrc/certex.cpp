@@ -971,9 +971,20 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
     sorted(static_cast<size_t>(B));
   CERTEX_HIP_TRY(hipMemcpyAsync(lab.data(), qlabels, size_t(B) * 4, hipMemcpyDeviceToHost, stream));
   CERTEX_HIP_TRY(hipStreamSynchronize(stream));
-  for (int64_t i = 0; i < B; ++i) { order[size_t(i)] = int32_t(i); }
-  std::stable_sort(order.begin(), order.end(),
-                   [&](int32_t a, int32_t b) { return lab[size_t(a)] < lab[size_t(b)]; });
+  // queries in label order, stable: a counting sort when the batch's labels span a small range
+  // (one pass, no comparisons), else a comparison sort
+  const auto [lo_it, hi_it] = std::minmax_element(lab.begin(), lab.end());
+  const int64_t lo = B > 0 ? *lo_it : 0, span = B > 0 ? int64_t(*hi_it) - lo + 1 : 0;
+  if (span <= 4 * B + 1024) {
+    std::vector<int64_t> start(static_cast<size_t>(span) + 1, 0);
+    for (int64_t i = 0; i < B; ++i) { ++start[size_t(lab[size_t(i)] - lo) + 1]; }
+    for (int64_t v = 0; v < span; ++v) { start[size_t(v) + 1] += start[size_t(v)]; }
+    for (int64_t i = 0; i < B; ++i) { order[size_t(start[size_t(lab[size_t(i)] - lo)]++)] = int32_t(i); }
+  } else {
+    for (int64_t i = 0; i < B; ++i) { order[size_t(i)] = int32_t(i); }
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int32_t a, int32_t b) { return lab[size_t(a)] < lab[size_t(b)]; });
+  }
 
   const int64_t nq_pad = certex_amd::pad_queries(B);
   const bool f16       = !is_int(st.type);

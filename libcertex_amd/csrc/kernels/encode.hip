@@ -206,22 +206,49 @@ __global__ void encode_rows_f16_kernel(const void* x, elem t, int64_t n, int64_t
   atomic_max_pos(maxima + 1, sqrt_up(ez, dim));
 }
 
-__global__ void encode_queries_f16_kernel(const void* q, elem t, int64_t nq, int64_t nq_pad,
-                                          int64_t dim, int halves, bool normalize,
-                                          const double* center, double inv_alpha, uint16_t* qrows,
-                                          double* qscal)
+/** Sum of v over the 64 lanes of a wave (xor butterfly: every lane gets the sum). */
+__device__ inline double wave_sum(double v)
 {
-  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
-  if (i >= nq_pad) { return; }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) { v += __shfl_xor(v, off); }
+  return v;
+}
+
+/**
+ * One wave per query, its lanes over the coordinates j = lane, lane + 64, ... (coalesced loads):
+ * qrows[i] = fp16(W) with W = (q / |q| - center) / alpha (q / |q| when normalizing), subnormals
+ * set to 0, zero padded; qscal[3 i ..] = |W|^2 (lowered by 1e-13), |fp16(W)| and |W - fp16(W)|
+ * (raised for the rounding of their sums, sqrt_up). Per-lane fp64 partial sums and a butterfly:
+ * the sums only enter bounds that carry these slacks.
+ */
+__global__ __launch_bounds__(256) void encode_queries_f16_kernel(const void* q, elem t, int64_t nq,
+                                                                 int64_t nq_pad, int64_t dim,
+                                                                 int halves, bool normalize,
+                                                                 const double* center,
+                                                                 double inv_alpha, uint16_t* qrows,
+                                                                 double* qscal)
+{
+  const int64_t i = blockIdx.x * int64_t(blockDim.x / 64) + (threadIdx.x >> 6);
+  const int lane  = threadIdx.x & 63;
+  if (i >= nq_pad) { return; }  // uniform over the wave
   _Float16* dst = reinterpret_cast<_Float16*>(qrows + i * halves);
   if (i >= nq) {
-    for (int j = 0; j < halves; ++j) { dst[j] = _Float16(0.0f); }
-    qscal[3 * i] = qscal[3 * i + 1] = qscal[3 * i + 2] = 0.0;
+    for (int j = lane; j < halves; j += 64) { dst[j] = _Float16(0.0f); }
+    if (lane == 0) { qscal[3 * i] = qscal[3 * i + 1] = qscal[3 * i + 2] = 0.0; }
     return;
   }
-  const double nrm = normalize ? row_norm(q, t, i, dim) : 1.0;
+  double nrm = 1.0;
+  if (normalize) {
+    double s2 = 0;
+    for (int64_t j = lane; j < dim; j += 64) {
+      const double v = coord(q, t, i * dim + j);
+      s2             = fma(v, v, s2);
+    }
+    s2  = wave_sum(s2);
+    nrm = s2 > 0 ? sqrt(s2) : 1.0;
+  }
   double a = 0, nw = 0, ew = 0;
-  for (int64_t j = 0; j < dim; ++j) {
+  for (int64_t j = lane; j < dim; j += 64) {
     const double w   = (coord(q, t, i * dim + j) / nrm - center[j]) * inv_alpha;
     const _Float16 h = to_f16(w);
     const double e   = w - double(h);
@@ -230,10 +257,15 @@ __global__ void encode_queries_f16_kernel(const void* q, elem t, int64_t nq, int
     nw               = fma(double(h), double(h), nw);
     ew               = fma(e, e, ew);
   }
-  for (int64_t j = dim; j < halves; ++j) { dst[j] = _Float16(0.0f); }
-  qscal[3 * i]     = a * (1.0 - 1e-13);
-  qscal[3 * i + 1] = sqrt_up(nw, dim);
-  qscal[3 * i + 2] = sqrt_up(ew, dim);
+  for (int64_t j = dim + lane; j < halves; j += 64) { dst[j] = _Float16(0.0f); }
+  a  = wave_sum(a);
+  nw = wave_sum(nw);
+  ew = wave_sum(ew);
+  if (lane == 0) {
+    qscal[3 * i]     = a * (1.0 - 1e-13);
+    qscal[3 * i + 1] = sqrt_up(nw, dim);
+    qscal[3 * i + 2] = sqrt_up(ew, dim);
+  }
 }
 
 __global__ void remove_f_kernel(const int64_t* ids, int64_t n, int64_t size, float* rowc,
@@ -284,7 +316,8 @@ void encode_queries_f16(const void* q, elem t, int64_t nq, int64_t nq_pad, int64
                         uint16_t* qrows, double* qscal, hipStream_t stream)
 {
   if (nq_pad == 0) { return; }
-  encode_queries_f16_kernel<<<blocks_for(nq_pad), 256, 0, stream>>>(
+  // one wave per query, four per block
+  encode_queries_f16_kernel<<<unsigned((nq_pad + 3) / 4), 256, 0, stream>>>(
     q, t, nq, nq_pad, dim, halves, normalize, center, inv_alpha, qrows, qscal);
 }
 
