@@ -451,46 +451,35 @@ __device__ inline double fcoord(const void* p, elem t, int64_t i)
  * Coordinates j .. j + P - 1 of a stored row as doubles (zero past dim): one vector load when
  * `aligned` (dim a multiple of P, so that j is too), else one coordinate at a time.
  */
-template <int P>
-__device__ inline void load_coords(const void* vectors, elem t, int64_t row, int64_t dim,
-                                   int64_t j, bool aligned, double (&b)[P])
+/**
+ * Coordinates j .. j + P - 1 of stored row `row` as doubles, zero at and past dim. ALIGNED (dim a
+ * multiple of P, so that j is too): one vector load, from a clamped position when j >= dim; else
+ * one coordinate at a time, each from a clamped position. The loads are unconditional, so that a
+ * row's loads are issued together rather than each behind a branch.
+ */
+template <typename T, int P, bool ALIGNED>
+__device__ __forceinline__ void load_coords(const T* x, int64_t row, int64_t dim, int64_t j, double (&b)[P])
 {
-  if (aligned) {
-    if (j >= dim) {
-#pragma unroll
-      for (int u = 0; u < P; ++u) { b[u] = 0.0; }
-      return;
-    }
-    const int64_t i = row * dim + j;
-    if (t == elem::f32) {
-      const float* x = static_cast<const float*>(vectors) + i;
-      if constexpr (P == 4) {
-        const float4 v = *reinterpret_cast<const float4*>(x);
-        b[0] = v.x, b[1] = v.y, b[2] = v.z, b[3] = v.w;
-      } else if constexpr (P == 2) {
-        const float2 v = *reinterpret_cast<const float2*>(x);
-        b[0] = v.x, b[1] = v.y;
-      } else {
-        b[0] = x[0];
-      }
+  if constexpr (ALIGNED) {
+    const bool ok    = j < dim;
+    const T* src     = x + row * dim + (ok ? j : dim - P);
+    if constexpr (P == 1) {
+      const double v = double(src[0]);
+      b[0]           = ok ? v : 0.0;
     } else {
-      const _Float16* x = static_cast<const _Float16*>(vectors) + i;
-      if constexpr (P == 4) {
-        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-        const h4 v = *reinterpret_cast<const h4*>(x);
-        b[0] = double(v[0]), b[1] = double(v[1]), b[2] = double(v[2]), b[3] = double(v[3]);
-      } else if constexpr (P == 2) {
-        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-        const h2 v = *reinterpret_cast<const h2*>(x);
-        b[0] = double(v[0]), b[1] = double(v[1]);
-      } else {
-        b[0] = double(x[0]);
-      }
-    }
-    return;
-  }
+      typedef T tp __attribute__((ext_vector_type(P)));
+      const tp v = *reinterpret_cast<const tp*>(src);
 #pragma unroll
-  for (int u = 0; u < P; ++u) { b[u] = j + u < dim ? fcoord(vectors, t, row * dim + j + u) : 0.0; }
+      for (int u = 0; u < P; ++u) { b[u] = ok ? double(v[u]) : 0.0; }
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      const bool ok  = j + u < dim;
+      const double v = double(x[row * dim + (ok ? j + u : dim - 1)]);
+      b[u]           = ok ? v : 0.0;
+    }
+  }
 }
 
 /**
@@ -503,15 +492,15 @@ __device__ inline void load_coords(const void* vectors, elem t, int64_t row, int
  * below P combine partials inside a lane, so every lane of the slot ends with the same bits. With
  * L < 64 a wave scores 64 / L rows at once, NR rows per slot, U 64-coordinate blocks per
  * iteration. l2: sum (q - x)^2; inner: -sum q x; cosine: -sum q x / sqrt(sum q^2 sum x^2).
+ * The element type, the metric and the alignment are template parameters: the loop holds no
+ * branch, and the loads of an iteration go out together.
  */
-template <int L, int NR>
-__device__ inline void slot_scores(const double* qv, const void* vectors, elem t,
-                                   const int64_t (&rows)[NR], int64_t dim, metric_kind metric,
-                                   int g, double (&out)[NR])
+template <int L, int NR, typename T, metric_kind M, bool ALIGNED>
+__device__ __forceinline__ void slot_scores(const double* qv, const T* x, const int64_t (&rows)[NR],
+                                   int64_t dim, int g, double (&out)[NR])
 {
   constexpr int P = 64 / L;            // partials per lane
-  constexpr int U = 2;                 // 64-coordinate blocks per iteration (measured best)
-  const bool aligned = dim % P == 0;
+  constexpr int U = 64 / L >= 2 ? 2 : 4;  // 64-coordinate blocks per iteration
   double acc[NR][P], xx[NR][P], qq[P];
 #pragma unroll
   for (int u = 0; u < P; ++u) {
@@ -524,9 +513,7 @@ __device__ inline void slot_scores(const double* qv, const void* vectors, elem t
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
 #pragma unroll
-      for (int v = 0; v < U; ++v) {
-        load_coords<P>(vectors, t, rows[r], dim, j0 + 64 * v, aligned, b[r][v]);
-      }
+      for (int v = 0; v < U; ++v) { load_coords<T, P, ALIGNED>(x, rows[r], dim, j0 + 64 * v, b[r][v]); }
     }
 #pragma unroll
     for (int v = 0; v < U; ++v) {
@@ -535,16 +522,16 @@ __device__ inline void slot_scores(const double* qv, const void* vectors, elem t
         const int64_t j = j0 + 64 * v + u;
         if (j < dim) {
           const double a = qv[j];
-          if (metric == metric_kind::cosine) { qq[u] = fma(a, a, qq[u]); }
+          if constexpr (M == metric_kind::cosine) { qq[u] = fma(a, a, qq[u]); }
 #pragma unroll
           for (int r = 0; r < NR; ++r) {
-            const double x = b[r][v][u];
-            if (metric == metric_kind::l2) {
-              const double d = a - x;
+            const double xv = b[r][v][u];
+            if constexpr (M == metric_kind::l2) {
+              const double d = a - xv;
               acc[r][u]      = fma(d, d, acc[r][u]);
             } else {
-              acc[r][u] = fma(a, x, acc[r][u]);
-              if (metric == metric_kind::cosine) { xx[r][u] = fma(x, x, xx[r][u]); }
+              acc[r][u] = fma(a, xv, acc[r][u]);
+              if constexpr (M == metric_kind::cosine) { xx[r][u] = fma(xv, xv, xx[r][u]); }
             }
           }
         }
@@ -556,11 +543,11 @@ __device__ inline void slot_scores(const double* qv, const void* vectors, elem t
   for (int lx = 32 / P; lx >= 1; lx >>= 1) {
 #pragma unroll
     for (int u = 0; u < P; ++u) {
-      if (metric == metric_kind::cosine) { qq[u] += __shfl_xor(qq[u], lx); }
+      if constexpr (M == metric_kind::cosine) { qq[u] += __shfl_xor(qq[u], lx); }
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
         acc[r][u] += __shfl_xor(acc[r][u], lx);
-        if (metric == metric_kind::cosine) { xx[r][u] += __shfl_xor(xx[r][u], lx); }
+        if constexpr (M == metric_kind::cosine) { xx[r][u] += __shfl_xor(xx[r][u], lx); }
       }
     }
   }
@@ -580,9 +567,9 @@ __device__ inline void slot_scores(const double* qv, const void* vectors, elem t
   }
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
-    if (metric == metric_kind::l2) {
+    if constexpr (M == metric_kind::l2) {
       out[r] = acc[r][0];
-    } else if (metric == metric_kind::inner) {
+    } else if constexpr (M == metric_kind::inner) {
       out[r] = -acc[r][0];
     } else {
       out[r] = -acc[r][0] / sqrt(qq[0] * xx[r][0]);
@@ -590,11 +577,10 @@ __device__ inline void slot_scores(const double* qv, const void* vectors, elem t
   }
 }
 
-/** Scores rid[from, to) into key[] (ordered keys) with slots of L lanes, NR rows per slot. */
-template <int L>
-__device__ inline void score_rows_l(const double* qv, const void* vectors, elem t, int64_t dim,
-                                    metric_kind metric, const uint32_t* rid, uint64_t* key,
-                                    int from, int to)
+/** score_rows_l for one element type, metric and alignment. */
+template <int L, typename T, metric_kind M, bool ALIGNED>
+__device__ __forceinline__ void score_rows_t(const double* qv, const T* x, int64_t dim, const uint32_t* rid,
+                                    uint64_t* key, int from, int to)
 {
   constexpr int NR   = L == 16 ? 1 : 2;  // rows per slot (measured best at configs 3 and 4)
   constexpr int PER  = (64 / L) * NR;  // rows per wave at a time
@@ -609,7 +595,7 @@ __device__ inline void score_rows_l(const double* qv, const void* vectors, elem 
       rows[r]     = int64_t(rid[e < to ? e : to - 1]);
     }
     double sc[NR];
-    slot_scores<L, NR>(qv, vectors, t, rows, dim, metric, g, sc);
+    slot_scores<L, NR, T, M, ALIGNED>(qv, x, rows, dim, g, sc);
     if (g == 0) {
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
@@ -617,6 +603,41 @@ __device__ inline void score_rows_l(const double* qv, const void* vectors, elem 
         if (e < to) { key[e] = score_key(sc[r]); }
       }
     }
+  }
+}
+
+template <int L, typename T>
+__device__ __forceinline__ void score_rows_m(const double* qv, const T* x, int64_t dim, metric_kind metric,
+                                    const uint32_t* rid, uint64_t* key, int from, int to)
+{
+  constexpr int P    = 64 / L;
+  const bool aligned = dim % P == 0;
+  switch (metric) {
+    case metric_kind::l2:
+      aligned ? score_rows_t<L, T, metric_kind::l2, true>(qv, x, dim, rid, key, from, to)
+              : score_rows_t<L, T, metric_kind::l2, false>(qv, x, dim, rid, key, from, to);
+      break;
+    case metric_kind::inner:
+      aligned ? score_rows_t<L, T, metric_kind::inner, true>(qv, x, dim, rid, key, from, to)
+              : score_rows_t<L, T, metric_kind::inner, false>(qv, x, dim, rid, key, from, to);
+      break;
+    default:
+      aligned ? score_rows_t<L, T, metric_kind::cosine, true>(qv, x, dim, rid, key, from, to)
+              : score_rows_t<L, T, metric_kind::cosine, false>(qv, x, dim, rid, key, from, to);
+      break;
+  }
+}
+
+/** Scores rid[from, to) into key[] (ordered keys) with slots of L lanes, NR rows per slot. */
+template <int L>
+__device__ __forceinline__ void score_rows_l(const double* qv, const void* vectors, elem t, int64_t dim,
+                                    metric_kind metric, const uint32_t* rid, uint64_t* key,
+                                    int from, int to)
+{
+  if (t == elem::f32) {
+    score_rows_m<L>(qv, static_cast<const float*>(vectors), dim, metric, rid, key, from, to);
+  } else {
+    score_rows_m<L>(qv, static_cast<const _Float16*>(vectors), dim, metric, rid, key, from, to);
   }
 }
 
