@@ -291,23 +291,20 @@ int max_lds()
 
 /** Static LDS of the screen (thresholds, count) and a margin. */
 constexpr int kWideFixed = 16 * 6 * 4 + 512;
-/** Survivor list entries of the K-loop screen: at least this many, or the query tiles shrink. */
-constexpr int kWideMinHits = 4096;
 /** Most survivor list entries (hit_q, hit_row, hit_val: 12 bytes each). */
 constexpr int kWideMaxHits = 8192;
 
 /**
  * Query tiles of a workgroup for rows of `row_bytes`: the largest of 6, 4, 2 whose queries and a
- * survivor list of kWideMinHits entries fit the LDS, else the largest whose queries and 1,024
- * entries fit (0: none fits). A survivor that finds the list full waits for a global atomic, so
- * the fp16 screens, which keep thousands of rows per query, trade query tiles for list entries.
+ * survivor list of kHitCap entries fit the LDS (0: none fits); the list takes the rest of the LDS.
+ * More queries per workgroup means more work per row fetched; survivors past the list go to the
+ * workgroup's spill region, so a short list costs little (measured at d = 768: 96 queries and
+ * 1,280 entries ran the screen in 2.20 ms, 64 queries and 5,376 entries in 2.40 ms).
  */
 int wide_query_tiles(int row_bytes)
 {
-  for (int min_hits : {kWideMinHits, kHitCap}) {
-    for (int qt : {6, 4, 2}) {
-      if (16 * qt * row_bytes + 12 * min_hits + kWideFixed <= max_lds()) { return qt; }
-    }
+  for (int qt : {6, 4, 2}) {
+    if (16 * qt * row_bytes + 12 * kHitCap + kWideFixed <= max_lds()) { return qt; }
   }
   return 0;
 }
