@@ -39,6 +39,8 @@
 
 #include "screen_common.hpp"
 
+#include <type_traits>
+
 namespace certex_amd {
 namespace {
 
@@ -49,6 +51,16 @@ template <int KS>
 __device__ __forceinline__ int slot(int r, int c)
 {
   return KS == 2 ? (c ^ (r & 7)) : (c ^ (r & 15));
+}
+
+/** f(integral_constant<int, I>) for I = B .. E - 1, unrolled at compile time. */
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
 }
 
 template <typename R, int KS, int QB, bool ANCHORS, bool FILT, int BT, int QT>
@@ -63,9 +75,12 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   constexpr int TR     = 16 * BT;        // rows of a step
   constexpr int SPT    = TR / kStepRows; // chunk steps (kStepRows rows) per step
   constexpr bool ARGMX = ANCHORS && R::kArgmax;
+  // coarse anchor groups without argmax or filter: each lane folds its values into a register per
+  // (query group, query tile) every step; the lanes of a query reduce and write once per group
+  constexpr bool RUNREG = ANCHORS && !R::kArgmax && !FILT;
   static_assert(NG % 2 == 0, "query groups are processed in pairs");
   static_assert(BT * 4 <= 32, "a lane's survivor mask of one query tile is 32 bits");
-  static_assert(!ANCHORS || (BT == 4 && QT == 4), "the anchor pass runs 64-row steps");
+  static_assert(!ANCHORS || BT == 4, "the anchor pass runs 64-row steps");
   static_assert(!R::kValues || BT == 4, "screen values travel for 16 rows per query tile");
   __shared__ __attribute__((aligned(16))) uint8_t qlds[QB * ROWB];
   __shared__ val_t thl[ANCHORS ? 1 : QB];
@@ -172,8 +187,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   };
 
   int64_t row0 = 0;  // scan index of (bt = 0, r = 0) of this lane in the current step
-  auto group = [&](int g, const frag_t (&bf)[QT][KS], const val_t (&th)[QT]) {
-    acc_t acc[BT][QT];
+  auto mfmas = [&](const frag_t (&bf)[QT][KS], acc_t (&acc)[BT][QT]) {
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int bt = 0; bt < BT; ++bt) {
@@ -186,21 +200,25 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
       }
     }
     __builtin_amdgcn_s_setprio(0);
+  };
+  auto group = [&](int g, const frag_t (&bf)[QT][KS], const val_t (&th)[QT]) {
+    acc_t acc[BT][QT];
+    mfmas(bf, acc);
 
     if constexpr (ANCHORS) {
       if (a.fine) {
 #pragma unroll
-        for (int qt = 0; qt < 4; ++qt) {
+        for (int qt = 0; qt < QT; ++qt) {
           const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
-          const int64_t q    = q0 + g * 64 + qt * 16 + (lane & 15);
+          const int64_t q    = q0 + g * GQ + qt * 16 + (lane & 15);
           anchor_tile_fine<R, FILT>(col, row0, q, q < w.q_end, a, w, gmax);
         }
       } else {
 #pragma unroll
-        for (int qt = 0; qt < 4; ++qt) {
+        for (int qt = 0; qt < QT; ++qt) {
           const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
-          anchor_tile<R, FILT>(col, row0, q0 + g * 64 + qt * 16 + (lane & 15),
-                               wave * QB + g * 64 + qt * 16 + lane, a, w, gml, gmr);
+          anchor_tile<R, FILT>(col, row0, q0 + g * GQ + qt * 16 + (lane & 15),
+                               wave * QB + g * GQ + qt * 16 + lane, a, w, gml, gmr);
         }
       }
     } else {
@@ -248,8 +266,65 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   frag_t b0[QT][KS], b1[QT][KS];
   val_t t0[QT], t1[QT];
   read_queries(0, b0, t0);
+  val_t run[RUNREG ? NG : 1][QT];
+#pragma unroll
+  for (int g = 0; g < (RUNREG ? NG : 1); ++g) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) { run[g][qt] = R::lowest(); }
+  }
   auto step = [&](int64_t s) {
     row0 = s * TR + (lane >> 4) * 4;
+    if constexpr (RUNREG) {
+      if (!a.fine) {
+        // the groups at compile time, so that run[][] stays in registers
+        auto group_run = [&](auto gc, const frag_t (&bf)[QT][KS]) {
+          constexpr int g = decltype(gc)::value;
+          acc_t acc[BT][QT];
+          mfmas(bf, acc);
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) {
+            val_t m = run[g][qt];
+#pragma unroll
+            for (int bt = 0; bt < BT; ++bt) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) { m = R::vmax(m, acc[bt][qt][r]); }
+            }
+            run[g][qt] = m;
+          }
+        };
+        static_for<0, NG / 2>([&](auto pc) {
+          constexpr int g = 2 * decltype(pc)::value;
+          // keep each pair of groups in place: hoisting every group's query reads to the top of
+          // the unrolled loop would exceed the registers
+          __builtin_amdgcn_sched_barrier(0);
+          if (g < ng) {
+            read_queries(g + 1, b1, t1);
+            group_run(std::integral_constant<int, g>{}, b0);
+            read_queries(g + 2 < ng ? g + 2 : 0, b0, t0);
+            group_run(std::integral_constant<int, g + 1>{}, b1);
+          }
+        });
+        // end of an anchor group (group_steps steps, aligned to the wave's range): the maxima of
+        // the 4 lanes of each query (l, l ^ 16, l ^ 32, l ^ 48) go to the table
+        if ((s + 1) % a.group_steps == 0 || s + 1 == n_steps) {
+          static_for<0, NG>([&](auto gc) {
+            constexpr int g = decltype(gc)::value;
+            if (g < ng) {
+#pragma unroll
+              for (int qt = 0; qt < QT; ++qt) {
+                val_t m         = run[g][qt];
+                m               = R::vmax(m, __shfl_xor(m, 16));
+                m               = R::vmax(m, __shfl_xor(m, 32));
+                const int64_t q = q0 + g * GQ + qt * 16 + (lane & 15);
+                if (lane < 16 && q < w.q_end) { gmax[table_entry(a, q, s / a.group_steps)] = m; }
+                run[g][qt] = R::lowest();
+              }
+            }
+          });
+        }
+        return;
+      }
+    }
 #pragma unroll 1
     for (int g = 0; g < ng; g += 2) {
       read_queries(g + 1, b1, t1);
@@ -294,6 +369,9 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 }
 
 template <typename R, bool ANCHORS, bool FILT>
+void launch_other(const screen_args& b, dim3 grid, int ks, int qb_size, hipStream_t stream);
+
+template <typename R, bool ANCHORS, bool FILT>
 void launch(const screen_args& a, hipStream_t stream)
 {
   const int qb_size = screen_block_queries(a.nq_pad);
@@ -311,9 +389,30 @@ void launch(const screen_args& a, hipStream_t stream)
   const int ks  = a.row_bytes / 64;
   screen_args b = a;
   b.spill_cap   = !ANCHORS && a.spill_q != nullptr ? a.spill_pool / blocks : 0;
+  if constexpr (ANCHORS && !R::kArgmax && !FILT) {
+    // coarse groups keep their running maxima in registers: groups of 32 queries (2 tiles)
+    // leave room for them
+    if (ks == 2 && qb_size == 512) {
+      screen_kernel<R, 2, 512, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
+    } else if (ks == 2) {
+      screen_kernel<R, 2, 128, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
+    } else if (ks == 4 && qb_size == 512) {
+      screen_kernel<R, 4, 512, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
+    } else if (ks == 4) {
+      screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
+    }
+  } else {
+    launch_other<R, ANCHORS, FILT>(b, grid, ks, qb_size, stream);
+  }
+}
+
+/** The launches other than the register-maxima anchor pass. */
+template <typename R, bool ANCHORS, bool FILT>
+void launch_other(const screen_args& b, dim3 grid, int ks, int qb_size, hipStream_t stream)
+{
   if constexpr (!ANCHORS && !R::kValues) {
     // steps of 128 rows when every wave's share of a chunk is whole steps
-    if (ks == 2 && qb_size == 512 && (a.chunk_steps / 4) % 2 == 0) {
+    if (ks == 2 && qb_size == 512 && (b.chunk_steps / 4) % 2 == 0) {
       screen_kernel<R, 2, 512, ANCHORS, FILT, 8, 2><<<grid, 256, 0, stream>>>(b);
       return;
     }
