@@ -417,7 +417,8 @@ def bench_config5(args):
 def calibrate():
     """The rates the MFMA units sustain on this card, for reading the screens' roofline fractions:
     pure register MFMA streams (libcertex_calibrate.so; constant operands: clock-limited, random
-    operands: power-limited, shader clock read in the kernel) and hipBLASLt GEMMs through torch on
+    operands: power-limited, config 2's rows and queries: the operands of the headline screen;
+    shader clock read in the kernel) and hipBLASLt GEMMs through torch on
     random and all-zero operands. One JSON line; nothing of the search runs."""
     lib = ctypes.CDLL(os.path.join(ROOT, "libcertex_amd", "libcertex_calibrate.so"))
     lib.certex_calibrate_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
@@ -431,8 +432,25 @@ def calibrate():
             out["streams"][f"{name} {'random' if rnd else 'constant'} operands"] = {
                 "T_per_s": round(r[0] / 1e12, 1), "frac_of_peak": round(r[0] / 1e12 / peak, 4),
                 "shader_mhz": round(r[1]), "ms": round(r[2], 3)}
-    torch.manual_seed(0)
     dev = torch.device("cuda:0")
+    # the int8 stream on config 2's own operands: rows and queries of the 1,000-centre mixture in
+    # the screen's signed form (uint8 ^ 0x80), 128 bytes per row
+    lib.certex_calibrate_mfma_rows.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                               ctypes.c_int64, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    centres = torch.rand((1000, 128), generator=torch.Generator().manual_seed(1), dtype=torch.float64) * 80.0
+    centres = centres.float().to(dev)
+    rows = (mixture_u8(1 << 20, 128, 1000, centres, 2, dev) ^ 0x80).contiguous()
+    qrows = (mixture_u8(10_000, 128, 1000, centres, 3, dev) ^ 0x80).contiguous()
+    torch.cuda.synchronize()
+    r = (ctypes.c_double * 3)()
+    rc = lib.certex_calibrate_mfma_rows(rows.data_ptr(), rows.shape[0], qrows.data_ptr(), qrows.shape[0], 128, r)
+    if rc != 0:
+        raise RuntimeError(f"certex_calibrate_mfma_rows failed with HIP error {rc}")
+    out["streams"]["int8 16x16x64, config 2 rows x queries"] = {
+        "T_per_s": round(r[0] / 1e12, 1), "frac_of_peak": round(r[0] / 1e12 / P_INT8_TOPS, 4),
+        "shader_mhz": round(r[1]), "ms": round(r[2], 3)}
+    del rows, qrows
+    torch.manual_seed(0)
 
     def timed(f, ops):
         for _ in range(3):

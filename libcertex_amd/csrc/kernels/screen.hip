@@ -256,8 +256,8 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
               for (int r = 0; r < 4; ++r) { v16[bt * 4 + r] = acc[bt][qt][r]; }
             }
           }
-          push_hits<FILT, R::kValues>(bits, qloc, w.base + row0, q0, a, hit_q, hit_row, hit_val,
-                                      &n_hits, uint32_t(kHitCap), v16);
+          push_hits<BT * 4, FILT, R::kValues>(bits, qloc, w.base + row0, q0, a, hit_q, hit_row,
+                                              hit_val, &n_hits, uint32_t(kHitCap), v16);
         }
       }
     }

@@ -192,18 +192,21 @@ __device__ inline bool keeps_row(const screen_args& a, int64_t q, uint32_t row)
 
 /**
  * Appends the survivors of one 16-query tile of a step to the workgroup's list: `bits` is this
- * lane's survivor mask (up to 8 row tiles), `qloc` its query within the workgroup, row0 the
- * stored row of its bit 0, v the screen values of bits 0..15 (used when VALS). One round per
- * survivor of the busiest lane: ballot, rank by mbcnt, one LDS reservation per round; once the
- * list holds `cap` entries, survivors spill straight into the global bucket (one global atomic
- * per query and round, which waits for its reply). Every lane of the wave must call it.
+ * lane's survivor mask over NB = 16 or 32 rows (4 or 8 row tiles), `qloc` its query within the
+ * workgroup, row0 the stored row of its bit 0, v the screen values of bits 0..15 (used when VALS,
+ * NB = 16). The wave reserves all of its survivors with one LDS atomic: each lane's offset is the
+ * exclusive prefix of the survivor counts, summed from one ballot per bit of the count. The lanes
+ * then write their survivors in as many rounds as the busiest lane has survivors, with no vote or
+ * atomic per round. Every lane of the wave must call it.
  */
-template <bool FILT, bool VALS, typename V>
+template <int NB, bool FILT, bool VALS, typename V>
 __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t row0, int64_t q0,
                                           const screen_args& a, uint32_t* hit_q,
                                           uint32_t* hit_row, float* hit_val, uint32_t* n_hits,
                                           uint32_t cap, const V (&v)[16])
 {
+  static_assert(NB == 16 || NB == 32, "16 or 32 rows per lane");
+  static_assert(!VALS || NB == 16, "screen values come with 4 row tiles");
   if constexpr (FILT) {
     uint32_t scan = bits;
     while (scan) {
@@ -214,59 +217,51 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
       }
     }
   }
-  const int lane = threadIdx.x & 63;
-  while (true) {
-    const uint64_t mask = __ballot(bits != 0);
-    if (mask == 0) { break; }
-    const uint32_t rank =
-      __builtin_amdgcn_mbcnt_hi(uint32_t(mask >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(mask), 0u));
-    const int leader = __builtin_ctzll(mask);
-    uint32_t base    = 0;
-    if (lane == leader) { base = atomicAdd(n_hits, uint32_t(__builtin_popcountll(mask))); }
-    base = __builtin_amdgcn_readlane(base, leader);
-    const bool had     = bits != 0;
-    const int j        = had ? __builtin_ctz(bits) : 0;
+  const uint32_t cnt = uint32_t(__builtin_popcount(bits));
+  uint32_t excl = 0, total = 0;
+#pragma unroll
+  for (int b = 0; (1 << b) <= NB; ++b) {
+    const uint64_t m = __ballot((cnt >> b) & 1u);
+    excl += __builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u))
+            << b;
+    total += uint32_t(__builtin_popcountll(m)) << b;
+  }
+  if (total == 0) { return; }
+  const int lane   = threadIdx.x & 63;
+  const int leader = __builtin_ctzll(__ballot(1));
+  uint32_t base    = 0;
+  if (lane == leader) { base = atomicAdd(n_hits, total); }
+  uint32_t pos = uint32_t(__builtin_amdgcn_readlane(int(base), leader)) + excl;
+  // each lane writes its survivors at pos, pos + 1, ...: the list, then the workgroup's spill
+  // region (plain stores, moved to the buckets by the flush), then, when both are full (or no pool
+  // was provided), straight into the global bucket with one atomic each
+  while (bits != 0) {
+    const int j        = __builtin_ctz(bits);
     bits &= bits - 1;
     const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
-    const uint32_t pos = base + rank;
     float val          = 0.0f;
     if constexpr (VALS) {
 #pragma unroll
       for (int t = 0; t < 16; ++t) { val = t == j ? float(v[t]) : val; }
     }
-    if (had && pos < cap) {
+    if (pos < cap) {
       hit_q[pos]   = qloc;
       hit_row[pos] = row;
       if constexpr (VALS) { hit_val[pos] = val; }
-    }
-    // a full list: the workgroup's spill region (plain stores, moved to the buckets by the flush)
-    const uint32_t spos = pos - cap;
-    if (had && pos >= cap && spos < a.spill_cap) {
-      const int64_t e = int64_t(blockIdx.x) * a.spill_cap + spos;
+    } else if (pos - cap < uint32_t(a.spill_cap)) {
+      const int64_t e = int64_t(blockIdx.x) * a.spill_cap + (pos - cap);
       a.spill_q[e]    = qloc;
       a.spill_row[e]  = row;
       if constexpr (VALS) { a.spill_val[e] = val; }
-    }
-    // a full region too: straight to the global bucket, one atomic per query of the round (the 4
-    // lanes l, l ^ 16, l ^ 32, l ^ 48 hold the same query)
-    const uint64_t spill = __ballot(had && pos >= cap && spos >= a.spill_cap);
-    if (spill != 0) {
-      const uint64_t same = spill & (0x0001000100010001ull << (lane & 15));
-      const int first     = same ? __builtin_ctzll(same) : lane;
-      uint32_t at         = 0;
-      if (same && lane == first) {
-        at = atomicAdd(a.cand_count + q0 + qloc, uint32_t(__builtin_popcountll(same)));
-      }
-      at = uint32_t(__shfl(int(at), first));
-      if ((spill >> lane) & 1) {
-        const int64_t q      = q0 + qloc;
-        const uint32_t bslot = at + uint32_t(__builtin_popcountll(same & ((1ull << lane) - 1)));
-        if (bslot < a.cap) {
-          a.cand_rows[q * a.cap + bslot] = row;
-          if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = val; }
-        }
+    } else {
+      const int64_t q   = q0 + qloc;
+      const uint32_t at = atomicAdd(a.cand_count + q, 1u);
+      if (at < a.cap) {
+        a.cand_rows[q * a.cap + at] = row;
+        if constexpr (VALS) { a.cand_vals[q * a.cap + at] = val; }
       }
     }
+    ++pos;
   }
 }
 

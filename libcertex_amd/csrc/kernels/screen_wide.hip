@@ -102,7 +102,9 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
   // so that the compiler's wait counts see one straight path and the prefetches stay in flight.
   const gbytes codes     = (gbytes)a.codes;
   const int64_t row_step = int64_t(a.row_stride) * RB;  // bytes between consecutive scan rows
-  auto step_base = [&](int64_t s) { return codes + (w.base + s * kStepRows * a.row_stride) * RB; };
+  auto step_base = [&](int64_t s) {
+    return codes + (w.base + s * kStepRows * a.row_stride) * RB;
+  };
   auto offsets   = [&](int64_t s, uint32_t (&O)[4]) {
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
@@ -111,7 +113,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
       O[bt]     = uint32_t((r - s * kStepRows) * row_step + (lane >> 4) * 32);
     }
   };
-  auto load_chunk = [&](gbytes base, const uint32_t (&O)[4], int64_t off, frag_t (&A)[4][2]) {
+  auto load_chunk = [&](gbytes base, const uint32_t (&O)[4], int64_t off,
+                        frag_t (&A)[4][2]) {
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
       A[bt][0] = gload(base + off + O[bt]);
@@ -248,8 +251,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
                                  acc[1][qt][0], acc[1][qt][1], acc[1][qt][2], acc[1][qt][3],
                                  acc[2][qt][0], acc[2][qt][1], acc[2][qt][2], acc[2][qt][3],
                                  acc[3][qt][0], acc[3][qt][1], acc[3][qt][2], acc[3][qt][3]};
-          push_hits<FILT, true>(bits, uint32_t(qt * 16 + (lane & 15)), w.base + row0, q0, a, hit_q,
-                                hit_row, hit_val, &n_hits, uint32_t(hc), v16);
+          push_hits<16, FILT, true>(bits, uint32_t(qt * 16 + (lane & 15)), w.base + row0, q0, a,
+                                    hit_q, hit_row, hit_val, &n_hits, uint32_t(hc), v16);
         }
       }
     }
