@@ -417,14 +417,16 @@ void launch_other(const screen_args& b, dim3 grid, int ks, int qb_size, hipStrea
       return;
     }
   }
+  // groups of 32 queries: with 64, the fragments of 256-byte rows took more than the registers of
+  // two waves per SIMD, and the compiler made the group's code a function call
   if (ks == 2 && qb_size == 512) {
-    screen_kernel<R, 2, 512, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(b);
+    screen_kernel<R, 2, 512, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
   } else if (ks == 2) {
-    screen_kernel<R, 2, 128, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(b);
+    screen_kernel<R, 2, 128, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
   } else if (ks == 4 && qb_size == 512) {
-    screen_kernel<R, 4, 512, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(b);
+    screen_kernel<R, 4, 512, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
   } else if (ks == 4) {
-    screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 4><<<grid, 256, 0, stream>>>(b);
+    screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
   }
   // other row widths are rejected by the host before any launch
 }
