@@ -40,6 +40,27 @@ __device__ inline int block_scan_incl(int v, int* wave_tot)
   return incl + add;
 }
 
+/**
+ * Slot of this lane in an LDS list counted by *fill, for the lanes whose `take` is set: one LDS
+ * atomic per wave (the taking lanes in lane order) instead of one per entry, which would all hit
+ * the same word. Every lane of the wave calls it; the others get an unused value.
+ */
+__device__ inline int wave_append(bool take, int* fill)
+{
+  const uint64_t m = __ballot(take);
+  if (m == 0) { return 0; }
+  const int lane   = threadIdx.x & 63;
+  const int leader = __builtin_ctzll(m);
+  int base         = 0;
+  if (lane == leader) { base = atomicAdd(fill, __builtin_popcountll(m)); }
+  base = __builtin_amdgcn_readlane(base, leader);
+  return base + int(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32),
+                                               __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
+}
+
+/** Elements per thread whose global loads a scan issues together. */
+constexpr int kBatch = 8;
+
 /** Order-preserving map of a signed 32-bit value onto an unsigned key (descending value). */
 __device__ inline uint32_t desc_key(int32_t v) { return ~(uint32_t(v) ^ 0x80000000u); }
 __device__ inline int32_t desc_value(uint32_t key) { return int32_t(~key ^ 0x80000000u); }
@@ -334,11 +355,12 @@ __device__ inline uint64_t keep_k_best(uint64_t* key, uint32_t* row, int n, int 
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    const int e = threadIdx.x + i * kThreads;
-    if (e < n && (kk[i] < K || (kk[i] == K && rr[i] <= R))) {
-      const int s = atomicAdd(fill, 1);
-      key[s]      = kk[i];
-      row[s]      = rr[i];
+    const int e    = threadIdx.x + i * kThreads;
+    const bool in  = e < n && (kk[i] < K || (kk[i] == K && rr[i] <= R));
+    const int s    = wave_append(in, fill);
+    if (in) {
+      key[s] = kk[i];
+      row[s] = rr[i];
     }
   }
   __syncthreads();
@@ -825,9 +847,19 @@ __device__ uint32_t radix_select(int64_t n, int rank, F key_of, int* hist, int* 
   for (int shift = 24; shift >= 0; shift -= 8) {
     hist[tid] = 0;
     __syncthreads();
-    for (int64_t e = tid; e < n; e += kThreads) {
-      const uint32_t kk = key_of(e);
-      if ((kk & mask) == prefix) { atomicAdd(&hist[(kk >> shift) & 255], 1); }
+    for (int64_t e0 = 0; e0 < n; e0 += int64_t(kThreads) * kBatch) {
+      uint32_t kk[kBatch];  // loads first (from clamped positions), then the counts
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int64_t e = e0 + i * kThreads + tid;
+        kk[i]           = key_of(e < n ? e : n - 1);
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        if (e0 + i * kThreads + tid < n && (kk[i] & mask) == prefix) {
+          atomicAdd(&hist[(kk[i] >> shift) & 255], 1);
+        }
+      }
     }
     __syncthreads();
     const int c    = hist[tid];
@@ -854,7 +886,8 @@ __device__ uint32_t radix_select(int64_t n, int rank, F key_of, int* hist, int* 
  * stay in LDS.
  */
 template <int L>
-__global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a, int cap)
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(L == 64 ? 5 : 4)))
+void verify_topk_f_kernel(verify_f_args a, int cap)
 {
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
   auto* key = reinterpret_cast<uint64_t*>(dyn);                 // [cap]
@@ -905,10 +938,19 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
                       &sel_digit, &sel_rank);
     if (tid == 0) { fill = 0; }
     __syncthreads();
-    for (int64_t e = tid; e < n_cand; e += kThreads) {
-      if (~fkey(vals[e]) <= tk) {
-        const int slot = atomicAdd(&fill, 1);
-        if (slot < cap) { rid[slot] = to_id(cand[e]); }
+    for (int64_t e0 = 0; e0 < n_cand; e0 += int64_t(kThreads) * kBatch) {
+      float v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int64_t e = e0 + i * kThreads + tid;
+        v[i]            = vals[e < n_cand ? e : n_cand - 1];
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int64_t e = e0 + i * kThreads + tid;
+        const bool take = e < n_cand && ~fkey(v[i]) <= tk;
+        const int slot  = wave_append(take, &fill);
+        if (take && slot < cap) { rid[slot] = to_id(cand[e]); }
       }
     }
     __syncthreads();
@@ -929,26 +971,39 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
     }
   }
 
-  // phase B: the rest (everything when not ordered), in buffer-sized chunks
+  // phase B: the rest (everything when not ordered), in chunks of at most the buffer's free
+  // room. A cut back to the k best (which also tightens U) is a select over the whole buffer: it
+  // runs once the rows scored past the k best come to k / 8 (U then moves enough to save
+  // scores), or when the free room falls below a quarter of the buffer
   for (int64_t c0 = 0; c0 < n_cand;) {
     const int room  = cap - have;
     const int64_t m = n_cand - c0 < room ? n_cand - c0 : room;
     if (tid == 0) { fill = 0; }
     __syncthreads();
-    for (int64_t e = tid; e < m; e += kThreads) {
-      const int64_t idx = c0 + e;
-      uint32_t r;
-      bool take;
-      if (a.all_rows) {
-        r    = uint32_t(idx);
-        take = a.rowc[r] != -INFINITY && keeps(a.filter, q, r);
-        r    = listed_id(a.filter, r);
-      } else {
-        r    = to_id(cand[idx]);
-        take = !ordered || (~fkey(vals[idx]) > tk &&
-                            screen_lower_bound(vals[idx], aq, C, a.alpha2, a.metric) <= U);
+    for (int64_t e0 = 0; e0 < m; e0 += int64_t(kThreads) * kBatch) {
+      bool take[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int64_t e   = e0 + i * kThreads + tid;
+        const int64_t idx = c0 + (e < m ? e : m - 1);  // loads from clamped positions
+        if (a.all_rows) {
+          take[i] = a.rowc[idx] != -INFINITY && keeps(a.filter, q, uint32_t(idx));
+        } else if (ordered) {
+          const float v = vals[idx];
+          take[i] = ~fkey(v) > tk && screen_lower_bound(v, aq, C, a.alpha2, a.metric) <= U;
+        } else {
+          take[i] = true;
+        }
+        take[i] = take[i] && e < m;
       }
-      if (take) { rid[have + atomicAdd(&fill, 1)] = r; }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int slot = wave_append(take[i], &fill);
+        if (take[i]) {
+          const int64_t idx = c0 + e0 + i * kThreads + tid;
+          rid[have + slot]  = a.all_rows ? listed_id(a.filter, uint32_t(idx)) : to_id(cand[idx]);
+        }
+      }
     }
     __syncthreads();
     const int added = fill;
@@ -956,7 +1011,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_f_kernel(verify_f_args a
     have += added;
     c0 += m;
     __syncthreads();
-    if (have > k && c0 < n_cand) {
+    if (have > k && c0 < n_cand && (8 * (have - k) >= k || cap - have < cap / 4)) {
       keep_best();
       if (ordered) { U = key_score(kth); }
     }
