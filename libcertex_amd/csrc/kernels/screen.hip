@@ -187,6 +187,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   };
 
   int64_t row0 = 0;  // scan index of (bt = 0, r = 0) of this lane in the current step
+  step_labels SL;    // the label filter's row labels of the step (anchor pass with a filter)
   auto mfmas = [&](const frag_t (&bf)[QT][KS], acc_t (&acc)[BT][QT]) {
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -201,7 +202,8 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     }
     __builtin_amdgcn_s_setprio(0);
   };
-  auto group = [&](int g, const frag_t (&bf)[QT][KS], const val_t (&th)[QT]) {
+  auto group = [&](int g, const frag_t (&bf)[QT][KS], const val_t (&th)[QT])
+                   __attribute__((always_inline)) {
     acc_t acc[BT][QT];
     mfmas(bf, acc);
 
@@ -211,14 +213,19 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
         for (int qt = 0; qt < QT; ++qt) {
           const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
           const int64_t q    = q0 + g * GQ + qt * 16 + (lane & 15);
-          anchor_tile_fine<R, FILT>(col, row0, q, q < w.q_end, a, w, gmax);
+          const int64_t qc   = q < w.q_end ? q : w.q_end - 1;  // padding: any live query's
+          const uint32_t kp  = FILT ? filter_mask(a, w, SL, qc, row0) : 0u;
+          anchor_tile_fine<R, FILT>(col, row0, q, q < w.q_end, a, w, gmax, kp);
         }
       } else {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
           const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
-          anchor_tile<R, FILT>(col, row0, q0 + g * GQ + qt * 16 + (lane & 15),
-                               wave * QB + g * GQ + qt * 16 + lane, a, w, gml, gmr);
+          const int64_t q    = q0 + g * GQ + qt * 16 + (lane & 15);
+          const int64_t qc   = q < w.q_end ? q : w.q_end - 1;  // padding: any live query's
+          const uint32_t kp  = FILT ? filter_mask(a, w, SL, qc, row0) : 0u;
+          anchor_tile<R, FILT>(col, row0, q, wave * QB + g * GQ + qt * 16 + lane, a, w, gml, gmr,
+                               kp);
         }
       }
     } else {
@@ -274,6 +281,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   }
   auto step = [&](int64_t s) {
     row0 = s * TR + (lane >> 4) * 4;
+    if constexpr (ANCHORS && FILT) { load_step_labels(a, w, row0, SL); }
     if constexpr (RUNREG) {
       if (!a.fine) {
         // the groups at compile time, so that run[][] stays in registers

@@ -184,6 +184,59 @@ __device__ inline bool keeps_row(const screen_args& a, int64_t q, uint32_t row)
 }
 
 /**
+ * Label filter of the anchor pass, row side: the labels of the lane's 16 rows of a step (entry
+ * bt * 4 + r: scan index row0 + bt * 16 + r; 0xffffffff past the scan), read once per step. Each
+ * query tile then compares them with one query label instead of reading two labels per pair.
+ */
+struct step_labels {
+  bool on = false;  // a label filter (kind 3)
+  uint32_t v[16];
+};
+
+__device__ inline void load_step_labels(const screen_args& a, const screen_work& w, int64_t row0,
+                                        step_labels& L)
+{
+  L.on = a.filter.kind == 3;
+  if (!L.on) { return; }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int64_t idx = row0 + (j >> 2) * 16 + (j & 3);
+    const bool in     = idx < w.n_scan;
+    const uint32_t row = uint32_t(w.base + (in ? idx : 0) * a.row_stride);
+    const uint32_t id  = a.id_scale > 0 ? uint32_t(row * a.id_scale) : listed_id(a.filter, row);
+    const uint32_t lab = a.filter.row_labels[id];
+    L.v[j]             = in ? lab : 0xffffffffu;
+  }
+}
+
+/**
+ * The filter's verdicts for query q (q < q_end) on the lane's 16 rows of the step (bit
+ * bt * 4 + r; rows past the scan are cleared): one compare per row against the row labels of
+ * the step for a label filter, else one test per row in a rolled loop (which keeps the anchor
+ * pass's code small enough to stay inlined).
+ */
+__device__ __forceinline__ uint32_t filter_mask(const screen_args& a, const screen_work& w,
+                                                const step_labels& L, int64_t q, int64_t row0)
+{
+  if (L.on) {
+    const uint32_t qlab = uint32_t(a.filter.query_labels[a.filter.q0 + q]);
+    uint32_t keep       = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) { keep |= uint32_t(L.v[j] == qlab) << j; }
+    return keep;
+  }
+  uint32_t keep = 0;
+#pragma unroll 1
+  for (int j = 0; j < 16; ++j) {
+    const int64_t idx = row0 + (j >> 2) * 16 + (j & 3);
+    if (idx < w.n_scan && keeps_row(a, q, uint32_t(w.base + idx * a.row_stride))) {
+      keep |= 1u << j;
+    }
+  }
+  return keep;
+}
+
+/**
  * LDS survivor list of a workgroup: hit_q / hit_row / hit_val (the screen values, when the rows
  * carry them) of `cap` entries (kHitCap, or what the K-loop screen's LDS leaves) and the count
  * n_hits, passed as separate pointers (a struct of LDS addresses can end up as a constant
@@ -330,7 +383,7 @@ template <typename R, bool FILT>
 __device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], int64_t row0,
                                             int64_t q, int e, const screen_args& a,
                                             const screen_work& w, typename R::val_t* gml,
-                                            uint32_t* gmr)
+                                            uint32_t* gmr, uint32_t keep)
 {
   using val_t         = typename R::val_t;
   constexpr bool ARGX = R::kArgmax;
@@ -343,10 +396,7 @@ __device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], i
     for (int r = 0; r < 4; ++r) {
       val_t v = col[bt][r];
       if constexpr (FILT) {
-        const int64_t idx = row0 + bt * 16 + r;
-        if (idx < w.n_scan && !keeps_row(a, q, uint32_t(w.base + idx * a.row_stride))) {
-          v = R::lowest();
-        }
+        if (!((keep >> (bt * 4 + r)) & 1u)) { v = R::lowest(); }
       }
       if constexpr (ARGX) {
         if (v > m) {
@@ -390,7 +440,8 @@ __device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], i
 template <typename R, bool FILT>
 __device__ __forceinline__ void anchor_tile_fine(const typename R::acc_t (&col)[4], int64_t row0,
                                                  int64_t q, bool live, const screen_args& a,
-                                                 const screen_work& w, typename R::val_t* gmax)
+                                                 const screen_work& w, typename R::val_t* gmax,
+                                                 uint32_t keep)
 {
   using val_t = typename R::val_t;
 #pragma unroll
@@ -403,9 +454,7 @@ __device__ __forceinline__ void anchor_tile_fine(const typename R::acc_t (&col)[
       val_t v           = col[bt][r];
       const int64_t idx = first + r;
       if constexpr (FILT) {
-        if (idx < w.n_scan && !keeps_row(a, q, uint32_t(w.base + idx * a.row_stride))) {
-          v = R::lowest();
-        }
+        if (!((keep >> (bt * 4 + r)) & 1u)) { v = R::lowest(); }
       }
       if (v > m) {  // strict: ties keep the lower row
         m   = v;

@@ -209,20 +209,26 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
     for (int bt = 0; bt < 4; ++bt) { O[bt] = ON[bt]; }
 
     const int64_t row0 = s * kStepRows + (lane >> 4) * 4;
+    step_labels SL;  // the label filter's row labels of the step
+    if constexpr (ANCHORS && FILT) { load_step_labels(a, w, row0, SL); }
     if constexpr (ANCHORS) {
       if (a.fine) {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
           const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
           const int64_t q    = q0 + qt * 16 + (lane & 15);
-          anchor_tile_fine<R, FILT>(col, row0, q, q < w.q_end, a, w, gmax);
+          const int64_t qc   = q < w.q_end ? q : w.q_end - 1;  // padding: any live query's
+          const uint32_t kp  = FILT ? filter_mask(a, w, SL, qc, row0) : 0u;
+          anchor_tile_fine<R, FILT>(col, row0, q, q < w.q_end, a, w, gmax, kp);
         }
       } else {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
           const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
-          anchor_tile<R, FILT>(col, row0, q0 + qt * 16 + (lane & 15), wave * QB + qt * 16 + lane,
-                               a, w, gml, gmr);
+          const int64_t q    = q0 + qt * 16 + (lane & 15);
+          const int64_t qc   = q < w.q_end ? q : w.q_end - 1;  // padding: any live query's
+          const uint32_t kp  = FILT ? filter_mask(a, w, SL, qc, row0) : 0u;
+          anchor_tile<R, FILT>(col, row0, q, wave * QB + qt * 16 + lane, a, w, gml, gmr, kp);
         }
       }
       // end of an anchor group (group_steps steps, aligned to the wave's range)
