@@ -421,7 +421,8 @@ auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
 template <typename F>
 bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, int64_t size,
                          certex_amd::screen_args& sa, F&& screen, uint32_t*& count,
-                         uint32_t*& rows, int64_t& cap, float** vals = nullptr)
+                         uint32_t*& rows, int64_t& cap, float** vals = nullptr,
+                         int64_t* worst_out = nullptr)
 {
   auto& rs           = res.state();
   hipStream_t stream = rs.stream;
@@ -464,6 +465,7 @@ bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, 
     CERTEX_HIP_TRY(hipStreamSynchronize(stream));
     const int64_t worst = static_cast<uint32_t*>(rs.host_small)[0];
     if (static_cast<uint32_t*>(rs.host_small)[1] > 0) { rs.spill_pool = true; }
+    if (worst_out != nullptr) { *worst_out = worst; }
     if (worst <= cap) { return true; }
     if (worst > all_rows_above) { return false; }
     int64_t c = 1024;
@@ -776,12 +778,12 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
   }
 
   uint32_t *count = nullptr, *rows = nullptr;
-  int64_t cap = 0;
+  int64_t cap = 0, worst = -1;
   if (!all_rows) {
     sa.theta = theta;
     all_rows = !screen_into_buckets(res, B, nq_pad, size, sa,
                                     screen_pass(st, route, certex_amd::screen_i8), count, rows,
-                                    cap);
+                                    cap, nullptr, &worst);
   }
   count_stats(res, st, B, all_rows, count, cap);
 
@@ -794,6 +796,7 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
   va.cand_rows  = rows;
   va.cap        = cap;
   va.all_rows   = all_rows;
+  va.max_cand   = all_rows ? -1 : worst;
   va.n_rows     = size;
   va.codes      = st.codes.as<int8_t>();
   va.rowc       = st.rowc.as<int32_t>();

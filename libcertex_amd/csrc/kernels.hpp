@@ -244,7 +244,9 @@ struct verify_args {
   const uint32_t* cand_rows;
   int64_t cap;
   bool all_rows;
-  int64_t n_rows;  // rows of the index (all_rows)
+  int64_t max_cand  = -1;  // the largest bucket count when the host knows it (else -1)
+  int64_t small_max = -1;  // set by the launcher: buckets up to this size take the one-wave path
+  int64_t n_rows;         // rows of the index (all_rows)
   // vectors: integer codes (int path)
   const int8_t* codes;
   const int32_t* rowc;  // liveness (kDeadRow) for all_rows

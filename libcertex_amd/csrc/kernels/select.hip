@@ -390,6 +390,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a,
 
   const int64_t n_cand =
     a.all_rows ? a.n_rows : (a.cand_count[q] < a.cap ? int64_t(a.cand_count[q]) : a.cap);
+  if (!a.all_rows && n_cand <= a.small_max) { return; }  // the one-wave kernel's query
   const uint32_t* cand = a.cand_rows + q * a.cap;
 
   int have = 0;  // entries [0, have) of the buffer hold the best candidates so far
@@ -460,6 +461,100 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a,
   }
 }
 
+
+/**
+ * The integer re-rank for small buckets (at most kSmallBucket candidates, k <= 64): one wave per
+ * query. Each lane scores up to kSmallBucket / 64 candidates into registers; then k rounds of a
+ * wave minimum over (score key, id) emit the k best in order, with no LDS buffer and no barrier.
+ * The output is the block kernel's: the k smallest (key, id) pairs, ascending, then +inf / -1.
+ * Queries with larger buckets are left to the block kernel.
+ */
+/** Candidates per query up to which the integer re-rank runs one wave per query. */
+constexpr int kSmallBucket = 512;
+
+__global__ __launch_bounds__(kThreads) void verify_topk_i8_small_kernel(verify_args a)
+{
+  __shared__ __attribute__((aligned(16))) int8_t qlds[kThreads / 64][kMaxIntDim];
+  const int lane    = threadIdx.x & 63;
+  const int wave    = threadIdx.x >> 6;
+  const int64_t q   = int64_t(blockIdx.x) * (kThreads / 64) + wave;
+  const bool live_q = q < a.nq;
+  int8_t* qv        = qlds[wave];
+  if (live_q) {
+    for (int j = lane; j < a.row_bytes; j += 64) { qv[j] = a.qcodes[q * a.row_bytes + j]; }
+  }
+  __syncthreads();  // the query codes are in LDS (the block's only barrier)
+  if (!live_q) { return; }
+  int qq, qs;
+  query_sums(qv, a.row_bytes, qq, qs);
+  const int bias       = a.flip ? 128 : 0;
+  const int64_t n_cand = a.cand_count[q] < a.cap ? int64_t(a.cand_count[q]) : a.cap;
+  if (n_cand > kSmallBucket) { return; }
+  const uint32_t* cand = a.cand_rows + q * a.cap;
+  constexpr int NPL    = kSmallBucket / 64;  // candidates per lane
+  uint64_t key[NPL];
+  uint32_t rid[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int64_t e = lane + 64 * i;
+    key[i]          = ~0ull;
+    rid[i]          = ~0u;
+    if (e < n_cand) {
+      const uint32_t r   = cand[e];
+      const int8_t* base = a.codes;
+      uint32_t id;
+      if (a.part_ids != nullptr && r < a.n_part) {
+        base = a.part_codes;
+        id   = uint32_t(a.part_ids[r]);
+      } else {
+        id = listed_id(a.filter, r);
+      }
+      key[i] = score_key(int_score(qv, base + int64_t(r) * a.row_bytes, a.row_bytes, a.dim, bias,
+                                   qq, qs, a.metric));
+      rid[i] = id;
+    }
+  }
+  double my_s   = INFINITY;
+  int64_t my_r  = -1;
+  for (int j = 0; j < a.k; ++j) {
+    uint64_t bk = key[0];
+    uint32_t br = rid[0];
+#pragma unroll
+    for (int i = 1; i < NPL; ++i) {
+      if (key[i] < bk || (key[i] == bk && rid[i] < br)) {
+        bk = key[i];
+        br = rid[i];
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const uint32_t lo = uint32_t(__shfl_xor(int(uint32_t(bk)), off));
+      const uint32_t hi = uint32_t(__shfl_xor(int(uint32_t(bk >> 32)), off));
+      const uint64_t ok = (uint64_t(hi) << 32) | lo;
+      const uint32_t orr = uint32_t(__shfl_xor(int(br), off));
+      if (ok < bk || (ok == bk && orr < br)) {
+        bk = ok;
+        br = orr;
+      }
+    }
+    if (bk == ~0ull) { break; }  // every lane holds the same pair: fewer than k candidates
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      if (key[i] == bk && rid[i] == br) {
+        key[i] = ~0ull;
+        rid[i] = ~0u;
+      }
+    }
+    if (lane == j) {
+      my_s = key_score(bk);
+      my_r = int64_t(br);
+    }
+  }
+  if (lane < a.k) {
+    a.best_score[q * a.k + lane] = my_s;
+    a.best_row[q * a.k + lane]   = my_r;
+  }
+}
 
 // ---- float vectors ---------------------------------------------------------------------------
 
@@ -1084,12 +1179,21 @@ void sum_u32(const uint32_t* count, int64_t n, int64_t cap, unsigned long long* 
 void verify_topk_i8(const verify_args& a, hipStream_t stream)
 {
   if (a.nq == 0) { return; }
+  verify_args b = a;
+  b.small_max   = -1;
+  if (!a.all_rows && a.k <= 64) {
+    // buckets of up to kSmallBucket candidates: one wave per query; the block kernel then takes
+    // only the larger buckets (launched when the host saw one)
+    verify_topk_i8_small_kernel<<<unsigned((a.nq + 3) / 4), kThreads, 0, stream>>>(a);
+    if (a.max_cand >= 0 && a.max_cand <= kSmallBucket) { return; }
+    b.small_max = kSmallBucket;
+  }
   // room for 2 k candidates (at least 1,024): small k keeps the block's LDS small, so that many
   // blocks share a CU
   int cap = pow2_ge(2 * a.k);
   cap     = cap > 1024 ? (cap < kBuf ? cap : kBuf) : 1024;
   const size_t bytes = size_t(cap) * 12 + kMaxIntDim;
-  verify_topk_i8_kernel<<<unsigned(a.nq), kThreads, bytes, stream>>>(a, cap);
+  verify_topk_i8_kernel<<<unsigned(a.nq), kThreads, bytes, stream>>>(b, cap);
 }
 
 /** Launches a kernel with `bytes` of dynamic LDS (raising the kernel's limit when needed). */
