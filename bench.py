@@ -572,7 +572,8 @@ def main():
     row_b = 128 if d <= 128 else 256
     verify_bytes = (st.survivors * (4 + row_b) + nq * row_b) / max(1, launches[3] // args.steps)
     phase_roofs = {"verify_topk": hbm_roofline(
-        "verify_topk_i8_kernel", verify_bytes, ms[3] / max(1, launches[3]),
+        "verify_topk_i8_small_kernel (+ verify_topk_i8_kernel for buckets over 512)", verify_bytes,
+        ms[3] / max(1, launches[3]),
         f"{st.survivors / max(1, st.queries):.1f} survivors x ({row_b} B code row + 4 B bucket "
         f"entry), plus the query, per query")}
     batches = (nq + args.batch - 1) // args.batch
