@@ -854,9 +854,9 @@ __global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_arg
   if (tid == 0) { cnt = 0; }
   __syncthreads();
   for (int64_t e = tid; e < a.n_groups; e += kThreads) {
-    if (!(v[e] > -INFINITY) || ~fkey(v[e]) > prefix) { continue; }
-    const int slot = atomicAdd(&cnt, 1);
-    if (slot < cap) {
+    const bool take = v[e] > -INFINITY && ~fkey(v[e]) <= prefix;
+    const int slot  = wave_append(take, &cnt);  // the wave's lanes still in the loop
+    if (take && slot < cap) {
       const uint32_t row = r[e];
       rid[slot]          = e < a.id_cols                             ? uint32_t(row * a.id_scale)
                            : (a.part_ids != nullptr && row < a.n_part) ? uint32_t(a.part_ids[row])
