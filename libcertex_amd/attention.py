@@ -49,8 +49,9 @@ class KeyCache:
         _require(1 <= k <= 2048, f"k must be between 1 and 2048, not {k}")
         self.n_kv_heads, self.head_dim, self.k, self.capacity = int(n_kv_heads), int(head_dim), int(k), capacity
         self.index, self.dtype = None, None
-        self.local = None  # key id within its head, per id of the shared index
+        self.local = None  # key id within its head, per id of the shared index (grown in place)
         self.size = 0
+        self._labels = {}  # cached label vectors: appends of n keys, and searches of (H, m)
 
     def append(self, keys):
         """Append keys of shape (n_kv_heads, n, head_dim); ids continue from the keys before."""
@@ -74,13 +75,24 @@ class KeyCache:
                 anchor_stride=_stride(cap, self.k),
                 partition_labels=False,
             )
-        heads = torch.arange(self.n_kv_heads, device="cuda", dtype=torch.int32)
+        key = ("append", n)
+        if key not in self._labels:
+            heads = torch.arange(self.n_kv_heads, device="cuda", dtype=torch.int32)
+            self._labels[key] = heads.repeat_interleave(n)
+        n0 = self.n_kv_heads * self.size  # the shared index's first new id
         self.index.add(
             K.to(self.dtype).reshape(self.n_kv_heads * n, self.head_dim).contiguous(),
-            labels=heads.repeat_interleave(n),
+            labels=self._labels[key],
         )
-        local = torch.arange(self.size, self.size + n, device="cuda", dtype=torch.int64).repeat(self.n_kv_heads)
-        self.local = local if self.local is None else torch.cat([self.local, local])
+        need = n0 + self.n_kv_heads * n
+        if self.local is None or self.local.shape[0] < need:
+            grown = torch.empty(max(need, 2 * (0 if self.local is None else self.local.shape[0])),
+                                device="cuda", dtype=torch.int64)
+            if self.local is not None:
+                grown[:n0] = self.local[:n0]
+            self.local = grown
+        self.local[n0:need].view(self.n_kv_heads, n).copy_(
+            torch.arange(self.size, self.size + n, device="cuda", dtype=torch.int64))
         self.size += n
         core = self.index.core
         if (core.size - core.n_partitioned) * 16 > core.size:
@@ -103,7 +115,10 @@ class KeyCache:
         )
         H, m, d = Q.shape
         r = H // self.n_kv_heads
-        labels = (torch.arange(H, device="cuda", dtype=torch.int32) // r).repeat_interleave(m)
+        key = ("search", H, m)
+        if key not in self._labels:
+            self._labels[key] = (torch.arange(H, device="cuda", dtype=torch.int32) // r).repeat_interleave(m)
+        labels = self._labels[key]
         D, I = self.index.search(
             Q.to(self.dtype).reshape(H * m, d), k=k, batch=batch or max(2048, H * m), labels=labels
         )
