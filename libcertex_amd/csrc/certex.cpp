@@ -37,6 +37,7 @@ resources::~resources()
     (void)hipStreamSynchronize(s_->stream);
     for (auto& b : s_->slots) { b.release(); }
     if (s_->host_small) { (void)hipHostFree(s_->host_small); }
+    if (s_->host_stage) { (void)hipHostFree(s_->host_stage); }
     if (s_->owns_stream) { (void)hipStreamDestroy(s_->stream); }
   }
 }
@@ -970,10 +971,13 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
 {
   auto& rs           = res.state();
   hipStream_t stream = rs.stream;
+  // the labels come back through pinned staging (a pageable copy is staged by the runtime)
   std::vector<int32_t> lab(static_cast<size_t>(B)), order(static_cast<size_t>(B)),
     sorted(static_cast<size_t>(B));
-  CERTEX_HIP_TRY(hipMemcpyAsync(lab.data(), qlabels, size_t(B) * 4, hipMemcpyDeviceToHost, stream));
+  auto* hl = static_cast<int32_t*>(rs.stage(std::max<size_t>(16, size_t(B) * 4)));
+  CERTEX_HIP_TRY(hipMemcpyAsync(hl, qlabels, size_t(B) * 4, hipMemcpyDeviceToHost, stream));
   CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  std::copy(hl, hl + B, lab.begin());
   // queries in label order, stable: a counting sort when the batch's labels span a small range
   // (one pass, no comparisons), else a comparison sort
   const auto [lo_it, hi_it] = std::minmax_element(lab.begin(), lab.end());
@@ -1053,15 +1057,16 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   auto* d_sorted = reinterpret_cast<int32_t*>(dev + lab_bytes);
   auto* d_ga     = reinterpret_cast<certex_amd::screen_group*>(dev + 2 * lab_bytes);
   auto* d_gs     = reinterpret_cast<certex_amd::screen_group*>(dev + 2 * lab_bytes + tab_bytes);
-  CERTEX_HIP_TRY(hipMemcpyAsync(d_order, order.data(), size_t(B) * 4, hipMemcpyHostToDevice, stream));
-  CERTEX_HIP_TRY(
-    hipMemcpyAsync(d_sorted, sorted.data(), size_t(B) * 4, hipMemcpyHostToDevice, stream));
+  // the four tables packed as on the device, in pinned staging, then one copy
+  const size_t all_bytes = 2 * lab_bytes + 2 * tab_bytes;
+  char* hs               = static_cast<char*>(rs.stage(all_bytes));
+  std::memcpy(hs, order.data(), size_t(B) * 4);
+  std::memcpy(hs + lab_bytes, sorted.data(), size_t(B) * 4);
   if (!gs.empty()) {
-    CERTEX_HIP_TRY(hipMemcpyAsync(d_ga, ga.data(), ga.size() * sizeof(ga[0]),
-                                  hipMemcpyHostToDevice, stream));
-    CERTEX_HIP_TRY(hipMemcpyAsync(d_gs, gs.data(), gs.size() * sizeof(gs[0]),
-                                  hipMemcpyHostToDevice, stream));
+    std::memcpy(hs + 2 * lab_bytes, ga.data(), ga.size() * sizeof(ga[0]));
+    std::memcpy(hs + 2 * lab_bytes + tab_bytes, gs.data(), gs.size() * sizeof(gs[0]));
   }
+  CERTEX_HIP_TRY(hipMemcpyAsync(dev, hs, all_bytes, hipMemcpyHostToDevice, stream));
   route.anchor_groups = d_ga;
   route.screen_groups = d_gs;
 
@@ -1074,7 +1079,7 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   batch(res, st, q_sorted, B, k, 0, nb_s, ds_s, fa, params, &route);
   certex_amd::scatter_rows(nb_s, d_order, B, int64_t(k) * 8, neighbors, stream);
   certex_amd::scatter_rows(ds_s, d_order, B, int64_t(k) * 4, distances, stream);
-  CERTEX_HIP_TRY(hipStreamSynchronize(stream));  // the host tables above go out of scope
+  CERTEX_HIP_TRY(hipStreamSynchronize(stream));  // the staged tables are reused by the next batch
 }
 
 template <typename T>

@@ -120,6 +120,23 @@ struct resources_state {
   bool spill_pool     = false;  // a screen's LDS survivor lists overflowed: provide a spill pool
   device_buffer slots[ws_n_slots];
   void* host_small    = nullptr;  // pinned host words for counters read back by the host
+  void* host_stage    = nullptr;  // pinned host staging of the routing tables (grow-only)
+  size_t host_stage_bytes = 0;
+
+  /** Pinned host staging of at least `bytes` bytes (grow-only; waits for the stream first). */
+  void* stage(size_t bytes)
+  {
+    if (host_stage_bytes < bytes) {
+      CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+      if (host_stage != nullptr) { CERTEX_HIP_TRY(hipHostFree(host_stage)); }
+      host_stage       = nullptr;
+      host_stage_bytes = 0;
+      const size_t n   = bytes + bytes / 4;
+      CERTEX_HIP_TRY(hipHostMalloc(&host_stage, n, hipHostMallocDefault));
+      host_stage_bytes = n;
+    }
+    return host_stage;
+  }
 
   /** Scratch slot of at least `bytes` bytes (grow-only; waits for the stream before growing). */
   void* get(int slot, size_t bytes)
