@@ -301,8 +301,8 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
       hit_q[pos]   = qloc;
       hit_row[pos] = row;
       if constexpr (VALS) { hit_val[pos] = val; }
-    } else if (pos - cap < uint32_t(a.spill_cap)) {
-      const int64_t e = int64_t(blockIdx.x) * a.spill_cap + (pos - cap);
+    } else if (int64_t(pos - cap) < a.spill_cap) {
+      const int64_t e = int64_t(blockIdx.x) * a.spill_cap + int64_t(pos - cap);
       a.spill_q[e]    = qloc;
       a.spill_row[e]  = row;
       if constexpr (VALS) { a.spill_val[e] = val; }

@@ -462,6 +462,9 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a,
 }
 
 
+/** Candidates per query up to which the integer re-rank runs one wave per query. */
+constexpr int kSmallBucket = 512;
+
 /**
  * The integer re-rank for small buckets (at most kSmallBucket candidates, k <= 64): one wave per
  * query. Each lane scores up to kSmallBucket / 64 candidates into registers; then k rounds of a
@@ -469,9 +472,6 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a,
  * The output is the block kernel's: the k smallest (key, id) pairs, ascending, then +inf / -1.
  * Queries with larger buckets are left to the block kernel.
  */
-/** Candidates per query up to which the integer re-rank runs one wave per query. */
-constexpr int kSmallBucket = 512;
-
 __global__ __launch_bounds__(kThreads) void verify_topk_i8_small_kernel(verify_args a)
 {
   __shared__ __attribute__((aligned(16))) int8_t qlds[kThreads / 64][kMaxIntDim];
