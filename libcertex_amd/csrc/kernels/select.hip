@@ -1217,10 +1217,12 @@ void threshold_f16(const threshold_f_args& a, hipStream_t stream)
   const int cap       = want <= 512 ? 512 : (want + 255) / 256 * 256;
   const size_t bytes  = size_t(cap) * 12 + size_t(a.dim) * 8;
   const unsigned grid = unsigned(a.nq_pad);
-  switch (score_lanes(a.dim)) {
-    case 16: launch_dyn(threshold_f16_kernel<16>, grid, bytes, stream, a, cap); break;
-    case 32: launch_dyn(threshold_f16_kernel<32>, grid, bytes, stream, a, cap); break;
-    default: launch_dyn(threshold_f16_kernel<64>, grid, bytes, stream, a, cap); break;
+  // 32-lane slots also above 256 coordinates: twice the rows in flight per wave of whole-wave
+  // slots (config 3's threshold: 0.71 -> 0.64 ms; the verify measured best with whole waves)
+  if (a.dim <= 128) {
+    launch_dyn(threshold_f16_kernel<16>, grid, bytes, stream, a, cap);
+  } else {
+    launch_dyn(threshold_f16_kernel<32>, grid, bytes, stream, a, cap);
   }
 }
 
