@@ -699,7 +699,7 @@ template <int L, typename T, metric_kind M, bool ALIGNED>
 __device__ __forceinline__ void score_rows_t(const double* qv, const T* x, int64_t dim, const uint32_t* rid,
                                     uint64_t* key, int from, int to)
 {
-  constexpr int NR   = 2;  // rows per slot (1 and 4 measured slower at configs 3 and 4)
+  constexpr int NR   = 2;  // rows per slot (1, 3 and 4 measured slower at configs 3 and 4)
   constexpr int PER  = (64 / L) * NR;  // rows per wave at a time
   const int lane     = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g        = lane % L;
