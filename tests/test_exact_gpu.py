@@ -204,3 +204,19 @@ def test_many_survivors_spill(gpu):
         torch.cuda.synchronize()
         np.testing.assert_array_equal(I.cpu().numpy(), i)
         np.testing.assert_array_equal(D.cpu().numpy(), oracle.distances(s, i, "l2"))
+
+
+@pytest.mark.parametrize("k", [10, 64])
+def test_small_and_large_buckets(gpu, k):
+    """Half of the queries sit next to 2,000 copies of one row (buckets of thousands, the block
+    re-rank), the other half are random (buckets of a few hundred at most, the one-wave re-rank):
+    one search runs both paths and must equal the oracle (ties to the lower id)."""
+    rng = np.random.default_rng(11)
+    X = rng.integers(0, 256, (40_000, 128)).astype(np.uint8)
+    base = rng.integers(0, 256, 128).astype(np.uint8)
+    X[rng.permutation(40_000)[:2_000]] = base
+    near = np.clip(base.astype(np.int32) + rng.integers(-2, 3, (32, 128)), 0, 255).astype(np.uint8)
+    far = rng.integers(0, 256, (32, 128)).astype(np.uint8)
+    Q = np.concatenate([near, far])[rng.permutation(64)]
+    D, I, _ = run(X, Q, k)
+    check(X, Q, k, "l2", D, I)
