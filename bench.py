@@ -414,68 +414,6 @@ def bench_config5(args):
     }
 
 
-def calibrate():
-    """The rates the MFMA units sustain on this card, for reading the screens' roofline fractions:
-    pure register MFMA streams (libcertex_calibrate.so; constant operands: clock-limited, random
-    operands: power-limited, config 2's rows and queries: the operands of the headline screen;
-    shader clock read in the kernel) and hipBLASLt GEMMs through torch on
-    random and all-zero operands. One JSON line; nothing of the search runs."""
-    lib = ctypes.CDLL(os.path.join(ROOT, "libcertex_amd", "libcertex_calibrate.so"))
-    lib.certex_calibrate_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
-    out = {"metric": "MFMA calibration (dense ops/s on one MI355X)", "streams": {}, "gemms": {}}
-    for kind, name, peak in ((0, "int8 16x16x64", P_INT8_TOPS), (1, "fp16 16x16x32", P_FP16_TFLOPS)):
-        for rnd in (0, 1):
-            r = (ctypes.c_double * 3)()
-            rc = lib.certex_calibrate_mfma(kind, rnd, r)
-            if rc != 0:
-                raise RuntimeError(f"certex_calibrate_mfma failed with HIP error {rc}")
-            out["streams"][f"{name} {'random' if rnd else 'constant'} operands"] = {
-                "T_per_s": round(r[0] / 1e12, 1), "frac_of_peak": round(r[0] / 1e12 / peak, 4),
-                "shader_mhz": round(r[1]), "ms": round(r[2], 3)}
-    dev = torch.device("cuda:0")
-    # the int8 stream on config 2's own operands: rows and queries of the 1,000-centre mixture in
-    # the screen's signed form (uint8 ^ 0x80), 128 bytes per row
-    lib.certex_calibrate_mfma_rows.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
-                                               ctypes.c_int64, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
-    centres = torch.rand((1000, 128), generator=torch.Generator().manual_seed(1), dtype=torch.float64) * 80.0
-    centres = centres.float().to(dev)
-    rows = (mixture_u8(1 << 20, 128, 1000, centres, 2, dev) ^ 0x80).contiguous()
-    qrows = (mixture_u8(10_000, 128, 1000, centres, 3, dev) ^ 0x80).contiguous()
-    torch.cuda.synchronize()
-    r = (ctypes.c_double * 3)()
-    rc = lib.certex_calibrate_mfma_rows(rows.data_ptr(), rows.shape[0], qrows.data_ptr(), qrows.shape[0], 128, r)
-    if rc != 0:
-        raise RuntimeError(f"certex_calibrate_mfma_rows failed with HIP error {rc}")
-    out["streams"]["int8 16x16x64, config 2 rows x queries"] = {
-        "T_per_s": round(r[0] / 1e12, 1), "frac_of_peak": round(r[0] / 1e12 / P_INT8_TOPS, 4),
-        "shader_mhz": round(r[1]), "ms": round(r[2], 3)}
-    del rows, qrows
-    torch.manual_seed(0)
-
-    def timed(f, ops):
-        for _ in range(3):
-            f()
-        torch.cuda.synchronize()
-        t = time.perf_counter()
-        for _ in range(20):
-            f()
-        torch.cuda.synchronize()
-        return ops / ((time.perf_counter() - t) / 20) / 1e12
-
-    m = 8192
-    a = torch.randint(-128, 128, (m, m), dtype=torch.int8, device=dev)
-    b = torch.randint(-128, 128, (m, m), dtype=torch.int8, device=dev)
-    z = torch.zeros_like(a)
-    h = torch.randn((m, m), dtype=torch.float16, device=dev)
-    g = torch.randn((m, m), dtype=torch.float16, device=dev)
-    for name, f, peak in (("int8 8192^3 random (torch._int_mm)", lambda: torch._int_mm(a, b), P_INT8_TOPS),
-                          ("int8 8192^3 zeros (torch._int_mm)", lambda: torch._int_mm(z, z), P_INT8_TOPS),
-                          ("fp16 8192^3 random (torch.mm)", lambda: h @ g, P_FP16_TFLOPS)):
-        t = timed(f, 2.0 * m * m * m)
-        out["gemms"][name] = {"T_per_s": round(t, 1), "frac_of_peak": round(t / peak, 4)}
-    return out
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
@@ -493,8 +431,6 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--lists", type=int, default=-1, help="k-means lists (default: the config's; 0: none)")
     ap.add_argument("--probe", type=int, default=2, help="lists probed per query")
-    ap.add_argument("--calibrate", action="store_true",
-                    help="measure the MFMA rates this card sustains (streams and library GEMMs) instead")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -503,11 +439,6 @@ def main():
             file=sys.stderr,
         )
         sys.exit(2)
-
-    if args.calibrate:
-        torch.cuda.set_device(torch.device("cuda:0"))
-        print(json.dumps(calibrate()), flush=True)
-        return
 
     import libcertex_amd as certex
     from libcertex_amd import _capi as C

@@ -165,6 +165,15 @@ CUVS_EXPORT cuvsError_t cuvsCertexIndexGetLists(cuvsCertexIndex_t index,
 CUVS_EXPORT cuvsError_t cuvsCertexReserve(cuvsResources_t res,
                                           int64_t capacity,
                                           cuvsCertexIndex_t index);
+/**
+ * The ids in the order of the stored rows of an index with lists (core.cpp list_order, reference
+ * certex/index.py:353-359): `order` is an int32 device vector with one entry per vector added
+ * (cuvsCertexIndexGetSize). Queries taken in this order share their nearest lists within a batch.
+ * CUVS_ERROR when the index has no lists.
+ */
+CUVS_EXPORT cuvsError_t cuvsCertexIndexListOrder(cuvsResources_t res,
+                                                 cuvsCertexIndex_t index,
+                                                 DLManagedTensor* order);
 /** Start counting the searches of the calling thread (core.cpp stats_begin). */
 CUVS_EXPORT cuvsError_t cuvsCertexStatsBegin(void);
 /** Stop counting: queries, certified survivors, exact distances (core.cpp stats_end). */

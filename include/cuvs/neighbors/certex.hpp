@@ -200,6 +200,15 @@ void search(cuvs::resources const& res, search_params const& params, index<T> co
             float* distances, int64_t k);
 
 /**
+ * The ids in the order of the stored rows (reference Index.list_order, certex/index.py:353-359,
+ * served by python/src/core.cpp list_order): out[row] = the id stored at row, for all size()
+ * rows, written to device memory on the stream of `res`. Rows of the build are in list order;
+ * rows added later are their own ids. An index without lists is an error.
+ */
+template <typename T>
+void list_order(cuvs::resources const& res, index<T> const& idx, int32_t* out);
+
+/**
  * Save the index, its vectors and every quantity a search reads (reference
  * certex_serialize.cu:42-150). The file starts with the NumPy descriptor of the vector type padded
  * to 4 bytes ("<f4", "<f2", "|i1", "|u1"), the magic 0x43455258 and the format version.

@@ -149,6 +149,7 @@ def lib():
                     "cuvsCertexIndexGetPartitioned": [P(IndexHandle), P(i64)],
                     "cuvsCertexIndexGetLists": [P(IndexHandle), P(i32), P(i64)],
                     "cuvsCertexReserve": [ctypes.c_size_t, i64, P(IndexHandle)],
+                    "cuvsCertexIndexListOrder": [ctypes.c_size_t, P(IndexHandle), P(DLManagedTensor)],
                     "cuvsCertexStatsBegin": [],
                     "cuvsCertexStatsEnd": [P(i64), P(i64), P(i64)],
                     "cuvsCertexTimingBegin": [],

@@ -34,6 +34,20 @@ def _keys(x):
     return h if bool(torch.isfinite(h).all()) else x.to(torch.float32)
 
 
+def _fit(x, dtype, what):
+    """x in the cache's vector type; a conversion that would change a value (bfloat16 or float32
+    values that float16 rounds or overflows) is an error rather than a silent rounding."""
+    if x.dtype == dtype:
+        return x
+    y = x.to(dtype)
+    _require(
+        bool(torch.equal(y.to(x.dtype), x)),
+        f"the cache holds {dtype} keys, which cannot represent these {what} exactly: "
+        "start the cache with keys of this type (bfloat16 or float32 keys give a float32 cache)",
+    )
+    return y
+
+
 class KeyCache:
     """Exact top-k over the keys of a growing KV cache (attention.py:44-106).
 
@@ -81,7 +95,7 @@ class KeyCache:
             self._labels[key] = heads.repeat_interleave(n)
         n0 = self.n_kv_heads * self.size  # the shared index's first new id
         self.index.add(
-            K.to(self.dtype).reshape(self.n_kv_heads * n, self.head_dim).contiguous(),
+            _fit(K, self.dtype, "keys").reshape(self.n_kv_heads * n, self.head_dim).contiguous(),
             labels=self._labels[key],
         )
         need = n0 + self.n_kv_heads * n
@@ -120,7 +134,7 @@ class KeyCache:
             self._labels[key] = (torch.arange(H, device="cuda", dtype=torch.int32) // r).repeat_interleave(m)
         labels = self._labels[key]
         D, I = self.index.search(
-            Q.to(self.dtype).reshape(H * m, d), k=k, batch=batch or max(2048, H * m), labels=labels
+            _fit(Q, self.dtype, "queries").reshape(H * m, d), k=k, batch=batch or max(2048, H * m), labels=labels
         )
         scores = D.reshape(H, m, k)
         ids = self.local[I].reshape(H, m, k)

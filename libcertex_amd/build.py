@@ -3,8 +3,7 @@
     python -m libcertex_amd.build        # or: python libcertex_amd/build.py
 
 Every source is compiled on every call (a few seconds each, in parallel); the library is written
-next to this file so that it travels with the repository tree to the GPU box. The MFMA calibration
-streams (csrc/calibrate.hip) go into libcertex_calibrate.so, which only bench.py --calibrate loads.
+next to this file so that it travels with the repository tree to the GPU box.
 """
 
 import concurrent.futures
@@ -16,7 +15,6 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libcertex_c.so")
-CALIBRATE = os.path.join(HERE, "libcertex_calibrate.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -73,16 +71,6 @@ def build(verbose=False):
     os.replace(tmp, OUT)
     if verbose:
         print(f"built {OUT}")
-    # the MFMA calibration streams (bench.py --calibrate): a library of their own, not the C ABI
-    cal_obj = _compile("calibrate.hip", obj_dir)
-    tmp = CALIBRATE + ".tmp"
-    r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, cal_obj],
-                       capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, CALIBRATE)
-    if verbose:
-        print(f"built {CALIBRATE}")
     return OUT
 
 

@@ -565,6 +565,23 @@ cuvsError_t cuvsCertexReserve(cuvsResources_t res, int64_t capacity, cuvsCertexI
   });
 }
 
+cuvsError_t cuvsCertexIndexListOrder(cuvsResources_t res,
+                                     cuvsCertexIndex_t index,
+                                     DLManagedTensor* order)
+{
+  return translate([=] {
+    auto& r = res_of(res);
+    dispatch(index->dtype, [&](auto tag) {
+      using T         = decltype(tag);
+      auto const& idx = *as_index<T>(*index);
+      auto* out       = device_data<int32_t>(order, 1, "the list order");
+      certex::expects(order->dl_tensor.shape[0] == idx.size(),
+                      "certex: list_order needs an int32 device vector of one entry per vector");
+      certex::list_order<T>(r, idx, out);
+    });
+  });
+}
+
 cuvsError_t cuvsCertexStatsBegin(void)
 {
   return translate([] { certex::stats_begin(); });

@@ -178,8 +178,9 @@ void grow(cuvs::resources const& res, index_state& st, int64_t cap)
 void refresh_anchors(cuvs::resources const& res, index_state& st, int64_t first, int64_t end)
 {
   const int64_t s = std::max(1, st.anchor_stride);
+  // anchor j is id j * s, read from its stored row: id_rows[id] for listed ids
   certex_amd::gather_anchors(st.codes.p, st.rowc.p, st.row_bytes, s, (first + s - 1) / s,
-                             (end + s - 1) / s, st.row_ids.as<int32_t>(), st.n_listed,
+                             (end + s - 1) / s, st.id_rows.as<int32_t>(), st.n_listed,
                              st.anchor_codes.p, st.anchor_rowc.p,
                              static_cast<hipStream_t>(res.stream()));
 }
@@ -1507,6 +1508,20 @@ void remove(cuvs::resources const& res, const int64_t* ids, int64_t n_ids, index
 }
 
 template <typename T>
+void list_order(cuvs::resources const& res, index<T> const& idx, int32_t* out)
+{
+  index_state const& st = idx.state();
+  expects(st.n_lists > 0, "certex: the index has no lists");
+  std::shared_lock view(st.rw);
+  hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  if (st.n_listed > 0) {
+    CERTEX_HIP_TRY(hipMemcpyAsync(out, st.row_ids.p, size_t(st.n_listed) * sizeof(int32_t),
+                                  hipMemcpyDeviceToDevice, stream));
+  }
+  certex_amd::iota_i32(out + st.n_listed, st.size - st.n_listed, int32_t(st.n_listed), stream);
+}
+
+template <typename T>
 void set_labels(cuvs::resources const& res, const int32_t* labels, int64_t n, index<T>* idx,
                 int64_t first)
 {
@@ -1800,6 +1815,7 @@ void deserialize(cuvs::resources const& res, std::string const& filename, index<
   template void set_labels<T>(cuvs::resources const&, const int32_t*, int64_t, index<T>*,      \
                               int64_t);                                                        \
   template void partition_by_labels<T>(cuvs::resources const&, index<T>*);                     \
+  template void list_order<T>(cuvs::resources const&, index<T> const&, int32_t*);              \
   template void search<T>(cuvs::resources const&, search_params const&, index<T> const&,       \
                           matrix_view<const T>, int64_t*, float*, int64_t, filter);            \
   template void search<T>(cuvs::resources const&, search_params const&, index<T> const&,       \

@@ -87,6 +87,8 @@ void remove_rows_i8(const int64_t* ids, int64_t n, int64_t size, int32_t* rowc,
 
 void fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);
 void fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream);
+/** p[i] = first + i for i < n. */
+void iota_i32(int32_t* p, int64_t n, int32_t first, hipStream_t stream);
 
 // --- screen -------------------------------------------------------------------------------
 

@@ -93,6 +93,14 @@ __global__ void fill_kernel(T* p, int64_t n, T v)
   }
 }
 
+__global__ void iota_kernel(int32_t* p, int64_t n, int32_t first)
+{
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < n;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    p[i] = first + int32_t(i);
+  }
+}
+
 // ---- float vectors ---------------------------------------------------------------------------
 
 __device__ inline double coord(const void* p, elem t, int64_t i)
@@ -364,6 +372,13 @@ void fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t stream)
   if (n == 0) { return; }
   const unsigned b = blocks_for(n) < 4096 ? blocks_for(n) : 4096;
   fill_kernel<int32_t><<<b, 256, 0, stream>>>(p, n, v);
+}
+
+void iota_i32(int32_t* p, int64_t n, int32_t first, hipStream_t stream)
+{
+  if (n <= 0) { return; }
+  const unsigned b = blocks_for(n) < 4096 ? blocks_for(n) : 4096;
+  iota_kernel<<<b, 256, 0, stream>>>(p, n, first);
 }
 
 }  // namespace certex_amd

@@ -29,15 +29,31 @@ def row_len(m):
     return 64 if L <= 64 else 128 * ((L + 127) // 128)
 
 
-def _to_torch(x):
-    """A torch view of numpy, torch or DLPack arrays, and the kind of the input (certex/index.py:52-63)."""
-    if isinstance(x, np.ndarray):
-        return torch.from_numpy(np.ascontiguousarray(x)), "numpy"
+def _as_tensor(x):
+    """(tensor, restore): a torch view of a numpy array, torch tensor or DLPack-capable array, and
+    a function that returns a result tensor in the caller's array family (numpy arrays come back
+    as numpy on the host, torch as torch, other DLPack producers through their module's
+    from_dlpack when it has one). Reference interface: certex/index.py:54-84."""
     if isinstance(x, torch.Tensor):
-        return x, "torch"
-    if hasattr(x, "__dlpack__"):
-        return torch.from_dlpack(x), type(x).__module__.split(".")[0]
-    return torch.from_numpy(np.ascontiguousarray(np.asarray(x))), "numpy"
+        return x, lambda t: t
+    if isinstance(x, np.ndarray) or not hasattr(x, "__dlpack__"):
+        return torch.from_numpy(np.ascontiguousarray(np.asarray(x))), lambda t: t.cpu().numpy()
+    family = type(x).__module__.partition(".")[0]
+
+    def restore(t):
+        import importlib
+
+        try:
+            return importlib.import_module(family).from_dlpack(t)
+        except (ImportError, AttributeError, TypeError):
+            return t
+
+    return torch.from_dlpack(x), restore
+
+
+def _to_torch(x):
+    """The tensor of _as_tensor alone."""
+    return _as_tensor(x)[0]
 
 
 def _require(ok, message):
@@ -46,56 +62,61 @@ def _require(ok, message):
         raise ValueError(message)
 
 
-def _back(t, kind):
-    """t in the array type of an input of this kind (certex/index.py:72-84)."""
-    if kind == "numpy":
-        return t.cpu().numpy()
-    if kind == "torch":
-        return t
-    try:
-        import importlib
-
-        return importlib.import_module(kind).from_dlpack(t)
-    except (ImportError, AttributeError, TypeError):
-        return t
-
-
 def _cast(t, dtype):
-    """t in the data type of the index; non-representable values are an error (index.py:87-96)."""
+    """t in the index's vector type. An integer index takes only values that its type holds
+    exactly; anything else (fractions, out-of-range values) is a ValueError, as in the reference
+    (certex/index.py:87-96, tests/test_exact.py:342-350)."""
     if t.dtype == dtype:
         return t
-    if not dtype.is_floating_point:
-        lim = torch.iinfo(dtype)
-        f = t.double()
-        if not bool(((f == f.round()) & (f >= lim.min) & (f <= lim.max)).all()):
-            raise ValueError(f"the index holds {dtype} vectors: values must be integers in [{lim.min}, {lim.max}]")
-    return t.to(dtype)
+    if dtype.is_floating_point:
+        return t.to(dtype)
+    info = torch.iinfo(dtype)
+    y = t.to(dtype)
+    exact = t.numel() == 0 or (
+        bool(torch.equal(y.to(torch.float64), t.to(torch.float64)))
+        and float(t.min()) >= info.min
+        and float(t.max()) <= info.max
+    )
+    _require(exact, f"the index holds {dtype} vectors: values must be integers in [{info.min}, {info.max}]")
+    return y
+
+
+_BIT_WEIGHTS = {}
 
 
 def _pack(mask):
-    """A boolean mask, flattened row-major, as bitset words: bit j of word i is entry 32 i + j
-    (certex/index.py:99-104). Returned as int32 words on the mask's device."""
-    b = mask.reshape(-1).to(dtype=torch.int64)
-    b = torch.nn.functional.pad(b, (0, (-b.numel()) % 32)).view(-1, 32)
-    w = (b << torch.arange(32, device=b.device)).sum(1)
-    return torch.where(w >= 2**31, w - 2**32, w).to(torch.int32).contiguous()
+    """A boolean mask, flattened row-major, as 32-bit filter words on the mask's device: entry e is
+    bit e % 32 of word e // 32 (the reference's layout, certex/index.py:99-104). Eight entries
+    become one byte by a weighted sum, and four consecutive bytes are read as one little-endian
+    word; the returned words are int32."""
+    flat = mask.reshape(-1).to(torch.uint8)
+    flat = torch.nn.functional.pad(flat, (0, (-flat.numel()) % 32))
+    w = _BIT_WEIGHTS.get(flat.device)
+    if w is None:
+        w = _BIT_WEIGHTS[flat.device] = torch.tensor([1 << b for b in range(8)], dtype=torch.int32, device=flat.device)
+    octets = (flat.view(-1, 8).to(torch.int32) * w).sum(1).to(torch.uint8)
+    return octets.contiguous().view(torch.int32)
 
 
 def auto_width(X, metric, target=0.95, sample=200_000):
-    """Smallest tile-aligned width whose principal directions capture `target` of the variance
-    (certex/index.py:107-121)."""
-    X = _to_torch(X)[0]
-    d = X.shape[1]
-    S = X[torch.randperm(X.shape[0], device=X.device)[:sample]].float()
+    """The screening width the reference's rule picks (certex/index.py:107-121): the smallest
+    m = L - 5 over the tile lengths L = 64, 128, 256, 384, ... whose m leading principal directions
+    hold `target` of the variance (of the centred rows; raw rows for inner products), capped at the
+    dimension. Here the sample is every (n / sample)-th row, and the spectrum comes from the
+    singular values of the sample in float64."""
+    X = _to_torch(X)
+    n, d = X.shape
+    S = X[:: max(1, -(-n // sample))].to(torch.float64)
     if metric != "ip":
-        S = S - S.mean(0)
-    ev = torch.linalg.eigvalsh(S.double().T @ S.double()).flip(0).clamp_min(0)
-    frac = torch.cumsum(ev, 0) / ev.sum().clamp_min(1e-300)
-    for L in [64, 128] + list(range(256, 4097, 128)):
-        m = L - 5
-        if m >= d or float(frac[m - 1]) >= target:
-            return min(m, d)
-    return d
+        S = S - S.mean(0, keepdim=True)
+    var = torch.linalg.svdvals(S).square()
+    held = torch.cumsum(var, 0) / var.sum().clamp_min(1e-300)
+    # directions needed: the first count whose share reaches the target (1-based)
+    need = int(torch.searchsorted(held, torch.tensor([target], dtype=held.dtype), right=False)[0]) + 1
+    L = 64
+    while L - 5 < min(need, d):
+        L = 128 if L == 64 else L + 128
+    return min(L - 5, d)
 
 
 class search_stats:
@@ -232,7 +253,7 @@ class Index:
         return None if self.core is None else _TORCH[self.core.dtype]
 
     def _vectors(self, x, device):
-        t, kind = _to_torch(x)
+        t, kind = _as_tensor(x)
         if t.ndim == 1:
             t = t.reshape(1, -1)
         _require(
@@ -253,7 +274,7 @@ class Index:
         (certex/index.py:266-305)."""
         X, kind = self._vectors(x, device=False)
         if labels is not None:
-            labels = _to_torch(labels)[0].reshape(-1).to(device="cuda", dtype=torch.int32).contiguous()
+            labels = _to_torch(labels).reshape(-1).to(device="cuda", dtype=torch.int32).contiguous()
             _require(labels.shape[0] == X.shape[0] and int(labels.min()) >= 0, "one non-negative label per vector")
         L = C.lib()
         with self._writer:
@@ -292,7 +313,7 @@ class Index:
                 if self.partition_labels:
                     C.check(L.cuvsCertexPartitionByLabels(res, self.core.h))
         ids = torch.arange(n0, n0 + X.shape[0])
-        return _back(ids, kind)
+        return kind(ids)
 
     def partition(self):
         """Copy the screening rows into label order now (reference index.partition_by_labels): each
@@ -305,7 +326,7 @@ class Index:
     def remove(self, ids):
         """Remove vectors by id; they never appear in later results (certex/index.py:314-319)."""
         _require(self.core is not None, "add vectors first")
-        t = _to_torch(ids)[0].reshape(-1).to(device="cuda", dtype=torch.int64).contiguous()
+        t = _to_torch(ids).reshape(-1).to(device="cuda", dtype=torch.int64).contiguous()
         with self._writer:
             b = C.Borrowed(t)
             C.check(C.lib().cuvsCertexRemove(C.resources(), b.ptr, self.core.h))
@@ -314,7 +335,7 @@ class Index:
         """Exact k nearest neighbours of every query: (distances or similarities, ids), best first
         (certex/index.py:320-351)."""
         _require(self.core is not None, "the index is empty: add vectors first")
-        single = _to_torch(q)[0].ndim == 1
+        single = _to_torch(q).ndim == 1
         Q, kind = self._vectors(q, device=True)
         nq = Q.shape[0]
         _require(1 <= k <= 2048, f"k must be between 1 and 2048, not {k}")
@@ -325,10 +346,10 @@ class Index:
         ftype = C.NO_FILTER
         if labels is not None:
             _require(self.core.has_labels, "the index has no labels")
-            ql = _to_torch(labels)[0].reshape(-1).to(device="cuda", dtype=torch.int32).contiguous()
+            ql = _to_torch(labels).reshape(-1).to(device="cuda", dtype=torch.int32).contiguous()
             _require(ql.shape[0] == nq, "one label per query")
         if filter is not None:
-            m = _to_torch(filter)[0].to(torch.bool)
+            m = _to_torch(filter).to(torch.bool)
             _require(m.shape[-1] == self.core.size, "the filter needs one entry per id")
             _require(m.ndim == 1 or (m.ndim == 2 and m.shape[0] == nq), "a mask over the ids, or one row per query")
             words = _pack(m.cuda())
@@ -353,7 +374,18 @@ class Index:
             D = 1 - D
         if single:
             D, I = D[0], I[0]
-        return _back(D, kind), _back(I, kind)
+        return kind(D), kind(I)
+
+    def list_order(self):
+        """The ids in the order of the stored rows of an index with lists, list by list (rows added
+        after the build follow in id order); queries taken in this order share their nearest lists
+        within a batch (certex/index.py:353-359). An int64 tensor on the GPU."""
+        _require(self.core is not None and self.n_lists, "an index with lists")
+        out = torch.empty(self.core.size, dtype=torch.int32, device="cuda")
+        b = C.Borrowed(out)
+        C.check(C.lib().cuvsCertexIndexListOrder(C.resources(), self.core.h, b.ptr))
+        torch.cuda.current_stream().synchronize()
+        return out.long()
 
     def save(self, path):
         """Write the index to a file; load() restores it without rebuilding (certex/index.py:361-365)."""
@@ -368,7 +400,7 @@ class Index:
         _require(prefix[1:3] in _PREFIX, "not a certex index file")
         core = _Core()
         C.check(C.lib().cuvsCertexDeserialize(C.resources(), str(path).encode(), core.h))
-        idx = cls(core.dim, metric=core.metric, anchor_stride=core.anchor_stride)
+        idx = cls(core.dim, metric=core.metric, anchor_stride=core.anchor_stride, n_lists=core.lists[0])
         idx.core = core
         return idx
 
@@ -386,7 +418,7 @@ class Index:
 
 def search(xb, xq=None, k=10, metric="l2", **index_options):
     """The exact k nearest neighbours in one call (certex/index.py:422-447)."""
-    X, _ = _to_torch(xb)
+    X = _to_torch(xb)
     _require(X.ndim == 2, "xb must be a matrix (n, dim)")
     index_options.setdefault("storage", "device")
     index = Index(dim=X.shape[1], metric=metric, **index_options)
@@ -396,58 +428,68 @@ def search(xb, xq=None, k=10, metric="l2", **index_options):
     return D, I
 
 
+def _exact_scores(X, Q, dev, metric, rows_per_chunk):
+    """Exact float64 scores (smaller is better: l2 sum (q - x)^2, ip -<q, x>, cosine -cos) of every
+    query of Q against every row of X, yielded chunk by chunk of rows as (first row, scores)."""
+    for r0 in range(0, X.shape[0], rows_per_chunk):
+        R = X[r0 : r0 + rows_per_chunk].to(dev, torch.float64)
+        if metric == "l2":
+            s = (Q[:, None, :] - R[None]).square().sum(-1)
+        else:
+            if metric == "cosine":
+                R = R / torch.linalg.vector_norm(R, dim=1, keepdim=True)
+            s = -(Q @ R.T)
+        yield r0, s
+
+
 def verify(xb, xq, I, metric="l2", sample=100, seed=0):
-    """Fraction of checked queries whose returned neighbours have exactly the k best fp64 scores
-    (certex/index.py:450-548): a random sample of queries (torch generator seeded with `seed`) is
-    searched exhaustively in float64; ties count as exact whichever tied vector was returned. Runs
-    with torch on the queries' device (the GPU when available)."""
+    """Fraction of checked queries whose returned neighbours have exactly the k best float64 scores
+    (the reference's semantics, certex/index.py:450-548): queries are sampled at random (torch CPU
+    generator seeded with `seed`; all when sample is None), and ties count as exact whichever tied
+    vector was returned.
+
+    The check is a counting certificate rather than a second search. Let r_1 <= ... <= r_k be the
+    sorted exact scores of a query's k returned (distinct) ids. Those ids are the k best, up to the
+    tolerance t = 1e-9 max|r|, iff for every rank i fewer than i rows score below r_i - t. One pass
+    over the rows scores them exactly and, per query, histograms how many of the k bounds each score
+    falls under; a cumulative sum gives the counts. Runs on the GPU when one is present."""
     _require(metric in METRICS, f"metric must be one of {METRICS}, not {metric!r}")
-    X, _ = _to_torch(xb)
-    Q, _ = _to_torch(xq)
-    ids, _ = _to_torch(I)
+    X, Q, ids = _to_torch(xb), _to_torch(xq), _to_torch(I)
     if Q.ndim == 1:
         Q, ids = Q.reshape(1, -1), ids.reshape(1, -1)
     _require(X.ndim == 2 and Q.ndim == 2 and Q.shape[1] == X.shape[1], "xb and xq need the same dimension")
     _require(ids.shape[0] == Q.shape[0], "one row of ids per query")
-    dev = "cuda" if torch.cuda.is_available() else "cpu"
+    dev = torch.device("cuda" if torch.cuda.is_available() else "cpu")
     nq, k = ids.shape
-    pick = (
-        torch.arange(nq)
-        if sample is None or sample >= nq
-        else torch.randperm(nq, generator=torch.Generator().manual_seed(seed))[:sample]
-    )
-    Qs = Q[pick.to(Q.device)].to(dev).double()
-    got_ids = ids[pick.to(ids.device)].to(dev).long()
+    if sample is None or sample >= nq:
+        chosen = torch.arange(nq)
+    else:
+        chosen = torch.randperm(nq, generator=torch.Generator().manual_seed(seed))[:sample]
+    Qs = Q[chosen.to(Q.device)].to(dev, torch.float64)
+    got = ids[chosen.to(ids.device)].to(dev, torch.int64)
     if metric == "cosine":
-        Qs = Qs / Qs.norm(dim=1, keepdim=True)
-
-    def coarse(q, rows):
-        if metric == "l2":
-            return (q * q).sum(1, keepdim=True) + (rows * rows).sum(1)[None] - 2.0 * q @ rows.T
+        Qs = Qs / torch.linalg.vector_norm(Qs, dim=1, keepdim=True)
+    ns, n = Qs.shape[0], X.shape[0]
+    # the returned ids must be k distinct valid rows
+    ok = ((got >= 0) & (got < n)).all(1)
+    srt = got.sort(1).values
+    ok &= (srt[:, 1:] != srt[:, :-1]).all(1)
+    # exact scores of the returned rows, sorted: the bounds r_i
+    rows = X[got.clamp(0, n - 1).reshape(-1).to(X.device)].to(dev, torch.float64).reshape(ns, k, -1)
+    if metric == "l2":
+        r = (Qs[:, None, :] - rows).square().sum(-1)
+    else:
         if metric == "cosine":
-            rows = rows / rows.norm(dim=1, keepdim=True)
-        return -(q @ rows.T)
-
-    def exact(cand):
-        rows = X[cand.clamp_min(0).reshape(-1).to(X.device)].to(dev).double().reshape(*cand.shape, -1)
-        if metric == "l2":
-            s = ((Qs[:, None, :] - rows) ** 2).sum(-1)
-        else:
-            if metric == "cosine":
-                rows = rows / rows.norm(dim=-1, keepdim=True)
-            s = -(rows * Qs[:, None, :]).sum(-1)
-        return torch.where(cand >= 0, s, torch.full_like(s, float("inf")))
-
-    kc = min(k + 32, X.shape[0])
-    cv = torch.full((Qs.shape[0], kc), float("inf"), dtype=torch.float64, device=dev)
-    ci = torch.full((Qs.shape[0], kc), -1, dtype=torch.int64, device=dev)
-    chunk = max(1, (1 << 28) // (8 * X.shape[1]))
-    for i in range(0, X.shape[0], chunk):
-        s = coarse(Qs, X[i : i + chunk].to(dev).double())
-        idx = torch.arange(i, i + s.shape[1], device=dev).expand(s.shape[0], -1)
-        top = torch.topk(torch.cat([cv, s], 1), kc, dim=1, largest=False)
-        cv, ci = top.values, torch.gather(torch.cat([ci, idx], 1), 1, top.indices)
-    best = exact(ci).sort(1).values[:, :k]
-    got = exact(got_ids).sort(1).values
-    tol = 1e-9 * best.abs().amax(1, keepdim=True).clamp_min(1e-30)
-    return float(((got - best).abs() <= tol).all(1).float().mean())
+            rows = rows / torch.linalg.vector_norm(rows, dim=-1, keepdim=True)
+        r = -(rows * Qs[:, None, :]).sum(-1)
+    r = r.sort(1).values
+    bound = (r - 1e-9 * r.abs().amax(1, keepdim=True).clamp_min(1e-30)).contiguous()
+    # under[q, j] = rows of query q whose score lies below exactly the bounds j, j + 1, ..., k - 1
+    under = torch.zeros((ns, k + 1), dtype=torch.int64, device=dev)
+    per_chunk = max(1, (1 << 26) // max(1, ns * X.shape[1]))
+    for _, s in _exact_scores(X, Qs, dev, metric, per_chunk):
+        first = torch.searchsorted(bound, s.contiguous(), right=True)  # bounds <= the score
+        under.scatter_add_(1, first, torch.ones_like(first))
+    below = torch.cumsum(under, 1)[:, :k]  # below[:, i] = rows scoring under bound i
+    ok &= (below <= torch.arange(k, device=dev)).all(1)
+    return float(ok.double().mean())

@@ -175,3 +175,82 @@ def test_probe_coarse_groups(gpu, metric):
     idx.add(torch.from_numpy(X).cuda())
     D, I = search(idx, Q, 10, probe_lists=1)
     check(X, Q[:64], 10, metric, D[:64], I[:64])
+
+
+def nearest_removed(X, Q, metric):
+    """Ids of every query's nearest neighbour, and the removal mask that takes them all out."""
+    _, nn = oracle.knn(X, Q, 1, metric)
+    gone = np.unique(nn[:, 0])
+    removed = np.zeros(len(X), np.uint8)
+    removed[gone] = 1
+    return gone, removed
+
+
+def test_listed_anchors_follow_ids(gpu):
+    """Anchor j of an index stored in list order is id j * stride, read from that id's stored row.
+    With stride 1 every id is an anchor: removing each query's nearest neighbour must take its
+    anchor out too, for the thresholds without the probe (all from anchors) and under a bitmap
+    filter (which the probe does not serve)."""
+    X, Q = data.mixture_u8(30_000, seed=110), data.mixture_u8(300, seed=111)
+    idx = certex.Index(128, n_lists=64, anchor_stride=1)
+    idx.add(torch.from_numpy(X).cuda())
+    gone, removed = nearest_removed(X, Q, "l2")
+    idx.remove(torch.from_numpy(gone))
+    for k in (1, 10):
+        D, I = search(idx, Q, k, probe_lists=0)
+        check(X, Q, k, "l2", D, I, removed=removed)
+    km = np.random.default_rng(112).random((len(Q), len(X))) < 0.5
+    D, I = search(idx, Q, 10, filter=torch.from_numpy(km))
+    bits = np.packbits(km.reshape(-1), bitorder="little")
+    bits = np.pad(bits, (0, (-bits.size) % 4)).view(np.uint32)
+    check(X, Q, 10, "l2", D, I, removed=removed, bitmap=bits)
+    keep = np.random.default_rng(113).random(len(X)) < 0.5
+    D, I = search(idx, Q, 10, filter=torch.from_numpy(keep))
+    check(X, Q, 10, "l2", D, I, removed=(removed.astype(bool) | ~keep).astype(np.uint8))
+
+
+@pytest.mark.parametrize("stride", [1, 4])
+def test_listed_float_anchors_after_load(gpu, tmp_path, stride):
+    """A float index in list order with removals, saved and loaded (the anchor copy is gathered
+    again from the stored rows): searches without the probe take their thresholds from the anchors
+    and must still equal the oracle."""
+    X, Q = data.powerlaw_unit(20_000, 96, seed=114), data.powerlaw_unit(200, 96, seed=115)
+    idx = certex.Index(96, n_lists=50, anchor_stride=stride)
+    idx.add(torch.from_numpy(X).cuda())
+    gone, removed = nearest_removed(X, Q, "l2")
+    idx.remove(torch.from_numpy(gone))
+    D, I = search(idx, Q, 10, probe_lists=0)
+    check(X, Q, 10, "l2", D, I, removed=removed)
+    idx.save(tmp_path / "flisted.idx")
+    back = certex.Index.load(tmp_path / "flisted.idx")
+    for probe in (0, 2):
+        D, I = search(back, Q, 10, probe_lists=probe)
+        check(X, Q, 10, "l2", D, I, removed=removed)
+
+
+@pytest.mark.parametrize("kind", ["uint8", "float32"])
+def test_list_order(gpu, tmp_path, kind):
+    """list_order is a permutation of the ids (tests/test_exact.py:479-486): rows of the build in
+    list order, later rows in id order; searching stored vectors in that order finds themselves."""
+    if kind == "uint8":
+        X = data.uniform_int(20_000, 32, 116)
+    else:
+        X = np.random.default_rng(116).standard_normal((20_000, 32)).astype(np.float32)
+    idx = certex.Index(32, n_lists=16)
+    idx.add(torch.from_numpy(X[:18_000]).cuda())
+    idx.add(torch.from_numpy(X[18_000:]).cuda())
+    order = idx.list_order()
+    assert order.dtype == torch.int64 and order.is_cuda
+    o = order.cpu().numpy()
+    np.testing.assert_array_equal(np.sort(o), np.arange(20_000))
+    np.testing.assert_array_equal(o[18_000:], np.arange(18_000, 20_000))
+    assert not np.array_equal(o[:18_000], np.arange(18_000))  # the build's rows moved into lists
+    D, I = search(idx, X[o[:200]], 1)
+    np.testing.assert_array_equal(I[:, 0], o[:200])
+    idx.save(tmp_path / "order.idx")
+    back = certex.Index.load(tmp_path / "order.idx")
+    np.testing.assert_array_equal(back.list_order().cpu().numpy(), o)
+    with pytest.raises(ValueError):
+        plain = certex.Index(32)
+        plain.add(torch.from_numpy(X).cuda())
+        plain.list_order()
