@@ -111,6 +111,23 @@ CUVS_EXPORT cuvsError_t cuvsCertexSearch(cuvsResources_t res,
                                          DLManagedTensor* distances,
                                          cuvsFilter filter);
 
+/**
+ * cuvsCertexSearch with no device or pinned host memory allocated during the call. It has no
+ * counterpart in the reference; it is for callers that cannot allocate (tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, checks and results as cuvsCertexSearch. The
+ * scratch is one fixed 128 MiB device array per GPU, held from the library's load on that GPU
+ * until the process ends; larger batches are split into smaller ones, and a search that needs more
+ * than 128 MiB for a single query returns CUVS_ERROR. Calls that overlap on one GPU (from several
+ * threads or streams) share that array and race: issue them one at a time per GPU.
+ */
+CUVS_EXPORT cuvsError_t cuvsCertexSearchNoAlloc(cuvsResources_t res,
+                                                cuvsCertexSearchParams_t params,
+                                                cuvsCertexIndex_t index,
+                                                DLManagedTensor* queries,
+                                                DLManagedTensor* neighbors,
+                                                DLManagedTensor* distances,
+                                                cuvsFilter filter);
+
 /** Exact k nearest neighbours among the vectors of each query's label (certex.h:195-201). */
 CUVS_EXPORT cuvsError_t cuvsCertexSearchWithLabels(cuvsResources_t res,
                                                    cuvsCertexSearchParams_t params,

@@ -193,6 +193,20 @@ void search(cuvs::resources const& res, search_params const& params, index<T> co
             matrix_view<const T> queries, int64_t* neighbors, float* distances, int64_t k,
             filter f = {});
 
+/**
+ * The search above, with no device or pinned memory allocated during the call (no counterpart in
+ * the reference; for callers that cannot allocate, such as tight serving loops). Its scratch is a
+ * fixed array of no_alloc_scratch_bytes() (128 MiB) per GPU, held from the library's load on that
+ * GPU until the process ends; batches that need more are split. Calls that overlap on one GPU
+ * share that array and race: run one at a time per GPU. Throws when a single query needs more.
+ */
+template <typename T>
+void search_without_allocation(cuvs::resources const& res, search_params const& params,
+                               index<T> const& idx, matrix_view<const T> queries,
+                               int64_t* neighbors, float* distances, int64_t k, filter f = {});
+/** Bytes of the per-GPU scratch array of search_without_allocation. */
+auto no_alloc_scratch_bytes() -> size_t;
+
 /** Exact k nearest neighbours of every query among the vectors of its label (device int32). */
 template <typename T>
 void search(cuvs::resources const& res, search_params const& params, index<T> const& idx,

@@ -129,6 +129,15 @@ def lib():
                         P(DLManagedTensor),
                         Filter,
                     ],
+                    "cuvsCertexSearchNoAlloc": [
+                        ctypes.c_size_t,
+                        P(SearchParams),
+                        P(IndexHandle),
+                        P(DLManagedTensor),
+                        P(DLManagedTensor),
+                        P(DLManagedTensor),
+                        Filter,
+                    ],
                     "cuvsCertexSearchWithLabels": [
                         ctypes.c_size_t,
                         P(SearchParams),

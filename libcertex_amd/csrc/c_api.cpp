@@ -358,13 +358,20 @@ cuvsError_t cuvsCertexPartitionByLabels(cuvsResources_t res, cuvsCertexIndex_t i
   });
 }
 
-cuvsError_t cuvsCertexSearch(cuvsResources_t res,
-                             cuvsCertexSearchParams_t params,
-                             cuvsCertexIndex_t index,
-                             DLManagedTensor* queries,
-                             DLManagedTensor* neighbors,
-                             DLManagedTensor* distances,
-                             cuvsFilter filter)
+}  // extern "C"
+
+namespace {
+
+/** cuvsCertexSearch and cuvsCertexSearchNoAlloc: checks of the tensors and the filter, then the
+ *  search (reference certex.cpp:113-143, 292-311). */
+cuvsError_t search_c(cuvsResources_t res,
+                     cuvsCertexSearchParams_t params,
+                     cuvsCertexIndex_t index,
+                     DLManagedTensor* queries,
+                     DLManagedTensor* neighbors,
+                     DLManagedTensor* distances,
+                     cuvsFilter filter,
+                     bool no_alloc)
 {
   return translate([=] {
     auto& r      = res_of(res);
@@ -396,9 +403,39 @@ cuvsError_t cuvsCertexSearch(cuvsResources_t res,
       } else {
         certex::expects(filter.type == NO_FILTER, "certex: unsupported filter type");
       }
-      certex::search<T>(r, p, idx, q, nb, ds, k, f);
+      if (no_alloc) {
+        certex::search_without_allocation<T>(r, p, idx, q, nb, ds, k, f);
+      } else {
+        certex::search<T>(r, p, idx, q, nb, ds, k, f);
+      }
     });
   });
+}
+
+}  // namespace
+
+extern "C" {
+
+cuvsError_t cuvsCertexSearch(cuvsResources_t res,
+                             cuvsCertexSearchParams_t params,
+                             cuvsCertexIndex_t index,
+                             DLManagedTensor* queries,
+                             DLManagedTensor* neighbors,
+                             DLManagedTensor* distances,
+                             cuvsFilter filter)
+{
+  return search_c(res, params, index, queries, neighbors, distances, filter, false);
+}
+
+cuvsError_t cuvsCertexSearchNoAlloc(cuvsResources_t res,
+                                    cuvsCertexSearchParams_t params,
+                                    cuvsCertexIndex_t index,
+                                    DLManagedTensor* queries,
+                                    DLManagedTensor* neighbors,
+                                    DLManagedTensor* distances,
+                                    cuvsFilter filter)
+{
+  return search_c(res, params, index, queries, neighbors, distances, filter, true);
 }
 
 cuvsError_t cuvsCertexSearchWithLabels(cuvsResources_t res,

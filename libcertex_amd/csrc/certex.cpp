@@ -1086,7 +1086,7 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
 template <typename T>
 void search_impl(cuvs::resources const& res, search_params const& params, index<T> const& idx,
                  matrix_view<const T> queries, int64_t* neighbors, float* distances, int64_t k,
-                 certex_amd::filter_args fa)
+                 certex_amd::filter_args fa, bool no_alloc = false)
 {
   index_state const& st = idx.state();
   expects(queries.on_device, "certex: the queries must be in device memory");
@@ -1099,10 +1099,14 @@ void search_impl(cuvs::resources const& res, search_params const& params, index<
   const int64_t bs   = std::max(1, params.batch_size);
   const size_t qrow  = size_t(st.dim) * sizeof(T);
   const batch_fn batch = is_int(st.type) ? search_batch_int : search_batch_float;
+  // a search without allocation screens label queries through the label filter: routing a
+  // batch over the label partition stages its tables in pinned host memory
+  const bool route = fa.kind == 3 && st.label_part.n > 0 && !no_alloc;
   std::function<void(int64_t, int64_t)> run = [&](int64_t b0, int64_t B) {
+    if (no_alloc) { res.state().arena_reset(); }
     try {
       const char* q = reinterpret_cast<const char*>(queries.data) + size_t(b0) * qrow;
-      if (fa.kind == 3 && st.label_part.n > 0) {
+      if (route) {
         routed_batch(res, st, batch, q, qrow, B, int(k), fa.query_labels + b0, neighbors + b0 * k,
                      distances + b0 * k, fa, params);
       } else {
@@ -1114,7 +1118,7 @@ void search_impl(cuvs::resources const& res, search_params const& params, index<
       run(b0, B / 2);
       run(b0 + B / 2, B - B / 2);
     } catch (std::bad_alloc const&) {
-      if (B < 2) { throw; }
+      if (B < 2 || no_alloc) { throw; }
       res.sync();
       run(b0, B / 2);
       run(b0 + B / 2, B - B / 2);
@@ -1126,7 +1130,82 @@ void search_impl(cuvs::resources const& res, search_params const& params, index<
   }
 }
 
+/**
+ * Device scratch of the searches that allocate nothing (search_without_allocation): one array per
+ * GPU, allocated when the library's code object is loaded on that GPU and held until the process
+ * ends. Host code must not pass `scratch` itself (on the host it is a stand-in symbol, not a device
+ * address): scratch_of() returns the device address of each GPU's copy.
+ */
+constexpr size_t kNoAllocScratchBytes = size_t(128) << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+char* g_scratch[kMaxDevices] = {};
+
+/** The device address of `device`'s scratch array, looked up once per device with it current. */
+auto scratch_of(int device) -> char*
+{
+  expects(device >= 0 && device < kMaxDevices, "certex: device ordinal out of range");
+  std::lock_guard lk(g_scratch_mutex);
+  if (g_scratch[device] == nullptr) {
+    int current = 0;
+    CERTEX_HIP_TRY(hipGetDevice(&current));
+    if (current != device) { CERTEX_HIP_TRY(hipSetDevice(device)); }
+    void* ptr             = nullptr;
+    const hipError_t err  = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (current != device) { CERTEX_HIP_TRY(hipSetDevice(current)); }
+    CERTEX_HIP_TRY(err);
+    expects(ptr != nullptr, "certex: no device address for the scratch array");
+    g_scratch[device] = static_cast<char*>(ptr);
+  }
+  return g_scratch[device];
+}
+
+/** Arena mode of the resources for the duration of one call (restored on every exit). */
+struct arena_scope {
+  cuvs::detail::resources_state& rs;
+  arena_scope(cuvs::detail::resources_state& r, char* base, size_t bytes) : rs(r)
+  {
+    expects(rs.arena == nullptr, "certex: a search without allocation is already running on these resources");
+    rs.arena       = base;
+    rs.arena_bytes = bytes;
+    rs.arena_reset();
+  }
+  ~arena_scope()
+  {
+    rs.arena_reset();
+    rs.arena       = nullptr;
+    rs.arena_bytes = 0;
+  }
+};
+
 }  // namespace
+
+auto no_alloc_scratch_bytes() -> size_t { return kNoAllocScratchBytes; }
+
+template <typename T>
+void search_without_allocation(cuvs::resources const& res, search_params const& params,
+                               index<T> const& idx, matrix_view<const T> queries,
+                               int64_t* neighbors, float* distances, int64_t k, filter f)
+{
+  certex_amd::filter_args fa{};
+  if (f.type != filter::kind::none) {
+    expects(f.words != nullptr, "certex: a filter needs its words");
+    fa.kind      = f.type == filter::kind::bitset ? 1 : 2;
+    fa.words     = f.words;
+    fa.bitmap_ld = idx.size();
+  }
+  char* base = scratch_of(res.device());
+  arena_scope scope(res.state(), base, kNoAllocScratchBytes);
+  try {
+    search_impl(res, params, idx, queries, neighbors, distances, k, fa, true);
+  } catch (batch_too_large const&) {
+    throw std::runtime_error(
+      "certex: one query of this search needs more than the 128 MiB scratch of a search without "
+      "allocation; use the allocating search");
+  }
+}
 
 void stats_begin()
 {
@@ -1816,6 +1895,9 @@ void deserialize(cuvs::resources const& res, std::string const& filename, index<
                               int64_t);                                                        \
   template void partition_by_labels<T>(cuvs::resources const&, index<T>*);                     \
   template void list_order<T>(cuvs::resources const&, index<T> const&, int32_t*);              \
+  template void search_without_allocation<T>(cuvs::resources const&, search_params const&,     \
+                                             index<T> const&, matrix_view<const T>, int64_t*,  \
+                                             float*, int64_t, filter);                         \
   template void search<T>(cuvs::resources const&, search_params const&, index<T> const&,       \
                           matrix_view<const T>, int64_t*, float*, int64_t, filter);            \
   template void search<T>(cuvs::resources const&, search_params const&, index<T> const&,       \

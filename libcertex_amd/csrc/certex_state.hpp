@@ -112,6 +112,8 @@ enum ws_slot : int {
   ws_n_slots
 };
 
+[[noreturn]] inline void throw_too_large() { throw cuvs::neighbors::certex::batch_too_large(); }
+
 struct resources_state {
   int device          = 0;
   hipStream_t stream  = nullptr;
@@ -123,9 +125,32 @@ struct resources_state {
   void* host_stage    = nullptr;  // pinned host staging of the routing tables (grow-only)
   size_t host_stage_bytes = 0;
 
+  // Arena mode (searches that allocate nothing): while `arena` is set, get() carves the slots
+  // out of [arena, arena + arena_bytes) instead of the owned buffers, and a request that does
+  // not fit throws batch_too_large (the search then halves its batch and starts the arena over).
+  // Work is stream-ordered, so a batch may reuse what the previous batch of the stream carved.
+  char* arena        = nullptr;
+  size_t arena_bytes = 0;
+  size_t arena_used  = 0;
+  void* carved[ws_n_slots]        = {};
+  size_t carved_bytes[ws_n_slots] = {};
+
+  /** Forget every carved slot: the next batch carves from the start of the arena. */
+  void arena_reset()
+  {
+    arena_used = 0;
+    for (int i = 0; i < ws_n_slots; ++i) {
+      carved[i]       = nullptr;
+      carved_bytes[i] = 0;
+    }
+  }
+
   /** Pinned host staging of at least `bytes` bytes (grow-only; waits for the stream first). */
   void* stage(size_t bytes)
   {
+    if (arena != nullptr) {
+      throw std::logic_error("certex: a search without allocation cannot stage host memory");
+    }
     if (host_stage_bytes < bytes) {
       CERTEX_HIP_TRY(hipStreamSynchronize(stream));
       if (host_stage != nullptr) { CERTEX_HIP_TRY(hipHostFree(host_stage)); }
@@ -141,6 +166,15 @@ struct resources_state {
   /** Scratch slot of at least `bytes` bytes (grow-only; waits for the stream before growing). */
   void* get(int slot, size_t bytes)
   {
+    if (arena != nullptr) {
+      if (carved_bytes[slot] >= bytes) { return carved[slot]; }
+      const size_t n = (bytes + 255) / 256 * 256;
+      if (n > arena_bytes - arena_used) { throw_too_large(); }
+      carved[slot]       = arena + arena_used;
+      carved_bytes[slot] = n;
+      arena_used += n;
+      return carved[slot];
+    }
     device_buffer& b = slots[slot];
     if (b.bytes < bytes) {
       CERTEX_HIP_TRY(hipStreamSynchronize(stream));
