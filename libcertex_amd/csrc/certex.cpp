@@ -11,6 +11,7 @@
 #include "certex_state.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <functional>
@@ -29,6 +30,9 @@ resources::resources(void* stream) : s_(std::make_unique<detail::resources_state
     s_->owns_stream = true;
   }
   CERTEX_HIP_TRY(hipHostMalloc(&s_->host_small, 64, hipHostMallocDefault));
+  if (const char* cap = std::getenv("CERTEX_SCRATCH_SLOT_CAP")) {
+    s_->slot_cap = size_t(std::strtoull(cap, nullptr, 10));
+  }
 }
 
 resources::~resources()

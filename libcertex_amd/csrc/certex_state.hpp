@@ -124,6 +124,9 @@ struct resources_state {
   void* host_small    = nullptr;  // pinned host words for counters read back by the host
   void* host_stage    = nullptr;  // pinned host staging of the routing tables (grow-only)
   size_t host_stage_bytes = 0;
+  // test hook: a slot request above this many bytes fails as an allocation failure would
+  // (environment variable CERTEX_SCRATCH_SLOT_CAP, read when the resources are created; 0 = none)
+  size_t slot_cap = 0;
 
   // Arena mode (searches that allocate nothing): while `arena` is set, get() carves the slots
   // out of [arena, arena + arena_bytes) instead of the owned buffers, and a request that does
@@ -175,6 +178,7 @@ struct resources_state {
       arena_used += n;
       return carved[slot];
     }
+    if (slot_cap > 0 && bytes > slot_cap) { throw std::bad_alloc(); }
     device_buffer& b = slots[slot];
     if (b.bytes < bytes) {
       CERTEX_HIP_TRY(hipStreamSynchronize(stream));

@@ -1,65 +1,76 @@
-"""Config 5's kind of workload at a scale one test can afford: 100,000,000 x 128 uint8 rows (the
-config 2 / 5 mixture), with an extend of 1,000,000 rows and a removal of 1,000,000 random ids
-running while searches run (reference tests/test_updates: searches during updates return exact
-results over a snapshot of the live set). Checked by a GPU fp64 brute force, which is exact for
-8-bit data (every distance is an integer below 2^23): ids bit-exact with ties to the lower id.
+"""Full-size workloads of configs 2 and 5 under the GPU tests, checked by an exact GPU brute force
+(tests/exact_gpu.py: fp64 is exact for 8-bit data; ids bit-exact with ties to the lower id).
+
+Config 2 runs at its full size: 10,000,000 x 128 uint8 rows of the config 2 mixture, all 10,000
+queries in one batch, every id row checked.
+
+Config 5's workload runs at 100,000,000 rows (a tenth of config 5's rows, which one test can afford):
+4,096 k-means lists probed 2 per query (config 5's setting), and while searches run another thread
+extends the index by 1,000,000 rows (two additions) and removes 1,000,000 random ids. As in the
+reference's SearchDuringExtend (cpp/tests/neighbors/ann_certex/test_updates.cu:504-591), every
+search made during the updates must equal the exact top k of one published snapshot of the index;
+afterwards all 1,000 queries must equal the brute force over the live rows.
 """
 
 import threading
 
-import numpy as np
 import pytest
 import torch
 
 import libcertex_amd as certex
 from tests import data
+from tests.exact_gpu import topk_u8
 
 pytestmark = pytest.mark.gpu
 
-N, N_NEW, N_GONE, K = 100_000_000, 1_000_000, 1_000_000, 10
+K = 10
 
 
-def brute_force(X, live, Q, k, chunk=250_000):
-    """Exact (distance, id) top k of Q over the live rows of X, ties to the lower id: distances are
-    integers below 2^23 and ids below 2^30, so distance * 2^30 + id is exact in fp64."""
-    Qd = Q.double()
-    qq = (Qd * Qd).sum(1, keepdim=True)
-    best = torch.empty((Q.shape[0], 0), dtype=torch.float64, device="cuda")
-    for c in range(0, X.shape[0], chunk):
-        Xc = X[c : c + chunk].double()
-        d = qq + (Xc * Xc).sum(1)[None] - 2.0 * (Qd @ Xc.T)
-        key = d * float(1 << 30) + torch.arange(c, c + Xc.shape[0], device="cuda", dtype=torch.float64)[None]
-        key[:, ~live[c : c + chunk]] = float("inf")
-        best = torch.topk(torch.cat([best, key], 1), k, dim=1, largest=False).values
-    ids = torch.remainder(best, float(1 << 30)).long()
-    dist = torch.floor(best / float(1 << 30))
-    return dist, ids
+def test_config2_full_size(gpu):
+    # the bench's data: the same generators and chunks
+    X = data.mixture_u8_cuda(10_000_000, seed=2, chunk=1 << 20)
+    Q = data.mixture_u8_cuda(10_000, seed=3, chunk=1 << 20)
+    idx = certex.Index(128)
+    idx.add(X)
+    D, I = idx.search(Q, k=K, batch=10_000)
+    torch.cuda.synchronize()
+    ((dist, ids),) = topk_u8(X, Q, K, chunk=50_000)
+    assert torch.equal(I, ids)
+    assert torch.equal(D.double(), dist)
 
 
-def test_hundred_million_rows_with_concurrent_updates(gpu):
+N, N_NEW, N_GONE, N_LISTS = 100_000_000, 1_000_000, 1_000_000, 4_096
+
+
+def test_config5_workload_lists_during_updates(gpu):
     X = data.mixture_u8_cuda(N + N_NEW, seed=2)
     Q = data.mixture_u8_cuda(1_000, seed=3)
-    idx = certex.Index(128)
-    for c in range(0, N, 10_000_000):
-        idx.add(X[c : c + 10_000_000])
+    idx = certex.Index(128, n_lists=N_LISTS, capacity=N + N_NEW)
+    idx.add(X[:N])
     torch.cuda.synchronize()
+    assert idx.core.lists == (N_LISTS, N)
     gone = torch.randperm(N, generator=torch.Generator().manual_seed(4))[:N_GONE].cuda()
+    half = N + N_NEW // 2
     errors, results = [], []
+    done = threading.Event()
 
     def writer():
         try:
             with torch.cuda.stream(torch.cuda.Stream()):
-                idx.add(X[N:])
+                idx.add(X[N:half])
+                idx.add(X[half:])
                 idx.remove(gone)
                 torch.cuda.current_stream().synchronize()
         except Exception as e:  # noqa: BLE001
             errors.append(e)
+        finally:
+            done.set()
 
     def reader():
         try:
             with torch.cuda.stream(torch.cuda.Stream()):
-                for _ in range(3):
-                    D, I = idx.search(Q[:256], k=K)
+                while not done.is_set() or len(results) < 3:
+                    D, I = idx.search(Q[:256], k=K, probe_lists=2)
                     torch.cuda.current_stream().synchronize()
                     results.append((D, I))
         except Exception as e:  # noqa: BLE001
@@ -72,19 +83,25 @@ def test_hundred_million_rows_with_concurrent_updates(gpu):
         t.join()
     assert not errors, errors[0]
     assert idx.core.size == N + N_NEW and idx.ntotal == N + N_NEW - N_GONE
+    assert idx.core.lists == (N_LISTS, N)
 
-    # every search during the updates: ascending, returned distances exact for the returned ids
-    Qd = Q[:256].double()
-    for D, I in results:
-        assert (I >= 0).all() and (I < N + N_NEW).all()
-        assert (D[:, 1:] >= D[:, :-1]).all()
-        exact = ((Qd[:, None, :] - X[I].double()) ** 2).sum(-1)
-        assert torch.equal(D.double(), exact)
-
-    # after the updates: every query against the live set
+    # the published snapshots: the build, each addition, then the removal
     live = torch.ones(N + N_NEW, dtype=torch.bool, device="cuda")
     live[gone] = False
-    D, I = idx.search(Q, k=K)
-    dist, ids = brute_force(X, live, Q, K)
-    assert torch.equal(I, ids)
-    assert torch.equal(D.double(), dist)
+    prefix = lambda n: torch.ones(n, dtype=torch.bool, device="cuda")  # noqa: E731
+    snaps = topk_u8(X, Q, K, live_masks=(prefix(N), prefix(half), None, live))
+    for D, I in results:
+        matches = [
+            j
+            for j, (dist, ids) in enumerate(snaps)
+            if torch.equal(I, ids[:256]) and torch.equal(D.double(), dist[:256])
+        ]
+        assert matches, "a search during the updates equals no published snapshot"
+
+    # after the updates: all queries against the live rows, with and without the probe
+    dist, ids = snaps[-1]
+    for probe in (2, 0):
+        D, I = idx.search(Q, k=K, probe_lists=probe)
+        torch.cuda.synchronize()
+        assert torch.equal(I, ids)
+        assert torch.equal(D.double(), dist)
