@@ -88,6 +88,29 @@ def timed_steps(step, steps, warmup):
 
 
 PHASES = ("anchors", "threshold", "screen", "verify_topk")
+CPU_TARGET_S = 12.0  # CPU work of the baseline's timed sample, about
+
+
+def cpu_baseline(run, nq, first, what):
+    """The oracle timed on the host on a bounded sample: run(c) searches the first c queries and
+    returns their ids. `first` queries are timed first; the sample then grows to about CPU_TARGET_S
+    seconds of work (at most nq queries) and is timed again. Returns (record, c, ids)."""
+    import oracle
+
+    c = min(first, nq)
+    t0 = time.perf_counter()
+    ids = run(c)
+    t = time.perf_counter() - t0
+    if t < CPU_TARGET_S / 4 and c < nq:
+        c = int(min(nq, max(c + 1, c * CPU_TARGET_S / max(t, 1e-3))))
+        t0 = time.perf_counter()
+        ids = run(c)
+        t = time.perf_counter() - t0
+    rec = {"value": round(c / t, 3), "unit": "queries/s", "cores": oracle.threads(), "kind": "port",
+           "cpu": oracle.cpu_model(),
+           "sample": f"first {c} of the {nq} queries, {what} (oracle/oracle.c type-specialised scorers, "
+           f"OpenMP), {t:.1f} s"}
+    return rec, c, ids
 
 
 def hbm_roofline(kernel, bytes_per_launch, ms_per_launch, what):
@@ -157,15 +180,11 @@ def bench_config3(args):
 
         import oracle
 
-        cq = args.cpu_queries
-        t0 = time.perf_counter()
-        s_cpu, i_cpu = oracle.knn(X.cpu().numpy(), Q[:cq].cpu().numpy(), k, "cosine",
-                                  row_labels=lx.cpu().numpy(), query_labels=lq[:cq].cpu().numpy())
-        tc = time.perf_counter() - t0
-        agree = bool(np.array_equal(i_cpu, I[:cq].cpu().numpy()))
-        cpu = {"value": round(cq / tc, 3), "unit": "queries/s", "cores": oracle.threads(), "kind": "port",
-               "sample": f"first {cq} of the {nq} queries, exhaustive fp64 over all {n} rows with the label "
-               f"filter (oracle/oracle.c, OpenMP), {tc:.1f} s; ids equal to the GPU's: {agree}"}
+        Xh, Qh, lxh, lqh = X.cpu().numpy(), Q.cpu().numpy(), lx.cpu().numpy(), lq.cpu().numpy()
+        cpu, cq, i_cpu = cpu_baseline(
+            lambda c: oracle.knn(Xh, Qh[:c], k, "cosine", row_labels=lxh, query_labels=lqh[:c])[1], nq,
+            args.cpu_queries, f"exhaustive fp64 over all {n} rows with the label filter")
+        cpu["sample"] += f"; ids equal to the GPU's: {bool(np.array_equal(i_cpu, I[:cq].cpu().numpy()))}"
     return {
         "metric": "exact 100-NN queries/sec, 1M x 768 fp32 cosine, 16 labels, 1 MI355X",
         "value": round(nq / (ms_step / 1000.0), 1),
@@ -237,16 +256,13 @@ def bench_config4(args):
 
         import oracle
 
-        cq = args.cpu_queries
         # the keys of KV head 0 as the cache holds them (float32 holds bf16 exactly)
         head0 = torch.cat([kk[0] for kk in [first] + used], 0).float().cpu().numpy()
-        t0 = time.perf_counter()
-        s_cpu, i_cpu = oracle.knn(head0, q[0, :cq].float().cpu().numpy(), k, "ip")
-        tc = time.perf_counter() - t0
-        agree = bool(np.array_equal(i_cpu, ids[0, :cq].cpu().numpy()))
-        cpu = {"value": round(cq / tc, 3), "unit": "queries/s", "cores": oracle.threads(), "kind": "port",
-               "sample": f"first {cq} queries of query head 0 against KV head 0 ({head0.shape[0]} keys), "
-               f"exhaustive fp64 (oracle/oracle.c, OpenMP), {tc:.1f} s; ids equal to the GPU's: {agree}"}
+        q0 = q[0].float().cpu().numpy()
+        cpu, cq, i_cpu = cpu_baseline(
+            lambda c: oracle.knn(head0, q0[:c], k, "ip")[1], m, args.cpu_queries,
+            f"query head 0 against KV head 0 ({head0.shape[0]} keys), exhaustive fp64")
+        cpu["sample"] += f"; ids equal to the GPU's: {bool(np.array_equal(i_cpu, ids[0, :cq].cpu().numpy()))}"
     n_q = H * m
     # screen roofline per step: every query against the keys of its KV head (fp16 rows of 128
     # halves); the cache holds n + 256 (warmup + i + 1) keys per head in timed step i
@@ -520,21 +536,10 @@ def main():
 
         import oracle
 
-        cq = args.cpu_queries
-        Xh = X.cpu().numpy()
-        Qh = Q[:cq].cpu().numpy()
-        t0 = time.perf_counter()
-        s_cpu, i_cpu = oracle.knn(Xh, Qh, k, "l2")
-        tc = time.perf_counter() - t0
-        agree = bool(np.array_equal(i_cpu, I[:cq].cpu().numpy()))
-        cpu = {
-            "value": round(cq / tc, 3),
-            "unit": "queries/s",
-            "cores": oracle.threads(),
-            "kind": "port",
-            "sample": f"first {cq} of the {nq} queries against all {n} rows, exhaustive fp64 (oracle/oracle.c, "
-            f"OpenMP), {tc:.1f} s; ids equal to the GPU's: {agree}",
-        }
+        Xh, Qh = X.cpu().numpy(), Q.cpu().numpy()
+        cpu, cq, i_cpu = cpu_baseline(lambda c: oracle.knn(Xh, Qh[:c], k, "l2")[1], nq, args.cpu_queries,
+                                      f"exhaustive fp64 against all {n} rows")
+        cpu["sample"] += f"; ids equal to the GPU's: {bool(np.array_equal(i_cpu, I[:cq].cpu().numpy()))}"
 
     line = {
         "metric": "exact 10-NN queries/sec, 10M x 128 uint8 L2, 1 MI355X; screen % MFMA peak",

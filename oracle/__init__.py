@@ -40,12 +40,38 @@ def _load():
         lib.oracle_score.restype = dbl
         lib.oracle_threads.argtypes = []
         lib.oracle_threads.restype = i32
+        lib.oracle_set_generic.argtypes = [i32]
+        lib.oracle_set_generic.restype = i32
         _lib = lib
     return _lib
 
 
 def _ptr(a):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+class generic_scores:
+    """Inside the block, searches score through the generic per-coordinate scorer (oracle_score)
+    instead of the type-specialised ones; tests compare the two."""
+
+    def __enter__(self):
+        self.was = _load().oracle_set_generic(1)
+        return self
+
+    def __exit__(self, *exc):
+        _load().oracle_set_generic(self.was)
+        return False
+
+
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), for the CPU baseline's record."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def threads():

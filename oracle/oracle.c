@@ -20,6 +20,9 @@
  * removed ids never appear (tests/test_exact.py:83-84). Missing entries get id -1 and score +inf
  * (ann_certex.cuh:76-141 pads with -1).
  *
+ * The searches use type-specialised scorers (below) that give the same bits as oracle_score;
+ * tests/test_oracle.py checks them against it.
+ *
  * Pinned by tests/test_oracle.py: brute-force numpy on small inputs (integer data exactly), the
  * closed form for duplicates and ties, the reference's own known answers (verify = 2/3 after
  * corrupting 100 of 300 queries, test_exact.py:440-452) and the filter semantics.
@@ -99,6 +102,121 @@ double oracle_score(const void* q, const void* x, int dt, int64_t d, int metric)
 
 static int elem_size(int dt) { return dt == DT_F32 ? 4 : (dt == DT_F16 ? 2 : 1); }
 
+/*
+ * Type-specialised scorers: the same scores, bit for bit, without the per-coordinate type switch
+ * (they are what bench.py times as the CPU baseline). 8-bit data: every product and partial sum
+ * of the canonical order is an exact integer below 2^53, so an exact int32 sum converted to
+ * double equals it (d <= 32768 keeps |sum| below 2^31). Float data: the canonical order itself,
+ * with the 64 partial sums of one block of coordinates updated together so that the compiler
+ * vectorises across them; each partial still accumulates its coordinates in increasing order with
+ * one fused multiply-add each. target_clones picks AVX-512, AVX2 or the baseline at load time.
+ */
+#define CLONES __attribute__((target_clones("avx512f", "avx2", "default")))
+enum { MAX_FAST_INT_DIM = 32768 };
+
+CLONES static double score_u8(const void* qv, const void* xv, int64_t d, int metric)
+{
+  const uint8_t *q = (const uint8_t*)qv, *x = (const uint8_t*)xv;
+  int32_t acc = 0;
+  if (metric == M_L2) {
+    for (int64_t j = 0; j < d; ++j) {
+      const int32_t t = (int32_t)q[j] - (int32_t)x[j];
+      acc += t * t;
+    }
+    return (double)acc;
+  }
+  for (int64_t j = 0; j < d; ++j) { acc += (int32_t)q[j] * (int32_t)x[j]; }
+  return -(double)acc;
+}
+
+CLONES static double score_i8(const void* qv, const void* xv, int64_t d, int metric)
+{
+  const int8_t *q = (const int8_t*)qv, *x = (const int8_t*)xv;
+  int32_t acc = 0;
+  if (metric == M_L2) {
+    for (int64_t j = 0; j < d; ++j) {
+      const int32_t t = (int32_t)q[j] - (int32_t)x[j];
+      acc += t * t;
+    }
+    return (double)acc;
+  }
+  for (int64_t j = 0; j < d; ++j) { acc += (int32_t)q[j] * (int32_t)x[j]; }
+  return -(double)acc;
+}
+
+/* one float type: blocks of 64 coordinates, partial l takes coordinate 64 b + l */
+#define FLOAT_SCORER(name, T, load)                                                         \
+  CLONES static double name(const void* qv, const void* xv, int64_t d, int metric)          \
+  {                                                                                        \
+    const T *q = (const T*)qv, *x = (const T*)xv;                                          \
+    double acc[LANES], qq[LANES], xx[LANES];                                               \
+    for (int l = 0; l < LANES; ++l) { acc[l] = qq[l] = xx[l] = 0.0; }                      \
+    for (int64_t b = 0; b < d; b += LANES) {                                               \
+      const int m = d - b < LANES ? (int)(d - b) : LANES;                                  \
+      if (metric == M_L2) {                                                                \
+        for (int l = 0; l < m; ++l) {                                                      \
+          const double t = load(q[b + l]) - load(x[b + l]);                                \
+          acc[l]         = fma(t, t, acc[l]);                                              \
+        }                                                                                  \
+      } else {                                                                             \
+        for (int l = 0; l < m; ++l) {                                                      \
+          const double a = load(q[b + l]), c = load(x[b + l]);                             \
+          acc[l]         = fma(a, c, acc[l]);                                              \
+          if (metric == M_COSINE) {                                                        \
+            qq[l] = fma(a, a, qq[l]);                                                      \
+            xx[l] = fma(c, c, xx[l]);                                                      \
+          }                                                                                \
+        }                                                                                  \
+      }                                                                                    \
+    }                                                                                      \
+    const double s = combine(acc);                                                         \
+    if (metric == M_L2) { return s; }                                                      \
+    if (metric == M_INNER) { return -s; }                                                  \
+    return -s / sqrt(combine(qq) * combine(xx));                                           \
+  }
+
+#define LOAD_F32(v) ((double)(v))
+#define LOAD_F16(v) half_to_double(v)
+FLOAT_SCORER(score_f32, float, LOAD_F32)
+FLOAT_SCORER(score_f16, uint16_t, LOAD_F16)
+
+typedef double (*scorer_fn)(const void*, const void*, int64_t, int);
+
+static int g_generic = 0; /* tests: 1 = every score through oracle_score */
+
+/** Use the generic scorer (1) or the type-specialised ones (0); returns the previous setting. */
+int oracle_set_generic(int on)
+{
+  const int was = g_generic;
+  g_generic     = on;
+  return was;
+}
+
+static double generic_f32(const void* q, const void* x, int64_t d, int m) { return oracle_score(q, x, DT_F32, d, m); }
+static double generic_f16(const void* q, const void* x, int64_t d, int m) { return oracle_score(q, x, DT_F16, d, m); }
+static double generic_i8(const void* q, const void* x, int64_t d, int m) { return oracle_score(q, x, DT_I8, d, m); }
+static double generic_u8(const void* q, const void* x, int64_t d, int m) { return oracle_score(q, x, DT_U8, d, m); }
+
+/** The scorer of a type and metric: the generic one for cosine on 8-bit data and huge dims. */
+static scorer_fn scorer_of(int dt, int64_t d, int metric)
+{
+  const int integer = dt == DT_I8 || dt == DT_U8;
+  if (g_generic || (integer && (metric == M_COSINE || d > MAX_FAST_INT_DIM))) {
+    switch (dt) {
+      case DT_F32: return generic_f32;
+      case DT_F16: return generic_f16;
+      case DT_I8: return generic_i8;
+      default: return generic_u8;
+    }
+  }
+  switch (dt) {
+    case DT_F32: return score_f32;
+    case DT_F16: return score_f16;
+    case DT_I8: return score_i8;
+    default: return score_u8;
+  }
+}
+
 static int worse(double sa, int64_t ia, double sb, int64_t ib)
 {
   return sa > sb || (sa == sb && ia > ib);
@@ -147,7 +265,8 @@ void oracle_knn(const void* base, int dt, int64_t n, int64_t d, const void* quer
                 const uint32_t* bitmap, const int32_t* row_labels, const int32_t* query_labels,
                 double* out_score, int64_t* out_id)
 {
-  const int es = elem_size(dt);
+  const int es         = elem_size(dt);
+  const scorer_fn score = scorer_of(dt, d, metric);
 #pragma omp parallel for schedule(dynamic, 1)
   for (int64_t qi = 0; qi < nq; ++qi) {
     double* s   = (double*)malloc(sizeof(double) * (size_t)k);
@@ -162,7 +281,7 @@ void oracle_knn(const void* base, int dt, int64_t n, int64_t d, const void* quer
         if (!((bitmap[bit >> 5] >> (bit & 31)) & 1u)) { continue; }
       }
       if (row_labels && query_labels && row_labels[i] != query_labels[qi]) { continue; }
-      const double sc = oracle_score(q, (const char*)base + i * d * es, dt, d, metric);
+      const double sc = score(q, (const char*)base + i * d * es, d, metric);
       if (have < k) {
         s[have]  = sc;
         id[have] = i;
@@ -197,7 +316,8 @@ void oracle_knn(const void* base, int dt, int64_t n, int64_t d, const void* quer
 void oracle_scores_of(const void* base, int dt, int64_t n, int64_t d, const void* queries,
                       int64_t nq, int metric, int k, const int64_t* ids, double* out)
 {
-  const int es = elem_size(dt);
+  const int es         = elem_size(dt);
+  const scorer_fn score = scorer_of(dt, d, metric);
 #pragma omp parallel for schedule(static)
   for (int64_t qi = 0; qi < nq; ++qi) {
     const char* q = (const char*)queries + qi * d * es;
@@ -205,7 +325,7 @@ void oracle_scores_of(const void* base, int dt, int64_t n, int64_t d, const void
       const int64_t i     = ids[qi * k + j];
       out[qi * k + j] = (i < 0 || i >= n)
                           ? INFINITY
-                          : oracle_score(q, (const char*)base + i * d * es, dt, d, metric);
+                          : score(q, (const char*)base + i * d * es, d, metric);
     }
   }
 }

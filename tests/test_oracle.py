@@ -160,3 +160,34 @@ def test_verify_known_answer():
     wrong = I.copy()
     wrong[:100, 9] = (wrong[:100, 9] + 9_973) % X.shape[0]
     assert abs(verify(X, Q, wrong, sample=None) - 2 / 3) < 1e-6
+
+
+@pytest.mark.parametrize("dtype", [np.uint8, np.int8, np.float32, np.float16])
+@pytest.mark.parametrize("d", [5, 64, 100, 130, 257])
+def test_specialised_scorers_equal_the_generic_one(dtype, d):
+    """The searches score through type-specialised loops (exact int32 sums for 8-bit data, the
+    canonical 64-lane order vectorised for floats); they must give oracle_score's bits exactly,
+    ties and ids included."""
+    rng = np.random.default_rng(d)
+    if dtype in (np.uint8, np.int8):
+        info = np.iinfo(dtype)
+        X = rng.integers(info.min, info.max + 1, (2_000, d)).astype(dtype)
+        Q = rng.integers(info.min, info.max + 1, (16, d)).astype(dtype)
+        X[100:110] = X[5]  # exact ties
+        metrics = ("l2", "ip")
+    else:
+        X = (rng.standard_normal((2_000, d)) * 3).astype(dtype)
+        Q = (rng.standard_normal((16, d)) * 3).astype(dtype)
+        X[100:110] = X[5]
+        metrics = ("l2", "ip", "cosine")
+    for metric in metrics:
+        s1, i1 = oracle.knn(X, Q, 20, metric)
+        with oracle.generic_scores():
+            s0, i0 = oracle.knn(X, Q, 20, metric)
+        np.testing.assert_array_equal(i1, i0)
+        np.testing.assert_array_equal(s1.view(np.int64), s0.view(np.int64))
+        ids = np.tile(np.arange(0, 2_000, 100), (16, 1))
+        fast = oracle.scores_of(X, Q, ids, metric)
+        with oracle.generic_scores():
+            slow = oracle.scores_of(X, Q, ids, metric)
+        np.testing.assert_array_equal(fast.view(np.int64), slow.view(np.int64))
