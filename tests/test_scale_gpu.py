@@ -34,6 +34,7 @@ def test_config2_full_size(gpu):
     idx.add(X)
     D, I = idx.search(Q, k=K, batch=10_000)
     torch.cuda.synchronize()
+    print("config 2: searched 10,000 queries; brute force next", flush=True)
     ((dist, ids),) = topk_u8(X, Q, K, chunk=50_000)
     assert torch.equal(I, ids)
     assert torch.equal(D.double(), dist)
@@ -48,6 +49,7 @@ def test_config5_workload_lists_during_updates(gpu):
     idx = certex.Index(128, n_lists=N_LISTS, capacity=N + N_NEW)
     idx.add(X[:N])
     torch.cuda.synchronize()
+    print("config 5 workload: built 10^8 rows with 4,096 lists", flush=True)
     assert idx.core.lists == (N_LISTS, N)
     gone = torch.randperm(N, generator=torch.Generator().manual_seed(4))[:N_GONE].cuda()
     half = N + N_NEW // 2
@@ -82,6 +84,7 @@ def test_config5_workload_lists_during_updates(gpu):
     for t in threads:
         t.join()
     assert not errors, errors[0]
+    print(f"config 5 workload: {len(results)} searches during the updates; brute force next", flush=True)
     assert idx.core.size == N + N_NEW and idx.ntotal == N + N_NEW - N_GONE
     assert idx.core.lists == (N_LISTS, N)
 
