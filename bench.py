@@ -25,18 +25,36 @@ sys.path.insert(0, ROOT)
 
 P_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA peak, 10^12 ops/s
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "screen_i8_c2_traffic.txt")
+# the sources that decide the int8 screen's memory traffic; a traffic profile is stamped with their
+# hash and is used only while they are unchanged
+SCREEN_I8_SOURCES = ("kernels/screen.hip", "kernels/screen_common.hpp", "kernels.hpp")
+
+
+def sources_stamp(files=SCREEN_I8_SOURCES):
+    """First 16 hex digits of the SHA-256 over the given sources (paths under libcertex_amd/csrc)."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for f in files:
+        with open(os.path.join(ROOT, "libcertex_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
 
 
 def screen_traffic():
     """HBM bytes per screen launch at config 2, from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (calibrated against a plain copy); None when it is missing."""
+    WRITE_SIZE summary (calibrated against a plain copy). None when the summary is missing or was
+    measured on other screen sources than the ones built here (its sources stamp differs)."""
+    stamp, traffic = None, None
     try:
         for line in open(TRAFFIC_PROFILE):
+            if line.startswith("sources_stamp"):
+                stamp = line.split("=")[1].strip()
             if line.startswith("traffic_bytes_per_launch"):
-                return int(line.split("=")[1])
+                traffic = int(line.split("=")[1])
     except OSError:
-        pass
-    return None
+        return None
+    return traffic if stamp == sources_stamp() else None
 P_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA peak
 HBM_GBS = 8000.0
 
@@ -430,6 +448,70 @@ def bench_config5(args):
     }
 
 
+def summarize_profiles(dirs, warmup, steps, after=1):
+    """Text summary of rocprofv3 CSV output (kernel traces and counter collections) under `dirs`,
+    for a bench run of `warmup` + `steps` searches followed by `after` more (the survivor stats).
+    A kernel launched L times per search (calls = L * (warmup + steps + after)) is averaged over
+    all its launches and, separately, over the timed ones only (launches warmup * L up to
+    (warmup + steps) * L, in dispatch order); kernels with another call count (the build, data
+    generation) show '-' there. Durations in ms, counters per dispatch."""
+    import csv
+    import glob
+    import re
+    from collections import defaultdict
+
+    searches = warmup + steps + after
+
+    def short(name):  # "void ns::(anonymous namespace)::k<ns::T, 2>(args)" -> "k<T, 2>"
+        name = re.sub(r"^void ", "", name.strip())
+        depth, cut = 0, len(name)
+        for i, ch in enumerate(name):  # the first "(" outside template brackets opens the arguments
+            depth += ch == "<"
+            depth -= ch == ">"
+            if ch == "(" and depth == 0 and not name.startswith("(anonymous", i):
+                cut = i
+                break
+        return re.sub(r"(\(anonymous namespace\)::|\b\w+::)", "", name[:cut]).strip()
+
+    def timed(vals):
+        if len(vals) % searches:
+            return None
+        per = len(vals) // searches
+        sel = vals[warmup * per : (warmup + steps) * per]
+        return sum(sel) / len(sel) if sel else None
+
+    traces, counters = defaultdict(list), defaultdict(list)
+    for d in dirs:
+        for f in sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)):
+            for r in csv.DictReader(open(f)):
+                traces[short(r["Kernel_Name"])].append(
+                    (int(r["Dispatch_Id"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6))
+        for f in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
+            for r in csv.DictReader(open(f)):
+                counters[(short(r["Kernel_Name"]), r["Counter_Name"])].append(
+                    (int(r["Dispatch_Id"]), float(r["Counter_Value"])))
+    out = [f"# {searches} searches per run: {warmup} warm-up, {steps} timed, {after} after (stats)"]
+    if traces:
+        out.append(f"{'kernel':<64} {'calls':>5} {'total_ms':>10} {'avg_ms':>9} {'timed_avg_ms':>12} "
+                   f"{'min_ms':>8} {'max_ms':>8}")
+        rows = sorted(traces.items(), key=lambda kv: -sum(v for _, v in kv[1]))
+        for name, v in rows:
+            v.sort()
+            t = [x for _, x in v]
+            ta = timed(t)
+            out.append(f"{name[:64]:<64} {len(t):>5} {sum(t):>10.3f} {sum(t) / len(t):>9.4f} "
+                       f"{(f'{ta:.4f}' if ta is not None else '-'):>12} {min(t):>8.4f} {max(t):>8.4f}")
+    if counters:
+        out.append(f"{'kernel':<64} {'counter':<28} {'calls':>5} {'avg':>16} {'timed_avg':>16}")
+        for (name, cn), v in sorted(counters.items()):
+            v.sort()
+            t = [x for _, x in v]
+            ta = timed(t)
+            out.append(f"{name[:64]:<64} {cn:<28} {len(t):>5} {sum(t) / len(t):>16.1f} "
+                       f"{(f'{ta:.1f}' if ta is not None else '-'):>16}")
+    return "\n".join(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
@@ -447,7 +529,18 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--lists", type=int, default=-1, help="k-means lists (default: the config's; 0: none)")
     ap.add_argument("--probe", type=int, default=2, help="lists probed per query")
+    ap.add_argument("--summarize", nargs="+", metavar="DIR",
+                    help="print a summary of the rocprofv3 CSV output under DIR (of a run with the "
+                    "same --warmup and --steps) and exit; needs no GPU")
+    ap.add_argument("--stamp", action="store_true",
+                    help="print the sources stamp of the int8 screen (as traffic summaries record it) and exit")
     args = ap.parse_args()
+    if args.summarize:
+        print(summarize_profiles(args.summarize, args.warmup, args.steps))
+        return
+    if args.stamp:
+        print(sources_stamp())
+        return
     if args.gpus != 1:
         print(
             "bench.py measures one GPU: this build targets single-GPU boxes (the sharded search is a "
