@@ -21,6 +21,7 @@ ARCH = "gfx950"
 SOURCES = [
     "kernels/screen.hip",
     "kernels/screen_wide.hip",
+    "kernels/screen_tile.hip",
     "kernels/select.hip",
     "kernels/encode.hip",
     "kernels/partition.hip",

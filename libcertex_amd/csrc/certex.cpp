@@ -336,6 +336,9 @@ auto waves_of(index_state const& st) -> int64_t
   return certex_amd::screen_waves(!is_int(st.type), st.row_bytes);
 }
 
+/** The screen pass of fp16 rows of more than 128 halves runs the tiled kernel. */
+auto uses_tile_screen(index_state const& st) -> bool { return !is_int(st.type) && st.halves > 128; }
+
 /**
  * Anchor pass: every anchor of the index, or the partition's (routed) and the tail's, into the
  * columns [0, ap.n_groups) of a group table of row_len columns.
@@ -393,9 +396,15 @@ void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan 
 template <typename F>
 auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
 {
-  return [&st, route, launch](certex_amd::screen_args& sa, hipStream_t stream) {
+  // fp16 rows of more than 128 halves: the tiled screen, one tile of 256 rows per workgroup
+  const bool tiled = uses_tile_screen(st);
+  return [&st, route, launch, tiled](certex_amd::screen_args& sa, hipStream_t stream) {
+    auto chunk = [&](certex_amd::screen_args const& x) {
+      return tiled ? certex_amd::tile_chunk_steps()
+                   : plain_chunk(st, x.nq, x.nq_pad, x.n_scan, waves_of(st), kScreenChunk);
+    };
     if (route == nullptr) {
-      sa.chunk_steps = plain_chunk(st, sa.nq, sa.nq_pad, sa.n_scan, waves_of(st), kScreenChunk);
+      sa.chunk_steps = chunk(sa);
       launch(sa, stream);
       return;
     }
@@ -413,7 +422,7 @@ auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
       certex_amd::screen_args t = sa;
       t.row_base                = st.label_part.n;
       t.n_scan                  = tail;
-      t.chunk_steps = plain_chunk(st, t.nq, t.nq_pad, t.n_scan, waves_of(st), kScreenChunk);
+      t.chunk_steps             = chunk(t);
       launch(t, stream);
     }
   };
@@ -909,7 +918,7 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
     sa.theta = theta;
     all_rows = !screen_into_buckets(
       res, B, nq_pad, size, sa,
-      screen_pass(st, route, wide ? certex_amd::screen_f16_wide : certex_amd::screen_f16), count,
+      screen_pass(st, route, wide ? certex_amd::screen_f16_tile : certex_amd::screen_f16), count,
       rows, cap, &vals);
   }
   count_stats(res, st, B, all_rows, count, cap, true);
@@ -1038,19 +1047,23 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
       }
       return t;
     });
-  route.screen_chunk = pick_chunk(waves, kRoutedChunk, [&](int64_t c) {
-    int64_t t = 0;
-    for (auto const& e : gs) { t += certex_amd::screen_group_tiles(e.nq, e.nx, qb, int(c)); }
-    return t;
-  });
+  // the screen's groups: the tiled screen's query blocks and 256-row chunks for wide fp16 rows
+  const bool tiled = uses_tile_screen(st);
+  const int qbs    = tiled ? certex_amd::tile_block_queries() : qb;
+  route.screen_chunk =
+    tiled ? certex_amd::tile_chunk_steps() : pick_chunk(waves, kRoutedChunk, [&](int64_t c) {
+      int64_t t = 0;
+      for (auto const& e : gs) { t += certex_amd::screen_group_tiles(e.nq, e.nx, qb, int(c)); }
+      return t;
+    });
   for (auto& e : ga) {
     e.tile0            = certex_amd::screen_group_tile0(route.anchor_tiles, e.nq, qb);
     route.anchor_tiles = e.tile0 + certex_amd::screen_group_tiles(
                                      e.nq, (e.nx + stride - 1) / stride, qb, route.anchor_chunk);
   }
   for (auto& e : gs) {
-    e.tile0            = certex_amd::screen_group_tile0(route.screen_tiles, e.nq, qb);
-    route.screen_tiles = e.tile0 + certex_amd::screen_group_tiles(e.nq, e.nx, qb, route.screen_chunk);
+    e.tile0            = certex_amd::screen_group_tile0(route.screen_tiles, e.nq, qbs);
+    route.screen_tiles = e.tile0 + certex_amd::screen_group_tiles(e.nq, e.nx, qbs, route.screen_chunk);
   }
   route.n_route = int(gs.size());
 

@@ -219,11 +219,17 @@ void anchors_i8(const screen_args& a, hipStream_t stream);
 void screen_f16(const screen_args& a, hipStream_t stream);
 void anchors_f16(const screen_args& a, hipStream_t stream);
 /**
- * The fp16 passes for rows of more than 128 halves (a multiple of 128, at most kMaxF16Halves):
- * a K loop, workgroups of 8 waves; chunk_steps is a multiple of 8 (8 group_steps for anchors).
+ * The fp16 anchor pass for rows of more than 128 halves (a multiple of 128, at most
+ * kMaxF16Halves): a K loop, workgroups of 8 waves; chunk_steps is a multiple of 8 group_steps.
  */
-void screen_f16_wide(const screen_args& a, hipStream_t stream);
 void anchors_f16_wide(const screen_args& a, hipStream_t stream);
+/**
+ * The fp16 screen for rows of more than 128 halves as LDS-staged tiles: a workgroup multiplies
+ * 256 rows (chunk_steps = tile_chunk_steps()) with tile_block_queries() queries; row_stride 1.
+ */
+void screen_f16_tile(const screen_args& a, hipStream_t stream);
+int tile_block_queries();
+int tile_chunk_steps();
 
 /**
  * theta[q] = the k-th largest of gmax[q, 0 .. n_groups) (kKeepAll when n_groups < k, and never

@@ -1,0 +1,333 @@
+// fp16 certified screen for rows of more than 128 halves (gfx950): LDS-staged, double-buffered
+// tiles of rows and queries, both fed to the MFMA from LDS.
+//
+// Reference contract: detail/screen_sm80.cu:117-379 and detail/screen_sm90.cu:594-785 (fp16 MMA,
+// fp32 accumulation, keep a pair iff its screen value reaches the query threshold; the reference
+// stages 128 x 128 x 64 tiles). The certificate is the one of screen.hip: the row term enters as
+// the accumulator's initial value and the host folds every rounding error into the row term and
+// the threshold, so the test needs no per-pair arithmetic.
+//
+// Work decomposition:
+// - a workgroup of 4 waves computes one tile of 256 stored rows x TQ = 32 QT queries, all of the
+//   row's halves, in stages of 64 halves (128 bytes of every row and query);
+// - a stage of both operands is copied into LDS by global_load_lds_dwordx4 (no VGPRs, 8 lanes on
+//   one row's 128-byte line). The 16-byte chunk c of tile row r lands in slot c ^ (r & 7) of the
+//   row's 128 bytes: lane i of a copy writes slot i % 8 of row i / 8, so it reads chunk
+//   (i % 8) ^ (i / 8) of that row. The ds_read_b128 of a 16-row MFMA fragment is then free of bank
+//   conflicts (rows r and r + 8 share slots, and a b128 read serves 8 lanes per pass);
+// - two stage buffers: while the MFMAs run on stage s, the copies of stage s + 1 are in flight; one
+//   barrier per stage both publishes a stage and frees the other buffer. Within a stage the copies
+//   and the LDS reads of the second MFMA half are issued between the row tiles of the first half
+//   (pinned with sched_group_barrier), so that their issue and latency hide behind MFMAs;
+// - the waves form a 2 x 2 grid: wave (wr, wq) multiplies tile rows 128 wr .. 128 wr + 127 (8 row
+//   tiles) with tile queries 16 QT wq .. (QT query tiles), v_mfma_f32_16x16x32_f16, the row tiles as
+//   operand A: 32 QT accumulator registers per lane (AGPRs at one wave per SIMD);
+// - MFMA kk (0, 1) of a stage takes chunk 4 kk + lane / 16 of a lane's row and query (the same
+//   permutation of the summation order in both operands);
+// - after the last stage the staging LDS holds the survivor list. Per query tile a lane has 32
+//   rows; the wave reserves its survivors with one LDS atomic (exclusive prefix of the lanes'
+//   counts from one ballot + mbcnt per bit of the count), the lanes park their 32 screen values in
+//   LDS and write each survivor with its value read back by bit index (a per-survivor select over
+//   registers cost twice as much), then one flush per workgroup moves the list into the per-query
+//   buckets (flush_hits of screen_common.hpp).
+// Workgroup b runs on XCD b % 8; the query blocks of one row tile run on one XCD (work_of), so a
+// row tile is fetched from HBM about once.
+
+#include "screen_common.hpp"
+
+#include <algorithm>
+#include <stdexcept>
+#include <type_traits>
+
+namespace certex_amd {
+namespace {
+
+using namespace screen_detail;
+
+constexpr int kTileWaves = 4;
+constexpr int kTileRows  = 256;              // stored rows of a tile (4 steps of 64)
+constexpr int kStageB    = 128;              // bytes of a row per stage (64 halves)
+constexpr int kTileSteps = kTileRows / kStepRows;
+
+typedef const __attribute__((address_space(1))) void* gptr;
+typedef __attribute__((address_space(3))) void* lptr;
+
+/** s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): this wave's global loads,
+ *  LDS-DMA copies included, have completed. */
+__device__ __forceinline__ void wait_copies() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
+/** LDS bytes of a workgroup of TQ queries: two stage buffers of (256 + TQ) rows x 128 bytes. */
+constexpr int tile_lds(int tq) { return 2 * (kTileRows + tq) * kStageB; }
+
+/** Survivor list entries that fit the staging LDS: 12 bytes each plus the flush's rank word,
+ *  after the flush's 2 TQ counters and the waves' 8 KB of parked screen values. */
+constexpr int tile_hit_cap(int tq) { return (tile_lds(tq) - kTileWaves * 8192 - 8 * tq) / 16 / 64 * 64; }
+
+template <int QT, bool FILT>
+__global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_args a)
+{
+  using R           = f16_rows;
+  using acc_t       = v4f;
+  using frag_t      = v8h;
+  constexpr int TQ  = 32 * QT;
+  constexpr int BUF = (kTileRows + TQ) * kStageB;  // one stage buffer: rows, then queries
+  constexpr int CAP = tile_hit_cap(TQ);
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ uint32_t n_hits;
+
+  const int tid  = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wr   = wave >> 1;  // row half of the tile
+  const int wq   = wave & 1;   // query half of the tile
+
+  const screen_work w = work_of<TQ>(a, blockIdx.x);
+  if (!w.valid) { return; }
+  const int RB          = a.row_bytes;  // bytes per row: a multiple of 128
+  const int n_stages    = RB / kStageB;
+  const int64_t scan0   = w.chunk * kTileRows;  // scan index of tile row 0
+  const int64_t n_rows  = w.n_scan - scan0 < kTileRows ? w.n_scan - scan0 : kTileRows;
+  const int64_t n_q     = w.q_end - w.q0 < TQ ? w.q_end - w.q0 : TQ;
+
+  if (tid == 0) { n_hits = 0; }
+
+  // this lane's copy offsets: rows of copies j = 0..7 (tile rows (8 wave + j) * 8 + lane / 8), and
+  // queries of copies j = 0..QT-1 (tile queries (QT wave + j) * 8 + lane / 8); rows and queries
+  // past the tile's live ones repeat its last live one (their results are never kept)
+  const int crow   = lane >> 3;
+  const int cchunk = (lane & 7) ^ crow;
+  const char* rbase = reinterpret_cast<const char*>(a.codes) +
+                      (w.base + scan0 * a.row_stride) * int64_t(RB) + cchunk * 16;
+  const char* qbase = reinterpret_cast<const char*>(a.qcodes) + w.q0 * int64_t(RB) + cchunk * 16;
+  uint32_t roff[8], qoff[QT];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    int64_t r = (wave * 8 + j) * 8 + crow;
+    r         = r < n_rows ? r : n_rows - 1;
+    roff[j]   = uint32_t(r * a.row_stride * RB);
+  }
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    int64_t q = (wave * QT + j) * 8 + crow;
+    q         = q < n_q ? q : n_q - 1;
+    qoff[j]   = uint32_t(q * RB);
+  }
+  // copy j (0 .. 8 + QT - 1) of stage s: rows for j < 8, queries after; the LDS destination is
+  // wave-uniform (scalar: M0)
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  auto copy = [&](int s, int j) {
+    uint8_t* buf = lds + (s & 1) * BUF;
+    if (j < 8) {
+      __builtin_amdgcn_global_load_lds((gptr)(rbase + s * kStageB + roff[j]),
+                                       (lptr)(buf + ((wave_u * 8 + j) * 8) * kStageB), 16, 0, 0);
+    } else {
+      __builtin_amdgcn_global_load_lds(
+        (gptr)(qbase + s * kStageB + qoff[j - 8]),
+        (lptr)(buf + (kTileRows + (wave_u * QT + j - 8) * 8) * kStageB), 16, 0, 0);
+    }
+  };
+  auto issue = [&](int s) {
+#pragma unroll
+    for (int j = 0; j < 8 + QT; ++j) { copy(s, j); }
+  };
+
+  // accumulators start at the row terms (dead past the tile's live rows)
+  const float* rowc = static_cast<const float*>(a.rowc);
+  acc_t acc[8][QT];
+#pragma unroll
+  for (int bt = 0; bt < 8; ++bt) {
+    acc_t c;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t r = wr * 128 + bt * 16 + (lane >> 4) * 4 + j;
+      const bool ok   = r < n_rows;
+      const float v   = rowc[w.base + (scan0 + (ok ? r : 0)) * a.row_stride];
+      c[j]            = ok ? v : R::dead();
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = c; }
+  }
+
+  // fragment addresses within a stage buffer: row tile bt, query tile qt, chunk 4 kk + lane / 16
+  const int frow = lane & 15;
+  auto a_frag    = [&](const uint8_t* buf, int bt, int kk) {
+    const int r = wr * 128 + bt * 16 + frow;
+    const int c = kk * 4 + (lane >> 4);
+    return *reinterpret_cast<const frag_t*>(buf + r * kStageB + ((c ^ (r & 7)) << 4));
+  };
+  auto b_frag = [&](const uint8_t* buf, int qt, int kk) {
+    const int t = wq * 16 * QT + qt * 16 + frow;
+    const int c = kk * 4 + (lane >> 4);
+    return *reinterpret_cast<const frag_t*>(buf + (kTileRows + t) * kStageB + ((c ^ (t & 7)) << 4));
+  };
+
+  // one stage: the fragments of the first MFMA half are read up front; between the row tiles of
+  // the first half come the reads of the second half's fragments and (COPY) the copies of stage
+  // s + 1, so that their issue and latency hide behind MFMAs. The schedule is pinned with
+  // sched_group_barrier (DS read 0x100, VMEM read 0x020, MFMA 0x008).
+  auto stage = [&](int s, auto copy_next) {
+    constexpr bool COPY = decltype(copy_next)::value;
+    wait_copies();
+    __syncthreads();
+    const uint8_t* buf = lds + (s & 1) * BUF;
+    frag_t ar[2][8], bq[2][QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) { bq[0][qt] = b_frag(buf, qt, 0); }
+#pragma unroll
+    for (int bt = 0; bt < 8; ++bt) { ar[0][bt] = a_frag(buf, bt, 0); }
+    __builtin_amdgcn_sched_group_barrier(0x100, QT + 8, 0);
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int bt = 0; bt < 8; ++bt) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = R::mfma(ar[0][bt], bq[0][qt], acc[bt][qt]); }
+      __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);
+      ar[1][bt] = a_frag(buf, bt, 1);
+      if (bt < QT) {
+        bq[1][bt] = b_frag(buf, bt, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      if constexpr (COPY) {
+        copy(s + 1, 2 * bt);
+        copy(s + 1, 2 * bt + 1);
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+      }
+    }
+#pragma unroll
+    for (int bt = 0; bt < 8; ++bt) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = R::mfma(ar[1][bt], bq[1][qt], acc[bt][qt]); }
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+  static_assert(8 + QT == 16, "two copies per row tile of the first half");
+
+  issue(0);
+  for (int s = 0; s + 1 < n_stages; ++s) { stage(s, std::true_type{}); }
+  stage(n_stages - 1, std::false_type{});
+  wait_copies();
+  __syncthreads();  // the staging LDS becomes the survivor list
+
+  uint32_t* hit_q    = reinterpret_cast<uint32_t*>(lds);
+  uint32_t* hit_row  = hit_q + CAP;
+  float* hit_val     = reinterpret_cast<float*>(hit_row + CAP);
+  uint32_t* scratch  = reinterpret_cast<uint32_t*>(hit_val + CAP);  // 2 TQ + CAP words
+  // per wave 8 KB: a lane's 32 screen values of one query tile, 16-byte slot bt ^ (lane & 7) of
+  // its 128 bytes, so that the survivor loop reads a value by its bit index
+  uint8_t* vals      = lds + tile_lds(TQ) - kTileWaves * 8192 + wave * 8192 + lane * 128;
+  const float* theta = static_cast<const float*>(a.theta);
+  const int64_t row0 = w.base + scan0 + wr * 128 + (lane >> 4) * 4;  // stored row of bit 0
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qloc = wq * 16 * QT + qt * 16 + frow;
+    // a padding query keeps nothing: no value compares >= NaN
+    const float th = qloc < n_q ? theta[w.q0 + qloc] : R::keep_none();
+    uint32_t bits  = 0;  // bit bt * 4 + r: row row0 + 16 bt + r
+#pragma unroll
+    for (int bt = 0; bt < 8; ++bt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) { bits |= uint32_t(acc[bt][qt][r] >= th) << (bt * 4 + r); }
+    }
+    if (!__any(bits != 0)) { continue; }
+    if constexpr (FILT) {
+      uint32_t scan = bits;
+      while (scan) {
+        const int j = __builtin_ctz(scan);
+        scan &= scan - 1;
+        if (!keeps(a.filter, w.q0 + qloc, uint32_t(row0 + (j >> 2) * 16 + (j & 3)))) {
+          bits &= ~(1u << j);
+        }
+      }
+    }
+#pragma unroll
+    for (int bt = 0; bt < 8; ++bt) {
+      *reinterpret_cast<acc_t*>(vals + ((bt ^ (lane & 7)) << 4)) = acc[bt][qt];
+    }
+    const uint32_t cnt = uint32_t(__builtin_popcount(bits));
+    uint32_t excl = 0, total = 0;
+#pragma unroll
+    for (int b = 0; b < 6; ++b) {
+      const uint64_t m = __ballot((cnt >> b) & 1u);
+      excl += __builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)) << b;
+      total += uint32_t(__builtin_popcountll(m)) << b;
+    }
+    if (total == 0) { continue; }
+    const int leader = __builtin_ctzll(__ballot(1));
+    uint32_t base    = 0;
+    if (lane == leader) { base = atomicAdd(&n_hits, total); }
+    uint32_t pos = uint32_t(__builtin_amdgcn_readlane(int(base), leader)) + excl;
+    while (bits != 0) {
+      const int j        = __builtin_ctz(bits);
+      bits &= bits - 1;
+      const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
+      const float val    = *reinterpret_cast<const float*>(vals + ((((j >> 2) ^ (lane & 7)) << 4) | ((j & 3) << 2)));
+      if (pos < uint32_t(CAP)) {
+        hit_q[pos]   = uint32_t(qloc);
+        hit_row[pos] = row;
+        hit_val[pos] = val;
+      } else if (int64_t(pos - CAP) < a.spill_cap) {
+        const int64_t e = int64_t(blockIdx.x) * a.spill_cap + int64_t(pos - CAP);
+        a.spill_q[e]    = uint32_t(qloc);
+        a.spill_row[e]  = row;
+        a.spill_val[e]  = val;
+      } else {
+        const int64_t q   = w.q0 + qloc;
+        const uint32_t at = atomicAdd(a.cand_count + q, 1u);
+        if (at < a.cap) {
+          a.cand_rows[q * a.cap + at] = row;
+          a.cand_vals[q * a.cap + at] = val;
+        }
+      }
+      ++pos;
+    }
+  }
+  __syncthreads();
+  flush_hits<true>(w.q0, TQ, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(CAP), scratch);
+}
+
+template <int QT, bool FILT>
+void launch_qt(const screen_args& a, hipStream_t stream)
+{
+  constexpr int TQ = 32 * QT;
+  int64_t blocks   = 0;
+  if (a.groups != nullptr) {
+    blocks = a.n_tiles;
+  } else {
+    const int64_t n_steps  = screen_steps(a.n_scan);
+    const int64_t n_chunks = (n_steps + kTileSteps - 1) / kTileSteps;
+    const int64_t n_qb     = (a.nq + TQ - 1) / TQ;
+    blocks                 = n_steps == 0 ? 0 : 8 * n_qb * ((n_chunks + 7) / 8);
+  }
+  if (blocks == 0) { return; }
+  if (a.chunk_steps != kTileSteps || a.row_stride != 1 || a.row_bytes % kStageB != 0) {
+    throw std::logic_error("certex: the tiled screen needs chunks of 4 steps over rows of 128-byte multiples");
+  }
+  screen_args b = a;
+  b.spill_cap   = a.spill_q != nullptr ? a.spill_pool / blocks : 0;
+  auto* k       = &screen_tile_kernel<QT, FILT>;
+  const int lds = tile_lds(TQ);
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) {
+    (void)hipGetLastError();
+    throw std::runtime_error("certex: the tiled screen cannot reserve its LDS");
+  }
+  k<<<dim3(unsigned(blocks)), 64 * kTileWaves, lds, stream>>>(b);
+}
+
+}  // namespace
+
+int tile_block_queries() { return 32 * 8; }
+int tile_chunk_steps() { return kTileSteps; }
+
+void screen_f16_tile(const screen_args& a, hipStream_t stream)
+{
+  if (a.filter.kind != 0) {
+    launch_qt<8, true>(a, stream);
+  } else {
+    launch_qt<8, false>(a, stream);
+  }
+}
+
+}  // namespace certex_amd

@@ -1,10 +1,9 @@
-// fp16 certified screen for rows of more than 128 halves (gfx950): a K loop over the coordinates.
+// fp16 anchor pass for rows of more than 128 halves (gfx950): a K loop over the coordinates.
 //
-// Reference contract: detail/screen_sm80.cu:117-379 and detail/screen_sm90.cu:594-785 (fp16 MMA,
-// fp32 accumulation, keep a pair iff its screen value reaches the query threshold) and the anchor
-// pass of detail/kernels.hpp:125-135. The certificate is the one of screen.hip: the row term
-// enters as the accumulator's initial value and the host folds every rounding error into the
-// row term and the threshold, so the test needs no per-pair arithmetic.
+// Reference contract: the anchor groups of detail/kernels.hpp:125-135 and detail/screen_sm80.cu:
+// 304-372 (fp16 MMA, fp32 accumulation, the best screen value of every group of anchors for every
+// query). The screen pass of such rows is screen_tile.hip. The certificate is the one of
+// screen.hip: the row term enters as the accumulator's initial value.
 //
 // Work decomposition:
 // - a workgroup of 8 waves holds QB = 16 QT queries (all their halves) in LDS for its whole life,
@@ -20,7 +19,8 @@
 //   pipeline serves a quad that shares a line at once, and 16 lanes on 16 rows one line at a
 //   time), and 4 ds_bpermute per 16 bytes move them to the MFMA's lanes;
 // - block b runs on XCD b % 8; the query blocks of one row chunk run on one XCD together.
-// Survivors go through the ballot + mbcnt compaction of screen_common.hpp.
+// Group maxima (and the rows holding them) go to the group table, per coarse group of anchor
+// steps or per fine group of 4 anchors.
 
 #include "screen_common.hpp"
 
@@ -42,26 +42,20 @@ __device__ __forceinline__ v8h gload(gbytes p)
   return *reinterpret_cast<const __attribute__((address_space(1))) v8h*>(p);
 }
 
-template <int QT, bool ANCHORS, bool FILT>
-__global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_args a, int hc)
+template <int QT, bool FILT>
+__global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_args a)
 {
   using R      = f16_rows;
   using acc_t  = v4f;
   using frag_t = v8h;
   constexpr int QB = 16 * QT;
-  // dynamic LDS: the queries [QB][H] halves (swizzled), then the survivor list of hc entries
+  // dynamic LDS: the queries [QB][H] halves (swizzled)
   extern __shared__ __attribute__((aligned(16))) uint8_t qlds[];
-  __shared__ float thl[ANCHORS ? 1 : QB];
-  __shared__ float gml[ANCHORS ? kWideWaves * QB : 1];
-  __shared__ uint32_t gmr[ANCHORS ? kWideWaves * QB : 1];
-  __shared__ uint32_t n_hits;
-  uint32_t* hit_q   = reinterpret_cast<uint32_t*>(qlds + QB * a.row_bytes);
-  uint32_t* hit_row = hit_q + hc;
-  float* hit_val    = reinterpret_cast<float*>(hit_row + hc);
+  __shared__ float gml[kWideWaves * QB];
+  __shared__ uint32_t gmr[kWideWaves * QB];
 
-  const float* rowc  = static_cast<const float*>(a.rowc);
-  const float* theta = static_cast<const float*>(a.theta);
-  float* gmax        = static_cast<float*>(a.gmax);
+  const float* rowc = static_cast<const float*>(a.rowc);
+  float* gmax       = static_cast<float*>(a.gmax);
 
   const int tid   = threadIdx.x;
   const int lane  = tid & 63;
@@ -78,19 +72,11 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
   const int64_t w0      = w.chunk * a.chunk_steps + wave * eighth;
   const int64_t w1      = w0 + eighth < n_steps ? w0 + eighth : n_steps;
 
-  if (tid == 0) { n_hits = 0; }
   stage_queries<64 * kWideWaves>(a.qcodes, RB, q0, w.q_end, QB, qlds,
                                  [](int r, int c) { return c ^ (r & 15); });
-  if constexpr (ANCHORS) {
-    for (int e = tid; e < kWideWaves * QB; e += 64 * kWideWaves) {
-      gml[e] = R::lowest();
-      gmr[e] = 0xffffffffu;
-    }
-  } else {
-    for (int e = tid; e < QB; e += 64 * kWideWaves) {
-      // a padding query keeps nothing: no value compares >= NaN (not even a +inf row term)
-      thl[e] = q0 + e < w.q_end ? theta[q0 + e] : R::keep_none();
-    }
+  for (int e = tid; e < kWideWaves * QB; e += 64 * kWideWaves) {
+    gml[e] = R::lowest();
+    gmr[e] = 0xffffffffu;
   }
   __syncthreads();
 
@@ -210,94 +196,51 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
 
     const int64_t row0 = s * kStepRows + (lane >> 4) * 4;
     step_labels SL;  // the label filter's row labels of the step
-    if constexpr (ANCHORS && FILT) { load_step_labels(a, w, row0, SL); }
-    if constexpr (ANCHORS) {
-      if (a.fine) {
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-          const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
-          const int64_t q    = q0 + qt * 16 + (lane & 15);
-          const int64_t qc   = q < w.q_end ? q : w.q_end - 1;  // padding: any live query's
-          const uint32_t kp  = FILT ? filter_mask(a, w, SL, qc, row0) : 0u;
-          anchor_tile_fine<R, FILT>(col, row0, q, q < w.q_end, a, w, gmax, kp);
-        }
-      } else {
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-          const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
-          const int64_t q    = q0 + qt * 16 + (lane & 15);
-          const int64_t qc   = q < w.q_end ? q : w.q_end - 1;  // padding: any live query's
-          const uint32_t kp  = FILT ? filter_mask(a, w, SL, qc, row0) : 0u;
-          anchor_tile<R, FILT>(col, row0, q, wave * QB + qt * 16 + lane, a, w, gml, gmr, kp);
-        }
-      }
-      // end of an anchor group (group_steps steps, aligned to the wave's range)
-      if (!a.fine && ((s + 1) % a.group_steps == 0 || s + 1 == n_steps)) {
-        for (int e = lane; e < QB; e += 64) {
-          if (q0 + e < w.q_end) {
-            const int64_t t = table_entry(a, q0 + e, s / a.group_steps);
-            gmax[t]         = gml[wave * QB + e];
-            a.grow[t]       = gmr[wave * QB + e];
-          }
-          gml[wave * QB + e] = R::lowest();
-          gmr[wave * QB + e] = 0xffffffffu;
-        }
-      }
-    } else {
-      float mq[QT];
-      bool hit = false;
+    if constexpr (FILT) { load_step_labels(a, w, row0, SL); }
+    if (a.fine) {
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
-        float m = acc[0][qt][0];
-#pragma unroll
-        for (int bt = 0; bt < 4; ++bt) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) { m = fmaxf(m, acc[bt][qt][r]); }
-        }
-        mq[qt] = m;
-        hit |= m >= thl[qt * 16 + (lane & 15)];
+        const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
+        const int64_t q    = q0 + qt * 16 + (lane & 15);
+        const int64_t qc   = q < w.q_end ? q : w.q_end - 1;  // padding: any live query's
+        const uint32_t kp  = FILT ? filter_mask(a, w, SL, qc, row0) : 0u;
+        anchor_tile_fine<R, FILT>(col, row0, q, q < w.q_end, a, w, gmax, kp);
       }
-      if (__builtin_expect(__any(hit), 0)) {
+    } else {
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-          const float th = thl[qt * 16 + (lane & 15)];
-          if (!__any(mq[qt] >= th)) { continue; }
-          uint32_t bits = 0;
-#pragma unroll
-          for (int bt = 0; bt < 4; ++bt) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              bits |= uint32_t(acc[bt][qt][r] >= th) << (bt * 4 + r);
-            }
-          }
-          const float v16[16] = {acc[0][qt][0], acc[0][qt][1], acc[0][qt][2], acc[0][qt][3],
-                                 acc[1][qt][0], acc[1][qt][1], acc[1][qt][2], acc[1][qt][3],
-                                 acc[2][qt][0], acc[2][qt][1], acc[2][qt][2], acc[2][qt][3],
-                                 acc[3][qt][0], acc[3][qt][1], acc[3][qt][2], acc[3][qt][3]};
-          push_hits<16, FILT, true>(bits, uint32_t(qt * 16 + (lane & 15)), w.base + row0, q0, a,
-                                    hit_q, hit_row, hit_val, &n_hits, uint32_t(hc), v16);
+      for (int qt = 0; qt < QT; ++qt) {
+        const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
+        const int64_t q    = q0 + qt * 16 + (lane & 15);
+        const int64_t qc   = q < w.q_end ? q : w.q_end - 1;  // padding: any live query's
+        const uint32_t kp  = FILT ? filter_mask(a, w, SL, qc, row0) : 0u;
+        anchor_tile<R, FILT>(col, row0, q, wave * QB + qt * 16 + lane, a, w, gml, gmr, kp);
+      }
+    }
+    // end of an anchor group (group_steps steps, aligned to the wave's range)
+    if (!a.fine && ((s + 1) % a.group_steps == 0 || s + 1 == n_steps)) {
+      for (int e = lane; e < QB; e += 64) {
+        if (q0 + e < w.q_end) {
+          const int64_t t = table_entry(a, q0 + e, s / a.group_steps);
+          gmax[t]         = gml[wave * QB + e];
+          a.grow[t]       = gmr[wave * QB + e];
         }
+        gml[wave * QB + e] = R::lowest();
+        gmr[wave * QB + e] = 0xffffffffu;
       }
     }
   }
-
-  if constexpr (!ANCHORS) {
-    __syncthreads();
-    flush_hits<true>(q0, QB, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(hc),
-                     reinterpret_cast<uint32_t*>(qlds));
-  }
 }
 
-template <int QT, bool ANCHORS, bool FILT>
-void launch_qt(const screen_args& a, dim3 grid, size_t lds, int hc, hipStream_t stream)
+template <int QT, bool FILT>
+void launch_qt(const screen_args& a, dim3 grid, size_t lds, hipStream_t stream)
 {
-  auto* k = &screen_wide_kernel<QT, ANCHORS, FILT>;
+  auto* k = &screen_wide_kernel<QT, FILT>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(k),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess) {
     (void)hipGetLastError();
-    throw std::runtime_error("certex: the wide screen cannot reserve its LDS");
+    throw std::runtime_error("certex: the wide anchor pass cannot reserve its LDS");
   }
-  k<<<grid, 64 * kWideWaves, lds, stream>>>(a, hc);
+  k<<<grid, 64 * kWideWaves, lds, stream>>>(a);
 }
 
 /** LDS bytes a workgroup may use. */
@@ -315,37 +258,20 @@ int max_lds()
   return v;
 }
 
-/** Static LDS of the screen (thresholds, count) and a margin. */
-constexpr int kWideFixed = 16 * 6 * 4 + 512;
-/** Most survivor list entries (hit_q, hit_row, hit_val: 12 bytes each). */
-constexpr int kWideMaxHits = 8192;
-
 /**
- * Query tiles of a workgroup for rows of `row_bytes`: the largest of 6, 4, 2 whose queries and a
- * survivor list of kHitCap entries fit the LDS (0: none fits); the list takes the rest of the LDS.
- * More queries per workgroup means more work per row fetched; survivors past the list go to the
- * workgroup's spill region, so a short list costs little (measured at d = 768: 96 queries and
- * 1,280 entries ran the screen in 2.20 ms, 64 queries and 5,376 entries in 2.40 ms).
+ * Query tiles of a workgroup for rows of `row_bytes`: the largest of 6, 4, 2 whose queries and
+ * the group tables (gml, gmr: 8 bytes per query per wave) fit the LDS (0: none fits). More queries
+ * per workgroup means more work per row fetched.
  */
 int wide_query_tiles(int row_bytes)
 {
   for (int qt : {6, 4, 2}) {
-    if (16 * qt * row_bytes + 12 * kHitCap + kWideFixed <= max_lds()) { return qt; }
+    if (16 * qt * (row_bytes + 8 * kWideWaves) <= max_lds()) { return qt; }
   }
   return 0;
 }
 
-/** Survivor list entries of a screen workgroup of qt query tiles over rows of row_bytes. */
-int wide_hit_cap(int qt, int row_bytes)
-{
-  const int qbytes = 16 * qt * row_bytes;
-  int hc           = (max_lds() - qbytes - kWideFixed) / 12;
-  hc               = std::min(hc, kWideMaxHits);
-  hc               = std::min(hc, qbytes / 4 - 32 * qt);  // the flush ranks in the queries' space
-  return hc / 64 * 64;
-}
-
-template <bool ANCHORS, bool FILT>
+template <bool FILT>
 void launch(const screen_args& a, hipStream_t stream)
 {
   const int qt = wide_query_tiles(a.row_bytes);
@@ -362,14 +288,11 @@ void launch(const screen_args& a, hipStream_t stream)
   }
   if (blocks == 0) { return; }
   const dim3 grid{unsigned(blocks)};
-  const int hc     = ANCHORS ? 0 : wide_hit_cap(qt, a.row_bytes);
-  const size_t lds = size_t(qb) * size_t(a.row_bytes) + size_t(hc) * 12;
-  screen_args b    = a;
-  b.spill_cap      = !ANCHORS && a.spill_q != nullptr ? a.spill_pool / blocks : 0;
+  const size_t lds = size_t(qb) * size_t(a.row_bytes);
   switch (qt) {
-    case 6: launch_qt<6, ANCHORS, FILT>(b, grid, lds, hc, stream); break;
-    case 4: launch_qt<4, ANCHORS, FILT>(b, grid, lds, hc, stream); break;
-    default: launch_qt<2, ANCHORS, FILT>(b, grid, lds, hc, stream); break;
+    case 6: launch_qt<6, FILT>(a, grid, lds, stream); break;
+    case 4: launch_qt<4, FILT>(a, grid, lds, stream); break;
+    default: launch_qt<2, FILT>(a, grid, lds, stream); break;
   }
 }
 
@@ -377,21 +300,12 @@ void launch(const screen_args& a, hipStream_t stream)
 
 int wide_block_queries(int row_bytes) { return 16 * wide_query_tiles(row_bytes); }
 
-void screen_f16_wide(const screen_args& a, hipStream_t stream)
-{
-  if (a.filter.kind != 0) {
-    launch<false, true>(a, stream);
-  } else {
-    launch<false, false>(a, stream);
-  }
-}
-
 void anchors_f16_wide(const screen_args& a, hipStream_t stream)
 {
   if (a.filter.kind != 0) {
-    launch<true, true>(a, stream);
+    launch<true>(a, stream);
   } else {
-    launch<true, false>(a, stream);
+    launch<false>(a, stream);
   }
 }
 
