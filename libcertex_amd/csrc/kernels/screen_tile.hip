@@ -8,8 +8,9 @@
 // the threshold, so the test needs no per-pair arithmetic.
 //
 // Work decomposition:
-// - a workgroup of 4 waves computes one tile of 256 stored rows x TQ = 32 QT queries, all of the
-//   row's halves, in stages of 64 halves (128 bytes of every row and query);
+// - a workgroup of 4 waves computes one tile of 256 stored rows x TQ = 32 QT queries (QT = 8, or 7
+//   when that pads the batch's label groups less), all of the row's halves, in stages of 64 halves
+//   (128 bytes of every row and query);
 // - a stage of both operands is copied into LDS by global_load_lds_dwordx4 (no VGPRs, 8 lanes on
 //   one row's 128-byte line). The 16-byte chunk c of tile row r lands in slot c ^ (r & 7) of the
 //   row's 128 bytes: lane i of a copy writes slot i % 8 of row i / 8, so it reads chunk
@@ -190,9 +191,14 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
       if constexpr (COPY) {
-        copy(s + 1, 2 * bt);
-        copy(s + 1, 2 * bt + 1);
-        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+        if (2 * bt + 1 < 8 + QT) {
+          copy(s + 1, 2 * bt);
+          copy(s + 1, 2 * bt + 1);
+          __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+        } else if (2 * bt < 8 + QT) {
+          copy(s + 1, 2 * bt);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
       }
     }
 #pragma unroll
@@ -202,7 +208,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
     }
     __builtin_amdgcn_s_setprio(0);
   };
-  static_assert(8 + QT == 16, "two copies per row tile of the first half");
+  static_assert(8 + QT <= 16, "at most two copies per row tile of the first half");
 
   issue(0);
   for (int s = 0; s + 1 < n_stages; ++s) { stage(s, std::true_type{}); }
@@ -318,15 +324,33 @@ void launch_qt(const screen_args& a, hipStream_t stream)
 
 }  // namespace
 
-int tile_block_queries() { return 32 * 8; }
 int tile_chunk_steps() { return kTileSteps; }
+
+int tile_query_tiles(const int64_t* nq, int n)
+{
+  // cost of a workgroup tile ~ its MFMA work (TQ) plus half its LDS copies (256 + TQ), both
+  // measured as comparable limits at config 3; padding queries cost as much as live ones
+  double best = 0;
+  int pick    = 8;
+  for (int qt : {8, 7}) {
+    const int tq = 32 * qt;
+    double c     = 0;
+    for (int i = 0; i < n; ++i) { c += double((nq[i] + tq - 1) / tq) * (tq + 0.5 * (kTileRows + tq)); }
+    if (qt == 8 || c < best) {
+      best = c;
+      pick = qt;
+    }
+  }
+  return pick;
+}
 
 void screen_f16_tile(const screen_args& a, hipStream_t stream)
 {
-  if (a.filter.kind != 0) {
-    launch_qt<8, true>(a, stream);
-  } else {
-    launch_qt<8, false>(a, stream);
+  const bool filt = a.filter.kind != 0;
+  switch (a.tile_qt) {
+    case 8: filt ? launch_qt<8, true>(a, stream) : launch_qt<8, false>(a, stream); break;
+    case 7: filt ? launch_qt<7, true>(a, stream) : launch_qt<7, false>(a, stream); break;
+    default: throw std::logic_error("certex: the tiled screen takes 7 or 8 query tiles per wave pair");
   }
 }
 

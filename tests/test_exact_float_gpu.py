@@ -153,6 +153,15 @@ def test_wide_largest_rows(gpu):
         check(X, Q, 7, "l2", D, I)
 
 
+@pytest.mark.parametrize("nq", [512, 448, 700])
+def test_wide_query_tiles(gpu, nq):
+    """Batches of 512 and 700 queries run the tiled screen with 256-query tiles, 448 with 224-query
+    tiles (the launch picks the tile that pads the batch least); the last tile is ragged at 700."""
+    X, Q = correlated(20_000, 256, nq, seed=nq)
+    D, I, _ = run(X, Q, 10)
+    check(X, Q, 10, "l2", D, I)
+
+
 def test_wide_remove_filter_ties(gpu):
     X, Q = correlated(12_000, 256, 97, seed=21)
     X = np.concatenate([X, X[:500]])  # exact duplicates: ties go to the lower id
