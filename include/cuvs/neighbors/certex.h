@@ -163,6 +163,11 @@ CUVS_EXPORT cuvsError_t cuvsCertexIndexGetAnchorStride(cuvsCertexIndex_t index, 
 /** Whether labels were set (core.cpp has_labels). */
 CUVS_EXPORT cuvsError_t cuvsCertexIndexHasLabels(cuvsCertexIndex_t index, bool* has_labels);
 /**
+ * Whether the float vectors are kept in pinned host memory (core.cpp host_vectors, read by
+ * certex/index.py:379 when an index is loaded).
+ */
+CUVS_EXPORT cuvsError_t cuvsCertexIndexGetHostVectors(cuvsCertexIndex_t index, bool* host_vectors);
+/**
  * Vectors covered by the label partition (0 when none); the ones added later go through the
  * label filter (reference index::n_partitioned, certex.hpp:301-306).
  */

@@ -155,6 +155,7 @@ def lib():
                     "cuvsCertexIndexGetMetric": [P(IndexHandle), P(ctypes.c_int)],
                     "cuvsCertexIndexGetAnchorStride": [P(IndexHandle), P(i32)],
                     "cuvsCertexIndexHasLabels": [P(IndexHandle), P(ctypes.c_bool)],
+                    "cuvsCertexIndexGetHostVectors": [P(IndexHandle), P(ctypes.c_bool)],
                     "cuvsCertexIndexGetPartitioned": [P(IndexHandle), P(i64)],
                     "cuvsCertexIndexGetLists": [P(IndexHandle), P(i32), P(i64)],
                     "cuvsCertexReserve": [ctypes.c_size_t, i64, P(IndexHandle)],

@@ -566,6 +566,14 @@ cuvsError_t cuvsCertexIndexHasLabels(cuvsCertexIndex_t index, bool* has_labels)
   });
 }
 
+cuvsError_t cuvsCertexIndexGetHostVectors(cuvsCertexIndex_t index, bool* host_vectors)
+{
+  return translate([=] {
+    dispatch(index->dtype,
+             [&](auto tag) { *host_vectors = as_index<decltype(tag)>(*index)->host_vectors(); });
+  });
+}
+
 cuvsError_t cuvsCertexIndexGetPartitioned(cuvsCertexIndex_t index, int64_t* n_partitioned)
 {
   return translate([=] {

@@ -140,7 +140,7 @@ void grow(cuvs::resources const& res, index_state& st, int64_t cap)
   const size_t vbytes = is_int(st.type) ? 0 : size_t(st.dim) * elem_size(st.type);
   cuvs::detail::device_buffer codes(size_t(cap) * st.row_bytes);
   cuvs::detail::device_buffer rowc(size_t(cap) * 4);
-  cuvs::detail::device_buffer vectors(size_t(cap) * vbytes);
+  cuvs::detail::device_buffer vectors(size_t(cap) * vbytes, st.host_vectors);
   const int64_t s       = std::max(1, st.anchor_stride);
   const int64_t a_cap   = (cap + s - 1) / s;
   const int64_t a_size  = (st.size + s - 1) / s;
@@ -148,10 +148,8 @@ void grow(cuvs::resources const& res, index_state& st, int64_t cap)
   cuvs::detail::device_buffer anchor_rowc(size_t(a_cap) * 4);
   cuvs::detail::device_buffer labels;
   auto copy = [&](cuvs::detail::device_buffer& dst, cuvs::detail::device_buffer const& src,
-                  size_t bytes) {
-    if (bytes > 0) {
-      CERTEX_HIP_TRY(hipMemcpyAsync(dst.p, src.p, bytes, hipMemcpyDeviceToDevice, stream));
-    }
+                  size_t bytes) {  // device or pinned host memory on either side
+    if (bytes > 0) { CERTEX_HIP_TRY(hipMemcpyAsync(dst.p, src.p, bytes, hipMemcpyDefault, stream)); }
   };
   copy(codes, st.codes, size_t(st.size) * st.row_bytes);
   copy(rowc, st.rowc, size_t(st.size) * 4);
@@ -222,9 +220,9 @@ void append_float(cuvs::resources const& res, index_state& st, const void* x, in
   hipStream_t stream = static_cast<hipStream_t>(res.stream());
   const size_t rb    = size_t(st.dim) * elem_size(st.type);
   char* dst          = st.vectors.as<char>() + size_t(first) * rb;
-  CERTEX_HIP_TRY(hipMemcpyAsync(dst, x, size_t(n) * rb,
-                                on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
-                                stream));
+  // the stored vectors are device or pinned host memory, the source device or host memory
+  (void)on_device;
+  CERTEX_HIP_TRY(hipMemcpyAsync(dst, x, size_t(n) * rb, hipMemcpyDefault, stream));
   certex_amd::encode_rows_f16(dst, elem_of(st.type), n, st.dim, st.halves, st.normalize,
                               st.center.as<double>(), 1.0 / st.alpha, st.metric, st.gamma,
                               st.codes.as<uint16_t>() + size_t(first) * st.halves,
@@ -1473,6 +1471,21 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
   expects(params.n_lists <= certex_amd::kMaxLists, "certex: at most 16384 lists");
   expects(params.n_lists == 0 || dataset.rows < (int64_t(1) << 31),
           "certex: at most 2^31 - 1 vectors in an index with lists");
+  // options this build does not implement are refused rather than ignored. Every screen here
+  // reads full-dimension rows (the exact int8 screen of 8-bit vectors; for float vectors the
+  // certificate of full-dimension fp16 rows is folded into the row terms and thresholds), so the
+  // width is always the dimension: width 0 (auto) or at least the dimension is accepted, a
+  // projection below it is refused; variance and pca_sample only parametrize the auto rule
+  expects(params.width <= 0 || params.width >= dataset.cols,
+          "certex: a projection width below the dimension is not supported by this build (every "
+          "screen reads full-dimension rows): use width 0 or at least the dimension");
+  expects(params.variance > 0.0 && params.variance <= 1.0, "certex: variance must lie in (0, 1]");
+  expects(params.pca_sample >= 1, "certex: pca_sample must be at least 1");
+  expects(!params.local_projections,
+          "certex: local_projections (a projection per list) is not supported by this build");
+  expects(!params.int8_rows || is_int(st.type),
+          "certex: int8_rows needs 8-bit vectors in this build (float vectors are screened as "
+          "fp16 rows; 8-bit vectors always as exact int8 rows)");
   st.params        = params;
   st.dim           = dataset.cols;
   st.anchor_stride = params.anchor_stride;
@@ -1511,8 +1524,7 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
   // the vectors, then the center (mean; none for inner products) and the scale alpha that puts
   // every screening row within norm 64
   const size_t rb = size_t(st.dim) * sizeof(T);
-  CERTEX_HIP_TRY(hipMemcpyAsync(st.vectors.p, dataset.data, size_t(n) * rb,
-                                dataset.on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+  CERTEX_HIP_TRY(hipMemcpyAsync(st.vectors.p, dataset.data, size_t(n) * rb, hipMemcpyDefault,
                                 stream));
   st.center.resize_discard(size_t(st.dim) * sizeof(double));
   st.maxima.resize_discard(2 * sizeof(double));
@@ -1769,7 +1781,7 @@ void put_device(std::ostream& os, cuvs::resources const& res, const void* p, siz
 {
   std::vector<char> h(bytes);
   if (bytes > 0) {
-    CERTEX_HIP_TRY(hipMemcpyAsync(h.data(), p, bytes, hipMemcpyDeviceToHost,
+    CERTEX_HIP_TRY(hipMemcpyAsync(h.data(), p, bytes, hipMemcpyDefault,
                                   static_cast<hipStream_t>(res.stream())));
     res.sync();
   }
@@ -1781,7 +1793,7 @@ void get_device(std::istream& is, cuvs::resources const& res, void* p, size_t by
   is.read(h.data(), std::streamsize(bytes));
   expects(bool(is) || bytes == 0, "certex: the index file is truncated");
   if (bytes > 0) {
-    CERTEX_HIP_TRY(hipMemcpyAsync(p, h.data(), bytes, hipMemcpyHostToDevice,
+    CERTEX_HIP_TRY(hipMemcpyAsync(p, h.data(), bytes, hipMemcpyDefault,
                                   static_cast<hipStream_t>(res.stream())));
     res.sync();
   }

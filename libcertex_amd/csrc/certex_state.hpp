@@ -39,15 +39,19 @@ inline void expects(bool ok, const char* message)
 
 namespace cuvs::detail {
 
-/** Owned device memory. */
+/**
+ * Owned memory that kernels read: device memory, or (host = true) pinned host memory mapped into
+ * the device's address space (hipHostMalloc), which kernels read over PCIe.
+ */
 struct device_buffer {
   void* p      = nullptr;
   size_t bytes = 0;
+  bool host    = false;
   device_buffer() = default;
-  explicit device_buffer(size_t n) { resize_discard(n); }
+  explicit device_buffer(size_t n, bool in_host = false) : host(in_host) { resize_discard(n); }
   device_buffer(device_buffer const&)            = delete;
   device_buffer& operator=(device_buffer const&) = delete;
-  device_buffer(device_buffer&& o) noexcept : p(o.p), bytes(o.bytes)
+  device_buffer(device_buffer&& o) noexcept : p(o.p), bytes(o.bytes), host(o.host)
   {
     o.p     = nullptr;
     o.bytes = 0;
@@ -56,12 +60,13 @@ struct device_buffer {
   {
     std::swap(p, o.p);
     std::swap(bytes, o.bytes);
+    std::swap(host, o.host);
     return *this;
   }
   ~device_buffer() { release(); }
   void release()
   {
-    if (p != nullptr) { (void)hipFree(p); }
+    if (p != nullptr) { (void)(host ? hipHostFree(p) : hipFree(p)); }
     p     = nullptr;
     bytes = 0;
   }
@@ -70,7 +75,7 @@ struct device_buffer {
   {
     release();
     if (n > 0) {
-      const hipError_t e = hipMalloc(&p, n);
+      const hipError_t e = host ? hipHostMalloc(&p, n, hipHostMallocMapped) : hipMalloc(&p, n);
       if (e != hipSuccess) {
         (void)hipGetLastError();
         p = nullptr;
@@ -240,7 +245,8 @@ struct index_state {
   cuvs::detail::device_buffer codes;
   cuvs::detail::device_buffer rowc;
   cuvs::detail::device_buffer labels;
-  cuvs::detail::device_buffer vectors;  // float vectors [capacity, dim]
+  cuvs::detail::device_buffer vectors;  // float vectors [capacity, dim]; pinned host memory when
+                                        // host_vectors (the exact-score kernels read it over PCIe)
   // the anchor copy: anchor j holds the screening row and term of id j * anchor_stride, so that
   // the anchor pass reads consecutive rows whose groups mix rows from all over the index (the
   // stored rows may be in list order)

@@ -194,6 +194,10 @@ class _Core:
         return self._get("cuvsCertexIndexHasLabels", ctypes.c_bool)
 
     @property
+    def host_vectors(self):
+        return self._get("cuvsCertexIndexGetHostVectors", ctypes.c_bool)
+
+    @property
     def n_partitioned(self):
         return self._get("cuvsCertexIndexGetPartitioned", ctypes.c_int64)
 
@@ -400,7 +404,8 @@ class Index:
         _require(prefix[1:3] in _PREFIX, "not a certex index file")
         core = _Core()
         C.check(C.lib().cuvsCertexDeserialize(C.resources(), str(path).encode(), core.h))
-        idx = cls(core.dim, metric=core.metric, anchor_stride=core.anchor_stride, n_lists=core.lists[0])
+        idx = cls(core.dim, metric=core.metric, anchor_stride=core.anchor_stride, n_lists=core.lists[0],
+                  storage="host" if core.host_vectors else "device")
         idx.core = core
         return idx
 
