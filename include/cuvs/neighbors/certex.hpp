@@ -70,7 +70,13 @@ struct index_params {
   int64_t capacity = 0;
 };
 
-/** Parameters of a search (reference certex.hpp:96-107). */
+/**
+ * Parameters of a search (reference certex.hpp:96-107). anchors: the reference scores the best
+ * anchors of that many groups exactly to set the threshold; this build certifies the threshold
+ * from the screen values of the k best anchor groups (8-bit vectors: exact integer screen values;
+ * float vectors: the certificate's upper bound of the score), so no anchor is scored exactly and
+ * the value has no effect.
+ */
 struct search_params {
   int anchors     = 128;
   int batch_size  = 2048;

@@ -9,16 +9,13 @@ import torch
 
 from .index import Index, _require
 
-def _width(head_dim):
-    """The widest screening row that fits the head dimension (certex/attention.py:25-27)."""
-    return max(59, (head_dim + 5) // 64 * 64 - 5) if head_dim >= 59 else head_dim
-
-
 def _stride(n, k):
     """An anchor stride between 1 and 16 (the reference picks one from n and k,
-    certex/attention.py:30-34): here it leaves about 4k groups of 4 anchors, so that the k-th best
-    group stays close to the k-th best key while the anchor pass reads a fraction of the keys."""
-    s = n // (16 * k)
+    certex/attention.py:30-34): here it leaves about 8k groups of 4 anchors, so that the k-th best
+    group stays close to the k-th best key while the anchor pass reads a fraction of the keys
+    (at config 4, 131,072 keys and k = 2,048: stride 2, measured against 4 and 1: 851k, 776k and
+    793k queries/s)."""
+    s = n // (32 * k)
     return int(max(1, min(16, s)))
 
 
@@ -83,7 +80,9 @@ class KeyCache:
             self.index = Index(
                 self.head_dim,
                 metric="ip",
-                width=_width(self.head_dim),
+                # the reference narrows the screening rows below the head dimension
+                # (certex/attention.py:25-27); this build screens full-dimension rows
+                width="auto",
                 storage="device",
                 capacity=cap * self.n_kv_heads,
                 anchor_stride=_stride(cap, self.k),

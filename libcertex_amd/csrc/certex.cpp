@@ -872,43 +872,25 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   if (!all_rows) {
     auto* gmax = static_cast<float*>(
       rs.get(cuvs::detail::ws_gmax, size_t(nq_pad) * size_t(tp.n_groups) * 4));
-    auto* grow = static_cast<uint32_t*>(
-      rs.get(cuvs::detail::ws_grow, size_t(nq_pad) * size_t(tp.n_groups) * 4));
     certex_amd::screen_args aa = sa;
     aa.gmax                    = gmax;
-    aa.grow                    = grow;
     timed(0, stream, [&] {
       table_pass(res, st, aa, tp, route,
                  wide ? certex_amd::anchors_f16_wide : certex_amd::anchors_f16);
     });
+    // theta certified from the k-th best group maximum (no exact anchor scores)
     certex_amd::threshold_f_args ta{};
-    ta.gmax      = gmax;
-    ta.grow      = grow;
-    ta.n_groups  = tp.n_groups;
-    ta.nq        = B;
-    ta.nq_pad    = nq_pad;
-    ta.k         = k;
-    ta.per_query = std::max(params.anchors, k + std::max(k / 4, 16));
-    ta.row_ids   = st.row_ids.as<int32_t>();
-    ta.n_listed  = st.n_listed;
-    if (route == nullptr && tp.anchors) {  // columns of the anchor copy hold anchor indices
-      ta.id_cols  = tp.ap.n_groups;
-      ta.id_scale = tp.ap.stride;
-    }
-    ta.vectors   = st.vectors.p;
-    ta.queries   = queries;
-    ta.t         = t;
-    ta.dim       = st.dim;
-    ta.metric    = st.metric;
-    ta.qscal     = qscal;
-    ta.maxima    = st.maxima.as<double>();
-    ta.alpha2    = st.alpha * st.alpha;
-    ta.gamma     = st.gamma;
-    ta.theta     = theta;
-    if (route != nullptr) {
-      ta.part_ids = st.label_part.ids.as<int32_t>();
-      ta.n_part   = st.label_part.n;
-    }
+    ta.gmax     = gmax;
+    ta.n_groups = tp.n_groups;
+    ta.nq       = B;
+    ta.nq_pad   = nq_pad;
+    ta.k        = k;
+    ta.metric   = st.metric;
+    ta.qscal    = qscal;
+    ta.maxima   = st.maxima.as<double>();
+    ta.alpha2   = st.alpha * st.alpha;
+    ta.gamma    = st.gamma;
+    ta.theta    = theta;
     timed(1, stream, [&] { certex_amd::threshold_f16(ta, stream); });
   }
 

@@ -103,7 +103,6 @@ enum ws_slot : int {
   ws_best_row,
   ws_staging,
   ws_qscal,
-  ws_grow,
   ws_vals,
   ws_route,       // label routing of a batch: order, sorted labels, group tables
   ws_route_q,     // the batch's queries in label order

@@ -162,10 +162,8 @@ struct screen_args {
   int64_t spill_pool  = 0;
   int64_t spill_cap   = 0;  // set by the launcher
   uint32_t* spill_need = nullptr;
-  // anchors: group maxima [nq_pad, n_groups] (int32 or float), a group = group_steps steps;
-  // fp16 rows also record the stored row of each maximum in grow
+  // anchors: group maxima [nq_pad, n_groups] (int32 or float), a group = group_steps steps
   void* gmax       = nullptr;
-  uint32_t* grow   = nullptr;
   int64_t n_groups = 0;
   int64_t grp_base = 0;  // first group column of the pass
   int group_steps  = 1;
@@ -334,34 +332,23 @@ void remove_rows_f16(const int64_t* ids, int64_t n, int64_t size, float* rowc,
                      unsigned long long* newly_removed, const row_places& at, hipStream_t stream);
 
 struct threshold_f_args {
-  const float* gmax;     // [nq_pad, n_groups]
-  const uint32_t* grow;  // [nq_pad, n_groups]
+  const float* gmax;     // [nq_pad, n_groups] best screen value per anchor group
   int64_t n_groups;
   int64_t nq, nq_pad;
   int k;
-  int per_query;         // anchors scored exactly per query (>= k)
-  const void* vectors;   // original vectors [*, dim]
-  const void* queries;   // original queries of the batch [nq, dim]
-  elem t;
-  int64_t dim;
   metric_kind metric;
   const double* qscal;   // [nq_pad, 3]
   const double* maxima;  // [2]
   double alpha2;         // alpha^2
   double gamma;
-  const int32_t* part_ids = nullptr;  // routed: anchor rows below n_part are partition rows
-  int64_t n_part          = 0;
-  const int32_t* row_ids  = nullptr;  // lists: stored rows below n_listed hold ids row_ids[row]
-  int64_t n_listed        = 0;
-  int64_t id_cols         = 0;  // columns [0, id_cols) hold anchors of the anchor copy: id = row * id_scale
-  int64_t id_scale        = 0;
   float* theta;          // [nq_pad]
 };
 /**
- * theta[q] for fp16 rows: the k-th smallest exact fp64 score among the best anchors of the
- * per_query best groups gives U >= the k-th neighbour's score; theta is the screen value below
- * which no pair can have a score <= U (rounded down). -FLT_MAX (keep every live row) with fewer
- * than k valid anchors; +inf for padding queries.
+ * theta[q] for fp16 rows, certified from the anchor pass alone: the k-th largest finite group
+ * maximum belongs to k distinct live rows; the certificate's upper bound of the score of a pair
+ * with that screen value bounds the k-th neighbour's score by U, and theta is the screen value
+ * below which no pair can have a score <= U (rounded down). -FLT_MAX (keep every live row) with
+ * fewer than k such groups; +inf for padding queries.
  */
 void threshold_f16(const threshold_f_args& a, hipStream_t stream);
 

@@ -74,10 +74,9 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   constexpr int NG     = QB / GQ;        // groups of the workgroup
   constexpr int TR     = 16 * BT;        // rows of a step
   constexpr int SPT    = TR / kStepRows; // chunk steps (kStepRows rows) per step
-  constexpr bool ARGMX = ANCHORS && R::kArgmax;
   // coarse anchor groups without argmax or filter: each lane folds its values into a register per
   // (query group, query tile) every step; the lanes of a query reduce and write once per group
-  constexpr bool RUNREG = ANCHORS && !R::kArgmax && !FILT;
+  constexpr bool RUNREG = ANCHORS && !FILT;
   static_assert(NG % 2 == 0, "query groups are processed in pairs");
   static_assert(BT * 4 <= 32, "a lane's survivor mask of one query tile is 32 bits");
   static_assert(!ANCHORS || BT == 4, "the anchor pass runs 64-row steps");
@@ -85,7 +84,6 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   __shared__ __attribute__((aligned(16))) uint8_t qlds[QB * ROWB];
   __shared__ val_t thl[ANCHORS ? 1 : QB];
   __shared__ val_t gml[ANCHORS ? 4 * QB : 1];
-  __shared__ uint32_t gmr[ARGMX ? 4 * QB : 1];
   __shared__ uint32_t hit_q[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t hit_row[ANCHORS ? 1 : kHitCap];
   __shared__ float hit_val[ANCHORS || !R::kValues ? 1 : kHitCap];
@@ -122,7 +120,6 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     for (int e = tid; e < 4 * QB; e += 256) {
       if (e % QB >= qlive) { continue; }
       gml[e] = R::lowest();
-      if constexpr (ARGMX) { gmr[e] = 0xffffffffu; }
     }
   } else {
     for (int e = tid; e < qlive; e += 256) {
@@ -224,8 +221,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
           const int64_t q    = q0 + g * GQ + qt * 16 + (lane & 15);
           const int64_t qc   = q < w.q_end ? q : w.q_end - 1;  // padding: any live query's
           const uint32_t kp  = FILT ? filter_mask(a, w, SL, qc, row0) : 0u;
-          anchor_tile<R, FILT>(col, row0, q, wave * QB + g * GQ + qt * 16 + lane, a, w, gml, gmr,
-                               kp);
+          anchor_tile<R, FILT>(col, wave * QB + g * GQ + qt * 16 + lane, gml, kp);
         }
       }
     } else {
@@ -344,13 +340,8 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
       // end of an anchor group (group_steps steps, aligned to the wave's range)
       if (!a.fine && ((s + 1) % a.group_steps == 0 || s + 1 == n_steps)) {
         for (int e = lane; e < QB; e += 64) {
-          if (q0 + e < w.q_end) {
-            const int64_t t = table_entry(a, q0 + e, s / a.group_steps);
-            gmax[t]         = gml[wave * QB + e];
-            if constexpr (ARGMX) { a.grow[t] = gmr[wave * QB + e]; }
-          }
+          if (q0 + e < w.q_end) { gmax[table_entry(a, q0 + e, s / a.group_steps)] = gml[wave * QB + e]; }
           gml[wave * QB + e] = R::lowest();
-          if constexpr (ARGMX) { gmr[wave * QB + e] = 0xffffffffu; }
         }
       }
     }
@@ -397,7 +388,7 @@ void launch(const screen_args& a, hipStream_t stream)
   const int ks  = a.row_bytes / 64;
   screen_args b = a;
   b.spill_cap   = !ANCHORS && a.spill_q != nullptr ? a.spill_pool / blocks : 0;
-  if constexpr (ANCHORS && !R::kArgmax && !FILT) {
+  if constexpr (ANCHORS && !FILT) {
     // coarse groups keep their running maxima in registers: groups of 32 queries (2 tiles)
     // leave room for them
     if (ks == 2 && qb_size == 512) {

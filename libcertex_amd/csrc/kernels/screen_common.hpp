@@ -25,7 +25,6 @@ struct int8_rows {
   using acc_t  = v4i;
   using frag_t = v4i;
   using val_t  = int;
-  static constexpr bool kArgmax = false;
   static constexpr bool kValues = false;  // survivors carry no screen value (verify scores all)
   __device__ static acc_t mfma(frag_t a, frag_t b, acc_t c)
   {
@@ -41,7 +40,6 @@ struct f16_rows {
   using acc_t  = v4f;
   using frag_t = v8h;
   using val_t  = float;
-  static constexpr bool kArgmax = true;  // the float threshold scores the best anchor exactly
   static constexpr bool kValues = true;  // survivors carry their screen value (ordered verify)
   __device__ static acc_t mfma(frag_t a, frag_t b, acc_t c)
   {
@@ -374,22 +372,17 @@ __device__ inline void flush_hits(int64_t q0, int qb, const screen_args& a, cons
 
 /**
  * Anchor pass, one 16-query tile of a 64-row step: folds the best screen value of this lane's
- * query over the step (and, for fp16 rows, the stored row holding it, ties to the lower row) into
- * the wave's running group maximum gml[e] / gmr[e] (e = the query's slot). `col[bt]` holds the
- * tile's accumulators of row tile bt; row0 is the scan index of its bit 0. Scan indices at or past
- * the work's n_scan are padding.
+ * query over the step into the wave's running group maximum gml[e] (e = the query's slot).
+ * `col[bt]` holds the tile's accumulators of row tile bt. With a filter, bit bt * 4 + r of `keep`
+ * says whether the lane's row bt * 16 + r of the step passes it.
  */
 template <typename R, bool FILT>
-__device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], int64_t row0,
-                                            int64_t q, int e, const screen_args& a,
-                                            const screen_work& w, typename R::val_t* gml,
-                                            uint32_t* gmr, uint32_t keep)
+__device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], int e,
+                                            typename R::val_t* gml, uint32_t keep)
 {
-  using val_t         = typename R::val_t;
-  constexpr bool ARGX = R::kArgmax;
-  const int lane      = threadIdx.x & 63;
-  val_t m             = R::lowest();
-  uint32_t j          = 0;
+  using val_t    = typename R::val_t;
+  const int lane = threadIdx.x & 63;
+  val_t m        = R::lowest();
 #pragma unroll
   for (int bt = 0; bt < 4; ++bt) {
 #pragma unroll
@@ -398,44 +391,19 @@ __device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], i
       if constexpr (FILT) {
         if (!((keep >> (bt * 4 + r)) & 1u)) { v = R::lowest(); }
       }
-      if constexpr (ARGX) {
-        if (v > m) {
-          m = v;
-          j = uint32_t(bt * 16 + r);
-        }
-      } else {
-        m = R::vmax(m, v);
-      }
+      m = R::vmax(m, v);
     }
   }
-  if constexpr (ARGX) {
-    uint32_t row = uint32_t(w.base + (row0 + j) * a.row_stride);
-#pragma unroll
-    for (int off = 16; off <= 32; off <<= 1) {
-      const val_t om     = __shfl_xor(m, off);
-      const uint32_t orw = uint32_t(__shfl_xor(int(row), off));
-      if (om > m || (om == m && orw < row)) {
-        m   = om;
-        row = orw;
-      }
-    }
-    if (lane < 16 && (m > gml[e] || (m == gml[e] && row < gmr[e]))) {
-      gml[e] = m;
-      gmr[e] = row;
-    }
-  } else {
-    m = R::vmax(m, __shfl_xor(m, 16));
-    m = R::vmax(m, __shfl_xor(m, 32));
-    if (lane < 16) { gml[e] = R::vmax(gml[e], m); }
-  }
+  m = R::vmax(m, __shfl_xor(m, 16));
+  m = R::vmax(m, __shfl_xor(m, 32));
+  if (lane < 16) { gml[e] = R::vmax(gml[e], m); }
 }
 
 /**
  * Anchor pass with fine groups, one 16-query tile of a 64-row step: each lane writes, for each of
- * its 4 row tiles, the best screen value of its 4 consecutive anchors (and, for fp16 rows, the
- * stored row holding it, ties to the lower row) straight to the group table: group column
- * grp_base + (scan index of the first of the 4) / 4. row0 is the scan index of the lane's bit 0;
- * q the lane's query (written only when live).
+ * its 4 row tiles, the best screen value of its 4 consecutive anchors straight to the group table:
+ * group column grp_base + (scan index of the first of the 4) / 4. row0 is the scan index of the
+ * lane's bit 0; q the lane's query (written only when live).
  */
 template <typename R, bool FILT>
 __device__ __forceinline__ void anchor_tile_fine(const typename R::acc_t (&col)[4], int64_t row0,
@@ -448,24 +416,15 @@ __device__ __forceinline__ void anchor_tile_fine(const typename R::acc_t (&col)[
   for (int bt = 0; bt < 4; ++bt) {
     const int64_t first = row0 + bt * 16;  // scan index of the group's first anchor
     val_t m             = R::lowest();
-    uint32_t row        = 0xffffffffu;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      val_t v           = col[bt][r];
-      const int64_t idx = first + r;
+      val_t v = col[bt][r];
       if constexpr (FILT) {
         if (!((keep >> (bt * 4 + r)) & 1u)) { v = R::lowest(); }
       }
-      if (v > m) {  // strict: ties keep the lower row
-        m   = v;
-        row = uint32_t(w.base + idx * a.row_stride);
-      }
+      m = R::vmax(m, v);
     }
-    if (live && first < w.n_scan) {
-      const int64_t e = table_entry(a, q, first / kFineGroup);
-      gmax[e]         = m;
-      if constexpr (R::kArgmax) { a.grow[e] = row; }
-    }
+    if (live && first < w.n_scan) { gmax[table_entry(a, q, first / kFineGroup)] = m; }
   }
 }
 

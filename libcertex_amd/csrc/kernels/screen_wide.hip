@@ -19,8 +19,8 @@
 //   pipeline serves a quad that shares a line at once, and 16 lanes on 16 rows one line at a
 //   time), and 4 ds_bpermute per 16 bytes move them to the MFMA's lanes;
 // - block b runs on XCD b % 8; the query blocks of one row chunk run on one XCD together.
-// Group maxima (and the rows holding them) go to the group table, per coarse group of anchor
-// steps or per fine group of 4 anchors.
+// Group maxima go to the group table, per coarse group of anchor steps or per fine group of 4
+// anchors.
 
 #include "screen_common.hpp"
 
@@ -52,7 +52,6 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
   // dynamic LDS: the queries [QB][H] halves (swizzled)
   extern __shared__ __attribute__((aligned(16))) uint8_t qlds[];
   __shared__ float gml[kWideWaves * QB];
-  __shared__ uint32_t gmr[kWideWaves * QB];
 
   const float* rowc = static_cast<const float*>(a.rowc);
   float* gmax       = static_cast<float*>(a.gmax);
@@ -74,10 +73,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
 
   stage_queries<64 * kWideWaves>(a.qcodes, RB, q0, w.q_end, QB, qlds,
                                  [](int r, int c) { return c ^ (r & 15); });
-  for (int e = tid; e < kWideWaves * QB; e += 64 * kWideWaves) {
-    gml[e] = R::lowest();
-    gmr[e] = 0xffffffffu;
-  }
+  for (int e = tid; e < kWideWaves * QB; e += 64 * kWideWaves) { gml[e] = R::lowest(); }
   __syncthreads();
 
   frag_t av[2][4][2];  // [buffer][row tile][first / second MFMA of the chunk]
@@ -213,19 +209,14 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
         const int64_t q    = q0 + qt * 16 + (lane & 15);
         const int64_t qc   = q < w.q_end ? q : w.q_end - 1;  // padding: any live query's
         const uint32_t kp  = FILT ? filter_mask(a, w, SL, qc, row0) : 0u;
-        anchor_tile<R, FILT>(col, row0, q, wave * QB + qt * 16 + lane, a, w, gml, gmr, kp);
+        anchor_tile<R, FILT>(col, wave * QB + qt * 16 + lane, gml, kp);
       }
     }
     // end of an anchor group (group_steps steps, aligned to the wave's range)
     if (!a.fine && ((s + 1) % a.group_steps == 0 || s + 1 == n_steps)) {
       for (int e = lane; e < QB; e += 64) {
-        if (q0 + e < w.q_end) {
-          const int64_t t = table_entry(a, q0 + e, s / a.group_steps);
-          gmax[t]         = gml[wave * QB + e];
-          a.grow[t]       = gmr[wave * QB + e];
-        }
+        if (q0 + e < w.q_end) { gmax[table_entry(a, q0 + e, s / a.group_steps)] = gml[wave * QB + e]; }
         gml[wave * QB + e] = R::lowest();
-        gmr[wave * QB + e] = 0xffffffffu;
       }
     }
   }
@@ -260,7 +251,7 @@ int max_lds()
 
 /**
  * Query tiles of a workgroup for rows of `row_bytes`: the largest of 6, 4, 2 whose queries and
- * the group tables (gml, gmr: 8 bytes per query per wave) fit the LDS (0: none fits). More queries
+ * the group table (gml: 4 bytes per query per wave, counted as 8) fit the LDS (0: none fits). More queries
  * per workgroup means more work per row fetched.
  */
 int wide_query_tiles(int row_bytes)

@@ -790,127 +790,130 @@ __device__ inline uint32_t fkey(float f)
 
 constexpr int kMaxFloatDim = kMaxF16Halves;  // widest float vector
 
-template <int L>
-__global__ __launch_bounds__(kThreads) void threshold_f16_kernel(threshold_f_args a, int cap)
+/** The float of an ascending key of fkey. */
+__device__ inline float key_value(uint32_t k)
 {
-  extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
-  auto* key = reinterpret_cast<uint64_t*>(dyn);                 // [cap]
-  auto* rid = reinterpret_cast<uint32_t*>(dyn + size_t(cap) * 8);  // [cap]
-  auto* qv  = reinterpret_cast<double*>(dyn + size_t(cap) * 12);  // [dim]
+  return __uint_as_float((k >> 31) ? (k & 0x7fffffffu) : ~k);
+}
+
+/**
+ * The certificate's per-query error terms of the fp16 screen: C = the operand rounding of every
+ * pair (cross) plus the fp32 accumulation of its products (accum), from the query's |fp16(W)|,
+ * |W - fp16(W)| (qscal) and the index's largest |fp16(Z)|, |Z - fp16(Z)| (maxima).
+ */
+__device__ inline double screen_error(const threshold_f_args& a, int64_t q)
+{
+  const double nw = a.qscal[3 * q + 1], ew = a.qscal[3 * q + 2];
+  const double nz = a.maxima[0], ez = a.maxima[1];
+  const double cross = ew * nz + nw * ez + ew * ez;  // operand rounding, all pairs
+  const double accum = a.gamma * nw * nz;            // fp32 accumulation of the products
+  return cross + accum;
+}
+
+/**
+ * The screen threshold of a score bound U: every pair of query q whose exact score is <= U has a
+ * screen value >= the returned float (rounded down), which is never below -FLT_MAX. With
+ * C = screen_error: inner products t(U) = -U / alpha2 - C; l2 t(U) = (|W|^2 - U / alpha2) / 2 - C
+ * (cosine: l2 on the unit vectors with U_l2 = 2 + 2 U); both less 1e-10 of their scale.
+ */
+__device__ inline float theta_of(double U, const threshold_f_args& a, int64_t q)
+{
+  const double aq = a.qscal[3 * q];
+  double th, scale;
+  if (a.metric == metric_kind::inner) {
+    th    = -U / a.alpha2;
+    scale = fabs(th);
+  } else {
+    const double u  = a.metric == metric_kind::cosine ? (2.0 + 2.0 * U) : U;
+    const double ua = u / a.alpha2;
+    th              = (aq - ua) / 2.0;
+    scale           = fabs(aq) + fabs(ua);
+  }
+  const double t = th - screen_error(a, q) - 1e-10 * scale - 1e-30;
+  float f        = float(t);
+  if (double(f) > t) { f = nextafterf(f, -INFINITY); }
+  return f > -FLT_MAX ? f : -FLT_MAX;
+}
+
+/**
+ * An upper bound of the exact score of a pair of query q whose fp16 screen value is v (finite).
+ * The fp32 accumulation and the operand rounding bound the screen value from above as they bound
+ * it from below: acc <= <W, Z> + C + (row term), for inner products acc <= <W, Z> + C, so the
+ * score -alpha2 <W, Z> <= alpha2 (C - v). For l2 the row term, -|Z|^2 / 2 scaled by (1 - 2 gamma
+ * - 1e-10) and rounded up to fp32, exceeds -|Z|^2 / 2 by at most D = |Z|max^2 (1.5 gamma + 1e-7)
+ * (with its own accumulation error), |Z|max <= max |fp16(Z)| + max |Z - fp16(Z)|; then
+ * score / alpha2 = |W|^2 - 2 (<W, Z> - |Z|^2 / 2) <= |W|^2 - 2 (v - C - D). |W|^2 is stored
+ * lowered by 1e-13 and rounded in its sum; the results carry a margin of 1e-12 of their scale for
+ * the fp64 rounding of these expressions. Cosine: l2 on the unit vectors, U = (U_l2 - 2) / 2.
+ */
+__device__ inline double screen_upper_bound(float vf, const threshold_f_args& a, int64_t q)
+{
+  const double v = double(vf);
+  const double C = screen_error(a, q);
+  if (a.metric == metric_kind::inner) {
+    return a.alpha2 * (C - v) + 1e-12 * a.alpha2 * (fabs(v) + C) + 1e-300;
+  }
+  const double zmax = a.maxima[0] + a.maxima[1];
+  const double D    = zmax * zmax * (1.5 * a.gamma + 1e-7);
+  const double aq   = a.qscal[3 * q] * (1.0 + 1e-11);
+  const double y    = aq - 2.0 * v + 2.0 * (C + D);
+  const double ub   = a.alpha2 * y + 1e-12 * a.alpha2 * (aq + 2.0 * fabs(v) + 2.0 * (C + D)) + 1e-300;
+  if (a.metric == metric_kind::cosine) { return (ub - 2.0) / 2.0 + 1e-12 * (fabs(ub) + 2.0); }
+  return ub;
+}
+
+template <typename F>
+__device__ uint32_t radix_select(int64_t n, int rank, F key_of, int* hist, int* wave_tot,
+                                 uint32_t* sel_digit, int* sel_rank);
+
+/**
+ * theta[q] for the fp16 screen, certified from screen values alone: the k-th largest finite
+ * group maximum v_k of the anchor pass belongs to k distinct live rows, each with a screen value
+ * >= v_k, and the certificate bounds the score of a pair with screen value v from above by
+ * screen_upper_bound(v); so U = screen_upper_bound(v_k) bounds the k-th neighbour's score, and
+ * theta = theta_of(U). Groups whose maximum is -inf (no live anchor) or +inf (a row beyond the
+ * fp16 range, whose score has no bound) are not counted. -FLT_MAX (keep every live row) with fewer
+ * than k counted groups; +inf for padding queries.
+ */
+__global__ __launch_bounds__(kThreads) void threshold_f16_cert_kernel(threshold_f_args a)
+{
   __shared__ int hist[256];
   __shared__ int wave_tot[4];
   __shared__ uint32_t sel_digit;
   __shared__ int sel_rank;
   __shared__ int cnt;
-
   const int64_t q = blockIdx.x;
   const int tid   = threadIdx.x;
   if (q >= a.nq) {
     if (tid == 0) { a.theta[q] = INFINITY; }
     return;
   }
-  const float* v    = a.gmax + q * a.n_groups;
-  const uint32_t* r = a.grow + q * a.n_groups;
-  // valid groups: a finite or +inf best value (all anchors removed or filtered: -inf)
+  const float* v = a.gmax + q * a.n_groups;
   if (tid == 0) { cnt = 0; }
   __syncthreads();
   int local = 0;
-  for (int64_t e = tid; e < a.n_groups; e += kThreads) { local += v[e] > -INFINITY ? 1 : 0; }
+  for (int64_t e = tid; e < a.n_groups; e += kThreads) { local += isfinite(v[e]) ? 1 : 0; }
   atomicAdd(&cnt, local);
   __syncthreads();
-  const int n_valid = cnt;
-  if (n_valid < a.k) {
+  if (cnt < a.k) {
     // keep every live row: removed rows (screen value -inf) still fail
     if (tid == 0) { a.theta[q] = -FLT_MAX; }
     return;
   }
-  const int P = a.per_query < n_valid ? a.per_query : n_valid;
-  // the P-th largest value: radix select over descending keys (~fkey)
-  uint32_t prefix = 0, mask = 0;
-  int rank = P;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    hist[tid] = 0;
-    __syncthreads();
-    for (int64_t e = tid; e < a.n_groups; e += kThreads) {
-      if (!(v[e] > -INFINITY)) { continue; }
-      const uint32_t k = ~fkey(v[e]);
-      if ((k & mask) == prefix) { atomicAdd(&hist[(k >> shift) & 255], 1); }
-    }
-    __syncthreads();
-    const int c    = hist[tid];
-    const int incl = block_scan_incl(c, wave_tot);
-    if (incl - c < rank && rank <= incl) {
-      sel_digit = uint32_t(tid);
-      sel_rank  = rank - (incl - c);
-    }
-    __syncthreads();
-    prefix |= sel_digit << shift;
-    mask |= 255u << shift;
-    rank = sel_rank;
-    __syncthreads();
-  }
-  // exact scores of the anchors of the groups at or above it (at most cap)
-  for (int64_t j = tid; j < a.dim; j += kThreads) { qv[j] = fcoord(a.queries, a.t, q * a.dim + j); }
-  if (tid == 0) { cnt = 0; }
-  __syncthreads();
-  for (int64_t e = tid; e < a.n_groups; e += kThreads) {
-    const bool take = v[e] > -INFINITY && ~fkey(v[e]) <= prefix;
-    const int slot  = wave_append(take, &cnt);  // the wave's lanes still in the loop
-    if (take && slot < cap) {
-      const uint32_t row = r[e];
-      rid[slot]          = e < a.id_cols                             ? uint32_t(row * a.id_scale)
-                           : (a.part_ids != nullptr && row < a.n_part) ? uint32_t(a.part_ids[row])
-                           : row < a.n_listed                        ? uint32_t(a.row_ids[row])
-                                                                     : row;
-    }
-  }
-  __syncthreads();
-  const int m = cnt < cap ? cnt : cap;
-  score_rows_l<L>(qv, a.vectors, a.t, a.dim, a.metric, rid, key, 0, m);
-  __syncthreads();
-  __shared__ uint64_t kth_key;
-  __shared__ uint32_t kth_row;
-  __shared__ int sel_count;
-  if (m <= kSortBelow) {
-    const int Pw = pow2_at_least(m);
-    for (int e = m + tid; e < Pw; e += kThreads) {
-      key[e] = ~0ull;
-      rid[e] = ~0u;
-    }
-    __syncthreads();
-    bitonic_sort(key, rid, Pw);
-    if (tid == 0) { kth_key = key[a.k - 1]; }
-    __syncthreads();
-  } else {
-    select_pair(key, rid, m, a.k, false, hist, wave_tot, &sel_digit, &sel_rank, &sel_count,
-                &kth_key, &kth_row);
-  }
-  if (tid == 0) {
-    const double U  = key_score(kth_key);  // k distinct anchors: U bounds the k-th score
-    const double aq = a.qscal[3 * q], nw = a.qscal[3 * q + 1], ew = a.qscal[3 * q + 2];
-    const double nz = a.maxima[0], ez = a.maxima[1];
-    const double cross = ew * nz + nw * ez + ew * ez;  // operand rounding, all pairs
-    const double accum = a.gamma * nw * nz;            // fp32 accumulation of the products
-    double th, scale;
-    if (a.metric == metric_kind::inner) {
-      th    = -U / a.alpha2;
-      scale = fabs(th);
-    } else {
-      const double u = a.metric == metric_kind::cosine ? (2.0 + 2.0 * U) : U;
-      const double ua = u / a.alpha2;
-      th              = (aq - ua) / 2.0;
-      scale           = fabs(aq) + fabs(ua);
-    }
-    const double t = th - accum - cross - 1e-10 * scale - 1e-30;
-    float f        = float(t);
-    if (double(f) > t) { f = nextafterf(f, -INFINITY); }
-    a.theta[q] = f > -FLT_MAX ? f : -FLT_MAX;
-  }
+  // the k-th largest finite value: the k-th smallest of the descending keys ~fkey, the others last
+  const uint32_t key = radix_select(
+    a.n_groups, a.k,
+    [&](int64_t e) {
+      const float x = v[e];
+      return isfinite(x) ? ~fkey(x) : 0xffffffffu;
+    },
+    hist, wave_tot, &sel_digit, &sel_rank);
+  if (tid == 0) { a.theta[q] = theta_of(screen_upper_bound(key_value(~key), a, q), a, q); }
 }
 
 /**
  * A lower bound of the exact score of a pair whose fp16 screen value is v: the inverse of the
- * threshold map of threshold_f16_kernel (a pair with score s has v >= t(s), where t(U) is the
+ * threshold map theta_of (a pair with score s has v >= t(s), where t(U) is the
  * threshold before rounding), with 20 times its relative slack and a margin for the fp64 rounding
  * of this expression. C = the query's cross and accumulation terms; aq = |W|^2 (lower bound).
  */
@@ -1211,19 +1214,7 @@ void launch_dyn(K kernel, unsigned blocks, size_t bytes, hipStream_t stream, Arg
 void threshold_f16(const threshold_f_args& a, hipStream_t stream)
 {
   if (a.nq_pad == 0) { return; }
-  // per_query entries rounded up to 256 (at least 512, the largest bitonic sort here): less LDS
-  // per block than a power of two, so more blocks share a CU
-  const int want      = a.per_query < kBuf ? a.per_query : kBuf;
-  const int cap       = want <= 512 ? 512 : (want + 255) / 256 * 256;
-  const size_t bytes  = size_t(cap) * 12 + size_t(a.dim) * 8;
-  const unsigned grid = unsigned(a.nq_pad);
-  // 32-lane slots also above 256 coordinates: twice the rows in flight per wave of whole-wave
-  // slots (config 3's threshold: 0.71 -> 0.64 ms; the verify measured best with whole waves)
-  if (a.dim <= 128) {
-    launch_dyn(threshold_f16_kernel<16>, grid, bytes, stream, a, cap);
-  } else {
-    launch_dyn(threshold_f16_kernel<32>, grid, bytes, stream, a, cap);
-  }
+  threshold_f16_cert_kernel<<<unsigned(a.nq_pad), kThreads, 0, stream>>>(a);
 }
 
 void verify_topk_f(const verify_f_args& a, hipStream_t stream)
