@@ -451,10 +451,11 @@ def bench_config5(args):
 def summarize_profiles(dirs, warmup, steps, after=1):
     """Text summary of rocprofv3 CSV output (kernel traces and counter collections) under `dirs`,
     for a bench run of `warmup` + `steps` searches followed by `after` more (the survivor stats).
-    A kernel launched L times per search (calls = L * (warmup + steps + after)) is averaged over
-    all its launches and, separately, over the timed ones only (launches warmup * L up to
-    (warmup + steps) * L, in dispatch order); kernels with another call count (the build, data
-    generation) show '-' there. Durations in ms, counters per dispatch."""
+    A kernel launched L = calls // (warmup + steps + after) >= 1 times per search is averaged over
+    all its launches and, separately, over the timed ones only: in dispatch order, the steps * L
+    launches before the last after * L (the first search may launch a kernel more often, when its
+    survivor buckets grow). Kernels launched fewer times (the build, data generation) show '-'
+    there. Durations in ms, counters per dispatch."""
     import csv
     import glob
     import re
@@ -474,10 +475,10 @@ def summarize_profiles(dirs, warmup, steps, after=1):
         return re.sub(r"(\(anonymous namespace\)::|\b\w+::)", "", name[:cut]).strip()
 
     def timed(vals):
-        if len(vals) % searches:
-            return None
         per = len(vals) // searches
-        sel = vals[warmup * per : (warmup + steps) * per]
+        if per == 0:
+            return None
+        sel = vals[len(vals) - (steps + after) * per : len(vals) - after * per]
         return sum(sel) / len(sel) if sel else None
 
     traces, counters = defaultdict(list), defaultdict(list)

@@ -40,6 +40,24 @@ __device__ inline int block_scan_incl(int v, int* wave_tot)
   return incl + add;
 }
 
+/** The largest of key[0, n) over the block (every thread gets it); scratch: 4 LDS words x 2. */
+__device__ inline uint64_t block_max_key(const uint64_t* key, int n, uint64_t* wave_max)
+{
+  uint64_t m = 0;
+  for (int e = threadIdx.x; e < n; e += kThreads) { m = key[e] > m ? key[e] : m; }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t o = __shfl_xor(m, off);
+    m                = o > m ? o : m;
+  }
+  if ((threadIdx.x & 63) == 0) { wave_max[threadIdx.x >> 6] = m; }
+  __syncthreads();
+  uint64_t r = wave_max[0];
+  for (int w = 1; w < kThreads / 64; ++w) { r = wave_max[w] > r ? wave_max[w] : r; }
+  __syncthreads();
+  return r;
+}
+
 /**
  * Slot of this lane in an LDS list counted by *fill, for the lanes whose `take` is set: one LDS
  * atomic per wave (the taking lanes in lane order) instead of one per entry, which would all hit
@@ -1018,12 +1036,15 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
     score_rows_l<L>(qv, a.vectors, a.t, a.dim, a.metric, rid, key, from, to);
   };
   int have = 0;  // entries [0, have) of key / rid are scored
-  // the k best so far move to [0, k) (unordered); the k-th key bounds the k-th score
+  // the k best so far move to [0, k) (unordered); the k-th key bounds the k-th score. With
+  // exactly k entries the k-th key is their largest, and nothing moves
+  __shared__ uint64_t wave_max[kThreads / 64];
   uint64_t kth = ~0ull;
   auto keep_best = [&]() {
     if (have < k) { return; }
-    kth  = keep_k_best(key, rid, have, k, hist, wave_tot, &sel_digit, &sel_rank, &sel_count,
-                       &fill);
+    kth  = have == k ? block_max_key(key, k, wave_max)
+                     : keep_k_best(key, rid, have, k, hist, wave_tot, &sel_digit, &sel_rank,
+                                   &sel_count, &fill);
     have = k;
   };
 
@@ -1114,8 +1135,9 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
       if (ordered) { U = key_score(kth); }
     }
   }
-  keep_best();
-  {  // the final k in (score, row) order
+  {  // the final k in (score, row) order: one sort of all entries when they are few (the best
+     // k come first), else a cut back to the k best and a sort of those
+    if (have > kSortBelow) { keep_best(); }
     const int P = pow2_at_least(have > 1 ? have : 1);
     for (int j = have + tid; j < P; j += kThreads) {
       key[j] = ~0ull;
@@ -1123,6 +1145,7 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
     }
     __syncthreads();
     bitonic_sort(key, rid, P);
+    have = have < k ? have : k;
   }
   for (int j = tid; j < k; j += kThreads) {
     if (j < have) {
