@@ -292,7 +292,6 @@ struct route_plan {
   int64_t anchor_tiles = 0, screen_tiles = 0;
   int anchor_chunk     = 0;
   int screen_chunk     = 0;
-  int tile_qt          = 8;  // query tiles of the tiled screen (wide fp16 rows)
   int64_t part_groups  = 0;  // anchor group columns of the partition (the tail's follow)
   anchor_plan ap{};
 };
@@ -398,8 +397,7 @@ auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
   // fp16 rows of more than 128 halves: the tiled screen, one tile of 256 rows per workgroup
   const bool tiled = uses_tile_screen(st);
   return [&st, route, launch, tiled](certex_amd::screen_args& sa, hipStream_t stream) {
-    auto chunk = [&](certex_amd::screen_args& x) {
-      if (tiled) { x.tile_qt = certex_amd::tile_query_tiles(&x.nq, 1); }
+    auto chunk = [&](certex_amd::screen_args const& x) {
       return tiled ? certex_amd::tile_chunk_steps()
                    : plain_chunk(st, x.nq, x.nq_pad, x.n_scan, waves_of(st), kScreenChunk);
     };
@@ -415,7 +413,6 @@ auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
     r.n_route                 = route->n_route;
     r.n_tiles                 = route->screen_tiles;
     r.chunk_steps             = route->screen_chunk;
-    r.tile_qt                 = route->tile_qt;
     r.filter.kind             = 0;
     if (r.n_tiles > 0) { launch(r, stream); }
     const int64_t tail = st.size - st.label_part.n;
@@ -1030,15 +1027,9 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
       }
       return t;
     });
-  // the screen's groups: the tiled screen's query blocks (32 tile_qt queries, tile_qt chosen for
-  // the groups' sizes) and 256-row chunks for wide fp16 rows
+  // the screen's groups: the tiled screen's query blocks and 256-row chunks for wide fp16 rows
   const bool tiled = uses_tile_screen(st);
-  if (tiled) {
-    std::vector<int64_t> nqs;
-    for (auto const& e : gs) { nqs.push_back(e.nq); }
-    route.tile_qt = certex_amd::tile_query_tiles(nqs.data(), int(nqs.size()));
-  }
-  const int qbs = tiled ? 32 * route.tile_qt : qb;
+  const int qbs    = tiled ? certex_amd::tile_block_queries() : qb;
   route.screen_chunk =
     tiled ? certex_amd::tile_chunk_steps() : pick_chunk(waves, kRoutedChunk, [&](int64_t c) {
       int64_t t = 0;

@@ -143,7 +143,6 @@ struct screen_args {
   int64_t nq_pad;        // pad_queries(nq)
   int chunk_steps;       // steps of kStepRows rows per workgroup: 4 waves x a whole number of
                          // anchor groups
-  int tile_qt = 8;       // tiled fp16 screen: query tiles per pair of waves (32 tile_qt queries)
   filter_args filter;
   // screen: candidate buckets
   uint32_t* cand_count = nullptr;  // [nq_pad]
@@ -224,12 +223,11 @@ void anchors_f16(const screen_args& a, hipStream_t stream);
 void anchors_f16_wide(const screen_args& a, hipStream_t stream);
 /**
  * The fp16 screen for rows of more than 128 halves as LDS-staged tiles: a workgroup multiplies
- * 256 rows (chunk_steps = tile_chunk_steps()) with 32 tile_qt queries; row_stride 1.
+ * 256 rows (chunk_steps = tile_chunk_steps()) with tile_block_queries() queries; row_stride 1.
  */
 void screen_f16_tile(const screen_args& a, hipStream_t stream);
 int tile_chunk_steps();
-/** tile_qt (7 or 8) for a launch over groups of nq[0 .. n) queries: the one that pads least. */
-int tile_query_tiles(const int64_t* nq, int n);
+int tile_block_queries();
 
 /**
  * theta[q] = the k-th largest of gmax[q, 0 .. n_groups) (kKeepAll when n_groups < k, and never

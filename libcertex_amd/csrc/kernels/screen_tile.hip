@@ -8,9 +8,8 @@
 // the threshold, so the test needs no per-pair arithmetic.
 //
 // Work decomposition:
-// - a workgroup of 4 waves computes one tile of 256 stored rows x TQ = 32 QT queries (QT = 8, or 7
-//   when that pads the batch's label groups less), all of the row's halves, in stages of 64 halves
-//   (128 bytes of every row and query);
+// - a workgroup of 8 waves computes one tile of 256 stored rows x 256 queries, all of the row's
+//   halves, in stages of 64 halves (128 bytes of every row and query);
 // - a stage of both operands is copied into LDS by global_load_lds_dwordx4 (no VGPRs, 8 lanes on
 //   one row's 128-byte line). The 16-byte chunk c of tile row r lands in slot c ^ (r & 7) of the
 //   row's 128 bytes: lane i of a copy writes slot i % 8 of row i / 8, so it reads chunk
@@ -20,9 +19,11 @@
 //   barrier per stage both publishes a stage and frees the other buffer. Within a stage the copies
 //   and the LDS reads of the second MFMA half are issued between the row tiles of the first half
 //   (pinned with sched_group_barrier), so that their issue and latency hide behind MFMAs;
-// - the waves form a 2 x 2 grid: wave (wr, wq) multiplies tile rows 128 wr .. 128 wr + 127 (8 row
-//   tiles) with tile queries 16 QT wq .. (QT query tiles), v_mfma_f32_16x16x32_f16, the row tiles as
-//   operand A: 32 QT accumulator registers per lane (AGPRs at one wave per SIMD);
+// - the waves form a 2 x 4 grid: wave (wr, wq) multiplies tile rows 128 wr .. 128 wr + 127 (8 row
+//   tiles) with tile queries 64 wq .. 64 wq + 63 (4 query tiles), v_mfma_f32_16x16x32_f16, the row
+//   tiles as operand A: 128 accumulator registers per lane, two waves per SIMD (one wave's barrier
+//   and LDS waits hide behind the other's MFMAs: 4 waves with 256 accumulators each, one per SIMD,
+//   ran config 3's screen in 1.63 ms, these 8 in 1.50 ms);
 // - MFMA kk (0, 1) of a stage takes chunk 4 kk + lane / 16 of a lane's row and query (the same
 //   permutation of the summation order in both operands);
 // - after the last stage the staging LDS holds the survivor list. Per query tile a lane has 32
@@ -45,7 +46,7 @@ namespace {
 
 using namespace screen_detail;
 
-constexpr int kTileWaves = 4;
+constexpr int kTileWaves = 8;
 constexpr int kTileRows  = 256;              // stored rows of a tile (4 steps of 64)
 constexpr int kStageB    = 128;              // bytes of a row per stage (64 halves)
 constexpr int kTileSteps = kTileRows / kStepRows;
@@ -63,14 +64,18 @@ constexpr int tile_lds(int tq) { return 2 * (kTileRows + tq) * kStageB; }
 /** Survivor list entries that fit the staging LDS: 12 bytes each plus the flush's rank word,
  *  after the flush's 2 TQ counters and the waves' 8 KB of parked screen values. */
 constexpr int tile_hit_cap(int tq) { return (tile_lds(tq) - kTileWaves * 8192 - 8 * tq) / 16 / 64 * 64; }
+constexpr int kWQ = 4;  // waves along the queries (two along the rows)
 
+/** QT: query tiles (of 16) per wave. */
 template <int QT, bool FILT>
 __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_args a)
 {
   using R           = f16_rows;
   using acc_t       = v4f;
   using frag_t      = v8h;
-  constexpr int TQ  = 32 * QT;
+  constexpr int TQ  = 16 * kWQ * QT;
+  constexpr int CA  = kTileRows / 8 / kTileWaves;  // row copies per wave and stage
+  constexpr int CB  = TQ / 8 / kTileWaves;         // query copies per wave and stage
   constexpr int BUF = (kTileRows + TQ) * kStageB;  // one stage buffer: rows, then queries
   constexpr int CAP = tile_hit_cap(TQ);
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -79,8 +84,8 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
   const int tid  = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wr   = wave >> 1;  // row half of the tile
-  const int wq   = wave & 1;   // query half of the tile
+  const int wr   = wave / kWQ;  // row half of the tile
+  const int wq   = wave % kWQ;  // query part of the tile
 
   const screen_work w = work_of<TQ>(a, blockIdx.x);
   if (!w.valid) { return; }
@@ -92,44 +97,44 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
 
   if (tid == 0) { n_hits = 0; }
 
-  // this lane's copy offsets: rows of copies j = 0..7 (tile rows (8 wave + j) * 8 + lane / 8), and
-  // queries of copies j = 0..QT-1 (tile queries (QT wave + j) * 8 + lane / 8); rows and queries
-  // past the tile's live ones repeat its last live one (their results are never kept)
+  // this lane's copy offsets: rows of copies j < CA (tile rows (CA wave + j) * 8 + lane / 8), and
+  // queries of copies j < CB (tile queries (CB wave + j) * 8 + lane / 8); rows and queries past
+  // the tile's live ones repeat its last live one (their results are never kept)
   const int crow   = lane >> 3;
   const int cchunk = (lane & 7) ^ crow;
   const char* rbase = reinterpret_cast<const char*>(a.codes) +
                       (w.base + scan0 * a.row_stride) * int64_t(RB) + cchunk * 16;
   const char* qbase = reinterpret_cast<const char*>(a.qcodes) + w.q0 * int64_t(RB) + cchunk * 16;
-  uint32_t roff[8], qoff[QT];
+  uint32_t roff[CA], qoff[CB];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    int64_t r = (wave * 8 + j) * 8 + crow;
+  for (int j = 0; j < CA; ++j) {
+    int64_t r = (wave * CA + j) * 8 + crow;
     r         = r < n_rows ? r : n_rows - 1;
     roff[j]   = uint32_t(r * a.row_stride * RB);
   }
 #pragma unroll
-  for (int j = 0; j < QT; ++j) {
-    int64_t q = (wave * QT + j) * 8 + crow;
+  for (int j = 0; j < CB; ++j) {
+    int64_t q = (wave * CB + j) * 8 + crow;
     q         = q < n_q ? q : n_q - 1;
     qoff[j]   = uint32_t(q * RB);
   }
-  // copy j (0 .. 8 + QT - 1) of stage s: rows for j < 8, queries after; the LDS destination is
+  // copy j (0 .. CA + CB - 1) of stage s: rows for j < CA, queries after; the LDS destination is
   // wave-uniform (scalar: M0)
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   auto copy = [&](int s, int j) {
     uint8_t* buf = lds + (s & 1) * BUF;
-    if (j < 8) {
+    if (j < CA) {
       __builtin_amdgcn_global_load_lds((gptr)(rbase + s * kStageB + roff[j]),
-                                       (lptr)(buf + ((wave_u * 8 + j) * 8) * kStageB), 16, 0, 0);
+                                       (lptr)(buf + ((wave_u * CA + j) * 8) * kStageB), 16, 0, 0);
     } else {
       __builtin_amdgcn_global_load_lds(
-        (gptr)(qbase + s * kStageB + qoff[j - 8]),
-        (lptr)(buf + (kTileRows + (wave_u * QT + j - 8) * 8) * kStageB), 16, 0, 0);
+        (gptr)(qbase + s * kStageB + qoff[j - CA]),
+        (lptr)(buf + (kTileRows + (wave_u * CB + j - CA) * 8) * kStageB), 16, 0, 0);
     }
   };
   auto issue = [&](int s) {
 #pragma unroll
-    for (int j = 0; j < 8 + QT; ++j) { copy(s, j); }
+    for (int j = 0; j < CA + CB; ++j) { copy(s, j); }
   };
 
   // accumulators start at the row terms (dead past the tile's live rows)
@@ -191,12 +196,8 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
       if constexpr (COPY) {
-        if (2 * bt + 1 < 8 + QT) {
-          copy(s + 1, 2 * bt);
-          copy(s + 1, 2 * bt + 1);
-          __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
-        } else if (2 * bt < 8 + QT) {
-          copy(s + 1, 2 * bt);
+        if (bt < CA + CB) {
+          copy(s + 1, bt);
           __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         }
       }
@@ -208,7 +209,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
     }
     __builtin_amdgcn_s_setprio(0);
   };
-  static_assert(8 + QT <= 16, "at most two copies per row tile of the first half");
+  static_assert(CA + CB <= 8, "at most one copy per row tile of the first half");
 
   issue(0);
   for (int s = 0; s + 1 < n_stages; ++s) { stage(s, std::true_type{}); }
@@ -296,7 +297,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
 template <int QT, bool FILT>
 void launch_qt(const screen_args& a, hipStream_t stream)
 {
-  constexpr int TQ = 32 * QT;
+  constexpr int TQ = 16 * kWQ * QT;
   int64_t blocks   = 0;
   if (a.groups != nullptr) {
     blocks = a.n_tiles;
@@ -326,31 +327,15 @@ void launch_qt(const screen_args& a, hipStream_t stream)
 
 int tile_chunk_steps() { return kTileSteps; }
 
-int tile_query_tiles(const int64_t* nq, int n)
-{
-  // cost of a workgroup tile ~ its MFMA work (TQ) plus half its LDS copies (256 + TQ), both
-  // measured as comparable limits at config 3; padding queries cost as much as live ones
-  double best = 0;
-  int pick    = 8;
-  for (int qt : {8, 7}) {
-    const int tq = 32 * qt;
-    double c     = 0;
-    for (int i = 0; i < n; ++i) { c += double((nq[i] + tq - 1) / tq) * (tq + 0.5 * (kTileRows + tq)); }
-    if (qt == 8 || c < best) {
-      best = c;
-      pick = qt;
-    }
-  }
-  return pick;
-}
+int tile_block_queries() { return 16 * kWQ * 4; }
 
 void screen_f16_tile(const screen_args& a, hipStream_t stream)
 {
   const bool filt = a.filter.kind != 0;
-  switch (a.tile_qt) {
-    case 8: filt ? launch_qt<8, true>(a, stream) : launch_qt<8, false>(a, stream); break;
-    case 7: filt ? launch_qt<7, true>(a, stream) : launch_qt<7, false>(a, stream); break;
-    default: throw std::logic_error("certex: the tiled screen takes 7 or 8 query tiles per wave pair");
+  if (filt) {
+    launch_qt<4, true>(a, stream);
+  } else {
+    launch_qt<4, false>(a, stream);
   }
 }
 
