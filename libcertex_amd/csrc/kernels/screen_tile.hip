@@ -40,6 +40,7 @@
 #include <algorithm>
 #include <stdexcept>
 #include <type_traits>
+#include <utility>
 
 namespace certex_amd {
 namespace {
@@ -64,19 +65,46 @@ constexpr int tile_lds(int tq) { return 2 * (kTileRows + tq) * kStageB; }
 /** Survivor list entries that fit the staging LDS: 12 bytes each plus the flush's rank word,
  *  after the flush's 2 TQ counters and the waves' 8 KB of parked screen values. */
 constexpr int tile_hit_cap(int tq) { return (tile_lds(tq) - kTileWaves * 8192 - 8 * tq) / 16 / 64 * 64; }
-constexpr int kWQ = 4;  // waves along the queries (two along the rows)
 
-/** QT: query tiles (of 16) per wave. */
-template <int QT, bool FILT>
+/** f(std::integral_constant<int, i>{}) for i = 0 .. N - 1, unrolled at compile time. */
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>)
+{
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+/**
+ * The tile of a workgroup: RT row tiles (16 rows each) and QT query tiles per wave; 256 / (16 RT)
+ * waves along the rows and the rest of the 8 along the queries, TQ = 16 QT x that many queries.
+ */
+template <int RT, int QT>
+struct tile_shape {
+  static constexpr int WR = kTileRows / (16 * RT);
+  static constexpr int WQ = kTileWaves / WR;
+  static constexpr int TQ = 16 * QT * WQ;
+  static_assert(WR * WQ == kTileWaves && WR * 16 * RT == kTileRows, "8 waves cover the tile");
+};
+
+template <int RT, int QT, bool FILT>
 __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_args a)
 {
   using R           = f16_rows;
   using acc_t       = v4f;
   using frag_t      = v8h;
-  constexpr int TQ  = 16 * kWQ * QT;
-  constexpr int CA  = kTileRows / 8 / kTileWaves;  // row copies per wave and stage
-  constexpr int CB  = TQ / 8 / kTileWaves;         // query copies per wave and stage
-  constexpr int BUF = (kTileRows + TQ) * kStageB;  // one stage buffer: rows, then queries
+  using S           = tile_shape<RT, QT>;
+  constexpr int TQ  = S::TQ;
+  constexpr int CA  = kTileRows / 8 / kTileWaves;         // row copies per wave and stage
+  constexpr int CBT = TQ / 8;                              // query copies per stage
+  constexpr int CB  = (CBT + kTileWaves - 1) / kTileWaves;  // per wave (the last may take fewer)
+  constexpr int NC  = CA + CB;                             // copies per wave
+  constexpr int CPT = (NC + RT - 1) / RT;                  // copies per first-half row tile
+  constexpr int QPT = (QT + RT - 1) / RT;                  // second-half query fragments per row tile
+  constexpr int BUF = (kTileRows + TQ) * kStageB;          // one stage buffer: rows, then queries
   constexpr int CAP = tile_hit_cap(TQ);
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ uint32_t n_hits;
@@ -84,8 +112,8 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
   const int tid  = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wr   = wave / kWQ;  // row half of the tile
-  const int wq   = wave % kWQ;  // query part of the tile
+  const int wr   = wave / S::WQ;  // row part of the tile
+  const int wq   = wave % S::WQ;  // query part of the tile
 
   const screen_work w = work_of<TQ>(a, blockIdx.x);
   if (!w.valid) { return; }
@@ -98,8 +126,9 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
   if (tid == 0) { n_hits = 0; }
 
   // this lane's copy offsets: rows of copies j < CA (tile rows (CA wave + j) * 8 + lane / 8), and
-  // queries of copies j < CB (tile queries (CB wave + j) * 8 + lane / 8); rows and queries past
-  // the tile's live ones repeat its last live one (their results are never kept)
+  // queries of copies j < CB (tile queries (CB wave + j) * 8 + lane / 8, when that copy exists);
+  // rows and queries past the tile's live ones repeat its last live one (their results are never
+  // kept)
   const int crow   = lane >> 3;
   const int cchunk = (lane & 7) ^ crow;
   const char* rbase = reinterpret_cast<const char*>(a.codes) +
@@ -118,7 +147,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
     q         = q < n_q ? q : n_q - 1;
     qoff[j]   = uint32_t(q * RB);
   }
-  // copy j (0 .. CA + CB - 1) of stage s: rows for j < CA, queries after; the LDS destination is
+  // copy j (0 .. NC - 1) of stage s: rows for j < CA, queries after; the LDS destination is
   // wave-uniform (scalar: M0)
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   auto copy = [&](int s, int j) {
@@ -126,7 +155,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
     if (j < CA) {
       __builtin_amdgcn_global_load_lds((gptr)(rbase + s * kStageB + roff[j]),
                                        (lptr)(buf + ((wave_u * CA + j) * 8) * kStageB), 16, 0, 0);
-    } else {
+    } else if (wave_u * CB + j - CA < CBT) {
       __builtin_amdgcn_global_load_lds(
         (gptr)(qbase + s * kStageB + qoff[j - CA]),
         (lptr)(buf + (kTileRows + (wave_u * CB + j - CA) * 8) * kStageB), 16, 0, 0);
@@ -134,18 +163,18 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
   };
   auto issue = [&](int s) {
 #pragma unroll
-    for (int j = 0; j < CA + CB; ++j) { copy(s, j); }
+    for (int j = 0; j < NC; ++j) { copy(s, j); }
   };
 
   // accumulators start at the row terms (dead past the tile's live rows)
   const float* rowc = static_cast<const float*>(a.rowc);
-  acc_t acc[8][QT];
+  acc_t acc[RT][QT];
 #pragma unroll
-  for (int bt = 0; bt < 8; ++bt) {
+  for (int bt = 0; bt < RT; ++bt) {
     acc_t c;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int64_t r = wr * 128 + bt * 16 + (lane >> 4) * 4 + j;
+      const int64_t r = wr * 16 * RT + bt * 16 + (lane >> 4) * 4 + j;
       const bool ok   = r < n_rows;
       const float v   = rowc[w.base + (scan0 + (ok ? r : 0)) * a.row_stride];
       c[j]            = ok ? v : R::dead();
@@ -157,7 +186,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
   // fragment addresses within a stage buffer: row tile bt, query tile qt, chunk 4 kk + lane / 16
   const int frow = lane & 15;
   auto a_frag    = [&](const uint8_t* buf, int bt, int kk) {
-    const int r = wr * 128 + bt * 16 + frow;
+    const int r = wr * 16 * RT + bt * 16 + frow;
     const int c = kk * 4 + (lane >> 4);
     return *reinterpret_cast<const frag_t*>(buf + r * kStageB + ((c ^ (r & 7)) << 4));
   };
@@ -176,40 +205,41 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
     wait_copies();
     __syncthreads();
     const uint8_t* buf = lds + (s & 1) * BUF;
-    frag_t ar[2][8], bq[2][QT];
+    frag_t ar[2][RT], bq[2][QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) { bq[0][qt] = b_frag(buf, qt, 0); }
 #pragma unroll
-    for (int bt = 0; bt < 8; ++bt) { ar[0][bt] = a_frag(buf, bt, 0); }
-    __builtin_amdgcn_sched_group_barrier(0x100, QT + 8, 0);
+    for (int bt = 0; bt < RT; ++bt) { ar[0][bt] = a_frag(buf, bt, 0); }
+    __builtin_amdgcn_sched_group_barrier(0x100, QT + RT, 0);
     __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int bt = 0; bt < 8; ++bt) {
+    static_for<RT>([&](auto BT) {
+      constexpr int bt = decltype(BT)::value;
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = R::mfma(ar[0][bt], bq[0][qt], acc[bt][qt]); }
       __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);
+      constexpr int q0 = bt * QPT;
+      constexpr int q1 = q0 + QPT < QT ? q0 + QPT : QT;
       ar[1][bt] = a_frag(buf, bt, 1);
-      if (bt < QT) {
-        bq[1][bt] = b_frag(buf, bt, 1);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      } else {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
+#pragma unroll
+      for (int qt = q0; qt < q1; ++qt) { bq[1][qt] = b_frag(buf, qt, 1); }
+      __builtin_amdgcn_sched_group_barrier(0x100, 1 + (q1 > q0 ? q1 - q0 : 0), 0);
       if constexpr (COPY) {
-        if (bt < CA + CB) {
-          copy(s + 1, bt);
-          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        constexpr int c0 = bt * CPT;
+        constexpr int c1 = c0 + CPT < NC ? c0 + CPT : NC;
+        if constexpr (c1 > c0) {
+#pragma unroll
+          for (int j = c0; j < c1; ++j) { copy(s + 1, j); }
+          __builtin_amdgcn_sched_group_barrier(0x020, c1 - c0, 0);
         }
       }
-    }
+    });
 #pragma unroll
-    for (int bt = 0; bt < 8; ++bt) {
+    for (int bt = 0; bt < RT; ++bt) {
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = R::mfma(ar[1][bt], bq[1][qt], acc[bt][qt]); }
     }
     __builtin_amdgcn_s_setprio(0);
   };
-  static_assert(CA + CB <= 8, "at most one copy per row tile of the first half");
 
   issue(0);
   for (int s = 0; s + 1 < n_stages; ++s) { stage(s, std::true_type{}); }
@@ -221,11 +251,11 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
   uint32_t* hit_row  = hit_q + CAP;
   float* hit_val     = reinterpret_cast<float*>(hit_row + CAP);
   uint32_t* scratch  = reinterpret_cast<uint32_t*>(hit_val + CAP);  // 2 TQ + CAP words
-  // per wave 8 KB: a lane's 32 screen values of one query tile, 16-byte slot bt ^ (lane & 7) of
+  // per wave 8 KB: a lane's 4 RT screen values of one query tile, 16-byte slot bt ^ (lane & 7) of
   // its 128 bytes, so that the survivor loop reads a value by its bit index
   uint8_t* vals      = lds + tile_lds(TQ) - kTileWaves * 8192 + wave * 8192 + lane * 128;
   const float* theta = static_cast<const float*>(a.theta);
-  const int64_t row0 = w.base + scan0 + wr * 128 + (lane >> 4) * 4;  // stored row of bit 0
+  const int64_t row0 = w.base + scan0 + wr * 16 * RT + (lane >> 4) * 4;  // stored row of bit 0
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int qloc = wq * 16 * QT + qt * 16 + frow;
@@ -233,7 +263,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
     const float th = qloc < n_q ? theta[w.q0 + qloc] : R::keep_none();
     uint32_t bits  = 0;  // bit bt * 4 + r: row row0 + 16 bt + r
 #pragma unroll
-    for (int bt = 0; bt < 8; ++bt) {
+    for (int bt = 0; bt < RT; ++bt) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) { bits |= uint32_t(acc[bt][qt][r] >= th) << (bt * 4 + r); }
     }
@@ -249,13 +279,13 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
       }
     }
 #pragma unroll
-    for (int bt = 0; bt < 8; ++bt) {
+    for (int bt = 0; bt < RT; ++bt) {
       *reinterpret_cast<acc_t*>(vals + ((bt ^ (lane & 7)) << 4)) = acc[bt][qt];
     }
     const uint32_t cnt = uint32_t(__builtin_popcount(bits));
     uint32_t excl = 0, total = 0;
 #pragma unroll
-    for (int b = 0; b < 6; ++b) {
+    for (int b = 0; (1 << b) <= 4 * RT; ++b) {
       const uint64_t m = __ballot((cnt >> b) & 1u);
       excl += __builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)) << b;
       total += uint32_t(__builtin_popcountll(m)) << b;
@@ -294,10 +324,10 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
   flush_hits<true>(w.q0, TQ, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(CAP), scratch);
 }
 
-template <int QT, bool FILT>
-void launch_qt(const screen_args& a, hipStream_t stream)
+template <int RT, int QT, bool FILT>
+void launch_shape(const screen_args& a, hipStream_t stream)
 {
-  constexpr int TQ = 16 * kWQ * QT;
+  constexpr int TQ = tile_shape<RT, QT>::TQ;
   int64_t blocks   = 0;
   if (a.groups != nullptr) {
     blocks = a.n_tiles;
@@ -313,7 +343,7 @@ void launch_qt(const screen_args& a, hipStream_t stream)
   }
   screen_args b = a;
   b.spill_cap   = a.spill_q != nullptr ? a.spill_pool / blocks : 0;
-  auto* k       = &screen_tile_kernel<QT, FILT>;
+  auto* k       = &screen_tile_kernel<RT, QT, FILT>;
   const int lds = tile_lds(TQ);
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(k),
                           hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) {
@@ -327,15 +357,14 @@ void launch_qt(const screen_args& a, hipStream_t stream)
 
 int tile_chunk_steps() { return kTileSteps; }
 
-int tile_block_queries() { return 16 * kWQ * 4; }
+int tile_block_queries() { return tile_shape<8, 4>::TQ; }
 
 void screen_f16_tile(const screen_args& a, hipStream_t stream)
 {
-  const bool filt = a.filter.kind != 0;
-  if (filt) {
-    launch_qt<4, true>(a, stream);
+  if (a.filter.kind != 0) {
+    launch_shape<8, 4, true>(a, stream);
   } else {
-    launch_qt<4, false>(a, stream);
+    launch_shape<8, 4, false>(a, stream);
   }
 }
 
