@@ -336,14 +336,14 @@ constexpr int kSortBelow = 512;
 /**
  * Keeps the k best (key, row) pairs of [0, n), k <= n <= kBuf, in [0, k) of the same arrays (in
  * order after a sort of few pairs, else in no particular order), and returns the k-th smallest
- * key (which bounds the k-th score). With the select, each thread holds its at most
- * kBuf / kThreads pairs in registers while the kept ones are rewritten.
+ * key (which bounds the k-th score). With the select, the kept pairs are compacted in place, 4
+ * pairs per thread at a time (all pairs of a thread in registers had taken 48 VGPRs, which bounded
+ * the verify kernels' occupancy).
  */
 __device__ inline uint64_t keep_k_best(uint64_t* key, uint32_t* row, int n, int k, int* hist,
                                        int* wave_tot, uint32_t* sel_digit, int* sel_rank,
                                        int* sel_count, int* fill)
 {
-  constexpr int kPer = kBuf / kThreads;
   if (n <= kSortBelow) {  // few pairs: one bitonic sort costs fewer barriers than the select
     const int P = pow2_at_least(n);
     for (int j = n + threadIdx.x; j < P; j += kThreads) {
@@ -361,27 +361,33 @@ __device__ inline uint64_t keep_k_best(uint64_t* key, uint32_t* row, int n, int 
   const uint64_t K = kth_key;
   if (n == k) { return K; }
   const uint32_t R = kth_row;
-  uint64_t kk[kPer];
-  uint32_t rr[kPer];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int e = threadIdx.x + i * kThreads;
-    kk[i]       = e < n ? key[e] : ~0ull;
-    rr[i]       = e < n ? row[e] : ~0u;
-  }
+  // in place, in chunks of kPer entries per thread: a chunk is read whole (barrier) before any of
+  // its kept entries is written, and the kept count never passes the entries read so far
+  constexpr int kPer = 4;
   if (threadIdx.x == 0) { *fill = 0; }
   __syncthreads();
+  for (int c0 = 0; c0 < n; c0 += kThreads * kPer) {
+    uint64_t kk[kPer];
+    uint32_t rr[kPer];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int e    = threadIdx.x + i * kThreads;
-    const bool in  = e < n && (kk[i] < K || (kk[i] == K && rr[i] <= R));
-    const int s    = wave_append(in, fill);
-    if (in) {
-      key[s] = kk[i];
-      row[s] = rr[i];
+    for (int i = 0; i < kPer; ++i) {
+      const int e = c0 + threadIdx.x + i * kThreads;
+      kk[i]       = e < n ? key[e] : ~0ull;
+      rr[i]       = e < n ? row[e] : ~0u;
     }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int e   = c0 + threadIdx.x + i * kThreads;
+      const bool in = e < n && (kk[i] < K || (kk[i] == K && rr[i] <= R));
+      const int s   = wave_append(in, fill);
+      if (in) {
+        key[s] = kk[i];
+        row[s] = rr[i];
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
   return K;
 }
 
@@ -1002,7 +1008,7 @@ __device__ uint32_t radix_select(int64_t n, int rank, F key_of, int* hist, int* 
  * stay in LDS.
  */
 template <int L>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(L == 64 ? 5 : 4)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(L == 64 ? 6 : 4)))
 void verify_topk_f_kernel(verify_f_args a, int cap)
 {
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
