@@ -141,17 +141,11 @@ def hbm_roofline(kernel, bytes_per_launch, ms_per_launch, what):
 
 
 def float_phase_rooflines(ms, launches, steps, st, nq, d, k, elem):
-    """Threshold and verify rooflines of a float search (one batch per step): the threshold scores
-    max(128, k + max(k / 4, 16)) anchors per query exactly; the verify reads every survivor's
-    bucket entry (row and screen value) and the vectors of the rows it scores."""
-    per_query = max(128, k + max(k // 4, 16))
-    t_ms = ms[1] / max(1, launches[1])
+    """Verify roofline of a float search (one batch per step): the verify reads every survivor's
+    bucket entry (row and screen value), the query and the vectors of the rows it scores."""
     v_ms = ms[3] / max(1, launches[3])
     per_launch = max(1, launches[3] // steps)
     return {
-        "threshold": hbm_roofline(
-            "threshold_f16_kernel", nq * (per_query * d * elem + d * elem) / per_launch, t_ms,
-            f"{per_query} anchor vectors of {d} x {elem} B and the query, per query"),
         "verify_topk": hbm_roofline(
             "verify_topk_f_kernel", (st.verified * d * elem + st.survivors * 8 + nq * d * elem) / per_launch,
             v_ms, f"{st.verified / max(1, st.queries):.1f} scored vectors of {d} x {elem} B and "
@@ -481,17 +475,25 @@ def summarize_profiles(dirs, warmup, steps, after=1):
         sel = vals[len(vals) - (steps + after) * per : len(vals) - after * per]
         return sum(sel) / len(sel) if sel else None
 
+    def data_gen(name):
+        return " at::" in name or name.startswith("at::") or name.startswith("Cijk_")
+
     traces, counters = defaultdict(list), defaultdict(list)
     for d in dirs:
         for f in sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)):
             for r in csv.DictReader(open(f)):
+                if data_gen(r["Kernel_Name"]):
+                    continue
                 traces[short(r["Kernel_Name"])].append(
                     (int(r["Dispatch_Id"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6))
         for f in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
             for r in csv.DictReader(open(f)):
+                if data_gen(r["Kernel_Name"]):
+                    continue
                 counters[(short(r["Kernel_Name"]), r["Counter_Name"])].append(
                     (int(r["Dispatch_Id"]), float(r["Counter_Value"])))
-    out = [f"# {searches} searches per run: {warmup} warm-up, {steps} timed, {after} after (stats)"]
+    out = [f"# {searches} searches per run: {warmup} warm-up, {steps} timed, {after} after (stats); "
+           "torch's and hipBLASLt's data-generation kernels left out"]
     if traces:
         out.append(f"{'kernel':<64} {'calls':>5} {'total_ms':>10} {'avg_ms':>9} {'timed_avg_ms':>12} "
                    f"{'min_ms':>8} {'max_ms':>8}")
