@@ -220,7 +220,7 @@ def bench_config3(args):
             "phase_rooflines": float_phase_rooflines(ms, launches, args.steps, st, nq, d, k, 4),
         },
         "roofline": {
-            "bound": "mfma", "kernel": "screen_tile_kernel (fp16 MFMA screen, LDS-staged 256-row x 256-query tiles, label-routed)",
+            "bound": "mfma", "kernel": "screen_tile_kernel (fp16 MFMA screen, LDS-staged 256-row x 128-query tiles, two workgroups per CU, label-routed)",
             "achieved": round(achieved, 2), "peak": P_FP16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / P_FP16_TFLOPS, 4), "traffic": None,
             "avg_launch_ms": round(screen_ms, 4), "flops_per_launch": flops_per_launch,

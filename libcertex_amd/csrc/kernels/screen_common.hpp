@@ -61,12 +61,20 @@ struct screen_work {
   bool valid;
 };
 
+/** x / d for x >= 0 and d > 0, in 32-bit arithmetic when x fits (the usual case). */
+__device__ inline int64_t div_small(int64_t x, int64_t d)
+{
+  if ((uint64_t(x) >> 32) == 0 && (uint64_t(d) >> 32) == 0) { return int64_t(uint32_t(x) / uint32_t(d)); }
+  return x / d;
+}
+
 /**
  * Work of block b. Plain launches: block b runs on XCD b % 8 and the query blocks of one row
  * chunk are consecutive on one XCD (chunk = (b / 8 / n_qb) * 8 + b % 8). Routed launches: the
- * group whose tiles hold b (binary search over tile0), then query block and chunk within it, in
- * the same XCD order when the group has several query blocks (its tile0 is then a multiple of 8,
- * screen_group_tile0). Blocks past a group's chunks (octet padding, alignment gaps) are invalid.
+ * group whose tiles hold b (a ballot over the first tiles of up to 64 groups, else a binary
+ * search over them), then query block and chunk within it, in the same XCD order when the group
+ * has several query blocks (its tile0 is then a multiple of 8, screen_group_tile0). Blocks past a
+ * group's chunks (octet padding, alignment gaps) are invalid. Every lane of the block calls it.
  */
 template <int QB>
 __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
@@ -85,26 +93,35 @@ __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
     w.valid                = w.chunk < n_chunks;
     return w;
   }
-  int lo = 0, hi = a.n_route - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (a.groups[mid].tile0 <= int64_t(b)) {
-      lo = mid;
-    } else {
-      hi = mid - 1;
+  // the group: one vector load of up to 64 groups' first tiles and a ballot, else a binary search
+  int lo = 0;
+  if (a.n_route <= 64) {
+    const int lane   = threadIdx.x & 63;
+    const int64_t t0 = lane < a.n_route ? a.groups[lane].tile0 : INT64_MAX;
+    const int c      = __popcll(__ballot(t0 <= int64_t(b)));
+    lo               = __builtin_amdgcn_readfirstlane(c > 0 ? c - 1 : 0);
+  } else {
+    int hi = a.n_route - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (a.groups[mid].tile0 <= int64_t(b)) {
+        lo = mid;
+      } else {
+        hi = mid - 1;
+      }
     }
   }
   const screen_group g = a.groups[lo];
   const int64_t t      = int64_t(b) - g.tile0;
-  const int64_t n_qb   = (g.nq + QB - 1) / QB;
-  const int64_t i      = t >> 3;
-  w.q0                 = g.q0 + (n_qb > 1 ? i % n_qb : 0) * QB;
+  const uint32_t n_qb  = uint32_t(div_small(g.nq + QB - 1, QB));
+  const uint32_t i     = uint32_t(t) >> 3;
+  w.q0                 = g.q0 + int64_t(n_qb > 1 ? i % n_qb : 0) * QB;
   w.q_end              = g.q0 + g.nq;
-  w.chunk              = n_qb > 1 ? (i / n_qb) * 8 + (t & 7) : t;
-  w.n_scan             = (g.nx + a.row_stride - 1) / a.row_stride;
+  w.chunk              = n_qb > 1 ? int64_t(i / n_qb) * 8 + (t & 7) : t;
+  w.n_scan             = a.row_stride == 1 ? g.nx : div_small(g.nx + a.row_stride - 1, a.row_stride);
   w.base               = g.x0;
   const int64_t steps  = screen_steps(w.n_scan);
-  w.valid              = t >= 0 && w.chunk < (steps + a.chunk_steps - 1) / a.chunk_steps;
+  w.valid              = t >= 0 && w.chunk < div_small(steps + a.chunk_steps - 1, a.chunk_steps);
   return w;
 }
 

@@ -1,5 +1,5 @@
-// fp16 certified screen for rows of more than 128 halves (gfx950): LDS-staged, double-buffered
-// tiles of rows and queries, both fed to the MFMA from LDS.
+// fp16 certified screen for rows of more than 128 halves (gfx950): LDS-staged tiles of rows and
+// queries, both fed to the MFMA from LDS, two workgroups resident per CU.
 //
 // Reference contract: detail/screen_sm80.cu:117-379 and detail/screen_sm90.cu:594-785 (fp16 MMA,
 // fp32 accumulation, keep a pair iff its screen value reaches the query threshold; the reference
@@ -8,24 +8,24 @@
 // the threshold, so the test needs no per-pair arithmetic.
 //
 // Work decomposition:
-// - a workgroup of 8 waves computes one tile of 256 stored rows x 256 queries, all of the row's
-//   halves, in stages of 64 halves (128 bytes of every row and query);
-// - a stage of both operands is copied into LDS by global_load_lds_dwordx4 (no VGPRs, 8 lanes on
-//   one row's 128-byte line). The 16-byte chunk c of tile row r lands in slot c ^ (r & 7) of the
-//   row's 128 bytes: lane i of a copy writes slot i % 8 of row i / 8, so it reads chunk
-//   (i % 8) ^ (i / 8) of that row. The ds_read_b128 of a 16-row MFMA fragment is then free of bank
-//   conflicts (rows r and r + 8 share slots, and a b128 read serves 8 lanes per pass);
-// - two stage buffers: while the MFMAs run on stage s, the copies of stage s + 1 are in flight; one
-//   barrier per stage both publishes a stage and frees the other buffer. Within a stage the copies
-//   and the LDS reads of the second MFMA half are issued between the row tiles of the first half
-//   (pinned with sched_group_barrier), so that their issue and latency hide behind MFMAs;
-// - the waves form a 2 x 4 grid: wave (wr, wq) multiplies tile rows 128 wr .. 128 wr + 127 (8 row
+// - a workgroup of 4 waves computes one tile of 256 stored rows x 128 queries, all of the row's
+//   halves, in stages of 32 halves (64 bytes of every row and query, one MFMA k-step);
+// - two workgroups share a CU (73.5 KB of LDS and 4 waves each, 2 waves per SIMD), so that one
+//   workgroup's barriers, copies' latency, survivor epilogue and flush overlap the other's MFMAs;
+// - a stage of both operands is copied into LDS by global_load_lds_dwordx4 (no VGPRs): a copy
+//   moves 16 rows x 64 bytes, lane i on row i / 4. Row r's 64 bytes are half of a 128-byte LDS
+//   line (the line of rows r & ~1), and its 16-byte chunk c lands in slot c ^ ((r >> 1) & 3) of
+//   that half, so lane i reads chunk (i & 3) ^ ((i >> 3) & 3) of its row. The ds_read_b128 of a
+//   16-row MFMA fragment (lanes on 16 rows, one chunk) then serves 8 lanes per pass from 8
+//   distinct 16-byte slots of a 128-byte line: no bank conflicts;
+// - three stage buffers: the copies of stage s + 2 fly while the MFMAs run on stage s; at the top
+//   of stage s a wave waits for its own copies of stage s only (those of s + 1 stay in flight),
+//   then one barrier publishes stage s and frees the buffer of stage s - 1;
+// - the waves form a 2 x 2 grid: wave (wr, wq) multiplies tile rows 128 wr .. 128 wr + 127 (8 row
 //   tiles) with tile queries 64 wq .. 64 wq + 63 (4 query tiles), v_mfma_f32_16x16x32_f16, the row
-//   tiles as operand A: 128 accumulator registers per lane, two waves per SIMD (one wave's barrier
-//   and LDS waits hide behind the other's MFMAs: 4 waves with 256 accumulators each, one per SIMD,
-//   ran config 3's screen in 1.63 ms, these 8 in 1.50 ms);
-// - MFMA kk (0, 1) of a stage takes chunk 4 kk + lane / 16 of a lane's row and query (the same
-//   permutation of the summation order in both operands);
+//   tiles as operand A: 128 accumulator registers per lane. Chunk lane / 16 of a stage's 64 bytes
+//   is the k-slice of a lane in both operands (the same permutation of the summation order);
+// - the row terms and the query thresholds are copied into LDS with the first stages;
 // - after the last stage the staging LDS holds the survivor list. Per query tile a lane has 32
 //   rows; the wave reserves its survivors with one LDS atomic (exclusive prefix of the lanes'
 //   counts from one ballot + mbcnt per bit of the count), the lanes park their 32 screen values in
@@ -47,20 +47,29 @@ namespace {
 
 using namespace screen_detail;
 
-constexpr int kTileWaves = 8;
+constexpr int kTileWaves = 4;
 constexpr int kTileRows  = 256;              // stored rows of a tile (4 steps of 64)
-constexpr int kStageB    = 128;              // bytes of a row per stage (64 halves)
+constexpr int kStageB    = 64;               // bytes of a row per stage (32 halves)
+constexpr int kBufs      = 3;                // stage buffers
 constexpr int kTileSteps = kTileRows / kStepRows;
 
 typedef const __attribute__((address_space(1))) void* gptr;
 typedef __attribute__((address_space(3))) void* lptr;
 
-/** s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima): this wave's global loads,
- *  LDS-DMA copies included, have completed. */
-__device__ __forceinline__ void wait_copies() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+/** s_waitcnt vmcnt(N) (expcnt and lgkmcnt left at their maxima): at most N of this wave's global
+ *  loads, LDS-DMA copies included, are still in flight (they complete in issue order). */
+template <int N>
+__device__ __forceinline__ void wait_copies()
+{
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
 
-/** LDS bytes of a workgroup of TQ queries: two stage buffers of (256 + TQ) rows x 128 bytes. */
-constexpr int tile_lds(int tq) { return 2 * (kTileRows + tq) * kStageB; }
+/** Staging LDS of a workgroup of TQ queries: three stage buffers of (256 + TQ) rows x 64 bytes. */
+constexpr int tile_lds(int tq) { return kBufs * (kTileRows + tq) * kStageB; }
+
+/** All LDS of a workgroup: the staging, then the TQ query thresholds and the 256 row terms. */
+constexpr int tile_lds_total(int tq) { return tile_lds(tq) + 4 * tq + 4 * kTileRows; }
 
 /** Survivor list entries that fit the staging LDS: 12 bytes each plus the flush's rank word,
  *  after the flush's 2 TQ counters and the waves' 8 KB of parked screen values. */
@@ -80,31 +89,31 @@ __device__ __forceinline__ void static_for(F&& f)
 
 /**
  * The tile of a workgroup: RT row tiles (16 rows each) and QT query tiles per wave; 256 / (16 RT)
- * waves along the rows and the rest of the 8 along the queries, TQ = 16 QT x that many queries.
+ * waves along the rows and the rest of the 4 along the queries, TQ = 16 QT x that many queries.
  */
 template <int RT, int QT>
 struct tile_shape {
   static constexpr int WR = kTileRows / (16 * RT);
   static constexpr int WQ = kTileWaves / WR;
   static constexpr int TQ = 16 * QT * WQ;
-  static_assert(WR * WQ == kTileWaves && WR * 16 * RT == kTileRows, "8 waves cover the tile");
+  static_assert(WR * WQ == kTileWaves && WR * 16 * RT == kTileRows, "4 waves cover the tile");
 };
 
 template <int RT, int QT, bool FILT>
-__global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_args a)
+__global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_args a)
 {
   using R           = f16_rows;
   using acc_t       = v4f;
   using frag_t      = v8h;
   using S           = tile_shape<RT, QT>;
   constexpr int TQ  = S::TQ;
-  constexpr int CA  = kTileRows / 8 / kTileWaves;         // row copies per wave and stage
-  constexpr int CBT = TQ / 8;                              // query copies per stage
-  constexpr int CB  = (CBT + kTileWaves - 1) / kTileWaves;  // per wave (the last may take fewer)
-  constexpr int NC  = CA + CB;                             // copies per wave
-  constexpr int CPT = (NC + RT - 1) / RT;                  // copies per first-half row tile
-  constexpr int QPT = (QT + RT - 1) / RT;                  // second-half query fragments per row tile
-  constexpr int BUF = (kTileRows + TQ) * kStageB;          // one stage buffer: rows, then queries
+  constexpr int CA  = kTileRows / 16 / kTileWaves;  // row copies per wave and stage
+  constexpr int CB  = TQ / 16 / kTileWaves;         // query copies per wave and stage
+  constexpr int NC  = CA + CB;                      // copies per wave and stage
+  static_assert(CA * 16 * kTileWaves == kTileRows && CB * 16 * kTileWaves == TQ,
+                "every wave issues the same copies (the stage waits count them)");
+  constexpr int CPT = (NC + RT - 1) / RT;           // copies per row tile
+  constexpr int BUF = (kTileRows + TQ) * kStageB;   // one stage buffer: rows, then queries
   constexpr int CAP = tile_hit_cap(TQ);
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ uint32_t n_hits;
@@ -117,7 +126,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
 
   const screen_work w = work_of<TQ>(a, blockIdx.x);
   if (!w.valid) { return; }
-  const int RB          = a.row_bytes;  // bytes per row: a multiple of 128
+  const int RB          = a.row_bytes;  // bytes per row: a multiple of 64
   const int n_stages    = RB / kStageB;
   const int64_t scan0   = w.chunk * kTileRows;  // scan index of tile row 0
   const int64_t n_rows  = w.n_scan - scan0 < kTileRows ? w.n_scan - scan0 : kTileRows;
@@ -125,40 +134,55 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
 
   if (tid == 0) { n_hits = 0; }
 
-  // this lane's copy offsets: rows of copies j < CA (tile rows (CA wave + j) * 8 + lane / 8), and
-  // queries of copies j < CB (tile queries (CB wave + j) * 8 + lane / 8, when that copy exists);
-  // rows and queries past the tile's live ones repeat its last live one (their results are never
-  // kept)
-  const int crow   = lane >> 3;
-  const int cchunk = (lane & 7) ^ crow;
-  const char* rbase = reinterpret_cast<const char*>(a.codes) +
-                      (w.base + scan0 * a.row_stride) * int64_t(RB) + cchunk * 16;
+  // the query thresholds and the row terms into LDS past the staging (waited for with stage 0);
+  // indices past the live queries and rows repeat the last live one
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  float* th_lds    = reinterpret_cast<float*>(lds + tile_lds(TQ));
+  float* rc_lds    = th_lds + TQ;
+  {
+    const int64_t r = wave_u * 64 + lane;
+    __builtin_amdgcn_global_load_lds(
+      (gptr)(static_cast<const float*>(a.rowc) + w.base + scan0 + (r < n_rows ? r : n_rows - 1)),
+      (lptr)(rc_lds + wave_u * 64), 4, 0, 0);
+    if (wave_u * 64 < TQ) {
+      const int64_t q = wave_u * 64 + lane;
+      __builtin_amdgcn_global_load_lds(
+        (gptr)(static_cast<const float*>(a.theta) + w.q0 + (q < n_q ? q : n_q - 1)),
+        (lptr)(th_lds + wave_u * 64), 4, 0, 0);
+    }
+  }
+
+  // this lane's copy offsets: rows of copies j < CA (tile rows (CA wave + j) * 16 + lane / 4), and
+  // queries of copies j < CB (tile queries (CB wave + j) * 16 + lane / 4); rows and queries past
+  // the tile's live ones repeat its last live one (their results are never kept)
+  const int crow   = lane >> 2;
+  const int cchunk = (lane & 3) ^ ((lane >> 3) & 3);
+  const char* rbase = reinterpret_cast<const char*>(a.codes) + (w.base + scan0) * int64_t(RB) + cchunk * 16;
   const char* qbase = reinterpret_cast<const char*>(a.qcodes) + w.q0 * int64_t(RB) + cchunk * 16;
   uint32_t roff[CA], qoff[CB];
 #pragma unroll
   for (int j = 0; j < CA; ++j) {
-    int64_t r = (wave * CA + j) * 8 + crow;
+    int64_t r = (wave * CA + j) * 16 + crow;
     r         = r < n_rows ? r : n_rows - 1;
-    roff[j]   = uint32_t(r * a.row_stride * RB);
+    roff[j]   = uint32_t(r * RB);
   }
 #pragma unroll
   for (int j = 0; j < CB; ++j) {
-    int64_t q = (wave * CB + j) * 8 + crow;
+    int64_t q = (wave * CB + j) * 16 + crow;
     q         = q < n_q ? q : n_q - 1;
     qoff[j]   = uint32_t(q * RB);
   }
   // copy j (0 .. NC - 1) of stage s: rows for j < CA, queries after; the LDS destination is
   // wave-uniform (scalar: M0)
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   auto copy = [&](int s, int j) {
-    uint8_t* buf = lds + (s & 1) * BUF;
+    uint8_t* buf = lds + (s % kBufs) * BUF;
     if (j < CA) {
       __builtin_amdgcn_global_load_lds((gptr)(rbase + s * kStageB + roff[j]),
-                                       (lptr)(buf + ((wave_u * CA + j) * 8) * kStageB), 16, 0, 0);
-    } else if (wave_u * CB + j - CA < CBT) {
+                                       (lptr)(buf + ((wave_u * CA + j) * 16) * kStageB), 16, 0, 0);
+    } else {
       __builtin_amdgcn_global_load_lds(
         (gptr)(qbase + s * kStageB + qoff[j - CA]),
-        (lptr)(buf + (kTileRows + (wave_u * CB + j - CA) * 8) * kStageB), 16, 0, 0);
+        (lptr)(buf + (kTileRows + (wave_u * CB + j - CA) * 16) * kStageB), 16, 0, 0);
     }
   };
   auto issue = [&](int s) {
@@ -166,85 +190,77 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
     for (int j = 0; j < NC; ++j) { copy(s, j); }
   };
 
-  // accumulators start at the row terms (dead past the tile's live rows)
-  const float* rowc = static_cast<const float*>(a.rowc);
-  acc_t acc[RT][QT];
-#pragma unroll
-  for (int bt = 0; bt < RT; ++bt) {
-    acc_t c;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t r = wr * 16 * RT + bt * 16 + (lane >> 4) * 4 + j;
-      const bool ok   = r < n_rows;
-      const float v   = rowc[w.base + (scan0 + (ok ? r : 0)) * a.row_stride];
-      c[j]            = ok ? v : R::dead();
-    }
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = c; }
-  }
-
-  // fragment addresses within a stage buffer: row tile bt, query tile qt, chunk 4 kk + lane / 16
+  // fragment addresses within a stage buffer: row tile bt, query tile qt, chunk lane / 16
   const int frow = lane & 15;
-  auto a_frag    = [&](const uint8_t* buf, int bt, int kk) {
+  const int fch  = lane >> 4;
+  auto a_frag    = [&](const uint8_t* buf, int bt) {
     const int r = wr * 16 * RT + bt * 16 + frow;
-    const int c = kk * 4 + (lane >> 4);
-    return *reinterpret_cast<const frag_t*>(buf + r * kStageB + ((c ^ (r & 7)) << 4));
+    return *reinterpret_cast<const frag_t*>(buf + r * kStageB + ((fch ^ ((r >> 1) & 3)) << 4));
   };
-  auto b_frag = [&](const uint8_t* buf, int qt, int kk) {
+  auto b_frag = [&](const uint8_t* buf, int qt) {
     const int t = wq * 16 * QT + qt * 16 + frow;
-    const int c = kk * 4 + (lane >> 4);
-    return *reinterpret_cast<const frag_t*>(buf + (kTileRows + t) * kStageB + ((c ^ (t & 7)) << 4));
+    return *reinterpret_cast<const frag_t*>(buf + (kTileRows + t) * kStageB + ((fch ^ ((t >> 1) & 3)) << 4));
   };
 
-  // one stage: the fragments of the first MFMA half are read up front; between the row tiles of
-  // the first half come the reads of the second half's fragments and (COPY) the copies of stage
-  // s + 1, so that their issue and latency hide behind MFMAs. The schedule is pinned with
-  // sched_group_barrier (DS read 0x100, VMEM read 0x020, MFMA 0x008).
-  auto stage = [&](int s, auto copy_next) {
-    constexpr bool COPY = decltype(copy_next)::value;
-    wait_copies();
+  acc_t acc[RT][QT];
+
+  // one stage: wait for this wave's copies of stage s (with COPY, those of stage s + 1 stay in
+  // flight), publish the stage, read its fragments and run its MFMAs; with COPY the copies of stage
+  // s + 2 go between the row tiles, pinned with sched_group_barrier (DS read 0x100, VMEM read
+  // 0x020, MFMA 0x008), so that their issue hides behind MFMAs
+  auto stage = [&](int s, auto more, auto copy_next) {
+    constexpr bool MORE = decltype(more)::value;       // stage s + 1 is in flight
+    constexpr bool COPY = decltype(copy_next)::value;  // issue stage s + 2
+    if constexpr (MORE) {
+      wait_copies<NC>();
+    } else {
+      wait_copies<0>();
+    }
     __syncthreads();
-    const uint8_t* buf = lds + (s & 1) * BUF;
-    frag_t ar[2][RT], bq[2][QT];
+    const uint8_t* buf = lds + (s % kBufs) * BUF;
+    frag_t ar[RT], bq[QT];
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) { bq[0][qt] = b_frag(buf, qt, 0); }
+    for (int qt = 0; qt < QT; ++qt) { bq[qt] = b_frag(buf, qt); }
 #pragma unroll
-    for (int bt = 0; bt < RT; ++bt) { ar[0][bt] = a_frag(buf, bt, 0); }
+    for (int bt = 0; bt < RT; ++bt) { ar[bt] = a_frag(buf, bt); }
     __builtin_amdgcn_sched_group_barrier(0x100, QT + RT, 0);
     __builtin_amdgcn_s_setprio(1);
     static_for<RT>([&](auto BT) {
       constexpr int bt = decltype(BT)::value;
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = R::mfma(ar[0][bt], bq[0][qt], acc[bt][qt]); }
+      for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = R::mfma(ar[bt], bq[qt], acc[bt][qt]); }
       __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);
-      constexpr int q0 = bt * QPT;
-      constexpr int q1 = q0 + QPT < QT ? q0 + QPT : QT;
-      ar[1][bt] = a_frag(buf, bt, 1);
-#pragma unroll
-      for (int qt = q0; qt < q1; ++qt) { bq[1][qt] = b_frag(buf, qt, 1); }
-      __builtin_amdgcn_sched_group_barrier(0x100, 1 + (q1 > q0 ? q1 - q0 : 0), 0);
       if constexpr (COPY) {
         constexpr int c0 = bt * CPT;
         constexpr int c1 = c0 + CPT < NC ? c0 + CPT : NC;
         if constexpr (c1 > c0) {
 #pragma unroll
-          for (int j = c0; j < c1; ++j) { copy(s + 1, j); }
+          for (int j = c0; j < c1; ++j) { copy(s + 2, j); }
           __builtin_amdgcn_sched_group_barrier(0x020, c1 - c0, 0);
         }
       }
     });
-#pragma unroll
-    for (int bt = 0; bt < RT; ++bt) {
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = R::mfma(ar[1][bt], bq[1][qt], acc[bt][qt]); }
-    }
     __builtin_amdgcn_s_setprio(0);
   };
 
   issue(0);
-  for (int s = 0; s + 1 < n_stages; ++s) { stage(s, std::true_type{}); }
-  stage(n_stages - 1, std::false_type{});
-  wait_copies();
+  issue(1);
+  // stage 0 also publishes the row terms: the accumulators start at them (dead past the live rows)
+  wait_copies<NC>();
+  __syncthreads();
+#pragma unroll
+  for (int bt = 0; bt < RT; ++bt) {
+    const int r0 = wr * 16 * RT + bt * 16 + (lane >> 4) * 4;
+    acc_t c      = *reinterpret_cast<const acc_t*>(rc_lds + r0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { c[j] = r0 + j < n_rows ? c[j] : R::dead(); }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = c; }
+  }
+  int s = 0;
+  for (; s + 2 < n_stages; ++s) { stage(s, std::true_type{}, std::true_type{}); }
+  stage(s, std::true_type{}, std::false_type{});
+  stage(s + 1, std::false_type{}, std::false_type{});
   __syncthreads();  // the staging LDS becomes the survivor list
 
   uint32_t* hit_q    = reinterpret_cast<uint32_t*>(lds);
@@ -254,13 +270,12 @@ __global__ __launch_bounds__(64 * kTileWaves, 1) void screen_tile_kernel(screen_
   // per wave 8 KB: a lane's 4 RT screen values of one query tile, 16-byte slot bt ^ (lane & 7) of
   // its 128 bytes, so that the survivor loop reads a value by its bit index
   uint8_t* vals      = lds + tile_lds(TQ) - kTileWaves * 8192 + wave * 8192 + lane * 128;
-  const float* theta = static_cast<const float*>(a.theta);
   const int64_t row0 = w.base + scan0 + wr * 16 * RT + (lane >> 4) * 4;  // stored row of bit 0
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int qloc = wq * 16 * QT + qt * 16 + frow;
     // a padding query keeps nothing: no value compares >= NaN
-    const float th = qloc < n_q ? theta[w.q0 + qloc] : R::keep_none();
+    const float th = qloc < n_q ? th_lds[qloc] : R::keep_none();
     uint32_t bits  = 0;  // bit bt * 4 + r: row row0 + 16 bt + r
 #pragma unroll
     for (int bt = 0; bt < RT; ++bt) {
@@ -338,13 +353,14 @@ void launch_shape(const screen_args& a, hipStream_t stream)
     blocks                 = n_steps == 0 ? 0 : 8 * n_qb * ((n_chunks + 7) / 8);
   }
   if (blocks == 0) { return; }
-  if (a.chunk_steps != kTileSteps || a.row_stride != 1 || a.row_bytes % kStageB != 0) {
-    throw std::logic_error("certex: the tiled screen needs chunks of 4 steps over rows of 128-byte multiples");
+  if (a.chunk_steps != kTileSteps || a.row_stride != 1 || a.row_bytes % kStageB != 0 ||
+      a.row_bytes / kStageB < 2) {
+    throw std::logic_error("certex: the tiled screen needs chunks of 4 steps over rows of 64-byte multiples");
   }
   screen_args b = a;
   b.spill_cap   = a.spill_q != nullptr ? a.spill_pool / blocks : 0;
   auto* k       = &screen_tile_kernel<RT, QT, FILT>;
-  const int lds = tile_lds(TQ);
+  const int lds = tile_lds_total(TQ);
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(k),
                           hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) {
     (void)hipGetLastError();

@@ -155,8 +155,8 @@ def test_wide_largest_rows(gpu):
 
 @pytest.mark.parametrize("nq", [512, 448, 700])
 def test_wide_query_tiles(gpu, nq):
-    """Batches of 512, 448 and 700 queries over the tiled screen's 256-query tiles: whole tiles,
-    and last tiles of 192 and 188 live queries."""
+    """Batches of 512, 448 and 700 queries over the tiled screen's 128-query tiles: whole tiles,
+    and last tiles of 64 and 60 live queries."""
     X, Q = correlated(20_000, 256, nq, seed=nq)
     D, I, _ = run(X, Q, 10)
     check(X, Q, 10, "l2", D, I)
