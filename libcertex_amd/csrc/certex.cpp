@@ -373,6 +373,7 @@ void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan 
   certex_amd::screen_args r = aa;
   r.codes                   = st.label_part.codes.as<int8_t>();
   r.rowc                    = st.label_part.rowc.p;
+  r.rows_paired             = st.label_part.paired;
   r.groups                  = route->anchor_groups;
   r.n_route                 = route->n_route;
   r.n_tiles                 = route->anchor_tiles;
@@ -409,6 +410,7 @@ auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
     certex_amd::screen_args r = sa;
     r.codes                   = st.label_part.codes.as<int8_t>();
     r.rowc                    = st.label_part.rowc.p;
+    r.rows_paired             = st.label_part.paired;
     r.groups                  = route->screen_groups;
     r.n_route                 = route->n_route;
     r.n_tiles                 = route->screen_tiles;
@@ -851,8 +853,14 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   auto* qrows =
     static_cast<uint16_t*>(rs.get(cuvs::detail::ws_qcodes, size_t(nq_pad) * st.row_bytes));
   auto* qscal = static_cast<double*>(rs.get(cuvs::detail::ws_qscal, size_t(nq_pad) * 3 * 8));
+  // the tiled screen reads the queries in the paired layout (a second copy, written by the same
+  // kernel; nq_pad is even)
+  auto* qpaired = wide ? static_cast<uint16_t*>(rs.get(cuvs::detail::ws_qpaired,
+                                                       size_t(nq_pad) * st.row_bytes))
+                       : nullptr;
   certex_amd::encode_queries_f16(queries, t, B, nq_pad, st.dim, st.halves, st.normalize,
-                                 st.center.as<double>(), 1.0 / st.alpha, qrows, qscal, stream);
+                                 st.center.as<double>(), 1.0 / st.alpha, qrows, qscal, stream,
+                                 qpaired);
 
   const table_plan tp = plan_table(res, st, qrows, B, nq_pad, k, params, fa, route);
   certex_amd::screen_args sa{};
@@ -860,6 +868,7 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   sa.rowc      = st.rowc.p;
   sa.row_bytes = st.row_bytes;
   sa.qcodes    = reinterpret_cast<const int8_t*>(qrows);
+  sa.qpaired   = reinterpret_cast<const int8_t*>(qpaired);
   sa.nq        = B;
   sa.nq_pad    = nq_pad;
   sa.filter    = fa;
@@ -1041,9 +1050,16 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
     route.anchor_tiles = e.tile0 + certex_amd::screen_group_tiles(
                                      e.nq, (e.nx + stride - 1) / stride, qb, route.anchor_chunk);
   }
+  // the tiled screen aligns a group's query blocks (and, over paired rows, its tiles) to pairs
   for (auto& e : gs) {
-    e.tile0            = certex_amd::screen_group_tile0(route.screen_tiles, e.nq, qbs);
-    route.screen_tiles = e.tile0 + certex_amd::screen_group_tiles(e.nq, e.nx, qbs, route.screen_chunk);
+    if (tiled) {
+      e.tile0            = certex_amd::screen_group_tile0(route.screen_tiles, e.nq + (e.q0 & 1), qbs);
+      route.screen_tiles = e.tile0 + certex_amd::paired_group_tiles(e, st.label_part.paired, qbs,
+                                                                    route.screen_chunk);
+    } else {
+      e.tile0            = certex_amd::screen_group_tile0(route.screen_tiles, e.nq, qbs);
+      route.screen_tiles = e.tile0 + certex_amd::screen_group_tiles(e.nq, e.nx, qbs, route.screen_chunk);
+    }
   }
   route.n_route = int(gs.size());
 
@@ -1644,8 +1660,13 @@ void partition_by_labels(cuvs::resources const& res, index<T>* idx)
   expects(n < (int64_t(1) << 31), "certex: at most 2^31 - 1 vectors per partition");
   hipStream_t stream = static_cast<hipStream_t>(res.stream());
   using cuvs::detail::device_buffer;
+  // fp16 rows of more than 128 halves: the copy is paired, so that the tiled screen copies whole
+  // 128-byte lines per stage
+  const bool paired = uses_tile_screen(st);
   device_buffer keys(size_t(n) * 4), ids_tmp(size_t(n) * 4), ids(size_t(n) * 4),
-    pos(size_t(n) * 4), codes(size_t(n) * st.row_bytes), rowc(size_t(n) * 4);
+    pos(size_t(n) * 4),
+    codes(size_t(paired ? certex_amd::paired_bytes(n, st.row_bytes) : n * int64_t(st.row_bytes))),
+    rowc(size_t(n) * 4);
   std::vector<int64_t> offsets;
   if (n > 0) {
     const size_t tb = certex_amd::sort_by_label_temp_bytes(n);
@@ -1670,7 +1691,11 @@ void partition_by_labels(cuvs::resources const& res, index<T>* idx)
                               ids_tmp.as<int32_t>(), stream);
       from = ids_tmp.as<int32_t>();
     }
-    certex_amd::gather_rows(st.codes.p, from, n, st.row_bytes, codes.p, stream);
+    if (paired) {
+      certex_amd::gather_rows_paired(st.codes.p, from, n, st.row_bytes, codes.p, stream);
+    } else {
+      certex_amd::gather_rows(st.codes.p, from, n, st.row_bytes, codes.p, stream);
+    }
     certex_amd::gather_rows(st.rowc.p, from, n, 4, rowc.p, stream);
     certex_amd::invert_ids(ids.as<int32_t>(), n, pos.as<int32_t>(), stream);
     CERTEX_HIP_TRY(hipStreamSynchronize(stream));
@@ -1682,6 +1707,7 @@ void partition_by_labels(cuvs::resources const& res, index<T>* idx)
   st.label_part.ids     = std::move(ids);
   st.label_part.pos     = std::move(pos);
   st.label_part.offsets = std::move(offsets);
+  st.label_part.paired  = paired;
   st.label_part.n       = n;
 }
 

@@ -113,6 +113,7 @@ enum ws_slot : int {
   ws_spill_q,     // screen spill pool: query of each entry
   ws_spill_row,   // screen spill pool: row of each entry
   ws_spill_val,   // screen spill pool: screen value of each entry (fp16 rows)
+  ws_qpaired,     // the batch's fp16 query rows in the paired layout (the tiled screen)
   ws_n_slots
 };
 
@@ -215,7 +216,8 @@ constexpr vtype vtype_of<uint8_t>() { return vtype::u8; }
  * [offsets[j], offsets[j + 1]).
  */
 struct row_partition {
-  int64_t n = 0;
+  int64_t n   = 0;
+  bool paired = false;  // codes in the paired layout (fp16 rows of more than 128 halves)
   cuvs::detail::device_buffer codes;
   cuvs::detail::device_buffer rowc;
   cuvs::detail::device_buffer ids;

@@ -43,6 +43,19 @@ __host__ __device__ inline int screen_block_queries(int64_t nq_pad) { return nq_
 
 enum class metric_kind : int { l2 = 0, inner = 1, cosine = 2 };
 
+/**
+ * Paired row layout of fp16 rows (row_bytes a multiple of 128): rows 2p and 2p + 1 share 2
+ * row_bytes bytes, and their 64-byte pieces c alternate, so that one 128-byte line holds piece c
+ * of both rows: byte b of row r sits at (r / 2) 2 row_bytes + (b / 64) 128 + (r % 2) 64 + b % 64.
+ * The tiled screen copies a stage (one 64-byte piece of every row of a tile) as whole lines.
+ */
+__host__ __device__ inline int64_t paired_offset(int64_t r, int64_t b, int64_t row_bytes)
+{
+  return (r >> 1) * 2 * row_bytes + (b >> 6) * 128 + (r & 1) * 64 + (b & 63);
+}
+/** Bytes of n rows in the paired layout (a whole number of pairs). */
+__host__ __device__ inline int64_t paired_bytes(int64_t n, int64_t row_bytes) { return (n + 1) / 2 * 2 * row_bytes; }
+
 /** Bytes of a stored integer screening row of `dim` coordinates: 128 or 256 (zero padded). */
 __host__ __device__ inline int int_row_bytes(int64_t dim) { return dim <= 128 ? 128 : 256; }
 
@@ -141,6 +154,10 @@ struct screen_args {
   const void* theta;     // [nq_pad] int32 or float (screen only)
   int64_t nq;            // live queries
   int64_t nq_pad;        // pad_queries(nq)
+  // the queries again in the paired layout (fp16 rows read by the tiled screen), and whether the
+  // stored rows are paired (the label partition of fp16 rows of more than 128 halves)
+  const int8_t* qpaired = nullptr;
+  bool rows_paired      = false;
   int chunk_steps;       // steps of kStepRows rows per workgroup: 4 waves x a whole number of
                          // anchor groups
   filter_args filter;
@@ -194,6 +211,14 @@ inline int64_t screen_group_tiles(int64_t nq, int64_t n_scan, int qb, int chunk_
   const int64_t n_chunks = (steps + chunk_steps - 1) / chunk_steps;
   const int64_t n_qb     = (nq + qb - 1) / qb;
   return n_qb > 1 ? 8 * n_qb * ((n_chunks + 7) / 8) : n_chunks;
+}
+/**
+ * The same for the tiled screen over paired queries (and rows, rows_paired): a group whose first
+ * query (row) is odd starts one slot earlier, at the pair's first query (row).
+ */
+inline int64_t paired_group_tiles(const screen_group& g, bool rows_paired, int qb, int chunk_steps)
+{
+  return screen_group_tiles(g.nq + (g.q0 & 1), g.nx + (rows_paired ? (g.x0 & 1) : 0), qb, chunk_steps);
 }
 /**
  * First workgroup of a routed group that follows `tiles` workgroups: a multiple of 8 for a group
@@ -323,7 +348,8 @@ void encode_rows_f16(const void* x, elem t, int64_t n, int64_t dim, int halves, 
  */
 void encode_queries_f16(const void* q, elem t, int64_t nq, int64_t nq_pad, int64_t dim,
                         int halves, bool normalize, const double* center, double inv_alpha,
-                        uint16_t* qrows, double* qscal, hipStream_t stream);
+                        uint16_t* qrows, double* qscal, hipStream_t stream,
+                        uint16_t* qpaired = nullptr);
 
 /** Float tombstones (row term -inf) of ids, as remove_rows_i8. */
 void remove_rows_f16(const int64_t* ids, int64_t n, int64_t size, float* rowc,
@@ -399,6 +425,9 @@ void label_offsets(const int32_t* keys_sorted, int64_t n, int64_t n_labels, int6
 /** dst row i = src row ids[i] (rows of row_bytes bytes). */
 void gather_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes, void* dst,
                  hipStream_t stream);
+/** The same into the paired layout of dst (row_bytes a multiple of 128, paired_bytes(n) bytes). */
+void gather_rows_paired(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes,
+                        void* dst, hipStream_t stream);
 /** dst row ids[i] = src row i. */
 void scatter_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes, void* dst,
                   hipStream_t stream);

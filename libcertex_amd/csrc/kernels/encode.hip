@@ -234,14 +234,21 @@ __global__ __launch_bounds__(256) void encode_queries_f16_kernel(const void* q, 
                                                                  int halves, bool normalize,
                                                                  const double* center,
                                                                  double inv_alpha, uint16_t* qrows,
-                                                                 double* qscal)
+                                                                 double* qscal, uint16_t* qpaired)
 {
   const int64_t i = blockIdx.x * int64_t(blockDim.x / 64) + (threadIdx.x >> 6);
   const int lane  = threadIdx.x & 63;
   if (i >= nq_pad) { return; }  // uniform over the wave
   _Float16* dst = reinterpret_cast<_Float16*>(qrows + i * halves);
+  // half j of the query, and of its paired copy when there is one
+  auto put = [&](int64_t j, _Float16 h) {
+    dst[j] = h;
+    if (qpaired != nullptr) {
+      reinterpret_cast<_Float16*>(qpaired)[paired_offset(i, 2 * j, 2 * int64_t(halves)) / 2] = h;
+    }
+  };
   if (i >= nq) {
-    for (int j = lane; j < halves; j += 64) { dst[j] = _Float16(0.0f); }
+    for (int j = lane; j < halves; j += 64) { put(j, _Float16(0.0f)); }
     if (lane == 0) { qscal[3 * i] = qscal[3 * i + 1] = qscal[3 * i + 2] = 0.0; }
     return;
   }
@@ -260,12 +267,12 @@ __global__ __launch_bounds__(256) void encode_queries_f16_kernel(const void* q, 
     const double w   = (coord(q, t, i * dim + j) / nrm - center[j]) * inv_alpha;
     const _Float16 h = to_f16(w);
     const double e   = w - double(h);
-    dst[j]           = h;
+    put(j, h);
     a                = fma(w, w, a);
     nw               = fma(double(h), double(h), nw);
     ew               = fma(e, e, ew);
   }
-  for (int64_t j = dim + lane; j < halves; j += 64) { dst[j] = _Float16(0.0f); }
+  for (int64_t j = dim + lane; j < halves; j += 64) { put(j, _Float16(0.0f)); }
   a  = wave_sum(a);
   nw = wave_sum(nw);
   ew = wave_sum(ew);
@@ -321,12 +328,12 @@ void encode_rows_f16(const void* x, elem t, int64_t n, int64_t dim, int halves, 
 
 void encode_queries_f16(const void* q, elem t, int64_t nq, int64_t nq_pad, int64_t dim,
                         int halves, bool normalize, const double* center, double inv_alpha,
-                        uint16_t* qrows, double* qscal, hipStream_t stream)
+                        uint16_t* qrows, double* qscal, hipStream_t stream, uint16_t* qpaired)
 {
   if (nq_pad == 0) { return; }
   // one wave per query, four per block
   encode_queries_f16_kernel<<<unsigned((nq_pad + 3) / 4), 256, 0, stream>>>(
-    q, t, nq, nq_pad, dim, halves, normalize, center, inv_alpha, qrows, qscal);
+    q, t, nq, nq_pad, dim, halves, normalize, center, inv_alpha, qrows, qscal, qpaired);
 }
 
 void remove_rows_f16(const int64_t* ids, int64_t n, int64_t size, float* rowc,

@@ -9,6 +9,7 @@
 #include "../kernels.hpp"
 
 #include <hipcub/hipcub.hpp>
+#include <stdexcept>
 
 namespace certex_amd {
 namespace {
@@ -54,6 +55,19 @@ __global__ void gather_units_kernel(const int4* src, const int32_t* ids, int64_t
        t += int64_t(gridDim.x) * blockDim.x) {
     const int64_t i = t / units, u = t % units;
     dst[t]          = src[int64_t(ids[i]) * units + u];
+  }
+}
+
+/** dst row i = src row ids[i] in the paired layout: 16-byte unit u of row i at unit
+ *  (i / 2) 2 units + (u / 4) 8 + (i % 2) 4 + u % 4 (units = row bytes / 16, a multiple of 8). */
+__global__ void gather_paired_kernel(const int4* src, const int32_t* ids, int64_t n, int64_t units,
+                                     int4* dst)
+{
+  const int64_t total = n * units;
+  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < total;
+       t += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t i = t / units, u = t % units;
+    dst[(i >> 1) * 2 * units + (u >> 2) * 8 + (i & 1) * 4 + (u & 3)] = src[int64_t(ids[i]) * units + u];
   }
 }
 
@@ -187,6 +201,15 @@ void gather_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_byt
     gather_bytes_kernel<<<blocks_for(n * row_bytes), 256, 0, stream>>>(
       static_cast<const uint8_t*>(src), ids, n, row_bytes, static_cast<uint8_t*>(dst));
   }
+}
+
+void gather_rows_paired(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes,
+                        void* dst, hipStream_t stream)
+{
+  if (n == 0) { return; }
+  if (row_bytes % 128 != 0) { throw std::logic_error("certex: paired rows are whole 128-byte lines"); }
+  gather_paired_kernel<<<blocks_for(n * (row_bytes / 16)), 256, 0, stream>>>(
+    static_cast<const int4*>(src), ids, n, row_bytes / 16, static_cast<int4*>(dst));
 }
 
 void scatter_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes, void* dst,

@@ -53,11 +53,13 @@ struct f16_rows {
 
 /** The share of one workgroup of a screen launch. */
 struct screen_work {
-  int64_t q0;      // first query of the block
-  int64_t q_end;   // queries [q0, q_end) are live (others in the block are padding)
-  int64_t chunk;   // row chunk: scan steps [chunk * chunk_steps, (chunk + 1) * chunk_steps)
-  int64_t n_scan;  // scan indices of the pass
-  int64_t base;    // stored row of scan index i: base + i * row_stride
+  int64_t q0;       // first query of the block
+  int64_t q_end;    // queries [q_first, q_end) are live (others in the block are padding)
+  int64_t q_first;  // first live query of the group (q0 or later)
+  int64_t chunk;    // row chunk: scan steps [chunk * chunk_steps, (chunk + 1) * chunk_steps)
+  int64_t n_scan;   // scan indices of the pass
+  int64_t base;     // stored row of scan index i: base + i * row_stride
+  int rlead;        // scan indices below rlead are not live (pair alignment)
   bool valid;
 };
 
@@ -75,11 +77,17 @@ __device__ inline int64_t div_small(int64_t x, int64_t d)
  * search over them), then query block and chunk within it, in the same XCD order when the group
  * has several query blocks (its tile0 is then a multiple of 8, screen_group_tile0). Blocks past a
  * group's chunks (octet padding, alignment gaps) are invalid. Every lane of the block calls it.
+ * PAIRS (the tiled screen over paired queries and, with rows_paired, paired rows): a routed
+ * group's query blocks start at an even query and its tiles at an even row, one slot before the
+ * group when its first query or row is odd (that slot is not live); screen_group_tiles counts
+ * such a group with nq + (q0 & 1) queries and nx + (x0 & 1) rows (paired_group_tiles).
  */
-template <int QB>
+template <int QB, bool PAIRS = false>
 __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
 {
   screen_work w;
+  w.q_first = 0;
+  w.rlead   = 0;
   if (a.groups == nullptr) {
     const int64_t n_steps  = screen_steps(a.n_scan);
     const int64_t n_chunks = (n_steps + a.chunk_steps - 1) / a.chunk_steps;
@@ -113,13 +121,18 @@ __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
   }
   const screen_group g = a.groups[lo];
   const int64_t t      = int64_t(b) - g.tile0;
-  const uint32_t n_qb  = uint32_t(div_small(g.nq + QB - 1, QB));
+  const int qlead      = PAIRS ? int(g.q0 & 1) : 0;
+  const int rlead      = PAIRS && a.rows_paired ? int(g.x0 & 1) : 0;
+  const uint32_t n_qb  = uint32_t(div_small(g.nq + qlead + QB - 1, QB));
   const uint32_t i     = uint32_t(t) >> 3;
-  w.q0                 = g.q0 + int64_t(n_qb > 1 ? i % n_qb : 0) * QB;
+  w.q0                 = g.q0 - qlead + int64_t(n_qb > 1 ? i % n_qb : 0) * QB;
   w.q_end              = g.q0 + g.nq;
+  w.q_first            = g.q0;
   w.chunk              = n_qb > 1 ? int64_t(i / n_qb) * 8 + (t & 7) : t;
-  w.n_scan             = a.row_stride == 1 ? g.nx : div_small(g.nx + a.row_stride - 1, a.row_stride);
-  w.base               = g.x0;
+  w.n_scan             = a.row_stride == 1 ? g.nx + rlead
+                                           : div_small(g.nx + a.row_stride - 1, a.row_stride);
+  w.base               = g.x0 - rlead;
+  w.rlead              = rlead;
   const int64_t steps  = screen_steps(w.n_scan);
   w.valid              = t >= 0 && w.chunk < div_small(steps + a.chunk_steps - 1, a.chunk_steps);
   return w;

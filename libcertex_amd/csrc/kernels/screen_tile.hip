@@ -18,6 +18,11 @@
 //   that half, so lane i reads chunk (i & 3) ^ ((i >> 3) & 3) of its row. The ds_read_b128 of a
 //   16-row MFMA fragment (lanes on 16 rows, one chunk) then serves 8 lanes per pass from 8
 //   distinct 16-byte slots of a 128-byte line: no bank conflicts;
+// - the queries, and the rows of a routed pass (the label partition), are stored in the paired
+//   layout (paired_offset): piece s of rows 2p and 2p + 1 share one 128-byte line, so a copy asks
+//   for 8 whole lines. The memory pipeline serves whole lines about twice as fast as half lines
+//   (measured: 33 against 15 TB/s of LDS-DMA from L2). A tile starts at an even row and query;
+//   a group whose first row (query) is odd starts one slot early, and that slot is not live;
 // - three stage buffers: the copies of stage s + 2 fly while the MFMAs run on stage s; at the top
 //   of stage s a wave waits for its own copies of stage s only (those of s + 1 stay in flight),
 //   then one barrier publishes stage s and frees the buffer of stage s - 1;
@@ -63,6 +68,29 @@ __device__ __forceinline__ void wait_copies()
 {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
+
+/** LDS-DMA copy of 16 (B = 16) or 4 (B = 4) bytes per lane from g to LDS byte m0 + B * lane, issued
+ *  as inline assembly: the compiler then neither counts it among the loads it waits for nor orders
+ *  LDS reads against it (it models such copies as LDS stores of unknown address and would wait for
+ *  every LDS read before each copy). The kernel orders the copies itself: a stage's copies target
+ *  a buffer that no wave reads, and s_waitcnt vmcnt plus a barrier publish them. An LDS-DMA
+ *  instruction needs one wait state after the write of M0. */
+template <int B>
+__device__ __forceinline__ void lds_copy(const void* g, uint32_t m0)
+{
+  if constexpr (B == 16) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "m0");
+  } else {
+    static_assert(B == 4, "4 or 16 bytes per lane");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m0) : "m0");
+  }
+}
+
+/** The LDS byte address of p (a pointer into the workgroup's LDS). */
+__device__ __forceinline__ uint32_t lds_addr(const void* p)
+{
+  return uint32_t(reinterpret_cast<uintptr_t>((lptr)(const_cast<void*>(p))));
 }
 
 /** Staging LDS of a workgroup of TQ queries: three stage buffers of (256 + TQ) rows x 64 bytes. */
@@ -124,65 +152,72 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
   const int wr   = wave / S::WQ;  // row part of the tile
   const int wq   = wave % S::WQ;  // query part of the tile
 
-  const screen_work w = work_of<TQ>(a, blockIdx.x);
+  const screen_work w = work_of<TQ, true>(a, blockIdx.x);
   if (!w.valid) { return; }
-  const int RB          = a.row_bytes;  // bytes per row: a multiple of 64
+  const int RB          = a.row_bytes;  // bytes per row: a multiple of 128
   const int n_stages    = RB / kStageB;
-  const int64_t scan0   = w.chunk * kTileRows;  // scan index of tile row 0
+  const int64_t scan0   = w.chunk * kTileRows;  // scan index of tile row 0 (an even stored row
+                                                // with paired rows, as the first query is even)
+  // live tile rows [r_lo, n_rows) and tile queries [q_lo, n_q): a group whose first row (query)
+  // is odd starts its tiles one paired row (query) early
   const int64_t n_rows  = w.n_scan - scan0 < kTileRows ? w.n_scan - scan0 : kTileRows;
+  const int r_lo        = scan0 == 0 ? w.rlead : 0;
   const int64_t n_q     = w.q_end - w.q0 < TQ ? w.q_end - w.q0 : TQ;
+  const int q_lo        = w.q_first > w.q0 ? int(w.q_first - w.q0) : 0;
 
   if (tid == 0) { n_hits = 0; }
 
   // the query thresholds and the row terms into LDS past the staging (waited for with stage 0);
-  // indices past the live queries and rows repeat the last live one
+  // indices past the live queries and rows repeat the last live one (the slot before a group's
+  // first live one reads its neighbour, in the same allocation)
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   float* th_lds    = reinterpret_cast<float*>(lds + tile_lds(TQ));
   float* rc_lds    = th_lds + TQ;
   {
     const int64_t r = wave_u * 64 + lane;
-    __builtin_amdgcn_global_load_lds(
-      (gptr)(static_cast<const float*>(a.rowc) + w.base + scan0 + (r < n_rows ? r : n_rows - 1)),
-      (lptr)(rc_lds + wave_u * 64), 4, 0, 0);
+    lds_copy<4>(static_cast<const float*>(a.rowc) + w.base + scan0 + (r < n_rows ? r : n_rows - 1),
+                lds_addr(rc_lds + wave_u * 64));
     if (wave_u * 64 < TQ) {
       const int64_t q = wave_u * 64 + lane;
-      __builtin_amdgcn_global_load_lds(
-        (gptr)(static_cast<const float*>(a.theta) + w.q0 + (q < n_q ? q : n_q - 1)),
-        (lptr)(th_lds + wave_u * 64), 4, 0, 0);
+      lds_copy<4>(static_cast<const float*>(a.theta) + w.q0 + (q < n_q ? q : n_q - 1),
+                  lds_addr(th_lds + wave_u * 64));
     }
   }
 
   // this lane's copy offsets: rows of copies j < CA (tile rows (CA wave + j) * 16 + lane / 4), and
   // queries of copies j < CB (tile queries (CB wave + j) * 16 + lane / 4); rows and queries past
-  // the tile's live ones repeat its last live one (their results are never kept)
-  const int crow   = lane >> 2;
-  const int cchunk = (lane & 3) ^ ((lane >> 3) & 3);
+  // the tile's live ones repeat its last live one (their results are never kept). The queries are
+  // paired, and so are the rows with rows_paired: the 8 lanes of a row pair then read one whole
+  // 128-byte line per copy, and a stage advances 128 bytes (64 unpaired). A paired tile starts at
+  // an even row and query, where the pair starts.
+  const bool rp     = a.rows_paired;
+  const int rstep   = rp ? 128 : kStageB;
+  const int crow    = lane >> 2;
+  const int cchunk  = (lane & 3) ^ ((lane >> 3) & 3);
   const char* rbase = reinterpret_cast<const char*>(a.codes) + (w.base + scan0) * int64_t(RB) + cchunk * 16;
-  const char* qbase = reinterpret_cast<const char*>(a.qcodes) + w.q0 * int64_t(RB) + cchunk * 16;
+  const char* qbase = reinterpret_cast<const char*>(a.qpaired) + w.q0 * int64_t(RB) + cchunk * 16;
   uint32_t roff[CA], qoff[CB];
 #pragma unroll
   for (int j = 0; j < CA; ++j) {
     int64_t r = (wave * CA + j) * 16 + crow;
     r         = r < n_rows ? r : n_rows - 1;
-    roff[j]   = uint32_t(r * RB);
+    roff[j]   = uint32_t(rp ? (r & ~int64_t(1)) * RB + (r & 1) * 64 : r * RB);
   }
 #pragma unroll
   for (int j = 0; j < CB; ++j) {
     int64_t q = (wave * CB + j) * 16 + crow;
     q         = q < n_q ? q : n_q - 1;
-    qoff[j]   = uint32_t(q * RB);
+    qoff[j]   = uint32_t((q & ~int64_t(1)) * RB + (q & 1) * 64);
   }
   // copy j (0 .. NC - 1) of stage s: rows for j < CA, queries after; the LDS destination is
   // wave-uniform (scalar: M0)
   auto copy = [&](int s, int j) {
     uint8_t* buf = lds + (s % kBufs) * BUF;
     if (j < CA) {
-      __builtin_amdgcn_global_load_lds((gptr)(rbase + s * kStageB + roff[j]),
-                                       (lptr)(buf + ((wave_u * CA + j) * 16) * kStageB), 16, 0, 0);
+      lds_copy<16>(rbase + s * rstep + roff[j], lds_addr(buf + ((wave_u * CA + j) * 16) * kStageB));
     } else {
-      __builtin_amdgcn_global_load_lds(
-        (gptr)(qbase + s * kStageB + qoff[j - CA]),
-        (lptr)(buf + (kTileRows + (wave_u * CB + j - CA) * 16) * kStageB), 16, 0, 0);
+      lds_copy<16>(qbase + s * 128 + qoff[j - CA],
+                   lds_addr(buf + (kTileRows + (wave_u * CB + j - CA) * 16) * kStageB));
     }
   };
   auto issue = [&](int s) {
@@ -253,7 +288,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
     const int r0 = wr * 16 * RT + bt * 16 + (lane >> 4) * 4;
     acc_t c      = *reinterpret_cast<const acc_t*>(rc_lds + r0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) { c[j] = r0 + j < n_rows ? c[j] : R::dead(); }
+    for (int j = 0; j < 4; ++j) { c[j] = r0 + j >= r_lo && r0 + j < n_rows ? c[j] : R::dead(); }
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) { acc[bt][qt] = c; }
   }
@@ -275,7 +310,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
   for (int qt = 0; qt < QT; ++qt) {
     const int qloc = wq * 16 * QT + qt * 16 + frow;
     // a padding query keeps nothing: no value compares >= NaN
-    const float th = qloc < n_q ? th_lds[qloc] : R::keep_none();
+    const float th = qloc >= q_lo && qloc < n_q ? th_lds[qloc] : R::keep_none();
     uint32_t bits  = 0;  // bit bt * 4 + r: row row0 + 16 bt + r
 #pragma unroll
     for (int bt = 0; bt < RT; ++bt) {
@@ -353,9 +388,11 @@ void launch_shape(const screen_args& a, hipStream_t stream)
     blocks                 = n_steps == 0 ? 0 : 8 * n_qb * ((n_chunks + 7) / 8);
   }
   if (blocks == 0) { return; }
-  if (a.chunk_steps != kTileSteps || a.row_stride != 1 || a.row_bytes % kStageB != 0 ||
-      a.row_bytes / kStageB < 2) {
-    throw std::logic_error("certex: the tiled screen needs chunks of 4 steps over rows of 64-byte multiples");
+  if (a.chunk_steps != kTileSteps || a.row_stride != 1 || a.row_bytes % 128 != 0 ||
+      a.qpaired == nullptr || (a.rows_paired && a.groups == nullptr)) {
+    throw std::logic_error(
+      "certex: the tiled screen needs chunks of 4 steps over rows of 128-byte multiples, paired "
+      "queries, and paired rows only in routed passes");
   }
   screen_args b = a;
   b.spill_cap   = a.spill_q != nullptr ? a.spill_pool / blocks : 0;

@@ -86,17 +86,25 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
   // and a lane keeps 4 offsets per step instead of 4 pointers (64-bit pointers for this and the
   // next step pushed the kernel past 256 VGPRs). Every load of the main loop is unconditional,
   // so that the compiler's wait counts see one straight path and the prefetches stay in flight.
+  // Paired rows (rows_paired): byte b of stored row R at paired_offset(R, b); a 64-half chunk of a
+  // row is then two 64-byte pieces 128 bytes apart, lanes 0-1 of a quad on the first and 2-3 on
+  // the second, and chunk c starts 256 c bytes into the pair.
   const gbytes codes     = (gbytes)a.codes;
-  const int64_t row_step = int64_t(a.row_stride) * RB;  // bytes between consecutive scan rows
+  const bool rp          = a.rows_paired;
+  const int64_t cstep    = rp ? 256 : 128;  // bytes between consecutive 64-half chunks of a row
+  auto row_at = [&](int64_t R) { return rp ? (R & ~int64_t(1)) * RB + (R & 1) * 64 : R * RB; };
   auto step_base = [&](int64_t s) {
-    return codes + (w.base + s * kStepRows * a.row_stride) * RB;
+    return codes + row_at((w.base + s * kStepRows * a.row_stride) & ~int64_t(rp ? 1 : 0));
   };
   auto offsets   = [&](int64_t s, uint32_t (&O)[4]) {
+    const int64_t R0 = (w.base + s * kStepRows * a.row_stride) & ~int64_t(rp ? 1 : 0);
+    const int q      = lane & 3;
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
       int64_t r = s * kStepRows + bt * 16 + (lane >> 2);
       r         = r < w.n_scan ? r : w.n_scan - 1;
-      O[bt]     = uint32_t((r - s * kStepRows) * row_step + (lane & 3) * 32);
+      O[bt]     = uint32_t(row_at(w.base + r * a.row_stride) - row_at(R0) +
+                           (rp ? (q >> 1) * 128 + (q & 1) * 32 : q * 32));
     }
   };
   auto load_chunk = [&](gbytes base, const uint32_t (&O)[4], int64_t off,
@@ -170,9 +178,9 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
     }
 #pragma unroll 1
     for (int c = 0; c < NC - 2; c += 2) {
-      load_chunk(B, O, int64_t(c + 1) * 128, av[1]);
+      load_chunk(B, O, int64_t(c + 1) * cstep, av[1]);
       compute(c, av[0]);
-      load_chunk(B, O, int64_t(c + 2) * 128, av[0]);
+      load_chunk(B, O, int64_t(c + 2) * cstep, av[0]);
       compute(c + 1, av[1]);
     }
     // the last two chunks; the next step's terms and first chunk are loaded meanwhile (the last
@@ -182,7 +190,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
     uint32_t ON[4];
     offsets(sn, ON);
     load_terms(sn);
-    load_chunk(B, O, int64_t(NC - 1) * 128, av[1]);
+    load_chunk(B, O, int64_t(NC - 1) * cstep, av[1]);
     compute(NC - 2, av[0]);
     load_chunk(BN, ON, 0, av[0]);
     compute(NC - 1, av[1]);
