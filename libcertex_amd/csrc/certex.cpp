@@ -30,6 +30,7 @@ resources::resources(void* stream) : s_(std::make_unique<detail::resources_state
     s_->owns_stream = true;
   }
   CERTEX_HIP_TRY(hipHostMalloc(&s_->host_small, 64, hipHostMallocDefault));
+  CERTEX_HIP_TRY(hipEventCreateWithFlags(&s_->read_back, hipEventDisableTiming));
   if (const char* cap = std::getenv("CERTEX_SCRATCH_SLOT_CAP")) {
     s_->slot_cap = size_t(std::strtoull(cap, nullptr, 10));
   }
@@ -41,6 +42,7 @@ resources::~resources()
     (void)hipStreamSynchronize(s_->stream);
     for (auto& b : s_->slots) { b.release(); }
     if (s_->host_small) { (void)hipHostFree(s_->host_small); }
+    if (s_->read_back) { (void)hipEventDestroy(s_->read_back); }
     if (s_->host_stage) { (void)hipHostFree(s_->host_stage); }
     if (s_->owns_stream) { (void)hipStreamDestroy(s_->stream); }
   }
@@ -428,16 +430,26 @@ auto screen_pass(index_state const& st, route_plan const* route, F&& launch)
   };
 }
 
+/** No work launched behind the screen before its bucket check (see screen_into_buckets). */
+struct no_speculation {
+  void operator()() const {}
+};
+
 /**
  * Screen pass into per-query buckets, re-run with larger buckets while one overflows (the
  * reference re-runs on segment overflow, certex.cu:1208-1269). Returns false when some query
  * keeps so many rows that scoring every row is cheaper (all_rows).
+ * `speculate` launches the work that reads the buckets (the exact re-rank) right behind the
+ * screen, before the host has read back the largest bucket: the host then waits for that read-back
+ * only (an event), not for the re-rank. When the check fails (a re-run, or all_rows) the
+ * speculative work has read clipped buckets, and what the caller launches next overwrites its
+ * results in stream order.
  */
-template <typename F>
+template <typename F, typename V = no_speculation>
 bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, int64_t size,
                          certex_amd::screen_args& sa, F&& screen, uint32_t*& count,
                          uint32_t*& rows, int64_t& cap, float** vals = nullptr,
-                         int64_t* worst_out = nullptr)
+                         int64_t* worst_out = nullptr, V&& speculate = V{})
 {
   auto& rs           = res.state();
   hipStream_t stream = rs.stream;
@@ -477,7 +489,9 @@ bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, 
     timed(2, stream, [&] { screen(sa, stream); });
     certex_amd::max_u32(count, B, small, stream);
     CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, small, 8, hipMemcpyDeviceToHost, stream));
-    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+    CERTEX_HIP_TRY(hipEventRecord(rs.read_back, stream));
+    speculate();
+    CERTEX_HIP_TRY(hipEventSynchronize(rs.read_back));
     const int64_t worst = static_cast<uint32_t*>(rs.host_small)[0];
     if (static_cast<uint32_t*>(rs.host_small)[1] > 0) { rs.spill_pool = true; }
     if (worst_out != nullptr) { *worst_out = worst; }
@@ -903,25 +917,16 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   uint32_t *count = nullptr, *rows = nullptr;
   float* vals = nullptr;
   int64_t cap = 0;
-  if (!all_rows) {
-    sa.theta = theta;
-    all_rows = !screen_into_buckets(
-      res, B, nq_pad, size, sa,
-      screen_pass(st, route, wide ? certex_amd::screen_f16_tile : certex_amd::screen_f16), count,
-      rows, cap, &vals);
-  }
-  count_stats(res, st, B, all_rows, count, cap, true);
-
   auto* best_score =
     static_cast<double*>(rs.get(cuvs::detail::ws_best_score, size_t(B) * k * sizeof(double)));
   auto* best_row =
     static_cast<int64_t*>(rs.get(cuvs::detail::ws_best_row, size_t(B) * k * sizeof(int64_t)));
+  unsigned long long* scored = nullptr;
+  if (t_stats_on) {
+    auto* small = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_small, 64));
+    scored      = reinterpret_cast<unsigned long long*>(small + 8);
+  }
   certex_amd::verify_f_args va{};
-  va.cand_count = count;
-  va.cand_rows  = rows;
-  va.cand_vals  = vals;
-  va.cap        = cap;
-  va.all_rows   = all_rows;
   va.n_rows     = size;
   va.vectors    = st.vectors.p;
   va.qscal      = qscal;
@@ -938,18 +943,32 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   va.k          = k;
   va.best_score = best_score;
   va.best_row   = best_row;
-  unsigned long long* scored = nullptr;
-  if (t_stats_on) {
-    auto* small = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_small, 64));
-    scored      = reinterpret_cast<unsigned long long*>(small + 8);
-    certex_amd::fill_u32(small + 8, 2, 0, stream);
-  }
-  va.scored = scored;
+  va.scored     = scored;
   if (route != nullptr) {
     va.part_ids = st.label_part.ids.as<int32_t>();
     va.n_part   = st.label_part.n;
   }
-  timed(3, stream, [&] { certex_amd::verify_topk_f(va, stream); });
+  // the exact re-rank over the buckets as they are, or over every row (all_rows)
+  auto verify = [&](bool every_row) {
+    va.cand_count = count;
+    va.cand_rows  = rows;
+    va.cand_vals  = vals;
+    va.cap        = cap;
+    va.all_rows   = every_row;
+    if (scored != nullptr) { certex_amd::fill_u32(reinterpret_cast<uint32_t*>(scored), 2, 0, stream); }
+    timed(3, stream, [&] { certex_amd::verify_topk_f(va, stream); });
+  };
+  bool verified = false;
+  if (!all_rows) {
+    sa.theta = theta;
+    all_rows = !screen_into_buckets(
+      res, B, nq_pad, size, sa,
+      screen_pass(st, route, wide ? certex_amd::screen_f16_tile : certex_amd::screen_f16), count,
+      rows, cap, &vals, nullptr, [&] { verify(false); });
+    verified = !all_rows;
+  }
+  if (!verified) { verify(true); }
+  count_stats(res, st, B, all_rows, count, cap, true);
   if (scored != nullptr) {
     CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, scored, 8, hipMemcpyDeviceToHost, stream));
     CERTEX_HIP_TRY(hipStreamSynchronize(stream));
@@ -1093,7 +1112,8 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   batch(res, st, q_sorted, B, k, 0, nb_s, ds_s, fa, params, &route);
   certex_amd::scatter_rows(nb_s, d_order, B, int64_t(k) * 8, neighbors, stream);
   certex_amd::scatter_rows(ds_s, d_order, B, int64_t(k) * 4, distances, stream);
-  CERTEX_HIP_TRY(hipStreamSynchronize(stream));  // the staged tables are reused by the next batch
+  // no wait here: the next routed batch stages its labels and tables only after a read-back on
+  // this stream, which orders them after this batch's copy of the tables
 }
 
 template <typename T>

@@ -127,6 +127,7 @@ struct resources_state {
   bool spill_pool     = false;  // a screen's LDS survivor lists overflowed: provide a spill pool
   device_buffer slots[ws_n_slots];
   void* host_small    = nullptr;  // pinned host words for counters read back by the host
+  hipEvent_t read_back = nullptr;  // recorded behind a read-back into host_small
   void* host_stage    = nullptr;  // pinned host staging of the routing tables (grow-only)
   size_t host_stage_bytes = 0;
   // test hook: a slot request above this many bytes fails as an allocation failure would

@@ -83,6 +83,18 @@ __global__ void gather_bytes_kernel(const uint8_t* src, const int32_t* ids, int6
   }
 }
 
+/** dst row ids[i] = src row i, rows of `units` 16-byte units. */
+__global__ void scatter_units_kernel(const int4* src, const int32_t* ids, int64_t n, int64_t units,
+                                     int4* dst)
+{
+  const int64_t total = n * units;
+  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < total;
+       t += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t i = t / units, u = t % units;
+    dst[int64_t(ids[i]) * units + u] = src[t];
+  }
+}
+
 /** dst row ids[i] = src row i, rows of `bytes` bytes. */
 __global__ void scatter_bytes_kernel(const uint8_t* src, const int32_t* ids, int64_t n,
                                      int64_t bytes, uint8_t* dst)
@@ -216,6 +228,12 @@ void scatter_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_by
                   hipStream_t stream)
 {
   if (n == 0 || row_bytes == 0) { return; }
+  if (row_bytes % 16 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(dst) % 16 == 0) {
+    scatter_units_kernel<<<blocks_for(n * (row_bytes / 16)), 256, 0, stream>>>(
+      static_cast<const int4*>(src), ids, n, row_bytes / 16, static_cast<int4*>(dst));
+    return;
+  }
   scatter_bytes_kernel<<<blocks_for(n * row_bytes), 256, 0, stream>>>(
     static_cast<const uint8_t*>(src), ids, n, row_bytes, static_cast<uint8_t*>(dst));
 }
