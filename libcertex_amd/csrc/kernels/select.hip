@@ -1100,6 +1100,7 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
   // room. A cut back to the k best (which also tightens U) is a select over the whole buffer: it
   // runs once the rows scored past the k best come to k / 8 (U then moves enough to save
   // scores), or when the free room falls below a quarter of the buffer
+  int pending = have;  // entries [pending, have) are appended and not scored yet
   for (int64_t c0 = 0; c0 < n_cand;) {
     const int room  = cap - have;
     const int64_t m = n_cand - c0 < room ? n_cand - c0 : room;
@@ -1132,13 +1133,20 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
     }
     __syncthreads();
     const int added = fill;
-    score(have, have + added);
     have += added;
     c0 += m;
-    __syncthreads();
-    if (have > k && c0 < n_cand && (8 * (have - k) >= k || cap - have < cap / 4)) {
-      keep_best();
-      if (ordered) { U = key_score(kth); }
+    __syncthreads();  // every thread has read fill before the next chunk resets it
+    // a scoring round costs a memory latency even for one row: score once the buffer runs short
+    // of room or the scan ends (U tightens only through scored rows)
+    if (c0 >= n_cand || cap - have < cap / 4) {
+      score(pending, have);
+      pending = have;
+      __syncthreads();
+      if (have > k && c0 < n_cand && (8 * (have - k) >= k || cap - have < cap / 4)) {
+        keep_best();
+        pending = have;
+        if (ordered) { U = key_score(kth); }
+      }
     }
   }
   {  // the final k in (score, row) order: one sort of all entries when they are few (the best
