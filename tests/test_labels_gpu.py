@@ -111,3 +111,25 @@ def test_rare_label_fewer_than_k(gpu):
     D, I = search(idx, Q, 8, lq)
     assert (I[0::2, 3:] == -1).all()
     check(X, Q, 8, "l2", D, I, row_labels=lx, query_labels=lq)
+
+
+@pytest.mark.parametrize("metric", ["l2", "cosine"])
+def test_paired_layout_odd_starts(gpu, metric):
+    """Float rows over 128 halves keep the label partition and the queries in the paired layout,
+    and a routed group whose first row or query is odd starts one slot early (that slot is not
+    live). Label sizes put group starts at odd rows and odd queries, with one-row and one-query
+    groups, groups of several 256-row tiles and of several 128-query tiles, and labels with fewer
+    rows than k; ids and distances must still equal the oracle's."""
+    rng = np.random.default_rng(90)
+    row_counts = {0: 1, 1: 3, 2: 777, 3: 2, 4: 1500, 6: 301, 7: 9}
+    query_counts = {0: 1, 1: 2, 2: 131, 3: 1, 4: 257, 5: 3, 6: 20, 7: 5}
+    lx = rng.permutation(np.concatenate([np.full(c, l, np.int32) for l, c in row_counts.items()]))
+    lq = rng.permutation(np.concatenate([np.full(c, l, np.int32) for l, c in query_counts.items()]))
+    X = data.powerlaw_unit(len(lx), 200, seed=91)
+    Q = data.powerlaw_unit(len(lq), 200, seed=92)
+    idx = certex.Index(200, metric=metric)
+    idx.add(torch.from_numpy(X).cuda(), labels=torch.from_numpy(lx))
+    assert idx.core.n_partitioned == len(lx)
+    for batch in (1024, 100):
+        D, I = search(idx, Q, 10, lq, batch)
+        check(X, Q, 10, metric, D, I, row_labels=lx, query_labels=lq)
