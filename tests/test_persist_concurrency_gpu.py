@@ -48,10 +48,18 @@ def test_load_rejects_foreign_files(gpu, tmp_path):
         certex.Index.load(tmp_path / "junk")
 
 
-def test_concurrent_search_and_add(gpu):
-    X = data.mixture_u8(40_000, seed=5)
-    Q = data.mixture_u8(200, seed=6)
-    idx = certex.Index(128)
+@pytest.mark.parametrize("dtype", [np.uint8, np.float32])
+def test_concurrent_search_and_add(gpu, dtype):
+    """Searches on three streams while a fourth adds rows: every search equals the oracle on one
+    published snapshot. Float rows of 256 coordinates take the tiled screen, and additions raise
+    the index's fp16 maxima (the certificate's operand bounds) while searches read them."""
+    if dtype == np.uint8:
+        X = data.mixture_u8(40_000, seed=5)
+        Q = data.mixture_u8(200, seed=6)
+    else:
+        X = data.powerlaw_unit(40_000, 256, seed=5) * np.linspace(1, 3, 40_000, dtype=np.float32)[:, None]
+        Q = data.powerlaw_unit(200, 256, seed=6)
+    idx = certex.Index(X.shape[1])
     idx.add(X[:20_000])
     sizes = list(range(20_000, 40_001, 2_000))
     refs = [oracle.knn(X[:n], Q, 10, "l2")[1] for n in sizes]
