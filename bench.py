@@ -6,7 +6,10 @@ A step is one search of all 10,000 queries (k = 10) against the 10,000,000-row i
 index built and the queries resident in HBM before the timed region. The data follow config 2:
 1,000 centres uniform in [0, 80]^128, each vector a random centre plus N(0, 20^2) per coordinate,
 rounded half-to-even and clipped to [0, 255]; drawn with torch generators seeded 1 (centres), 2
-(base) and 3 (queries). Prints one JSON line with the roofline of the dominant kernel (the int8
+(base) and 3 (queries). The index stores its rows in the order of 4,096 k-means lists (built
+with the index; --lists 0 keeps id order) and the searches probe none of them (--probe 0): every
+row is screened, and similar consecutive rows switch fewer bits in the MFMA (about 3% faster
+screen, measured). Prints one JSON line with the roofline of the dominant kernel (the int8
 MFMA screen, timed with HIP events inside the library over the timed steps) and the CPU oracle's
 exhaustive fp64 search timed on the first queries against the full base.
 """
@@ -336,6 +339,7 @@ def bench_config5(args):
         return mixture_u8(m, d, 1000, centres, 100 + i if i >= 0 else 99, dev)
 
     n_lists = 4096 if args.lists < 0 else args.lists
+    args.probe = 2 if args.probe < 0 else args.probe
     idx = certex.Index(d, metric="l2", capacity=n + n_new, n_lists=n_lists)
     t_build = time.perf_counter()
     if n_lists > 0:
@@ -448,8 +452,9 @@ def summarize_profiles(dirs, warmup, steps, after=1):
     A kernel launched L = calls // (warmup + steps + after) >= 1 times per search is averaged over
     all its launches and, separately, over the timed ones only: in dispatch order, the steps * L
     launches before the last after * L (the first search may launch a kernel more often, when its
-    survivor buckets grow). Kernels launched fewer times (the build, data generation) show '-'
-    there. Durations in ms, counters per dispatch."""
+    survivor buckets grow). Kernels launched fewer times, and the index build's kernels (every
+    dispatch before the first of a screen kernel), show '-' there. Durations in ms, counters per
+    dispatch."""
     import csv
     import glob
     import re
@@ -492,6 +497,17 @@ def summarize_profiles(dirs, warmup, steps, after=1):
                     continue
                 counters[(short(r["Kernel_Name"]), r["Counter_Name"])].append(
                     (int(r["Dispatch_Id"]), float(r["Counter_Value"])))
+    # the searches start with the first screen launch (the index build's kernels all run before)
+    first = {}
+    for kind in (traces, counters):
+        for key, v in kind.items():
+            name = key if isinstance(key, str) else key[0]
+            if name.startswith("screen_"):
+                first[id(kind)] = min(first.get(id(kind), 1 << 62), min(d for d, _ in v))
+
+    def build_only(kind, v):
+        return id(kind) in first and max(d for d, _ in v) < first[id(kind)]
+
     out = [f"# {searches} searches per run: {warmup} warm-up, {steps} timed, {after} after (stats); "
            "torch's and hipBLASLt's data-generation kernels left out"]
     if traces:
@@ -501,7 +517,7 @@ def summarize_profiles(dirs, warmup, steps, after=1):
         for name, v in rows:
             v.sort()
             t = [x for _, x in v]
-            ta = timed(t)
+            ta = None if build_only(traces, v) else timed(t)
             out.append(f"{name[:64]:<64} {len(t):>5} {sum(t):>10.3f} {sum(t) / len(t):>9.4f} "
                        f"{(f'{ta:.4f}' if ta is not None else '-'):>12} {min(t):>8.4f} {max(t):>8.4f}")
     if counters:
@@ -509,7 +525,7 @@ def summarize_profiles(dirs, warmup, steps, after=1):
         for (name, cn), v in sorted(counters.items()):
             v.sort()
             t = [x for _, x in v]
-            ta = timed(t)
+            ta = None if build_only(counters, v) else timed(t)
             out.append(f"{name[:64]:<64} {cn:<28} {len(t):>5} {sum(t) / len(t):>16.1f} "
                        f"{(f'{ta:.1f}' if ta is not None else '-'):>16}")
     return "\n".join(out)
@@ -531,7 +547,8 @@ def main():
     ap.add_argument("--cpu-queries", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--lists", type=int, default=-1, help="k-means lists (default: the config's; 0: none)")
-    ap.add_argument("--probe", type=int, default=2, help="lists probed per query")
+    ap.add_argument("--probe", type=int, default=-1,
+                    help="lists probed per query (default: the config's, 0 for config 2, 2 for config 5)")
     ap.add_argument("--summarize", nargs="+", metavar="DIR",
                     help="print a summary of the rocprofv3 CSV output under DIR (of a run with the "
                     "same --warmup and --steps) and exit; needs no GPU")
@@ -578,7 +595,10 @@ def main():
     Q = mixture_u8(nq, d, 1000, centres, 3, dev)
     torch.cuda.synchronize()
 
-    n_lists = max(0, args.lists)
+    # the rows are stored in the order of 4,096 k-means lists that no search probes: the same
+    # exhaustive screen, whose MFMA operands then change less from one row tile to the next
+    n_lists = 4096 if args.lists < 0 else args.lists
+    args.probe = 0 if args.probe < 0 else args.probe
     idx = certex.Index(d, metric="l2", n_lists=n_lists)
     t_build = time.perf_counter()
     idx.add(X)
@@ -660,6 +680,8 @@ def main():
             "anchor_stride": 16,
             "n_lists": n_lists,
             "probe_lists": args.probe if n_lists else 0,
+            "row_order": ("k-means list order" if n_lists else "id order")
+            + (" (the lists only order the stored rows; every row is screened)" if n_lists and not args.probe else ""),
             "build_s": round(t_build, 2),
             "screen": "int8 MFMA (exact), re-rank fp64",
             "phase_ms_per_step": phase_ms,
@@ -674,7 +696,8 @@ def main():
             "unit": "TOP/s",
             "frac": round(achieved / P_INT8_TOPS, 4),
             # measured only for the default workload (profiles/screen_i8_c2_traffic.txt)
-            "traffic": screen_traffic() if (n, d, nq, args.batch) == (10_000_000, 128, 10_000, 10_000) else None,
+            "traffic": screen_traffic()
+            if (n, d, nq, args.batch, n_lists, args.probe) == (10_000_000, 128, 10_000, 10_000, 4096, 0) else None,
             "avg_launch_ms": round(screen_ms, 4),
             "ops_per_launch": ops_per_launch,
         },

@@ -2,7 +2,8 @@
 (tests/exact_gpu.py: fp64 is exact for 8-bit data; ids bit-exact with ties to the lower id).
 
 Config 2 runs at its full size: 10,000,000 x 128 uint8 rows of the config 2 mixture, all 10,000
-queries in one batch, every id row checked.
+queries in one batch, every id row checked; in id order and in the order of 4,096 k-means lists
+(the bench's index), searched with and without a probe.
 
 Config 5's workload runs at 100,000,000 rows (a tenth of config 5's rows, which one test can afford):
 4,096 k-means lists probed 2 per query (config 5's setting), and while searches run another thread
@@ -38,6 +39,18 @@ def test_config2_full_size(gpu):
     ((dist, ids),) = topk_u8(X, Q, K, chunk=50_000)
     assert torch.equal(I, ids)
     assert torch.equal(D.double(), dist)
+    # the bench's index: rows stored in the order of 4,096 k-means lists, searched without a probe
+    # (every row screened) and with one
+    del idx
+    listed = certex.Index(128, n_lists=4096)
+    listed.add(X)
+    assert listed.core.lists == (4096, 10_000_000)
+    for probe in (0, 2):
+        D, I = listed.search(Q, k=K, batch=10_000, probe_lists=probe)
+        torch.cuda.synchronize()
+        print(f"config 2 in list order, probe {probe}: searched", flush=True)
+        assert torch.equal(I, ids)
+        assert torch.equal(D.double(), dist)
 
 
 N, N_NEW, N_GONE, N_LISTS = 100_000_000, 1_000_000, 1_000_000, 4_096
