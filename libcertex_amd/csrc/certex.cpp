@@ -376,6 +376,7 @@ void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan 
   r.codes                   = st.label_part.codes.as<int8_t>();
   r.rowc                    = st.label_part.rowc.p;
   r.rows_paired             = st.label_part.paired;
+  r.anchor_pairs            = st.label_part.paired;
   r.groups                  = route->anchor_groups;
   r.n_route                 = route->n_route;
   r.n_tiles                 = route->anchor_tiles;
@@ -1041,18 +1042,24 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
                          max_nx / (4 * certex_amd::kFineGroup * int64_t(k)))));
   // anchor groups: per label as plan_anchors sizes them for the largest label; the tail's
   // columns follow the partition's
+  // a label's anchors: one row every stride, or over a paired partition the row pairs every
+  // 2 stride (the anchor pass then reads whole lines)
+  const bool apairs = st.label_part.paired;
+  auto anchors_of   = [&](certex_amd::screen_group const& e) {
+    return apairs ? certex_amd::paired_anchor_count(e.x0, e.nx, stride) : (e.nx + stride - 1) / stride;
+  };
+  int64_t max_anchors = 0;
+  for (auto const& e : ga) { max_anchors = std::max(max_anchors, anchors_of(e)); }
   route_plan route;
   route.ap.stride   = stride;
   route.ap.n_anchor = 0;
-  size_groups(route.ap, (max_nx + stride - 1) / stride,
-              (st.size - st.label_part.n + stride - 1) / stride, nq_pad, k, &route.part_groups);
+  size_groups(route.ap, max_anchors, (st.size - st.label_part.n + stride - 1) / stride, nq_pad, k,
+              &route.part_groups);
   const int64_t waves = waves_of(st);
   route.anchor_chunk  = pick_chunk(
     waves * route.ap.group_steps, anchor_chunk_steps(wide, route.ap.group_steps), [&](int64_t c) {
       int64_t t = 0;
-      for (auto const& e : ga) {
-        t += certex_amd::screen_group_tiles(e.nq, (e.nx + stride - 1) / stride, qb, int(c));
-      }
+      for (auto const& e : ga) { t += certex_amd::screen_group_tiles(e.nq, anchors_of(e), qb, int(c)); }
       return t;
     });
   // the screen's groups: the tiled screen's query blocks and 256-row chunks for wide fp16 rows
@@ -1066,8 +1073,8 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
     });
   for (auto& e : ga) {
     e.tile0            = certex_amd::screen_group_tile0(route.anchor_tiles, e.nq, qb);
-    route.anchor_tiles = e.tile0 + certex_amd::screen_group_tiles(
-                                     e.nq, (e.nx + stride - 1) / stride, qb, route.anchor_chunk);
+    route.anchor_tiles =
+      e.tile0 + certex_amd::screen_group_tiles(e.nq, anchors_of(e), qb, route.anchor_chunk);
   }
   // the tiled screen aligns a group's query blocks (and, over paired rows, its tiles) to pairs
   for (auto& e : gs) {

@@ -55,6 +55,20 @@ __host__ __device__ inline int64_t paired_offset(int64_t r, int64_t b, int64_t r
 }
 /** Bytes of n rows in the paired layout (a whole number of pairs). */
 __host__ __device__ inline int64_t paired_bytes(int64_t n, int64_t row_bytes) { return (n + 1) / 2 * 2 * row_bytes; }
+/**
+ * Anchors of a routed group of rows [x0, x0 + nx) of a paired partition, taken in pairs: both rows
+ * of the row pairs that start at x0e + 2 s j (x0e: x0 rounded up to even), while they lie in the
+ * group. Scan index i is stored row x0e + (i / 2) 2 s + i % 2, so that the anchor pass reads whole
+ * 128-byte lines (both rows of a line) where single rows every s would take half lines. About nx / s
+ * anchors, as with one row every s.
+ */
+__host__ __device__ inline int64_t paired_anchor_count(int64_t x0, int64_t nx, int64_t s)
+{
+  const int64_t avail = nx - (x0 & 1);
+  if (avail <= 0) { return 0; }
+  const int64_t pairs = (avail + 2 * s - 1) / (2 * s);
+  return 2 * pairs - (2 * s * (pairs - 1) + 1 >= avail ? 1 : 0);
+}
 
 /** Bytes of a stored integer screening row of `dim` coordinates: 128 or 256 (zero padded). */
 __host__ __device__ inline int int_row_bytes(int64_t dim) { return dim <= 128 ? 128 : 256; }
@@ -158,6 +172,9 @@ struct screen_args {
   // stored rows are paired (the label partition of fp16 rows of more than 128 halves)
   const int8_t* qpaired = nullptr;
   bool rows_paired      = false;
+  // routed anchor pass over a paired partition: the anchors of a group are row pairs
+  // (paired_anchor_count), row_stride the pairs' half spacing
+  bool anchor_pairs = false;
   int chunk_steps;       // steps of kStepRows rows per workgroup: 4 waves x a whole number of
                          // anchor groups
   filter_args filter;

@@ -58,7 +58,8 @@ struct screen_work {
   int64_t q_first;  // first live query of the group (q0 or later)
   int64_t chunk;    // row chunk: scan steps [chunk * chunk_steps, (chunk + 1) * chunk_steps)
   int64_t n_scan;   // scan indices of the pass
-  int64_t base;     // stored row of scan index i: base + i * row_stride
+  int64_t base;     // stored row of scan index i: base + i * row_stride (anchor pairs:
+                    // base + (i / 2) 2 row_stride + i % 2)
   int rlead;        // scan indices below rlead are not live (pair alignment)
   bool valid;
 };
@@ -129,9 +130,10 @@ __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
   w.q_end              = g.q0 + g.nq;
   w.q_first            = g.q0;
   w.chunk              = n_qb > 1 ? int64_t(i / n_qb) * 8 + (t & 7) : t;
-  w.n_scan             = a.row_stride == 1 ? g.nx + rlead
-                                           : div_small(g.nx + a.row_stride - 1, a.row_stride);
-  w.base               = g.x0 - rlead;
+  w.n_scan             = a.anchor_pairs      ? paired_anchor_count(g.x0, g.nx, a.row_stride)
+                         : a.row_stride == 1 ? g.nx + rlead
+                                             : div_small(g.nx + a.row_stride - 1, a.row_stride);
+  w.base               = a.anchor_pairs ? g.x0 + (g.x0 & 1) : g.x0 - rlead;
   w.rlead              = rlead;
   const int64_t steps  = screen_steps(w.n_scan);
   w.valid              = t >= 0 && w.chunk < div_small(steps + a.chunk_steps - 1, a.chunk_steps);

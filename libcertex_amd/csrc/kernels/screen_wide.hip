@@ -93,17 +93,23 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
   const bool rp          = a.rows_paired;
   const int64_t cstep    = rp ? 256 : 128;  // bytes between consecutive 64-half chunks of a row
   auto row_at = [&](int64_t R) { return rp ? (R & ~int64_t(1)) * RB + (R & 1) * 64 : R * RB; };
+  // stored row of scan index i: one row every row_stride, or with anchor pairs both rows of a
+  // pair every 2 row_stride from an even base (the two quads of a pair then read one whole line)
+  const bool apairs = a.anchor_pairs;
+  auto row_of = [&](int64_t i) {
+    return apairs ? w.base + (i >> 1) * (2 * int64_t(a.row_stride)) + (i & 1) : w.base + i * a.row_stride;
+  };
   auto step_base = [&](int64_t s) {
-    return codes + row_at((w.base + s * kStepRows * a.row_stride) & ~int64_t(rp ? 1 : 0));
+    return codes + row_at(row_of(s * kStepRows) & ~int64_t(rp ? 1 : 0));
   };
   auto offsets   = [&](int64_t s, uint32_t (&O)[4]) {
-    const int64_t R0 = (w.base + s * kStepRows * a.row_stride) & ~int64_t(rp ? 1 : 0);
+    const int64_t R0 = row_of(s * kStepRows) & ~int64_t(rp ? 1 : 0);
     const int q      = lane & 3;
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
       int64_t r = s * kStepRows + bt * 16 + (lane >> 2);
       r         = r < w.n_scan ? r : w.n_scan - 1;
-      O[bt]     = uint32_t(row_at(w.base + r * a.row_stride) - row_at(R0) +
+      O[bt]     = uint32_t(row_at(row_of(r)) - row_at(R0) +
                            (rp ? (q >> 1) * 128 + (q & 1) * 32 : q * 32));
     }
   };
@@ -122,7 +128,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const bool ok  = r4 + j < w.n_scan;
-        const float v  = rowc[w.base + (ok ? r4 + j : 0) * a.row_stride];
+        const float v  = rowc[row_of(ok ? r4 + j : 0)];
         cc[bt][j]      = ok ? v : R::dead();
       }
     }
@@ -286,6 +292,9 @@ void launch(const screen_args& a, hipStream_t stream)
     blocks                 = n_steps == 0 ? 0 : 8 * n_qb * ((n_chunks + 7) / 8);
   }
   if (blocks == 0) { return; }
+  if (a.anchor_pairs && (a.groups == nullptr || !a.rows_paired || a.filter.kind != 0)) {
+    throw std::logic_error("certex: anchor pairs need a routed pass over paired rows without a filter");
+  }
   const dim3 grid{unsigned(blocks)};
   const size_t lds = size_t(qb) * size_t(a.row_bytes);
   switch (qt) {
