@@ -294,6 +294,7 @@ struct route_plan {
   int64_t anchor_tiles = 0, screen_tiles = 0;
   int anchor_chunk     = 0;
   int screen_chunk     = 0;
+  bool anchor_tiled    = false;  // the partition's anchor pass runs as tiles (anchors_f16_tile)
   int64_t part_groups  = 0;  // anchor group columns of the partition (the tail's follow)
   anchor_plan ap{};
 };
@@ -377,6 +378,7 @@ void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan 
   r.rowc                    = st.label_part.rowc.p;
   r.rows_paired             = st.label_part.paired;
   r.anchor_pairs            = st.label_part.paired;
+  r.tiled                   = route->anchor_tiled;
   r.groups                  = route->anchor_groups;
   r.n_route                 = route->n_route;
   r.n_tiles                 = route->anchor_tiles;
@@ -1056,14 +1058,22 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   size_groups(route.ap, max_anchors, (st.size - st.label_part.n + stride - 1) / stride, nq_pad, k,
               &route.part_groups);
   const int64_t waves = waves_of(st);
-  route.anchor_chunk  = pick_chunk(
-    waves * route.ap.group_steps, anchor_chunk_steps(wide, route.ap.group_steps), [&](int64_t c) {
-      int64_t t = 0;
-      for (auto const& e : ga) { t += certex_amd::screen_group_tiles(e.nq, anchors_of(e), qb, int(c)); }
-      return t;
-    });
-  // the screen's groups: the tiled screen's query blocks and 256-row chunks for wide fp16 rows
-  const bool tiled = uses_tile_screen(st);
+  // the screen's groups: the tiled screen's query blocks and 256-row chunks for wide fp16 rows;
+  // so too the anchor pass over anchor pairs with fine groups (its tiles start at an even query)
+  const bool tiled    = uses_tile_screen(st);
+  route.anchor_tiled  = tiled && apairs && route.ap.fine;
+  const int qba       = route.anchor_tiled ? certex_amd::tile_block_queries() : qb;
+  const int64_t alead = route.anchor_tiled ? 1 : 0;  // odd first queries take one slot more
+  route.anchor_chunk  = route.anchor_tiled
+                          ? certex_amd::tile_chunk_steps()
+                          : pick_chunk(waves * route.ap.group_steps,
+                                       anchor_chunk_steps(wide, route.ap.group_steps), [&](int64_t c) {
+                                         int64_t t = 0;
+                                         for (auto const& e : ga) {
+                                           t += certex_amd::screen_group_tiles(e.nq, anchors_of(e), qb, int(c));
+                                         }
+                                         return t;
+                                       });
   const int qbs    = tiled ? certex_amd::tile_block_queries() : qb;
   route.screen_chunk =
     tiled ? certex_amd::tile_chunk_steps() : pick_chunk(waves, kRoutedChunk, [&](int64_t c) {
@@ -1072,9 +1082,10 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
       return t;
     });
   for (auto& e : ga) {
-    e.tile0            = certex_amd::screen_group_tile0(route.anchor_tiles, e.nq, qb);
+    const int64_t nq   = e.nq + (e.q0 & alead);
+    e.tile0            = certex_amd::screen_group_tile0(route.anchor_tiles, nq, qba);
     route.anchor_tiles =
-      e.tile0 + certex_amd::screen_group_tiles(e.nq, anchors_of(e), qb, route.anchor_chunk);
+      e.tile0 + certex_amd::screen_group_tiles(nq, anchors_of(e), qba, route.anchor_chunk);
   }
   // the tiled screen aligns a group's query blocks (and, over paired rows, its tiles) to pairs
   for (auto& e : gs) {

@@ -173,8 +173,10 @@ struct screen_args {
   const int8_t* qpaired = nullptr;
   bool rows_paired      = false;
   // routed anchor pass over a paired partition: the anchors of a group are row pairs
-  // (paired_anchor_count), row_stride the pairs' half spacing
+  // (paired_anchor_count), row_stride the pairs' half spacing; with tiled, the pass runs as tiles
+  // of the tiled screen (fine groups, paired queries, chunk_steps = tile_chunk_steps())
   bool anchor_pairs = false;
+  bool tiled        = false;
   int chunk_steps;       // steps of kStepRows rows per workgroup: 4 waves x a whole number of
                          // anchor groups
   filter_args filter;
@@ -268,6 +270,13 @@ void anchors_f16_wide(const screen_args& a, hipStream_t stream);
  * 256 rows (chunk_steps = tile_chunk_steps()) with tile_block_queries() queries; row_stride 1.
  */
 void screen_f16_tile(const screen_args& a, hipStream_t stream);
+/**
+ * The routed fp16 anchor pass over a paired partition with anchor pairs and fine groups, as tiles
+ * of the same kernel (256 anchors x tile_block_queries() queries): each lane writes the best
+ * screen value of its 4 consecutive anchors of every row tile and query tile to the group table.
+ * anchors_f16_wide runs it for a pass with `tiled`.
+ */
+void anchors_f16_tile(const screen_args& a, hipStream_t stream);
 int tile_chunk_steps();
 int tile_block_queries();
 

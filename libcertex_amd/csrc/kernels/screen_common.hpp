@@ -123,7 +123,7 @@ __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
   const screen_group g = a.groups[lo];
   const int64_t t      = int64_t(b) - g.tile0;
   const int qlead      = PAIRS ? int(g.q0 & 1) : 0;
-  const int rlead      = PAIRS && a.rows_paired ? int(g.x0 & 1) : 0;
+  const int rlead      = PAIRS && a.rows_paired && !a.anchor_pairs ? int(g.x0 & 1) : 0;
   const uint32_t n_qb  = uint32_t(div_small(g.nq + qlead + QB - 1, QB));
   const uint32_t i     = uint32_t(t) >> 3;
   w.q0                 = g.q0 - qlead + int64_t(n_qb > 1 ? i % n_qb : 0) * QB;

@@ -127,7 +127,7 @@ struct tile_shape {
   static_assert(WR * WQ == kTileWaves && WR * 16 * RT == kTileRows, "4 waves cover the tile");
 };
 
-template <int RT, int QT, bool FILT>
+template <int RT, int QT, bool FILT, bool ANCH>
 __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_args a)
 {
   using R           = f16_rows;
@@ -164,6 +164,12 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
   const int r_lo        = scan0 == 0 ? w.rlead : 0;
   const int64_t n_q     = w.q_end - w.q0 < TQ ? w.q_end - w.q0 : TQ;
   const int q_lo        = w.q_first > w.q0 ? int(w.q_first - w.q0) : 0;
+  // stored row of tile row r: consecutive rows, or (ANCH, anchor pairs) both rows of a pair
+  // every 2 row_stride rows from the tile's first pair (scan index i = stored row
+  // base + (i / 2) 2 row_stride + i % 2; scan0 is even)
+  const int64_t s2     = ANCH ? 2 * int64_t(a.row_stride) : 2;
+  const int64_t row_t0 = ANCH ? w.base + (scan0 >> 1) * s2 : w.base + scan0;
+  auto tile_rel        = [&](int64_t r) { return ANCH ? (r >> 1) * s2 + (r & 1) : r; };
 
   if (tid == 0) { n_hits = 0; }
 
@@ -175,9 +181,9 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
   float* rc_lds    = th_lds + TQ;
   {
     const int64_t r = wave_u * 64 + lane;
-    lds_copy<4>(static_cast<const float*>(a.rowc) + w.base + scan0 + (r < n_rows ? r : n_rows - 1),
+    lds_copy<4>(static_cast<const float*>(a.rowc) + row_t0 + tile_rel(r < n_rows ? r : n_rows - 1),
                 lds_addr(rc_lds + wave_u * 64));
-    if (wave_u * 64 < TQ) {
+    if (!ANCH && wave_u * 64 < TQ) {
       const int64_t q = wave_u * 64 + lane;
       lds_copy<4>(static_cast<const float*>(a.theta) + w.q0 + (q < n_q ? q : n_q - 1),
                   lds_addr(th_lds + wave_u * 64));
@@ -194,13 +200,13 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
   const int rstep   = rp ? 128 : kStageB;
   const int crow    = lane >> 2;
   const int cchunk  = (lane & 3) ^ ((lane >> 3) & 3);
-  const char* rbase = reinterpret_cast<const char*>(a.codes) + (w.base + scan0) * int64_t(RB) + cchunk * 16;
+  const char* rbase = reinterpret_cast<const char*>(a.codes) + row_t0 * int64_t(RB) + cchunk * 16;
   const char* qbase = reinterpret_cast<const char*>(a.qpaired) + w.q0 * int64_t(RB) + cchunk * 16;
   uint32_t roff[CA], qoff[CB];
 #pragma unroll
   for (int j = 0; j < CA; ++j) {
     int64_t r = (wave * CA + j) * 16 + crow;
-    r         = r < n_rows ? r : n_rows - 1;
+    r         = tile_rel(r < n_rows ? r : n_rows - 1);
     roff[j]   = uint32_t(rp ? (r & ~int64_t(1)) * RB + (r & 1) * 64 : r * RB);
   }
 #pragma unroll
@@ -296,6 +302,24 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
   for (; s + 2 < n_stages; ++s) { stage(s, std::true_type{}, std::true_type{}); }
   stage(s, std::true_type{}, std::false_type{});
   stage(s + 1, std::false_type{}, std::false_type{});
+
+  if constexpr (ANCH) {
+    // fine groups: the 4 consecutive anchors of a lane's row tile are one group of the table
+    float* gmax = static_cast<float*>(a.gmax);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int qloc  = wq * 16 * QT + qt * 16 + frow;
+      const bool live = qloc >= q_lo && qloc < n_q;
+#pragma unroll
+      for (int bt = 0; bt < RT; ++bt) {
+        const int64_t first = scan0 + wr * 16 * RT + bt * 16 + fch * 4;  // scan index
+        const acc_t v       = acc[bt][qt];
+        const float m       = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+        if (live && first < w.n_scan) { gmax[table_entry(a, w.q0 + qloc, first / kFineGroup)] = m; }
+      }
+    }
+    return;
+  }
   __syncthreads();  // the staging LDS becomes the survivor list
 
   uint32_t* hit_q    = reinterpret_cast<uint32_t*>(lds);
@@ -374,7 +398,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
   flush_hits<true>(w.q0, TQ, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(CAP), scratch);
 }
 
-template <int RT, int QT, bool FILT>
+template <int RT, int QT, bool FILT, bool ANCH>
 void launch_shape(const screen_args& a, hipStream_t stream)
 {
   constexpr int TQ = tile_shape<RT, QT>::TQ;
@@ -388,15 +412,18 @@ void launch_shape(const screen_args& a, hipStream_t stream)
     blocks                 = n_steps == 0 ? 0 : 8 * n_qb * ((n_chunks + 7) / 8);
   }
   if (blocks == 0) { return; }
-  if (a.chunk_steps != kTileSteps || a.row_stride != 1 || a.row_bytes % 128 != 0 ||
-      a.qpaired == nullptr || (a.rows_paired && a.groups == nullptr)) {
+  const bool shape = ANCH ? a.groups != nullptr && a.anchor_pairs && a.rows_paired && a.fine &&
+                             a.filter.kind == 0 && a.gmax != nullptr
+                           : a.row_stride == 1 && !(a.rows_paired && a.groups == nullptr);
+  if (!shape || a.chunk_steps != kTileSteps || a.row_bytes % 128 != 0 || a.qpaired == nullptr) {
     throw std::logic_error(
       "certex: the tiled screen needs chunks of 4 steps over rows of 128-byte multiples, paired "
-      "queries, and paired rows only in routed passes");
+      "queries, and paired rows only in routed passes (anchor passes: routed over anchor pairs, "
+      "fine groups, no filter)");
   }
   screen_args b = a;
-  b.spill_cap   = a.spill_q != nullptr ? a.spill_pool / blocks : 0;
-  auto* k       = &screen_tile_kernel<RT, QT, FILT>;
+  b.spill_cap   = !ANCH && a.spill_q != nullptr ? a.spill_pool / blocks : 0;
+  auto* k       = &screen_tile_kernel<RT, QT, FILT, ANCH>;
   const int lds = tile_lds_total(TQ);
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(k),
                           hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) {
@@ -415,10 +442,12 @@ int tile_block_queries() { return tile_shape<8, 4>::TQ; }
 void screen_f16_tile(const screen_args& a, hipStream_t stream)
 {
   if (a.filter.kind != 0) {
-    launch_shape<8, 4, true>(a, stream);
+    launch_shape<8, 4, true, false>(a, stream);
   } else {
-    launch_shape<8, 4, false>(a, stream);
+    launch_shape<8, 4, false, false>(a, stream);
   }
 }
+
+void anchors_f16_tile(const screen_args& a, hipStream_t stream) { launch_shape<8, 4, false, true>(a, stream); }
 
 }  // namespace certex_amd

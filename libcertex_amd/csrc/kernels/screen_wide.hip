@@ -310,7 +310,9 @@ int wide_block_queries(int row_bytes) { return 16 * wide_query_tiles(row_bytes);
 
 void anchors_f16_wide(const screen_args& a, hipStream_t stream)
 {
-  if (a.filter.kind != 0) {
+  if (a.tiled) {
+    anchors_f16_tile(a, stream);
+  } else if (a.filter.kind != 0) {
     launch<true>(a, stream);
   } else {
     launch<false>(a, stream);

@@ -133,3 +133,21 @@ def test_paired_layout_odd_starts(gpu, metric):
     for batch in (1024, 100):
         D, I = search(idx, Q, 10, lq, batch)
         check(X, Q, 10, metric, D, I, row_labels=lx, query_labels=lq)
+
+
+@pytest.mark.parametrize("k", [1, 5])
+def test_paired_anchor_pairs_coarse_and_fine(gpu, k):
+    """The anchor pass over a paired partition takes row pairs as anchors. Labels of about 70,000
+    rows give k = 1 coarse anchor groups (the K-loop anchor pass) and k = 5 fine groups (the anchor
+    pass as tiles of the tiled screen); a label with an odd first row and one of 2 rows ride along."""
+    rng = np.random.default_rng(93)
+    row_counts = {0: 70_001, 1: 2, 2: 68_999}
+    lx = rng.permutation(np.concatenate([np.full(c, l, np.int32) for l, c in row_counts.items()]))
+    lq = rng.integers(0, 3, 300).astype(np.int32)
+    X = data.powerlaw_unit(len(lx), 200, seed=94)
+    Q = data.powerlaw_unit(len(lq), 200, seed=95)
+    idx = certex.Index(200, metric="l2")
+    idx.add(torch.from_numpy(X).cuda(), labels=torch.from_numpy(lx))
+    assert idx.core.n_partitioned == len(lx)
+    D, I = search(idx, Q, k, lq)
+    check(X, Q, k, "l2", D, I, row_labels=lx, query_labels=lq)
