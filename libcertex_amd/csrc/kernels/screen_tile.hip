@@ -39,6 +39,11 @@
 //   buckets (flush_hits of screen_common.hpp).
 // Workgroup b runs on XCD b % 8; the query blocks of one row tile run on one XCD (work_of), so a
 // row tile is fetched from HBM about once.
+//
+// The same kernel (ANCH) runs the routed anchor pass over a paired partition with fine groups: a
+// tile's 256 rows are anchors taken in row pairs (scan index i is stored row base + (i / 2) 2 s +
+// i % 2), and instead of survivors each lane writes the maximum of its 4 accumulators of every row
+// tile and query tile, the screen value of one fine group of 4 anchors, to the group table.
 
 #include "screen_common.hpp"
 
