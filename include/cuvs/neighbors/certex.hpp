@@ -213,11 +213,16 @@ void search_without_allocation(cuvs::resources const& res, search_params const& 
 /** Bytes of the per-GPU scratch array of search_without_allocation. */
 auto no_alloc_scratch_bytes() -> size_t;
 
-/** Exact k nearest neighbours of every query among the vectors of its label (device int32). */
+/**
+ * Exact k nearest neighbours of every query among the vectors of its label (int32 labels, one per
+ * query). The labels are in device memory, or in host memory with labels_on_host: the search over
+ * the label partition plans its launches from them on the host, and host labels spare it a copy
+ * back and a wait for the stream.
+ */
 template <typename T>
 void search(cuvs::resources const& res, search_params const& params, index<T> const& idx,
             matrix_view<const T> queries, const int32_t* query_labels, int64_t* neighbors,
-            float* distances, int64_t k);
+            float* distances, int64_t k, bool labels_on_host = false);
 
 /**
  * The ids in the order of the stored rows (reference Index.list_order, certex/index.py:353-359,

@@ -27,6 +27,8 @@ def _keys(x):
     x = torch.as_tensor(x, device="cuda")
     if x.dtype == torch.bfloat16:
         return x.to(torch.float32)
+    if x.dtype == torch.float16:
+        return x  # nothing to convert (no check that would wait for the GPU)
     h = x.to(torch.float16)
     return h if bool(torch.isfinite(h).all()) else x.to(torch.float32)
 
@@ -93,9 +95,11 @@ class KeyCache:
             heads = torch.arange(self.n_kv_heads, device="cuda", dtype=torch.int32)
             self._labels[key] = heads.repeat_interleave(n)
         n0 = self.n_kv_heads * self.size  # the shared index's first new id
-        self.index.add(
+        # the head labels are built here (non-negative): no check that would wait for the GPU
+        self.index._add(
             _fit(K, self.dtype, "keys").reshape(self.n_kv_heads * n, self.head_dim).contiguous(),
-            labels=self._labels[key],
+            self._labels[key],
+            check_labels=False,
         )
         need = n0 + self.n_kv_heads * n
         if self.local is None or self.local.shape[0] < need:
@@ -130,7 +134,9 @@ class KeyCache:
         r = H // self.n_kv_heads
         key = ("search", H, m)
         if key not in self._labels:
-            self._labels[key] = (torch.arange(H, device="cuda", dtype=torch.int32) // r).repeat_interleave(m)
+            # in host memory: the label-routed search plans its launches from them without a
+            # read-back from the GPU
+            self._labels[key] = (torch.arange(H, dtype=torch.int32) // r).repeat_interleave(m)
         labels = self._labels[key]
         D, I = self.index.search(
             _fit(Q, self.dtype, "queries").reshape(H * m, d), k=k, batch=batch or max(2048, H * m), labels=labels

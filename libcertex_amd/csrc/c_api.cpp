@@ -454,8 +454,12 @@ cuvsError_t cuvsCertexSearchWithLabels(cuvsResources_t res,
       auto& idx = *as_index<T>(*index);
       auto q    = matrix_of<T>(queries, "the queries");
       certex::expects(q.on_device, "certex: expected a tensor in device memory");
-      const auto* ql = device_data<int32_t>(query_labels, 1, "the query labels");
-      certex::expects(query_labels->dl_tensor.shape[0] == q.rows, "one label per query");
+      // query labels in device or host memory (host labels spare the routed search a read-back)
+      check_tensor<int32_t>(query_labels, 1, "the query labels");
+      const DLTensor& lt = query_labels->dl_tensor;
+      certex::expects(is_device(lt) || is_host(lt), "certex: unsupported DLPack device");
+      const auto* ql = data_of<const int32_t>(lt);
+      certex::expects(lt.shape[0] == q.rows, "one label per query");
       auto* nb        = device_data<int64_t>(neighbors, 2, "the neighbors");
       auto* ds        = device_data<float>(distances, 2, "the distances");
       const int64_t k = neighbors->dl_tensor.shape[1];
@@ -463,7 +467,7 @@ cuvsError_t cuvsCertexSearchWithLabels(cuvsResources_t res,
                         distances->dl_tensor.shape[0] == q.rows &&
                         distances->dl_tensor.shape[1] == k,
                       "output shapes do not match the queries");
-      certex::search<T>(r, p, idx, q, ql, nb, ds, k);
+      certex::search<T>(r, p, idx, q, ql, nb, ds, k, is_host(lt));
     });
   });
 }

@@ -31,6 +31,7 @@ resources::resources(void* stream) : s_(std::make_unique<detail::resources_state
   }
   CERTEX_HIP_TRY(hipHostMalloc(&s_->host_small, 64, hipHostMallocDefault));
   CERTEX_HIP_TRY(hipEventCreateWithFlags(&s_->read_back, hipEventDisableTiming));
+  CERTEX_HIP_TRY(hipEventCreateWithFlags(&s_->staged, hipEventDisableTiming));
   if (const char* cap = std::getenv("CERTEX_SCRATCH_SLOT_CAP")) {
     s_->slot_cap = size_t(std::strtoull(cap, nullptr, 10));
   }
@@ -43,6 +44,7 @@ resources::~resources()
     for (auto& b : s_->slots) { b.release(); }
     if (s_->host_small) { (void)hipHostFree(s_->host_small); }
     if (s_->read_back) { (void)hipEventDestroy(s_->read_back); }
+    if (s_->staged) { (void)hipEventDestroy(s_->staged); }
     if (s_->host_stage) { (void)hipHostFree(s_->host_stage); }
     if (s_->owns_stream) { (void)hipStreamDestroy(s_->stream); }
   }
@@ -991,18 +993,22 @@ using batch_fn = void (*)(cuvs::resources const&, index_state const&, const void
  */
 void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn batch,
                   const char* queries, size_t qrow, int64_t B, int k, const int32_t* qlabels,
-                  int64_t* neighbors, float* distances, certex_amd::filter_args fa,
-                  search_params const& params)
+                  const int32_t* hlabels, int64_t* neighbors, float* distances,
+                  certex_amd::filter_args fa, search_params const& params)
 {
   auto& rs           = res.state();
   hipStream_t stream = rs.stream;
-  // the labels come back through pinned staging (a pageable copy is staged by the runtime)
   std::vector<int32_t> lab(static_cast<size_t>(B)), order(static_cast<size_t>(B)),
     sorted(static_cast<size_t>(B));
-  auto* hl = static_cast<int32_t*>(rs.stage(std::max<size_t>(16, size_t(B) * 4)));
-  CERTEX_HIP_TRY(hipMemcpyAsync(hl, qlabels, size_t(B) * 4, hipMemcpyDeviceToHost, stream));
-  CERTEX_HIP_TRY(hipStreamSynchronize(stream));
-  std::copy(hl, hl + B, lab.begin());
+  if (hlabels != nullptr) {
+    std::copy(hlabels, hlabels + B, lab.begin());  // host labels: no read-back, no wait
+  } else {
+    // device labels come back through pinned staging (a pageable copy is staged by the runtime)
+    auto* hl = static_cast<int32_t*>(rs.stage(std::max<size_t>(16, size_t(B) * 4)));
+    CERTEX_HIP_TRY(hipMemcpyAsync(hl, qlabels, size_t(B) * 4, hipMemcpyDeviceToHost, stream));
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+    std::copy(hl, hl + B, lab.begin());
+  }
   // queries in label order, stable: a counting sort when the batch's labels span a small range
   // (one pass, no comparisons), else a comparison sort
   const auto [lo_it, hi_it] = std::minmax_element(lab.begin(), lab.end());
@@ -1117,7 +1123,7 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
     std::memcpy(hs + 2 * lab_bytes, ga.data(), ga.size() * sizeof(ga[0]));
     std::memcpy(hs + 2 * lab_bytes + tab_bytes, gs.data(), gs.size() * sizeof(gs[0]));
   }
-  CERTEX_HIP_TRY(hipMemcpyAsync(dev, hs, all_bytes, hipMemcpyHostToDevice, stream));
+  rs.copy_staged(dev, all_bytes);
   route.anchor_groups = d_ga;
   route.screen_groups = d_gs;
 
@@ -1130,14 +1136,14 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   batch(res, st, q_sorted, B, k, 0, nb_s, ds_s, fa, params, &route);
   certex_amd::scatter_rows(nb_s, d_order, B, int64_t(k) * 8, neighbors, stream);
   certex_amd::scatter_rows(ds_s, d_order, B, int64_t(k) * 4, distances, stream);
-  // no wait here: the next routed batch stages its labels and tables only after a read-back on
-  // this stream, which orders them after this batch's copy of the tables
+  // no wait here: the next use of the staging waits for this batch's copy of the tables
 }
 
 template <typename T>
 void search_impl(cuvs::resources const& res, search_params const& params, index<T> const& idx,
                  matrix_view<const T> queries, int64_t* neighbors, float* distances, int64_t k,
-                 certex_amd::filter_args fa, bool no_alloc = false)
+                 certex_amd::filter_args fa, bool no_alloc = false,
+                 const int32_t* host_labels = nullptr)
 {
   index_state const& st = idx.state();
   expects(queries.on_device, "certex: the queries must be in device memory");
@@ -1153,12 +1159,22 @@ void search_impl(cuvs::resources const& res, search_params const& params, index<
   // a search without allocation screens label queries through the label filter: routing a
   // batch over the label partition stages its tables in pinned host memory
   const bool route = fa.kind == 3 && st.label_part.n > 0 && !no_alloc;
+  if (host_labels != nullptr && !route) {
+    // the label filter reads the query labels on the GPU: one copy through pinned staging
+    auto& rs  = res.state();
+    auto* dev = static_cast<int32_t*>(rs.get(cuvs::detail::ws_qlabels, size_t(nq) * 4));
+    std::memcpy(rs.stage(size_t(nq) * 4), host_labels, size_t(nq) * 4);
+    rs.copy_staged(dev, size_t(nq) * 4);
+    fa.query_labels = dev;
+  }
   std::function<void(int64_t, int64_t)> run = [&](int64_t b0, int64_t B) {
     if (no_alloc) { res.state().arena_reset(); }
     try {
       const char* q = reinterpret_cast<const char*>(queries.data) + size_t(b0) * qrow;
       if (route) {
-        routed_batch(res, st, batch, q, qrow, B, int(k), fa.query_labels + b0, neighbors + b0 * k,
+        routed_batch(res, st, batch, q, qrow, B, int(k),
+                     host_labels != nullptr ? nullptr : fa.query_labels + b0,
+                     host_labels != nullptr ? host_labels + b0 : nullptr, neighbors + b0 * k,
                      distances + b0 * k, fa, params);
       } else {
         batch(res, st, q, B, int(k), b0, neighbors + b0 * k, distances + b0 * k, fa, params,
@@ -1177,6 +1193,7 @@ void search_impl(cuvs::resources const& res, search_params const& params, index<
   };
   for (int64_t b0 = 0; b0 < nq; b0 += bs) {
     std::shared_lock batch_view(st.rw);  // the rows of this batch stay fixed during updates
+    st.await_updates(res.state().stream);
     run(b0, std::min(bs, nq - b0));
   }
 }
@@ -1598,6 +1615,8 @@ void extend(cuvs::resources const& res, matrix_view<const T> new_vectors, index<
   expects(new_vectors.cols == st.dim, "dimension mismatch");
   if (new_vectors.rows == 0) { return; }
   std::lock_guard w(st.writer);
+  const hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  st.await_updates(stream);
   const int64_t need = st.size + new_vectors.rows;
   if (need > st.capacity) { grow(res, st, std::max(need, 2 * st.capacity)); }
   if (is_int(st.type)) {
@@ -1607,7 +1626,10 @@ void extend(cuvs::resources const& res, matrix_view<const T> new_vectors, index<
     append_float(res, st, new_vectors.data, new_vectors.rows, new_vectors.on_device, st.size);
   }
   refresh_anchors(res, st, st.size, need);  // anchors of the new ids only: searches read the others
-  res.sync();
+  // vectors from host memory are read by the copy: it completes before the call returns; device
+  // vectors are read in stream order, and searches on other streams wait for the update's event
+  if (!new_vectors.on_device) { res.sync(); }
+  st.mark_update(stream);
   std::unique_lock publish(st.rw);
   st.size = need;
 }
@@ -1658,6 +1680,7 @@ void list_order(cuvs::resources const& res, index<T> const& idx, int32_t* out)
   expects(st.n_lists > 0, "certex: the index has no lists");
   std::shared_lock view(st.rw);
   hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  st.await_updates(stream);
   if (st.n_listed > 0) {
     CERTEX_HIP_TRY(hipMemcpyAsync(out, st.row_ids.p, size_t(st.n_listed) * sizeof(int32_t),
                                   hipMemcpyDeviceToDevice, stream));
@@ -1673,6 +1696,7 @@ void set_labels(cuvs::resources const& res, const int32_t* labels, int64_t n, in
   expects(first >= 0 && first + n <= st.size, "certex: labels beyond the vectors of the index");
   std::lock_guard w(st.writer);
   hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  st.await_updates(stream);
   std::unique_lock publish(st.rw);
   if (!st.has_labels) {
     CERTEX_HIP_TRY(hipDeviceSynchronize());
@@ -1684,7 +1708,7 @@ void set_labels(cuvs::resources const& res, const int32_t* labels, int64_t n, in
     CERTEX_HIP_TRY(hipMemcpyAsync(st.labels.as<int32_t>() + first, labels,
                                   size_t(n) * sizeof(int32_t), hipMemcpyDeviceToDevice, stream));
   }
-  CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  st.mark_update(stream);
   if (n > 0 && first < st.label_part.n) { st.label_part.n = 0; }  // the partition no longer matches
 }
 
@@ -1697,6 +1721,7 @@ void partition_by_labels(cuvs::resources const& res, index<T>* idx)
   const int64_t n = st.size;
   expects(n < (int64_t(1) << 31), "certex: at most 2^31 - 1 vectors per partition");
   hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  st.await_updates(stream);
   using cuvs::detail::device_buffer;
   // fp16 rows of more than 128 halves: the copy is paired, so that the tiled screen copies whole
   // 128-byte lines per stage
@@ -1767,14 +1792,15 @@ void search(cuvs::resources const& res, search_params const& params, index<T> co
 template <typename T>
 void search(cuvs::resources const& res, search_params const& params, index<T> const& idx,
             matrix_view<const T> queries, const int32_t* query_labels, int64_t* neighbors,
-            float* distances, int64_t k)
+            float* distances, int64_t k, bool labels_on_host)
 {
   expects(idx.has_labels(), "certex: the index has no labels");
   certex_amd::filter_args fa{};
   fa.kind         = 3;
   fa.row_labels   = idx.state().labels.template as<int32_t>();
-  fa.query_labels = query_labels;
-  search_impl(res, params, idx, queries, neighbors, distances, k, fa);
+  fa.query_labels = labels_on_host ? nullptr : query_labels;
+  search_impl(res, params, idx, queries, neighbors, distances, k, fa, false,
+              labels_on_host ? query_labels : nullptr);
 }
 
 
@@ -1843,6 +1869,7 @@ void serialize(cuvs::resources const& res, std::string const& filename, index<T>
 {
   index_state const& st = idx.state();
   std::shared_lock view(st.rw);
+  st.await_updates(static_cast<hipStream_t>(res.stream()));
   std::ofstream os(filename, std::ios::binary);
   expects(os.good(), "certex: cannot open the index file for writing");
   os << dtype_prefix<T>();
@@ -1976,7 +2003,8 @@ void deserialize(cuvs::resources const& res, std::string const& filename, index<
   template void search<T>(cuvs::resources const&, search_params const&, index<T> const&,       \
                           matrix_view<const T>, int64_t*, float*, int64_t, filter);            \
   template void search<T>(cuvs::resources const&, search_params const&, index<T> const&,       \
-                          matrix_view<const T>, const int32_t*, int64_t*, float*, int64_t);    \
+                          matrix_view<const T>, const int32_t*, int64_t*, float*, int64_t,     \
+                          bool);                                                               \
   template void serialize<T>(cuvs::resources const&, std::string const&, index<T> const&);     \
   template void deserialize<T>(cuvs::resources const&, std::string const&, index<T>*);
 

@@ -114,6 +114,7 @@ enum ws_slot : int {
   ws_spill_row,   // screen spill pool: row of each entry
   ws_spill_val,   // screen spill pool: screen value of each entry (fp16 rows)
   ws_qpaired,     // the batch's fp16 query rows in the paired layout (the tiled screen)
+  ws_qlabels,     // query labels given in host memory, copied for the label filter
   ws_n_slots
 };
 
@@ -130,6 +131,8 @@ struct resources_state {
   hipEvent_t read_back = nullptr;  // recorded behind a read-back into host_small
   void* host_stage    = nullptr;  // pinned host staging of the routing tables (grow-only)
   size_t host_stage_bytes = 0;
+  hipEvent_t staged   = nullptr;  // recorded behind the last copy out of host_stage
+  bool staged_pending = false;    // `staged` has been recorded
   // test hook: a slot request above this many bytes fails as an allocation failure would
   // (environment variable CERTEX_SCRATCH_SLOT_CAP, read when the resources are created; 0 = none)
   size_t slot_cap = 0;
@@ -154,11 +157,16 @@ struct resources_state {
     }
   }
 
-  /** Pinned host staging of at least `bytes` bytes (grow-only; waits for the stream first). */
+  /** Pinned host staging of at least `bytes` bytes (grow-only; waits for the stream first). The
+   *  last copy out of it has completed when this returns. */
   void* stage(size_t bytes)
   {
     if (arena != nullptr) {
       throw std::logic_error("certex: a search without allocation cannot stage host memory");
+    }
+    if (staged_pending) {
+      CERTEX_HIP_TRY(hipEventSynchronize(staged));
+      staged_pending = false;
     }
     if (host_stage_bytes < bytes) {
       CERTEX_HIP_TRY(hipStreamSynchronize(stream));
@@ -170,6 +178,15 @@ struct resources_state {
       host_stage_bytes = n;
     }
     return host_stage;
+  }
+
+  /** Copies `bytes` of the staging to device memory `dst` on the stream, without waiting; the
+   *  next stage() waits for the copy before it hands the staging out again. */
+  void copy_staged(void* dst, size_t bytes)
+  {
+    CERTEX_HIP_TRY(hipMemcpyAsync(dst, host_stage, bytes, hipMemcpyHostToDevice, stream));
+    CERTEX_HIP_TRY(hipEventRecord(staged, stream));
+    staged_pending = true;
   }
 
   /** Scratch slot of at least `bytes` bytes (grow-only; waits for the stream before growing). */
@@ -277,6 +294,24 @@ struct index_state {
   int list_width = 0;  // elements of a screening row: row_bytes (int8) or halves (fp16)
   mutable std::shared_mutex rw;  // searches: shared per batch; publication of updates: exclusive
   std::mutex writer;             // one update at a time
+  // the GPU work of the last published update: a writer records it on its stream before it
+  // publishes, and every later search or update waits for it on its own stream (a wait on the
+  // GPU, not on the host), so that an update needs no host synchronisation to be visible to
+  // searches on other streams
+  hipEvent_t updated = nullptr;
+
+  index_state() { CERTEX_HIP_TRY(hipEventCreateWithFlags(&updated, hipEventDisableTiming)); }
+  ~index_state()
+  {
+    if (updated != nullptr) { (void)hipEventDestroy(updated); }
+  }
+  index_state(index_state const&)            = delete;
+  index_state& operator=(index_state const&) = delete;
+
+  /** Orders `stream` after the last published update (searches, and writers before they write). */
+  void await_updates(hipStream_t stream) const { CERTEX_HIP_TRY(hipStreamWaitEvent(stream, updated, 0)); }
+  /** Marks the work queued so far on `stream` as the update about to be published. */
+  void mark_update(hipStream_t stream) { CERTEX_HIP_TRY(hipEventRecord(updated, stream)); }
 };
 
 }  // namespace cuvs::neighbors::certex::detail

@@ -276,10 +276,17 @@ class Index:
     def add(self, x, labels=None):
         """Add vectors, optionally with one non-negative label each; returns their ids
         (certex/index.py:266-305)."""
+        return self._add(x, labels, check_labels=True)
+
+    def _add(self, x, labels, check_labels):
+        """add(); labels the caller built itself (check_labels false) are not checked, which
+        spares a read of the labels back from the GPU and the wait for the stream it needs."""
         X, kind = self._vectors(x, device=False)
         if labels is not None:
             labels = _to_torch(labels).reshape(-1).to(device="cuda", dtype=torch.int32).contiguous()
-            _require(labels.shape[0] == X.shape[0] and int(labels.min()) >= 0, "one non-negative label per vector")
+            _require(labels.shape[0] == X.shape[0], "one non-negative label per vector")
+            if check_labels:
+                _require(labels.numel() == 0 or int(labels.min()) >= 0, "one non-negative label per vector")
         L = C.lib()
         with self._writer:
             if self.core is not None and self.core.has_labels:
@@ -350,7 +357,10 @@ class Index:
         ftype = C.NO_FILTER
         if labels is not None:
             _require(self.core.has_labels, "the index has no labels")
-            ql = _to_torch(labels).reshape(-1).to(device="cuda", dtype=torch.int32).contiguous()
+            # labels on the GPU stay there; labels from the host stay in host memory, where the
+            # search plans its label routing without reading them back from the GPU
+            ql = _to_torch(labels).reshape(-1)
+            ql = ql.to(dtype=torch.int32).contiguous()
             _require(ql.shape[0] == nq, "one label per query")
         if filter is not None:
             m = _to_torch(filter).to(torch.bool)

@@ -151,3 +151,26 @@ def test_paired_anchor_pairs_coarse_and_fine(gpu, k):
     assert idx.core.n_partitioned == len(lx)
     D, I = search(idx, Q, k, lq)
     check(X, Q, k, "l2", D, I, row_labels=lx, query_labels=lq)
+
+
+@pytest.mark.parametrize("partition", [True, False])
+def test_host_and_device_labels(gpu, partition):
+    """Query labels in host memory (the routed search plans from them without a read-back; the
+    unpartitioned search copies them through pinned staging) and on the GPU give the same results,
+    equal to the oracle, over ragged batches and over searches queued back to back without a wait
+    in between (the staging is reused only once its last copy is done)."""
+    X = data.mixture_u8(30_000, seed=71)
+    Q = data.mixture_u8(500, seed=72)
+    lx, lq = skewed_labels(len(X), 73), data.labels(len(Q), 18, 74)
+    idx = certex.Index(X.shape[1], partition_labels=partition)
+    idx.add(torch.from_numpy(X).cuda(), labels=torch.from_numpy(lx))
+    assert (idx.core.n_partitioned > 0) == partition
+    Qd = torch.from_numpy(Q).cuda()
+    host, dev = torch.from_numpy(lq), torch.from_numpy(lq).cuda()
+    outs = []
+    for batch in (2048, 130, 2048):
+        for labels in (host, dev):
+            outs.append(idx.search(Qd, k=10, batch=batch, labels=labels))
+    torch.cuda.synchronize()
+    for D, I in outs:
+        check(X, Q, 10, "l2", D.cpu().numpy(), I.cpu().numpy(), row_labels=lx, query_labels=lq)
