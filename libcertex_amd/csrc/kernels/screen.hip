@@ -187,14 +187,18 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   step_labels SL;    // the label filter's row labels of the step (anchor pass with a filter)
   auto mfmas = [&](const frag_t (&bf)[QT][KS], acc_t (&acc)[BT][QT]) {
     __builtin_amdgcn_s_setprio(1);
+    // K-slice outermost: consecutive MFMAs share their row fragment (operand A) across the query
+    // tiles, so fewer operand bits switch from one MFMA to the next on this power-limited part
+    // (measured against the slices of one tile back to back: 0.8% faster, and 2% faster than
+    // holding the query fragment across the row tiles)
 #pragma unroll
-    for (int bt = 0; bt < BT; ++bt) {
+    for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        acc_t t = R::mfma(av[bt][0], bf[qt][0], cc[bt]);
+      for (int bt = 0; bt < BT; ++bt) {
 #pragma unroll
-        for (int ks = 1; ks < KS; ++ks) { t = R::mfma(av[bt][ks], bf[qt][ks], t); }
-        acc[bt][qt] = t;
+        for (int qt = 0; qt < QT; ++qt) {
+          acc[bt][qt] = R::mfma(av[bt][ks], bf[qt][ks], ks == 0 ? cc[bt] : acc[bt][qt]);
+        }
       }
     }
     __builtin_amdgcn_s_setprio(0);
