@@ -83,11 +83,20 @@ constexpr int kBatch = 8;
 __device__ inline uint32_t desc_key(int32_t v) { return ~(uint32_t(v) ^ 0x80000000u); }
 __device__ inline int32_t desc_value(uint32_t key) { return int32_t(~key ^ 0x80000000u); }
 
+template <typename F>
+__device__ uint32_t radix_select(int64_t n, int rank, F key_of, uint32_t lo, uint32_t hi, int* hist,
+                                 int* wave_tot, uint32_t* sel_digit, int* sel_rank);
+
+template <typename F>
+__device__ void key_range(int64_t n, F key_of, uint32_t& lo, uint32_t& hi, int& below,
+                          uint32_t* red);
+
 __global__ __launch_bounds__(kThreads) void threshold_kernel(
   const int32_t* gmax, int64_t n_groups, int64_t nq, int k, int32_t* theta)
 {
   __shared__ int hist[256];
   __shared__ int wave_tot[4];
+  __shared__ uint32_t red[48];
   __shared__ uint32_t sel_digit;
   __shared__ int sel_rank;
   const int64_t q = blockIdx.x;
@@ -101,30 +110,15 @@ __global__ __launch_bounds__(kThreads) void threshold_kernel(
     return;
   }
   const int32_t* v = gmax + q * n_groups;
-  uint32_t prefix = 0, mask = 0;
-  int rank = k;  // 1-based rank among ascending keys
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    hist[tid] = 0;
-    __syncthreads();
-    for (int64_t e = tid; e < n_groups; e += kThreads) {
-      const uint32_t key = desc_key(v[e]);
-      if ((key & mask) == prefix) { atomicAdd(&hist[(key >> shift) & 255], 1); }
-    }
-    __syncthreads();
-    const int c    = hist[tid];
-    const int incl = block_scan_incl(c, wave_tot);
-    if (incl - c < rank && rank <= incl) {
-      sel_digit = uint32_t(tid);
-      sel_rank  = rank - (incl - c);
-    }
-    __syncthreads();
-    prefix |= sel_digit << shift;
-    mask |= 255u << shift;
-    rank = sel_rank;
-    __syncthreads();
-  }
+  auto key_of      = [&](int64_t e) { return desc_key(v[e]); };
+  uint32_t lo, hi;
+  int below;
+  key_range(n_groups, key_of, lo, hi, below, red);
+  // the k-th largest value: the k-th smallest descending key (0xffffffff is the lowest value)
+  const uint32_t key = k > below ? 0xffffffffu
+                                 : radix_select(n_groups, k, key_of, lo, hi, hist, wave_tot, &sel_digit, &sel_rank);
   if (tid == 0) {
-    const int32_t t = desc_value(prefix);
+    const int32_t t = desc_value(key);
     theta[q]        = t > kKeepAll ? t : kKeepAll;
   }
 }
@@ -886,9 +880,6 @@ __device__ inline double screen_upper_bound(float vf, const threshold_f_args& a,
   return ub;
 }
 
-template <typename F>
-__device__ uint32_t radix_select(int64_t n, int rank, F key_of, int* hist, int* wave_tot,
-                                 uint32_t* sel_digit, int* sel_rank);
 
 /**
  * theta[q] for the fp16 screen, certified from screen values alone: the k-th largest finite
@@ -903,9 +894,9 @@ __global__ __launch_bounds__(kThreads) void threshold_f16_cert_kernel(threshold_
 {
   __shared__ int hist[256];
   __shared__ int wave_tot[4];
+  __shared__ uint32_t red[48];
   __shared__ uint32_t sel_digit;
   __shared__ int sel_rank;
-  __shared__ int cnt;
   const int64_t q = blockIdx.x;
   const int tid   = threadIdx.x;
   if (q >= a.nq) {
@@ -913,25 +904,21 @@ __global__ __launch_bounds__(kThreads) void threshold_f16_cert_kernel(threshold_
     return;
   }
   const float* v = a.gmax + q * a.n_groups;
-  if (tid == 0) { cnt = 0; }
-  __syncthreads();
-  int local = 0;
-  for (int64_t e = tid; e < a.n_groups; e += kThreads) { local += isfinite(v[e]) ? 1 : 0; }
-  atomicAdd(&cnt, local);
-  __syncthreads();
-  if (cnt < a.k) {
+  // the k-th largest finite value: the k-th smallest of the descending keys ~fkey, the others
+  // (0xffffffff) last; the range pass counts the finite ones
+  auto key_of = [&](int64_t e) {
+    const float x = v[e];
+    return isfinite(x) ? ~fkey(x) : 0xffffffffu;
+  };
+  uint32_t lo, hi;
+  int finite;
+  key_range(a.n_groups, key_of, lo, hi, finite, red);
+  if (finite < a.k) {
     // keep every live row: removed rows (screen value -inf) still fail
     if (tid == 0) { a.theta[q] = -FLT_MAX; }
     return;
   }
-  // the k-th largest finite value: the k-th smallest of the descending keys ~fkey, the others last
-  const uint32_t key = radix_select(
-    a.n_groups, a.k,
-    [&](int64_t e) {
-      const float x = v[e];
-      return isfinite(x) ? ~fkey(x) : 0xffffffffu;
-    },
-    hist, wave_tot, &sel_digit, &sel_rank);
+  const uint32_t key = radix_select(a.n_groups, a.k, key_of, lo, hi, hist, wave_tot, &sel_digit, &sel_rank);
   if (tid == 0) { a.theta[q] = theta_of(screen_upper_bound(key_value(~key), a, q), a, q); }
 }
 
@@ -956,17 +943,116 @@ __device__ inline double screen_lower_bound(float v, double aq, double C, double
   return lb;
 }
 
+/** Inclusive prefix sum over the T threads of a block of T = 64 (one wave), kThreads or 1024. */
+template <int T>
+__device__ inline int scan_incl_t(int v, int* wave_tot)
+{
+  static_assert(T == 64 || T == kThreads || T == 1024, "block shapes of the selects");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off);
+    if (lane >= off) { incl += t; }
+  }
+  if constexpr (T == 64) {
+    return incl;
+  } else {
+    if (lane == 63) { wave_tot[wave] = incl; }
+    __syncthreads();
+    int add = 0;
+    for (int w = 0; w < wave; ++w) { add += wave_tot[w]; }
+    __syncthreads();
+    return incl + add;
+  }
+}
+
+/** The minimum, the maximum and the sum of (lo, hi, n) over the T threads of a block; every
+ *  thread gets them. red: 3 * 16 LDS words. */
+template <int T>
+__device__ inline void block_min_max_sum(uint32_t& lo, uint32_t& hi, int& n, uint32_t* red)
+{
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t l = __shfl_xor(lo, off), h = __shfl_xor(hi, off);
+    const int c      = __shfl_xor(n, off);
+    lo               = l < lo ? l : lo;
+    hi               = h > hi ? h : hi;
+    n += c;
+  }
+  if constexpr (T > 64) {
+    constexpr int W = T / 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+      red[wave]      = lo;
+      red[16 + wave] = hi;
+      red[32 + wave] = uint32_t(n);
+    }
+    __syncthreads();
+    lo = red[0];
+    hi = red[16];
+    n  = int(red[32]);
+    for (int w = 1; w < W; ++w) {
+      lo = red[w] < lo ? red[w] : lo;
+      hi = red[16 + w] > hi ? red[16 + w] : hi;
+      n += int(red[32 + w]);
+    }
+    __syncthreads();
+  }
+}
+
 /**
- * The rank-th smallest (1-based) of the 32-bit keys key_of(e), e < n: an LDS radix select over
- * four 8-bit digits. Every thread of the block calls it and gets the same key.
+ * The smallest key lo, the largest key hi below 0xffffffff and the number of keys below
+ * 0xffffffff among key_of(e), e < n, over the block (every thread gets them); red: 48 LDS words.
  */
 template <typename F>
-__device__ uint32_t radix_select(int64_t n, int rank, F key_of, int* hist, int* wave_tot,
-                                 uint32_t* sel_digit, int* sel_rank)
+__device__ void key_range(int64_t n, F key_of, uint32_t& lo, uint32_t& hi, int& below, uint32_t* red)
 {
+  lo    = 0xffffffffu;
+  hi    = 0;
+  below = 0;
+  for (int64_t e0 = 0; e0 < n; e0 += int64_t(kThreads) * kBatch) {
+    uint32_t kk[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int64_t e = e0 + i * kThreads + threadIdx.x;
+      kk[i]           = key_of(e < n ? e : n - 1);
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (e0 + i * kThreads + threadIdx.x < n) {
+        lo = kk[i] < lo ? kk[i] : lo;
+        if (kk[i] != 0xffffffffu) {
+          hi = kk[i] > hi ? kk[i] : hi;
+          ++below;
+        }
+      }
+    }
+  }
+  block_min_max_sum<kThreads>(lo, hi, below, red);
+}
+
+/**
+ * The rank-th smallest (1-based) of the 32-bit keys key_of(e), e < n, given their range: lo the
+ * smallest key, hi the largest below 0xffffffff, and rank at most the number of keys below
+ * 0xffffffff. An LDS radix select, 8 bits at a time from the top of the bits below the common
+ * prefix of lo and hi (every key in between shares that prefix; a key 0xffffffff that shares it
+ * sorts last and leaves the rank-th unchanged). Every thread of the block calls it and gets the
+ * same key.
+ */
+template <typename F>
+__device__ uint32_t radix_select(int64_t n, int rank, F key_of, uint32_t lo, uint32_t hi, int* hist,
+                                 int* wave_tot, uint32_t* sel_digit, int* sel_rank)
+{
+  if (lo == hi) { return lo; }
   const int tid   = threadIdx.x;
-  uint32_t prefix = 0, mask = 0;
-  for (int shift = 24; shift >= 0; shift -= 8) {
+  int r           = 32 - __builtin_clz(lo ^ hi);  // bits below the common prefix
+  uint32_t mask   = r == 32 ? 0u : ~((1u << r) - 1u);
+  uint32_t prefix = lo & mask;
+  while (r > 0) {
+    const int w       = r < 8 ? r : 8;
+    const int shift   = r - w;
+    const uint32_t dm = (1u << w) - 1u;
     hist[tid] = 0;
     __syncthreads();
     for (int64_t e0 = 0; e0 < n; e0 += int64_t(kThreads) * kBatch) {
@@ -979,7 +1065,7 @@ __device__ uint32_t radix_select(int64_t n, int rank, F key_of, int* hist, int* 
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         if (e0 + i * kThreads + tid < n && (kk[i] & mask) == prefix) {
-          atomicAdd(&hist[(kk[i] >> shift) & 255], 1);
+          atomicAdd(&hist[(kk[i] >> shift) & dm], 1);
         }
       }
     }
@@ -992,12 +1078,180 @@ __device__ uint32_t radix_select(int64_t n, int rank, F key_of, int* hist, int* 
     }
     __syncthreads();
     prefix |= *sel_digit << shift;
-    mask |= 255u << shift;
+    mask |= dm << shift;
     rank = *sel_rank;
+    r -= w;
     __syncthreads();
   }
   return prefix;
 }
+
+/**
+ * The rank-th smallest (1-based) of the keys that the T threads of a block hold in registers,
+ * VPT each (0xffffffff past the table, which sorts last and leaves every rank up to the number of
+ * smaller keys unchanged): the LDS radix select of radix_select, reading the keys once from global
+ * memory instead of once per digit. The bits that the smallest key and the largest key below
+ * 0xffffffff share are shared by every key in between and are skipped: a query's group maxima lie
+ * close together, and a first digit among those bits sends every count to one histogram bin.
+ * The rest is selected 8 bits at a time from the top. Every thread gets the key.
+ */
+template <int T, int VPT>
+__device__ uint32_t radix_select_regs(const uint32_t (&kk)[VPT], int rank, int* hist, int* wave_tot,
+                                      uint32_t* red, uint32_t* sel_digit, int* sel_rank)
+{
+  constexpr int BPT = 256 / T > 0 ? 256 / T : 1;  // histogram bins per thread in the scan
+  const int tid     = threadIdx.x;
+  uint32_t lo = 0xffffffffu, hi = 0;
+  int below = 0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    lo = kk[i] < lo ? kk[i] : lo;
+    if (kk[i] != 0xffffffffu) {
+      hi = kk[i] > hi ? kk[i] : hi;
+      ++below;
+    }
+  }
+  block_min_max_sum<T>(lo, hi, below, red);
+  if (rank > below) { return 0xffffffffu; }
+  if (lo == hi) { return lo; }
+  int r           = 32 - __builtin_clz(lo ^ hi);  // bits below the common prefix
+  uint32_t mask   = r == 32 ? 0u : ~((1u << r) - 1u);
+  uint32_t prefix = lo & mask;
+  while (r > 0) {
+    const int w       = r < 8 ? r : 8;
+    const int shift   = r - w;
+    const uint32_t dm = (1u << w) - 1u;
+    if (tid * BPT < 256) {
+#pragma unroll
+      for (int j = 0; j < BPT; ++j) { hist[tid * BPT + j] = 0; }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      if ((kk[i] & mask) == prefix) { atomicAdd(&hist[(kk[i] >> shift) & dm], 1); }
+    }
+    __syncthreads();
+    int c[BPT], sum = 0;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      c[j] = tid * BPT < 256 ? hist[tid * BPT + j] : 0;
+      sum += c[j];
+    }
+    int run = scan_incl_t<T>(sum, wave_tot) - sum;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      if (run < rank && rank <= run + c[j]) {
+        *sel_digit = uint32_t(tid * BPT + j);
+        *sel_rank  = rank - run;
+      }
+      run += c[j];
+    }
+    __syncthreads();
+    prefix |= *sel_digit << shift;
+    mask |= dm << shift;
+    rank = *sel_rank;
+    r -= w;
+    __syncthreads();
+  }
+  return prefix;
+}
+
+/** threshold_kernel with the query's group maxima read once into registers (n_groups <= T VPT). */
+template <int T, int VPT>
+__global__ __launch_bounds__(T) void threshold_regs_kernel(const int32_t* gmax, int64_t n_groups,
+                                                           int64_t nq, int k, int32_t* theta)
+{
+  __shared__ int hist[256];
+  __shared__ int wave_tot[16];
+  __shared__ uint32_t red[48];
+  __shared__ uint32_t sel_digit;
+  __shared__ int sel_rank;
+  const int64_t q = blockIdx.x;
+  const int tid   = threadIdx.x;
+  if (q >= nq) {
+    if (tid == 0) { theta[q] = kKeepNone; }
+    return;
+  }
+  if (n_groups < k) {
+    if (tid == 0) { theta[q] = kKeepAll; }
+    return;
+  }
+  const int32_t* v = gmax + q * n_groups;
+  uint32_t kk[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int64_t e = int64_t(i) * T + tid;
+    kk[i]           = e < n_groups ? desc_key(v[e]) : 0xffffffffu;
+  }
+  const uint32_t key = radix_select_regs<T, VPT>(kk, k, hist, wave_tot, red, &sel_digit, &sel_rank);
+  if (tid == 0) {
+    const int32_t t = desc_value(key);
+    theta[q]        = t > kKeepAll ? t : kKeepAll;
+  }
+}
+
+/** threshold_f16_cert_kernel with the query's group maxima read once into registers
+ *  (n_groups <= T VPT); the count of finite groups comes from the same registers. */
+template <int T, int VPT>
+__global__ __launch_bounds__(T) void threshold_f16_cert_regs_kernel(threshold_f_args a)
+{
+  __shared__ int hist[256];
+  __shared__ int wave_tot[16];
+  __shared__ uint32_t red[48];
+  __shared__ uint32_t sel_digit;
+  __shared__ int sel_rank;
+  const int64_t q = blockIdx.x;
+  const int tid   = threadIdx.x;
+  if (q >= a.nq) {
+    if (tid == 0) { a.theta[q] = INFINITY; }
+    return;
+  }
+  const float* v = a.gmax + q * a.n_groups;
+  uint32_t kk[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int64_t e = int64_t(i) * T + tid;
+    const float x   = e < a.n_groups ? v[e] : INFINITY;
+    kk[i]           = isfinite(x) ? ~fkey(x) : 0xffffffffu;
+  }
+  // non-finite groups map to 0xffffffff: the select returns it when fewer than k are finite
+  const uint32_t key = radix_select_regs<T, VPT>(kk, a.k, hist, wave_tot, red, &sel_digit, &sel_rank);
+  if (tid != 0) { return; }
+  if (key == 0xffffffffu) {
+    a.theta[q] = -FLT_MAX;  // keep every live row: removed rows (screen value -inf) still fail
+  } else {
+    a.theta[q] = theta_of(screen_upper_bound(key_value(~key), a, q), a, q);
+  }
+}
+
+/** Launches K<T, VPT> for the smallest register shape holding n keys per query, one block per
+ *  query; false when n exceeds the largest shape (the streaming kernel then runs). */
+template <template <int, int> class L, typename... Args>
+bool launch_select_regs(int64_t n, unsigned blocks, hipStream_t stream, Args... args)
+{
+  if (n <= 64 * 8) { L<64, 8>::go(blocks, stream, args...); return true; }
+  if (n <= 64 * 16) { L<64, 16>::go(blocks, stream, args...); return true; }
+  if (n <= kThreads * 8) { L<kThreads, 8>::go(blocks, stream, args...); return true; }
+  if (n <= kThreads * 16) { L<kThreads, 16>::go(blocks, stream, args...); return true; }
+  return false;  // larger tables: the streaming kernels (more blocks per CU, measured faster)
+}
+
+template <int T, int VPT>
+struct threshold_regs_launch {
+  static void go(unsigned blocks, hipStream_t stream, const int32_t* gmax, int64_t n_groups,
+                 int64_t nq, int k, int32_t* theta)
+  {
+    threshold_regs_kernel<T, VPT><<<blocks, T, 0, stream>>>(gmax, n_groups, nq, k, theta);
+  }
+};
+
+template <int T, int VPT>
+struct threshold_f_regs_launch {
+  static void go(unsigned blocks, hipStream_t stream, const threshold_f_args& a)
+  {
+    threshold_f16_cert_regs_kernel<T, VPT><<<blocks, T, 0, stream>>>(a);
+  }
+};
 
 /**
  * Exact re-rank of one query's survivors, one block per query. With screen values (fp16 rows),
@@ -1059,7 +1313,7 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
   uint32_t tk  = 0;
   double U = INFINITY, aq = 0, C = 0;
   if (ordered) {
-    tk = radix_select(n_cand, k, [&](int64_t e) { return ~fkey(vals[e]); }, hist, wave_tot,
+    tk = radix_select(n_cand, k, [&](int64_t e) { return ~fkey(vals[e]); }, 0u, 0xfffffffeu, hist, wave_tot,
                       &sel_digit, &sel_rank);
     if (tid == 0) { fill = 0; }
     __syncthreads();
@@ -1200,6 +1454,10 @@ void threshold_i8(const int32_t* gmax, int64_t n_groups, int64_t nq, int64_t nq_
                   int32_t* theta, hipStream_t stream)
 {
   if (nq_pad == 0) { return; }
+  if (launch_select_regs<threshold_regs_launch>(n_groups, unsigned(nq_pad), stream, gmax, n_groups,
+                                                nq, k, theta)) {
+    return;
+  }
   threshold_kernel<<<unsigned(nq_pad), kThreads, 0, stream>>>(gmax, n_groups, nq, k, theta);
 }
 
@@ -1251,6 +1509,9 @@ void launch_dyn(K kernel, unsigned blocks, size_t bytes, hipStream_t stream, Arg
 void threshold_f16(const threshold_f_args& a, hipStream_t stream)
 {
   if (a.nq_pad == 0) { return; }
+  if (launch_select_regs<threshold_f_regs_launch>(a.n_groups, unsigned(a.nq_pad), stream, a)) {
+    return;
+  }
   threshold_f16_cert_kernel<<<unsigned(a.nq_pad), kThreads, 0, stream>>>(a);
 }
 
