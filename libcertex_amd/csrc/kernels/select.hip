@@ -1313,8 +1313,14 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
   uint32_t tk  = 0;
   double U = INFINITY, aq = 0, C = 0;
   if (ordered) {
-    tk = radix_select(n_cand, k, [&](int64_t e) { return ~fkey(vals[e]); }, 0u, 0xfffffffeu, hist, wave_tot,
-                      &sel_digit, &sel_rank);
+    // the survivors' screen values lie close together above theta: the select starts below the
+    // bits they share (all finite or +inf, so every key is below 0xffffffff)
+    auto key_of = [&](int64_t e) { return ~fkey(vals[e]); };
+    uint32_t lo, hi;
+    int below;
+    key_range(n_cand, key_of, lo, hi, below, reinterpret_cast<uint32_t*>(hist));
+    tk = k <= below ? radix_select(n_cand, k, key_of, lo, hi, hist, wave_tot, &sel_digit, &sel_rank)
+                    : radix_select(n_cand, k, key_of, 0u, 0xfffffffeu, hist, wave_tot, &sel_digit, &sel_rank);
     if (tid == 0) { fill = 0; }
     __syncthreads();
     for (int64_t e0 = 0; e0 < n_cand; e0 += int64_t(kThreads) * kBatch) {
