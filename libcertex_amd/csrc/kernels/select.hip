@@ -265,14 +265,48 @@ __device__ inline void select_pair(const uint64_t* key, const uint32_t* row, int
                                    int* sel_rank, int* sel_count, uint64_t* out_key,
                                    uint32_t* out_row)
 {
-  const int tid   = threadIdx.x;
-  uint64_t prefix = 0, mask = 0;
-  for (int shift = 56; shift >= 0; shift -= 8) {
+  const int tid = threadIdx.x;
+  // the keys' range: the bits that the smallest and the largest share are shared by every key (the
+  // best scores of a query lie close together) and need no pass, whose counts would all go to one
+  // histogram bin; the select runs 8 bits at a time from the first differing bit down
+  __shared__ uint64_t rng[2 * (kThreads / 64)];
+  uint64_t lo = ~0ull, hi = 0;
+  for (int e = tid; e < n; e += kThreads) {
+    const uint64_t kk = key[e];
+    lo                = kk < lo ? kk : lo;
+    hi                = kk > hi ? kk : hi;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint64_t l = __shfl_xor(lo, off), h = __shfl_xor(hi, off);
+    lo               = l < lo ? l : lo;
+    hi               = h > hi ? h : hi;
+  }
+  if ((tid & 63) == 0) {
+    rng[tid >> 6]                 = lo;
+    rng[kThreads / 64 + (tid >> 6)] = hi;
+  }
+  __syncthreads();
+  lo = rng[0];
+  hi = rng[kThreads / 64];
+  for (int w = 1; w < kThreads / 64; ++w) {
+    lo = rng[w] < lo ? rng[w] : lo;
+    hi = rng[kThreads / 64 + w] > hi ? rng[kThreads / 64 + w] : hi;
+  }
+  __syncthreads();
+  int r           = lo == hi ? 0 : 64 - __builtin_clzll(lo ^ hi);  // bits below the common prefix
+  uint64_t mask   = r == 64 ? 0ull : ~((uint64_t(1) << r) - 1);
+  uint64_t prefix = lo & mask;
+  if (r == 0 && tid == 0) { *sel_count = n; }  // every key is the selected one
+  while (r > 0) {
+    const int w       = r < 8 ? r : 8;
+    const int shift   = r - w;
+    const uint64_t dm = (uint64_t(1) << w) - 1;
     hist[tid] = 0;
     __syncthreads();
     for (int e = tid; e < n; e += kThreads) {
       const uint64_t kk = key[e];
-      if ((kk & mask) == prefix) { atomicAdd(&hist[int(kk >> shift) & 255], 1); }
+      if ((kk & mask) == prefix) { atomicAdd(&hist[int((kk >> shift) & dm)], 1); }
     }
     __syncthreads();
     const int c    = hist[tid];
@@ -284,10 +318,12 @@ __device__ inline void select_pair(const uint64_t* key, const uint32_t* row, int
     }
     __syncthreads();
     prefix |= uint64_t(*sel_digit) << shift;
-    mask |= uint64_t(255) << shift;
+    mask |= dm << shift;
     rank = *sel_rank;
+    r -= w;
     __syncthreads();
   }
+  __syncthreads();
   *out_key = prefix;
   if (!with_row) { return; }
   const int same = *sel_count;  // pairs whose key is the selected one
