@@ -53,6 +53,12 @@ struct half_t {
   uint16_t bits;
 };
 
+/** Storage of a bfloat16 coordinate (the upper 16 bits of an IEEE binary32). An addition of this
+ *  build: a float index of bfloat16 vectors keeps them exactly at 2 bytes per coordinate. */
+struct bfloat16_t {
+  uint16_t bits;
+};
+
 /** Parameters of an index (reference certex.hpp:43-89). */
 struct index_params {
   cuvs::distance::DistanceType metric = cuvs::distance::DistanceType::L2Expanded;

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libcertex_c.so")
 
 kDLCPU, kDLROCM = 1, 10
-kDLInt, kDLUInt, kDLFloat = 0, 1, 2
+kDLInt, kDLUInt, kDLFloat, kDLBfloat = 0, 1, 2, 4
 NO_FILTER, BITSET, BITMAP = 0, 1, 2
 L2Expanded, CosineExpanded, InnerProduct = 0, 2, 6
 CUVS_ERROR, CUVS_SUCCESS = 0, 1
@@ -23,6 +23,7 @@ CUVS_ERROR, CUVS_SUCCESS = 0, 1
 _DL = {
     torch.float32: (kDLFloat, 32),
     torch.float16: (kDLFloat, 16),
+    torch.bfloat16: (kDLBfloat, 16),
     torch.int8: (kDLInt, 8),
     torch.uint8: (kDLUInt, 8),
     torch.int64: (kDLInt, 64),

@@ -21,12 +21,12 @@ def _stride(n, k):
 
 def _keys(x):
     """Keys or queries on the GPU as float16, or float32 when float16 would overflow
-    (certex/attention.py:37-41). bfloat16 inputs become float32, which holds them exactly, so that
-    the top k is exact for the values given (float16 would round bfloat16 values below its normal
-    range)."""
+    (certex/attention.py:37-41). bfloat16 inputs stay bfloat16: the index keeps them exactly at
+    2 bytes per coordinate (float16 would round bfloat16 values below its normal range), and the
+    exact re-rank reads half the bytes of float32 rows."""
     x = torch.as_tensor(x, device="cuda")
     if x.dtype == torch.bfloat16:
-        return x.to(torch.float32)
+        return x
     if x.dtype == torch.float16:
         return x  # nothing to convert (no check that would wait for the GPU)
     h = x.to(torch.float16)
@@ -34,15 +34,17 @@ def _keys(x):
 
 
 def _fit(x, dtype, what):
-    """x in the cache's vector type; a conversion that would change a value (bfloat16 or float32
-    values that float16 rounds or overflows) is an error rather than a silent rounding."""
+    """x in the cache's vector type; a conversion that would change a value (float32 or bfloat16
+    values that float16 rounds or overflows, float32 or float16 values that bfloat16 rounds) is an
+    error rather than a silent rounding."""
     if x.dtype == dtype:
         return x
     y = x.to(dtype)
     _require(
         bool(torch.equal(y.to(x.dtype), x)),
         f"the cache holds {dtype} keys, which cannot represent these {what} exactly: "
-        "start the cache with keys of this type (bfloat16 or float32 keys give a float32 cache)",
+        "start the cache with keys of this type (float32 keys give a float32 cache, which holds "
+        "float16 and bfloat16 values exactly)",
     )
     return y
 

@@ -55,6 +55,8 @@ auto code_of() -> uint8_t
 {
   if constexpr (std::is_same_v<T, float> || std::is_same_v<T, certex::half_t>) {
     return kDLFloat;
+  } else if constexpr (std::is_same_v<T, certex::bfloat16_t>) {
+    return kDLBfloat;
   } else if constexpr (std::is_signed_v<T>) {
     return kDLInt;
   } else {
@@ -127,12 +129,14 @@ void dispatch(DLDataType dtype, F&& f)
     f(float{});
   } else if (dtype.code == kDLFloat && dtype.bits == 16) {
     f(certex::half_t{});
+  } else if (dtype.code == kDLBfloat && dtype.bits == 16) {
+    f(certex::bfloat16_t{});
   } else if (dtype.code == kDLInt && dtype.bits == 8) {
     f(int8_t{});
   } else if (dtype.code == kDLUInt && dtype.bits == 8) {
     f(uint8_t{});
   } else {
-    throw std::invalid_argument("certex: vectors must be float32, float16, int8, or uint8");
+    throw std::invalid_argument("certex: vectors must be float32, float16, bfloat16, int8, or uint8");
   }
 }
 
@@ -493,6 +497,7 @@ static DLDataType dtype_of_file(const char* filename)
   const std::string d(prefix + 1, 2);
   if (d == "f4") { return {kDLFloat, 32, 1}; }
   if (d == "f2") { return {kDLFloat, 16, 1}; }
+  if (d == "b2") { return {kDLBfloat, 16, 1}; }
   if (d == "i1") { return {kDLInt, 8, 1}; }
   if (d == "u1") { return {kDLUInt, 8, 1}; }
   throw std::invalid_argument("certex: not a CertEx index file");

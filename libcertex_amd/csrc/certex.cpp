@@ -132,9 +132,13 @@ auto to_kind(cuvs::distance::DistanceType m) -> metric_kind
 auto is_int(vtype t) -> bool { return t == vtype::i8 || t == vtype::u8; }
 auto elem_of(vtype t) -> certex_amd::elem
 {
-  return t == vtype::f32 ? certex_amd::elem::f32 : certex_amd::elem::f16;
+  return t == vtype::f32 ? certex_amd::elem::f32
+                         : (t == vtype::bf16 ? certex_amd::elem::bf16 : certex_amd::elem::f16);
 }
-auto elem_size(vtype t) -> size_t { return t == vtype::f32 ? 4 : (t == vtype::f16 ? 2 : 1); }
+auto elem_size(vtype t) -> size_t
+{
+  return t == vtype::f32 ? 4 : ((t == vtype::f16 || t == vtype::bf16) ? 2 : 1);
+}
 
 /** Grow every per-row array to `cap` rows (the caller holds the writer lock). */
 void grow(cuvs::resources const& res, index_state& st, int64_t cap)
@@ -1817,6 +1821,8 @@ auto dtype_prefix() -> std::string
     s = "<f4";
   } else if constexpr (std::is_same_v<T, half_t>) {
     s = "<f2";
+  } else if constexpr (std::is_same_v<T, bfloat16_t>) {
+    s = "<b2";  // no NumPy descriptor: this build's own prefix for bfloat16 vectors
   } else if constexpr (std::is_same_v<T, int8_t>) {
     s = "|i1";
   } else {
@@ -2010,6 +2016,7 @@ void deserialize(cuvs::resources const& res, std::string const& filename, index<
 
 CERTEX_INSTANTIATE(float)
 CERTEX_INSTANTIATE(half_t)
+CERTEX_INSTANTIATE(bfloat16_t)
 CERTEX_INSTANTIATE(int8_t)
 CERTEX_INSTANTIATE(uint8_t)
 

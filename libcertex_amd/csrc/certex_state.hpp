@@ -215,7 +215,7 @@ struct resources_state {
 
 namespace cuvs::neighbors::certex::detail {
 
-enum class vtype : int { f32 = 0, f16 = 1, i8 = 2, u8 = 3 };
+enum class vtype : int { f32 = 0, f16 = 1, i8 = 2, u8 = 3, bf16 = 4 };
 
 template <typename T>
 constexpr vtype vtype_of();
@@ -223,6 +223,8 @@ template <>
 constexpr vtype vtype_of<float>() { return vtype::f32; }
 template <>
 constexpr vtype vtype_of<half_t>() { return vtype::f16; }
+template <>
+constexpr vtype vtype_of<bfloat16_t>() { return vtype::bf16; }
 template <>
 constexpr vtype vtype_of<int8_t>() { return vtype::i8; }
 template <>

@@ -329,7 +329,7 @@ void verify_topk_i8(const verify_args& a, hipStream_t stream);
 
 // --- float vectors (float32 / float16) ------------------------------------------------------
 
-enum class elem : int { f32 = 0, f16 = 1 };
+enum class elem : int { f32 = 0, f16 = 1, bf16 = 2 };
 
 /** Widest fp16 screening row (halves) of the screens. */
 constexpr int kMaxF16Halves = 2048;

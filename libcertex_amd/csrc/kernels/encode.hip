@@ -105,6 +105,7 @@ __global__ void iota_kernel(int32_t* p, int64_t n, int32_t first)
 
 __device__ inline double coord(const void* p, elem t, int64_t i)
 {
+  if (t == elem::bf16) { return double(static_cast<const __bf16*>(p)[i]); }
   return t == elem::f32 ? double(static_cast<const float*>(p)[i])
                         : double(static_cast<const _Float16*>(p)[i]);
 }

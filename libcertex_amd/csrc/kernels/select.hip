@@ -614,6 +614,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_small_kernel(verify_a
 
 __device__ inline double fcoord(const void* p, elem t, int64_t i)
 {
+  if (t == elem::bf16) { return double(static_cast<const __bf16*>(p)[i]); }
   return t == elem::f32 ? double(static_cast<const float*>(p)[i])
                         : double(static_cast<const _Float16*>(p)[i]);
 }
@@ -807,6 +808,8 @@ __device__ __forceinline__ void score_rows_l(const double* qv, const void* vecto
 {
   if (t == elem::f32) {
     score_rows_m<L>(qv, static_cast<const float*>(vectors), dim, metric, rid, key, from, to);
+  } else if (t == elem::bf16) {
+    score_rows_m<L>(qv, static_cast<const __bf16*>(vectors), dim, metric, rid, key, from, to);
   } else {
     score_rows_m<L>(qv, static_cast<const _Float16*>(vectors), dim, metric, rid, key, from, to);
   }

@@ -15,11 +15,17 @@ import torch
 from . import _capi as C
 
 METRICS = ("l2", "cosine", "ip")
-_DTYPES = {torch.float32: "float32", torch.float16: "float16", torch.int8: "int8", torch.uint8: "uint8"}
+_DTYPES = {
+    torch.float32: "float32",
+    torch.float16: "float16",
+    torch.bfloat16: "bfloat16",  # an addition of this build: bfloat16 vectors kept exactly
+    torch.int8: "int8",
+    torch.uint8: "uint8",
+}
 _TORCH = {v: k for k, v in _DTYPES.items()}
 _METRIC_C = {"l2": C.L2Expanded, "cosine": C.CosineExpanded, "ip": C.InnerProduct}
 _METRIC_PY = {v: k for k, v in _METRIC_C.items()}
-_PREFIX = {b"f4": "float32", b"f2": "float16", b"i1": "int8", b"u1": "uint8"}
+_PREFIX = {b"f4": "float32", b"f2": "float16", b"b2": "bfloat16", b"i1": "int8", b"u1": "uint8"}
 
 
 def row_len(m):
@@ -211,9 +217,13 @@ class _Core:
     @property
     def dtype(self):
         d = self.h.contents.dtype
-        return {(C.kDLFloat, 32): "float32", (C.kDLFloat, 16): "float16", (C.kDLInt, 8): "int8", (C.kDLUInt, 8): "uint8"}[
-            (d.code, d.bits)
-        ]
+        return {
+            (C.kDLFloat, 32): "float32",
+            (C.kDLFloat, 16): "float16",
+            (C.kDLBfloat, 16): "bfloat16",
+            (C.kDLInt, 8): "int8",
+            (C.kDLUInt, 8): "uint8",
+        }[(d.code, d.bits)]
 
 
 class Index:

@@ -67,7 +67,7 @@ def test_errors_become_status_and_text():
         C.check(L.cuvsCertexIndexGetSize(h, ctypes.byref(size)))
     h.contents.dtype = C.DLDataType(C.kDLFloat, 64, 1)
     assert L.cuvsCertexIndexGetDim(h, ctypes.byref(size)) == C.CUVS_ERROR
-    assert b"float32, float16, int8, or uint8" in L.cuvsGetLastErrorText()
+    assert b"float32, float16, bfloat16, int8, or uint8" in L.cuvsGetLastErrorText()
     # a successful call clears the text
     C.check(L.cuvsCertexStatsBegin())
     assert L.cuvsGetLastErrorText() is None
