@@ -26,11 +26,18 @@ import torch
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-P_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA peak, 10^12 ops/s
+P_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA peak, 10^12 ops/s (256 CUs at 2.4 GHz)
+PEAK_CLOCK_MHZ = 2400.0  # the shader clock the datasheet peaks assume
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "screen_i8_c2_traffic.txt")
-# the sources that decide the int8 screen's memory traffic; a traffic profile is stamped with their
-# hash and is used only while they are unchanged
+# the sources that decide a screen's memory traffic; a traffic profile is stamped with their hash
+# and is used only while they are unchanged
 SCREEN_I8_SOURCES = ("kernels/screen.hip", "kernels/screen_common.hpp", "kernels.hpp")
+# every kernel source: the stamp of the config 3 and 4 counter profiles
+KERNEL_SOURCES = ("kernels/screen.hip", "kernels/screen_tile.hip", "kernels/screen_wide.hip",
+                  "kernels/screen_common.hpp", "kernels/select.hip", "kernels/encode.hip",
+                  "kernels/partition.hip", "kernels/lists.hip", "kernels.hpp")
+PROFILE_C3 = os.path.join(ROOT, "profiles", "screen_f16_c3_counters.txt")
+PROFILE_C4 = os.path.join(ROOT, "profiles", "screen_f16_c4_counters.txt")
 
 
 def sources_stamp(files=SCREEN_I8_SOURCES):
@@ -44,20 +51,48 @@ def sources_stamp(files=SCREEN_I8_SOURCES):
     return h.hexdigest()[:16]
 
 
-def screen_traffic():
-    """HBM bytes per screen launch at config 2, from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (calibrated against a plain copy). None when the summary is missing or was
-    measured on other screen sources than the ones built here (its sources stamp differs)."""
+def profile_traffic(path=TRAFFIC_PROFILE, kernel=None, files=SCREEN_I8_SOURCES):
+    """HBM bytes per launch of a kernel from a committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (calibrated against a plain copy): its line `traffic_bytes_per_launch <kernel> = N` (the first
+    such line when kernel is None). None when the summary is missing or was measured on other
+    sources than the ones built here (its `sources_stamp` line differs from the stamp of `files`)."""
     stamp, traffic = None, None
     try:
-        for line in open(TRAFFIC_PROFILE):
+        for line in open(path):
             if line.startswith("sources_stamp"):
                 stamp = line.split("=")[1].strip()
-            if line.startswith("traffic_bytes_per_launch"):
-                traffic = int(line.split("=")[1])
+            if line.startswith("traffic_bytes_per_launch") and traffic is None:
+                name = line.split("=")[0][len("traffic_bytes_per_launch"):].strip()
+                if kernel is None or name.startswith(kernel):
+                    traffic = int(line.split("=")[1])
     except OSError:
         return None
-    return traffic if stamp == sources_stamp() else None
+    return traffic if stamp == sources_stamp(files) else None
+
+
+def screen_traffic():
+    """HBM bytes per int8 screen launch at config 2 (profiles/screen_i8_c2_traffic.txt)."""
+    return profile_traffic()
+
+
+def shader_clock_mhz():
+    """Average shader clock (MHz) of the screen workgroups of the last timed region, as the
+    kernels read it (s_memtime cycles over s_memrealtime time); None if no screen ran."""
+    from libcertex_amd import _capi as C
+
+    mhz = ctypes.c_double(0)
+    C.check(C.lib().cuvsCertexTimingShaderClock(ctypes.byref(mhz)))
+    return round(mhz.value, 1) if mhz.value > 0 else None
+
+
+def clock_fields(achieved, peak):
+    """The screen's shader clock and its fraction of the peak scaled to that clock (the datasheet
+    peak assumes 2.4 GHz): what the line's frac leaves to the clock, and what to the kernel."""
+    mhz = shader_clock_mhz()
+    if mhz is None:
+        return {"shader_clock_mhz": None}
+    return {"shader_clock_mhz": mhz,
+            "frac_of_peak_at_clock": round(achieved / (peak * mhz / PEAK_CLOCK_MHZ), 4)}
 P_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA peak
 HBM_GBS = 8000.0
 
@@ -143,17 +178,18 @@ def hbm_roofline(kernel, bytes_per_launch, ms_per_launch, what):
             "avg_launch_ms": round(ms_per_launch, 4), "bytes": what}
 
 
-def float_phase_rooflines(ms, launches, steps, st, nq, d, k, elem):
+def float_phase_rooflines(ms, launches, steps, st, nq, d, k, elem, traffic=None):
     """Verify roofline of a float search (one batch per step): the verify reads every survivor's
-    bucket entry (row and screen value), the query and the vectors of the rows it scores."""
+    bucket entry (row and screen value), the query and the vectors of the rows it scores, `elem`
+    bytes per coordinate (the index's vector type: 4 for float32, 2 for bfloat16 or float16)."""
     v_ms = ms[3] / max(1, launches[3])
     per_launch = max(1, launches[3] // steps)
-    return {
-        "verify_topk": hbm_roofline(
-            "verify_topk_f_kernel", (st.verified * d * elem + st.survivors * 8 + nq * d * elem) / per_launch,
-            v_ms, f"{st.verified / max(1, st.queries):.1f} scored vectors of {d} x {elem} B and "
-            f"{st.survivors / max(1, st.queries):.1f} bucket entries of 8 B, per query"),
-    }
+    r = hbm_roofline(
+        "verify_topk_f_kernel", (st.verified * d * elem + st.survivors * 8 + nq * d * elem) / per_launch,
+        v_ms, f"{st.verified / max(1, st.queries):.1f} scored vectors of {d} x {elem} B and "
+        f"{st.survivors / max(1, st.queries):.1f} bucket entries of 8 B, per query")
+    r["traffic"] = traffic
+    return {"verify_topk": r}
 
 
 def bench_config3(args):
@@ -184,6 +220,9 @@ def bench_config3(args):
     torch.cuda.synchronize()
     halves = (d + 127) // 128 * 128
     screen_ms = ms[2] / max(1, launches[2])
+    elem = idx.dtype.itemsize
+    # the committed counter profile holds the default workload's traffic
+    default = (n, d, nq, k, batch) == (1_000_000, 768, 10_000, 100, 10_000)
     # algorithmic work of the label-routed screen: every query against the rows of its label
     per_label = torch.bincount(lx.long(), minlength=16)
     pairs = float(per_label[lq.long()].sum().item())
@@ -220,13 +259,17 @@ def bench_config3(args):
             "launches_per_step": {p: launches[i] // args.steps for i, p in enumerate(PHASES)},
             "survivors_per_query": round(st.survivors / max(1, st.queries), 2),
             "verified_per_query": round(st.verified / max(1, st.queries), 2),
-            "phase_rooflines": float_phase_rooflines(ms, launches, args.steps, st, nq, d, k, 4),
+            "phase_rooflines": float_phase_rooflines(
+                ms, launches, args.steps, st, nq, d, k, elem,
+                profile_traffic(PROFILE_C3, "verify_topk_f_kernel", KERNEL_SOURCES) if default else None),
         },
         "roofline": {
             "bound": "mfma", "kernel": "screen_tile_kernel (fp16 MFMA screen, LDS-staged 256-row x 128-query tiles, two workgroups per CU, label-routed)",
             "achieved": round(achieved, 2), "peak": P_FP16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / P_FP16_TFLOPS, 4), "traffic": None,
+            "frac": round(achieved / P_FP16_TFLOPS, 4),
+            "traffic": profile_traffic(PROFILE_C3, "screen_tile_kernel", KERNEL_SOURCES) if default else None,
             "avg_launch_ms": round(screen_ms, 4), "flops_per_launch": flops_per_launch,
+            **clock_fields(achieved, P_FP16_TFLOPS),
         },
         "cpu_baseline": cpu,
     }
@@ -285,6 +328,8 @@ def bench_config4(args):
     flops_per_step = 2.0 * n_q * keys_avg * ((d + 127) // 128 * 128)
     screen_ms_step = ms[2] / args.steps
     achieved = flops_per_step / (screen_ms_step / 1000.0) / 1e12
+    elem = cache.index.dtype.itemsize  # bfloat16 keys: 2 bytes per coordinate
+    default = (n, d, k) == (131_072, 128, 2048)
     return {
         "metric": "exact top-2048 attention queries/sec, 8 KV heads x 131k keys, GQA 4:1, 1 MI355X",
         "value": round(n_q / (ms_step / 1000.0), 1),
@@ -305,13 +350,17 @@ def bench_config4(args):
             "launches_per_step": {p: launches[i] // args.steps for i, p in enumerate(PHASES)},
             "survivors_per_query": round(st.survivors / max(1, st.queries), 2),
             "verified_per_query": round(st.verified / max(1, st.queries), 2),
-            "phase_rooflines": float_phase_rooflines(ms, launches, args.steps, st, n_q, d, k, 4),
+            "phase_rooflines": float_phase_rooflines(
+                ms, launches, args.steps, st, n_q, d, k, elem,
+                profile_traffic(PROFILE_C4, "verify_topk_f_kernel", KERNEL_SOURCES) if default else None),
         },
         "roofline": {
             "bound": "mfma", "kernel": "screen_kernel<f16_rows,4,...> (fp16 MFMA screen, label-routed, + tail)",
             "achieved": round(achieved, 2), "peak": P_FP16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / P_FP16_TFLOPS, 4), "traffic": None,
+            "frac": round(achieved / P_FP16_TFLOPS, 4),
+            "traffic": profile_traffic(PROFILE_C4, "screen_kernel<f16_rows", KERNEL_SOURCES) if default else None,
             "screen_ms_per_step": round(screen_ms_step, 4), "flops_per_step": flops_per_step,
+            **clock_fields(achieved, P_FP16_TFLOPS),
         },
         "cpu_baseline": cpu,
     }
@@ -441,6 +490,7 @@ def bench_config5(args):
             "achieved": round(achieved, 2), "peak": P_INT8_TOPS, "unit": "TOP/s",
             "frac": round(achieved / P_INT8_TOPS, 4), "traffic": None,
             "avg_launch_ms": round(screen_ms, 4), "ops_per_launch": ops_per_launch,
+            **clock_fields(achieved, P_INT8_TOPS),
         },
         "cpu_baseline": None,
     }
@@ -642,6 +692,7 @@ def main():
     batches = (nq + args.batch - 1) // args.batch
     ops_per_launch = 2.0 * n * d * nq / batches
     achieved = ops_per_launch / (screen_ms / 1000.0) / 1e12
+    clock = clock_fields(achieved, P_INT8_TOPS)
     phase_ms = {
         name: round(ms[i] / args.steps, 4) for i, name in enumerate(("anchors", "threshold", "screen", "verify_topk"))
     }
@@ -700,6 +751,7 @@ def main():
             if (n, d, nq, args.batch, n_lists, args.probe) == (10_000_000, 128, 10_000, 10_000, 4096, 0) else None,
             "avg_launch_ms": round(screen_ms, 4),
             "ops_per_launch": ops_per_launch,
+            **clock,
         },
         "cpu_baseline": cpu,
     }

@@ -117,8 +117,10 @@ CUVS_EXPORT cuvsError_t cuvsCertexSearch(cuvsResources_t res,
  * harnesses that forbid hipMalloc). Same arguments, checks and results as cuvsCertexSearch. The
  * scratch is one fixed 128 MiB device array per GPU, held from the library's load on that GPU
  * until the process ends; larger batches are split into smaller ones, and a search that needs more
- * than 128 MiB for a single query returns CUVS_ERROR. Calls that overlap on one GPU (from several
- * threads or streams) share that array and race: issue them one at a time per GPU.
+ * than 128 MiB for a single query returns CUVS_ERROR. Calls on one GPU share that array and take
+ * turns: a call waits on the host for the previous call to return, and its stream waits on the GPU
+ * (an event, no host sync) for the previous call's last kernel, whatever stream or resources that
+ * call used. The array keeps the previous call's contents; each call clears what must start at 0.
  */
 CUVS_EXPORT cuvsError_t cuvsCertexSearchNoAlloc(cuvsResources_t res,
                                                 cuvsCertexSearchParams_t params,
@@ -218,6 +220,26 @@ CUVS_EXPORT cuvsError_t cuvsCertexTimingBegin(void);
 /** Stop recording; waits for the recorded events and returns per phase the summed kernel time in
  *  milliseconds and the number of launches (arrays of CERTEX_N_PHASES). */
 CUVS_EXPORT cuvsError_t cuvsCertexTimingEnd(double* ms, int64_t* launches);
+/** The average shader clock in MHz of the screen workgroups timed between the last
+ *  cuvsCertexTimingBegin and cuvsCertexTimingEnd: each workgroup's life in shader clock cycles
+ *  (s_memtime) over its life in real time (s_memrealtime, 100 MHz), summed over the workgroups;
+ *  0 if no screen ran. The clock the card sustained on this work, next to its 2.4 GHz peak. */
+CUVS_EXPORT cuvsError_t cuvsCertexTimingShaderClock(double* mhz);
+
+/**
+ * Free the scratch memory that searches on `res` have grown (device buffers and pinned host
+ * staging), after waiting for its stream; later searches grow it again. The counterpart of the
+ * reference's Python trim_pool (certex/index.py:165-169), which returns the unused memory of the
+ * device's stream-ordered pool.
+ */
+CUVS_EXPORT cuvsError_t cuvsCertexTrimPool(cuvsResources_t res);
+
+/**
+ * Testing only, no counterpart in the reference: every scratch request of searches on `res` above
+ * `bytes` fails as an allocation failure would, so that tests can exercise the batch halving
+ * (reference certex.cu:1477-1502). 0 removes the cap.
+ */
+CUVS_EXPORT cuvsError_t cuvsCertexTestScratchCap(cuvsResources_t res, int64_t bytes);
 
 #ifdef __cplusplus
 }

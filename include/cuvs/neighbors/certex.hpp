@@ -38,6 +38,13 @@ class resources {
   void set_stream(void* stream);
   [[nodiscard]] auto device() const -> int;
   void sync() const;
+  /** Free the scratch memory that the searches on these resources have grown (device slots and
+   *  pinned host staging), after waiting for the stream; later searches grow it again. The
+   *  counterpart of the reference's trim_pool (certex/index.py:165-169). */
+  void trim() const;
+  /** Testing only (no counterpart in the reference): a scratch request above `bytes` fails as an
+   *  allocation failure would, so that the search's batch halving can be exercised; 0 = no cap. */
+  void set_scratch_cap(size_t bytes) const;
   [[nodiscard]] auto state() const -> detail::resources_state&;
 
  private:
@@ -123,6 +130,9 @@ struct kernel_times {
 };
 void timing_begin();
 auto timing_end() -> kernel_times;
+/** Average shader clock (MHz) of the screen workgroups timed between the last timing_begin() and
+ *  timing_end(): their lives in shader clock cycles over their lives in real time; 0 if none. */
+auto timing_shader_clock_mhz() -> double;
 
 namespace detail {
 struct index_state;
@@ -209,8 +219,9 @@ void search(cuvs::resources const& res, search_params const& params, index<T> co
  * The search above, with no device or pinned memory allocated during the call (no counterpart in
  * the reference; for callers that cannot allocate, such as tight serving loops). Its scratch is a
  * fixed array of no_alloc_scratch_bytes() (128 MiB) per GPU, held from the library's load on that
- * GPU until the process ends; batches that need more are split. Calls that overlap on one GPU
- * share that array and race: run one at a time per GPU. Throws when a single query needs more.
+ * GPU until the process ends; batches that need more are split. Calls on one GPU take turns on
+ * that array: on the host by a lock, and on the GPU by an event that each call's stream waits for
+ * and records again after its last kernel. Throws when a single query needs more.
  */
 template <typename T>
 void search_without_allocation(cuvs::resources const& res, search_params const& params,

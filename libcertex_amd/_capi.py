@@ -163,6 +163,9 @@ def lib():
                     "cuvsCertexIndexListOrder": [ctypes.c_size_t, P(IndexHandle), P(DLManagedTensor)],
                     "cuvsCertexStatsBegin": [],
                     "cuvsCertexStatsEnd": [P(i64), P(i64), P(i64)],
+                    "cuvsCertexTimingShaderClock": [P(ctypes.c_double)],
+                    "cuvsCertexTrimPool": [ctypes.c_size_t],
+                    "cuvsCertexTestScratchCap": [ctypes.c_size_t, i64],
                     "cuvsCertexTimingBegin": [],
                     "cuvsCertexTimingEnd": [P(ctypes.c_double), P(i64)],
                 }

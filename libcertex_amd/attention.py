@@ -33,10 +33,26 @@ def _keys(x):
     return h if bool(torch.isfinite(h).all()) else x.to(torch.float32)
 
 
+def _queries(q, dtype):
+    """Queries in the cache's vector type, rounded to nearest as the reference rounds them
+    (certex/attention.py:97, `.to(self.dtype)`): the top k is then exact for the rounded queries.
+    Queries are converted once from the type they come in (float32 queries against bfloat16 keys
+    are not rounded to float16 first). A finite value that the cache's type overflows is an error."""
+    x = torch.as_tensor(q, device="cuda")
+    if x.dtype == dtype:
+        return x
+    y = x.to(dtype)
+    _require(
+        bool((torch.isfinite(y) | ~torch.isfinite(x)).all()),
+        f"these queries overflow the cache's {dtype} keys: start the cache with float32 keys",
+    )
+    return y
+
+
 def _fit(x, dtype, what):
-    """x in the cache's vector type; a conversion that would change a value (float32 or bfloat16
+    """Keys in the cache's vector type; a conversion that would change a key (float32 or bfloat16
     values that float16 rounds or overflows, float32 or float16 values that bfloat16 rounds) is an
-    error rather than a silent rounding."""
+    error rather than a silent rounding of the cache."""
     if x.dtype == dtype:
         return x
     y = x.to(dtype)
@@ -124,7 +140,7 @@ class KeyCache:
         _require(self.index is not None, "the cache is empty: append keys first")
         k = self.k if k is None else int(k)
         _require(1 <= k <= min(2048, self.size), f"k must be between 1 and {min(2048, self.size)}, not {k}")
-        Q = _keys(q)
+        Q = _queries(q, self.dtype)
         single = Q.ndim == 2
         if single:
             Q = Q[:, None, :]
@@ -141,7 +157,7 @@ class KeyCache:
             self._labels[key] = (torch.arange(H, dtype=torch.int32) // r).repeat_interleave(m)
         labels = self._labels[key]
         D, I = self.index.search(
-            _fit(Q, self.dtype, "queries").reshape(H * m, d), k=k, batch=batch or max(2048, H * m), labels=labels
+            Q.reshape(H * m, d), k=k, batch=batch or max(2048, H * m), labels=labels
         )
         scores = D.reshape(H, m, k)
         ids = self.local[I].reshape(H, m, k)

@@ -651,6 +651,27 @@ cuvsError_t cuvsCertexStatsEnd(int64_t* queries, int64_t* survivors, int64_t* ve
   });
 }
 
+cuvsError_t cuvsCertexTimingShaderClock(double* mhz)
+{
+  return translate([=] {
+    certex::expects(mhz != nullptr, "certex: NULL output");
+    *mhz = certex::timing_shader_clock_mhz();
+  });
+}
+
+cuvsError_t cuvsCertexTrimPool(cuvsResources_t res)
+{
+  return translate([=] { res_of(res).trim(); });
+}
+
+cuvsError_t cuvsCertexTestScratchCap(cuvsResources_t res, int64_t bytes)
+{
+  return translate([=] {
+    certex::expects(bytes >= 0, "certex: the scratch cap must not be negative");
+    res_of(res).set_scratch_cap(size_t(bytes));
+  });
+}
+
 cuvsError_t cuvsCertexTimingBegin(void)
 {
   return translate([] { certex::timing_begin(); });

@@ -32,9 +32,6 @@ resources::resources(void* stream) : s_(std::make_unique<detail::resources_state
   CERTEX_HIP_TRY(hipHostMalloc(&s_->host_small, 64, hipHostMallocDefault));
   CERTEX_HIP_TRY(hipEventCreateWithFlags(&s_->read_back, hipEventDisableTiming));
   CERTEX_HIP_TRY(hipEventCreateWithFlags(&s_->staged, hipEventDisableTiming));
-  if (const char* cap = std::getenv("CERTEX_SCRATCH_SLOT_CAP")) {
-    s_->slot_cap = size_t(std::strtoull(cap, nullptr, 10));
-  }
 }
 
 resources::~resources()
@@ -66,6 +63,23 @@ auto resources::device() const -> int { return s_->device; }
 
 void resources::sync() const { CERTEX_HIP_TRY(hipStreamSynchronize(s_->stream)); }
 
+void resources::trim() const
+{
+  if (s_->arena != nullptr) {
+    throw std::logic_error("certex: trim during a search without allocation on these resources");
+  }
+  CERTEX_HIP_TRY(hipStreamSynchronize(s_->stream));
+  for (auto& b : s_->slots) { b.release(); }
+  if (s_->host_stage != nullptr) {
+    CERTEX_HIP_TRY(hipHostFree(s_->host_stage));
+    s_->host_stage       = nullptr;
+    s_->host_stage_bytes = 0;
+    s_->staged_pending   = false;
+  }
+}
+
+void resources::set_scratch_cap(size_t bytes) const { s_->slot_cap = bytes; }
+
 auto resources::state() const -> detail::resources_state& { return *s_; }
 
 }  // namespace cuvs
@@ -77,9 +91,12 @@ namespace {
 thread_local bool t_stats_on = false;
 thread_local search_stats t_stats{};
 
-/** Event pairs around the kernels of the calling thread's searches while timing is on. */
+/** Event pairs around the kernels of the calling thread's searches while timing is on, and the
+ *  shader clock counters of the timed screens (two device words, cycles and 100 MHz ticks). */
 struct timing_state {
   bool on = false;
+  unsigned long long* clock = nullptr;
+  double clock_mhz          = 0;
   struct mark {
     int phase;
     hipEvent_t start, stop;
@@ -495,7 +512,9 @@ bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, 
     sa.cand_count  = count;
     sa.cand_rows   = rows;
     sa.cap         = cap;
+    sa.clock = t_timing.on ? t_timing.clock : nullptr;
     timed(2, stream, [&] { screen(sa, stream); });
+    sa.clock = nullptr;
     certex_amd::max_u32(count, B, small, stream);
     CERTEX_HIP_TRY(hipMemcpyAsync(rs.host_small, small, 8, hipMemcpyDeviceToHost, stream));
     CERTEX_HIP_TRY(hipEventRecord(rs.read_back, stream));
@@ -1214,8 +1233,13 @@ static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 char* g_scratch[kMaxDevices] = {};
+/** Per GPU: held by the search that uses the scratch array, from its first launch to its last. */
+std::mutex g_scratch_use[kMaxDevices];
+/** Per GPU: recorded after the last launch of the latest search on the scratch array. */
+hipEvent_t g_scratch_done[kMaxDevices] = {};
 
-/** The device address of `device`'s scratch array, looked up once per device with it current. */
+/** The device address of `device`'s scratch array, looked up once per device with it current
+ * (the event that orders its users is created at the same time). */
 auto scratch_of(int device) -> char*
 {
   expects(device >= 0 && device < kMaxDevices, "certex: device ordinal out of range");
@@ -1224,15 +1248,36 @@ auto scratch_of(int device) -> char*
     int current = 0;
     CERTEX_HIP_TRY(hipGetDevice(&current));
     if (current != device) { CERTEX_HIP_TRY(hipSetDevice(device)); }
-    void* ptr             = nullptr;
-    const hipError_t err  = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    void* ptr            = nullptr;
+    hipError_t err       = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    hipEvent_t done      = nullptr;
+    if (err == hipSuccess) { err = hipEventCreateWithFlags(&done, hipEventDisableTiming); }
     if (current != device) { CERTEX_HIP_TRY(hipSetDevice(current)); }
     CERTEX_HIP_TRY(err);
     expects(ptr != nullptr, "certex: no device address for the scratch array");
-    g_scratch[device] = static_cast<char*>(ptr);
+    g_scratch_done[device] = done;
+    g_scratch[device]      = static_cast<char*>(ptr);
   }
   return g_scratch[device];
 }
+
+/**
+ * Exclusive use of one GPU's scratch array for one search. The host lock orders the calls; on the
+ * GPU, the search's stream first waits for the event recorded after the previous search's last
+ * launch (on whatever stream that ran), and the event is recorded again after this search's last
+ * launch. So searches on different streams or resources never overlap on the array, even though
+ * each call returns with its last kernels still queued.
+ */
+struct scratch_turn {
+  int device;
+  hipStream_t stream;
+  std::unique_lock<std::mutex> lk;
+  scratch_turn(int dev, hipStream_t s) : device(dev), stream(s), lk(g_scratch_use[dev])
+  {
+    CERTEX_HIP_TRY(hipStreamWaitEvent(stream, g_scratch_done[device], 0));
+  }
+  ~scratch_turn() { (void)hipEventRecord(g_scratch_done[device], stream); }
+};
 
 /** Arena mode of the resources for the duration of one call (restored on every exit). */
 struct arena_scope {
@@ -1269,6 +1314,7 @@ void search_without_allocation(cuvs::resources const& res, search_params const& 
     fa.bitmap_ld = idx.size();
   }
   char* base = scratch_of(res.device());
+  scratch_turn turn(res.device(), static_cast<hipStream_t>(res.stream()));
   arena_scope scope(res.state(), base, kNoAllocScratchBytes);
   try {
     search_impl(res, params, idx, queries, neighbors, distances, k, fa, true);
@@ -1293,6 +1339,13 @@ auto stats_end() -> search_stats
 
 void timing_begin()
 {
+  if (t_timing.clock == nullptr) {
+    CERTEX_HIP_TRY(hipMalloc(&t_timing.clock, 2 * sizeof(unsigned long long)));
+  }
+  CERTEX_HIP_TRY(hipDeviceSynchronize());
+  CERTEX_HIP_TRY(hipMemset(t_timing.clock, 0, 2 * sizeof(unsigned long long)));
+  CERTEX_HIP_TRY(hipDeviceSynchronize());
+  t_timing.clock_mhz = 0;
   t_timing.on = true;
   for (auto& m : t_timing.marks) {
     t_timing.pool.push_back(m.start);
@@ -1315,8 +1368,17 @@ auto timing_end() -> kernel_times
     t_timing.pool.push_back(m.stop);
   }
   t_timing.marks.clear();
+  if (t_timing.clock != nullptr) {
+    CERTEX_HIP_TRY(hipDeviceSynchronize());
+    unsigned long long c[2] = {};
+    CERTEX_HIP_TRY(hipMemcpy(c, t_timing.clock, sizeof(c), hipMemcpyDeviceToHost));
+    // s_memrealtime counts at a constant 100 MHz
+    t_timing.clock_mhz = c[1] > 0 ? double(c[0]) / double(c[1]) * 100.0 : 0.0;
+  }
   return out;
 }
+
+auto timing_shader_clock_mhz() -> double { return t_timing.clock_mhz; }
 
 template <typename T>
 index<T>::index(cuvs::resources const& res) : s_(std::make_unique<index_state>())
@@ -1846,27 +1908,85 @@ auto get(std::istream& is) -> V
   return v;
 }
 
-void put_device(std::ostream& os, cuvs::resources const& res, const void* p, size_t bytes)
-{
-  std::vector<char> h(bytes);
-  if (bytes > 0) {
-    CERTEX_HIP_TRY(hipMemcpyAsync(h.data(), p, bytes, hipMemcpyDefault,
-                                  static_cast<hipStream_t>(res.stream())));
-    res.sync();
+/**
+ * Two pinned host buffers of at most 64 MiB through which the arrays of an index move between the
+ * device and a file, chunk by chunk: the copy of one chunk overlaps the file I/O of the other,
+ * and host memory stays bounded whatever the size of the index (a 10^9-row index holds 128 GB
+ * of rows).
+ */
+struct io_staging {
+  static constexpr size_t kChunk = size_t(64) << 20;
+  hipStream_t stream;
+  size_t chunk     = 0;
+  void* buf[2]     = {};
+  hipEvent_t ev[2] = {};
+  bool pending[2]  = {};
+  io_staging(cuvs::resources const& res, size_t largest)
+    : stream(static_cast<hipStream_t>(res.stream())), chunk(std::min(kChunk, std::max<size_t>(largest, size_t(1) << 20)))
+  {
+    for (int i = 0; i < 2; ++i) {
+      CERTEX_HIP_TRY(hipHostMalloc(&buf[i], chunk, hipHostMallocDefault));
+      CERTEX_HIP_TRY(hipEventCreateWithFlags(&ev[i], hipEventDisableTiming));
+    }
   }
-  os.write(h.data(), std::streamsize(bytes));
-}
-void get_device(std::istream& is, cuvs::resources const& res, void* p, size_t bytes)
-{
-  std::vector<char> h(bytes);
-  is.read(h.data(), std::streamsize(bytes));
-  expects(bool(is) || bytes == 0, "certex: the index file is truncated");
-  if (bytes > 0) {
-    CERTEX_HIP_TRY(hipMemcpyAsync(p, h.data(), bytes, hipMemcpyDefault,
-                                  static_cast<hipStream_t>(res.stream())));
-    res.sync();
+  ~io_staging()
+  {
+    (void)hipStreamSynchronize(stream);
+    for (int i = 0; i < 2; ++i) {
+      if (buf[i] != nullptr) { (void)hipHostFree(buf[i]); }
+      if (ev[i] != nullptr) { (void)hipEventDestroy(ev[i]); }
+    }
   }
-}
+  io_staging(io_staging const&)            = delete;
+  io_staging& operator=(io_staging const&) = delete;
+  void wait(int i)
+  {
+    if (pending[i]) { CERTEX_HIP_TRY(hipEventSynchronize(ev[i])); }
+    pending[i] = false;
+  }
+  void copy(int i, void* dst, const void* src, size_t bytes)
+  {
+    CERTEX_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, stream));
+    CERTEX_HIP_TRY(hipEventRecord(ev[i], stream));
+    pending[i] = true;
+  }
+
+  /** Write `bytes` of device (or mapped host) memory at `p` to the file. */
+  void put(std::ostream& os, const void* p, size_t bytes)
+  {
+    const char* src  = static_cast<const char*>(p);
+    const size_t n   = (bytes + chunk - 1) / chunk;
+    auto len         = [&](size_t c) { return std::min(chunk, bytes - c * chunk); };
+    if (n > 0) { copy(0, buf[0], src, len(0)); }
+    for (size_t c = 0; c < n; ++c) {
+      const int b = int(c & 1);
+      if (c + 1 < n) {
+        wait(b ^ 1);  // its chunk went to the file in the previous iteration
+        copy(b ^ 1, buf[b ^ 1], src + (c + 1) * chunk, len(c + 1));
+      }
+      wait(b);
+      os.write(static_cast<const char*>(buf[b]), std::streamsize(len(c)));
+    }
+  }
+
+  /** Read `bytes` from the file into device (or mapped host) memory at `p`; the stream is
+   *  synchronised before this returns. */
+  void get(std::istream& is, void* p, size_t bytes)
+  {
+    char* dst      = static_cast<char*>(p);
+    const size_t n = (bytes + chunk - 1) / chunk;
+    for (size_t c = 0; c < n; ++c) {
+      const int b      = int(c & 1);
+      const size_t len = std::min(chunk, bytes - c * chunk);
+      wait(b);  // the copy of chunk c - 2 out of this buffer is done
+      is.read(static_cast<char*>(buf[b]), std::streamsize(len));
+      expects(bool(is), "certex: the index file is truncated");
+      copy(b, dst + c * chunk, buf[b], len);
+    }
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+    pending[0] = pending[1] = false;
+  }
+};
 
 }  // namespace
 
@@ -1895,22 +2015,23 @@ void serialize(cuvs::resources const& res, std::string const& filename, index<T>
   put(os, int32_t(st.halves));
   put(os, uint8_t(st.normalize));
   const size_t n = size_t(st.size);
-  put_device(os, res, st.codes.p, n * st.row_bytes);
-  put_device(os, res, st.rowc.p, n * 4);
+  io_staging io(res, n * std::max<size_t>(st.row_bytes, size_t(st.dim) * elem_size(st.type)));
+  io.put(os, st.codes.p, n * st.row_bytes);
+  io.put(os, st.rowc.p, n * 4);
   if (!is_int(st.type)) {
-    put_device(os, res, st.vectors.p, n * size_t(st.dim) * elem_size(st.type));
-    put_device(os, res, st.center.p, size_t(st.dim) * sizeof(double));
-    put_device(os, res, st.maxima.p, 2 * sizeof(double));
+    io.put(os, st.vectors.p, n * size_t(st.dim) * elem_size(st.type));
+    io.put(os, st.center.p, size_t(st.dim) * sizeof(double));
+    io.put(os, st.maxima.p, 2 * sizeof(double));
   }
-  if (st.has_labels) { put_device(os, res, st.labels.p, n * sizeof(int32_t)); }
+  if (st.has_labels) { io.put(os, st.labels.p, n * sizeof(int32_t)); }
   put(os, int32_t(st.n_lists));
   if (st.n_lists > 0) {
     put(os, int64_t(st.n_listed));
     put(os, int32_t(st.list_width));
     os.write(reinterpret_cast<const char*>(st.list_offsets.data()),
              std::streamsize(st.list_offsets.size() * 8));
-    put_device(os, res, st.row_ids.p, size_t(st.n_listed) * 4);
-    put_device(os, res, st.centers.p, size_t(st.n_lists) * st.list_width * 4);
+    io.put(os, st.row_ids.p, size_t(st.n_listed) * 4);
+    io.put(os, st.centers.p, size_t(st.n_lists) * st.list_width * 4);
   }
   expects(os.good(), "certex: writing the index file failed");
 }
@@ -1947,18 +2068,19 @@ void deserialize(cuvs::resources const& res, std::string const& filename, index<
   st.size     = 0;
   st.capacity = 0;
   grow(res, st, std::max<int64_t>(n, 1));
-  get_device(is, res, st.codes.p, size_t(n) * st.row_bytes);
-  get_device(is, res, st.rowc.p, size_t(n) * 4);
+  io_staging io(res, size_t(n) * std::max<size_t>(st.row_bytes, size_t(st.dim) * elem_size(st.type)));
+  io.get(is, st.codes.p, size_t(n) * st.row_bytes);
+  io.get(is, st.rowc.p, size_t(n) * 4);
   if (!is_int(st.type)) {
     st.center.resize_discard(size_t(st.dim) * sizeof(double));
     st.maxima.resize_discard(2 * sizeof(double));
-    get_device(is, res, st.vectors.p, size_t(n) * size_t(st.dim) * elem_size(st.type));
-    get_device(is, res, st.center.p, size_t(st.dim) * sizeof(double));
-    get_device(is, res, st.maxima.p, 2 * sizeof(double));
+    io.get(is, st.vectors.p, size_t(n) * size_t(st.dim) * elem_size(st.type));
+    io.get(is, st.center.p, size_t(st.dim) * sizeof(double));
+    io.get(is, st.maxima.p, 2 * sizeof(double));
   }
   if (labels) {
     st.labels.resize_discard(size_t(st.capacity) * sizeof(int32_t));
-    get_device(is, res, st.labels.p, size_t(n) * sizeof(int32_t));
+    io.get(is, st.labels.p, size_t(n) * sizeof(int32_t));
     st.has_labels = true;
   }
   const int32_t L = get<int32_t>(is);
@@ -1977,8 +2099,8 @@ void deserialize(cuvs::resources const& res, std::string const& filename, index<
     st.centers.resize_discard(size_t(L) * st.list_width * 4);
     st.centers_q.resize_discard(size_t(Lp) * st.row_bytes);
     st.cterm.resize_discard(size_t(Lp) * 4);
-    get_device(is, res, st.row_ids.p, size_t(st.n_listed) * 4);
-    get_device(is, res, st.centers.p, size_t(L) * st.list_width * 4);
+    io.get(is, st.row_ids.p, size_t(st.n_listed) * 4);
+    io.get(is, st.centers.p, size_t(L) * st.list_width * 4);
     hipStream_t stream = static_cast<hipStream_t>(res.stream());
     certex_amd::invert_ids(st.row_ids.as<int32_t>(), st.n_listed, st.id_rows.as<int32_t>(), stream);
     certex_amd::finish_centers(nullptr, nullptr, L, Lp, st.list_width, !is_int(st.type),

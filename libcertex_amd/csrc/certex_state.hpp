@@ -133,8 +133,8 @@ struct resources_state {
   size_t host_stage_bytes = 0;
   hipEvent_t staged   = nullptr;  // recorded behind the last copy out of host_stage
   bool staged_pending = false;    // `staged` has been recorded
-  // test hook: a slot request above this many bytes fails as an allocation failure would
-  // (environment variable CERTEX_SCRATCH_SLOT_CAP, read when the resources are created; 0 = none)
+  // testing only: a slot request above this many bytes fails as an allocation failure would
+  // (resources::set_scratch_cap, C cuvsCertexTestScratchCap; 0 = none)
   size_t slot_cap = 0;
 
   // Arena mode (searches that allocate nothing): while `arena` is set, get() carves the slots

@@ -197,6 +197,10 @@ struct screen_args {
   int64_t spill_pool  = 0;
   int64_t spill_cap   = 0;  // set by the launcher
   uint32_t* spill_need = nullptr;
+  // shader clock of the screen's workgroups (timing mode only, else null): every workgroup adds
+  // its life in shader clock cycles (s_memtime) to clock[0] and in ticks of the constant 100 MHz
+  // counter (s_memrealtime) to clock[1]
+  unsigned long long* clock = nullptr;
   // anchors: group maxima [nq_pad, n_groups] (int32 or float), a group = group_steps steps
   void* gmax       = nullptr;
   int64_t n_groups = 0;

@@ -99,6 +99,8 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
 
   const screen_work w = work_of<QB>(a, blockIdx.x);
   if (!w.valid) { return; }
+  wg_clock clk;
+  if constexpr (!ANCHORS) { clk.start(a); }
   const int64_t n_steps = screen_steps(w.n_scan);  // chunk steps
   const int64_t q0      = w.q0;
   // groups holding a live query, rounded up to a pair (the last query block of a batch or of a
@@ -368,6 +370,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     __syncthreads();
     flush_hits<R::kValues>(q0, QB, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(kHitCap),
                            reinterpret_cast<uint32_t*>(qlds));
+    clk.stop(a);
   }
 }
 

@@ -402,6 +402,28 @@ __device__ inline void flush_hits(int64_t q0, int qb, const screen_args& a, cons
   }
 }
 
+/** A workgroup's life by the shader clock and by the constant 100 MHz counter, added to
+ *  a.clock[0] and a.clock[1] at stop() when the launch is timed (a.clock non-null). */
+struct wg_clock {
+  uint64_t t0 = 0, r0 = 0;
+  __device__ __forceinline__ void start(const screen_args& a)
+  {
+    if (a.clock != nullptr) {
+      t0 = __builtin_amdgcn_s_memtime();
+      r0 = __builtin_amdgcn_s_memrealtime();
+    }
+  }
+  __device__ __forceinline__ void stop(const screen_args& a) const
+  {
+    if (a.clock != nullptr && threadIdx.x == 0) {
+      const uint64_t t1 = __builtin_amdgcn_s_memtime();
+      const uint64_t r1 = __builtin_amdgcn_s_memrealtime();
+      atomicAdd(a.clock, static_cast<unsigned long long>(t1 - t0));
+      atomicAdd(a.clock + 1, static_cast<unsigned long long>(r1 - r0));
+    }
+  }
+};
+
 /**
  * Anchor pass, one 16-query tile of a 64-row step: folds the best screen value of this lane's
  * query over the step into the wave's running group maximum gml[e] (e = the query's slot).

@@ -159,6 +159,8 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
 
   const screen_work w = work_of<TQ, true>(a, blockIdx.x);
   if (!w.valid) { return; }
+  wg_clock clk;
+  if constexpr (!ANCH) { clk.start(a); }
   const int RB          = a.row_bytes;  // bytes per row: a multiple of 128
   const int n_stages    = RB / kStageB;
   const int64_t scan0   = w.chunk * kTileRows;  // scan index of tile row 0 (an even stored row
@@ -401,6 +403,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
   }
   __syncthreads();
   flush_hits<true>(w.q0, TQ, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(CAP), scratch);
+  clk.stop(a);
 }
 
 template <int RT, int QT, bool FILT, bool ANCH>

@@ -125,6 +125,13 @@ def auto_width(X, metric, target=0.95, sample=200_000):
     return min(L - 5, d)
 
 
+def trim_pool():
+    """Free the scratch memory that the calling thread's searches on the current device have grown
+    (certex/index.py:165-169, which returns the unused memory of the device's stream-ordered pool
+    to the driver), after waiting for the thread's current stream; later searches grow it again."""
+    C.check(C.lib().cuvsCertexTrimPool(C.resources()))
+
+
 class search_stats:
     """Counters of the searches of the calling thread inside the block: queries, certified
     survivors and verified exact distances (certex/index.py:171-188).

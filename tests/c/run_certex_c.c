@@ -1,7 +1,10 @@
 /* The C API driven from C (compiled as C99), as the reference's c/tests/neighbors/run_certex_c.c
- * does: build an index of uint8 vectors, search with and without a bitset filter, remove ids, and
- * check every returned id and distance against a brute force in this file. Exit status 0 = pass. */
+ * and certex_c.cu (cases Plain, Lists, Bitset, SaveLoad) do: build an index of uint8 vectors,
+ * search with and without a bitset filter, remove ids; build one with k-means lists and search it
+ * with the list probe; save it, load it into a new handle and search again. Every returned id and
+ * distance is checked against a brute force in this file. Exit status 0 = pass. */
 #define __HIP_PLATFORM_AMD__ 1
+#define _XOPEN_SOURCE 700 /* mkstemp, close, unlink */
 #include <cuvs/neighbors/certex.h>
 #include <hip/hip_runtime_api.h>
 
@@ -9,6 +12,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 #define CHECK(call)                                                            \
   do {                                                                         \
@@ -185,6 +189,62 @@ int main(void)
   HCHECK(hipMemcpy(got_ids, dn, sizeof(int64_t) * nq * k, hipMemcpyDeviceToHost));
   HCHECK(hipMemcpy(got_d, dd, sizeof(float) * nq * k, hipMemcpyDeviceToHost));
   if (compare(x, q, n, d, nq, k, keep, got_ids, got_d)) return 1;
+
+  /* Lists: 32 k-means lists, two probed per query (reference certex_c.cu:135), with the
+   * removals applied to this index too, then a bitset */
+  cuvsCertexIndex_t listed;
+  CHECK(cuvsCertexIndexCreate(&listed));
+  params->n_lists = 32;
+  CHECK(cuvsCertexBuild(res, params, &X, listed));
+  CHECK(cuvsCertexRemove(res, &R, listed));
+  sp->probe_lists = 2;
+  CHECK(cuvsCertexSearch(res, sp, listed, &Q, &NB, &DS, none));
+  CHECK(cuvsStreamSync(res));
+  HCHECK(hipMemcpy(got_ids, dn, sizeof(int64_t) * nq * k, hipMemcpyDeviceToHost));
+  HCHECK(hipMemcpy(got_d, dd, sizeof(float) * nq * k, hipMemcpyDeviceToHost));
+  if (compare(x, q, n, d, nq, k, keep, got_ids, got_d)) return 1;
+  for (int64_t i = 0; i < n; ++i) keep[i] = (uint8_t)(i >= 5000 && i % 3 == 0);
+  CHECK(cuvsCertexSearch(res, sp, listed, &Q, &NB, &DS, bits));
+  CHECK(cuvsStreamSync(res));
+  HCHECK(hipMemcpy(got_ids, dn, sizeof(int64_t) * nq * k, hipMemcpyDeviceToHost));
+  HCHECK(hipMemcpy(got_d, dd, sizeof(float) * nq * k, hipMemcpyDeviceToHost));
+  if (compare(x, q, n, d, nq, k, keep, got_ids, got_d)) return 1;
+
+  /* SaveLoad (reference certex_c.cu:139): the index with lists and removals, into a new handle */
+  char path[] = "/tmp/run_certex_c_XXXXXX";
+  const int fd = mkstemp(path);
+  if (fd < 0) {
+    fprintf(stderr, "FAIL: no temporary file\n");
+    return 1;
+  }
+  close(fd);
+  CHECK(cuvsCertexSerialize(res, path, listed));
+  CHECK(cuvsCertexIndexDestroy(listed));
+  cuvsCertexIndex_t loaded;
+  CHECK(cuvsCertexIndexCreate(&loaded));
+  CHECK(cuvsCertexDeserialize(res, path, loaded));
+  if (cuvsCertexDeserialize(res, path, loaded) != CUVS_ERROR) { /* refuses a non-empty handle */
+    fprintf(stderr, "FAIL: deserialize into a non-empty handle accepted\n");
+    return 1;
+  }
+  unlink(path);
+  CHECK(cuvsCertexIndexGetSize(loaded, &size));
+  if (size != n) {
+    fprintf(stderr, "FAIL: loaded size %lld\n", (long long)size);
+    return 1;
+  }
+  CHECK(cuvsCertexSearch(res, sp, loaded, &Q, &NB, &DS, bits));
+  CHECK(cuvsStreamSync(res));
+  HCHECK(hipMemcpy(got_ids, dn, sizeof(int64_t) * nq * k, hipMemcpyDeviceToHost));
+  HCHECK(hipMemcpy(got_d, dd, sizeof(float) * nq * k, hipMemcpyDeviceToHost));
+  if (compare(x, q, n, d, nq, k, keep, got_ids, got_d)) return 1;
+  for (int64_t i = 0; i < n; ++i) keep[i] = (uint8_t)(i >= 5000);
+  CHECK(cuvsCertexSearch(res, sp, loaded, &Q, &NB, &DS, none));
+  CHECK(cuvsStreamSync(res));
+  HCHECK(hipMemcpy(got_ids, dn, sizeof(int64_t) * nq * k, hipMemcpyDeviceToHost));
+  HCHECK(hipMemcpy(got_d, dd, sizeof(float) * nq * k, hipMemcpyDeviceToHost));
+  if (compare(x, q, n, d, nq, k, keep, got_ids, got_d)) return 1;
+  CHECK(cuvsCertexIndexDestroy(loaded));
 
   /* queries of another vector type are rejected */
   DLManagedTensor QF;

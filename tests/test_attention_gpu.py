@@ -69,3 +69,26 @@ def test_outlier_channels(gpu):
     keys[..., :4] *= 20
     scores, ids = certex.topk(q, keys.half(), 100)
     assert_exact(q, keys.half(), scores, ids, 100)
+
+
+@pytest.mark.parametrize("key_type", [torch.bfloat16, torch.float16])
+def test_queries_of_another_type(gpu, key_type):
+    """float32 queries against a bfloat16 or float16 cache are rounded to the cache's type, as
+    the reference rounds them; the top k is exact for the rounded queries."""
+    q, keys = data(n_kv=2, H=4, n=30_000, m=8, seed=5)
+    q32 = q.float() + 1e-3 * torch.randn(q.shape, generator=torch.Generator(device="cuda").manual_seed(6),
+                                         device="cuda")
+    cache = certex.KeyCache(2, 128, k=64).append(keys.to(key_type))
+    scores, ids = cache.topk(q32, 64)
+    assert_exact(q32.to(key_type).float(), keys.to(key_type).float(), scores, ids, 64)
+    s16, i16 = cache.topk(q32.half(), 64)  # float16 queries against the same cache
+    assert_exact(q32.half().to(key_type).float(), keys.to(key_type).float(), s16, i16, 64)
+
+
+def test_queries_that_overflow_the_cache(gpu):
+    q, keys = data(n_kv=1, H=1, n=5_000, m=2, seed=7)
+    cache = certex.KeyCache(1, 128, k=8).append(keys)  # a float16 cache
+    big = q.float()
+    big[0, 0, 0] = 1e6  # beyond float16's range
+    with pytest.raises(ValueError, match="overflow"):
+        cache.topk(big, 8)

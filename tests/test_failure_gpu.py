@@ -1,15 +1,14 @@
 """Failure paths and update races of the search, against the CPU oracle.
 
 - Allocation failure: the reference halves a batch on rmm::bad_alloc or batch_too_large and
-  retries (certex.cu:1477-1502). The test hook CERTEX_SCRATCH_SLOT_CAP (read when the C resources
-  are created) makes every scratch request above the cap fail as an allocation would, so the
+  retries (certex.cu:1477-1502). The testing-only call cuvsCertexTestScratchCap makes every
+  scratch request of the thread's resources above the cap fail as an allocation would, so the
   halving runs; results must equal the oracle, and a single query that cannot fit is an error.
 - Fractional queries of an integer index are rejected (tests/test_exact.py:342-350).
 - Searches of a float index during concurrent additions each equal the exact top k of one
   published snapshot (cpp/tests/neighbors/ann_certex/test_updates.cu:504-591).
 """
 
-import os
 import threading
 
 import numpy as np
@@ -25,16 +24,12 @@ pytestmark = pytest.mark.gpu
 
 
 def in_fresh_resources(fn, cap):
-    """Run fn() in a new thread, whose C resources are created with the scratch cap set."""
+    """Run fn() in a new thread, whose C resources get the scratch cap (a testing-only call)."""
     out, errors = [], []
 
     def body():
-        os.environ["CERTEX_SCRATCH_SLOT_CAP"] = str(cap)
         try:
-            C.resources()  # created now, with the cap
-        finally:
-            del os.environ["CERTEX_SCRATCH_SLOT_CAP"]
-        try:
+            C.check(C.lib().cuvsCertexTestScratchCap(C.resources(), cap))
             out.append(fn())
         except Exception as e:  # noqa: BLE001
             errors.append(e)

@@ -99,3 +99,21 @@ def test_int8_rows_of_8bit_vectors(gpu):
         idx.add(torch.from_numpy(X).cuda())
         D, I = idx.search(torch.from_numpy(Q).cuda(), k=10)
         check(X, Q, 10, "l2", D, I)
+
+
+def test_trim_pool(gpu):
+    """trim_pool frees the scratch the thread's searches grew (reference certex/index.py:165-169);
+    the next search grows it again and returns the same results."""
+    X = data.mixture_u8(200_000, seed=160)
+    Q = torch.from_numpy(data.mixture_u8(4_000, seed=161)).cuda()
+    idx = certex.Index(128)
+    idx.add(torch.from_numpy(X).cuda())
+    D0, I0 = idx.search(Q, k=100, batch=4_000)
+    torch.cuda.synchronize()
+    before = torch.cuda.mem_get_info()[0]
+    certex.trim_pool()
+    freed = torch.cuda.mem_get_info()[0] - before
+    assert freed >= 4_000 * 100 * 12  # at least the batch's best lists (score f64 + row i64 per entry)
+    D1, I1 = idx.search(Q, k=100, batch=4_000)
+    assert torch.equal(I0, I1) and torch.equal(D0, D1)
+    check(X, Q[:50].cpu().numpy(), 100, "l2", D1[:50], I1[:50])

@@ -38,6 +38,36 @@ def test_save_load(gpu, tmp_path, dtype):
     assert back.ntotal == idx.ntotal + 1000
 
 
+@pytest.mark.parametrize("dtype", [np.uint8, np.float32])
+def test_save_load_in_chunks(gpu, tmp_path, dtype):
+    """Arrays larger than the 64 MiB staging buffers move in several chunks each (an odd count for
+    the rows), with labels and lists; the loaded index answers exactly as the saved one."""
+    if dtype == np.uint8:
+        X = data.mixture_u8(1_300_000, seed=7)  # 166 MB of rows: 3 chunks
+        Q = data.mixture_u8(300, seed=8)
+    else:
+        X = data.gaussian(330_000, 128, 7, np.float32)  # 169 MB of vectors: 3 chunks
+        Q = data.gaussian(300, 128, 8, np.float32)
+    labels = torch.from_numpy(np.random.default_rng(9).integers(0, 5, len(X)).astype(np.int32))
+    idx = certex.Index(128, metric="l2", n_lists=32)
+    idx.add(X, labels=labels)
+    idx.remove(torch.arange(3, len(X), 101))
+    D0, I0 = idx.search(Q, k=10)
+    ql = torch.from_numpy(np.random.default_rng(10).integers(0, 5, len(Q)).astype(np.int32))
+    Dl0, Il0 = idx.search(Q, k=10, labels=ql)
+    path = tmp_path / "big.cx"
+    idx.save(path)
+    back = certex.Index.load(path)
+    assert back.ntotal == idx.ntotal and back.core.lists == idx.core.lists
+    assert torch.equal(back.list_order(), idx.list_order())
+    D1, I1 = back.search(Q, k=10)
+    np.testing.assert_array_equal(I0, I1)
+    np.testing.assert_array_equal(D0, D1)
+    Dl1, Il1 = back.search(Q, k=10, labels=ql)
+    np.testing.assert_array_equal(Il0, Il1)
+    np.testing.assert_array_equal(Dl0, Dl1)
+
+
 def test_load_rejects_foreign_files(gpu, tmp_path):
     bad = tmp_path / "bad.cx"
     bad.write_bytes(b"<f4\x00" + (0x43455258).to_bytes(4, "little") + (1).to_bytes(4, "little") + b"\x00" * 64)

@@ -2,8 +2,9 @@
 
 The search without allocation takes its scratch from one fixed 128 MiB array per GPU instead of
 growing buffers. Its results must equal the allocating search's bit for bit (ids and distances),
-on two calls in a row, the second with fewer queries, and when a batch outgrows the array and is
-split. The device's free memory must not move during a call.
+on two calls in a row, the second with fewer queries, when a batch outgrows the array and is
+split, and when two threads with their own resources and streams call one after the other. The
+device's free memory must not move during a call.
 """
 
 import ctypes
@@ -89,9 +90,51 @@ def test_lists_and_free_memory(gpu):
     D = torch.empty((800, 10), dtype=torch.float32, device="cuda")
     sp = C.SearchParams(128, 2048, 2)
     qb, ib, db = C.Borrowed(Q), C.Borrowed(I), C.Borrowed(D)
-    torch.cuda.synchronize()
+
+    def call():
+        C.check(C.lib().cuvsCertexSearchNoAlloc(C.resources(), ctypes.byref(sp), idx.core.h, qb.ptr, ib.ptr,
+                                                db.ptr, C.Filter(0, C.NO_FILTER)))
+        torch.cuda.synchronize()
+
+    call()  # the same shape once before: code objects the runtime loads lazily are loaded by now
     before = torch.cuda.mem_get_info()[0]
-    C.check(C.lib().cuvsCertexSearchNoAlloc(C.resources(), ctypes.byref(sp), idx.core.h, qb.ptr, ib.ptr, db.ptr,
-                                            C.Filter(0, C.NO_FILTER)))
+    call()
+    # the smallest slot the allocating search would carve is 1 MiB; nothing else allocates here
+    assert abs(torch.cuda.mem_get_info()[0] - before) < (1 << 20)
+
+
+def test_two_threads_take_turns(gpu):
+    """Two threads, each with its own resources and stream, call one after the other without a
+    sync between them. Each call returns with its verify still queued; the second call's stream
+    must wait for it on the GPU before it reuses the scratch array."""
+    import threading
+
+    X = np.random.default_rng(150).standard_normal((120_000, 128)).astype(np.float32)
+    Qs = [torch.from_numpy(np.random.default_rng(151 + i).standard_normal((512, 128)).astype(np.float32)).cuda()
+          for i in range(2)]
+    idx = certex.Index(128, metric="ip")
+    idx.add(torch.from_numpy(X).cuda())
+    k = 1024
+    want = [c_search(idx, Q, k, "cuvsCertexSearch", batch=512) for Q in Qs]
+    out = [None, None]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
     torch.cuda.synchronize()
-    assert torch.cuda.mem_get_info()[0] == before
+
+    def run(i):
+        with torch.cuda.stream(streams[i]):
+            I = torch.full((512, k), -7, dtype=torch.int64, device="cuda")
+            D = torch.full((512, k), -7.0, dtype=torch.float32, device="cuda")
+            sp = C.SearchParams(128, 512, 2)
+            qb, ib, db = C.Borrowed(Qs[i]), C.Borrowed(I), C.Borrowed(D)
+            C.check(C.lib().cuvsCertexSearchNoAlloc(C.resources(), ctypes.byref(sp), idx.core.h, qb.ptr, ib.ptr,
+                                                    db.ptr, C.Filter(0, C.NO_FILTER)))
+            out[i] = (D, I, (qb, ib, db))  # no sync here: the next call starts while these kernels run
+
+    for i in range(2):
+        t = threading.Thread(target=run, args=(i,))
+        t.start()
+        t.join()
+    torch.cuda.synchronize()
+    for i in range(2):
+        np.testing.assert_array_equal(out[i][1].cpu().numpy(), want[i][1])
+        np.testing.assert_array_equal(out[i][0].cpu().numpy(), want[i][0])
