@@ -112,6 +112,10 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   const int64_t quarter = a.chunk_steps / 4;
   const int64_t w0      = w.chunk * a.chunk_steps + wave * quarter;
   const int64_t w1      = w0 + quarter < n_steps ? w0 + quarter : n_steps;
+  // coarse anchor groups of one group per wave: each wave's group maxima wait in LDS, and the
+  // workgroup writes each query's 4 consecutive columns together at its end (one 16-byte run per
+  // query instead of four 4-byte stores to four lines of the table)
+  const bool staged = RUNREG && !a.fine && quarter == a.group_steps;
 
   if (tid == 0) { n_hits = 0; }
   // only the groups that run are staged (a routed group's block is often mostly padding)
@@ -326,7 +330,11 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
                 m               = R::vmax(m, __shfl_xor(m, 16));
                 m               = R::vmax(m, __shfl_xor(m, 32));
                 const int64_t q = q0 + g * GQ + qt * 16 + (lane & 15);
-                if (lane < 16 && q < w.q_end) { gmax[table_entry(a, q, s / a.group_steps)] = m; }
+                if (staged) {
+                  if (lane < 16) { gml[wave * QB + g * GQ + qt * 16 + lane] = m; }
+                } else if (lane < 16 && q < w.q_end) {
+                  gmax[table_entry(a, q, s / a.group_steps)] = m;
+                }
                 run[g][qt] = R::lowest();
               }
             }
@@ -366,6 +374,19 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     step(full);
   }
 
+  if constexpr (RUNREG) {
+    if (staged) {
+      // wave v's group is column 4 chunk + v (its quarter is that one group); a wave of the last
+      // chunk past the scan has no group
+      __syncthreads();
+      const int64_t col0 = w.chunk * 4;
+      for (int i = tid; i < 4 * qlive; i += 256) {
+        const int e = i >> 2, v = i & 3;
+        const bool has = w.chunk * a.chunk_steps + v * quarter < n_steps;
+        if (has && q0 + e < w.q_end) { gmax[table_entry(a, q0 + e, col0 + v)] = gml[v * QB + e]; }
+      }
+    }
+  }
   if constexpr (!ANCHORS) {
     __syncthreads();
     flush_hits<R::kValues>(q0, QB, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(kHitCap),
