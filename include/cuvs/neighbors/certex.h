@@ -241,6 +241,22 @@ CUVS_EXPORT cuvsError_t cuvsCertexTrimPool(cuvsResources_t res);
  */
 CUVS_EXPORT cuvsError_t cuvsCertexTestScratchCap(cuvsResources_t res, int64_t bytes);
 
+/**
+ * Testing only, no counterpart in the reference (it replaces the kernel-level harness of
+ * cpp/tests/neighbors/certex_kernels.cu:62-180): the next search batch of the calling thread (an
+ * unrouted search without a list probe) copies its intermediate arrays to host memory, taken from
+ * its own launches: the encoded queries ("qrows"), the anchor group table ("gmax"), the
+ * thresholds ("theta"), the buckets ("count", "rows", and "vals" for float indexes), for float
+ * indexes the certified bound U of each query ("ub_q"), the query scalars ("qscal"), and the
+ * certificate's lower and upper bound of every bucket entry ("lb", "ub"), plus the index's
+ * screening rows ("codes", "rowc") and the batch's shape (int64 "B", "k", "cap", "n_groups",
+ * "group_steps", "fine", "anchor_stride", "row_bytes", "size", "all_rows").
+ */
+CUVS_EXPORT cuvsError_t cuvsCertexTestCaptureBegin(void);
+/** Testing only: the size in bytes of a captured array in *bytes, and a copy to `host` unless
+ *  NULL; CUVS_ERROR for a name that the last capture does not hold. */
+CUVS_EXPORT cuvsError_t cuvsCertexTestCaptureGet(const char* name, void* host, int64_t* bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -130,6 +130,11 @@ struct kernel_times {
 };
 void timing_begin();
 auto timing_end() -> kernel_times;
+/** Testing only (no counterpart in the reference): copy the intermediate arrays of the calling
+ *  thread's next search batch (an unrouted search without a list probe) and the index's screening
+ *  rows; capture_get returns an array's bytes and copies it to `host` unless null. */
+void capture_begin();
+auto capture_get(std::string const& name, void* host) -> int64_t;
 /** Average shader clock (MHz) of the screen workgroups timed between the last timing_begin() and
  *  timing_end(): their lives in shader clock cycles over their lives in real time; 0 if none. */
 auto timing_shader_clock_mhz() -> double;

@@ -164,6 +164,8 @@ def lib():
                     "cuvsCertexStatsBegin": [],
                     "cuvsCertexStatsEnd": [P(i64), P(i64), P(i64)],
                     "cuvsCertexTimingShaderClock": [P(ctypes.c_double)],
+                    "cuvsCertexTestCaptureBegin": [],
+                    "cuvsCertexTestCaptureGet": [ctypes.c_char_p, vp, P(i64)],
                     "cuvsCertexTrimPool": [ctypes.c_size_t],
                     "cuvsCertexTestScratchCap": [ctypes.c_size_t, i64],
                     "cuvsCertexTimingBegin": [],

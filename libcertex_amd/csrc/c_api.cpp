@@ -651,6 +651,19 @@ cuvsError_t cuvsCertexStatsEnd(int64_t* queries, int64_t* survivors, int64_t* ve
   });
 }
 
+cuvsError_t cuvsCertexTestCaptureBegin(void)
+{
+  return translate([] { certex::capture_begin(); });
+}
+
+cuvsError_t cuvsCertexTestCaptureGet(const char* name, void* host, int64_t* bytes)
+{
+  return translate([=] {
+    certex::expects(name != nullptr && bytes != nullptr, "certex: NULL argument");
+    *bytes = certex::capture_get(std::string(name), host);
+  });
+}
+
 cuvsError_t cuvsCertexTimingShaderClock(double* mhz)
 {
   return translate([=] {

@@ -15,6 +15,8 @@
 #include <cstring>
 #include <fstream>
 #include <functional>
+#include <map>
+#include <memory>
 #include <new>
 #include <thread>
 
@@ -116,6 +118,41 @@ struct timing_state {
   }
 };
 thread_local timing_state t_timing;
+
+/**
+ * Testing only: copies of the intermediate arrays of the next search batch of the calling thread
+ * (query rows, group table, thresholds, buckets, certificate bounds) and of the index's screening
+ * rows, taken from the search's own launches, so that tests can check the screen and the
+ * certificate against a brute force (capture_begin, capture_get).
+ */
+struct capture_state {
+  bool on = false;
+  std::map<std::string, std::vector<char>> arrays;
+  void put(const char* name, const void* dev, size_t bytes, hipStream_t stream)
+  {
+    auto& v = arrays[name];
+    v.resize(bytes);
+    if (bytes > 0) { CERTEX_HIP_TRY(hipMemcpyAsync(v.data(), dev, bytes, hipMemcpyDefault, stream)); }
+  }
+  template <typename V>
+  void value(const char* name, V x)
+  {
+    auto& v = arrays[name];
+    v.resize(sizeof(V));
+    std::memcpy(v.data(), &x, sizeof(V));
+  }
+};
+thread_local capture_state t_capture;
+
+/** A device array of n elements that lives for one capture (testing only). */
+template <typename V>
+struct capture_buffer {
+  V* p = nullptr;
+  explicit capture_buffer(size_t n) { CERTEX_HIP_TRY(hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(V))); }
+  ~capture_buffer() { (void)hipFree(p); }
+  capture_buffer(capture_buffer const&)            = delete;
+  capture_buffer& operator=(capture_buffer const&) = delete;
+};
 
 /** Run `launch` between two events of `phase` when timing is on. */
 template <typename F>
@@ -790,6 +827,28 @@ void table_pass(cuvs::resources const& res, index_state const& st, certex_amd::s
   }
 }
 
+/** Testing only: the batch's shape, its table plan and the index's screening rows. */
+void capture_common(index_state const& st, table_plan const& tp, int64_t B, int64_t nq_pad, int k,
+                    bool all_rows, int64_t cap, route_plan const* route, hipStream_t stream)
+{
+  expects(route == nullptr && tp.pp.n_pairs == 0,
+          "certex: a capture covers unrouted searches without a list probe");
+  expects(B <= 65535, "certex: a capture covers batches of at most 65,535 queries");
+  t_capture.value("B", int64_t(B));
+  t_capture.value("nq_pad", int64_t(nq_pad));
+  t_capture.value("k", int64_t(k));
+  t_capture.value("all_rows", int64_t(all_rows));
+  t_capture.value("cap", int64_t(all_rows ? 0 : cap));
+  t_capture.value("n_groups", int64_t(tp.n_groups));
+  t_capture.value("group_steps", int64_t(tp.ap.group_steps));
+  t_capture.value("fine", int64_t(tp.ap.fine));
+  t_capture.value("anchor_stride", int64_t(tp.ap.stride));
+  t_capture.value("row_bytes", int64_t(st.row_bytes));
+  t_capture.value("size", int64_t(st.size));
+  t_capture.put("codes", st.codes.p, size_t(st.size) * st.row_bytes, stream);
+  t_capture.put("rowc", st.rowc.p, size_t(st.size) * 4, stream);
+}
+
 /** One batch of queries of an integer index (the caller holds the shared lock). */
 void search_batch_int(cuvs::resources const& res, index_state const& st, const void* queries,
                       int64_t B, int k, int64_t q0, int64_t* neighbors, float* distances,
@@ -843,6 +902,20 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
                                     cap, nullptr, &worst);
   }
   count_stats(res, st, B, all_rows, count, cap);
+  if (t_capture.on) {
+    capture_common(st, tp, B, nq_pad, k, all_rows, cap, route, stream);
+    t_capture.put("qrows", qcodes, size_t(B) * st.row_bytes, stream);
+    t_capture.put("theta", theta, size_t(B) * 4, stream);
+    if (tp.n_groups >= k) {
+      t_capture.put("gmax", rs.get(cuvs::detail::ws_gmax, 1), size_t(B) * tp.n_groups * 4, stream);
+    }
+    if (!all_rows) {
+      t_capture.put("count", count, size_t(B) * 4, stream);
+      t_capture.put("rows", rows, size_t(B) * cap * 4, stream);
+    }
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+    t_capture.on = false;
+  }
 
   auto* best_score =
     static_cast<double*>(rs.get(cuvs::detail::ws_best_score, size_t(B) * k * sizeof(double)));
@@ -917,6 +990,8 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
 
   auto* theta   = static_cast<float*>(rs.get(cuvs::detail::ws_theta, size_t(nq_pad) * 4));
   bool all_rows = tp.n_groups < k;
+  certex_amd::threshold_f_args ta{};
+  std::unique_ptr<capture_buffer<double>> ub_q;  // testing: U per query
   if (!all_rows) {
     auto* gmax = static_cast<float*>(
       rs.get(cuvs::detail::ws_gmax, size_t(nq_pad) * size_t(tp.n_groups) * 4));
@@ -927,7 +1002,6 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
                  wide ? certex_amd::anchors_f16_wide : certex_amd::anchors_f16);
     });
     // theta certified from the k-th best group maximum (no exact anchor scores)
-    certex_amd::threshold_f_args ta{};
     ta.gmax     = gmax;
     ta.n_groups = tp.n_groups;
     ta.nq       = B;
@@ -939,7 +1013,12 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
     ta.alpha2   = st.alpha * st.alpha;
     ta.gamma    = st.gamma;
     ta.theta    = theta;
+    if (t_capture.on) {
+      ub_q = std::make_unique<capture_buffer<double>>(size_t(nq_pad));
+      ta.ub = ub_q->p;
+    }
     timed(1, stream, [&] { certex_amd::threshold_f16(ta, stream); });
+    ta.ub = nullptr;
   }
 
   uint32_t *count = nullptr, *rows = nullptr;
@@ -987,13 +1066,50 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
     timed(3, stream, [&] { certex_amd::verify_topk_f(va, stream); });
   };
   bool verified = false;
+  // a capture reads the buckets before the verification (which compacts them in place)
+  const bool capture = t_capture.on;
   if (!all_rows) {
     sa.theta = theta;
     all_rows = !screen_into_buckets(
       res, B, nq_pad, size, sa,
       screen_pass(st, route, wide ? certex_amd::screen_f16_tile : certex_amd::screen_f16), count,
-      rows, cap, &vals, nullptr, [&] { verify(false); });
-    verified = !all_rows;
+      rows, cap, &vals, nullptr, [&] {
+        if (!capture) { verify(false); }
+      });
+    verified = !all_rows && !capture;
+  }
+  if (capture) {
+    capture_common(st, tp, B, nq_pad, k, all_rows, cap, route, stream);
+    t_capture.put("qrows", qrows, size_t(B) * st.row_bytes, stream);
+    t_capture.put("qscal", qscal, size_t(B) * 3 * 8, stream);
+    t_capture.put("theta", theta, size_t(B) * 4, stream);
+    t_capture.put("maxima", st.maxima.p, 2 * sizeof(double), stream);
+    t_capture.value("alpha2", st.alpha * st.alpha);
+    t_capture.value("gamma", st.gamma);
+    t_capture.value("halves", int64_t(st.halves));
+    if (ub_q) {
+      t_capture.put("gmax", ta.gmax, size_t(B) * tp.n_groups * 4, stream);
+      t_capture.put("ub_q", ub_q->p, size_t(B) * 8, stream);
+    }
+    if (!all_rows) {
+      t_capture.put("count", count, size_t(B) * 4, stream);
+      t_capture.put("rows", rows, size_t(B) * cap * 4, stream);
+      t_capture.put("vals", vals, size_t(B) * cap * 4, stream);
+      certex_amd::threshold_f_args ca{};
+      ca.nq = B, ca.nq_pad = nq_pad, ca.k = k, ca.metric = st.metric, ca.qscal = qscal;
+      ca.maxima = st.maxima.as<double>(), ca.alpha2 = st.alpha * st.alpha, ca.gamma = st.gamma;
+      capture_buffer<double> lb(size_t(B) * cap), ub(size_t(B) * cap);
+      certex_amd::certificate_bounds(ca, count, vals, cap, lb.p, ub.p, stream);
+      t_capture.put("lb", lb.p, size_t(B) * cap * 8, stream);
+      t_capture.put("ub", ub.p, size_t(B) * cap * 8, stream);
+      CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+    }
+    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+    t_capture.on = false;
+    if (!all_rows) {
+      verify(false);
+      verified = true;
+    }
   }
   if (!verified) { verify(true); }
   count_stats(res, st, B, all_rows, count, cap, true);
@@ -1313,6 +1429,7 @@ void search_without_allocation(cuvs::resources const& res, search_params const& 
     fa.words     = f.words;
     fa.bitmap_ld = idx.size();
   }
+  expects(!t_capture.on, "certex: a capture covers the allocating search");
   char* base = scratch_of(res.device());
   scratch_turn turn(res.device(), static_cast<hipStream_t>(res.stream()));
   arena_scope scope(res.state(), base, kNoAllocScratchBytes);
@@ -1323,6 +1440,20 @@ void search_without_allocation(cuvs::resources const& res, search_params const& 
       "certex: one query of this search needs more than the 128 MiB scratch of a search without "
       "allocation; use the allocating search");
   }
+}
+
+void capture_begin()
+{
+  t_capture.arrays.clear();
+  t_capture.on = true;
+}
+
+auto capture_get(std::string const& name, void* host) -> int64_t
+{
+  auto it = t_capture.arrays.find(name);
+  expects(it != t_capture.arrays.end(), "certex: the capture holds no array of that name");
+  if (host != nullptr) { std::memcpy(host, it->second.data(), it->second.size()); }
+  return int64_t(it->second.size());
 }
 
 void stats_begin()

@@ -396,6 +396,9 @@ struct threshold_f_args {
   double alpha2;         // alpha^2
   double gamma;
   float* theta;          // [nq_pad]
+  // testing only (null in searches): U per live query, the certified bound of its k-th
+  // neighbour's score that theta is derived from (+inf when fewer than k groups count)
+  double* ub = nullptr;
 };
 /**
  * theta[q] for fp16 rows, certified from the anchor pass alone: the k-th largest finite group
@@ -405,6 +408,14 @@ struct threshold_f_args {
  * fewer than k such groups; +inf for padding queries.
  */
 void threshold_f16(const threshold_f_args& a, hipStream_t stream);
+
+/**
+ * Testing only: the certificate's bounds of the exact score of every bucket entry of the live
+ * queries, from its screen value v: lb[q, slot] = the lower bound that the ordered verification
+ * uses, ub[q, slot] = the upper bound that the threshold uses (both for slot < min(count[q], cap)).
+ */
+void certificate_bounds(const threshold_f_args& a, const uint32_t* count, const float* vals,
+                        int64_t cap, double* lb, double* ub, hipStream_t stream);
 
 struct verify_f_args {
   const uint32_t* cand_count;

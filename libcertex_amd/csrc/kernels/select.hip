@@ -954,12 +954,20 @@ __global__ __launch_bounds__(kThreads) void threshold_f16_cert_kernel(threshold_
   key_range(a.n_groups, key_of, lo, hi, finite, red);
   if (finite < a.k) {
     // keep every live row: removed rows (screen value -inf) still fail
-    if (tid == 0) { a.theta[q] = -FLT_MAX; }
+    if (tid == 0) {
+      a.theta[q] = -FLT_MAX;
+      if (a.ub != nullptr) { a.ub[q] = INFINITY; }
+    }
     return;
   }
   const uint32_t key = radix_select(a.n_groups, a.k, key_of, lo, hi, hist, wave_tot, &sel_digit, &sel_rank);
-  if (tid == 0) { a.theta[q] = theta_of(screen_upper_bound(key_value(~key), a, q), a, q); }
+  if (tid == 0) {
+    const double U = screen_upper_bound(key_value(~key), a, q);
+    a.theta[q]     = theta_of(U, a, q);
+    if (a.ub != nullptr) { a.ub[q] = U; }
+  }
 }
+
 
 /**
  * A lower bound of the exact score of a pair whose fp16 screen value is v: the inverse of the
@@ -980,6 +988,23 @@ __device__ inline double screen_lower_bound(float v, double aq, double C, double
   const double lb = alpha2 * y - 1e-12 * alpha2 * (fabs(aq) + 2.0 * fabs(R) + 1e-300);
   if (metric == metric_kind::cosine) { return (lb - 2.0) / 2.0 - 1e-12 * (fabs(lb) + 2.0); }
   return lb;
+}
+
+/** Testing only: the certificate's two bounds of every bucket entry (certificate_bounds). */
+__global__ void certificate_bounds_kernel(threshold_f_args a, const uint32_t* count,
+                                          const float* vals, int64_t cap, double* lb, double* ub)
+{
+  const int64_t q = blockIdx.y;
+  if (q >= a.nq) { return; }
+  const int64_t n = count[q] < uint64_t(cap) ? int64_t(count[q]) : cap;
+  const double aq = a.qscal[3 * q];
+  const double C  = screen_error(a, q);
+  for (int64_t slot = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; slot < n;
+       slot += int64_t(gridDim.x) * blockDim.x) {
+    const float v       = vals[q * cap + slot];
+    lb[q * cap + slot] = screen_lower_bound(v, aq, C, a.alpha2, a.metric);
+    ub[q * cap + slot] = screen_upper_bound(v, a, q);
+  }
 }
 
 /** Inclusive prefix sum over the T threads of a block of T = 64 (one wave), kThreads or 1024. */
@@ -1258,8 +1283,11 @@ __global__ __launch_bounds__(T) void threshold_f16_cert_regs_kernel(threshold_f_
   if (tid != 0) { return; }
   if (key == 0xffffffffu) {
     a.theta[q] = -FLT_MAX;  // keep every live row: removed rows (screen value -inf) still fail
+    if (a.ub != nullptr) { a.ub[q] = INFINITY; }
   } else {
-    a.theta[q] = theta_of(screen_upper_bound(key_value(~key), a, q), a, q);
+    const double U = screen_upper_bound(key_value(~key), a, q);
+    a.theta[q]     = theta_of(U, a, q);
+    if (a.ub != nullptr) { a.ub[q] = U; }
   }
 }
 
@@ -1558,6 +1586,14 @@ void threshold_f16(const threshold_f_args& a, hipStream_t stream)
     return;
   }
   threshold_f16_cert_kernel<<<unsigned(a.nq_pad), kThreads, 0, stream>>>(a);
+}
+
+void certificate_bounds(const threshold_f_args& a, const uint32_t* count, const float* vals,
+                        int64_t cap, double* lb, double* ub, hipStream_t stream)
+{
+  if (a.nq == 0 || cap == 0) { return; }
+  const dim3 grid(unsigned((cap + 255) / 256 < 64 ? (cap + 255) / 256 : 64), unsigned(a.nq));
+  certificate_bounds_kernel<<<grid, 256, 0, stream>>>(a, count, vals, cap, lb, ub);
 }
 
 void verify_topk_f(const verify_f_args& a, hipStream_t stream)
