@@ -397,8 +397,9 @@ auto waves_of(index_state const& st) -> int64_t
   return certex_amd::screen_waves(!is_int(st.type), st.row_bytes);
 }
 
-/** The screen pass of fp16 rows of more than 128 halves runs the tiled kernel. */
-auto uses_tile_screen(index_state const& st) -> bool { return !is_int(st.type) && st.halves > 128; }
+/** The screen pass of rows of more than 256 bytes (fp16 rows of more than 128 halves, int8 rows of
+ *  more than 256 coordinates) runs the tiled kernel. */
+auto uses_tile_screen(index_state const& st) -> bool { return st.row_bytes > 256; }
 
 /**
  * Anchor pass: every anchor of the index, or the partition's (routed) and the tail's, into the
@@ -706,7 +707,7 @@ bool plan_probe(cuvs::resources const& res, index_state const& st, const void* q
     }
   }
   if (pp.groups.empty()) { return false; }
-  const bool wide     = f16 && st.row_bytes > 256;
+  const bool wide     = st.row_bytes > 256;
   const int qb        = certex_amd::screen_query_block(f16, st.row_bytes, pp.nq_pad);
   const int64_t waves = waves_of(st);
   const int64_t gs    = std::max<int64_t>(1, g);
@@ -866,8 +867,14 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
 
   auto* qcodes =
     static_cast<int8_t*>(rs.get(cuvs::detail::ws_qcodes, size_t(nq_pad) * st.row_bytes));
+  // rows of more than 256 bytes: the tiled screen reads the queries in the paired layout (a second
+  // copy, written by the same kernel)
+  const bool wide = uses_tile_screen(st);
+  auto* qpaired   = wide ? static_cast<int8_t*>(rs.get(cuvs::detail::ws_qpaired,
+                                                       size_t(nq_pad) * st.row_bytes))
+                         : nullptr;
   certex_amd::encode_queries_i8(static_cast<const uint8_t*>(queries), B, nq_pad, st.dim,
-                                st.row_bytes, flip, qcodes, stream);
+                                st.row_bytes, flip, qcodes, stream, qpaired);
 
   // group table: the best screen value of every group of anchors (every anchor_stride-th stored
   // row) and of the probed lists' rows; the k-th best group is the threshold of the query
@@ -877,6 +884,7 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
   sa.rowc      = st.rowc.p;
   sa.row_bytes = st.row_bytes;
   sa.qcodes    = qcodes;
+  sa.qpaired   = qpaired;
   sa.nq        = B;
   sa.nq_pad    = nq_pad;
   sa.filter    = fa;
@@ -941,7 +949,8 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
   if (route != nullptr) {
     va.part_ids   = st.label_part.ids.as<int32_t>();
     va.n_part     = st.label_part.n;
-    va.part_codes = st.label_part.codes.as<int8_t>();
+    va.part_codes  = st.label_part.codes.as<int8_t>();
+    va.part_paired = st.label_part.paired;
   }
   va.best_score = best_score;
   va.best_row   = best_row;
@@ -1165,7 +1174,7 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
 
   const int64_t nq_pad = certex_amd::pad_queries(B);
   const bool f16       = !is_int(st.type);
-  const bool wide      = f16 && st.row_bytes > 256;
+  const bool wide      = st.row_bytes > 256;
   const int qb         = certex_amd::screen_query_block(f16, st.row_bytes, nq_pad);
   const auto& off      = st.label_part.offsets;
   std::vector<certex_amd::screen_group> ga, gs;
@@ -1734,7 +1743,7 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
   std::lock_guard w(st.writer);
   if (is_int(st.type)) {
     expects(dataset.cols <= certex_amd::kMaxIntDim,
-            "certex: integer vectors of more than 256 coordinates are not supported by this build");
+            "certex: integer vectors of more than 4096 coordinates are not supported by this build");
     st.row_bytes = certex_amd::int_row_bytes(st.dim);
     st.width     = int(st.dim);
     grow(res, st, std::max(dataset.rows, params.capacity));
@@ -1751,7 +1760,7 @@ auto build(cuvs::resources const& res, index_params const& params, matrix_view<c
     return out;
   }
   expects(dataset.cols <= certex_amd::kMaxF16Halves,
-          "certex: float vectors of more than 2048 coordinates are not supported by this build");
+          "certex: float vectors of more than 4096 coordinates are not supported by this build");
   hipStream_t stream = static_cast<hipStream_t>(res.stream());
   st.halves          = certex_amd::f16_row_halves(st.dim);
   st.row_bytes       = 2 * st.halves;

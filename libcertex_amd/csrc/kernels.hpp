@@ -28,7 +28,7 @@ constexpr int32_t kKeepNone = 0x7fffffff;
 /** Rows of one screen step. */
 constexpr int kStepRows  = 64;
 /** Widest integer row (bytes) that the MFMA screen instantiates. */
-constexpr int kMaxIntDim = 256;
+constexpr int kMaxIntDim = 4096;
 
 /** Queries per screen workgroup for a batch of nq queries (512, or 128 for small batches). */
 __host__ __device__ inline int query_block(int64_t nq) { return nq > 128 ? 512 : 128; }
@@ -70,8 +70,12 @@ __host__ __device__ inline int64_t paired_anchor_count(int64_t x0, int64_t nx, i
   return 2 * pairs - (2 * s * (pairs - 1) + 1 >= avail ? 1 : 0);
 }
 
-/** Bytes of a stored integer screening row of `dim` coordinates: 128 or 256 (zero padded). */
-__host__ __device__ inline int int_row_bytes(int64_t dim) { return dim <= 128 ? 128 : 256; }
+/** Bytes of a stored integer screening row of `dim` coordinates (zero padded): 128, 256, or
+ *  above 256 coordinates a multiple of 256 (the tiled screen and the K-loop anchor pass). */
+__host__ __device__ inline int int_row_bytes(int64_t dim)
+{
+  return dim <= 128 ? 128 : int((dim + 255) / 256 * 256);
+}
 
 // --- encoding -------------------------------------------------------------------------------
 
@@ -83,9 +87,10 @@ __host__ __device__ inline int int_row_bytes(int64_t dim) { return dim <= 128 ? 
 void encode_rows_i8(const uint8_t* x, int64_t n, int64_t dim, int row_bytes, uint8_t flip,
                     metric_kind metric, int8_t* codes, int32_t* rowc, hipStream_t stream);
 
-/** qcodes[i] = q[i] ^ flip, zero padded, for i < nq; padding queries [nq, nq_pad) are zero. */
+/** qcodes[i] = q[i] ^ flip, zero padded, for i < nq; padding queries [nq, nq_pad) are zero; the
+ *  same codes again in the paired layout into qpaired unless null (the tiled screen's queries). */
 void encode_queries_i8(const uint8_t* q, int64_t nq, int64_t nq_pad, int64_t dim, int row_bytes,
-                       uint8_t flip, int8_t* qcodes, hipStream_t stream);
+                       uint8_t flip, int8_t* qcodes, hipStream_t stream, int8_t* qpaired = nullptr);
 
 /**
  * Tombstones of ids and where their rows are stored: with lists the ids below n_listed live in
@@ -255,10 +260,12 @@ inline int64_t screen_group_tile0(int64_t tiles, int64_t nq, int qb)
 /** Steps of kStepRows rows that cover n_scan rows. */
 __host__ __device__ inline int64_t screen_steps(int64_t n_scan) { return (n_scan + kStepRows - 1) / kStepRows; }
 
-/** Int8 MFMA pass that keeps (query, row) pairs whose screen value reaches the query threshold. */
+/** Int8 MFMA pass that keeps (query, row) pairs whose screen value reaches the query threshold
+ *  (rows of more than 256 bytes: screen_i8_tile). */
 void screen_i8(const screen_args& a, hipStream_t stream);
 
-/** Int8 MFMA pass that records the best screen value of every group of anchors for every query. */
+/** Int8 MFMA pass that records the best screen value of every group of anchors for every query
+ *  (rows of more than 256 bytes: anchors_i8_wide). */
 void anchors_i8(const screen_args& a, hipStream_t stream);
 
 /** The same two passes over fp16 rows (f32 accumulation, certified threshold). */
@@ -269,6 +276,8 @@ void anchors_f16(const screen_args& a, hipStream_t stream);
  * kMaxF16Halves): a K loop, workgroups of 8 waves; chunk_steps is a multiple of 8 group_steps.
  */
 void anchors_f16_wide(const screen_args& a, hipStream_t stream);
+/** The same K-loop anchor pass over int8 rows of more than 256 bytes (a multiple of 256). */
+void anchors_i8_wide(const screen_args& a, hipStream_t stream);
 /**
  * The fp16 screen for rows of more than 128 halves as LDS-staged tiles: a workgroup multiplies
  * 256 rows (chunk_steps = tile_chunk_steps()) with tile_block_queries() queries; row_stride 1.
@@ -281,6 +290,10 @@ void screen_f16_tile(const screen_args& a, hipStream_t stream);
  * anchors_f16_wide runs it for a pass with `tiled`.
  */
 void anchors_f16_tile(const screen_args& a, hipStream_t stream);
+/** The tiled screen and tiled anchor pass over int8 rows of more than 256 bytes (exact int32
+ *  screen values; survivors carry no value). */
+void screen_i8_tile(const screen_args& a, hipStream_t stream);
+void anchors_i8_tile(const screen_args& a, hipStream_t stream);
 int tile_chunk_steps();
 int tile_block_queries();
 
@@ -324,6 +337,7 @@ struct verify_args {
   const int32_t* part_ids  = nullptr;
   int64_t n_part           = 0;
   const int8_t* part_codes = nullptr;
+  bool part_paired         = false;  // part_codes in the paired layout (rows of more than 256 bytes)
   double* best_score;  // [nq, k], smaller is better; +inf where missing
   int64_t* best_row;   // [nq, k], -1 where missing
 };
@@ -336,7 +350,7 @@ void verify_topk_i8(const verify_args& a, hipStream_t stream);
 enum class elem : int { f32 = 0, f16 = 1, bf16 = 2 };
 
 /** Widest fp16 screening row (halves) of the screens. */
-constexpr int kMaxF16Halves = 2048;
+constexpr int kMaxF16Halves = 4096;
 /**
  * Row length (halves) of the fp16 screening rows for dimension dim: 64, 128, or dim rounded up
  * to a multiple of 128 (rows of more than 128 halves use the K-loop screen).
@@ -345,10 +359,12 @@ __host__ __device__ inline int f16_row_halves(int64_t dim)
 {
   return dim <= 64 ? 64 : int((dim + 127) / 128 * 128);
 }
-/** Waves of a screen workgroup: 8 for the K-loop screen of wide fp16 rows, 4 otherwise. */
+/** Waves of a screen workgroup: 8 for the K-loop anchor pass of rows of more than 256 bytes (fp16
+ *  or int8), 4 otherwise. */
 __host__ __device__ inline int screen_waves(bool f16, int row_bytes)
 {
-  return f16 && row_bytes > 256 ? 8 : 4;
+  (void)f16;
+  return row_bytes > 256 ? 8 : 4;
 }
 
 /**

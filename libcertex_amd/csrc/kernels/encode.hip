@@ -56,13 +56,45 @@ __global__ void encode_rows_kernel(const uint8_t* x, int64_t n, int64_t dim, int
   }
 }
 
+/**
+ * The rows of more than 256 bytes (row_bytes a multiple of 256): one wave per row, lane l on the
+ * 16-byte chunks l, l + 64, ...; the row's norm and sum meet by shuffles over the wave.
+ */
+__global__ void encode_rows_wide_kernel(const uint8_t* x, int64_t n, int64_t dim, int row_bytes,
+                                        uint8_t flip, metric_kind metric, int8_t* codes, int32_t* rowc)
+{
+  const int64_t r = (blockIdx.x * int64_t(blockDim.x) + threadIdx.x) >> 6;
+  const int lane  = threadIdx.x & 63;
+  if (r >= n) { return; }  // whole waves leave together (64 divides the block)
+  int norm = 0, sum = 0;
+  for (int c = lane; c < row_bytes / 16; c += 64) {
+    const int64_t j0 = int64_t(c) * 16;
+    int8_t out[16];
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      const int code = j0 + b < dim ? int(int8_t(x[r * dim + j0 + b] ^ flip)) : 0;
+      out[b]         = int8_t(code);
+      norm += code * code;
+      sum += code;
+    }
+    *reinterpret_cast<int4*>(codes + r * row_bytes + j0) = *reinterpret_cast<const int4*>(out);
+  }
+  for (int off = 1; off < 64; off <<= 1) {
+    norm += __shfl_xor(norm, off);
+    sum += __shfl_xor(sum, off);
+  }
+  if (lane == 0) { rowc[r] = metric == metric_kind::l2 ? -(norm >> 1) : (flip ? 128 * sum : 0); }
+}
+
 __global__ void encode_queries_kernel(const uint8_t* q, int64_t nq, int64_t nq_pad, int64_t dim,
-                                      int row_bytes, uint8_t flip, int8_t* qcodes)
+                                      int row_bytes, uint8_t flip, int8_t* qcodes, int8_t* qpaired)
 {
   const int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
   if (t >= nq_pad * row_bytes) { return; }
   const int64_t i = t / row_bytes, j = t % row_bytes;
-  qcodes[t]       = (i < nq && j < dim) ? int8_t(q[i * dim + j] ^ flip) : int8_t(0);
+  const int8_t c  = (i < nq && j < dim) ? int8_t(q[i * dim + j] ^ flip) : int8_t(0);
+  qcodes[t]       = c;
+  if (qpaired != nullptr) { qpaired[paired_offset(i, j, row_bytes)] = c; }
 }
 
 __device__ inline int64_t stored_row(const row_places& at, int64_t id)
@@ -348,17 +380,22 @@ void encode_rows_i8(const uint8_t* x, int64_t n, int64_t dim, int row_bytes, uin
                     metric_kind metric, int8_t* codes, int32_t* rowc, hipStream_t stream)
 {
   if (n == 0) { return; }
+  if (row_bytes > 256) {
+    encode_rows_wide_kernel<<<blocks_for(n * 64), 256, 0, stream>>>(x, n, dim, row_bytes, flip,
+                                                                   metric, codes, rowc);
+    return;
+  }
   encode_rows_kernel<<<blocks_for(n * (row_bytes / 16)), 256, 0, stream>>>(x, n, dim, row_bytes,
                                                                           flip, metric, codes, rowc);
 }
 
 void encode_queries_i8(const uint8_t* q, int64_t nq, int64_t nq_pad, int64_t dim, int row_bytes,
-                       uint8_t flip, int8_t* qcodes, hipStream_t stream)
+                       uint8_t flip, int8_t* qcodes, hipStream_t stream, int8_t* qpaired)
 {
   const int64_t n = nq_pad * row_bytes;
   if (n == 0) { return; }
   encode_queries_kernel<<<blocks_for(n), 256, 0, stream>>>(q, nq, nq_pad, dim, row_bytes, flip,
-                                                           qcodes);
+                                                           qcodes, qpaired);
 }
 
 void remove_rows_i8(const int64_t* ids, int64_t n, int64_t size, int32_t* rowc,

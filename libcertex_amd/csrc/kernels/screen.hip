@@ -464,12 +464,15 @@ int wide_block_queries(int row_bytes);  // screen_wide.hip
 
 int screen_query_block(bool f16, int row_bytes, int64_t nq_pad)
 {
-  return f16 && row_bytes > 256 ? wide_block_queries(row_bytes) : screen_block_queries(nq_pad);
+  (void)f16;  // rows of more than 256 bytes (fp16 or int8) take the K-loop anchor pass's blocks
+  return row_bytes > 256 ? wide_block_queries(row_bytes) : screen_block_queries(nq_pad);
 }
 
 void screen_i8(const screen_args& a, hipStream_t stream)
 {
-  if (a.filter.kind != 0) {
+  if (a.row_bytes > 256) {  // int8 rows of more than 256 coordinates: the tiled screen
+    screen_i8_tile(a, stream);
+  } else if (a.filter.kind != 0) {
     launch<int8_rows, false, true>(a, stream);
   } else {
     launch<int8_rows, false, false>(a, stream);
@@ -478,7 +481,9 @@ void screen_i8(const screen_args& a, hipStream_t stream)
 
 void anchors_i8(const screen_args& a, hipStream_t stream)
 {
-  if (a.filter.kind != 0) {
+  if (a.row_bytes > 256) {  // the K-loop anchor pass (or its tiled form over anchor pairs)
+    anchors_i8_wide(a, stream);
+  } else if (a.filter.kind != 0) {
     launch<int8_rows, true, true>(a, stream);
   } else {
     launch<int8_rows, true, false>(a, stream);

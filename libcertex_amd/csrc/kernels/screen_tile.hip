@@ -1,5 +1,6 @@
-// fp16 certified screen for rows of more than 128 halves (gfx950): LDS-staged tiles of rows and
-// queries, both fed to the MFMA from LDS, two workgroups resident per CU.
+// Screen for rows of more than 256 bytes (gfx950): fp16 rows of more than 128 halves (certified)
+// and int8 rows of more than 256 coordinates (exact); LDS-staged tiles of rows and queries, both
+// fed to the MFMA from LDS, two workgroups resident per CU.
 //
 // Reference contract: detail/screen_sm80.cu:117-379 and detail/screen_sm90.cu:594-785 (fp16 MMA,
 // fp32 accumulation, keep a pair iff its screen value reaches the query threshold; the reference
@@ -9,7 +10,7 @@
 //
 // Work decomposition:
 // - a workgroup of 4 waves computes one tile of 256 stored rows x 128 queries, all of the row's
-//   halves, in stages of 32 halves (64 bytes of every row and query, one MFMA k-step);
+//   bytes, in stages of 64 bytes of every row and query (one MFMA k-step: 32 halves or 64 int8);
 // - two workgroups share a CU (73.5 KB of LDS and 4 waves each, 2 waves per SIMD), so that one
 //   workgroup's barriers, copies' latency, survivor epilogue and flush overlap the other's MFMAs;
 // - a stage of both operands is copied into LDS by global_load_lds_dwordx4 (no VGPRs): a copy
@@ -27,16 +28,16 @@
 //   of stage s a wave waits for its own copies of stage s only (those of s + 1 stay in flight),
 //   then one barrier publishes stage s and frees the buffer of stage s - 1;
 // - the waves form a 2 x 2 grid: wave (wr, wq) multiplies tile rows 128 wr .. 128 wr + 127 (8 row
-//   tiles) with tile queries 64 wq .. 64 wq + 63 (4 query tiles), v_mfma_f32_16x16x32_f16, the row
-//   tiles as operand A: 128 accumulator registers per lane. Chunk lane / 16 of a stage's 64 bytes
-//   is the k-slice of a lane in both operands (the same permutation of the summation order);
+//   tiles) with tile queries 64 wq .. 64 wq + 63 (4 query tiles), v_mfma_f32_16x16x32_f16 (fp16)
+//   or v_mfma_i32_16x16x64_i8 (int8), the row tiles as operand A: 128 accumulator registers per
+//   lane. Chunk lane / 16 of a stage's 64 bytes is the k-slice of a lane in both operands;
 // - the row terms and the query thresholds are copied into LDS with the first stages;
 // - after the last stage the staging LDS holds the survivor list. Per query tile a lane has 32
 //   rows; the wave reserves its survivors with one LDS atomic (exclusive prefix of the lanes'
 //   counts from one ballot + mbcnt per bit of the count), the lanes park their 32 screen values in
 //   LDS and write each survivor with its value read back by bit index (a per-survivor select over
-//   registers cost twice as much), then one flush per workgroup moves the list into the per-query
-//   buckets (flush_hits of screen_common.hpp).
+//   registers cost twice as much; int8 rows carry no value), then one flush per workgroup moves the
+//   list into the per-query buckets (flush_hits of screen_common.hpp).
 // Workgroup b runs on XCD b % 8; the query blocks of one row tile run on one XCD (work_of), so a
 // row tile is fetched from HBM about once.
 //
@@ -132,13 +133,14 @@ struct tile_shape {
   static_assert(WR * WQ == kTileWaves && WR * 16 * RT == kTileRows, "4 waves cover the tile");
 };
 
-template <int RT, int QT, bool FILT, bool ANCH>
+template <typename R, int RT, int QT, bool FILT, bool ANCH>
 __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_args a)
 {
-  using R           = f16_rows;
-  using acc_t       = v4f;
-  using frag_t      = v8h;
+  using acc_t       = typename R::acc_t;
+  using frag_t      = typename R::frag_t;
+  using val_t       = typename R::val_t;
   using S           = tile_shape<RT, QT>;
+  static_assert(sizeof(frag_t) == 16 && sizeof(val_t) == 4, "16-byte operands, 4-byte values");
   constexpr int TQ  = S::TQ;
   constexpr int CA  = kTileRows / 16 / kTileWaves;  // row copies per wave and stage
   constexpr int CB  = TQ / 16 / kTileWaves;         // query copies per wave and stage
@@ -184,15 +186,15 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
   // indices past the live queries and rows repeat the last live one (the slot before a group's
   // first live one reads its neighbour, in the same allocation)
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  float* th_lds    = reinterpret_cast<float*>(lds + tile_lds(TQ));
-  float* rc_lds    = th_lds + TQ;
+  val_t* th_lds    = reinterpret_cast<val_t*>(lds + tile_lds(TQ));
+  val_t* rc_lds    = th_lds + TQ;
   {
     const int64_t r = wave_u * 64 + lane;
-    lds_copy<4>(static_cast<const float*>(a.rowc) + row_t0 + tile_rel(r < n_rows ? r : n_rows - 1),
+    lds_copy<4>(static_cast<const val_t*>(a.rowc) + row_t0 + tile_rel(r < n_rows ? r : n_rows - 1),
                 lds_addr(rc_lds + wave_u * 64));
     if (!ANCH && wave_u * 64 < TQ) {
       const int64_t q = wave_u * 64 + lane;
-      lds_copy<4>(static_cast<const float*>(a.theta) + w.q0 + (q < n_q ? q : n_q - 1),
+      lds_copy<4>(static_cast<const val_t*>(a.theta) + w.q0 + (q < n_q ? q : n_q - 1),
                   lds_addr(th_lds + wave_u * 64));
     }
   }
@@ -312,7 +314,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
 
   if constexpr (ANCH) {
     // fine groups: the 4 consecutive anchors of a lane's row tile are one group of the table
-    float* gmax = static_cast<float*>(a.gmax);
+    val_t* gmax = static_cast<val_t*>(a.gmax);
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       const int qloc  = wq * 16 * QT + qt * 16 + frow;
@@ -321,7 +323,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
       for (int bt = 0; bt < RT; ++bt) {
         const int64_t first = scan0 + wr * 16 * RT + bt * 16 + fch * 4;  // scan index
         const acc_t v       = acc[bt][qt];
-        const float m       = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+        const val_t m       = R::vmax(R::vmax(v[0], v[1]), R::vmax(v[2], v[3]));
         if (live && first < w.n_scan) { gmax[table_entry(a, w.q0 + qloc, first / kFineGroup)] = m; }
       }
     }
@@ -331,7 +333,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
 
   uint32_t* hit_q    = reinterpret_cast<uint32_t*>(lds);
   uint32_t* hit_row  = hit_q + CAP;
-  float* hit_val     = reinterpret_cast<float*>(hit_row + CAP);
+  float* hit_val     = reinterpret_cast<float*>(hit_row + CAP);  // fp16 rows only
   uint32_t* scratch  = reinterpret_cast<uint32_t*>(hit_val + CAP);  // 2 TQ + CAP words
   // per wave 8 KB: a lane's 4 RT screen values of one query tile, 16-byte slot bt ^ (lane & 7) of
   // its 128 bytes, so that the survivor loop reads a value by its bit index
@@ -340,8 +342,8 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int qloc = wq * 16 * QT + qt * 16 + frow;
-    // a padding query keeps nothing: no value compares >= NaN
-    const float th = qloc >= q_lo && qloc < n_q ? th_lds[qloc] : R::keep_none();
+    // a padding query keeps nothing (fp16: no value compares >= NaN; int8: none reaches the max)
+    const val_t th = qloc >= q_lo && qloc < n_q ? th_lds[qloc] : R::keep_none();
     uint32_t bits  = 0;  // bit bt * 4 + r: row row0 + 16 bt + r
 #pragma unroll
     for (int bt = 0; bt < RT; ++bt) {
@@ -359,9 +361,11 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
         }
       }
     }
+    if constexpr (R::kValues) {
 #pragma unroll
-    for (int bt = 0; bt < RT; ++bt) {
-      *reinterpret_cast<acc_t*>(vals + ((bt ^ (lane & 7)) << 4)) = acc[bt][qt];
+      for (int bt = 0; bt < RT; ++bt) {
+        *reinterpret_cast<acc_t*>(vals + ((bt ^ (lane & 7)) << 4)) = acc[bt][qt];
+      }
     }
     const uint32_t cnt = uint32_t(__builtin_popcount(bits));
     uint32_t excl = 0, total = 0;
@@ -380,33 +384,36 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
       const int j        = __builtin_ctz(bits);
       bits &= bits - 1;
       const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
-      const float val    = *reinterpret_cast<const float*>(vals + ((((j >> 2) ^ (lane & 7)) << 4) | ((j & 3) << 2)));
+      float val          = 0;
+      if constexpr (R::kValues) {
+        val = *reinterpret_cast<const float*>(vals + ((((j >> 2) ^ (lane & 7)) << 4) | ((j & 3) << 2)));
+      }
       if (pos < uint32_t(CAP)) {
         hit_q[pos]   = uint32_t(qloc);
         hit_row[pos] = row;
-        hit_val[pos] = val;
+        if constexpr (R::kValues) { hit_val[pos] = val; }
       } else if (int64_t(pos - CAP) < a.spill_cap) {
         const int64_t e = int64_t(blockIdx.x) * a.spill_cap + int64_t(pos - CAP);
         a.spill_q[e]    = uint32_t(qloc);
         a.spill_row[e]  = row;
-        a.spill_val[e]  = val;
+        if constexpr (R::kValues) { a.spill_val[e] = val; }
       } else {
         const int64_t q   = w.q0 + qloc;
         const uint32_t at = atomicAdd(a.cand_count + q, 1u);
         if (at < a.cap) {
           a.cand_rows[q * a.cap + at] = row;
-          a.cand_vals[q * a.cap + at] = val;
+          if constexpr (R::kValues) { a.cand_vals[q * a.cap + at] = val; }
         }
       }
       ++pos;
     }
   }
   __syncthreads();
-  flush_hits<true>(w.q0, TQ, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(CAP), scratch);
+  flush_hits<R::kValues>(w.q0, TQ, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(CAP), scratch);
   clk.stop(a);
 }
 
-template <int RT, int QT, bool FILT, bool ANCH>
+template <typename R, int RT, int QT, bool FILT, bool ANCH>
 void launch_shape(const screen_args& a, hipStream_t stream)
 {
   constexpr int TQ = tile_shape<RT, QT>::TQ;
@@ -431,7 +438,7 @@ void launch_shape(const screen_args& a, hipStream_t stream)
   }
   screen_args b = a;
   b.spill_cap   = !ANCH && a.spill_q != nullptr ? a.spill_pool / blocks : 0;
-  auto* k       = &screen_tile_kernel<RT, QT, FILT, ANCH>;
+  auto* k       = &screen_tile_kernel<R, RT, QT, FILT, ANCH>;
   const int lds = tile_lds_total(TQ);
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(k),
                           hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) {
@@ -450,12 +457,29 @@ int tile_block_queries() { return tile_shape<8, 4>::TQ; }
 void screen_f16_tile(const screen_args& a, hipStream_t stream)
 {
   if (a.filter.kind != 0) {
-    launch_shape<8, 4, true, false>(a, stream);
+    launch_shape<f16_rows, 8, 4, true, false>(a, stream);
   } else {
-    launch_shape<8, 4, false, false>(a, stream);
+    launch_shape<f16_rows, 8, 4, false, false>(a, stream);
   }
 }
 
-void anchors_f16_tile(const screen_args& a, hipStream_t stream) { launch_shape<8, 4, false, true>(a, stream); }
+void anchors_f16_tile(const screen_args& a, hipStream_t stream)
+{
+  launch_shape<f16_rows, 8, 4, false, true>(a, stream);
+}
+
+void screen_i8_tile(const screen_args& a, hipStream_t stream)
+{
+  if (a.filter.kind != 0) {
+    launch_shape<int8_rows, 8, 4, true, false>(a, stream);
+  } else {
+    launch_shape<int8_rows, 8, 4, false, false>(a, stream);
+  }
+}
+
+void anchors_i8_tile(const screen_args& a, hipStream_t stream)
+{
+  launch_shape<int8_rows, 8, 4, false, true>(a, stream);
+}
 
 }  // namespace certex_amd

@@ -1,21 +1,22 @@
-// fp16 anchor pass for rows of more than 128 halves (gfx950): a K loop over the coordinates.
+// Anchor pass for rows of more than 256 bytes (gfx950): fp16 rows of more than 128 halves and
+// int8 rows of more than 256 coordinates, a K loop over the row's bytes.
 //
 // Reference contract: the anchor groups of detail/kernels.hpp:125-135 and detail/screen_sm80.cu:
 // 304-372 (fp16 MMA, fp32 accumulation, the best screen value of every group of anchors for every
-// query). The screen pass of such rows is screen_tile.hip. The certificate is the one of
-// screen.hip: the row term enters as the accumulator's initial value.
+// query) and, for int8 rows, the exact int32 screen values of screen.hip. The screen pass of such
+// rows is screen_tile.hip. The row term enters as the accumulator's initial value.
 //
 // Work decomposition:
-// - a workgroup of 8 waves holds QB = 16 QT queries (all their halves) in LDS for its whole life,
+// - a workgroup of 8 waves holds QB = 16 QT queries (all their bytes) in LDS for its whole life,
 //   16-byte chunks XOR-swizzled by the query (chunk c of query r sits in slot c ^ (r & 15)), so
 //   the ds_read_b128 of a 16-query fragment is free of bank conflicts;
 // - each wave streams its own contiguous eighth of a chunk of stored rows, 64 rows per step, and
-//   runs the K loop in chunks of 64 halves; the next chunk's row fragments are loaded into a
+//   runs the K loop in chunks of 128 bytes; the next chunk's row fragments are loaded into a
 //   second register set while the MFMAs of the current chunk run. No barrier in the main loop.
-// - within a 64-half chunk, lane group g = lane / 16 supplies halves 16 g .. 16 g + 7 to the first
-//   v_mfma_f32_16x16x32_f16 and 16 g + 8 .. 16 g + 15 to the second, in both operands (a
-//   permutation of the summation order), so a row's fragments are 32 contiguous bytes per lane
-//   group. The rows are loaded with the 4 lanes of a quad on one row's 128-byte line (the memory
+// - within a 128-byte chunk, lane group g = lane / 16 supplies bytes 32 g .. 32 g + 15 to the
+//   first MFMA (v_mfma_f32_16x16x32_f16: 8 halves; v_mfma_i32_16x16x64_i8: 16 int8) and 32 g + 16
+//   .. 32 g + 31 to the second, in both operands (a permutation of the summation order), so a
+//   row's fragments are 32 contiguous bytes per lane group. The rows are loaded with the 4 lanes of a quad on one row's 128-byte line (the memory
 //   pipeline serves a quad that shares a line at once, and 16 lanes on 16 rows one line at a
 //   time), and 4 ds_bpermute per 16 bytes move them to the MFMA's lanes;
 // - block b runs on XCD b % 8; the query blocks of one row chunk run on one XCD together.
@@ -37,31 +38,32 @@ constexpr int kWideWaves = 8;
 /** Pointers into global memory, so that loads through them stay global (never flat) loads. */
 typedef const __attribute__((address_space(1))) int8_t* gbytes;
 
-__device__ __forceinline__ v8h gload(gbytes p)
+template <typename F>
+__device__ __forceinline__ F gload(gbytes p)
 {
-  return *reinterpret_cast<const __attribute__((address_space(1))) v8h*>(p);
+  return *reinterpret_cast<const __attribute__((address_space(1))) F*>(p);
 }
 
-template <int QT, bool FILT>
+template <typename R, int QT, bool FILT>
 __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_args a)
 {
-  using R      = f16_rows;
-  using acc_t  = v4f;
-  using frag_t = v8h;
+  using acc_t  = typename R::acc_t;
+  using frag_t = typename R::frag_t;
+  using val_t  = typename R::val_t;
+  static_assert(sizeof(frag_t) == 16, "a lane's MFMA operand is 16 bytes");
   constexpr int QB = 16 * QT;
-  // dynamic LDS: the queries [QB][H] halves (swizzled)
+  // dynamic LDS: the queries [QB][row_bytes] (swizzled)
   extern __shared__ __attribute__((aligned(16))) uint8_t qlds[];
-  __shared__ float gml[kWideWaves * QB];
+  __shared__ val_t gml[kWideWaves * QB];
 
-  const float* rowc = static_cast<const float*>(a.rowc);
-  float* gmax       = static_cast<float*>(a.gmax);
+  const val_t* rowc = static_cast<const val_t*>(a.rowc);
+  val_t* gmax       = static_cast<val_t*>(a.gmax);
 
   const int tid   = threadIdx.x;
   const int lane  = tid & 63;
   const int wave  = tid >> 6;
-  const int H     = a.row_bytes / 2;  // halves per row, a multiple of 128
-  const int NC    = H / 64;           // K chunks, even
-  const int RB    = a.row_bytes;      // bytes per row (stored rows and LDS query rows)
+  const int RB    = a.row_bytes;      // bytes per row (stored rows and LDS query rows), a multiple of 256
+  const int NC    = RB / 128;         // K chunks of 128 bytes, even
 
   const screen_work w = work_of<QB>(a, blockIdx.x);
   if (!w.valid) { return; }
@@ -86,13 +88,13 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
   // and a lane keeps 4 offsets per step instead of 4 pointers (64-bit pointers for this and the
   // next step pushed the kernel past 256 VGPRs). Every load of the main loop is unconditional,
   // so that the compiler's wait counts see one straight path and the prefetches stay in flight.
-  // Paired rows (rows_paired): byte b of stored row R at paired_offset(R, b); a 64-half chunk of a
+  // Paired rows (rows_paired): byte b of stored row R at paired_offset(R, b); a 128-byte chunk of a
   // row is then two 64-byte pieces 128 bytes apart, lanes 0-1 of a quad on the first and 2-3 on
   // the second, and chunk c starts 256 c bytes into the pair.
   const gbytes codes     = (gbytes)a.codes;
   const bool rp          = a.rows_paired;
-  const int64_t cstep    = rp ? 256 : 128;  // bytes between consecutive 64-half chunks of a row
-  auto row_at = [&](int64_t R) { return rp ? (R & ~int64_t(1)) * RB + (R & 1) * 64 : R * RB; };
+  const int64_t cstep    = rp ? 256 : 128;  // bytes between consecutive 128-byte chunks of a row
+  auto row_at = [&](int64_t sr) { return rp ? (sr & ~int64_t(1)) * RB + (sr & 1) * 64 : sr * RB; };
   // stored row of scan index i: one row every row_stride, or with anchor pairs both rows of a
   // pair every 2 row_stride from an even base (the two quads of a pair then read one whole line)
   const bool apairs = a.anchor_pairs;
@@ -117,8 +119,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
                         frag_t (&A)[4][2]) {
 #pragma unroll
     for (int bt = 0; bt < 4; ++bt) {
-      A[bt][0] = gload(base + off + O[bt]);
-      A[bt][1] = gload(base + off + 16 + O[bt]);
+      A[bt][0] = gload<frag_t>(base + off + O[bt]);
+      A[bt][1] = gload<frag_t>(base + off + 16 + O[bt]);
     }
   };
   auto load_terms = [&](int64_t s) {
@@ -128,7 +130,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const bool ok  = r4 + j < w.n_scan;
-        const float v  = rowc[row_of(ok ? r4 + j : 0)];
+        const val_t v  = rowc[row_of(ok ? r4 + j : 0)];
         cc[bt][j]      = ok ? v : R::dead();
       }
     }
@@ -236,10 +238,10 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void screen_wide_kernel(screen_
   }
 }
 
-template <int QT, bool FILT>
+template <typename R, int QT, bool FILT>
 void launch_qt(const screen_args& a, dim3 grid, size_t lds, hipStream_t stream)
 {
-  auto* k = &screen_wide_kernel<QT, FILT>;
+  auto* k = &screen_wide_kernel<R, QT, FILT>;
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(k),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess) {
     (void)hipGetLastError();
@@ -264,24 +266,27 @@ int max_lds()
 }
 
 /**
- * Query tiles of a workgroup for rows of `row_bytes`: the largest of 6, 4, 2 whose queries and
+ * Query tiles of a workgroup for rows of `row_bytes`: the largest of 6, 4, 2, 1 whose queries and
  * the group table (gml: 4 bytes per query per wave, counted as 8) fit the LDS (0: none fits). More queries
  * per workgroup means more work per row fetched.
  */
 int wide_query_tiles(int row_bytes)
 {
-  for (int qt : {6, 4, 2}) {
+  for (int qt : {6, 4, 2, 1}) {
     if (16 * qt * (row_bytes + 8 * kWideWaves) <= max_lds()) { return qt; }
   }
   return 0;
 }
 
-template <bool FILT>
+template <typename R, bool FILT>
 void launch(const screen_args& a, hipStream_t stream)
 {
   const int qt = wide_query_tiles(a.row_bytes);
   const int qb = 16 * qt;
-  if (qt == 0) { throw std::invalid_argument("certex: the fp16 rows are too wide for the LDS"); }
+  if (qt == 0) { throw std::invalid_argument("certex: the rows are too wide for the LDS"); }
+  if (a.row_bytes % 256 != 0) {
+    throw std::logic_error("certex: the K-loop anchor pass takes rows of whole 256-byte pairs of chunks");
+  }
   int64_t blocks = 0;
   if (a.groups != nullptr) {
     blocks = a.n_tiles;
@@ -298,9 +303,10 @@ void launch(const screen_args& a, hipStream_t stream)
   const dim3 grid{unsigned(blocks)};
   const size_t lds = size_t(qb) * size_t(a.row_bytes);
   switch (qt) {
-    case 6: launch_qt<6, FILT>(a, grid, lds, stream); break;
-    case 4: launch_qt<4, FILT>(a, grid, lds, stream); break;
-    default: launch_qt<2, FILT>(a, grid, lds, stream); break;
+    case 6: launch_qt<R, 6, FILT>(a, grid, lds, stream); break;
+    case 4: launch_qt<R, 4, FILT>(a, grid, lds, stream); break;
+    case 2: launch_qt<R, 2, FILT>(a, grid, lds, stream); break;
+    default: launch_qt<R, 1, FILT>(a, grid, lds, stream); break;
   }
 }
 
@@ -313,9 +319,20 @@ void anchors_f16_wide(const screen_args& a, hipStream_t stream)
   if (a.tiled) {
     anchors_f16_tile(a, stream);
   } else if (a.filter.kind != 0) {
-    launch<true>(a, stream);
+    launch<f16_rows, true>(a, stream);
   } else {
-    launch<false>(a, stream);
+    launch<f16_rows, false>(a, stream);
+  }
+}
+
+void anchors_i8_wide(const screen_args& a, hipStream_t stream)
+{
+  if (a.tiled) {
+    anchors_i8_tile(a, stream);
+  } else if (a.filter.kind != 0) {
+    launch<int8_rows, true>(a, stream);
+  } else {
+    launch<int8_rows, false>(a, stream);
   }
 }
 

@@ -187,12 +187,17 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
  *   inner: -sum (q + bias)(x + bias) = -(<q, x> + bias (sum q + sum x) + bias^2 dim)
  * qq = |q|^2 and qs = sum q of the query codes. Each 16-byte load feeds twelve v_dot4_i32_i8.
  */
-__device__ inline double int_score(const int8_t* qv, const int8_t* xrow, int row_bytes,
-                                   int64_t dim, int bias, int qq, int qs, metric_kind metric)
+__device__ inline double int_score(const int8_t* qv, const int8_t* base, int64_t r, bool paired,
+                                   int row_bytes, int64_t dim, int bias, int qq, int qs,
+                                   metric_kind metric)
 {
   int qx = 0, xx = 0, xs = 0;
+  // row r of `base`: contiguous, or in the paired layout (a wide label partition), where each
+  // 16-byte chunk lies whole inside one 64-byte piece
+  const int8_t* xrow = base + (paired ? (r >> 1) * 2 * int64_t(row_bytes) + (r & 1) * 64 : r * int64_t(row_bytes));
   for (int j = 0; j < row_bytes; j += 16) {
-    const v4i_t x  = *reinterpret_cast<const v4i_t*>(xrow + j);
+    const int jo   = paired ? (j >> 6) * 128 + (j & 63) : j;
+    const v4i_t x  = *reinterpret_cast<const v4i_t*>(xrow + jo);
     const v4i_t qw = *reinterpret_cast<const v4i_t*>(qv + j);
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
@@ -467,15 +472,17 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a,
         live = true;
       }
       uint32_t id;
+      bool paired = false;
       if (!a.all_rows && a.part_ids != nullptr && r < a.n_part) {
-        base = a.part_codes;
-        id   = uint32_t(a.part_ids[r]);
+        base   = a.part_codes;
+        paired = a.part_paired;
+        id     = uint32_t(a.part_ids[r]);
       } else {
         id = listed_id(a.filter, r);
       }
       if (live) {
         const double s =
-          int_score(qv, base + int64_t(r) * a.row_bytes, a.row_bytes, a.dim, bias, qq, qs, a.metric);
+          int_score(qv, base, r, paired, a.row_bytes, a.dim, bias, qq, qs, a.metric);
         const int slot = have + atomicAdd(&fill, 1);
         key[slot]      = score_key(s);
         rid[slot]      = id;
@@ -528,12 +535,13 @@ constexpr int kSmallBucket = 512;
  */
 __global__ __launch_bounds__(kThreads) void verify_topk_i8_small_kernel(verify_args a)
 {
-  __shared__ __attribute__((aligned(16))) int8_t qlds[kThreads / 64][kMaxIntDim];
+  // dynamic LDS: the query codes of the block's waves [kThreads / 64][row_bytes]
+  extern __shared__ __attribute__((aligned(16))) int8_t qlds[];
   const int lane    = threadIdx.x & 63;
   const int wave    = threadIdx.x >> 6;
   const int64_t q   = int64_t(blockIdx.x) * (kThreads / 64) + wave;
   const bool live_q = q < a.nq;
-  int8_t* qv        = qlds[wave];
+  int8_t* qv        = qlds + wave * a.row_bytes;
   if (live_q) {
     for (int j = lane; j < a.row_bytes; j += 64) { qv[j] = a.qcodes[q * a.row_bytes + j]; }
   }
@@ -557,13 +565,15 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_small_kernel(verify_a
       const uint32_t r   = cand[e];
       const int8_t* base = a.codes;
       uint32_t id;
+      bool paired = false;
       if (a.part_ids != nullptr && r < a.n_part) {
-        base = a.part_codes;
-        id   = uint32_t(a.part_ids[r]);
+        base   = a.part_codes;
+        paired = a.part_paired;
+        id     = uint32_t(a.part_ids[r]);
       } else {
         id = listed_id(a.filter, r);
       }
-      key[i] = score_key(int_score(qv, base + int64_t(r) * a.row_bytes, a.row_bytes, a.dim, bias,
+      key[i] = score_key(int_score(qv, base, r, paired, a.row_bytes, a.dim, bias,
                                    qq, qs, a.metric));
       rid[i] = id;
     }
@@ -1555,7 +1565,8 @@ void verify_topk_i8(const verify_args& a, hipStream_t stream)
   if (!a.all_rows && a.k <= 64) {
     // buckets of up to kSmallBucket candidates: one wave per query; the block kernel then takes
     // only the larger buckets (launched when the host saw one)
-    verify_topk_i8_small_kernel<<<unsigned((a.nq + 3) / 4), kThreads, 0, stream>>>(a);
+    verify_topk_i8_small_kernel<<<unsigned((a.nq + 3) / 4), kThreads,
+                                  size_t(kThreads / 64) * size_t(a.row_bytes), stream>>>(a);
     if (a.max_cand >= 0 && a.max_cand <= kSmallBucket) { return; }
     b.small_max = kSmallBucket;
   }
@@ -1563,7 +1574,7 @@ void verify_topk_i8(const verify_args& a, hipStream_t stream)
   // blocks share a CU
   int cap = pow2_ge(2 * a.k);
   cap     = cap > 1024 ? (cap < kBuf ? cap : kBuf) : 1024;
-  const size_t bytes = size_t(cap) * 12 + kMaxIntDim;
+  const size_t bytes = size_t(cap) * 12 + size_t(a.row_bytes);
   verify_topk_i8_kernel<<<unsigned(a.nq), kThreads, bytes, stream>>>(b, cap);
 }
 

@@ -9,7 +9,8 @@ the certified bound U of each query and the certificate's two bounds of every bu
 against a CPU brute force:
 
 int8 rows (exact integer screen):
-- the stored codes and row terms are the encoding of the vectors (x ^ 0x80, -floor(|x'|^2 / 2));
+- the stored codes and row terms are the encoding of the vectors (x ^ 0x80, -floor(|x'|^2 / 2)),
+  for rows of 128 bytes (the narrow screen) and of 512 bytes (the tiled screen, K-loop anchors);
 - every group maximum equals the largest <q', x'> + rowc over the group's anchors;
 - theta is the k-th largest group maximum (floored at the keep-all value), and no row of the true
   top k (ties at the k-th value included) lies below it;
@@ -79,40 +80,42 @@ def groups_of(n_anchor, fine, group_steps):
 # --- int8 rows -------------------------------------------------------------------------------
 
 
-def int8_case(n, nq, kind, seed):
+def int8_case(n, nq, kind, seed, d=128):
     rng = np.random.default_rng(seed)
     if kind == "uint8":
-        X = data.mixture_u8(n, seed=seed)
-        Q = data.mixture_u8(nq, seed=seed + 1)
+        X = data.mixture_u8(n, d=d, seed=seed)
+        Q = data.mixture_u8(nq, d=d, seed=seed + 1)
         X[:50] = 0  # extreme codes (-128) and exact ties
         X[50:100] = 255
         X[100:400] = X[400:700]  # duplicated rows: ties at every distance
         Q[:4] = X[400:404]  # queries on duplicated rows
     else:
-        X = data.uniform_int(n, 128, seed, np.int8)
-        Q = data.uniform_int(nq, 128, seed + 1, np.int8)
+        X = data.uniform_int(n, d, seed, np.int8)
+        Q = data.uniform_int(nq, d, seed + 1, np.int8)
         X[:64] = -128
     removed = rng.choice(n, n // 50, replace=False)
     return X, Q, removed
 
 
-@pytest.mark.parametrize("n, k, kind, metric", [
-    (200_000, 10, "uint8", "l2"),     # fine anchor groups (4 anchors each)
-    (200_000, 64, "uint8", "ip"),
-    (1_200_000, 10, "uint8", "l2"),   # coarse anchor groups (whole 64-anchor steps)
-    (150_000, 32, "int8", "l2"),
-    (150_000, 10, "int8", "ip"),
+@pytest.mark.parametrize("n, k, kind, metric, d", [
+    (200_000, 10, "uint8", "l2", 128),     # fine anchor groups (4 anchors each)
+    (200_000, 64, "uint8", "ip", 128),
+    (1_200_000, 10, "uint8", "l2", 128),   # coarse anchor groups (whole 64-anchor steps)
+    (150_000, 32, "int8", "l2", 128),
+    (150_000, 10, "int8", "ip", 128),
+    (120_000, 10, "uint8", "l2", 384),     # rows of 512 bytes: the tiled int8 screen, K-loop anchors
+    (700_000, 10, "uint8", "ip", 300),     # coarse groups in the K-loop anchor pass
 ])
-def test_int8_screen(gpu, n, k, kind, metric):
+def test_int8_screen(gpu, n, k, kind, metric, d):
     nq = 96
-    X, Q, removed = int8_case(n, nq, kind, seed=n % 97 + k)
-    idx = certex.Index(128, metric=metric)
+    X, Q, removed = int8_case(n, nq, kind, seed=n % 97 + k, d=d)
+    idx = certex.Index(d, metric=metric)
     idx.add(torch.from_numpy(X).cuda())
     idx.remove(torch.from_numpy(removed))
     Qg = torch.from_numpy(Q).cuda()
     get = captured(lambda: idx.search(Qg, k=k, batch=nq))
     B, size, rb = int(get("B")), int(get("size")), int(get("row_bytes"))
-    assert (B, size, rb) == (nq, n, 128) and not get("all_rows")
+    assert (B, size, rb) == (nq, n, 128 if d <= 128 else (d + 255) // 256 * 256) and not get("all_rows")
 
     # the encoding of the rows and queries
     flip = 0x80 if kind == "uint8" else 0
@@ -120,8 +123,8 @@ def test_int8_screen(gpu, n, k, kind, metric):
     rowc = get("rowc", np.int32).astype(np.int64)
     qrows = get("qrows", np.int8, (B, rb)).astype(np.int64)
     xc = (X.view(np.uint8) ^ flip).view(np.int8).astype(np.int64)
-    assert np.array_equal(codes[:, :128], xc)
-    assert np.array_equal(qrows[:, :128], (Q.view(np.uint8) ^ flip).view(np.int8).astype(np.int64))
+    assert np.array_equal(codes[:, :d], xc) and not codes[:, d:].any()
+    assert np.array_equal(qrows[:, :d], (Q.view(np.uint8) ^ flip).view(np.int8).astype(np.int64))
     live = np.ones(n, bool)
     live[removed] = False
     if metric == "l2":
@@ -232,7 +235,7 @@ def test_fp16_certificate(gpu, kind, d, metric, k):
     lb = get("lb", np.float64, (B, cap))
     ub = get("ub", np.float64, (B, cap))
     U = get("ub_q", np.float64)
-    gamma = float(get("gamma", np.float64))
+    gamma = float(get("gamma", np.float64)[0])
     z = get("codes", np.float16, (size, halves)).astype(np.float64)
     w = get("qrows", np.float16, (B, halves)).astype(np.float64)
     rowc = get("rowc", np.float32).astype(np.float64)
