@@ -1138,59 +1138,71 @@ using batch_fn = void (*)(cuvs::resources const&, index_state const&, const void
  * Label search of one batch over the label partition (reference search_by_labels,
  * certex.cu:1613-1735): the queries in label order (stable), one routed group per label that has
  * partition rows, the tail through the label filter, and the results back in query order.
+ *
+ * Query labels in host memory are sorted and grouped on the host (exact workgroup counts, no wait
+ * for the GPU). Labels in device memory never come back: a stable radix sort of the batch's labels
+ * and route_tables build the groups on the device, one per label of the partition, and each pass
+ * is launched with an upper bound of its workgroups (route_tiles_bound), the ones past the last
+ * group exiting at once.
  */
 void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn batch,
                   const char* queries, size_t qrow, int64_t B, int k, const int32_t* qlabels,
                   const int32_t* hlabels, int64_t* neighbors, float* distances,
                   certex_amd::filter_args fa, search_params const& params)
 {
-  auto& rs           = res.state();
-  hipStream_t stream = rs.stream;
-  std::vector<int32_t> lab(static_cast<size_t>(B)), order(static_cast<size_t>(B)),
-    sorted(static_cast<size_t>(B));
-  if (hlabels != nullptr) {
-    std::copy(hlabels, hlabels + B, lab.begin());  // host labels: no read-back, no wait
+  auto& rs             = res.state();
+  hipStream_t stream   = rs.stream;
+  const bool on_device = hlabels == nullptr;
+  const auto& off      = st.label_part.offsets;
+  const int64_t n_lab  = int64_t(off.size()) - 1;
+  std::vector<int32_t> order, sorted;
+  std::vector<certex_amd::screen_group> ga, gs;
+  if (!on_device) {
+    // queries in label order, stable: a counting sort when the batch's labels span a small range
+    // (one pass, no comparisons), else a comparison sort
+    const int32_t* lab = hlabels;
+    order.resize(size_t(B));
+    sorted.resize(size_t(B));
+    const auto [lo_it, hi_it] = std::minmax_element(lab, lab + B);
+    const int64_t lo = B > 0 ? *lo_it : 0, span = B > 0 ? int64_t(*hi_it) - lo + 1 : 0;
+    if (span <= 4 * B + 1024) {
+      std::vector<int64_t> start(static_cast<size_t>(span) + 1, 0);
+      for (int64_t i = 0; i < B; ++i) { ++start[size_t(lab[i] - lo) + 1]; }
+      for (int64_t v = 0; v < span; ++v) { start[size_t(v) + 1] += start[size_t(v)]; }
+      for (int64_t i = 0; i < B; ++i) { order[size_t(start[size_t(lab[i] - lo)]++)] = int32_t(i); }
+    } else {
+      for (int64_t i = 0; i < B; ++i) { order[size_t(i)] = int32_t(i); }
+      std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return lab[a] < lab[b]; });
+    }
+    for (int64_t i = 0; i < B;) {
+      const int32_t l = lab[order[size_t(i)]];
+      int64_t j       = i;
+      while (j < B && lab[order[size_t(j)]] == l) { sorted[size_t(j++)] = l; }
+      if (l >= 0 && int64_t(l) < n_lab && off[size_t(l) + 1] > off[size_t(l)]) {
+        certex_amd::screen_group g{i, j - i, off[size_t(l)], off[size_t(l) + 1] - off[size_t(l)], 0};
+        ga.push_back(g);
+        gs.push_back(g);
+      }
+      i = j;
+    }
   } else {
-    // device labels come back through pinned staging (a pageable copy is staged by the runtime)
-    auto* hl = static_cast<int32_t*>(rs.stage(std::max<size_t>(16, size_t(B) * 4)));
-    CERTEX_HIP_TRY(hipMemcpyAsync(hl, qlabels, size_t(B) * 4, hipMemcpyDeviceToHost, stream));
-    CERTEX_HIP_TRY(hipStreamSynchronize(stream));
-    std::copy(hl, hl + B, lab.begin());
+    // the groups the device will build, with queries spread over the labels as their rows are:
+    // the plan (stride, group columns, chunks) then does not depend on the labels of the batch
+    for (int64_t l = 0; l < n_lab; ++l) {
+      const int64_t nx = off[size_t(l) + 1] - off[size_t(l)];
+      if (nx == 0) { continue; }
+      const int64_t nq = std::max<int64_t>(1, (B * nx + st.label_part.n - 1) / std::max<int64_t>(1, st.label_part.n));
+      gs.push_back({0, nq, off[size_t(l)], nx, 0});
+    }
+    ga = gs;
   }
-  // queries in label order, stable: a counting sort when the batch's labels span a small range
-  // (one pass, no comparisons), else a comparison sort
-  const auto [lo_it, hi_it] = std::minmax_element(lab.begin(), lab.end());
-  const int64_t lo = B > 0 ? *lo_it : 0, span = B > 0 ? int64_t(*hi_it) - lo + 1 : 0;
-  if (span <= 4 * B + 1024) {
-    std::vector<int64_t> start(static_cast<size_t>(span) + 1, 0);
-    for (int64_t i = 0; i < B; ++i) { ++start[size_t(lab[size_t(i)] - lo) + 1]; }
-    for (int64_t v = 0; v < span; ++v) { start[size_t(v) + 1] += start[size_t(v)]; }
-    for (int64_t i = 0; i < B; ++i) { order[size_t(start[size_t(lab[size_t(i)] - lo)]++)] = int32_t(i); }
-  } else {
-    for (int64_t i = 0; i < B; ++i) { order[size_t(i)] = int32_t(i); }
-    std::stable_sort(order.begin(), order.end(),
-                     [&](int32_t a, int32_t b) { return lab[size_t(a)] < lab[size_t(b)]; });
-  }
+  int64_t max_nx = 0;
+  for (auto const& e : ga) { max_nx = std::max(max_nx, e.nx); }
 
   const int64_t nq_pad = certex_amd::pad_queries(B);
   const bool f16       = !is_int(st.type);
   const bool wide      = st.row_bytes > 256;
   const int qb         = certex_amd::screen_query_block(f16, st.row_bytes, nq_pad);
-  const auto& off      = st.label_part.offsets;
-  std::vector<certex_amd::screen_group> ga, gs;
-  int64_t max_nx = 0;
-  for (int64_t i = 0; i < B;) {
-    const int32_t l = lab[size_t(order[size_t(i)])];
-    int64_t j       = i;
-    while (j < B && lab[size_t(order[size_t(j)])] == l) { sorted[size_t(j++)] = l; }
-    if (l >= 0 && int64_t(l) + 1 < int64_t(off.size()) && off[size_t(l) + 1] > off[size_t(l)]) {
-      certex_amd::screen_group g{i, j - i, off[size_t(l)], off[size_t(l) + 1] - off[size_t(l)], 0};
-      ga.push_back(g);
-      gs.push_back(g);
-      max_nx = std::max(max_nx, g.nx);
-    }
-    i = j;
-  }
   // the largest label's anchors should form at least 4 k fine groups: below the index's stride,
   // a denser one (a query whose label still has fewer than k groups keeps all of its rows)
   const int stride = int(std::max<int64_t>(
@@ -1212,7 +1224,7 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   size_groups(route.ap, max_anchors, (st.size - st.label_part.n + stride - 1) / stride, nq_pad, k,
               &route.part_groups);
   const int64_t waves = waves_of(st);
-  // the screen's groups: the tiled screen's query blocks and 256-row chunks for wide fp16 rows;
+  // the screen's groups: the tiled screen's query blocks and 256-row chunks for wide rows;
   // so too the anchor pass over anchor pairs with fine groups (its tiles start at an even query)
   const bool tiled    = uses_tile_screen(st);
   route.anchor_tiled  = tiled && apairs && route.ap.fine;
@@ -1235,45 +1247,96 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
       for (auto const& e : gs) { t += certex_amd::screen_group_tiles(e.nq, e.nx, qb, int(c)); }
       return t;
     });
-  for (auto& e : ga) {
-    const int64_t nq   = e.nq + (e.q0 & alead);
-    e.tile0            = certex_amd::screen_group_tile0(route.anchor_tiles, nq, qba);
-    route.anchor_tiles =
-      e.tile0 + certex_amd::screen_group_tiles(nq, anchors_of(e), qba, route.anchor_chunk);
-  }
-  // the tiled screen aligns a group's query blocks (and, over paired rows, its tiles) to pairs
-  for (auto& e : gs) {
-    if (tiled) {
-      e.tile0            = certex_amd::screen_group_tile0(route.screen_tiles, e.nq + (e.q0 & 1), qbs);
-      route.screen_tiles = e.tile0 + certex_amd::paired_group_tiles(e, st.label_part.paired, qbs,
-                                                                    route.screen_chunk);
-    } else {
-      e.tile0            = certex_amd::screen_group_tile0(route.screen_tiles, e.nq, qbs);
-      route.screen_tiles = e.tile0 + certex_amd::screen_group_tiles(e.nq, e.nx, qbs, route.screen_chunk);
-    }
-  }
-  route.n_route = int(gs.size());
 
-  // device copies: order, sorted labels, the two group tables
   const size_t lab_bytes = (size_t(B) * 4 + 15) / 16 * 16;
-  const size_t tab_bytes = std::max<size_t>(1, gs.size()) * sizeof(certex_amd::screen_group);
-  char* dev = static_cast<char*>(rs.get(cuvs::detail::ws_route, 2 * lab_bytes + 2 * tab_bytes));
-  auto* d_order  = reinterpret_cast<int32_t*>(dev);
-  auto* d_sorted = reinterpret_cast<int32_t*>(dev + lab_bytes);
-  auto* d_ga     = reinterpret_cast<certex_amd::screen_group*>(dev + 2 * lab_bytes);
-  auto* d_gs     = reinterpret_cast<certex_amd::screen_group*>(dev + 2 * lab_bytes + tab_bytes);
-  // the four tables packed as on the device, in pinned staging, then one copy
-  const size_t all_bytes = 2 * lab_bytes + 2 * tab_bytes;
-  char* hs               = static_cast<char*>(rs.stage(all_bytes));
-  std::memcpy(hs, order.data(), size_t(B) * 4);
-  std::memcpy(hs + lab_bytes, sorted.data(), size_t(B) * 4);
-  if (!gs.empty()) {
-    std::memcpy(hs + 2 * lab_bytes, ga.data(), ga.size() * sizeof(ga[0]));
-    std::memcpy(hs + 2 * lab_bytes + tab_bytes, gs.data(), gs.size() * sizeof(gs[0]));
+  int32_t *d_order = nullptr, *d_sorted = nullptr;
+  if (!on_device) {
+    for (auto& e : ga) {
+      const int64_t nq   = e.nq + (e.q0 & alead);
+      e.tile0            = certex_amd::screen_group_tile0(route.anchor_tiles, nq, qba);
+      route.anchor_tiles =
+        e.tile0 + certex_amd::screen_group_tiles(nq, anchors_of(e), qba, route.anchor_chunk);
+    }
+    // the tiled screen aligns a group's query blocks (and, over paired rows, its tiles) to pairs
+    for (auto& e : gs) {
+      if (tiled) {
+        e.tile0            = certex_amd::screen_group_tile0(route.screen_tiles, e.nq + (e.q0 & 1), qbs);
+        route.screen_tiles = e.tile0 + certex_amd::paired_group_tiles(e, st.label_part.paired, qbs,
+                                                                      route.screen_chunk);
+      } else {
+        e.tile0            = certex_amd::screen_group_tile0(route.screen_tiles, e.nq, qbs);
+        route.screen_tiles = e.tile0 + certex_amd::screen_group_tiles(e.nq, e.nx, qbs, route.screen_chunk);
+      }
+    }
+    route.n_route = int(gs.size());
+    // device copies: order, sorted labels, the two group tables, packed as on the device in
+    // pinned staging, then one copy
+    const size_t tab_bytes = std::max<size_t>(1, gs.size()) * sizeof(certex_amd::screen_group);
+    char* dev = static_cast<char*>(rs.get(cuvs::detail::ws_route, 2 * lab_bytes + 2 * tab_bytes));
+    d_order  = reinterpret_cast<int32_t*>(dev);
+    d_sorted = reinterpret_cast<int32_t*>(dev + lab_bytes);
+    auto* d_ga = reinterpret_cast<certex_amd::screen_group*>(dev + 2 * lab_bytes);
+    auto* d_gs = reinterpret_cast<certex_amd::screen_group*>(dev + 2 * lab_bytes + tab_bytes);
+    const size_t all_bytes = 2 * lab_bytes + 2 * tab_bytes;
+    char* hs               = static_cast<char*>(rs.stage(all_bytes));
+    std::memcpy(hs, order.data(), size_t(B) * 4);
+    std::memcpy(hs + lab_bytes, sorted.data(), size_t(B) * 4);
+    if (!gs.empty()) {
+      std::memcpy(hs + 2 * lab_bytes, ga.data(), ga.size() * sizeof(ga[0]));
+      std::memcpy(hs + 2 * lab_bytes + tab_bytes, gs.data(), gs.size() * sizeof(gs[0]));
+    }
+    rs.copy_staged(dev, all_bytes);
+    route.anchor_groups = d_ga;
+    route.screen_groups = d_gs;
+  } else {
+    // workgroups of a pass, at most: a label with chunk count c and n_qb query blocks takes
+    // 8 n_qb ceil(c / 8) (rounded up to 8), and n_qb <= 1 + (nq + 1) / qb summed over labels
+    // stays below labels + (B + labels) / qb
+    auto bound = [&](auto&& scans, int q_blk, int chunk) {
+      int64_t sum = 0, cmax = 0, n = 0;
+      for (auto const& e : gs) {
+        const int64_t c = 8 * ((certex_amd::screen_group_tiles(1, scans(e), q_blk, chunk) + 7) / 8);
+        sum += c;
+        cmax = std::max(cmax, c);
+        ++n;
+      }
+      return sum + cmax * ((B + 2 * n + q_blk - 1) / q_blk);
+    };
+    route.anchor_tiles = bound([&](auto const& e) { return anchors_of(e); }, qba, route.anchor_chunk);
+    route.screen_tiles = bound([&](auto const& e) { return e.nx + 1; }, qbs, route.screen_chunk);
+    route.n_route      = int(n_lab);
+    const size_t tab_bytes  = size_t(std::max<int64_t>(1, n_lab)) * sizeof(certex_amd::screen_group);
+    const size_t sort_bytes = (certex_amd::sort_by_label_temp_bytes(B) + 255) / 256 * 256;
+    char* dev = static_cast<char*>(
+      rs.get(cuvs::detail::ws_route, 3 * lab_bytes + 2 * tab_bytes + sort_bytes));
+    d_order      = reinterpret_cast<int32_t*>(dev);
+    d_sorted     = reinterpret_cast<int32_t*>(dev + lab_bytes);
+    auto* d_iota = reinterpret_cast<int32_t*>(dev + 2 * lab_bytes);
+    auto* d_ga   = reinterpret_cast<certex_amd::screen_group*>(dev + 3 * lab_bytes);
+    auto* d_gs   = reinterpret_cast<certex_amd::screen_group*>(dev + 3 * lab_bytes + tab_bytes);
+    void* temp   = dev + 3 * lab_bytes + 2 * tab_bytes;
+    CERTEX_HIP_TRY(certex_amd::sort_by_label(qlabels, B, d_iota, d_sorted, d_order, temp, sort_bytes,
+                                             stream));
+    certex_amd::route_table_args ra{};
+    ra.sorted        = d_sorted;
+    ra.B             = B;
+    ra.offsets       = st.label_part.offsets_dev.as<int64_t>();
+    ra.n_labels      = n_lab;
+    ra.anchor_stride = stride;
+    ra.anchor_pairs  = apairs;
+    ra.anchor_qb     = qba;
+    ra.anchor_chunk  = route.anchor_chunk;
+    ra.anchor_lead   = int(alead);
+    ra.screen_tiled  = tiled;
+    ra.rows_paired   = st.label_part.paired;
+    ra.screen_qb     = qbs;
+    ra.screen_chunk  = route.screen_chunk;
+    ra.anchor_groups = d_ga;
+    ra.screen_groups = d_gs;
+    certex_amd::route_tables(ra, stream);
+    route.anchor_groups = d_ga;
+    route.screen_groups = d_gs;
   }
-  rs.copy_staged(dev, all_bytes);
-  route.anchor_groups = d_ga;
-  route.screen_groups = d_gs;
 
   auto* q_sorted = rs.get(cuvs::detail::ws_route_q, size_t(B) * qrow);
   certex_amd::gather_rows(queries, d_order, B, int64_t(qrow), q_sorted, stream);
@@ -1929,7 +1992,7 @@ void partition_by_labels(cuvs::resources const& res, index<T>* idx)
   hipStream_t stream = static_cast<hipStream_t>(res.stream());
   st.await_updates(stream);
   using cuvs::detail::device_buffer;
-  // fp16 rows of more than 128 halves: the copy is paired, so that the tiled screen copies whole
+  // rows of more than 256 bytes: the copy is paired, so that the tiled screen copies whole
   // 128-byte lines per stage
   const bool paired = uses_tile_screen(st);
   device_buffer keys(size_t(n) * 4), ids_tmp(size_t(n) * 4), ids(size_t(n) * 4),
@@ -1937,6 +2000,7 @@ void partition_by_labels(cuvs::resources const& res, index<T>* idx)
     codes(size_t(paired ? certex_amd::paired_bytes(n, st.row_bytes) : n * int64_t(st.row_bytes))),
     rowc(size_t(n) * 4);
   std::vector<int64_t> offsets;
+  device_buffer offsets_dev;
   if (n > 0) {
     const size_t tb = certex_amd::sort_by_label_temp_bytes(n);
     device_buffer temp(std::max<size_t>(tb, 16));
@@ -1953,6 +2017,7 @@ void partition_by_labels(cuvs::resources const& res, index<T>* idx)
     offsets.resize(size_t(n_labels + 1));
     CERTEX_HIP_TRY(hipMemcpyAsync(offsets.data(), offs.p, offsets.size() * 8,
                                   hipMemcpyDeviceToHost, stream));
+    offsets_dev = std::move(offs);
     // the stored row of every id (they differ in an index with lists)
     const int32_t* from = ids.as<int32_t>();
     if (st.n_listed > 0) {
@@ -1976,6 +2041,7 @@ void partition_by_labels(cuvs::resources const& res, index<T>* idx)
   st.label_part.ids     = std::move(ids);
   st.label_part.pos     = std::move(pos);
   st.label_part.offsets = std::move(offsets);
+  st.label_part.offsets_dev = std::move(offsets_dev);
   st.label_part.paired  = paired;
   st.label_part.n       = n;
 }

@@ -237,12 +237,13 @@ constexpr vtype vtype_of<uint8_t>() { return vtype::u8; }
  */
 struct row_partition {
   int64_t n   = 0;
-  bool paired = false;  // codes in the paired layout (fp16 rows of more than 128 halves)
+  bool paired = false;  // codes in the paired layout (rows of more than 256 bytes)
   cuvs::detail::device_buffer codes;
   cuvs::detail::device_buffer rowc;
   cuvs::detail::device_buffer ids;
   cuvs::detail::device_buffer pos;
   std::vector<int64_t> offsets;
+  cuvs::detail::device_buffer offsets_dev;  // the same offsets on the device (int64)
 };
 
 struct index_state {

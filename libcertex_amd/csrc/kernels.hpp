@@ -233,7 +233,7 @@ int screen_query_block(bool f16, int row_bytes, int64_t nq_pad);
  * takes its chunks in octets (8 n_qb workgroups per octet, the last octet padded with workgroups
  * that exit at once), so that the query blocks of one chunk run on one XCD, as in plain launches.
  */
-inline int64_t screen_group_tiles(int64_t nq, int64_t n_scan, int qb, int chunk_steps)
+__host__ __device__ inline int64_t screen_group_tiles(int64_t nq, int64_t n_scan, int qb, int chunk_steps)
 {
   const int64_t steps    = (n_scan + kStepRows - 1) / kStepRows;
   const int64_t n_chunks = (steps + chunk_steps - 1) / chunk_steps;
@@ -244,7 +244,7 @@ inline int64_t screen_group_tiles(int64_t nq, int64_t n_scan, int qb, int chunk_
  * The same for the tiled screen over paired queries (and rows, rows_paired): a group whose first
  * query (row) is odd starts one slot earlier, at the pair's first query (row).
  */
-inline int64_t paired_group_tiles(const screen_group& g, bool rows_paired, int qb, int chunk_steps)
+__host__ __device__ inline int64_t paired_group_tiles(const screen_group& g, bool rows_paired, int qb, int chunk_steps)
 {
   return screen_group_tiles(g.nq + (g.q0 & 1), g.nx + (rows_paired ? (g.x0 & 1) : 0), qb, chunk_steps);
 }
@@ -252,7 +252,7 @@ inline int64_t paired_group_tiles(const screen_group& g, bool rows_paired, int q
  * First workgroup of a routed group that follows `tiles` workgroups: a multiple of 8 for a group
  * of several query blocks (workgroup b runs on XCD b % 8), else `tiles`.
  */
-inline int64_t screen_group_tile0(int64_t tiles, int64_t nq, int qb)
+__host__ __device__ inline int64_t screen_group_tile0(int64_t tiles, int64_t nq, int qb)
 {
   return (nq + qb - 1) / qb > 1 ? (tiles + 7) / 8 * 8 : tiles;
 }
@@ -479,6 +479,35 @@ hipError_t sort_by_label(const int32_t* labels, int64_t n, int32_t* ids_scratch,
 /** offsets[l] = first position of label >= l in keys_sorted, l = 0 .. n_labels. */
 void label_offsets(const int32_t* keys_sorted, int64_t n, int64_t n_labels, int64_t* offsets,
                    hipStream_t stream);
+
+/**
+ * The routing tables of a label search over the label partition, built on the device from the
+ * batch's labels sorted ascending (sorted[B]) and the partition's label offsets (offsets[n_labels
+ * + 1]): one group per label l of the partition, in both tables, with the queries [q0, q0 + nq) of
+ * label l (none when the label has no rows) and its rows [offsets[l], offsets[l + 1]). Each
+ * group's workgroups follow the previous group's, their count rounded up to a multiple of 8 (so a
+ * group's first workgroup is a multiple of 8). The anchor table counts the group's anchors (row
+ * pairs with anchor_pairs, else one row every anchor_stride), the screen table its rows. The host
+ * launches each pass with route_tiles_bound workgroups; those past the last group exit.
+ */
+struct route_table_args {
+  const int32_t* sorted;
+  int64_t B;
+  const int64_t* offsets;
+  int64_t n_labels;
+  int anchor_stride;
+  bool anchor_pairs;
+  int anchor_qb;
+  int anchor_chunk;
+  int anchor_lead;  // 1: a group whose first query is odd starts one query early (paired queries)
+  bool screen_tiled;
+  bool rows_paired;
+  int screen_qb;
+  int screen_chunk;
+  screen_group* anchor_groups;
+  screen_group* screen_groups;
+};
+void route_tables(const route_table_args& a, hipStream_t stream);
 /** dst row i = src row ids[i] (rows of row_bytes bytes). */
 void gather_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes, void* dst,
                  hipStream_t stream);

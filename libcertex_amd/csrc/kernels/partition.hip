@@ -46,6 +46,82 @@ __global__ void label_offsets_kernel(const int32_t* keys, int64_t n, int64_t n_l
   offsets[l] = lo;
 }
 
+/** The first position in sorted[0, n) whose value is >= v. */
+__device__ inline int64_t lower_pos(const int32_t* sorted, int64_t n, int64_t v)
+{
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (int64_t(sorted[mid]) < v) {
+      lo = mid + 1;
+    } else {
+      hi = mid;
+    }
+  }
+  return lo;
+}
+
+constexpr int kRouteThreads = 1024;
+
+/**
+ * route_tables: one block; per round of kRouteThreads labels, each thread builds its label's two
+ * groups and workgroup counts (rounded up to 8), an exclusive scan over the block places them
+ * after the previous rounds' groups.
+ */
+__global__ __launch_bounds__(kRouteThreads) void route_tables_kernel(route_table_args a)
+{
+  __shared__ int64_t sa[kRouteThreads], ss[kRouteThreads];
+  __shared__ int64_t base_a, base_s;
+  const int tid = threadIdx.x;
+  if (tid == 0) { base_a = base_s = 0; }
+  __syncthreads();
+  for (int64_t l0 = 0; l0 < a.n_labels; l0 += kRouteThreads) {
+    const int64_t l = l0 + tid;
+    screen_group g{0, 0, 0, 0, 0};
+    int64_t ta = 0, ts = 0;
+    if (l < a.n_labels) {
+      g.x0 = a.offsets[l];
+      g.nx = a.offsets[l + 1] - g.x0;
+      g.q0 = lower_pos(a.sorted, a.B, l);
+      g.nq = g.nx > 0 ? lower_pos(a.sorted, a.B, l + 1) - g.q0 : 0;
+      if (g.nq > 0) {
+        const int64_t anchors = a.anchor_pairs ? paired_anchor_count(g.x0, g.nx, a.anchor_stride)
+                                               : (g.nx + a.anchor_stride - 1) / a.anchor_stride;
+        ta = screen_group_tiles(g.nq + (g.q0 & a.anchor_lead), anchors, a.anchor_qb, a.anchor_chunk);
+        ts = a.screen_tiled ? paired_group_tiles(g, a.rows_paired, a.screen_qb, a.screen_chunk)
+                            : screen_group_tiles(g.nq, g.nx, a.screen_qb, a.screen_chunk);
+        ta = (ta + 7) / 8 * 8;
+        ts = (ts + 7) / 8 * 8;
+      }
+    }
+    // exclusive scan of the workgroup counts over the round (Hillis-Steele in LDS)
+    sa[tid] = ta;
+    ss[tid] = ts;
+    __syncthreads();
+    for (int off = 1; off < kRouteThreads; off <<= 1) {
+      const int64_t va = tid >= off ? sa[tid - off] : 0;
+      const int64_t vs = tid >= off ? ss[tid - off] : 0;
+      __syncthreads();
+      sa[tid] += va;
+      ss[tid] += vs;
+      __syncthreads();
+    }
+    if (l < a.n_labels) {
+      screen_group ga = g, gs = g;
+      ga.tile0 = base_a + sa[tid] - ta;
+      gs.tile0 = base_s + ss[tid] - ts;
+      a.anchor_groups[l] = ga;
+      a.screen_groups[l] = gs;
+    }
+    __syncthreads();
+    if (tid == kRouteThreads - 1) {
+      base_a += sa[tid];
+      base_s += ss[tid];
+    }
+    __syncthreads();
+  }
+}
+
 /** dst row i = src row ids[i], rows of `units` 16-byte units. */
 __global__ void gather_units_kernel(const int4* src, const int32_t* ids, int64_t n, int64_t units,
                                     int4* dst)
@@ -193,6 +269,12 @@ hipError_t sort_by_label(const int32_t* labels, int64_t n, int32_t* ids_scratch,
   iota_kernel<<<blocks_for(n), 256, 0, stream>>>(ids_scratch, n);
   return hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, labels, keys_out, ids_scratch,
                                             ids_out, int(n), 0, 32, stream);
+}
+
+void route_tables(const route_table_args& a, hipStream_t stream)
+{
+  if (a.n_labels == 0) { return; }
+  route_tables_kernel<<<1, kRouteThreads, 0, stream>>>(a);
 }
 
 void label_offsets(const int32_t* keys_sorted, int64_t n, int64_t n_labels, int64_t* offsets,

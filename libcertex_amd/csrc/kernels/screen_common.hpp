@@ -136,7 +136,8 @@ __device__ inline screen_work work_of(const screen_args& a, uint32_t b)
   w.base               = a.anchor_pairs ? g.x0 + (g.x0 & 1) : g.x0 - rlead;
   w.rlead              = rlead;
   const int64_t steps  = screen_steps(w.n_scan);
-  w.valid              = t >= 0 && w.chunk < div_small(steps + a.chunk_steps - 1, a.chunk_steps);
+  // a group without queries (a label search's table has one group per label) runs nothing
+  w.valid              = g.nq > 0 && t >= 0 && w.chunk < div_small(steps + a.chunk_steps - 1, a.chunk_steps);
   return w;
 }
 

@@ -5,7 +5,8 @@ that label's rows, the rows added after the partition go through the label filte
 must stay bit-exact: ids equal to the oracle's exhaustive fp64 search among the rows of the
 query's label, ties to the lower id. Cases follow the reference's label tests
 (tests/test_exact.py label cases, ann_certex.cuh label matrix): skewed and missing labels,
-queries whose label has no rows, additions and removals after the partition, ragged batches.
+queries whose label has no rows, additions and removals after the partition, ragged batches;
+each with the query labels in host memory and in device memory (the device builds the routing).
 """
 
 import numpy as np
@@ -28,8 +29,23 @@ def check(X, Q, k, metric, D, I, **okw):
     np.testing.assert_array_equal(D, d)
 
 
+PLACE = {"labels": "host"}
+
+
+@pytest.fixture(params=["host", "device"], autouse=True)
+def label_place(request):
+    """Every case twice: query labels in host memory (routing planned on the host) and in device
+    memory (routing built on the device, no read-back)."""
+    PLACE["labels"] = request.param
+    yield
+    PLACE["labels"] = "host"
+
+
 def search(idx, Q, k, ql, batch=2048):
-    D, I = idx.search(torch.from_numpy(Q).cuda(), k=k, batch=batch, labels=torch.from_numpy(ql))
+    lq = torch.from_numpy(ql)
+    if PLACE["labels"] == "device":
+        lq = lq.cuda()
+    D, I = idx.search(torch.from_numpy(Q).cuda(), k=k, batch=batch, labels=lq)
     torch.cuda.synchronize()
     return D.cpu().numpy(), I.cpu().numpy()
 
