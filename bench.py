@@ -596,6 +596,8 @@ def main():
     ap.add_argument("--batch", type=int, default=0)
     ap.add_argument("--cpu-queries", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-defaults", action="store_true",
+                    help="config 2: skip the second measurement with the API's defaults (id order, batch 2,048)")
     ap.add_argument("--lists", type=int, default=-1, help="k-means lists (default: the config's; 0: none)")
     ap.add_argument("--probe", type=int, default=-1,
                     help="lists probed per query (default: the config's, 0 for config 2, 2 for config 5)")
@@ -697,6 +699,26 @@ def main():
         name: round(ms[i] / args.steps, 4) for i, name in enumerate(("anchors", "threshold", "screen", "verify_topk"))
     }
 
+    # the same search with the API's defaults: an index in id order (no lists) and batches of
+    # 2,048 queries; timed the same way, for the number a caller who changes nothing gets
+    defaults = None
+    if not args.no_defaults:
+        plain = certex.Index(d, metric="l2")
+        plain.add(X)
+
+        def plain_step():
+            return plain.search(Q, k=k)
+
+        d_ms, d_phase, d_launch = timed_steps(plain_step, args.steps, args.warmup)
+        d_screen = d_phase[2] / max(1, d_launch[2])
+        d_ops = 2.0 * n * d * nq / max(1, d_launch[2] // args.steps)
+        defaults = {"value": round(nq / (d_ms / 1000.0), 1), "ms_per_step": round(d_ms, 4),
+                    "batch": 2048, "row_order": "id order (no lists)",
+                    "screen_frac": round(d_ops / (d_screen / 1000.0) / 1e12 / P_INT8_TOPS, 4),
+                    "phase_ms_per_step": {p: round(d_phase[i] / args.steps, 4) for i, p in enumerate(PHASES)}}
+        del plain
+        torch.cuda.synchronize()
+
     cpu = None
     if not args.no_cpu:
         import numpy as np
@@ -738,6 +760,7 @@ def main():
             "phase_ms_per_step": phase_ms,
             "survivors_per_query": round(st.survivors / max(1, st.queries), 2),
             "phase_rooflines": phase_roofs,
+            "api_defaults": defaults,
         },
         "roofline": {
             "bound": "mfma",

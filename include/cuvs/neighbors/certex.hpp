@@ -84,11 +84,12 @@ struct index_params {
 };
 
 /**
- * Parameters of a search (reference certex.hpp:96-107). anchors: the reference scores the best
- * anchors of that many groups exactly to set the threshold; this build certifies the threshold
- * from the screen values of the k best anchor groups (8-bit vectors: exact integer screen values;
- * float vectors: the certificate's upper bound of the score), so no anchor is scored exactly and
- * the value has no effect.
+ * Parameters of a search (reference certex.hpp:96-107). anchors: the reference scores exactly the
+ * best anchor of each of max(anchors, 2k) top anchor groups and takes the k-th best score; this
+ * build takes the k-th best over every anchor group, certified from screen values (8-bit vectors:
+ * exact integer screen values; float vectors: the certificate's upper bound of the score), which
+ * is the reference's choice with anchors at least the number of groups, so the value cannot
+ * change the threshold; any value is accepted, as in the reference.
  */
 struct search_params {
   int anchors     = 128;
