@@ -40,6 +40,15 @@ __host__ __device__ inline int64_t pad_queries(int64_t nq)
 }
 /** Query block of a padded batch (the kernels' view of query_block). */
 __host__ __device__ inline int screen_block_queries(int64_t nq_pad) { return nq_pad % 512 == 0 ? 512 : 128; }
+/**
+ * Query block of the narrow screens: screen_block_queries, except fp16 rows of 128 halves, which
+ * take 128 queries (32 KB of LDS, several workgroups per CU, where 512 took 128 KB and left one);
+ * their survivors, thousands per query in a KV-cache search, then overlap other workgroups' MFMAs.
+ */
+__host__ __device__ inline int narrow_block_queries(bool f16, int row_bytes, int64_t nq_pad)
+{
+  return f16 && row_bytes == 256 ? 128 : screen_block_queries(nq_pad);
+}
 
 enum class metric_kind : int { l2 = 0, inner = 1, cosine = 2 };
 

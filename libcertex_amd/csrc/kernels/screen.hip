@@ -401,7 +401,7 @@ void launch_other(const screen_args& b, dim3 grid, int ks, int qb_size, hipStrea
 template <typename R, bool ANCHORS, bool FILT>
 void launch(const screen_args& a, hipStream_t stream)
 {
-  const int qb_size = screen_block_queries(a.nq_pad);
+  const int qb_size = narrow_block_queries(R::kValues, a.row_bytes, a.nq_pad);
   int64_t blocks    = 0;
   if (a.groups != nullptr) {
     blocks = a.n_tiles;
@@ -464,8 +464,8 @@ int wide_block_queries(int row_bytes);  // screen_wide.hip
 
 int screen_query_block(bool f16, int row_bytes, int64_t nq_pad)
 {
-  (void)f16;  // rows of more than 256 bytes (fp16 or int8) take the K-loop anchor pass's blocks
-  return row_bytes > 256 ? wide_block_queries(row_bytes) : screen_block_queries(nq_pad);
+  // rows of more than 256 bytes (fp16 or int8) take the K-loop anchor pass's blocks
+  return row_bytes > 256 ? wide_block_queries(row_bytes) : narrow_block_queries(f16, row_bytes, nq_pad);
 }
 
 void screen_i8(const screen_args& a, hipStream_t stream)
