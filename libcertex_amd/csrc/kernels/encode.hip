@@ -182,20 +182,6 @@ __global__ void column_sums_kernel(const void* x, elem t, int64_t n, int64_t dim
   }
 }
 
-__global__ void max_norm_kernel(const void* x, elem t, int64_t n, int64_t dim, bool normalize,
-                                const double* center, double* out)
-{
-  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
-  if (i >= n) { return; }
-  const double nrm = normalize ? row_norm(x, t, i, dim) : 1.0;
-  double s         = 0;
-  for (int64_t j = 0; j < dim; ++j) {
-    const double v = coord(x, t, i * dim + j) / nrm - center[j];
-    s              = fma(v, v, s);
-  }
-  atomic_max_pos(out, sqrt_up(s, dim));
-}
-
 constexpr double kF16Safe = 4096.0;  // |Z| above this: the row is always a candidate
 
 /** fp16 value of z (round to nearest), 0 for results below the smallest normal fp16. */
@@ -205,54 +191,132 @@ __device__ inline _Float16 to_f16(double z)
   return fabs(double(h)) < 6.103515625e-05 ? _Float16(0.0f) : h;
 }
 
-__global__ void encode_rows_f16_kernel(const void* x, elem t, int64_t n, int64_t dim, int halves,
-                                       bool normalize, const double* center, double inv_alpha,
-                                       metric_kind metric, double gamma, uint16_t* rows,
-                                       float* rowc, double* maxima)
-{
-  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
-  if (i >= n) { return; }
-  _Float16* dst    = reinterpret_cast<_Float16*>(rows + i * halves);
-  const double nrm = normalize ? row_norm(x, t, i, dim) : 1.0;
-  double a = 0;
-  for (int64_t j = 0; j < dim; ++j) {
-    const double z = (coord(x, t, i * dim + j) / nrm - center[j]) * inv_alpha;
-    a              = fma(z, z, a);
-  }
-  if (!(sqrt(a) <= kF16Safe)) {
-    for (int j = 0; j < halves; ++j) { dst[j] = _Float16(0.0f); }
-    rowc[i] = INFINITY;
-    return;
-  }
-  double nz = 0, ez = 0;
-  for (int64_t j = 0; j < dim; ++j) {
-    const double z = (coord(x, t, i * dim + j) / nrm - center[j]) * inv_alpha;
-    const _Float16 h = to_f16(z);
-    const double e   = z - double(h);  // exact (Sterbenz, or h = 0)
-    dst[j]           = h;
-    nz               = fma(double(h), double(h), nz);
-    ez               = fma(e, e, ez);
-  }
-  for (int64_t j = dim; j < halves; ++j) { dst[j] = _Float16(0.0f); }
-  if (metric == metric_kind::inner) {
-    rowc[i] = 0.0f;
-  } else {
-    // row term rounded up: the fp32 accumulation error of this term is folded in (factor 1 - 2g)
-    const double c = -(a * (1.0 - 1e-13) / 2.0) * (1.0 - 2.0 * gamma - 1e-10);
-    float f        = float(c);
-    if (double(f) < c) { f = nextafterf(f, INFINITY); }
-    rowc[i] = f;
-  }
-  atomic_max_pos(maxima + 0, sqrt_up(nz, dim));
-  atomic_max_pos(maxima + 1, sqrt_up(ez, dim));
-}
-
 /** Sum of v over the 64 lanes of a wave (xor butterfly: every lane gets the sum). */
 __device__ inline double wave_sum(double v)
 {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) { v += __shfl_xor(v, off); }
   return v;
+}
+
+/**
+ * out[0] raised to the largest |x / |x| - center| (|x - center| without normalizing) over the n
+ * rows, sqrt_up of the fp64 sum: rows by waves over a grid stride as encode_rows_f16_kernel takes
+ * them, one atomic per workgroup.
+ */
+__global__ __launch_bounds__(256) void max_norm_kernel(const void* x, elem t, int64_t n,
+                                                       int64_t dim, bool normalize,
+                                                       const double* center, double* out)
+{
+  __shared__ double wmax[4];
+  const int lane      = threadIdx.x & 63;
+  const int wave      = threadIdx.x >> 6;
+  const int64_t waves = int64_t(gridDim.x) * 4;
+  double m            = 0;
+  for (int64_t i = blockIdx.x * int64_t(4) + wave; i < n; i += waves) {
+    double nrm = 1.0;
+    if (normalize) {
+      double s2 = 0;
+      for (int64_t j = lane; j < dim; j += 64) {
+        const double v = coord(x, t, i * dim + j);
+        s2             = fma(v, v, s2);
+      }
+      s2  = wave_sum(s2);
+      nrm = s2 > 0 ? sqrt(s2) : 1.0;
+    }
+    double s = 0;
+    for (int64_t j = lane; j < dim; j += 64) {
+      const double v = coord(x, t, i * dim + j) / nrm - center[j];
+      s              = fma(v, v, s);
+    }
+    m = fmax(m, sqrt_up(wave_sum(s), dim));
+  }
+  if (lane == 0) { wmax[wave] = m; }
+  __syncthreads();
+  if (threadIdx.x == 0) { atomic_max_pos(out, fmax(fmax(wmax[0], wmax[1]), fmax(wmax[2], wmax[3]))); }
+}
+
+/**
+ * Rows i = w, w + W, ... for wave w of W (a grid stride), each by one wave whose lanes take the
+ * coordinates j = lane, lane + 64, ... (coalesced loads and stores): rows[i] = fp16(Z) with
+ * Z = (x / |x| - center) / alpha (x / |x| when normalizing), subnormals set to 0, zero padded;
+ * rowc[i] = -|Z|^2 / 2, raised so that it bounds the term's fp32 accumulation (0 for the inner
+ * product); a row with |Z| above kF16Safe is stored as zeros with rowc = +inf (always a
+ * candidate). maxima[0] and maxima[1] are raised to the largest |fp16(Z)| and |Z - fp16(Z)|
+ * (sqrt_up of their sums), one atomic each per workgroup. The fp64 sums are per-lane partials
+ * and a butterfly; they only enter bounds that carry their rounding slack.
+ */
+__global__ __launch_bounds__(256) void encode_rows_f16_kernel(const void* x, elem t, int64_t n,
+                                                              int64_t dim, int halves,
+                                                              bool normalize, const double* center,
+                                                              double inv_alpha, metric_kind metric,
+                                                              double gamma, uint16_t* rows,
+                                                              float* rowc, double* maxima)
+{
+  __shared__ double wmax[2][4];
+  const int lane      = threadIdx.x & 63;
+  const int wave      = threadIdx.x >> 6;
+  const int64_t waves = int64_t(gridDim.x) * 4;
+  double mh = 0, me = 0;  // this wave's largest bounds of |fp16(Z)| and |Z - fp16(Z)|
+  for (int64_t i = blockIdx.x * int64_t(4) + wave; i < n; i += waves) {
+    _Float16* dst = reinterpret_cast<_Float16*>(rows + i * halves);
+    double nrm    = 1.0;
+    if (normalize) {
+      double s2 = 0;
+      for (int64_t j = lane; j < dim; j += 64) {
+        const double v = coord(x, t, i * dim + j);
+        s2             = fma(v, v, s2);
+      }
+      s2  = wave_sum(s2);
+      nrm = s2 > 0 ? sqrt(s2) : 1.0;
+    }
+    double a = 0;
+    for (int64_t j = lane; j < dim; j += 64) {
+      const double z = (coord(x, t, i * dim + j) / nrm - center[j]) * inv_alpha;
+      a              = fma(z, z, a);
+    }
+    a = wave_sum(a);  // the same value in every lane: the branch below is uniform
+    if (!(sqrt(a) <= kF16Safe)) {
+      for (int64_t j = lane; j < halves; j += 64) { dst[j] = _Float16(0.0f); }
+      if (lane == 0) { rowc[i] = INFINITY; }
+      continue;
+    }
+    double nz = 0, ez = 0;
+    for (int64_t j = lane; j < dim; j += 64) {
+      const double z   = (coord(x, t, i * dim + j) / nrm - center[j]) * inv_alpha;
+      const _Float16 h = to_f16(z);
+      const double e   = z - double(h);  // exact (Sterbenz, or h = 0)
+      dst[j]           = h;
+      nz               = fma(double(h), double(h), nz);
+      ez               = fma(e, e, ez);
+    }
+    for (int64_t j = dim + lane; j < halves; j += 64) { dst[j] = _Float16(0.0f); }
+    nz = wave_sum(nz);
+    ez = wave_sum(ez);
+    if (lane == 0) {
+      if (metric == metric_kind::inner) {
+        rowc[i] = 0.0f;
+      } else {
+        // row term rounded up: the fp32 accumulation error of this term is folded in (factor
+        // 1 - 2g)
+        const double c = -(a * (1.0 - 1e-13) / 2.0) * (1.0 - 2.0 * gamma - 1e-10);
+        float f        = float(c);
+        if (double(f) < c) { f = nextafterf(f, INFINITY); }
+        rowc[i] = f;
+      }
+    }
+    mh = fmax(mh, sqrt_up(nz, dim));
+    me = fmax(me, sqrt_up(ez, dim));
+  }
+  if (lane == 0) {
+    wmax[0][wave] = mh;
+    wmax[1][wave] = me;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    atomic_max_pos(maxima + 0, fmax(fmax(wmax[0][0], wmax[0][1]), fmax(wmax[0][2], wmax[0][3])));
+    atomic_max_pos(maxima + 1, fmax(fmax(wmax[1][0], wmax[1][1]), fmax(wmax[1][2], wmax[1][3])));
+  }
 }
 
 /**
@@ -347,7 +411,8 @@ void max_norm(const void* x, elem t, int64_t n, int64_t dim, bool normalize, con
               double* out, hipStream_t stream)
 {
   if (n == 0) { return; }
-  max_norm_kernel<<<blocks_for(n), 256, 0, stream>>>(x, t, n, dim, normalize, center, out);
+  const unsigned blocks = unsigned(std::min<int64_t>((n + 3) / 4, 4096));
+  max_norm_kernel<<<blocks, 256, 0, stream>>>(x, t, n, dim, normalize, center, out);
 }
 
 void encode_rows_f16(const void* x, elem t, int64_t n, int64_t dim, int halves, bool normalize,
@@ -355,8 +420,10 @@ void encode_rows_f16(const void* x, elem t, int64_t n, int64_t dim, int halves, 
                      uint16_t* rows, float* rowc, double* maxima, hipStream_t stream)
 {
   if (n == 0) { return; }
-  encode_rows_f16_kernel<<<blocks_for(n), 256, 0, stream>>>(
-    x, t, n, dim, halves, normalize, center, inv_alpha, metric, gamma, rows, rowc, maxima);
+  // four rows per workgroup at a time, at most 4,096 workgroups (16 per CU) striding over the rest
+  const unsigned blocks = unsigned(std::min<int64_t>((n + 3) / 4, 4096));
+  encode_rows_f16_kernel<<<blocks, 256, 0, stream>>>(x, t, n, dim, halves, normalize, center,
+                                                     inv_alpha, metric, gamma, rows, rowc, maxima);
 }
 
 void encode_queries_f16(const void* q, elem t, int64_t nq, int64_t nq_pad, int64_t dim,
