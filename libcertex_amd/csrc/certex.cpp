@@ -356,6 +356,9 @@ struct route_plan {
   int screen_chunk     = 0;
   bool anchor_tiled    = false;  // the partition's anchor pass runs as tiles (anchors_f16_tile)
   int64_t part_groups  = 0;  // anchor group columns of the partition (the tail's follow)
+  // every query of the batch is routed and every label's fine groups fill all part_groups
+  // columns: the routed anchor pass then writes every column of the batch's table rows itself
+  bool covers_table = false;
   anchor_plan ap{};
 };
 
@@ -426,13 +429,16 @@ void anchor_pass(index_state const& st, certex_amd::screen_args aa, anchor_plan 
     launch(aa, stream);
     return;
   }
-  // columns of labels with fewer groups stay at the lowest value (no anchor)
-  if (is_int(st.type)) {
-    certex_amd::fill_i32(static_cast<int32_t*>(aa.gmax), aa.nq_pad * ap.n_groups, INT32_MIN,
-                         stream);
-  } else {
-    certex_amd::fill_u32(static_cast<uint32_t*>(aa.gmax), aa.nq_pad * ap.n_groups, 0xff800000u,
-                         stream);
+  // columns of labels with fewer groups, and the rows of queries in no group, stay at the lowest
+  // value (no anchor); nothing to fill when the routed pass writes every column of every row
+  if (!route->covers_table) {
+    if (is_int(st.type)) {
+      certex_amd::fill_i32(static_cast<int32_t*>(aa.gmax), aa.nq_pad * ap.n_groups, INT32_MIN,
+                           stream);
+    } else {
+      certex_amd::fill_u32(static_cast<uint32_t*>(aa.gmax), aa.nq_pad * ap.n_groups, 0xff800000u,
+                           stream);
+    }
   }
   certex_amd::screen_args r = aa;
   r.codes                   = st.label_part.codes.as<int8_t>();
@@ -925,10 +931,6 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
     t_capture.on = false;
   }
 
-  auto* best_score =
-    static_cast<double*>(rs.get(cuvs::detail::ws_best_score, size_t(B) * k * sizeof(double)));
-  auto* best_row =
-    static_cast<int64_t*>(rs.get(cuvs::detail::ws_best_row, size_t(B) * k * sizeof(int64_t)));
   certex_amd::verify_args va{};
   va.cand_count = count;
   va.cand_rows  = rows;
@@ -952,10 +954,9 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
     va.part_codes  = st.label_part.codes.as<int8_t>();
     va.part_paired = st.label_part.paired;
   }
-  va.best_score = best_score;
-  va.best_row   = best_row;
+  va.distances = distances;
+  va.neighbors = neighbors;
   timed(3, stream, [&] { certex_amd::verify_topk_i8(va, stream); });
-  certex_amd::finish(best_score, best_row, B, k, st.metric, distances, neighbors, stream);
 }
 
 /** One batch of queries of a float index (the caller holds the shared lock). */
@@ -1033,10 +1034,6 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   uint32_t *count = nullptr, *rows = nullptr;
   float* vals = nullptr;
   int64_t cap = 0;
-  auto* best_score =
-    static_cast<double*>(rs.get(cuvs::detail::ws_best_score, size_t(B) * k * sizeof(double)));
-  auto* best_row =
-    static_cast<int64_t*>(rs.get(cuvs::detail::ws_best_row, size_t(B) * k * sizeof(int64_t)));
   unsigned long long* scored = nullptr;
   if (t_stats_on) {
     auto* small = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_small, 64));
@@ -1057,8 +1054,8 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   va.filter     = fa;
   va.nq         = B;
   va.k          = k;
-  va.best_score = best_score;
-  va.best_row   = best_row;
+  va.distances  = distances;
+  va.neighbors  = neighbors;
   va.scored     = scored;
   if (route != nullptr) {
     va.part_ids = st.label_part.ids.as<int32_t>();
@@ -1127,7 +1124,6 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
     CERTEX_HIP_TRY(hipStreamSynchronize(stream));
     t_stats.verified += int64_t(*static_cast<unsigned long long*>(rs.host_small));
   }
-  certex_amd::finish(best_score, best_row, B, k, st.metric, distances, neighbors, stream);
 }
 
 using batch_fn = void (*)(cuvs::resources const&, index_state const&, const void*, int64_t, int,
@@ -1157,6 +1153,7 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   const int64_t n_lab  = int64_t(off.size()) - 1;
   std::vector<int32_t> order, sorted;
   std::vector<certex_amd::screen_group> ga, gs;
+  bool in_order = false;  // host labels in non-decreasing order: no gather or scatter
   if (!on_device) {
     // queries in label order, stable: a counting sort when the batch's labels span a small range
     // (one pass, no comparisons), else a comparison sort
@@ -1174,6 +1171,7 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
       for (int64_t i = 0; i < B; ++i) { order[size_t(i)] = int32_t(i); }
       std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return lab[a] < lab[b]; });
     }
+    in_order = std::is_sorted(lab, lab + B);
     for (int64_t i = 0; i < B;) {
       const int32_t l = lab[order[size_t(i)]];
       int64_t j       = i;
@@ -1223,6 +1221,15 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   route.ap.n_anchor = 0;
   size_groups(route.ap, max_anchors, (st.size - st.label_part.n + stride - 1) / stride, nq_pad, k,
               &route.part_groups);
+  if (!on_device && route.ap.fine) {
+    int64_t routed = 0;
+    bool equal     = true;
+    for (auto const& e : ga) {
+      routed += e.nq;
+      equal = equal && anchors_of(e) == max_anchors;
+    }
+    route.covers_table = routed == B && equal;
+  }
   const int64_t waves = waves_of(st);
   // the screen's groups: the tiled screen's query blocks and 256-row chunks for wide rows;
   // so too the anchor pass over anchor pairs with fine groups (its tiles start at an even query)
@@ -1338,12 +1345,17 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
     route.screen_groups = d_gs;
   }
 
+  fa.query_labels = d_sorted;  // the label filter of the tail, in the sorted order
+  if (in_order) {
+    // host labels already in label order (a KeyCache's heads): the sorted batch is the batch
+    batch(res, st, queries, B, k, 0, neighbors, distances, fa, params, &route);
+    return;
+  }
   auto* q_sorted = rs.get(cuvs::detail::ws_route_q, size_t(B) * qrow);
   certex_amd::gather_rows(queries, d_order, B, int64_t(qrow), q_sorted, stream);
   auto* out   = static_cast<char*>(rs.get(cuvs::detail::ws_route_out, size_t(B) * k * 12));
   auto* nb_s  = reinterpret_cast<int64_t*>(out);
   auto* ds_s  = reinterpret_cast<float*>(out + size_t(B) * k * 8);
-  fa.query_labels = d_sorted;  // the label filter of the tail, in the sorted order
   batch(res, st, q_sorted, B, k, 0, nb_s, ds_s, fa, params, &route);
   certex_amd::scatter_rows(nb_s, d_order, B, int64_t(k) * 8, neighbors, stream);
   certex_amd::scatter_rows(ds_s, d_order, B, int64_t(k) * 4, distances, stream);

@@ -99,8 +99,6 @@ enum ws_slot : int {
   ws_count,
   ws_rows,
   ws_small,
-  ws_best_score,
-  ws_best_row,
   ws_staging,
   ws_qscal,
   ws_vals,

@@ -347,8 +347,10 @@ struct verify_args {
   int64_t n_part           = 0;
   const int8_t* part_codes = nullptr;
   bool part_paired         = false;  // part_codes in the paired layout (rows of more than 256 bytes)
-  double* best_score;  // [nq, k], smaller is better; +inf where missing
-  int64_t* best_row;   // [nq, k], -1 where missing
+  // the results as the caller receives them, in (score, id) order: distances [nq, k] in the
+  // metric's form (+inf, -inf for the inner product, where missing), ids [nq, k] (-1 where missing)
+  float* distances;
+  int64_t* neighbors;
 };
 
 /** fp64 exact scores of the candidates of every query and their k best by (score, row). */
@@ -466,8 +468,8 @@ struct verify_f_args {
   unsigned long long* scored;  // optional: += the rows scored exactly (the stats' verified count)
   const int32_t* part_ids = nullptr;  // routed: candidate rows below n_part are partition rows
   int64_t n_part          = 0;
-  double* best_score;
-  int64_t* best_row;
+  float* distances;    // as in verify_args
+  int64_t* neighbors;
 };
 /**
  * fp64 exact scores (the canonical order of the oracle) and top-k by (score, row); with screen
@@ -575,12 +577,5 @@ void finish_centers(const float* sums, const unsigned int* counts, int n_centers
 /** centers[c] = rows[ids[c]] as floats. */
 void rows_to_centers(const void* rows, bool f16, const int32_t* ids, int n_centers, int width,
                      float* centers, hipStream_t stream);
-
-/**
- * Output conversion: distances (l2: score; inner: -score = <q, x>; cosine: score + 1 = 1 - cos)
- * as float32, -1 / +-inf for missing entries, and row -> id.
- */
-void finish(const double* best_score, const int64_t* best_row, int64_t nq, int k,
-            metric_kind metric, float* distances, int64_t* neighbors, hipStream_t stream);
 
 }  // namespace certex_amd

@@ -161,6 +161,29 @@ __device__ inline double key_score(uint64_t k)
   return __longlong_as_double((long long)b);
 }
 
+/**
+ * Result t (query q, place j: t = q k + j) as the caller receives it, the output conversion of
+ * certex.cu:224-250 (finish): the distance of fp64 score s (smaller is better) as float32 (l2:
+ * s; inner product: -s = <q, x>; cosine: 1 + s = 1 - cos) and the id; id < 0: a missing entry,
+ * +inf (-inf for the inner product) and -1.
+ */
+template <typename A>
+__device__ inline void put_result(const A& a, int64_t t, double s, int64_t id)
+{
+  float d;
+  if (id < 0) {
+    d = a.metric == metric_kind::inner ? -INFINITY : INFINITY;
+  } else if (a.metric == metric_kind::inner) {
+    d = float(-s);
+  } else if (a.metric == metric_kind::cosine) {
+    d = float(1.0 + s);
+  } else {
+    d = float(s);
+  }
+  a.distances[t] = d;
+  a.neighbors[t] = id < 0 ? -1 : id;
+}
+
 __device__ inline bool keeps(const filter_args& f, int64_t q, uint32_t row)
 {
   if (f.kind == 0) { return true; }
@@ -512,13 +535,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a,
   __syncthreads();
   bitonic_sort(key, rid, P);
   for (int j = tid; j < k; j += kThreads) {
-    if (j < have) {
-      a.best_score[q * k + j] = key_score(key[j]);
-      a.best_row[q * k + j]   = int64_t(rid[j]);
-    } else {
-      a.best_score[q * k + j] = INFINITY;
-      a.best_row[q * k + j]   = -1;
-    }
+    put_result(a, q * k + j, j < have ? key_score(key[j]) : 0.0, j < have ? int64_t(rid[j]) : -1);
   }
 }
 
@@ -614,10 +631,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_small_kernel(verify_a
       my_r = int64_t(br);
     }
   }
-  if (lane < a.k) {
-    a.best_score[q * a.k + lane] = my_s;
-    a.best_row[q * a.k + lane]   = my_r;
-  }
+  if (lane < a.k) { put_result(a, q * a.k + lane, my_s, my_r); }
 }
 
 // ---- float vectors ---------------------------------------------------------------------------
@@ -1499,37 +1513,11 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
     have = have < k ? have : k;
   }
   for (int j = tid; j < k; j += kThreads) {
-    if (j < have) {
-      a.best_score[q * k + j] = key_score(key[j]);
-      a.best_row[q * k + j]   = int64_t(rid[j]);
-    } else {
-      a.best_score[q * k + j] = INFINITY;
-      a.best_row[q * k + j]   = -1;
-    }
+    put_result(a, q * k + j, j < have ? key_score(key[j]) : 0.0, j < have ? int64_t(rid[j]) : -1);
   }
   if (a.scored != nullptr && tid == 0) { atomicAdd(a.scored, (unsigned long long)n_scored); }
 }
 
-__global__ void finish_kernel(const double* best_score, const int64_t* best_row, int64_t n, int k,
-                              metric_kind metric, float* distances, int64_t* neighbors)
-{
-  const int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
-  if (t >= n * k) { return; }
-  const int64_t r = best_row[t];
-  const double s  = best_score[t];
-  float d;
-  if (r < 0) {
-    d = metric == metric_kind::inner ? -INFINITY : INFINITY;
-  } else if (metric == metric_kind::inner) {
-    d = float(-s);
-  } else if (metric == metric_kind::cosine) {
-    d = float(1.0 + s);
-  } else {
-    d = float(s);
-  }
-  distances[t] = d;
-  neighbors[t] = r;
-}
 
 }  // namespace
 
@@ -1622,15 +1610,6 @@ void verify_topk_f(const verify_f_args& a, hipStream_t stream)
     case 32: launch_dyn(verify_topk_f_kernel<32>, grid, bytes, stream, a, cap); break;
     default: launch_dyn(verify_topk_f_kernel<64>, grid, bytes, stream, a, cap); break;
   }
-}
-
-void finish(const double* best_score, const int64_t* best_row, int64_t nq, int k,
-            metric_kind metric, float* distances, int64_t* neighbors, hipStream_t stream)
-{
-  const int64_t n = nq * k;
-  if (n == 0) { return; }
-  finish_kernel<<<unsigned((n + 255) / 256), 256, 0, stream>>>(best_score, best_row, nq, k, metric,
-                                                              distances, neighbors);
 }
 
 }  // namespace certex_amd
