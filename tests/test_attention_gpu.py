@@ -92,3 +92,19 @@ def test_queries_that_overflow_the_cache(gpu):
     big[0, 0, 0] = 1e6  # beyond float16's range
     with pytest.raises(ValueError, match="overflow"):
         cache.topk(big, 8)
+
+
+def test_group_table_of_an_earlier_search(gpu):
+    """A KeyCache's search (KV heads of equal size, queries in head order) writes every column of
+    its group table itself: a table of larger values that an earlier search on the same thread
+    left in the workspace (every query equal to every row) changes nothing."""
+    v = torch.randn((1, 128), generator=torch.Generator(device="cuda").manual_seed(9), device="cuda")
+    P = v.repeat(100_000, 1)
+    poison = certex.Index(128, metric="ip")
+    poison.add(P)
+    poison.search(P[:2048].contiguous(), k=16, batch=2048)
+    q, keys = data(n_kv=2, H=4, n=20_000, m=16, seed=11)
+    cache = certex.KeyCache(2, 128, k=16)
+    cache.append(keys[:, :19_000]).append(keys[:, 19_000:])  # the partition, then a tail
+    scores, ids = cache.topk(q, 16)
+    assert_exact(q, keys, scores, ids, 16)
