@@ -599,6 +599,8 @@ def main():
     ap.add_argument("--no-defaults", action="store_true",
                     help="config 2: skip the second measurement with the API's defaults (id order, batch 2,048)")
     ap.add_argument("--lists", type=int, default=-1, help="k-means lists (default: the config's; 0: none)")
+    ap.add_argument("--stride", type=int, default=0,
+                    help="config 2: the index's anchor stride (default: the API's, 16)")
     ap.add_argument("--probe", type=int, default=-1,
                     help="lists probed per query (default: the config's, 0 for config 2, 2 for config 5)")
     ap.add_argument("--summarize", nargs="+", metavar="DIR",
@@ -651,7 +653,8 @@ def main():
     # exhaustive screen, whose MFMA operands then change less from one row tile to the next
     n_lists = 4096 if args.lists < 0 else args.lists
     args.probe = 0 if args.probe < 0 else args.probe
-    idx = certex.Index(d, metric="l2", n_lists=n_lists)
+    stride_kw = {"anchor_stride": args.stride} if args.stride > 0 else {}
+    idx = certex.Index(d, metric="l2", n_lists=n_lists, **stride_kw)
     t_build = time.perf_counter()
     idx.add(X)
     torch.cuda.synchronize()
@@ -750,7 +753,7 @@ def main():
             "n_queries": nq,
             "k": k,
             "batch": args.batch,
-            "anchor_stride": 16,
+            "anchor_stride": idx.anchor_stride,
             "n_lists": n_lists,
             "probe_lists": args.probe if n_lists else 0,
             "row_order": ("k-means list order" if n_lists else "id order")
@@ -771,7 +774,8 @@ def main():
             "frac": round(achieved / P_INT8_TOPS, 4),
             # measured only for the default workload (profiles/screen_i8_c2_traffic.txt)
             "traffic": screen_traffic()
-            if (n, d, nq, args.batch, n_lists, args.probe) == (10_000_000, 128, 10_000, 10_000, 4096, 0) else None,
+            if (n, d, nq, args.batch, n_lists, args.probe, idx.anchor_stride)
+            == (10_000_000, 128, 10_000, 10_000, 4096, 0, 16) else None,
             "avg_launch_ms": round(screen_ms, 4),
             "ops_per_launch": ops_per_launch,
             **clock,

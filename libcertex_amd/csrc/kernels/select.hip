@@ -1451,10 +1451,15 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
   // room. A cut back to the k best (which also tightens U) is a select over the whole buffer: it
   // runs once the rows scored past the k best come to k / 8 (U then moves enough to save
   // scores), or when the free room falls below a quarter of the buffer
+  // The ordered scan keeps few candidates (those whose lower bound reaches U), so a chunk spans
+  // the whole rest of them: a chunk no longer than the room would cost one round of barriers and
+  // loads per room's worth of candidates (1,024 at k = 2,048). When it keeps more than the room
+  // holds, that chunk is scanned again at the room's size, and so is every chunk after it.
   int pending = have;  // entries [pending, have) are appended and not scored yet
+  bool wide   = ordered;
   for (int64_t c0 = 0; c0 < n_cand;) {
     const int room  = cap - have;
-    const int64_t m = n_cand - c0 < room ? n_cand - c0 : room;
+    const int64_t m = wide || n_cand - c0 < room ? n_cand - c0 : room;
     if (tid == 0) { fill = 0; }
     __syncthreads();
     for (int64_t e0 = 0; e0 < m; e0 += int64_t(kThreads) * kBatch) {
@@ -1476,7 +1481,7 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         const int slot = wave_append(take[i], &fill);
-        if (take[i]) {
+        if (take[i] && slot < room) {
           const int64_t idx = c0 + e0 + i * kThreads + tid;
           rid[have + slot]  = a.all_rows ? listed_id(a.filter, uint32_t(idx)) : to_id(cand[idx]);
         }
@@ -1484,9 +1489,13 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
     }
     __syncthreads();
     const int added = fill;
+    __syncthreads();  // every thread has read fill before the next chunk resets it
+    if (added > room) {  // more kept than the room holds: this chunk again, at the room's size
+      wide = false;
+      continue;
+    }
     have += added;
     c0 += m;
-    __syncthreads();  // every thread has read fill before the next chunk resets it
     // a scoring round costs a memory latency even for one row: score once the buffer runs short
     // of room or the scan ends (U tightens only through scored rows)
     if (c0 >= n_cand || cap - have < cap / 4) {
