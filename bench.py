@@ -206,7 +206,7 @@ def bench_config3(args):
     gl = torch.Generator(device=dev).manual_seed(34)
     lx = torch.randint(0, 16, (n,), generator=gl, device=dev, dtype=torch.int32)
     lq = torch.randint(0, 16, (nq,), generator=gl, device=dev, dtype=torch.int32)
-    idx = certex.Index(d, metric="cosine")
+    idx = certex.Index(d, metric="cosine", **({"anchor_stride": args.stride} if args.stride > 0 else {}))
     idx.add(X, labels=lx)
     torch.cuda.synchronize()
     batch = args.batch or 10_000
@@ -222,7 +222,7 @@ def bench_config3(args):
     screen_ms = ms[2] / max(1, launches[2])
     elem = idx.dtype.itemsize
     # the committed counter profile holds the default workload's traffic
-    default = (n, d, nq, k, batch) == (1_000_000, 768, 10_000, 100, 10_000)
+    default = (n, d, nq, k, batch, idx.anchor_stride) == (1_000_000, 768, 10_000, 100, 10_000, 16)
     # algorithmic work of the label-routed screen: every query against the rows of its label
     per_label = torch.bincount(lx.long(), minlength=16)
     pairs = float(per_label[lq.long()].sum().item())
@@ -254,7 +254,7 @@ def bench_config3(args):
         "data": "synthetic (config 3 power-law embeddings, torch generators seeded 31/32/33/34)",
         "config": {
             "workload": f"config 3: exact {k}-NN, cosine, base {n} x {d} fp32, {nq} queries, 16 labels",
-            "n": n, "dim": d, "n_queries": nq, "k": k, "batch": batch,
+            "n": n, "dim": d, "n_queries": nq, "k": k, "batch": batch, "anchor_stride": idx.anchor_stride,
             "phase_ms_per_step": {p: round(ms[i] / args.steps, 4) for i, p in enumerate(PHASES)},
             "launches_per_step": {p: launches[i] // args.steps for i, p in enumerate(PHASES)},
             "survivors_per_query": round(st.survivors / max(1, st.queries), 2),
@@ -600,7 +600,7 @@ def main():
                     help="config 2: skip the second measurement with the API's defaults (id order, batch 2,048)")
     ap.add_argument("--lists", type=int, default=-1, help="k-means lists (default: the config's; 0: none)")
     ap.add_argument("--stride", type=int, default=0,
-                    help="config 2: the index's anchor stride (default: the API's, 16)")
+                    help="configs 2 and 3: the index's anchor stride (default: the API's, 16)")
     ap.add_argument("--probe", type=int, default=-1,
                     help="lists probed per query (default: the config's, 0 for config 2, 2 for config 5)")
     ap.add_argument("--summarize", nargs="+", metavar="DIR",

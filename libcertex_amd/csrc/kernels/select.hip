@@ -1362,10 +1362,16 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
   auto* qv  = reinterpret_cast<double*>(dyn + size_t(cap) * 12);  // [dim]
   __shared__ int hist[256];
   __shared__ int wave_tot[4];
+  __shared__ uint32_t red[48];
   __shared__ uint32_t sel_digit;
   __shared__ int sel_rank;
   __shared__ int sel_count;
   __shared__ int fill;
+  // survivors whose screen values phase A selects in registers, 24 per thread; not with 64-lane
+  // slots (d above 256), whose six waves per SIMD leave no registers to spare (16 per thread
+  // there measured 4% slower than the streaming select, config 3)
+  constexpr bool REGS = L != 64;
+  constexpr int RV    = 24;
 
   const int64_t q = blockIdx.x;
   const int tid   = threadIdx.x;
@@ -1403,7 +1409,27 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
   bool ordered = vals != nullptr && n_cand > k;
   uint32_t tk  = 0;
   double U = INFINITY, aq = 0, C = 0;
-  if (ordered) {
+  if (REGS && ordered && n_cand <= int64_t(kThreads) * RV) {
+    // the survivors' screen values read once into registers (RV per thread; 0xffffffff past the
+    // bucket sorts last), selected there, and the k best collected from the same registers
+    uint32_t kk[RV];
+#pragma unroll
+    for (int i = 0; i < RV; ++i) {
+      const int64_t e = int64_t(i) * kThreads + tid;
+      kk[i]           = e < n_cand ? ~fkey(vals[e]) : 0xffffffffu;
+    }
+    tk = radix_select_regs<kThreads, RV>(kk, k, hist, wave_tot, red, &sel_digit, &sel_rank);
+    if (tid == 0) { fill = 0; }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < RV; ++i) {
+      const int64_t e = int64_t(i) * kThreads + tid;
+      const bool take = e < n_cand && kk[i] <= tk;
+      const int slot  = wave_append(take, &fill);
+      if (take && slot < cap) { rid[slot] = to_id(cand[e]); }
+    }
+    __syncthreads();
+  } else if (ordered) {
     // the survivors' screen values lie close together above theta: the select starts below the
     // bits they share (all finite or +inf, so every key is below 0xffffffff)
     auto key_of = [&](int64_t e) { return ~fkey(vals[e]); };
@@ -1430,6 +1456,8 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
       }
     }
     __syncthreads();
+  }
+  if (ordered) {
     const int c = fill;
     __syncthreads();
     if (c <= cap) {
@@ -1450,11 +1478,11 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
   // phase B: the rest (everything when not ordered), in chunks of at most the buffer's free
   // room. A cut back to the k best (which also tightens U) is a select over the whole buffer: it
   // runs once the rows scored past the k best come to k / 8 (U then moves enough to save
-  // scores), or when the free room falls below a quarter of the buffer
-  // The ordered scan keeps few candidates (those whose lower bound reaches U), so a chunk spans
-  // the whole rest of them: a chunk no longer than the room would cost one round of barriers and
-  // loads per room's worth of candidates (1,024 at k = 2,048). When it keeps more than the room
-  // holds, that chunk is scanned again at the room's size, and so is every chunk after it.
+  // scores), or when the free room falls below a quarter of the buffer. The ordered scan keeps
+  // few candidates (those whose lower bound reaches U), so its chunk spans the whole rest of
+  // them: a chunk no longer than the room would cost one round of barriers and loads per room's
+  // worth of candidates (1,024 at k = 2,048). When it keeps more than the room holds, that chunk
+  // is scanned again at the room's size, and so is every chunk after it.
   int pending = have;  // entries [pending, have) are appended and not scored yet
   bool wide   = ordered;
   for (int64_t c0 = 0; c0 < n_cand;) {
