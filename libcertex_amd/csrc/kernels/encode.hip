@@ -199,6 +199,62 @@ __device__ inline double wave_sum(double v)
   return v;
 }
 
+/** A lane's coordinates of one row loaded together: j = j0 + 64 u + lane, u < kLaneChunk. */
+constexpr int kLaneChunk = 16;
+
+template <typename T>
+__device__ inline void lane_coords_t(const T* row, int64_t dim, int64_t j0, int lane,
+                                     double (&v)[kLaneChunk])
+{
+  T x[kLaneChunk];  // loads from clamped positions, unconditional: all issued before any use
+#pragma unroll
+  for (int u = 0; u < kLaneChunk; ++u) {
+    const int64_t j = j0 + 64 * u + lane;
+    x[u]            = row[j < dim ? j : dim - 1];
+  }
+#pragma unroll
+  for (int u = 0; u < kLaneChunk; ++u) { v[u] = j0 + 64 * u + lane < dim ? double(x[u]) : 0.0; }
+}
+
+/** Coordinates j0 + 64 u + lane of row i (0 at and past dim), all loads issued before any use:
+ *  a loop that used each coordinate as it arrived waited for one load at a time. */
+__device__ inline void lane_coords(const void* x, elem t, int64_t i, int64_t dim, int64_t j0,
+                                   int lane, double (&v)[kLaneChunk])
+{
+  if (t == elem::bf16) {
+    lane_coords_t(static_cast<const __bf16*>(x) + i * dim, dim, j0, lane, v);
+  } else if (t == elem::f32) {
+    lane_coords_t(static_cast<const float*>(x) + i * dim, dim, j0, lane, v);
+  } else {
+    lane_coords_t(static_cast<const _Float16*>(x) + i * dim, dim, j0, lane, v);
+  }
+}
+
+/** center[j0 + 64 u + lane], u < kLaneChunk (clamped positions past dim), loaded together. */
+__device__ inline void lane_center(const double* center, int64_t dim, int64_t j0, int lane,
+                                   double (&c)[kLaneChunk])
+{
+#pragma unroll
+  for (int u = 0; u < kLaneChunk; ++u) {
+    const int64_t j = j0 + 64 * u + lane;
+    c[u]            = center[j < dim ? j : dim - 1];
+  }
+}
+
+/** |x_i| (1 when zero) by a wave: per-lane fp64 partial sums in coordinate order, a butterfly. */
+__device__ inline double wave_row_norm(const void* x, elem t, int64_t i, int64_t dim, int lane)
+{
+  double s2 = 0;
+  for (int64_t j0 = 0; j0 < dim; j0 += 64 * kLaneChunk) {
+    double v[kLaneChunk];
+    lane_coords(x, t, i, dim, j0, lane, v);
+#pragma unroll
+    for (int u = 0; u < kLaneChunk; ++u) { s2 = fma(v[u], v[u], s2); }  // past dim: + 0, exact
+  }
+  s2 = wave_sum(s2);
+  return s2 > 0 ? sqrt(s2) : 1.0;
+}
+
 /**
  * out[0] raised to the largest |x / |x| - center| (|x - center| without normalizing) over the n
  * rows, sqrt_up of the fp64 sum: rows by waves over a grid stride as encode_rows_f16_kernel takes
@@ -214,20 +270,19 @@ __global__ __launch_bounds__(256) void max_norm_kernel(const void* x, elem t, in
   const int64_t waves = int64_t(gridDim.x) * 4;
   double m            = 0;
   for (int64_t i = blockIdx.x * int64_t(4) + wave; i < n; i += waves) {
-    double nrm = 1.0;
-    if (normalize) {
-      double s2 = 0;
-      for (int64_t j = lane; j < dim; j += 64) {
-        const double v = coord(x, t, i * dim + j);
-        s2             = fma(v, v, s2);
+    const double nrm = normalize ? wave_row_norm(x, t, i, dim, lane) : 1.0;
+    double s         = 0;
+    for (int64_t j0 = 0; j0 < dim; j0 += 64 * kLaneChunk) {
+      double v[kLaneChunk], c[kLaneChunk];
+      lane_coords(x, t, i, dim, j0, lane, v);
+      lane_center(center, dim, j0, lane, c);
+#pragma unroll
+      for (int u = 0; u < kLaneChunk; ++u) {
+        if (j0 + 64 * u + lane < dim) {
+          const double z = v[u] / nrm - c[u];
+          s              = fma(z, z, s);
+        }
       }
-      s2  = wave_sum(s2);
-      nrm = s2 > 0 ? sqrt(s2) : 1.0;
-    }
-    double s = 0;
-    for (int64_t j = lane; j < dim; j += 64) {
-      const double v = coord(x, t, i * dim + j) / nrm - center[j];
-      s              = fma(v, v, s);
     }
     m = fmax(m, sqrt_up(wave_sum(s), dim));
   }
@@ -259,21 +314,20 @@ __global__ __launch_bounds__(256) void encode_rows_f16_kernel(const void* x, ele
   const int64_t waves = int64_t(gridDim.x) * 4;
   double mh = 0, me = 0;  // this wave's largest bounds of |fp16(Z)| and |Z - fp16(Z)|
   for (int64_t i = blockIdx.x * int64_t(4) + wave; i < n; i += waves) {
-    _Float16* dst = reinterpret_cast<_Float16*>(rows + i * halves);
-    double nrm    = 1.0;
-    if (normalize) {
-      double s2 = 0;
-      for (int64_t j = lane; j < dim; j += 64) {
-        const double v = coord(x, t, i * dim + j);
-        s2             = fma(v, v, s2);
+    _Float16* dst    = reinterpret_cast<_Float16*>(rows + i * halves);
+    const double nrm = normalize ? wave_row_norm(x, t, i, dim, lane) : 1.0;
+    double a         = 0;
+    for (int64_t j0 = 0; j0 < dim; j0 += 64 * kLaneChunk) {
+      double v[kLaneChunk], c[kLaneChunk];
+      lane_coords(x, t, i, dim, j0, lane, v);
+      lane_center(center, dim, j0, lane, c);
+#pragma unroll
+      for (int u = 0; u < kLaneChunk; ++u) {
+        if (j0 + 64 * u + lane < dim) {
+          const double z = (v[u] / nrm - c[u]) * inv_alpha;
+          a              = fma(z, z, a);
+        }
       }
-      s2  = wave_sum(s2);
-      nrm = s2 > 0 ? sqrt(s2) : 1.0;
-    }
-    double a = 0;
-    for (int64_t j = lane; j < dim; j += 64) {
-      const double z = (coord(x, t, i * dim + j) / nrm - center[j]) * inv_alpha;
-      a              = fma(z, z, a);
     }
     a = wave_sum(a);  // the same value in every lane: the branch below is uniform
     if (!(sqrt(a) <= kF16Safe)) {
@@ -282,13 +336,22 @@ __global__ __launch_bounds__(256) void encode_rows_f16_kernel(const void* x, ele
       continue;
     }
     double nz = 0, ez = 0;
-    for (int64_t j = lane; j < dim; j += 64) {
-      const double z   = (coord(x, t, i * dim + j) / nrm - center[j]) * inv_alpha;
-      const _Float16 h = to_f16(z);
-      const double e   = z - double(h);  // exact (Sterbenz, or h = 0)
-      dst[j]           = h;
-      nz               = fma(double(h), double(h), nz);
-      ez               = fma(e, e, ez);
+    for (int64_t j0 = 0; j0 < dim; j0 += 64 * kLaneChunk) {
+      double v[kLaneChunk], c[kLaneChunk];
+      lane_coords(x, t, i, dim, j0, lane, v);
+      lane_center(center, dim, j0, lane, c);
+#pragma unroll
+      for (int u = 0; u < kLaneChunk; ++u) {
+        const int64_t j = j0 + 64 * u + lane;
+        if (j < dim) {
+          const double z   = (v[u] / nrm - c[u]) * inv_alpha;
+          const _Float16 h = to_f16(z);
+          const double e   = z - double(h);  // exact (Sterbenz, or h = 0)
+          dst[j]           = h;
+          nz               = fma(double(h), double(h), nz);
+          ez               = fma(e, e, ez);
+        }
+      }
     }
     for (int64_t j = dim + lane; j < halves; j += 64) { dst[j] = _Float16(0.0f); }
     nz = wave_sum(nz);
@@ -349,25 +412,25 @@ __global__ __launch_bounds__(256) void encode_queries_f16_kernel(const void* q, 
     if (lane == 0) { qscal[3 * i] = qscal[3 * i + 1] = qscal[3 * i + 2] = 0.0; }
     return;
   }
-  double nrm = 1.0;
-  if (normalize) {
-    double s2 = 0;
-    for (int64_t j = lane; j < dim; j += 64) {
-      const double v = coord(q, t, i * dim + j);
-      s2             = fma(v, v, s2);
-    }
-    s2  = wave_sum(s2);
-    nrm = s2 > 0 ? sqrt(s2) : 1.0;
-  }
+  const double nrm = normalize ? wave_row_norm(q, t, i, dim, lane) : 1.0;
   double a = 0, nw = 0, ew = 0;
-  for (int64_t j = lane; j < dim; j += 64) {
-    const double w   = (coord(q, t, i * dim + j) / nrm - center[j]) * inv_alpha;
-    const _Float16 h = to_f16(w);
-    const double e   = w - double(h);
-    put(j, h);
-    a                = fma(w, w, a);
-    nw               = fma(double(h), double(h), nw);
-    ew               = fma(e, e, ew);
+  for (int64_t j0 = 0; j0 < dim; j0 += 64 * kLaneChunk) {
+    double v[kLaneChunk], c[kLaneChunk];
+    lane_coords(q, t, i, dim, j0, lane, v);
+    lane_center(center, dim, j0, lane, c);
+#pragma unroll
+    for (int u = 0; u < kLaneChunk; ++u) {
+      const int64_t j = j0 + 64 * u + lane;
+      if (j < dim) {
+        const double w   = (v[u] / nrm - c[u]) * inv_alpha;
+        const _Float16 h = to_f16(w);
+        const double e   = w - double(h);
+        put(j, h);
+        a  = fma(w, w, a);
+        nw = fma(double(h), double(h), nw);
+        ew = fma(e, e, ew);
+      }
+    }
   }
   for (int64_t j = dim + lane; j < halves; j += 64) { put(j, _Float16(0.0f)); }
   a  = wave_sum(a);
