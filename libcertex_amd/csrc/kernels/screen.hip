@@ -418,7 +418,7 @@ void launch(const screen_args& a, hipStream_t stream)
   b.spill_cap   = !ANCHORS && a.spill_q != nullptr ? a.spill_pool / blocks : 0;
   if constexpr (ANCHORS && !FILT) {
     // coarse groups keep their running maxima in registers: groups of 32 queries (2 tiles)
-    // leave room for them
+    // leave room for them; 16 (one tile) for 256-byte rows in 128-query blocks, as below
     if (ks == 2 && qb_size == 512) {
       screen_kernel<R, 2, 512, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
     } else if (ks == 2) {
@@ -426,7 +426,7 @@ void launch(const screen_args& a, hipStream_t stream)
     } else if (ks == 4 && qb_size == 512) {
       screen_kernel<R, 4, 512, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
     } else if (ks == 4) {
-      screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
+      screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 1><<<grid, 256, 0, stream>>>(b);
     }
   } else {
     launch_other<R, ANCHORS, FILT>(b, grid, ks, qb_size, stream);
@@ -445,7 +445,9 @@ void launch_other(const screen_args& b, dim3 grid, int ks, int qb_size, hipStrea
     }
   }
   // groups of 32 queries: with 64, the fragments of 256-byte rows took more than the registers of
-  // two waves per SIMD, and the compiler made the group's code a function call
+  // two waves per SIMD, and the compiler made the group's code a function call. 256-byte rows in
+  // 128-query blocks take groups of 16 (one query tile): 166 VGPRs, three waves per SIMD, whose
+  // row loads (each feeding a quarter of the MFMAs of a 512-query block) then overlap more
   if (ks == 2 && qb_size == 512) {
     screen_kernel<R, 2, 512, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
   } else if (ks == 2) {
@@ -453,7 +455,7 @@ void launch_other(const screen_args& b, dim3 grid, int ks, int qb_size, hipStrea
   } else if (ks == 4 && qb_size == 512) {
     screen_kernel<R, 4, 512, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
   } else if (ks == 4) {
-    screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
+    screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 1><<<grid, 256, 0, stream>>>(b);
   }
   // other row widths are rejected by the host before any launch
 }
