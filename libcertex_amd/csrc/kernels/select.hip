@@ -274,6 +274,133 @@ __device__ inline void bitonic_sort(uint64_t* key, uint32_t* row, int P)
   }
 }
 
+/** (ka, ra) comes before (kb, rb): ascending key, then ascending row. */
+__device__ __forceinline__ bool pair_less(uint64_t ka, uint32_t ra, uint64_t kb, uint32_t rb)
+{
+  return ka < kb || (ka == kb && ra < rb);
+}
+
+/**
+ * One compare-exchange stage (SIZE, STRIDE) of bitonic_sort over kThreads E pairs held E per
+ * thread in registers, thread t holding positions t E .. t E + E - 1: within the thread for
+ * STRIDE < E, by a cross-lane exchange for partners in the same wave (STRIDE < 64 E), else
+ * through LDS (key / row, two barriers).
+ */
+template <int E, int SIZE, int STRIDE>
+__device__ __forceinline__ void bitonic_stage_regs(uint64_t (&k)[E], uint32_t (&r)[E],
+                                                   uint64_t* key, uint32_t* row)
+{
+  const int t = threadIdx.x;
+  if constexpr (STRIDE < E) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if ((e & STRIDE) == 0) {
+        const int p     = e + STRIDE;
+        const bool up   = ((t * E + e) & SIZE) == 0;
+        const bool swap = up ? pair_less(k[p], r[p], k[e], r[e]) : pair_less(k[e], r[e], k[p], r[p]);
+        const uint64_t ke = k[e], kp = k[p];
+        const uint32_t re = r[e], rp = r[p];
+        k[e] = swap ? kp : ke;
+        k[p] = swap ? ke : kp;
+        r[e] = swap ? rp : re;
+        r[p] = swap ? re : rp;
+      }
+    }
+  } else if constexpr (STRIDE < 64 * E) {
+    constexpr int D  = STRIDE / E;  // partner lane distance
+    const bool lower = (t & D) == 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const uint64_t ok  = __shfl_xor(k[e], D);
+      const uint32_t orr = __shfl_xor(r[e], D);
+      const bool up      = ((t * E + e) & SIZE) == 0;
+      if (pair_less(k[e], r[e], ok, orr) != (lower == up)) {  // the lower one keeps the minimum
+        k[e] = ok;                                             // going up
+        r[e] = orr;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      key[t * E + e] = k[e];
+      row[t * E + e] = r[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int g        = t * E + e;
+      const uint64_t ok  = key[g ^ STRIDE];
+      const uint32_t orr = row[g ^ STRIDE];
+      const bool up      = (g & SIZE) == 0;
+      if (pair_less(k[e], r[e], ok, orr) != (((g & STRIDE) == 0) == up)) {
+        k[e] = ok;
+        r[e] = orr;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int E, int SIZE, int STRIDE>
+__device__ __forceinline__ void bitonic_strides_regs(uint64_t (&k)[E], uint32_t (&r)[E],
+                                                     uint64_t* key, uint32_t* row)
+{
+  bitonic_stage_regs<E, SIZE, STRIDE>(k, r, key, row);
+  if constexpr (STRIDE > 1) { bitonic_strides_regs<E, SIZE, STRIDE / 2>(k, r, key, row); }
+}
+
+template <int E, int SIZE>
+__device__ __forceinline__ void bitonic_sizes_regs(uint64_t (&k)[E], uint32_t (&r)[E],
+                                                   uint64_t* key, uint32_t* row)
+{
+  bitonic_strides_regs<E, SIZE, SIZE / 2>(k, r, key, row);
+  if constexpr (SIZE < kThreads * E) { bitonic_sizes_regs<E, 2 * SIZE>(k, r, key, row); }
+}
+
+/**
+ * bitonic_sort of exactly kThreads E pairs (the same network, the same result), the pairs held E
+ * per thread in registers: of the 66 stages of 2,048 pairs only the 3 whose partners sit in
+ * another wave go through LDS and barriers (every stage of the LDS sort takes a barrier).
+ */
+template <int E>
+__device__ void bitonic_sort_regs(uint64_t* key, uint32_t* row)
+{
+  const int t = threadIdx.x;
+  uint64_t k[E];
+  uint32_t r[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    k[e] = key[t * E + e];
+    r[e] = row[t * E + e];
+  }
+  __syncthreads();  // every pair is read before the cross-wave stages write
+  bitonic_sizes_regs<E, 2>(k, r, key, row);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    key[t * E + e] = k[e];
+    row[t * E + e] = r[e];
+  }
+  __syncthreads();
+}
+
+/** bitonic_sort; with REGS, the register form for 1,024 and 2,048 pairs (it takes about 130
+ *  VGPRs, which a kernel pays at every phase). */
+template <bool REGS>
+__device__ inline void sort_pairs(uint64_t* key, uint32_t* row, int P)
+{
+  if constexpr (REGS) {
+    if (P == 8 * kThreads) {
+      bitonic_sort_regs<8>(key, row);
+      return;
+    }
+    if (P == 4 * kThreads) {
+      bitonic_sort_regs<4>(key, row);
+      return;
+    }
+  }
+  bitonic_sort(key, row, P);
+}
+
 __device__ inline int pow2_at_least(int v)
 {
   int p = 1;
@@ -533,7 +660,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a,
     rid[j] = ~0u;
   }
   __syncthreads();
-  bitonic_sort(key, rid, P);
+  sort_pairs<false>(key, rid, P);
   for (int j = tid; j < k; j += kThreads) {
     put_result(a, q * k + j, j < have ? key_score(key[j]) : 0.0, j < have ? int64_t(rid[j]) : -1);
   }
@@ -1546,7 +1673,7 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
       rid[j] = ~0u;
     }
     __syncthreads();
-    bitonic_sort(key, rid, P);
+    sort_pairs<L == 16>(key, rid, P);
     have = have < k ? have : k;
   }
   for (int j = tid; j < k; j += kThreads) {
