@@ -84,6 +84,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   __shared__ __attribute__((aligned(16))) uint8_t qlds[QB * ROWB];
   __shared__ val_t thl[ANCHORS ? 1 : QB];
   __shared__ val_t gml[ANCHORS ? 4 * QB : 1];
+  __shared__ val_t ftr[ANCHORS ? 4 * 256 : 1];  // fine groups: each wave's 16 x 16 transpose
   __shared__ uint32_t hit_q[ANCHORS ? 1 : kHitCap];
   __shared__ uint32_t hit_row[ANCHORS ? 1 : kHitCap];
   __shared__ float hit_val[ANCHORS || !R::kValues ? 1 : kHitCap];
@@ -222,7 +223,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
           const int64_t q    = q0 + g * GQ + qt * 16 + (lane & 15);
           const int64_t qc   = q < w.q_end ? q : w.q_end - 1;  // padding: any live query's
           const uint32_t kp  = FILT ? filter_mask(a, w, SL, qc, row0) : 0u;
-          anchor_tile_fine<R, FILT>(col, row0, q, q < w.q_end, a, w, gmax, kp);
+          anchor_tile_fine<R, FILT>(col, row0, q, q < w.q_end, a, w, gmax, kp, ftr + wave * 256);
         }
       } else {
 #pragma unroll

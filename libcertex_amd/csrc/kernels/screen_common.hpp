@@ -455,32 +455,66 @@ __device__ __forceinline__ void anchor_tile(const typename R::acc_t (&col)[4], i
 }
 
 /**
- * Anchor pass with fine groups, one 16-query tile of a 64-row step: each lane writes, for each of
- * its 4 row tiles, the best screen value of its 4 consecutive anchors straight to the group table:
- * group column grp_base + (scan index of the first of the 4) / 4. row0 is the scan index of the
- * lane's bit 0; q the lane's query (written only when live).
+ * Anchor pass with fine groups, one 16-query tile of a 64-row step: the best screen value of each
+ * lane's 4 consecutive anchors of each of its 4 row tiles is one group, column grp_base + (scan
+ * index of the first of the 4) / 4 of the query's row of the group table. row0 is the scan index
+ * of the lane's bit 0; q the lane's query (written only when live).
+ *
+ * With a wave's LDS block tr (256 values), the 16 x 16 (query, group) values of the tile go
+ * through tr so that each store instruction writes 4 queries x 16 consecutive groups (64 bytes of
+ * each of 4 table rows); stored straight from the accumulators, each store instruction wrote 4
+ * bytes to each of 16 rows. Without tr the lanes store their values directly.
  */
 template <typename R, bool FILT>
 __device__ __forceinline__ void anchor_tile_fine(const typename R::acc_t (&col)[4], int64_t row0,
                                                  int64_t q, bool live, const screen_args& a,
                                                  const screen_work& w, typename R::val_t* gmax,
-                                                 uint32_t keep)
+                                                 uint32_t keep, typename R::val_t* tr = nullptr)
 {
-  using val_t = typename R::val_t;
+  using val_t    = typename R::val_t;
+  const int lane = threadIdx.x & 63;
+  val_t m[4];
 #pragma unroll
   for (int bt = 0; bt < 4; ++bt) {
-    const int64_t first = row0 + bt * 16;  // scan index of the group's first anchor
-    val_t m             = R::lowest();
+    m[bt] = R::lowest();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       val_t v = col[bt][r];
       if constexpr (FILT) {
         if (!((keep >> (bt * 4 + r)) & 1u)) { v = R::lowest(); }
       }
-      m = R::vmax(m, v);
+      m[bt] = R::vmax(m[bt], v);
     }
-    if (live && first < w.n_scan) { gmax[table_entry(a, q, first / kFineGroup)] = m; }
   }
+  if (tr == nullptr) {
+#pragma unroll
+    for (int bt = 0; bt < 4; ++bt) {
+      const int64_t first = row0 + bt * 16;  // scan index of the group's first anchor
+      if (live && first < w.n_scan) { gmax[table_entry(a, q, first / kFineGroup)] = m[bt]; }
+    }
+    return;
+  }
+  // lane (query ql, sub) holds groups 4 bt + sub of the step: into tr[query][group of the step]
+  const int ql  = lane & 15;
+  const int sub = lane >> 4;
+#pragma unroll
+  for (int bt = 0; bt < 4; ++bt) { tr[ql * 16 + bt * 4 + sub] = m[bt]; }
+  // LDS operations of a wave complete in order; the fence keeps the compiler from moving the
+  // reads above the other lanes' writes
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  // store c: lane (sub, gi) takes group gi of query 4 c + sub of the tile
+  const int gi          = lane & 15;
+  const int64_t first   = row0 - 4 * sub + 4 * gi;  // the step's first row (a multiple of 64), + 4 gi
+  const int64_t q_tile  = q - ql;
+  const bool has_group  = first < w.n_scan;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int qi    = 4 * c + sub;
+    const val_t v   = tr[qi * 16 + gi];
+    const int64_t x = q_tile + qi;
+    if (has_group && x < w.q_end) { gmax[table_entry(a, x, first / kFineGroup)] = v; }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // every read before the next tile's writes
 }
 
 }  // namespace certex_amd::screen_detail

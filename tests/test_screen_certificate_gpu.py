@@ -231,7 +231,8 @@ def test_fp16_certificate(gpu, kind, d, metric, k):
     if get("all_rows"):
         pytest.skip("fewer than k anchor groups: every row is scored, no screen to check")
     cap, count, rows = buckets(get, B)
-    vals = get("vals", np.float32, (B, cap)).astype(np.float64)
+    with np.errstate(invalid="ignore"):  # slots past a query's count hold whatever was there
+        vals = get("vals", np.float32, (B, cap)).astype(np.float64)
     lb = get("lb", np.float64, (B, cap))
     ub = get("ub", np.float64, (B, cap))
     U = get("ub_q", np.float64)
