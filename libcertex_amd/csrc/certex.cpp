@@ -1322,8 +1322,11 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
     auto* d_ga   = reinterpret_cast<certex_amd::screen_group*>(dev + 3 * lab_bytes);
     auto* d_gs   = reinterpret_cast<certex_amd::screen_group*>(dev + 3 * lab_bytes + tab_bytes);
     void* temp   = dev + 3 * lab_bytes + 2 * tab_bytes;
-    CERTEX_HIP_TRY(certex_amd::sort_by_label(qlabels, B, d_iota, d_sorted, d_order, temp, sort_bytes,
-                                             stream));
+    const bool small = certex_amd::route_small_fits(B, n_lab);
+    if (!small) {
+      CERTEX_HIP_TRY(certex_amd::sort_by_label(qlabels, B, d_iota, d_sorted, d_order, temp,
+                                               sort_bytes, stream));
+    }
     certex_amd::route_table_args ra{};
     ra.sorted        = d_sorted;
     ra.B             = B;
@@ -1340,7 +1343,11 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
     ra.screen_chunk  = route.screen_chunk;
     ra.anchor_groups = d_ga;
     ra.screen_groups = d_gs;
-    certex_amd::route_tables(ra, stream);
+    if (small) {  // few labels: the sort and the tables in one launch
+      certex_amd::route_small(ra, qlabels, d_order, d_sorted, stream);
+    } else {
+      certex_amd::route_tables(ra, stream);
+    }
     route.anchor_groups = d_ga;
     route.screen_groups = d_gs;
   }

@@ -519,6 +519,13 @@ struct route_table_args {
   screen_group* screen_groups;
 };
 void route_tables(const route_table_args& a, hipStream_t stream);
+/** Whether route_small takes a batch of B labels over n_labels partition labels. */
+bool route_small_fits(int64_t B, int64_t n_labels);
+/** The routing of a batch in one launch for few labels: order / sorted of the batch's labels (a
+ *  stable sort by label, as sort_by_label; a.sorted = sorted) and the group tables of
+ *  route_tables. */
+void route_small(const route_table_args& a, const int32_t* labels, int32_t* order, int32_t* sorted,
+                 hipStream_t stream);
 /** dst row i = src row ids[i] (rows of row_bytes bytes). */
 void gather_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes, void* dst,
                  hipStream_t stream);

@@ -68,6 +68,29 @@ constexpr int kRouteThreads = 1024;
  * groups and workgroup counts (rounded up to 8), an exclusive scan over the block places them
  * after the previous rounds' groups.
  */
+/** Label l's group (its partition rows, its queries [q0, q0 + nq) of the sorted batch) and the
+ *  workgroups of its anchor pass (ta) and screen (ts), each rounded up to 8 (an XCD octet). */
+__device__ inline screen_group route_group(const route_table_args& a, int64_t l, int64_t q0,
+                                           int64_t nq, int64_t& ta, int64_t& ts)
+{
+  screen_group g{0, 0, 0, 0, 0};
+  ta = ts = 0;
+  g.x0 = a.offsets[l];
+  g.nx = a.offsets[l + 1] - g.x0;
+  g.q0 = q0;
+  g.nq = g.nx > 0 ? nq : 0;
+  if (g.nq > 0) {
+    const int64_t anchors = a.anchor_pairs ? paired_anchor_count(g.x0, g.nx, a.anchor_stride)
+                                           : (g.nx + a.anchor_stride - 1) / a.anchor_stride;
+    ta = screen_group_tiles(g.nq + (g.q0 & a.anchor_lead), anchors, a.anchor_qb, a.anchor_chunk);
+    ts = a.screen_tiled ? paired_group_tiles(g, a.rows_paired, a.screen_qb, a.screen_chunk)
+                        : screen_group_tiles(g.nq, g.nx, a.screen_qb, a.screen_chunk);
+    ta = (ta + 7) / 8 * 8;
+    ts = (ts + 7) / 8 * 8;
+  }
+  return g;
+}
+
 __global__ __launch_bounds__(kRouteThreads) void route_tables_kernel(route_table_args a)
 {
   __shared__ int64_t sa[kRouteThreads], ss[kRouteThreads];
@@ -80,19 +103,8 @@ __global__ __launch_bounds__(kRouteThreads) void route_tables_kernel(route_table
     screen_group g{0, 0, 0, 0, 0};
     int64_t ta = 0, ts = 0;
     if (l < a.n_labels) {
-      g.x0 = a.offsets[l];
-      g.nx = a.offsets[l + 1] - g.x0;
-      g.q0 = lower_pos(a.sorted, a.B, l);
-      g.nq = g.nx > 0 ? lower_pos(a.sorted, a.B, l + 1) - g.q0 : 0;
-      if (g.nq > 0) {
-        const int64_t anchors = a.anchor_pairs ? paired_anchor_count(g.x0, g.nx, a.anchor_stride)
-                                               : (g.nx + a.anchor_stride - 1) / a.anchor_stride;
-        ta = screen_group_tiles(g.nq + (g.q0 & a.anchor_lead), anchors, a.anchor_qb, a.anchor_chunk);
-        ts = a.screen_tiled ? paired_group_tiles(g, a.rows_paired, a.screen_qb, a.screen_chunk)
-                            : screen_group_tiles(g.nq, g.nx, a.screen_qb, a.screen_chunk);
-        ta = (ta + 7) / 8 * 8;
-        ts = (ts + 7) / 8 * 8;
-      }
+      const int64_t q0 = lower_pos(a.sorted, a.B, l);
+      g                = route_group(a, l, q0, lower_pos(a.sorted, a.B, l + 1) - q0, ta, ts);
     }
     // exclusive scan of the workgroup counts over the round (Hillis-Steele in LDS)
     sa[tid] = ta;
@@ -119,6 +131,117 @@ __global__ __launch_bounds__(kRouteThreads) void route_tables_kernel(route_table
       base_s += ss[tid];
     }
     __syncthreads();
+  }
+}
+
+/**
+ * The routing of a batch of B query labels in one workgroup, for few labels (kSmallBuckets
+ * buckets at most: labels below 0, each label of the partition, labels past it): a stable
+ * counting sort of the batch by label into order / sorted, then the group tables of
+ * route_tables_kernel, their queries read off the bucket counts. Chunks of 64 queries go to the
+ * waves in turn; per chunk, one ballot per bucket gives the bucket's count and each query's rank
+ * within the chunk. Replaces the radix sort (an index fill and five launches) and the separate
+ * group-table launch. Labels below 0 and past the partition keep their relative order but not
+ * their order by value: the groups only ask where each partition label starts and ends.
+ */
+constexpr int kSmallBuckets = 64;
+constexpr int kSmallCounts  = 12288;  // LDS words for (chunk, bucket) counts: chunks x buckets
+
+__global__ __launch_bounds__(kRouteThreads) void route_small_kernel(route_table_args a,
+                                                                    const int32_t* labels,
+                                                                    int32_t* order, int32_t* sorted)
+{
+  __shared__ int cnt[kSmallCounts];   // [chunk][bucket]: count, then its exclusive prefix over chunks
+  __shared__ int tot[kSmallBuckets];  // queries per bucket
+  __shared__ int start[kSmallBuckets + 1];
+  __shared__ int64_t sa[kSmallBuckets], ss[kSmallBuckets];
+  const int tid      = threadIdx.x;
+  const int lane     = tid & 63;
+  const int wave     = tid >> 6;
+  constexpr int W    = kRouteThreads / 64;
+  const int64_t B    = a.B;
+  const int nb       = int(a.n_labels) + 2;
+  const int n_chunks = int((B + 63) / 64);
+  auto bucket_of     = [&](int64_t i) {
+    const int32_t l = labels[i];
+    return l < 0 ? 0 : (l < a.n_labels ? l + 1 : nb - 1);
+  };
+  // counts per (chunk, bucket)
+  for (int c = wave; c < n_chunks; c += W) {
+    const int64_t i = int64_t(c) * 64 + lane;
+    const int b     = i < B ? bucket_of(i) : -1;
+    for (int v = 0; v < nb; ++v) {
+      const uint64_t m = __ballot(b == v);
+      if (lane == 0) { cnt[c * nb + v] = __builtin_popcountll(m); }
+    }
+  }
+  __syncthreads();
+  // per bucket, the exclusive prefix of its counts over the chunks (a wave per bucket)
+  for (int v = wave; v < nb; v += W) {
+    int carry = 0;
+    for (int c0 = 0; c0 < n_chunks; c0 += 64) {
+      const int c = c0 + lane;
+      const int x = c < n_chunks ? cnt[c * nb + v] : 0;
+      int incl    = x;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off);
+        if (lane >= off) { incl += y; }
+      }
+      if (c < n_chunks) { cnt[c * nb + v] = carry + incl - x; }
+      carry += __shfl(incl, 63);
+    }
+    if (lane == 0) { tot[v] = carry; }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int v = 0; v < nb; ++v) {
+      start[v] = run;
+      run += tot[v];
+    }
+    start[nb] = run;
+  }
+  __syncthreads();
+  // the scatter: a query's place is its bucket's start, the bucket's count in earlier chunks and
+  // its rank among the chunk's queries of the bucket
+  for (int c = wave; c < n_chunks; c += W) {
+    const int64_t i = int64_t(c) * 64 + lane;
+    const int b     = i < B ? bucket_of(i) : -1;
+    int rank        = 0;
+    for (int v = 0; v < nb; ++v) {
+      const uint64_t m = __ballot(b == v);
+      if (b == v) {
+        rank = int(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
+      }
+    }
+    if (b >= 0) {
+      const int pos = start[b] + cnt[c * nb + b] + rank;
+      order[pos]    = int32_t(i);
+      sorted[pos]   = labels[i];
+    }
+  }
+  // the group tables: label l is bucket l + 1; the workgroup counts' exclusive scan over the labels
+  const int64_t l = tid;
+  int64_t ta = 0, ts = 0;
+  screen_group g{0, 0, 0, 0, 0};
+  if (l < a.n_labels) { g = route_group(a, l, start[l + 1], tot[l + 1], ta, ts); }
+  if (tid < kSmallBuckets) {
+    sa[tid] = ta;
+    ss[tid] = ts;
+  }
+  __syncthreads();
+  if (l < a.n_labels) {
+    int64_t pa = 0, ps = 0;
+    for (int64_t j = 0; j < l; ++j) {
+      pa += sa[j];
+      ps += ss[j];
+    }
+    screen_group ga = g, gs = g;
+    ga.tile0 = pa;
+    gs.tile0 = ps;
+    a.anchor_groups[l] = ga;
+    a.screen_groups[l] = gs;
   }
 }
 
@@ -275,6 +398,21 @@ void route_tables(const route_table_args& a, hipStream_t stream)
 {
   if (a.n_labels == 0) { return; }
   route_tables_kernel<<<1, kRouteThreads, 0, stream>>>(a);
+}
+
+bool route_small_fits(int64_t B, int64_t n_labels)
+{
+  const int64_t nb = n_labels + 2;
+  return n_labels > 0 && nb <= kSmallBuckets && (B + 63) / 64 * nb <= kSmallCounts;
+}
+
+void route_small(const route_table_args& a, const int32_t* labels, int32_t* order, int32_t* sorted,
+                 hipStream_t stream)
+{
+  if (!route_small_fits(a.B, a.n_labels)) {
+    throw std::logic_error("certex: the one-workgroup routing takes at most 62 labels and 12,288 chunk counts");
+  }
+  route_small_kernel<<<1, kRouteThreads, 0, stream>>>(a, labels, order, sorted);
 }
 
 void label_offsets(const int32_t* keys_sorted, int64_t n, int64_t n_labels, int64_t* offsets,

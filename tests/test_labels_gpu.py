@@ -222,3 +222,26 @@ def test_equal_labels_in_label_order_after_another_search(gpu, kind):
     assert idx.core.n_partitioned == len(X)
     D, I = search(idx, Q, 10, lq)
     check(X, Q, 10, metric, D, I, row_labels=lx, query_labels=lq)
+
+
+@pytest.mark.parametrize("kind", ["uint8", "float32"])
+def test_query_labels_outside_the_partition(gpu, kind):
+    """Query labels below 0 and past the partition's labels, mixed with the partition's own, in a
+    ragged batch: such queries match no partition row (only rows added later with that label,
+    through the filter). On the device the routing sorts them into buckets before and after the
+    partition's labels; both placements must give the oracle's results."""
+    d = 128
+    if kind == "uint8":
+        X, Q, metric = data.mixture_u8(20_000, seed=91), data.mixture_u8(1_037, seed=92), "l2"
+    else:
+        X, Q, metric = data.gaussian(20_000, d, 91), data.gaussian(1_037, d, 92), "ip"
+    lx = data.labels(len(X), 5, 93)
+    lq = np.random.default_rng(94).choice(np.array([-7, -1, 0, 1, 2, 3, 4, 5, 40], np.int32), len(Q))
+    idx = certex.Index(d, metric=metric)
+    idx.add(torch.from_numpy(X[:19_000]).cuda(), labels=torch.from_numpy(lx[:19_000]))
+    idx.partition_labels = False  # the next rows stay outside the partition: a tail
+    idx.add(torch.from_numpy(X[19_000:]).cuda(), labels=torch.from_numpy(lx[19_000:]))
+    assert idx.core.n_partitioned == 19_000
+    for batch in (2048, 300):
+        D, I = search(idx, Q, 10, lq, batch=batch)
+        check(X, Q, 10, metric, D, I, row_labels=lx, query_labels=lq)
