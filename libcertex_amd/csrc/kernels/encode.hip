@@ -412,12 +412,29 @@ __global__ __launch_bounds__(256) void encode_queries_f16_kernel(const void* q, 
     if (lane == 0) { qscal[3 * i] = qscal[3 * i + 1] = qscal[3 * i + 2] = 0.0; }
     return;
   }
-  const double nrm = normalize ? wave_row_norm(q, t, i, dim, lane) : 1.0;
+  // a query of at most 64 kLaneChunk coordinates is loaded once, for its norm and its encoding
+  const bool one_chunk = dim <= 64 * kLaneChunk;
+  double v[kLaneChunk], c[kLaneChunk];
+  double nrm = 1.0;
+  if (one_chunk) {
+    lane_coords(q, t, i, dim, 0, lane, v);
+    lane_center(center, dim, 0, lane, c);
+    if (normalize) {
+      double s2 = 0;
+#pragma unroll
+      for (int u = 0; u < kLaneChunk; ++u) { s2 = fma(v[u], v[u], s2); }  // past dim: + 0, exact
+      s2  = wave_sum(s2);
+      nrm = s2 > 0 ? sqrt(s2) : 1.0;
+    }
+  } else if (normalize) {
+    nrm = wave_row_norm(q, t, i, dim, lane);
+  }
   double a = 0, nw = 0, ew = 0;
   for (int64_t j0 = 0; j0 < dim; j0 += 64 * kLaneChunk) {
-    double v[kLaneChunk], c[kLaneChunk];
-    lane_coords(q, t, i, dim, j0, lane, v);
-    lane_center(center, dim, j0, lane, c);
+    if (!one_chunk) {
+      lane_coords(q, t, i, dim, j0, lane, v);
+      lane_center(center, dim, j0, lane, c);
+    }
 #pragma unroll
     for (int u = 0; u < kLaneChunk; ++u) {
       const int64_t j = j0 + 64 * u + lane;
