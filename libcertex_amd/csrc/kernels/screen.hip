@@ -63,8 +63,10 @@ __device__ __forceinline__ void static_for(F&& f)
   }
 }
 
-template <typename R, int KS, int QB, bool ANCHORS, bool FILT, int BT, int QT>
-__global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
+template <typename R, int KS, int QB, bool ANCHORS, bool FILT, int BT, int QT, bool FINE = false>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(QT == 1 && QB == 128 && (!ANCHORS || (FINE && !FILT)) ? 3 : 2)))
+void screen_kernel(screen_args a)
 {
   using acc_t  = typename R::acc_t;
   using frag_t = typename R::frag_t;
@@ -76,7 +78,10 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   constexpr int SPT    = TR / kStepRows; // chunk steps (kStepRows rows) per step
   // coarse anchor groups without argmax or filter: each lane folds its values into a register per
   // (query group, query tile) every step; the lanes of a query reduce and write once per group
-  constexpr bool RUNREG = ANCHORS && !FILT;
+  constexpr bool RUNREG = ANCHORS && !FILT && !FINE;
+  // FINE (anchor passes with fine groups of 4 anchors, a.fine) and coarse anchor passes are
+  // separate kernels: each carries only its own group code, and its registers
+  static_assert(ANCHORS || !FINE, "fine groups are an anchor pass's");
   static_assert(NG % 2 == 0, "query groups are processed in pairs");
   static_assert(BT * 4 <= 32, "a lane's survivor mask of one query tile is 32 bits");
   static_assert(!ANCHORS || BT == 4, "the anchor pass runs 64-row steps");
@@ -116,7 +121,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   // coarse anchor groups of one group per wave: each wave's group maxima wait in LDS, and the
   // workgroup writes each query's 4 consecutive columns together at its end (one 16-byte run per
   // query instead of four 4-byte stores to four lines of the table)
-  const bool staged = RUNREG && !a.fine && quarter == a.group_steps;
+  const bool staged = RUNREG && quarter == a.group_steps;
 
   if (tid == 0) { n_hits = 0; }
   // only the groups that run are staged (a routed group's block is often mostly padding)
@@ -216,7 +221,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     mfmas(bf, acc);
 
     if constexpr (ANCHORS) {
-      if (a.fine) {
+      if constexpr (FINE) {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
           const acc_t col[4] = {acc[0][qt], acc[1][qt], acc[2][qt], acc[3][qt]};
@@ -290,7 +295,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     row0 = s * TR + (lane >> 4) * 4;
     if constexpr (ANCHORS && FILT) { load_step_labels(a, w, row0, SL); }
     if constexpr (RUNREG) {
-      if (!a.fine) {
+      {
         // the groups at compile time, so that run[][] stays in registers
         auto group_run = [&](auto gc, const frag_t (&bf)[QT][KS]) {
           constexpr int g = decltype(gc)::value;
@@ -353,7 +358,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
     }
     if constexpr (ANCHORS) {
       // end of an anchor group (group_steps steps, aligned to the wave's range)
-      if (!a.fine && ((s + 1) % a.group_steps == 0 || s + 1 == n_steps)) {
+      if (!FINE && ((s + 1) % a.group_steps == 0 || s + 1 == n_steps)) {
         for (int e = lane; e < QB; e += 64) {
           if (q0 + e < w.q_end) { gmax[table_entry(a, q0 + e, s / a.group_steps)] = gml[wave * QB + e]; }
           gml[wave * QB + e] = R::lowest();
@@ -396,7 +401,7 @@ __global__ __launch_bounds__(256, 2) void screen_kernel(screen_args a)
   }
 }
 
-template <typename R, bool ANCHORS, bool FILT>
+template <typename R, bool ANCHORS, bool FILT, bool FINE>
 void launch_other(const screen_args& b, dim3 grid, int ks, int qb_size, hipStream_t stream);
 
 template <typename R, bool ANCHORS, bool FILT>
@@ -417,6 +422,12 @@ void launch(const screen_args& a, hipStream_t stream)
   const int ks  = a.row_bytes / 64;
   screen_args b = a;
   b.spill_cap   = !ANCHORS && a.spill_q != nullptr ? a.spill_pool / blocks : 0;
+  if constexpr (ANCHORS) {
+    if (a.fine) {
+      launch_other<R, ANCHORS, FILT, true>(b, grid, ks, qb_size, stream);
+      return;
+    }
+  }
   if constexpr (ANCHORS && !FILT) {
     // coarse groups keep their running maxima in registers: groups of 32 queries (2 tiles)
     // leave room for them; 16 (one tile) for 256-byte rows in 128-query blocks, as below
@@ -430,12 +441,13 @@ void launch(const screen_args& a, hipStream_t stream)
       screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 1><<<grid, 256, 0, stream>>>(b);
     }
   } else {
-    launch_other<R, ANCHORS, FILT>(b, grid, ks, qb_size, stream);
+    launch_other<R, ANCHORS, FILT, false>(b, grid, ks, qb_size, stream);
   }
 }
 
-/** The launches other than the register-maxima anchor pass. */
-template <typename R, bool ANCHORS, bool FILT>
+/** The launches other than the register-maxima anchor pass (FINE: anchor passes with fine
+ *  groups). */
+template <typename R, bool ANCHORS, bool FILT, bool FINE>
 void launch_other(const screen_args& b, dim3 grid, int ks, int qb_size, hipStream_t stream)
 {
   if constexpr (!ANCHORS && !R::kValues) {
@@ -450,13 +462,13 @@ void launch_other(const screen_args& b, dim3 grid, int ks, int qb_size, hipStrea
   // 128-query blocks take groups of 16 (one query tile): 166 VGPRs, three waves per SIMD, whose
   // row loads (each feeding a quarter of the MFMAs of a 512-query block) then overlap more
   if (ks == 2 && qb_size == 512) {
-    screen_kernel<R, 2, 512, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
+    screen_kernel<R, 2, 512, ANCHORS, FILT, 4, 2, FINE><<<grid, 256, 0, stream>>>(b);
   } else if (ks == 2) {
-    screen_kernel<R, 2, 128, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
+    screen_kernel<R, 2, 128, ANCHORS, FILT, 4, 2, FINE><<<grid, 256, 0, stream>>>(b);
   } else if (ks == 4 && qb_size == 512) {
-    screen_kernel<R, 4, 512, ANCHORS, FILT, 4, 2><<<grid, 256, 0, stream>>>(b);
+    screen_kernel<R, 4, 512, ANCHORS, FILT, 4, 2, FINE><<<grid, 256, 0, stream>>>(b);
   } else if (ks == 4) {
-    screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 1><<<grid, 256, 0, stream>>>(b);
+    screen_kernel<R, 4, 128, ANCHORS, FILT, 4, 1, FINE><<<grid, 256, 0, stream>>>(b);
   }
   // other row widths are rejected by the host before any launch
 }
