@@ -91,10 +91,17 @@ template <typename F>
 __device__ void key_range(int64_t n, F key_of, uint32_t& lo, uint32_t& hi, int& below,
                           uint32_t* red);
 
+constexpr int kCollect = 2048;  // keys of the selected first digit copied into LDS, at most
+
+template <typename F>
+__device__ uint32_t radix_select_collect(int64_t n, int rank, F key_of, uint32_t lo, uint32_t hi,
+                                         int* hist, int* wave_tot, uint32_t* sel_digit,
+                                         int* sel_rank, uint32_t* list, int* n_list);
+
 __global__ __launch_bounds__(kThreads) void threshold_kernel(
   const int32_t* gmax, int64_t n_groups, int64_t nq, int k, int32_t* theta)
 {
-  __shared__ int hist[256];
+  __shared__ int hist[257];
   __shared__ int wave_tot[4];
   __shared__ uint32_t red[48];
   __shared__ uint32_t sel_digit;
@@ -115,8 +122,11 @@ __global__ __launch_bounds__(kThreads) void threshold_kernel(
   int below;
   key_range(n_groups, key_of, lo, hi, below, red);
   // the k-th largest value: the k-th smallest descending key (0xffffffff is the lowest value)
+  __shared__ uint32_t list[kCollect];
+  __shared__ int n_list;
   const uint32_t key = k > below ? 0xffffffffu
-                                 : radix_select(n_groups, k, key_of, lo, hi, hist, wave_tot, &sel_digit, &sel_rank);
+                                 : radix_select_collect(n_groups, k, key_of, lo, hi, hist, wave_tot,
+                                                        &sel_digit, &sel_rank, list, &n_list);
   if (tid == 0) {
     const int32_t t = desc_value(key);
     theta[q]        = t > kKeepAll ? t : kKeepAll;
@@ -1082,7 +1092,7 @@ __device__ inline double screen_upper_bound(float vf, const threshold_f_args& a,
  */
 __global__ __launch_bounds__(kThreads) void threshold_f16_cert_kernel(threshold_f_args a)
 {
-  __shared__ int hist[256];
+  __shared__ int hist[257];
   __shared__ int wave_tot[4];
   __shared__ uint32_t red[48];
   __shared__ uint32_t sel_digit;
@@ -1111,7 +1121,10 @@ __global__ __launch_bounds__(kThreads) void threshold_f16_cert_kernel(threshold_
     }
     return;
   }
-  const uint32_t key = radix_select(a.n_groups, a.k, key_of, lo, hi, hist, wave_tot, &sel_digit, &sel_rank);
+  __shared__ uint32_t list[kCollect];
+  __shared__ int n_list;
+  const uint32_t key = radix_select_collect(a.n_groups, a.k, key_of, lo, hi, hist, wave_tot,
+                                            &sel_digit, &sel_rank, list, &n_list);
   if (tid == 0) {
     const double U = screen_upper_bound(key_value(~key), a, q);
     a.theta[q]     = theta_of(U, a, q);
@@ -1247,31 +1260,112 @@ __device__ void key_range(int64_t n, F key_of, uint32_t& lo, uint32_t& hi, int& 
   block_min_max_sum<kThreads>(lo, hi, below, red);
 }
 
+/** The state of an LDS radix select: the bits fixed so far (prefix under mask), the bits below
+ *  them (r), and the rank still sought among the keys that share the prefix. */
+struct radix_state {
+  uint32_t prefix, mask;
+  int r, rank;
+};
+
+/** The select's start: every key in [lo, hi] shares the bits above the first one where lo and hi
+ *  differ. */
+__device__ inline radix_state radix_start(uint32_t lo, uint32_t hi, int rank)
+{
+  radix_state st;
+  st.r      = lo == hi ? 0 : 32 - __builtin_clz(lo ^ hi);
+  st.mask   = st.r == 32 ? 0u : ~((1u << st.r) - 1u);
+  st.prefix = lo & st.mask;
+  st.rank   = rank;
+  return st;
+}
+
+/**
+ * One digit of the select (the top 8 of the r bits left, or all of them): an LDS histogram of
+ * that digit over the keys key_of(e), e < n, that share the prefix, and the digit that holds the
+ * rank. Returns how many keys share the longer prefix. Every thread of the block calls it.
+ */
+template <typename F>
+__device__ int radix_pass(int64_t n, F key_of, radix_state& st, int* hist, int* wave_tot,
+                          uint32_t* sel_digit, int* sel_rank)
+{
+  const int tid     = threadIdx.x;
+  const int w       = st.r < 8 ? st.r : 8;
+  const int shift   = st.r - w;
+  const uint32_t dm = (1u << w) - 1u;
+  hist[tid]         = 0;
+  __syncthreads();
+  for (int64_t e0 = 0; e0 < n; e0 += int64_t(kThreads) * kBatch) {
+    uint32_t kk[kBatch];  // loads first (from clamped positions), then the counts
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int64_t e = e0 + i * kThreads + tid;
+      kk[i]           = key_of(e < n ? e : n - 1);
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      if (e0 + i * kThreads + tid < n && (kk[i] & st.mask) == st.prefix) {
+        atomicAdd(&hist[(kk[i] >> shift) & dm], 1);
+      }
+    }
+  }
+  __syncthreads();
+  const int c    = hist[tid];
+  const int incl = block_scan_incl(c, wave_tot);
+  if (incl - c < st.rank && st.rank <= incl) {
+    *sel_digit = uint32_t(tid);
+    *sel_rank  = st.rank - (incl - c);
+    hist[256]  = c;  // the digit's count (one word past the histogram)
+  }
+  __syncthreads();
+  st.prefix |= *sel_digit << shift;
+  st.mask |= dm << shift;
+  st.rank = *sel_rank;
+  st.r -= w;
+  const int count = hist[256];
+  __syncthreads();
+  return count;
+}
+
 /**
  * The rank-th smallest (1-based) of the 32-bit keys key_of(e), e < n, given their range: lo the
  * smallest key, hi the largest below 0xffffffff, and rank at most the number of keys below
  * 0xffffffff. An LDS radix select, 8 bits at a time from the top of the bits below the common
  * prefix of lo and hi (every key in between shares that prefix; a key 0xffffffff that shares it
  * sorts last and leaves the rank-th unchanged). Every thread of the block calls it and gets the
- * same key.
+ * same key. hist holds 257 words.
  */
 template <typename F>
 __device__ uint32_t radix_select(int64_t n, int rank, F key_of, uint32_t lo, uint32_t hi, int* hist,
                                  int* wave_tot, uint32_t* sel_digit, int* sel_rank)
 {
-  if (lo == hi) { return lo; }
-  const int tid   = threadIdx.x;
-  int r           = 32 - __builtin_clz(lo ^ hi);  // bits below the common prefix
-  uint32_t mask   = r == 32 ? 0u : ~((1u << r) - 1u);
-  uint32_t prefix = lo & mask;
-  while (r > 0) {
-    const int w       = r < 8 ? r : 8;
-    const int shift   = r - w;
-    const uint32_t dm = (1u << w) - 1u;
-    hist[tid] = 0;
+  radix_state st = radix_start(lo, hi, rank);
+  while (st.r > 0) { (void)radix_pass(n, key_of, st, hist, wave_tot, sel_digit, sel_rank); }
+  return st.prefix;
+}
+
+/**
+ * radix_select for large n (a long row of a table in memory): after the first digit that leaves
+ * at most kCollect keys sharing the prefix, one more pass copies them into list (LDS) and the
+ * other digits read them there instead of all n keys, which saves the row's reads of the digits
+ * after it. The same key as radix_select.
+ */
+template <typename F>
+__device__ uint32_t radix_select_collect(int64_t n, int rank, F key_of, uint32_t lo, uint32_t hi,
+                                         int* hist, int* wave_tot, uint32_t* sel_digit,
+                                         int* sel_rank, uint32_t* list, int* n_list)
+{
+  radix_state st = radix_start(lo, hi, rank);
+  if (st.r == 0) { return st.prefix; }
+  int count = radix_pass(n, key_of, st, hist, wave_tot, sel_digit, sel_rank);
+  while (st.r > 0 && count > kCollect) {
+    count = radix_pass(n, key_of, st, hist, wave_tot, sel_digit, sel_rank);
+  }
+  if (st.r > 0) {
+    const int tid = threadIdx.x;
+    if (tid == 0) { *n_list = 0; }
     __syncthreads();
     for (int64_t e0 = 0; e0 < n; e0 += int64_t(kThreads) * kBatch) {
-      uint32_t kk[kBatch];  // loads first (from clamped positions), then the counts
+      uint32_t kk[kBatch];
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
         const int64_t e = e0 + i * kThreads + tid;
@@ -1279,26 +1373,17 @@ __device__ uint32_t radix_select(int64_t n, int rank, F key_of, uint32_t lo, uin
       }
 #pragma unroll
       for (int i = 0; i < kBatch; ++i) {
-        if (e0 + i * kThreads + tid < n && (kk[i] & mask) == prefix) {
-          atomicAdd(&hist[(kk[i] >> shift) & dm], 1);
-        }
+        const bool take = e0 + i * kThreads + tid < n && (kk[i] & st.mask) == st.prefix;
+        const int slot  = wave_append(take, n_list);
+        if (take) { list[slot] = kk[i]; }
       }
     }
     __syncthreads();
-    const int c    = hist[tid];
-    const int incl = block_scan_incl(c, wave_tot);
-    if (incl - c < rank && rank <= incl) {
-      *sel_digit = uint32_t(tid);
-      *sel_rank  = rank - (incl - c);
-    }
-    __syncthreads();
-    prefix |= *sel_digit << shift;
-    mask |= dm << shift;
-    rank = *sel_rank;
-    r -= w;
-    __syncthreads();
+    const int nl = *n_list;  // = count
+    auto key_at  = [&](int64_t e) { return list[e]; };
+    while (st.r > 0) { (void)radix_pass(nl, key_at, st, hist, wave_tot, sel_digit, sel_rank); }
   }
-  return prefix;
+  return st.prefix;
 }
 
 /**
@@ -1487,7 +1572,7 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
   auto* key = reinterpret_cast<uint64_t*>(dyn);                 // [cap]
   auto* rid = reinterpret_cast<uint32_t*>(dyn + size_t(cap) * 8);  // [cap]
   auto* qv  = reinterpret_cast<double*>(dyn + size_t(cap) * 12);  // [dim]
-  __shared__ int hist[256];
+  __shared__ int hist[257];
   __shared__ int wave_tot[4];
   __shared__ uint32_t red[48];
   __shared__ uint32_t sel_digit;
