@@ -486,7 +486,7 @@ def bench_config5(args):
             "ids_equal_to_brute_force_16_queries": agree,
         },
         "roofline": {
-            "bound": "mfma", "kernel": "screen_kernel<int8_rows,2,512,false,false,8,2> (int8 MFMA screen, 128-row steps)",
+            "bound": "mfma", "kernel": "screen_kernel<int8_rows,2,512,false,false,8,2,false> (int8 MFMA screen, 128-row steps)",
             "achieved": round(achieved, 2), "peak": P_INT8_TOPS, "unit": "TOP/s",
             "frac": round(achieved / P_INT8_TOPS, 4), "traffic": None,
             "avg_launch_ms": round(screen_ms, 4), "ops_per_launch": ops_per_launch,
@@ -767,7 +767,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma",
-            "kernel": "screen_kernel<int8_rows,2,512,false,false,8,2> (int8 MFMA screen, 128-row steps)",
+            "kernel": "screen_kernel<int8_rows,2,512,false,false,8,2,false> (int8 MFMA screen, 128-row steps)",
             "achieved": round(achieved, 2),
             "peak": P_INT8_TOPS,
             "unit": "TOP/s",
