@@ -313,18 +313,41 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
   stage(s + 1, std::false_type{}, std::false_type{});
 
   if constexpr (ANCH) {
-    // fine groups: the 4 consecutive anchors of a lane's row tile are one group of the table
-    val_t* gmax = static_cast<val_t*>(a.gmax);
+    // fine groups: the 4 consecutive anchors of a lane's row tile are one group of the table.
+    // Lane (query frow, fch) holds group 4 bt + fch of the wave's 16 RT / 4 consecutive groups
+    // for each row tile bt; the values go through the staging LDS (free after the last stage),
+    // transposed to the wave's queries x groups, so that each store instruction writes whole
+    // 128-byte runs of 2 table rows instead of 16 bytes of each of 16 rows
+    constexpr int NGW = 4 * RT;       // groups of the wave per query tile
+    constexpr int TS  = NGW + 1;      // LDS words per query (one more: fewer bank conflicts)
+    constexpr int QPS = 64 / NGW;     // queries per store instruction
+    static_assert(64 % NGW == 0 && 16 % QPS == 0, "a store instruction covers whole query rows");
+    static_assert(kTileWaves * QT * 16 * TS * 4 <= tile_lds(TQ), "the transpose fits the staging");
+    __syncthreads();  // every wave is done with the stage buffers
+    val_t* gmax       = static_cast<val_t*>(a.gmax);
+    val_t* tr         = reinterpret_cast<val_t*>(lds) + (wave * QT) * 16 * TS;
+    const int64_t g0  = (scan0 + wr * 16 * RT) / kFineGroup;  // the wave's first group
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      const int qloc  = wq * 16 * QT + qt * 16 + frow;
-      const bool live = qloc >= q_lo && qloc < n_q;
 #pragma unroll
       for (int bt = 0; bt < RT; ++bt) {
-        const int64_t first = scan0 + wr * 16 * RT + bt * 16 + fch * 4;  // scan index
-        const acc_t v       = acc[bt][qt];
-        const val_t m       = R::vmax(R::vmax(v[0], v[1]), R::vmax(v[2], v[3]));
-        if (live && first < w.n_scan) { gmax[table_entry(a, w.q0 + qloc, first / kFineGroup)] = m; }
+        const acc_t v = acc[bt][qt];
+        tr[qt * 16 * TS + frow * TS + bt * 4 + fch] = R::vmax(R::vmax(v[0], v[1]), R::vmax(v[2], v[3]));
+      }
+    }
+    // LDS operations of a wave complete in order; the fence keeps the compiler from moving the
+    // reads above the other lanes' writes
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const int j          = lane % NGW;  // the lane's group of the wave
+    const bool has_group = (g0 + j) * kFineGroup < w.n_scan;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+      for (int c = 0; c < 16 / QPS; ++c) {
+        const int qi    = c * QPS + lane / NGW;  // query of the tile
+        const int qloc  = wq * 16 * QT + qt * 16 + qi;
+        const val_t m   = tr[qt * 16 * TS + qi * TS + j];
+        if (has_group && qloc >= q_lo && qloc < n_q) { gmax[table_entry(a, w.q0 + qloc, g0 + j)] = m; }
       }
     }
     return;
