@@ -94,8 +94,10 @@ def test_exact_ties(gpu):
 
 
 def test_k_up_to_2048(gpu):
+    """k from 500 to 2,048: the final sort of 1,024 and 2,048 pairs runs in registers (8 or 4 per
+    thread, k 513 to 2,048), smaller ones in LDS."""
     X, Q = correlated(12_000, 32, 40, seed=5)
-    for k in (2048, 500):
+    for k in (2048, 1024, 1000, 513, 500):
         D, I, _ = run(X, Q, k)
         check(X, Q, k, "l2", D, I)
 
