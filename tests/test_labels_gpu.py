@@ -245,3 +245,18 @@ def test_query_labels_outside_the_partition(gpu, kind):
     for batch in (2048, 300):
         D, I = search(idx, Q, 10, lq, batch=batch)
         check(X, Q, 10, metric, D, I, row_labels=lx, query_labels=lq)
+
+
+def test_many_labels(gpu):
+    """300 labels, more than the one-workgroup device routing takes (62): device labels go through
+    the radix sort and the group-table kernel; host labels through the host's counting sort."""
+    X = data.mixture_u8(60_000, seed=101)
+    Q = data.mixture_u8(900, seed=102)
+    lx = data.labels(len(X), 300, 103)
+    lq = data.labels(len(Q), 310, 104)  # labels 300 .. 309: no rows
+    idx = certex.Index(X.shape[1])
+    idx.add(torch.from_numpy(X).cuda(), labels=torch.from_numpy(lx))
+    assert idx.core.n_partitioned == len(X)
+    for batch in (2048, 257):
+        D, I = search(idx, Q, 10, lq, batch=batch)
+        check(X, Q, 10, "l2", D, I, row_labels=lx, query_labels=lq)
