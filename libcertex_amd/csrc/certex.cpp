@@ -777,12 +777,67 @@ void probe_pass(cuvs::resources const& res, index_state const& st, certex_amd::s
  * row may sit in two groups: the k-th best group must stand for k distinct rows. Without enough
  * rows in some query's probed lists the batch uses the anchors alone.
  */
+/** Fewest anchors of a list whose anchors may bound a threshold (8 such lists hold 4 k anchors
+ *  for every k <= 64). */
+constexpr int64_t kListAnchorMin = 32;
+
 struct table_plan {
   anchor_plan ap{};
   bool anchors = true;
   probe_plan pp;
+  int list_anchors = 0;  // > 0: the groups are the list anchors of this many nearest lists
   int64_t n_groups = 0;
 };
+
+/**
+ * The list-anchor threshold's center terms: cterm, with +inf for every list of fewer than
+ * kListAnchorMin anchors (rows list_offsets[j] + i anchor_stride), so that the nearest lists of a
+ * query are lists of at least that many anchors. Set where the lists are set (build, load).
+ */
+void set_anchor_centers(cuvs::resources const& res, index_state& st)
+{
+  hipStream_t stream = static_cast<hipStream_t>(res.stream());
+  const int L        = st.n_lists;
+  const int Lp       = certex_amd::pad_centers(L);
+  const int64_t s    = std::max(1, st.anchor_stride);
+  std::vector<float> ct(static_cast<size_t>(Lp));
+  CERTEX_HIP_TRY(hipMemcpyAsync(ct.data(), st.cterm.p, size_t(Lp) * 4, hipMemcpyDeviceToHost, stream));
+  CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  int big = 0;
+  for (int j = 0; j < L; ++j) {
+    const int64_t na = (st.list_offsets[size_t(j) + 1] - st.list_offsets[size_t(j)] + s - 1) / s;
+    if (na < kListAnchorMin) {
+      ct[size_t(j)] = INFINITY;
+    } else {
+      ++big;
+    }
+  }
+  st.cterm_anchor.resize_discard(size_t(Lp) * 4);
+  CERTEX_HIP_TRY(hipMemcpyAsync(st.cterm_anchor.p, ct.data(), size_t(Lp) * 4, hipMemcpyHostToDevice, stream));
+  CERTEX_HIP_TRY(hipStreamSynchronize(stream));
+  st.n_anchor_lists = big;
+}
+
+/**
+ * Lists whose anchors bound the threshold of a search that probes no list: the p = min(lists, 8)
+ * nearest lists of each query, or 0 where the anchors of every row serve instead. Any k distinct
+ * rows bound the k-th best screen value from below, so the threshold is exact either way; the
+ * lists only pick rows near the query, and the anchors of its 8 nearest lists (about 1,200 at
+ * 10M rows in 4,096 lists) hold the anchors that set the threshold of the anchors of every row.
+ * Integer rows of at most 256 bytes, no filter (the anchors would have to pass it), k <= 64, at
+ * least half of the rows listed, and 8 lists of at least kListAnchorMin anchors to choose from
+ * (the nearest lists are chosen among those: every query meets 8 kListAnchorMin >= 4 k anchors).
+ */
+int list_anchor_lists(index_state const& st, int k, search_params const& params,
+                      certex_amd::filter_args const& fa)
+{
+  const int p = certex_amd::kMaxProbe;
+  if (!is_int(st.type) || st.row_bytes > 256 || st.n_anchor_lists < p || params.probe_lists > 0 ||
+      fa.kind != 0 || k > 64 || 2 * st.n_listed < st.size) {
+    return 0;
+  }
+  return p;
+}
 
 auto plan_table(cuvs::resources const& res, index_state const& st, const void* qrows, int64_t B,
                 int64_t nq_pad, int k, search_params const& params,
@@ -792,6 +847,12 @@ auto plan_table(cuvs::resources const& res, index_state const& st, const void* q
   if (route != nullptr) {
     tp.ap       = route->ap;
     tp.n_groups = tp.ap.n_groups;
+    return tp;
+  }
+  tp.list_anchors = list_anchor_lists(st, k, params, fa);
+  if (tp.list_anchors > 0) {
+    tp.anchors  = false;
+    tp.n_groups = 64 * int64_t(tp.list_anchors);
     return tp;
   }
   bool probe = st.n_lists > 0 && params.probe_lists > 0 && (fa.kind == 0 || fa.kind == 1) &&
@@ -818,7 +879,23 @@ template <typename F>
 void table_pass(cuvs::resources const& res, index_state const& st, certex_amd::screen_args aa,
                 table_plan const& tp, route_plan const* route, F&& launch)
 {
-  hipStream_t stream = res.state().stream;
+  auto& rs           = res.state();
+  hipStream_t stream = rs.stream;
+  if (tp.list_anchors > 0) {
+    // the nearest lists of every query, then the group table of their anchors (every column)
+    const int p  = tp.list_anchors;
+    const int Lp = certex_amd::pad_centers(st.n_lists);
+    auto* lists  = static_cast<int32_t*>(rs.get(cuvs::detail::ws_probe, size_t(aa.nq) * p * 4));
+    void* temp   = rs.get(cuvs::detail::ws_probe_dist,
+                          certex_amd::list_anchor_temp_bytes(aa.nq, st.n_lists));
+    certex_amd::nearest_lists_i8(aa.qcodes, st.row_bytes, aa.nq, st.centers_q.p,
+                                 st.cterm_anchor.as<float>(), Lp, lists, stream);
+    certex_amd::list_anchor_groups(st.codes.as<int8_t>(), st.rowc.as<int32_t>(), st.row_bytes,
+                                   aa.qcodes, aa.nq, lists, st.list_offsets_dev.as<int64_t>(),
+                                   st.n_lists, std::max(1, st.anchor_stride), temp,
+                                   static_cast<int32_t*>(aa.gmax), stream);
+    return;
+  }
   if (tp.pp.n_pairs > 0) {
     if (is_int(st.type)) {
       certex_amd::fill_i32(static_cast<int32_t*>(aa.gmax), aa.nq_pad * tp.n_groups, INT32_MIN,
@@ -850,6 +927,7 @@ void capture_common(index_state const& st, table_plan const& tp, int64_t B, int6
   t_capture.value("group_steps", int64_t(tp.ap.group_steps));
   t_capture.value("fine", int64_t(tp.ap.fine));
   t_capture.value("anchor_stride", int64_t(tp.ap.stride));
+  t_capture.value("list_anchors", int64_t(tp.list_anchors));
   t_capture.value("row_bytes", int64_t(st.row_bytes));
   t_capture.value("size", int64_t(st.size));
   t_capture.put("codes", st.codes.p, size_t(st.size) * st.row_bytes, stream);
@@ -922,6 +1000,11 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
     t_capture.put("theta", theta, size_t(B) * 4, stream);
     if (tp.n_groups >= k) {
       t_capture.put("gmax", rs.get(cuvs::detail::ws_gmax, 1), size_t(B) * tp.n_groups * 4, stream);
+    }
+    if (tp.list_anchors > 0) {
+      t_capture.put("lists", rs.get(cuvs::detail::ws_probe, 1), size_t(B) * tp.list_anchors * 4,
+                    stream);
+      t_capture.put("list_offsets", st.list_offsets_dev.p, size_t(st.n_lists + 1) * 8, stream);
     }
     if (!all_rows) {
       t_capture.put("count", count, size_t(B) * 4, stream);
@@ -1709,13 +1792,15 @@ void fit_lists(cuvs::resources const& res, index_state& st, int64_t n)
                                   hipMemcpyDeviceToHost, stream));
     CERTEX_HIP_TRY(hipStreamSynchronize(stream));
   }
-  st.n_lists    = L;
-  st.list_width = width;
+  st.n_lists          = L;
+  st.list_width       = width;
+  st.list_offsets_dev = std::move(offs);
   st.centers    = std::move(centers);
   st.centers_q  = std::move(centers_q);
   st.cterm      = std::move(cterm);
   st.row_ids    = std::move(row_ids);
   st.id_rows    = std::move(id_rows);
+  set_anchor_centers(res, st);
 }
 
 /**
@@ -2318,6 +2403,10 @@ void deserialize(cuvs::resources const& res, std::string const& filename, index<
     st.list_offsets.assign(size_t(L) + 1, 0);
     is.read(reinterpret_cast<char*>(st.list_offsets.data()), std::streamsize((L + 1) * 8));
     expects(bool(is), "certex: the index file is truncated");
+    // the searches read the rows of a list at these offsets on the GPU
+    expects(st.list_offsets.front() == 0 && st.list_offsets.back() == st.n_listed &&
+              std::is_sorted(st.list_offsets.begin(), st.list_offsets.end()),
+            "certex: corrupt index file");
     const int Lp = certex_amd::pad_centers(L);
     st.row_ids.resize_discard(size_t(std::max<int64_t>(st.n_listed, 1)) * 4);
     st.id_rows.resize_discard(size_t(std::max<int64_t>(st.n_listed, 1)) * 4);
@@ -2331,8 +2420,12 @@ void deserialize(cuvs::resources const& res, std::string const& filename, index<
     certex_amd::finish_centers(nullptr, nullptr, L, Lp, st.list_width, !is_int(st.type),
                                st.centers.as<float>(), st.centers_q.p, st.cterm.as<float>(),
                                stream);
+    st.list_offsets_dev.resize_discard(size_t(L + 1) * 8);
+    CERTEX_HIP_TRY(hipMemcpyAsync(st.list_offsets_dev.p, st.list_offsets.data(), size_t(L + 1) * 8,
+                                  hipMemcpyHostToDevice, stream));
     res.sync();
     st.n_lists = L;
+    set_anchor_centers(res, st);
   }
   refresh_anchors(res, st, 0, n);
   res.sync();

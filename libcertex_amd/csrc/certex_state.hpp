@@ -292,6 +292,11 @@ struct index_state {
   cuvs::detail::device_buffer centers_q;  // the centers in the rows' type [pad_centers, row_bytes]
   cuvs::detail::device_buffer cterm;      // float [pad_centers]: |centers_q|^2 / 2
   std::vector<int64_t> list_offsets;
+  cuvs::detail::device_buffer list_offsets_dev;  // the same offsets in device memory
+  // cterm with +inf for the lists of fewer than kListAnchorMin anchors, and the count of the others:
+  // the center terms of the list-anchor threshold, whose lists then all hold that many anchors
+  cuvs::detail::device_buffer cterm_anchor;
+  int n_anchor_lists = 0;
   int list_width = 0;  // elements of a screening row: row_bytes (int8) or halves (fp16)
   mutable std::shared_mutex rw;  // searches: shared per batch; publication of updates: exclusive
   std::mutex writer;             // one update at a time

@@ -571,6 +571,29 @@ void center_distances(const void* rows, bool f16, int64_t n, int row_bytes,
 /** lists[q, 0 .. p) = the p nearest of the n_lists centers of dist row q (ld floats), p <= 8. */
 void nearest_lists(const float* dist, int64_t nq, int n_lists, int ld, int p, int32_t* lists,
                    hipStream_t stream);
+/**
+ * lists[q, 0 .. 8) = the 8 nearest lists of int8 query q (codes of 128 or 256 bytes) by
+ * cterm[c] - <q', center c>, ascending, ties to the lower list; centers of cterm +inf are never
+ * taken (-1 where fewer than 8 are finite). No distance matrix.
+ */
+void nearest_lists_i8(const int8_t* qcodes, int row_bytes, int64_t nq, const void* centers_q,
+                      const float* cterm, int n_centers_pad, int32_t* lists, hipStream_t stream);
+/** Bytes of the temporary memory of list_anchor_groups. */
+size_t list_anchor_temp_bytes(int64_t nq, int n_lists);
+/**
+ * The group table of the list anchors, a threshold source of integer rows of 128 or 256 bytes:
+ * for query q < nq and its t-th nearest list j = lists[q 8 + t] (t < 8; -1: none), anchor i of
+ * j is the stored row offsets[j] + i stride (i < ceil(rows of j / stride)), and column
+ * t 64 + i % 64 of the query's row of gmax (512 columns) gets the largest screen value
+ * <q', x'> + rowc[x] of its anchors (INT32_MIN for a column without one). Every column holds
+ * distinct rows, so the k-th largest column bounds the k-th best screen value from below. The
+ * pairs (q, t) are grouped by list in temp (list_anchor_temp_bytes), so that one workgroup copies
+ * the anchors of a list into LDS once for all of its queries.
+ */
+void list_anchor_groups(const int8_t* codes, const int32_t* rowc, int row_bytes,
+                        const int8_t* qcodes, int64_t nq, const int32_t* lists,
+                        const int64_t* offsets, int n_lists, int64_t stride, void* temp,
+                        int32_t* gmax, hipStream_t stream);
 /** sums[assign[i]] += row i; counts[assign[i]] += 1 (float atomics; width elements per row). */
 void center_sums(const void* rows, bool f16, int64_t n, int width, const int32_t* assign,
                  int n_centers, float* sums, unsigned int* counts, hipStream_t stream);

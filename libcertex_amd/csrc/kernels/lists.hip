@@ -11,7 +11,9 @@
 
 #include "../kernels.hpp"
 
+#include <algorithm>
 #include <cfloat>
+#include <stdexcept>
 
 namespace certex_amd {
 namespace {
@@ -208,6 +210,314 @@ __global__ __launch_bounds__(256) void top_lists_kernel(const float* dist, int64
   }
 }
 
+/**
+ * The 8 nearest lists of 64 queries per workgroup (int8 codes of 64 KS bytes): center distances
+ * cterm[c] - <q', center c> on the MFMA (operand A the centers, B the 4 query tiles held in
+ * registers, so that a center tile is read once for 64 queries). A lane sees the values (query
+ * 16 qt + lane % 16, center 4 (lane / 16) + r) of every W-th center tile and keeps its 2 best per
+ * query; the 64 candidates of a query (2 from each of its 4 lanes in each of the 8 waves) meet in
+ * LDS, where 8 rounds of a wave argmin pick its 8 (ties to the lower list). Two best per lane keep
+ * the 8 nearest unless three of them fall to one lane (the lists choose anchors near the query, so
+ * a near list in place of a nearer one changes speed, never results). No distance matrix is
+ * written. Centers of cterm +inf (padding, lists left out) are never picked.
+ */
+template <int KS>
+__global__ __launch_bounds__(512) void nearest_lists_i8_kernel(const int8_t* qcodes, int64_t nq,
+                                                               const int8_t* centers,
+                                                               const float* cterm, int n_centers,
+                                                               int32_t* lists)
+{
+  constexpr int ROWB = 64 * KS;
+  constexpr int P    = kMaxProbe;
+  constexpr int W    = 8;           // waves: each takes every W-th center tile
+  constexpr int QT   = 4;           // query tiles of the workgroup
+  constexpr int NC   = 4 * W * 2;   // candidates of a query
+  static_assert(NC == 64, "one candidate per lane");
+  __shared__ float cv[16 * QT][NC];
+  __shared__ int ci[16 * QT][NC];
+  const int lane   = threadIdx.x & 63;
+  const int wave   = threadIdx.x >> 6;
+  const int64_t q0 = int64_t(blockIdx.x) * 16 * QT;
+  v4i qb[QT][KS];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int64_t q  = q0 + 16 * qt + (lane & 15);
+    const int64_t qr = q < nq ? q : nq - 1;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qb[qt][ks] = *reinterpret_cast<const v4i*>(qcodes + qr * ROWB + 64 * ks + 16 * (lane >> 4));
+    }
+  }
+  // per query tile, the lane's two best, b0 <= b1 (centers grow along a lane: strict < keeps the
+  // lower center on ties)
+  float b0[QT], b1[QT];
+  int i0[QT], i1[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    b0[qt] = b1[qt] = INFINITY;
+    i0[qt] = i1[qt] = INT32_MAX;
+  }
+  constexpr int U = 2;  // tiles whose loads are in flight together
+  for (int ct0 = wave * 16; ct0 < n_centers; ct0 += 16 * W * U) {
+    v4i a[U][KS];
+    v4f ch[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c0 = ct0 + 16 * W * u < n_centers ? ct0 + 16 * W * u : ct0;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        a[u][ks] = *reinterpret_cast<const v4i*>(centers + int64_t(c0 + (lane & 15)) * ROWB +
+                                                 64 * ks + 16 * (lane >> 4));
+      }
+      ch[u] = *reinterpret_cast<const v4f*>(cterm + c0 + 4 * (lane >> 4));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (ct0 + 16 * W * u >= n_centers) { break; }
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[u][ks], qb[qt][ks], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v  = ch[u][r] - float(acc[r]);
+          const int c    = ct0 + 16 * W * u + 4 * (lane >> 4) + r;
+          const bool lt0 = v < b0[qt], lt1 = v < b1[qt];
+          b1[qt]         = lt0 ? b0[qt] : (lt1 ? v : b1[qt]);
+          i1[qt]         = lt0 ? i0[qt] : (lt1 ? c : i1[qt]);
+          b0[qt]         = lt0 ? v : b0[qt];
+          i0[qt]         = lt0 ? c : i0[qt];
+        }
+      }
+    }
+  }
+  const int grp = wave * 4 + (lane >> 4);
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int ql         = 16 * qt + (lane & 15);
+    cv[ql][2 * grp]      = b0[qt];
+    ci[ql][2 * grp]      = i0[qt];
+    cv[ql][2 * grp + 1]  = b1[qt];
+    ci[ql][2 * grp + 1]  = i1[qt];
+  }
+  __syncthreads();
+  // wave w picks for queries 8 w .. 8 w + 7, one candidate per lane
+  for (int qq = 0; qq < 16 * QT / W; ++qq) {
+    const int ql    = wave * (16 * QT / W) + qq;
+    const int64_t q = q0 + ql;
+    if (q >= nq) { break; }
+    float cvl = cv[ql][lane];
+    int cil   = ci[ql][lane];
+    for (int r = 0; r < P; ++r) {
+      float v = cvl;
+      int i   = cil;
+      for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off);
+        const int oi   = __shfl_xor(i, off);
+        if (ov < v || (ov == v && oi < i)) {
+          v = ov;
+          i = oi;
+        }
+      }
+      if (lane == 0) { lists[q * P + r] = i < n_centers && v < INFINITY ? i : -1; }
+      if (cil == i) {  // the owner pops the winner (a list is one lane's candidate)
+        cvl = INFINITY;
+        cil = INT32_MAX;
+      }
+    }
+  }
+}
+
+/** counts[j] = the (query, slot) pairs of lists[0, n) that name list j (-1: none). */
+__global__ void list_pair_count_kernel(const int32_t* lists, int64_t n, int32_t* counts)
+{
+  for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < n;
+       e += int64_t(gridDim.x) * blockDim.x) {
+    const int32_t j = lists[e];
+    if (j >= 0) { atomicAdd(counts + j, 1); }
+  }
+}
+
+/** Pairs of a list per workgroup of list_anchor_groups_kernel. */
+constexpr int kSlicePairs = 32;
+
+/**
+ * start[j] = the exclusive prefix sum of counts[0, L) (start[L] = the total), cursor = start, and
+ * slice[j] = the exclusive prefix sum of ceil(counts[j] / kSlicePairs) (slice[L] = the total): the
+ * first workgroup of list j in list_anchor_groups_kernel. One workgroup of 1,024 threads, each over
+ * a run of consecutive lists.
+ */
+__global__ __launch_bounds__(1024) void list_pair_scan_kernel(const int32_t* counts, int L,
+                                                              int32_t* start, int32_t* cursor,
+                                                              int32_t* slice)
+{
+  __shared__ int part[1024], spart[1024];
+  const int t   = threadIdx.x;
+  const int per = (L + 1023) / 1024;
+  const int b   = t * per;
+  const int e   = b + per < L ? b + per : L;
+  int sum = 0, ssum = 0;
+  for (int j = b; j < e; ++j) {
+    sum += counts[j];
+    ssum += (counts[j] + kSlicePairs - 1) / kSlicePairs;
+  }
+  part[t]  = sum;
+  spart[t] = ssum;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int v  = t >= off ? part[t - off] : 0;
+    const int sv = t >= off ? spart[t - off] : 0;
+    __syncthreads();
+    part[t] += v;
+    spart[t] += sv;
+    __syncthreads();
+  }
+  int run = part[t] - sum, srun = spart[t] - ssum;
+  for (int j = b; j < e; ++j) {
+    start[j]  = run;
+    cursor[j] = run;
+    slice[j]  = srun;
+    run += counts[j];
+    srun += (counts[j] + kSlicePairs - 1) / kSlicePairs;
+  }
+  if (t == 1023) {
+    start[L] = part[t];
+    slice[L] = spart[t];
+  }
+}
+
+/** pairs[cursor[j]++] = e for every pair e of lists[0, n) naming list j (the order within a list
+ *  is that of the atomics; each pair writes its own columns, so it does not matter). A pair
+ *  without a list (-1) gets its 64 columns of gmax (64 p per query) at the lowest value here. */
+__global__ void list_pair_fill_kernel(const int32_t* lists, int64_t n, int p, int32_t* cursor,
+                                      int32_t* pairs, int32_t* gmax)
+{
+  for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < n;
+       e += int64_t(gridDim.x) * blockDim.x) {
+    const int32_t j = lists[e];
+    if (j >= 0) {
+      pairs[atomicAdd(cursor + j, 1)] = int32_t(e);
+    } else {
+      int32_t* col = gmax + (e / p) * 64 * int64_t(p) + (e % p) * 64;
+      for (int g = 0; g < 64; ++g) { col[g] = INT32_MIN; }
+    }
+  }
+}
+
+/**
+ * Group table of the list anchors (int8 rows of ROWB = 128 or 256 bytes). Workgroup b serves list j
+ * (slice[j] <= b < slice[j + 1]) and its pairs (query q, slot t) [start[j] + kSlicePairs s, + 32),
+ * s = b - slice[j]. The anchors of j, its stored rows offsets[j] + i stride (i < ceil(rows of j /
+ * stride)), go into LDS in chunks of AC, with the slice's queries; anchor i joins group i % 64 of
+ * the pair's 64 columns gmax[q, 64 t, +64), so the groups hold distinct rows. The scores run on the
+ * int8 MFMA: operand A 16 anchors (from LDS; chunk c of anchor u in slot c ^ (u % 8) of its row),
+ * B 16 pairs' queries (registers), C the anchors' row terms, so lane l gets anchor 16 T +
+ * 4 (l / 16) + r of pair l % 16, in group 16 (T % 4) + 4 (l / 16) + r. Wave w takes the pairs'
+ * tile w % 2 and the anchor tiles T = w / 2, w / 2 + 2, ...: the two waves of a pair tile keep
+ * disjoint groups (T % 4 even or odd), 8 maxima per lane. A later chunk of a long list merges into
+ * the columns the earlier wrote (the same lanes own them).
+ */
+template <int ROWB>
+__global__ __launch_bounds__(256) void list_anchor_groups_kernel(
+  const int8_t* codes, const int32_t* rowc, const int8_t* qcodes, int p, const int64_t* offsets,
+  int n_lists, int64_t stride, const int32_t* start, const int32_t* slice, const int32_t* pairs,
+  int32_t* gmax)
+{
+  constexpr int KS  = ROWB / 64;      // 64-byte k-slices of a row
+  constexpr int NCH = ROWB / 16;      // 16-byte chunks of a row
+  constexpr int AC  = 32768 / ROWB;   // anchors per LDS chunk (a multiple of 64)
+  static_assert(kSlicePairs == 32, "two pair tiles per workgroup");
+  __shared__ v4i la[AC * NCH];
+  __shared__ v4i lq[kSlicePairs * NCH];
+  __shared__ __attribute__((aligned(16))) int32_t lc[AC];
+  const int b = blockIdx.x;
+  if (b >= slice[n_lists]) { return; }
+  int lo = 0, hi = n_lists - 1;  // the last list whose first workgroup is <= b
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (slice[mid] <= b) {
+      lo = mid;
+    } else {
+      hi = mid - 1;
+    }
+  }
+  const int j    = lo;
+  const int b0   = start[j] + kSlicePairs * (b - slice[j]);
+  const int b1   = b0 + kSlicePairs < start[j + 1] ? b0 + kSlicePairs : start[j + 1];
+  const int tid  = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int pt   = wave & 1;   // pair tile
+  const int par  = wave >> 1;  // anchor tiles of this parity
+  const int64_t r0 = offsets[j];
+  const int64_t na = (offsets[j + 1] - r0 + stride - 1) / stride;
+  const int64_t ng = 64 * int64_t(p);
+  for (int u = tid; u < (b1 - b0) * NCH; u += 256) {
+    const int e = pairs[b0 + u / NCH];
+    lq[u]       = *reinterpret_cast<const v4i*>(qcodes + int64_t(e / p) * ROWB + 16 * (u % NCH));
+  }
+  const int pl   = 16 * pt + (lane & 15);  // the lane's pair in the slice
+  const bool own = b0 + pl < b1;
+  for (int64_t a0 = 0; a0 < na; a0 += AC) {
+    const int nc = int(na - a0 < AC ? na - a0 : AC);
+    if (a0 > 0) { __syncthreads(); }  // the previous chunk's reads are done
+#pragma unroll 4
+    for (int u = tid; u < nc * NCH; u += 256) {
+      const int i = u / NCH, c = u % NCH;
+      la[i * NCH + (c ^ (i & 7))] =
+        *reinterpret_cast<const v4i*>(codes + (r0 + (a0 + i) * stride) * ROWB + 16 * c);
+    }
+    for (int i = tid; i < nc; i += 256) { lc[i] = rowc[r0 + (a0 + i) * stride]; }
+    __syncthreads();
+    if (b0 + 16 * pt >= b1) { continue; }  // no pair in this wave's tile
+    v4i qv[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) { qv[ks] = lq[(own ? pl : 0) * NCH + 4 * ks + (lane >> 4)]; }
+    int32_t run[2][4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) { run[h][r] = INT32_MIN; }
+    }
+    const int nt = (nc + 15) / 16;
+    for (int T = par; T < nt; T += 2) {
+      const int ua = 16 * T + (lane & 15);  // the anchor of the lane's A operand
+      v4i acc = *reinterpret_cast<const v4i*>(lc + 16 * T + 4 * (lane >> 4));
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const v4i a = la[ua * NCH + ((4 * ks + (lane >> 4)) ^ (ua & 7))];
+        acc         = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qv[ks], acc, 0, 0, 0);
+      }
+      const int h = (T >> 1) & 1;  // T % 4 = par + 2 h
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool live = 16 * T + 4 * (lane >> 4) + r < nc;
+        if (live && acc[r] > run[h][r]) { run[h][r] = acc[r]; }
+      }
+    }
+    if (own) {
+      const int e  = pairs[b0 + pl];
+      int32_t* row = gmax + int64_t(e / p) * ng + (e % p) * 64;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          // anchor a0 + 16 T + 4 (l / 16) + r, a0 a multiple of 64: group 16 (T % 4) + 4 (l / 16) + r
+          int32_t* col = row + 16 * (par + 2 * h) + 4 * (lane >> 4) + r;
+          if (a0 == 0) {
+            *col = run[h][r];
+          } else if (run[h][r] > *col) {
+            *col = run[h][r];
+          }
+        }
+      }
+    }
+  }
+}
+
 __device__ inline float element(const int8_t* rows, bool f16, int64_t i)
 {
   return f16 ? float(reinterpret_cast<const _Float16*>(rows)[i]) : float(rows[i]);
@@ -328,6 +638,58 @@ void nearest_lists(const float* dist, int64_t nq, int n_lists, int ld, int p, in
 {
   if (nq == 0) { return; }
   top_lists_kernel<<<blocks_for(nq * 64), 256, 0, stream>>>(dist, nq, n_lists, ld, p, lists);
+}
+
+void nearest_lists_i8(const int8_t* qcodes, int row_bytes, int64_t nq, const void* centers_q,
+                      const float* cterm, int n_centers_pad, int32_t* lists, hipStream_t stream)
+{
+  if (nq == 0) { return; }
+  const unsigned grid = unsigned((nq + 63) / 64);
+  const auto* c       = static_cast<const int8_t*>(centers_q);
+  if (row_bytes == 128) {
+    nearest_lists_i8_kernel<2><<<grid, 512, 0, stream>>>(qcodes, nq, c, cterm, n_centers_pad, lists);
+  } else if (row_bytes == 256) {
+    nearest_lists_i8_kernel<4><<<grid, 512, 0, stream>>>(qcodes, nq, c, cterm, n_centers_pad, lists);
+  } else {
+    throw std::logic_error("certex: the nearest lists of int8 queries take rows of 128 or 256 bytes");
+  }
+}
+
+size_t list_anchor_temp_bytes(int64_t nq, int n_lists)
+{
+  return size_t(4 * (int64_t(n_lists) + 1) + nq * kMaxProbe) * 4;
+}
+
+void list_anchor_groups(const int8_t* codes, const int32_t* rowc, int row_bytes,
+                        const int8_t* qcodes, int64_t nq, const int32_t* lists,
+                        const int64_t* offsets, int n_lists, int64_t stride, void* temp,
+                        int32_t* gmax, hipStream_t stream)
+{
+  if (nq == 0 || n_lists == 0) { return; }
+  if (row_bytes != 128 && row_bytes != 256) {
+    throw std::logic_error("certex: list anchors take rows of 128 or 256 bytes");
+  }
+  if (stride < 1) { throw std::logic_error("certex: bad list anchor stride"); }
+  const int64_t n = nq * kMaxProbe;
+  auto* counts    = static_cast<int32_t*>(temp);
+  auto* start     = counts + (n_lists + 1);
+  auto* cursor    = start + (n_lists + 1);
+  auto* slice     = cursor + (n_lists + 1);
+  auto* pairs     = slice + (n_lists + 1);
+  fill_u32(reinterpret_cast<uint32_t*>(counts), n_lists, 0, stream);
+  const unsigned g = unsigned(std::min<int64_t>((n + 255) / 256, 1024));
+  list_pair_count_kernel<<<g, 256, 0, stream>>>(lists, n, counts);
+  list_pair_scan_kernel<<<1, 1024, 0, stream>>>(counts, n_lists, start, cursor, slice);
+  list_pair_fill_kernel<<<g, 256, 0, stream>>>(lists, n, kMaxProbe, cursor, pairs, gmax);
+  // at most one partial slice per list: n_lists + n / kSlicePairs workgroups cover every slice
+  const unsigned wg = unsigned(n_lists + (n + kSlicePairs - 1) / kSlicePairs);
+  if (row_bytes == 128) {
+    list_anchor_groups_kernel<128><<<wg, 256, 0, stream>>>(codes, rowc, qcodes, kMaxProbe, offsets,
+                                                           n_lists, stride, start, slice, pairs, gmax);
+  } else {
+    list_anchor_groups_kernel<256><<<wg, 256, 0, stream>>>(codes, rowc, qcodes, kMaxProbe, offsets,
+                                                           n_lists, stride, start, slice, pairs, gmax);
+  }
 }
 
 void center_sums(const void* rows, bool f16, int64_t n, int width, const int32_t* assign,

@@ -164,6 +164,62 @@ def test_int8_screen(gpu, n, k, kind, metric, d):
         assert set(got.tolist()) == set(np.nonzero(acc[q] >= theta[q])[0].tolist()), f"query {q}: survivors"
 
 
+@pytest.mark.parametrize("k, metric, stride, d", [
+    (10, "l2", 16, 128),
+    (64, "ip", 4, 128),
+    (1, "l2", 1, 200),  # rows of 256 bytes
+])
+def test_int8_list_anchors(gpu, k, metric, stride, d):
+    """An index stored in k-means lists and searched without a probe takes its thresholds from the
+    anchors of each query's 8 nearest lists: column 64 t + g of the group table holds the largest
+    <q', x'> + rowc over the anchors i = g, g + 64, ... of the query's t-th list (its stored rows
+    offset + i stride). Checked against the brute force as above: the table, theta as its k-th
+    largest column, no true top-k row below theta, the survivors exactly the rows at or above it."""
+    nq, n = 96, 120_000
+    X, Q, removed = int8_case(n, nq, "uint8", seed=k + stride, d=d)
+    idx = certex.Index(d, metric=metric, n_lists=64, anchor_stride=stride)
+    idx.add(torch.from_numpy(X).cuda())
+    idx.remove(torch.from_numpy(removed))
+    Qg = torch.from_numpy(Q).cuda()
+    get = captured(lambda: idx.search(Qg, k=k, batch=nq, probe_lists=0))
+    B, size, rb = int(get("B")), int(get("size")), int(get("row_bytes"))
+    p = int(get("list_anchors"))
+    assert (B, size, rb, p) == (nq, n, 128 if d <= 128 else 256, 8) and not get("all_rows")
+    codes = get("codes", np.int8, (size, rb)).astype(np.int64)
+    rowc = get("rowc", np.int32).astype(np.int64)
+    qrows = get("qrows", np.int8, (B, rb)).astype(np.int64)
+    live = rowc != DEAD
+    assert (~live).sum() == len(removed)
+    acc = (qrows.astype(np.float64) @ codes.T.astype(np.float64)).astype(np.int64) + rowc[None, :]
+
+    lists = get("lists", np.int32, (B, p)).astype(np.int64)
+    off = get("list_offsets", np.int64)
+    assert off[0] == 0 and off[-1] == size and (np.diff(off) >= 0).all()
+    assert ((lists >= 0) & (lists < 64)).all()
+    assert all(len(set(r)) == p for r in lists.tolist()), "a list twice among a query's nearest"
+    n_anchor = (np.diff(off) + stride - 1) // stride
+    assert (n_anchor[lists] >= 32).all(), "a list of fewer than 32 anchors among the nearest"
+    gmax = get("gmax", np.int32, (B, 64 * p)).astype(np.int64)
+    want = np.full((B, 64 * p), np.iinfo(np.int32).min, np.int64)
+    for q in range(B):
+        for t in range(p):
+            j = lists[q, t]
+            rows = np.arange(off[j], off[j + 1], stride)
+            np.maximum.at(want[q], t * 64 + np.arange(len(rows)) % 64, acc[q, rows])
+    assert np.array_equal(gmax, want), "list anchor group maxima"
+
+    theta = get("theta", np.int32).astype(np.int64)
+    kth_group = -np.sort(-gmax, axis=1)[:, k - 1]
+    assert np.array_equal(theta, np.maximum(kth_group, KEEP_ALL)), "theta is the k-th best group"
+    kth_true = -np.sort(-np.where(live, acc, -(1 << 62)), axis=1)[:, k - 1]
+    assert (theta <= kth_true).all(), "a row of the true top k lies below theta"
+    cap, count, rows = buckets(get, B)
+    for q in range(B):
+        got = rows[q, : count[q]]
+        assert len(np.unique(got)) == len(got), f"query {q}: a survivor twice"
+        assert set(got.tolist()) == set(np.nonzero(acc[q] >= theta[q])[0].tolist()), f"query {q}: survivors"
+
+
 # --- fp16 rows -------------------------------------------------------------------------------
 
 
