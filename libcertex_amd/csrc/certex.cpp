@@ -889,7 +889,7 @@ void table_pass(cuvs::resources const& res, index_state const& st, certex_amd::s
     void* temp   = rs.get(cuvs::detail::ws_probe_dist,
                           certex_amd::list_anchor_temp_bytes(aa.nq, st.n_lists));
     certex_amd::nearest_lists_i8(aa.qcodes, st.row_bytes, aa.nq, st.centers_q.p,
-                                 st.cterm_anchor.as<float>(), Lp, lists, stream);
+                                 st.cterm_anchor.as<float>(), Lp, st.n_lists, lists, temp, stream);
     certex_amd::list_anchor_groups(st.codes.as<int8_t>(), st.rowc.as<int32_t>(), st.row_bytes,
                                    aa.qcodes, aa.nq, lists, st.list_offsets_dev.as<int64_t>(),
                                    st.n_lists, std::max(1, st.anchor_stride), temp,

@@ -572,13 +572,17 @@ void center_distances(const void* rows, bool f16, int64_t n, int row_bytes,
 void nearest_lists(const float* dist, int64_t nq, int n_lists, int ld, int p, int32_t* lists,
                    hipStream_t stream);
 /**
- * lists[q, 0 .. 8) = the 8 nearest lists of int8 query q (codes of 128 or 256 bytes) by
- * cterm[c] - <q', center c>, ascending, ties to the lower list; centers of cterm +inf are never
- * taken (-1 where fewer than 8 are finite). No distance matrix.
+ * lists[q, 0 .. 8) = 8 nearest lists of int8 query q (codes of 128 or 256 bytes) by
+ * cterm[c] - <q', center c>, ascending, ties to the lower list: the best two lists of each of 32
+ * fixed parts of the centers, then the 8 best of those (a list may stand in for a nearer one of
+ * the same part as two nearer still); centers
+ * of cterm +inf are never taken (-1 where fewer than 8 are finite). No distance matrix. Also
+ * counts the queries of every list into temp (list_anchor_temp_bytes), for list_anchor_groups.
  */
 void nearest_lists_i8(const int8_t* qcodes, int row_bytes, int64_t nq, const void* centers_q,
-                      const float* cterm, int n_centers_pad, int32_t* lists, hipStream_t stream);
-/** Bytes of the temporary memory of list_anchor_groups. */
+                      const float* cterm, int n_centers_pad, int n_lists, int32_t* lists,
+                      void* temp, hipStream_t stream);
+/** Bytes of the temporary memory of nearest_lists_i8 and list_anchor_groups. */
 size_t list_anchor_temp_bytes(int64_t nq, int n_lists);
 /**
  * The group table of the list anchors, a threshold source of integer rows of 128 or 256 bytes:
@@ -587,8 +591,8 @@ size_t list_anchor_temp_bytes(int64_t nq, int n_lists);
  * t 64 + i % 64 of the query's row of gmax (512 columns) gets the largest screen value
  * <q', x'> + rowc[x] of its anchors (INT32_MIN for a column without one). Every column holds
  * distinct rows, so the k-th largest column bounds the k-th best screen value from below. The
- * pairs (q, t) are grouped by list in temp (list_anchor_temp_bytes), so that one workgroup copies
- * the anchors of a list into LDS once for all of its queries.
+ * pairs (q, t) are grouped by list in temp (counted there by nearest_lists_i8 on the same lists),
+ * so that one workgroup copies the anchors of a list into LDS once for up to 32 of its queries.
  */
 void list_anchor_groups(const int8_t* codes, const int32_t* rowc, int row_bytes,
                         const int8_t* qcodes, int64_t nq, const int32_t* lists,

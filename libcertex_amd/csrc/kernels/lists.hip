@@ -214,27 +214,29 @@ __global__ __launch_bounds__(256) void top_lists_kernel(const float* dist, int64
  * The 8 nearest lists of 64 queries per workgroup (int8 codes of 64 KS bytes): center distances
  * cterm[c] - <q', center c> on the MFMA (operand A the centers, B the 4 query tiles held in
  * registers, so that a center tile is read once for 64 queries). A lane sees the values (query
- * 16 qt + lane % 16, center 4 (lane / 16) + r) of every W-th center tile and keeps its 2 best per
- * query; the 64 candidates of a query (2 from each of its 4 lanes in each of the 8 waves) meet in
- * LDS, where 8 rounds of a wave argmin pick its 8 (ties to the lower list). Two best per lane keep
- * the 8 nearest unless three of them fall to one lane (the lists choose anchors near the query, so
- * a near list in place of a nearer one changes speed, never results). No distance matrix is
+ * 16 qt + lane % 16, center 4 (lane / 16) + r) of every W-th center tile, a fixed 32nd of the
+ * centers, and keeps the best two of them; the 64 candidates of a query (two from each of its 4
+ * lanes in each of the 8 waves) meet in LDS (candidate-major, so that the queries' threads read
+ * consecutive words), where one thread per query keeps its 8 best (ties to the lower list) and
+ * counts the query into counts[list] (the pairs per list of list_anchor_groups). These are the 8
+ * nearest lists unless three of them share a 32nd (the lists choose anchors near the query, so a
+ * near list in place of a nearer one changes speed, never results; keeping one list per 32nd
+ * measured 4% more survivors at config 2, with a tail past the small re-rank's buckets). No distance matrix is
  * written. Centers of cterm +inf (padding, lists left out) are never picked.
  */
 template <int KS>
 __global__ __launch_bounds__(512) void nearest_lists_i8_kernel(const int8_t* qcodes, int64_t nq,
                                                                const int8_t* centers,
                                                                const float* cterm, int n_centers,
-                                                               int32_t* lists)
+                                                               int32_t* lists, int32_t* counts)
 {
   constexpr int ROWB = 64 * KS;
   constexpr int P    = kMaxProbe;
   constexpr int W    = 8;           // waves: each takes every W-th center tile
   constexpr int QT   = 4;           // query tiles of the workgroup
-  constexpr int NC   = 4 * W * 2;   // candidates of a query
-  static_assert(NC == 64, "one candidate per lane");
-  __shared__ float cv[16 * QT][NC];
-  __shared__ int ci[16 * QT][NC];
+  constexpr int NC   = 4 * W * 2;   // candidates of a query: two per lane group
+  __shared__ float cv[NC][16 * QT];
+  __shared__ int ci[NC][16 * QT];
   const int lane   = threadIdx.x & 63;
   const int wave   = threadIdx.x >> 6;
   const int64_t q0 = int64_t(blockIdx.x) * 16 * QT;
@@ -257,7 +259,7 @@ __global__ __launch_bounds__(512) void nearest_lists_i8_kernel(const int8_t* qco
     b0[qt] = b1[qt] = INFINITY;
     i0[qt] = i1[qt] = INT32_MAX;
   }
-  constexpr int U = 2;  // tiles whose loads are in flight together
+  constexpr int U = 4;  // tiles whose loads are in flight together
   for (int ct0 = wave * 16; ct0 < n_centers; ct0 += 16 * W * U) {
     v4i a[U][KS];
     v4f ch[U];
@@ -297,47 +299,42 @@ __global__ __launch_bounds__(512) void nearest_lists_i8_kernel(const int8_t* qco
   const int grp = wave * 4 + (lane >> 4);
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    const int ql         = 16 * qt + (lane & 15);
-    cv[ql][2 * grp]      = b0[qt];
-    ci[ql][2 * grp]      = i0[qt];
-    cv[ql][2 * grp + 1]  = b1[qt];
-    ci[ql][2 * grp + 1]  = i1[qt];
+    const int ql        = 16 * qt + (lane & 15);
+    cv[2 * grp][ql]     = b0[qt];
+    ci[2 * grp][ql]     = i0[qt];
+    cv[2 * grp + 1][ql] = b1[qt];
+    ci[2 * grp + 1][ql] = i1[qt];
   }
   __syncthreads();
-  // wave w picks for queries 8 w .. 8 w + 7, one candidate per lane
-  for (int qq = 0; qq < 16 * QT / W; ++qq) {
-    const int ql    = wave * (16 * QT / W) + qq;
-    const int64_t q = q0 + ql;
-    if (q >= nq) { break; }
-    float cvl = cv[ql][lane];
-    int cil   = ci[ql][lane];
-    for (int r = 0; r < P; ++r) {
-      float v = cvl;
-      int i   = cil;
-      for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(v, off);
-        const int oi   = __shfl_xor(i, off);
-        if (ov < v || (ov == v && oi < i)) {
-          v = ov;
-          i = oi;
-        }
-      }
-      if (lane == 0) { lists[q * P + r] = i < n_centers && v < INFINITY ? i : -1; }
-      if (cil == i) {  // the owner pops the winner (a list is one lane's candidate)
-        cvl = INFINITY;
-        cil = INT32_MAX;
-      }
-    }
+  const int ql    = threadIdx.x;
+  const int64_t q = q0 + ql;
+  if (ql >= 16 * QT || q >= nq) { return; }
+  float bv[P];
+  int bi[P];
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    bv[r] = INFINITY;
+    bi[r] = INT32_MAX;
   }
-}
-
-/** counts[j] = the (query, slot) pairs of lists[0, n) that name list j (-1: none). */
-__global__ void list_pair_count_kernel(const int32_t* lists, int64_t n, int32_t* counts)
-{
-  for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < n;
-       e += int64_t(gridDim.x) * blockDim.x) {
-    const int32_t j = lists[e];
-    if (j >= 0) { atomicAdd(counts + j, 1); }
+  for (int c = 0; c < NC; ++c) {
+    const float v = cv[c][ql];
+    const int i   = ci[c][ql];
+    // insertion by (value, list): the candidates do not arrive in list order
+    if (!(v < bv[P - 1] || (v == bv[P - 1] && i < bi[P - 1]))) { continue; }
+    int at = P - 1;
+    while (at > 0 && (v < bv[at - 1] || (v == bv[at - 1] && i < bi[at - 1]))) {
+      bv[at] = bv[at - 1];
+      bi[at] = bi[at - 1];
+      --at;
+    }
+    bv[at] = v;
+    bi[at] = i;
+  }
+#pragma unroll
+  for (int r = 0; r < P; ++r) {
+    const int i = bi[r] < n_centers && bv[r] < INFINITY ? bi[r] : -1;
+    lists[q * P + r] = i;
+    if (i >= 0) { atomicAdd(counts + i, 1); }
   }
 }
 
@@ -347,12 +344,13 @@ constexpr int kSlicePairs = 32;
 /**
  * start[j] = the exclusive prefix sum of counts[0, L) (start[L] = the total), cursor = start, and
  * slice[j] = the exclusive prefix sum of ceil(counts[j] / kSlicePairs) (slice[L] = the total): the
- * first workgroup of list j in list_anchor_groups_kernel. One workgroup of 1,024 threads, each over
- * a run of consecutive lists.
+ * first workgroup of list j in list_anchor_groups_kernel, and slices[b] = {list, first pair, end
+ * pair, 0} of its workgroup b. One workgroup of 1,024 threads, each over a run of consecutive
+ * lists.
  */
 __global__ __launch_bounds__(1024) void list_pair_scan_kernel(const int32_t* counts, int L,
                                                               int32_t* start, int32_t* cursor,
-                                                              int32_t* slice)
+                                                              int32_t* slice, int4* slices)
 {
   __shared__ int part[1024], spart[1024];
   const int t   = threadIdx.x;
@@ -377,11 +375,17 @@ __global__ __launch_bounds__(1024) void list_pair_scan_kernel(const int32_t* cou
   }
   int run = part[t] - sum, srun = spart[t] - ssum;
   for (int j = b; j < e; ++j) {
-    start[j]  = run;
-    cursor[j] = run;
-    slice[j]  = srun;
+    start[j]     = run;
+    cursor[j]    = run;
+    slice[j]     = srun;
+    const int ns = (counts[j] + kSlicePairs - 1) / kSlicePairs;
+    for (int x = 0; x < ns; ++x) {
+      const int b0     = run + kSlicePairs * x;
+      const int b1     = b0 + kSlicePairs < run + counts[j] ? b0 + kSlicePairs : run + counts[j];
+      slices[srun + x] = int4{j, b0, b1, 0};
+    }
     run += counts[j];
-    srun += (counts[j] + kSlicePairs - 1) / kSlicePairs;
+    srun += ns;
   }
   if (t == 1023) {
     start[L] = part[t];
@@ -411,10 +415,10 @@ __global__ void list_pair_fill_kernel(const int32_t* lists, int64_t n, int p, in
  * Group table of the list anchors (int8 rows of ROWB = 128 or 256 bytes). Workgroup b serves list j
  * (slice[j] <= b < slice[j + 1]) and its pairs (query q, slot t) [start[j] + kSlicePairs s, + 32),
  * s = b - slice[j]. The anchors of j, its stored rows offsets[j] + i stride (i < ceil(rows of j /
- * stride)), go into LDS in chunks of AC, with the slice's queries; anchor i joins group i % 64 of
- * the pair's 64 columns gmax[q, 64 t, +64), so the groups hold distinct rows. The scores run on the
- * int8 MFMA: operand A 16 anchors (from LDS; chunk c of anchor u in slot c ^ (u % 8) of its row),
- * B 16 pairs' queries (registers), C the anchors' row terms, so lane l gets anchor 16 T +
+ * stride)), go into LDS in chunks of AC; anchor i joins group i % 64 of the pair's 64 columns
+ * gmax[q, 64 t, +64), so the groups hold distinct rows. The scores run on the int8 MFMA: operand A
+ * 16 anchors (from LDS; chunk c of anchor u in slot c ^ (u % 8) of its row), B 16 pairs' queries
+ * (registers, straight from the query codes), C the anchors' row terms, so lane l gets anchor 16 T +
  * 4 (l / 16) + r of pair l % 16, in group 16 (T % 4) + 4 (l / 16) + r. Wave w takes the pairs'
  * tile w % 2 and the anchor tiles T = w / 2, w / 2 + 2, ...: the two waves of a pair tile keep
  * disjoint groups (T % 4 even or odd), 8 maxima per lane. A later chunk of a long list merges into
@@ -423,30 +427,23 @@ __global__ void list_pair_fill_kernel(const int32_t* lists, int64_t n, int p, in
 template <int ROWB>
 __global__ __launch_bounds__(256) void list_anchor_groups_kernel(
   const int8_t* codes, const int32_t* rowc, const int8_t* qcodes, int p, const int64_t* offsets,
-  int n_lists, int64_t stride, const int32_t* start, const int32_t* slice, const int32_t* pairs,
+  int n_lists, int64_t stride, const int32_t* slice, const int4* slices, const int32_t* pairs,
   int32_t* gmax)
 {
   constexpr int KS  = ROWB / 64;      // 64-byte k-slices of a row
   constexpr int NCH = ROWB / 16;      // 16-byte chunks of a row
-  constexpr int AC  = 32768 / ROWB;   // anchors per LDS chunk (a multiple of 64)
+  // anchors per LDS chunk, a multiple of 64: 24 KB of 128-byte rows (a list of 10M rows in 4,096
+  // lists holds about 150 anchors at stride 16), 32 KB of 256-byte rows
+  constexpr int AC  = ROWB == 128 ? 192 : 128;
   static_assert(kSlicePairs == 32, "two pair tiles per workgroup");
   __shared__ v4i la[AC * NCH];
-  __shared__ v4i lq[kSlicePairs * NCH];
   __shared__ __attribute__((aligned(16))) int32_t lc[AC];
   const int b = blockIdx.x;
   if (b >= slice[n_lists]) { return; }
-  int lo = 0, hi = n_lists - 1;  // the last list whose first workgroup is <= b
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) / 2;
-    if (slice[mid] <= b) {
-      lo = mid;
-    } else {
-      hi = mid - 1;
-    }
-  }
-  const int j    = lo;
-  const int b0   = start[j] + kSlicePairs * (b - slice[j]);
-  const int b1   = b0 + kSlicePairs < start[j + 1] ? b0 + kSlicePairs : start[j + 1];
+  const int4 sl  = slices[b];
+  const int j    = sl.x;
+  const int b0   = sl.y;
+  const int b1   = sl.z;
   const int tid  = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -455,12 +452,15 @@ __global__ __launch_bounds__(256) void list_anchor_groups_kernel(
   const int64_t r0 = offsets[j];
   const int64_t na = (offsets[j + 1] - r0 + stride - 1) / stride;
   const int64_t ng = 64 * int64_t(p);
-  for (int u = tid; u < (b1 - b0) * NCH; u += 256) {
-    const int e = pairs[b0 + u / NCH];
-    lq[u]       = *reinterpret_cast<const v4i*>(qcodes + int64_t(e / p) * ROWB + 16 * (u % NCH));
-  }
   const int pl   = 16 * pt + (lane & 15);  // the lane's pair in the slice
   const bool own = b0 + pl < b1;
+  // the pair's query fragments (operand B), loaded while the anchors are copied
+  const int e0    = pairs[own ? b0 + pl : b0];
+  v4i qv[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    qv[ks] = *reinterpret_cast<const v4i*>(qcodes + int64_t(e0 / p) * ROWB + 64 * ks + 16 * (lane >> 4));
+  }
   for (int64_t a0 = 0; a0 < na; a0 += AC) {
     const int nc = int(na - a0 < AC ? na - a0 : AC);
     if (a0 > 0) { __syncthreads(); }  // the previous chunk's reads are done
@@ -473,9 +473,6 @@ __global__ __launch_bounds__(256) void list_anchor_groups_kernel(
     for (int i = tid; i < nc; i += 256) { lc[i] = rowc[r0 + (a0 + i) * stride]; }
     __syncthreads();
     if (b0 + 16 * pt >= b1) { continue; }  // no pair in this wave's tile
-    v4i qv[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) { qv[ks] = lq[(own ? pl : 0) * NCH + 4 * ks + (lane >> 4)]; }
     int32_t run[2][4];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -499,8 +496,7 @@ __global__ __launch_bounds__(256) void list_anchor_groups_kernel(
       }
     }
     if (own) {
-      const int e  = pairs[b0 + pl];
-      int32_t* row = gmax + int64_t(e / p) * ng + (e % p) * 64;
+      int32_t* row = gmax + int64_t(e0 / p) * ng + (e0 % p) * 64;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -641,15 +637,20 @@ void nearest_lists(const float* dist, int64_t nq, int n_lists, int ld, int p, in
 }
 
 void nearest_lists_i8(const int8_t* qcodes, int row_bytes, int64_t nq, const void* centers_q,
-                      const float* cterm, int n_centers_pad, int32_t* lists, hipStream_t stream)
+                      const float* cterm, int n_centers_pad, int n_lists, int32_t* lists,
+                      void* temp, hipStream_t stream)
 {
   if (nq == 0) { return; }
+  auto* counts = static_cast<int32_t*>(temp);  // the pairs per list (list_anchor_groups' temp)
+  fill_u32(reinterpret_cast<uint32_t*>(counts), n_lists, 0, stream);
   const unsigned grid = unsigned((nq + 63) / 64);
   const auto* c       = static_cast<const int8_t*>(centers_q);
   if (row_bytes == 128) {
-    nearest_lists_i8_kernel<2><<<grid, 512, 0, stream>>>(qcodes, nq, c, cterm, n_centers_pad, lists);
+    nearest_lists_i8_kernel<2><<<grid, 512, 0, stream>>>(qcodes, nq, c, cterm, n_centers_pad,
+                                                         lists, counts);
   } else if (row_bytes == 256) {
-    nearest_lists_i8_kernel<4><<<grid, 512, 0, stream>>>(qcodes, nq, c, cterm, n_centers_pad, lists);
+    nearest_lists_i8_kernel<4><<<grid, 512, 0, stream>>>(qcodes, nq, c, cterm, n_centers_pad,
+                                                         lists, counts);
   } else {
     throw std::logic_error("certex: the nearest lists of int8 queries take rows of 128 or 256 bytes");
   }
@@ -657,7 +658,9 @@ void nearest_lists_i8(const int8_t* qcodes, int row_bytes, int64_t nq, const voi
 
 size_t list_anchor_temp_bytes(int64_t nq, int n_lists)
 {
-  return size_t(4 * (int64_t(n_lists) + 1) + nq * kMaxProbe) * 4;
+  const int64_t n = nq * kMaxProbe;
+  return size_t(4 * (int64_t(n_lists) + 1) + (n + 3) / 4 * 4) * 4 +
+         size_t(n_lists + (n + kSlicePairs - 1) / kSlicePairs) * sizeof(int4);
 }
 
 void list_anchor_groups(const int8_t* codes, const int32_t* rowc, int row_bytes,
@@ -675,20 +678,21 @@ void list_anchor_groups(const int8_t* codes, const int32_t* rowc, int row_bytes,
   auto* start     = counts + (n_lists + 1);
   auto* cursor    = start + (n_lists + 1);
   auto* slice     = cursor + (n_lists + 1);
-  auto* pairs     = slice + (n_lists + 1);
-  fill_u32(reinterpret_cast<uint32_t*>(counts), n_lists, 0, stream);
+  auto* pairs      = slice + (n_lists + 1);
+  auto* slices     = reinterpret_cast<int4*>(pairs + (n + 3) / 4 * 4);
   const unsigned g = unsigned(std::min<int64_t>((n + 255) / 256, 1024));
-  list_pair_count_kernel<<<g, 256, 0, stream>>>(lists, n, counts);
-  list_pair_scan_kernel<<<1, 1024, 0, stream>>>(counts, n_lists, start, cursor, slice);
+  list_pair_scan_kernel<<<1, 1024, 0, stream>>>(counts, n_lists, start, cursor, slice, slices);
   list_pair_fill_kernel<<<g, 256, 0, stream>>>(lists, n, kMaxProbe, cursor, pairs, gmax);
   // at most one partial slice per list: n_lists + n / kSlicePairs workgroups cover every slice
   const unsigned wg = unsigned(n_lists + (n + kSlicePairs - 1) / kSlicePairs);
   if (row_bytes == 128) {
     list_anchor_groups_kernel<128><<<wg, 256, 0, stream>>>(codes, rowc, qcodes, kMaxProbe, offsets,
-                                                           n_lists, stride, start, slice, pairs, gmax);
+                                                           n_lists, stride, slice, slices,
+                                                           pairs, gmax);
   } else {
     list_anchor_groups_kernel<256><<<wg, 256, 0, stream>>>(codes, rowc, qcodes, kMaxProbe, offsets,
-                                                           n_lists, stride, start, slice, pairs, gmax);
+                                                           n_lists, stride, slice, slices,
+                                                           pairs, gmax);
   }
 }
 
