@@ -360,6 +360,9 @@ struct route_plan {
   // columns: the routed anchor pass then writes every column of the batch's table rows itself
   bool covers_table = false;
   anchor_plan ap{};
+  // query i of the batch (in label order) is the caller's query rows[i], and its results go to the
+  // caller's row rows[i] (null: the batch is in the caller's order)
+  const int32_t* rows = nullptr;
 };
 
 constexpr int kScreenChunk = 128;      // most steps per screen workgroup
@@ -957,8 +960,9 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
   auto* qpaired   = wide ? static_cast<int8_t*>(rs.get(cuvs::detail::ws_qpaired,
                                                        size_t(nq_pad) * st.row_bytes))
                          : nullptr;
+  const int32_t* qmap = route != nullptr ? route->rows : nullptr;
   certex_amd::encode_queries_i8(static_cast<const uint8_t*>(queries), B, nq_pad, st.dim,
-                                st.row_bytes, flip, qcodes, stream, qpaired);
+                                st.row_bytes, flip, qcodes, stream, qpaired, qmap);
 
   // group table: the best screen value of every group of anchors (every anchor_stride-th stored
   // row) and of the probed lists' rows; the k-th best group is the threshold of the query
@@ -1039,6 +1043,7 @@ void search_batch_int(cuvs::resources const& res, index_state const& st, const v
   }
   va.distances = distances;
   va.neighbors = neighbors;
+  va.out_rows  = qmap;
   timed(3, stream, [&] { certex_amd::verify_topk_i8(va, stream); });
 }
 
@@ -1066,9 +1071,10 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   auto* qpaired = wide ? static_cast<uint16_t*>(rs.get(cuvs::detail::ws_qpaired,
                                                        size_t(nq_pad) * st.row_bytes))
                        : nullptr;
+  const int32_t* qmap = route != nullptr ? route->rows : nullptr;
   certex_amd::encode_queries_f16(queries, t, B, nq_pad, st.dim, st.halves, st.normalize,
                                  st.center.as<double>(), 1.0 / st.alpha, qrows, qscal, stream,
-                                 qpaired);
+                                 qpaired, qmap);
 
   const table_plan tp = plan_table(res, st, qrows, B, nq_pad, k, params, fa, route);
   certex_amd::screen_args sa{};
@@ -1131,6 +1137,7 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   va.gamma      = st.gamma;
   va.rowc       = st.rowc.as<float>();
   va.queries    = queries;
+  va.query_rows = qmap;
   va.t          = t;
   va.dim        = st.dim;
   va.metric     = st.metric;
@@ -1139,6 +1146,7 @@ void search_batch_float(cuvs::resources const& res, index_state const& st, const
   va.k          = k;
   va.distances  = distances;
   va.neighbors  = neighbors;
+  va.out_rows   = qmap;
   va.scored     = scored;
   if (route != nullptr) {
     va.part_ids = st.label_part.ids.as<int32_t>();
@@ -1225,7 +1233,7 @@ using batch_fn = void (*)(cuvs::resources const&, index_state const&, const void
  * group exiting at once.
  */
 void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn batch,
-                  const char* queries, size_t qrow, int64_t B, int k, const int32_t* qlabels,
+                  const char* queries, int64_t B, int k, const int32_t* qlabels,
                   const int32_t* hlabels, int64_t* neighbors, float* distances,
                   certex_amd::filter_args fa, search_params const& params)
 {
@@ -1436,19 +1444,10 @@ void routed_batch(cuvs::resources const& res, index_state const& st, batch_fn ba
   }
 
   fa.query_labels = d_sorted;  // the label filter of the tail, in the sorted order
-  if (in_order) {
-    // host labels already in label order (a KeyCache's heads): the sorted batch is the batch
-    batch(res, st, queries, B, k, 0, neighbors, distances, fa, params, &route);
-    return;
-  }
-  auto* q_sorted = rs.get(cuvs::detail::ws_route_q, size_t(B) * qrow);
-  certex_amd::gather_rows(queries, d_order, B, int64_t(qrow), q_sorted, stream);
-  auto* out   = static_cast<char*>(rs.get(cuvs::detail::ws_route_out, size_t(B) * k * 12));
-  auto* nb_s  = reinterpret_cast<int64_t*>(out);
-  auto* ds_s  = reinterpret_cast<float*>(out + size_t(B) * k * 8);
-  batch(res, st, q_sorted, B, k, 0, nb_s, ds_s, fa, params, &route);
-  certex_amd::scatter_rows(nb_s, d_order, B, int64_t(k) * 8, neighbors, stream);
-  certex_amd::scatter_rows(ds_s, d_order, B, int64_t(k) * 4, distances, stream);
+  // the batch in label order reads the caller's queries through d_order and writes the results
+  // to their rows (host labels already in label order, a KeyCache's heads: the batch itself)
+  route.rows = in_order ? nullptr : d_order;
+  batch(res, st, queries, B, k, 0, neighbors, distances, fa, params, &route);
   // no wait here: the next use of the staging waits for this batch's copy of the tables
 }
 
@@ -1485,7 +1484,7 @@ void search_impl(cuvs::resources const& res, search_params const& params, index<
     try {
       const char* q = reinterpret_cast<const char*>(queries.data) + size_t(b0) * qrow;
       if (route) {
-        routed_batch(res, st, batch, q, qrow, B, int(k),
+        routed_batch(res, st, batch, q, B, int(k),
                      host_labels != nullptr ? nullptr : fa.query_labels + b0,
                      host_labels != nullptr ? host_labels + b0 : nullptr, neighbors + b0 * k,
                      distances + b0 * k, fa, params);

@@ -103,8 +103,6 @@ enum ws_slot : int {
   ws_qscal,
   ws_vals,
   ws_route,       // label routing of a batch: order, sorted labels, group tables
-  ws_route_q,     // the batch's queries in label order
-  ws_route_out,   // results in label order before they return to query order
   ws_probe_dist,  // list probe: center distances of the batch's queries
   ws_probe,       // list probe: nearest lists, pair tables
   ws_probe_rows,  // list probe: the query row of every (query, list) pair

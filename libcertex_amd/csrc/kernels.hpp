@@ -96,10 +96,12 @@ __host__ __device__ inline int int_row_bytes(int64_t dim)
 void encode_rows_i8(const uint8_t* x, int64_t n, int64_t dim, int row_bytes, uint8_t flip,
                     metric_kind metric, int8_t* codes, int32_t* rowc, hipStream_t stream);
 
-/** qcodes[i] = q[i] ^ flip, zero padded, for i < nq; padding queries [nq, nq_pad) are zero; the
- *  same codes again in the paired layout into qpaired unless null (the tiled screen's queries). */
+/** qcodes[i] = q[rows[i]] ^ flip (q[i] when rows is null), zero padded, for i < nq; padding
+ *  queries [nq, nq_pad) are zero; the same codes again in the paired layout into qpaired unless
+ *  null (the tiled screen's queries). */
 void encode_queries_i8(const uint8_t* q, int64_t nq, int64_t nq_pad, int64_t dim, int row_bytes,
-                       uint8_t flip, int8_t* qcodes, hipStream_t stream, int8_t* qpaired = nullptr);
+                       uint8_t flip, int8_t* qcodes, hipStream_t stream, int8_t* qpaired = nullptr,
+                       const int32_t* rows = nullptr);
 
 /**
  * Tombstones of ids and where their rows are stored: with lists the ids below n_listed live in
@@ -348,9 +350,11 @@ struct verify_args {
   const int8_t* part_codes = nullptr;
   bool part_paired         = false;  // part_codes in the paired layout (rows of more than 256 bytes)
   // the results as the caller receives them, in (score, id) order: distances [nq, k] in the
-  // metric's form (+inf, -inf for the inner product, where missing), ids [nq, k] (-1 where missing)
+  // metric's form (+inf, -inf for the inner product, where missing), ids [nq, k] (-1 where missing);
+  // query q's row of both is out_rows[q] (a routed batch in label order), or q when out_rows is null
   float* distances;
   int64_t* neighbors;
+  const int32_t* out_rows = nullptr;
 };
 
 /** fp64 exact scores of the candidates of every query and their k best by (score, row). */
@@ -400,13 +404,14 @@ void encode_rows_f16(const void* x, elem t, int64_t n, int64_t dim, int halves, 
                      uint16_t* rows, float* rowc, double* maxima, hipStream_t stream);
 
 /**
- * Query rows the same way; qscal[3 i + 0..2] = |W|^2, |fp16(W)| and |W - fp16(W)| (upper bounds,
- * |W|^2 a lower bound) for i < nq; padding queries are zero.
+ * Query rows the same way (row i from the caller's row rows[i], or i when rows is null);
+ * qscal[3 i + 0..2] = |W|^2, |fp16(W)| and |W - fp16(W)| (upper bounds, |W|^2 a lower bound) for
+ * i < nq; padding queries are zero.
  */
 void encode_queries_f16(const void* q, elem t, int64_t nq, int64_t nq_pad, int64_t dim,
                         int halves, bool normalize, const double* center, double inv_alpha,
                         uint16_t* qrows, double* qscal, hipStream_t stream,
-                        uint16_t* qpaired = nullptr);
+                        uint16_t* qpaired = nullptr, const int32_t* rows = nullptr);
 
 /** Float tombstones (row term -inf) of ids, as remove_rows_i8. */
 void remove_rows_f16(const int64_t* ids, int64_t n, int64_t size, float* rowc,
@@ -453,7 +458,8 @@ struct verify_f_args {
   int64_t n_rows;
   const void* vectors;  // original vectors [*, dim]
   const float* rowc;    // liveness (-inf) for all_rows
-  const void* queries;  // original queries of the batch
+  const void* queries;  // original queries: query q of the batch is row query_rows[q] (or q)
+  const int32_t* query_rows = nullptr;
   elem t;
   int64_t dim;
   metric_kind metric;
@@ -470,6 +476,7 @@ struct verify_f_args {
   int64_t n_part          = 0;
   float* distances;    // as in verify_args
   int64_t* neighbors;
+  const int32_t* out_rows = nullptr;  // as in verify_args
 };
 /**
  * fp64 exact scores (the canonical order of the oracle) and top-k by (score, row); with screen
@@ -532,9 +539,6 @@ void gather_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_byt
 /** The same into the paired layout of dst (row_bytes a multiple of 128, paired_bytes(n) bytes). */
 void gather_rows_paired(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes,
                         void* dst, hipStream_t stream);
-/** dst row ids[i] = src row i. */
-void scatter_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes, void* dst,
-                  hipStream_t stream);
 /** pos[ids[i]] = i. */
 void invert_ids(const int32_t* ids, int64_t n, int32_t* pos, hipStream_t stream);
 

@@ -86,13 +86,15 @@ __global__ void encode_rows_wide_kernel(const uint8_t* x, int64_t n, int64_t dim
   if (lane == 0) { rowc[r] = metric == metric_kind::l2 ? -(norm >> 1) : (flip ? 128 * sum : 0); }
 }
 
-__global__ void encode_queries_kernel(const uint8_t* q, int64_t nq, int64_t nq_pad, int64_t dim,
-                                      int row_bytes, uint8_t flip, int8_t* qcodes, int8_t* qpaired)
+__global__ void encode_queries_kernel(const uint8_t* q, const int32_t* rows, int64_t nq,
+                                      int64_t nq_pad, int64_t dim, int row_bytes, uint8_t flip,
+                                      int8_t* qcodes, int8_t* qpaired)
 {
   const int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
   if (t >= nq_pad * row_bytes) { return; }
   const int64_t i = t / row_bytes, j = t % row_bytes;
-  const int8_t c  = (i < nq && j < dim) ? int8_t(q[i * dim + j] ^ flip) : int8_t(0);
+  const int64_t r = i < nq && rows != nullptr ? int64_t(rows[i]) : i;  // the caller's query row
+  const int8_t c  = (i < nq && j < dim) ? int8_t(q[r * dim + j] ^ flip) : int8_t(0);
   qcodes[t]       = c;
   if (qpaired != nullptr) { qpaired[paired_offset(i, j, row_bytes)] = c; }
 }
@@ -389,7 +391,8 @@ __global__ __launch_bounds__(256) void encode_rows_f16_kernel(const void* x, ele
  * (raised for the rounding of their sums, sqrt_up). Per-lane fp64 partial sums and a butterfly:
  * the sums only enter bounds that carry these slacks.
  */
-__global__ __launch_bounds__(256) void encode_queries_f16_kernel(const void* q, elem t, int64_t nq,
+__global__ __launch_bounds__(256) void encode_queries_f16_kernel(const void* q, const int32_t* rows,
+                                                                 elem t, int64_t nq,
                                                                  int64_t nq_pad, int64_t dim,
                                                                  int halves, bool normalize,
                                                                  const double* center,
@@ -413,11 +416,12 @@ __global__ __launch_bounds__(256) void encode_queries_f16_kernel(const void* q, 
     return;
   }
   // a query of at most 64 kLaneChunk coordinates is loaded once, for its norm and its encoding
+  const int64_t r      = rows != nullptr ? int64_t(rows[i]) : i;  // the caller's query row
   const bool one_chunk = dim <= 64 * kLaneChunk;
   double v[kLaneChunk], c[kLaneChunk];
   double nrm = 1.0;
   if (one_chunk) {
-    lane_coords(q, t, i, dim, 0, lane, v);
+    lane_coords(q, t, r, dim, 0, lane, v);
     lane_center(center, dim, 0, lane, c);
     if (normalize) {
       double s2 = 0;
@@ -427,12 +431,12 @@ __global__ __launch_bounds__(256) void encode_queries_f16_kernel(const void* q, 
       nrm = s2 > 0 ? sqrt(s2) : 1.0;
     }
   } else if (normalize) {
-    nrm = wave_row_norm(q, t, i, dim, lane);
+    nrm = wave_row_norm(q, t, r, dim, lane);
   }
   double a = 0, nw = 0, ew = 0;
   for (int64_t j0 = 0; j0 < dim; j0 += 64 * kLaneChunk) {
     if (!one_chunk) {
-      lane_coords(q, t, i, dim, j0, lane, v);
+      lane_coords(q, t, r, dim, j0, lane, v);
       lane_center(center, dim, j0, lane, c);
     }
 #pragma unroll
@@ -508,12 +512,13 @@ void encode_rows_f16(const void* x, elem t, int64_t n, int64_t dim, int halves, 
 
 void encode_queries_f16(const void* q, elem t, int64_t nq, int64_t nq_pad, int64_t dim,
                         int halves, bool normalize, const double* center, double inv_alpha,
-                        uint16_t* qrows, double* qscal, hipStream_t stream, uint16_t* qpaired)
+                        uint16_t* qrows, double* qscal, hipStream_t stream, uint16_t* qpaired,
+                        const int32_t* rows)
 {
   if (nq_pad == 0) { return; }
   // one wave per query, four per block
   encode_queries_f16_kernel<<<unsigned((nq_pad + 3) / 4), 256, 0, stream>>>(
-    q, t, nq, nq_pad, dim, halves, normalize, center, inv_alpha, qrows, qscal, qpaired);
+    q, rows, t, nq, nq_pad, dim, halves, normalize, center, inv_alpha, qrows, qscal, qpaired);
 }
 
 void remove_rows_f16(const int64_t* ids, int64_t n, int64_t size, float* rowc,
@@ -537,12 +542,13 @@ void encode_rows_i8(const uint8_t* x, int64_t n, int64_t dim, int row_bytes, uin
 }
 
 void encode_queries_i8(const uint8_t* q, int64_t nq, int64_t nq_pad, int64_t dim, int row_bytes,
-                       uint8_t flip, int8_t* qcodes, hipStream_t stream, int8_t* qpaired)
+                       uint8_t flip, int8_t* qcodes, hipStream_t stream, int8_t* qpaired,
+                       const int32_t* rows)
 {
   const int64_t n = nq_pad * row_bytes;
   if (n == 0) { return; }
-  encode_queries_kernel<<<blocks_for(n), 256, 0, stream>>>(q, nq, nq_pad, dim, row_bytes, flip,
-                                                           qcodes, qpaired);
+  encode_queries_kernel<<<blocks_for(n), 256, 0, stream>>>(q, rows, nq, nq_pad, dim, row_bytes,
+                                                           flip, qcodes, qpaired);
 }
 
 void remove_rows_i8(const int64_t* ids, int64_t n, int64_t size, int32_t* rowc,

@@ -139,8 +139,8 @@ __global__ __launch_bounds__(kRouteThreads) void route_tables_kernel(route_table
  * buckets at most: labels below 0, each label of the partition, labels past it): a stable
  * counting sort of the batch by label into order / sorted, then the group tables of
  * route_tables_kernel, their queries read off the bucket counts. Chunks of 64 queries go to the
- * waves in turn; per chunk, one ballot per bucket gives the bucket's count and each query's rank
- * within the chunk. Replaces the radix sort (an index fill and five launches) and the separate
+ * waves in turn; per chunk, seven ballots (one per bit of the bucket index) give every query the
+ * lanes of its bucket, hence its rank within the chunk and the bucket's count. Replaces the radix sort (an index fill and five launches) and the separate
  * group-table launch. Labels below 0 and past the partition keep their relative order but not
  * their order by value: the groups only ask where each partition label starts and ends.
  */
@@ -162,17 +162,44 @@ __global__ __launch_bounds__(kRouteThreads) void route_small_kernel(route_table_
   const int64_t B    = a.B;
   const int nb       = int(a.n_labels) + 2;
   const int n_chunks = int((B + 63) / 64);
-  auto bucket_of     = [&](int64_t i) {
-    const int32_t l = labels[i];
-    return l < 0 ? 0 : (l < a.n_labels ? l + 1 : nb - 1);
+  auto bucket_of     = [&](int32_t l) { return l < 0 ? 0 : (l < a.n_labels ? l + 1 : nb - 1); };
+  // the labels of 4 chunks of a wave at a time, their loads in flight together (past B: none)
+  constexpr int CB = 4;
+  auto labels4     = [&](int c0, int32_t (&lb)[CB], bool (&in)[CB]) {
+#pragma unroll
+    for (int u = 0; u < CB; ++u) {
+      const int64_t i = int64_t(c0 + u * W) * 64 + lane;
+      in[u]           = i < B;
+      lb[u]           = in[u] ? labels[i] : 0;
+    }
   };
-  // counts per (chunk, bucket)
-  for (int c = wave; c < n_chunks; c += W) {
-    const int64_t i = int64_t(c) * 64 + lane;
-    const int b     = i < B ? bucket_of(i) : -1;
-    for (int v = 0; v < nb; ++v) {
-      const uint64_t m = __ballot(b == v);
-      if (lane == 0) { cnt[c * nb + v] = __builtin_popcountll(m); }
+  // the lanes of the wave whose bucket equals this lane's (7 bits: -1, past B, sets bit 6, which no
+  // bucket below 64 has); one ballot per bit instead of one per bucket
+  auto same_bucket = [&](int b) {
+    uint64_t m = ~uint64_t(0);
+#pragma unroll
+    for (int k = 0; k < 7; ++k) {
+      const bool bit     = (b >> k) & 1;
+      const uint64_t bal = __ballot(bit);
+      m &= bit ? bal : ~bal;
+    }
+    return m;
+  };
+  for (int e = tid; e < n_chunks * nb; e += kRouteThreads) { cnt[e] = 0; }
+  __syncthreads();
+  // counts per (chunk, bucket): the lowest lane of each bucket present writes its count
+  for (int c0 = wave; c0 < n_chunks; c0 += CB * W) {
+    int32_t lb[CB];
+    bool in[CB];
+    labels4(c0, lb, in);
+#pragma unroll
+    for (int u = 0; u < CB; ++u) {
+      const int c = c0 + u * W;
+      if (c >= n_chunks) { break; }
+      const int b      = in[u] ? bucket_of(lb[u]) : -1;
+      const uint64_t m = same_bucket(b);
+      const int below  = int(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
+      if (b >= 0 && below == 0) { cnt[c * nb + b] = __builtin_popcountll(m); }
     }
   }
   __syncthreads();
@@ -205,20 +232,23 @@ __global__ __launch_bounds__(kRouteThreads) void route_small_kernel(route_table_
   __syncthreads();
   // the scatter: a query's place is its bucket's start, the bucket's count in earlier chunks and
   // its rank among the chunk's queries of the bucket
-  for (int c = wave; c < n_chunks; c += W) {
-    const int64_t i = int64_t(c) * 64 + lane;
-    const int b     = i < B ? bucket_of(i) : -1;
-    int rank        = 0;
-    for (int v = 0; v < nb; ++v) {
-      const uint64_t m = __ballot(b == v);
-      if (b == v) {
-        rank = int(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
+  for (int c0 = wave; c0 < n_chunks; c0 += CB * W) {
+    int32_t lb[CB];
+    bool in[CB];
+    labels4(c0, lb, in);
+#pragma unroll
+    for (int u = 0; u < CB; ++u) {
+      const int c = c0 + u * W;
+      if (c >= n_chunks) { break; }
+      const int64_t i  = int64_t(c) * 64 + lane;
+      const int b      = in[u] ? bucket_of(lb[u]) : -1;
+      const uint64_t m = same_bucket(b);
+      const int rank   = int(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
+      if (b >= 0) {
+        const int pos = start[b] + cnt[c * nb + b] + rank;
+        order[pos]    = int32_t(i);
+        sorted[pos]   = lb[u];
       }
-    }
-    if (b >= 0) {
-      const int pos = start[b] + cnt[c * nb + b] + rank;
-      order[pos]    = int32_t(i);
-      sorted[pos]   = labels[i];
     }
   }
   // the group tables: label l is bucket l + 1; the workgroup counts' exclusive scan over the labels
@@ -279,30 +309,6 @@ __global__ void gather_bytes_kernel(const uint8_t* src, const int32_t* ids, int6
        t += int64_t(gridDim.x) * blockDim.x) {
     const int64_t i = t / bytes, b = t % bytes;
     dst[t]          = src[int64_t(ids[i]) * bytes + b];
-  }
-}
-
-/** dst row ids[i] = src row i, rows of `units` 16-byte units. */
-__global__ void scatter_units_kernel(const int4* src, const int32_t* ids, int64_t n, int64_t units,
-                                     int4* dst)
-{
-  const int64_t total = n * units;
-  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < total;
-       t += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t i = t / units, u = t % units;
-    dst[int64_t(ids[i]) * units + u] = src[t];
-  }
-}
-
-/** dst row ids[i] = src row i, rows of `bytes` bytes. */
-__global__ void scatter_bytes_kernel(const uint8_t* src, const int32_t* ids, int64_t n,
-                                     int64_t bytes, uint8_t* dst)
-{
-  const int64_t total = n * bytes;
-  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < total;
-       t += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t i = t / bytes, b = t % bytes;
-    dst[int64_t(ids[i]) * bytes + b] = src[t];
   }
 }
 
@@ -442,20 +448,6 @@ void gather_rows_paired(const void* src, const int32_t* ids, int64_t n, int64_t 
   if (row_bytes % 128 != 0) { throw std::logic_error("certex: paired rows are whole 128-byte lines"); }
   gather_paired_kernel<<<blocks_for(n * (row_bytes / 16)), 256, 0, stream>>>(
     static_cast<const int4*>(src), ids, n, row_bytes / 16, static_cast<int4*>(dst));
-}
-
-void scatter_rows(const void* src, const int32_t* ids, int64_t n, int64_t row_bytes, void* dst,
-                  hipStream_t stream)
-{
-  if (n == 0 || row_bytes == 0) { return; }
-  if (row_bytes % 16 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
-      reinterpret_cast<uintptr_t>(dst) % 16 == 0) {
-    scatter_units_kernel<<<blocks_for(n * (row_bytes / 16)), 256, 0, stream>>>(
-      static_cast<const int4*>(src), ids, n, row_bytes / 16, static_cast<int4*>(dst));
-    return;
-  }
-  scatter_bytes_kernel<<<blocks_for(n * row_bytes), 256, 0, stream>>>(
-    static_cast<const uint8_t*>(src), ids, n, row_bytes, static_cast<uint8_t*>(dst));
 }
 
 void invert_ids(const int32_t* ids, int64_t n, int32_t* pos, hipStream_t stream)

@@ -178,8 +178,9 @@ __device__ inline double key_score(uint64_t k)
  * +inf (-inf for the inner product) and -1.
  */
 template <typename A>
-__device__ inline void put_result(const A& a, int64_t t, double s, int64_t id)
+__device__ inline void put_result(const A& a, int64_t q, int j, double s, int64_t id)
 {
+  const int64_t t = (a.out_rows != nullptr ? int64_t(a.out_rows[q]) : q) * a.k + j;
   float d;
   if (id < 0) {
     d = a.metric == metric_kind::inner ? -INFINITY : INFINITY;
@@ -672,7 +673,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_kernel(verify_args a,
   __syncthreads();
   sort_pairs<false>(key, rid, P);
   for (int j = tid; j < k; j += kThreads) {
-    put_result(a, q * k + j, j < have ? key_score(key[j]) : 0.0, j < have ? int64_t(rid[j]) : -1);
+    put_result(a, q, j, j < have ? key_score(key[j]) : 0.0, j < have ? int64_t(rid[j]) : -1);
   }
 }
 
@@ -768,7 +769,7 @@ __global__ __launch_bounds__(kThreads) void verify_topk_i8_small_kernel(verify_a
       my_r = int64_t(br);
     }
   }
-  if (lane < a.k) { put_result(a, q * a.k + lane, my_s, my_r); }
+  if (lane < a.k) { put_result(a, q, lane, my_s, my_r); }
 }
 
 // ---- float vectors ---------------------------------------------------------------------------
@@ -1588,7 +1589,8 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
   const int64_t q = blockIdx.x;
   const int tid   = threadIdx.x;
   const int k     = a.k;
-  for (int64_t j = tid; j < a.dim; j += kThreads) { qv[j] = fcoord(a.queries, a.t, q * a.dim + j); }
+  const int64_t qr = a.query_rows != nullptr ? int64_t(a.query_rows[q]) : q;
+  for (int64_t j = tid; j < a.dim; j += kThreads) { qv[j] = fcoord(a.queries, a.t, qr * a.dim + j); }
 
   const int64_t n_cand =
     a.all_rows ? a.n_rows : (a.cand_count[q] < a.cap ? int64_t(a.cand_count[q]) : a.cap);
@@ -1762,7 +1764,7 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
     have = have < k ? have : k;
   }
   for (int j = tid; j < k; j += kThreads) {
-    put_result(a, q * k + j, j < have ? key_score(key[j]) : 0.0, j < have ? int64_t(rid[j]) : -1);
+    put_result(a, q, j, j < have ? key_score(key[j]) : 0.0, j < have ? int64_t(rid[j]) : -1);
   }
   if (a.scored != nullptr && tid == 0) { atomicAdd(a.scored, (unsigned long long)n_scored); }
 }
