@@ -204,24 +204,25 @@ __device__ inline double wave_sum(double v)
 /** A lane's coordinates of one row loaded together: j = j0 + 64 u + lane, u < kLaneChunk. */
 constexpr int kLaneChunk = 16;
 
-template <typename T>
+template <typename T, int N>
 __device__ inline void lane_coords_t(const T* row, int64_t dim, int64_t j0, int lane,
-                                     double (&v)[kLaneChunk])
+                                     double (&v)[N])
 {
-  T x[kLaneChunk];  // loads from clamped positions, unconditional: all issued before any use
+  T x[N];  // loads from clamped positions, unconditional: all issued before any use
 #pragma unroll
-  for (int u = 0; u < kLaneChunk; ++u) {
+  for (int u = 0; u < N; ++u) {
     const int64_t j = j0 + 64 * u + lane;
     x[u]            = row[j < dim ? j : dim - 1];
   }
 #pragma unroll
-  for (int u = 0; u < kLaneChunk; ++u) { v[u] = j0 + 64 * u + lane < dim ? double(x[u]) : 0.0; }
+  for (int u = 0; u < N; ++u) { v[u] = j0 + 64 * u + lane < dim ? double(x[u]) : 0.0; }
 }
 
 /** Coordinates j0 + 64 u + lane of row i (0 at and past dim), all loads issued before any use:
  *  a loop that used each coordinate as it arrived waited for one load at a time. */
+template <int N = kLaneChunk>
 __device__ inline void lane_coords(const void* x, elem t, int64_t i, int64_t dim, int64_t j0,
-                                   int lane, double (&v)[kLaneChunk])
+                                   int lane, double (&v)[N])
 {
   if (t == elem::bf16) {
     lane_coords_t(static_cast<const __bf16*>(x) + i * dim, dim, j0, lane, v);
@@ -232,12 +233,13 @@ __device__ inline void lane_coords(const void* x, elem t, int64_t i, int64_t dim
   }
 }
 
-/** center[j0 + 64 u + lane], u < kLaneChunk (clamped positions past dim), loaded together. */
+/** center[j0 + 64 u + lane], u < N (clamped positions past dim), loaded together. */
+template <int N = kLaneChunk>
 __device__ inline void lane_center(const double* center, int64_t dim, int64_t j0, int lane,
-                                   double (&c)[kLaneChunk])
+                                   double (&c)[N])
 {
 #pragma unroll
-  for (int u = 0; u < kLaneChunk; ++u) {
+  for (int u = 0; u < N; ++u) {
     const int64_t j = j0 + 64 * u + lane;
     c[u]            = center[j < dim ? j : dim - 1];
   }
@@ -391,6 +393,7 @@ __global__ __launch_bounds__(256) void encode_rows_f16_kernel(const void* x, ele
  * (raised for the rounding of their sums, sqrt_up). Per-lane fp64 partial sums and a butterfly:
  * the sums only enter bounds that carry these slacks.
  */
+template <int N>
 __global__ __launch_bounds__(256) void encode_queries_f16_kernel(const void* q, const int32_t* rows,
                                                                  elem t, int64_t nq,
                                                                  int64_t nq_pad, int64_t dim,
@@ -415,18 +418,19 @@ __global__ __launch_bounds__(256) void encode_queries_f16_kernel(const void* q, 
     if (lane == 0) { qscal[3 * i] = qscal[3 * i + 1] = qscal[3 * i + 2] = 0.0; }
     return;
   }
-  // a query of at most 64 kLaneChunk coordinates is loaded once, for its norm and its encoding
+  // a query of at most 64 N coordinates is loaded once, for its norm and its encoding (N, the
+  // coordinates per lane and chunk, is sized to the dimension: fewer registers, more waves)
   const int64_t r      = rows != nullptr ? int64_t(rows[i]) : i;  // the caller's query row
-  const bool one_chunk = dim <= 64 * kLaneChunk;
-  double v[kLaneChunk], c[kLaneChunk];
+  const bool one_chunk = dim <= 64 * N;
+  double v[N], c[N];
   double nrm = 1.0;
   if (one_chunk) {
-    lane_coords(q, t, r, dim, 0, lane, v);
-    lane_center(center, dim, 0, lane, c);
+    lane_coords<N>(q, t, r, dim, 0, lane, v);
+    lane_center<N>(center, dim, 0, lane, c);
     if (normalize) {
       double s2 = 0;
 #pragma unroll
-      for (int u = 0; u < kLaneChunk; ++u) { s2 = fma(v[u], v[u], s2); }  // past dim: + 0, exact
+      for (int u = 0; u < N; ++u) { s2 = fma(v[u], v[u], s2); }  // past dim: + 0, exact
       s2  = wave_sum(s2);
       nrm = s2 > 0 ? sqrt(s2) : 1.0;
     }
@@ -434,13 +438,13 @@ __global__ __launch_bounds__(256) void encode_queries_f16_kernel(const void* q, 
     nrm = wave_row_norm(q, t, r, dim, lane);
   }
   double a = 0, nw = 0, ew = 0;
-  for (int64_t j0 = 0; j0 < dim; j0 += 64 * kLaneChunk) {
+  for (int64_t j0 = 0; j0 < dim; j0 += 64 * N) {
     if (!one_chunk) {
-      lane_coords(q, t, r, dim, j0, lane, v);
-      lane_center(center, dim, j0, lane, c);
+      lane_coords<N>(q, t, r, dim, j0, lane, v);
+      lane_center<N>(center, dim, j0, lane, c);
     }
 #pragma unroll
-    for (int u = 0; u < kLaneChunk; ++u) {
+    for (int u = 0; u < N; ++u) {
       const int64_t j = j0 + 64 * u + lane;
       if (j < dim) {
         const double w   = (v[u] / nrm - c[u]) * inv_alpha;
@@ -516,9 +520,21 @@ void encode_queries_f16(const void* q, elem t, int64_t nq, int64_t nq_pad, int64
                         const int32_t* rows)
 {
   if (nq_pad == 0) { return; }
-  // one wave per query, four per block
-  encode_queries_f16_kernel<<<unsigned((nq_pad + 3) / 4), 256, 0, stream>>>(
-    q, rows, t, nq, nq_pad, dim, halves, normalize, center, inv_alpha, qrows, qscal, qpaired);
+  // one wave per query, four per block; a lane's coordinates per chunk sized to the dimension
+  const unsigned grid = unsigned((nq_pad + 3) / 4);
+  auto go = [&](auto kernel) {
+    kernel<<<grid, 256, 0, stream>>>(q, rows, t, nq, nq_pad, dim, halves, normalize, center,
+                                     inv_alpha, qrows, qscal, qpaired);
+  };
+  if (dim <= 256) {
+    go(encode_queries_f16_kernel<4>);
+  } else if (dim <= 512) {
+    go(encode_queries_f16_kernel<8>);
+  } else if (dim <= 768) {
+    go(encode_queries_f16_kernel<12>);
+  } else {
+    go(encode_queries_f16_kernel<kLaneChunk>);
+  }
 }
 
 void remove_rows_f16(const int64_t* ids, int64_t n, int64_t size, float* rowc,
