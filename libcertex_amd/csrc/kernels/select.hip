@@ -1537,7 +1537,8 @@ bool launch_select_regs(int64_t n, unsigned blocks, hipStream_t stream, Args... 
   if (n <= 64 * 16) { L<64, 16>::go(blocks, stream, args...); return true; }
   if (n <= kThreads * 8) { L<kThreads, 8>::go(blocks, stream, args...); return true; }
   if (n <= kThreads * 16) { L<kThreads, 16>::go(blocks, stream, args...); return true; }
-  return false;  // larger tables: the streaming kernels (more blocks per CU, measured faster)
+  if (n <= kThreads * 72) { L<kThreads, 72>::go(blocks, stream, args...); return true; }
+  return false;  // larger tables: the streaming kernels
 }
 
 template <int T, int VPT>
