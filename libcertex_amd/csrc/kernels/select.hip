@@ -1295,6 +1295,7 @@ __device__ int radix_pass(int64_t n, F key_of, radix_state& st, int* hist, int* 
   const uint32_t dm = (1u << w) - 1u;
   hist[tid]         = 0;
   __syncthreads();
+  int cur = -1, run_n = 0;  // a run of keys in one bin adds up before one atomic
   for (int64_t e0 = 0; e0 < n; e0 += int64_t(kThreads) * kBatch) {
     uint32_t kk[kBatch];  // loads first (from clamped positions), then the counts
 #pragma unroll
@@ -1305,10 +1306,18 @@ __device__ int radix_pass(int64_t n, F key_of, radix_state& st, int* hist, int* 
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
       if (e0 + i * kThreads + tid < n && (kk[i] & st.mask) == st.prefix) {
-        atomicAdd(&hist[(kk[i] >> shift) & dm], 1);
+        const int d = int((kk[i] >> shift) & dm);
+        if (d == cur) {
+          ++run_n;
+        } else {
+          if (run_n > 0) { atomicAdd(&hist[cur], run_n); }
+          cur   = d;
+          run_n = 1;
+        }
       }
     }
   }
+  if (run_n > 0) { atomicAdd(&hist[cur], run_n); }
   __syncthreads();
   const int c    = hist[tid];
   const int incl = block_scan_incl(c, wave_tot);
@@ -1427,10 +1436,23 @@ __device__ uint32_t radix_select_regs(const uint32_t (&kk)[VPT], int rank, int* 
       for (int j = 0; j < BPT; ++j) { hist[tid * BPT + j] = 0; }
     }
     __syncthreads();
+    // a thread's keys that fall into the bin of its previous key add up before one atomic: the
+    // group maxima of a query crowd into few bins, where every key's own atomic serialised
+    int cur = -1, run_n = 0;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      if ((kk[i] & mask) == prefix) { atomicAdd(&hist[(kk[i] >> shift) & dm], 1); }
+      if ((kk[i] & mask) == prefix) {
+        const int d = int((kk[i] >> shift) & dm);
+        if (d == cur) {
+          ++run_n;
+        } else {
+          if (run_n > 0) { atomicAdd(&hist[cur], run_n); }
+          cur   = d;
+          run_n = 1;
+        }
+      }
     }
+    if (run_n > 0) { atomicAdd(&hist[cur], run_n); }
     __syncthreads();
     int c[BPT], sum = 0;
 #pragma unroll
