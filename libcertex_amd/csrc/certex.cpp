@@ -793,16 +793,25 @@ struct table_plan {
 };
 
 /**
+ * Stride of the list anchors: half the anchor stride. The nearest lists hold the rows near the
+ * query, where twice the density of the anchors of every row halves the survivors (config 2: 163
+ * -> 82 per query; the screen 1.7% faster at one clock, the re-rank 0.105 -> 0.063 ms, the
+ * anchors 0.143 -> 0.190 ms). A quarter (41 survivors) cost more in the anchors (0.275 ms) than
+ * it saved.
+ */
+auto list_anchor_stride(index_state const& st) -> int64_t { return std::max(1, st.anchor_stride / 2); }
+
+/**
  * The list-anchor threshold's center terms: cterm, with +inf for every list of fewer than
- * kListAnchorMin anchors (rows list_offsets[j] + i anchor_stride), so that the nearest lists of a
- * query are lists of at least that many anchors. Set where the lists are set (build, load).
+ * kListAnchorMin anchors (rows list_offsets[j] + i list_anchor_stride), so that the nearest lists
+ * of a query are lists of at least that many anchors. Set where the lists are set (build, load).
  */
 void set_anchor_centers(cuvs::resources const& res, index_state& st)
 {
   hipStream_t stream = static_cast<hipStream_t>(res.stream());
   const int L        = st.n_lists;
   const int Lp       = certex_amd::pad_centers(L);
-  const int64_t s    = std::max(1, st.anchor_stride);
+  const int64_t s    = list_anchor_stride(st);
   std::vector<float> ct(static_cast<size_t>(Lp));
   CERTEX_HIP_TRY(hipMemcpyAsync(ct.data(), st.cterm.p, size_t(Lp) * 4, hipMemcpyDeviceToHost, stream));
   CERTEX_HIP_TRY(hipStreamSynchronize(stream));
@@ -895,7 +904,7 @@ void table_pass(cuvs::resources const& res, index_state const& st, certex_amd::s
                                  st.cterm_anchor.as<float>(), Lp, st.n_lists, lists, temp, stream);
     certex_amd::list_anchor_groups(st.codes.as<int8_t>(), st.rowc.as<int32_t>(), st.row_bytes,
                                    aa.qcodes, aa.nq, lists, st.list_offsets_dev.as<int64_t>(),
-                                   st.n_lists, std::max(1, st.anchor_stride), temp,
+                                   st.n_lists, list_anchor_stride(st), temp,
                                    static_cast<int32_t*>(aa.gmax), stream);
     return;
   }
@@ -931,6 +940,7 @@ void capture_common(index_state const& st, table_plan const& tp, int64_t B, int6
   t_capture.value("fine", int64_t(tp.ap.fine));
   t_capture.value("anchor_stride", int64_t(tp.ap.stride));
   t_capture.value("list_anchors", int64_t(tp.list_anchors));
+  t_capture.value("list_anchor_stride", list_anchor_stride(st));
   t_capture.value("row_bytes", int64_t(st.row_bytes));
   t_capture.value("size", int64_t(st.size));
   t_capture.put("codes", st.codes.p, size_t(st.size) * st.row_bytes, stream);

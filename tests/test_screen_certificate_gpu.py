@@ -173,7 +173,7 @@ def test_int8_list_anchors(gpu, k, metric, stride, d):
     """An index stored in k-means lists and searched without a probe takes its thresholds from the
     anchors of each query's 8 nearest lists: column 64 t + g of the group table holds the largest
     <q', x'> + rowc over the anchors i = g, g + 64, ... of the query's t-th list (its stored rows
-    offset + i stride). Checked against the brute force as above: the table, theta as its k-th
+    offset + i stride / 4). Checked against the brute force as above: the table, theta as its k-th
     largest column, no true top-k row below theta, the survivors exactly the rows at or above it."""
     nq, n = 96, 120_000
     X, Q, removed = int8_case(n, nq, "uint8", seed=k + stride, d=d)
@@ -183,8 +183,9 @@ def test_int8_list_anchors(gpu, k, metric, stride, d):
     Qg = torch.from_numpy(Q).cuda()
     get = captured(lambda: idx.search(Qg, k=k, batch=nq, probe_lists=0))
     B, size, rb = int(get("B")), int(get("size")), int(get("row_bytes"))
-    p = int(get("list_anchors"))
+    p, ls = int(get("list_anchors")), int(get("list_anchor_stride"))
     assert (B, size, rb, p) == (nq, n, 128 if d <= 128 else 256, 8) and not get("all_rows")
+    assert ls == max(1, stride // 2)
     codes = get("codes", np.int8, (size, rb)).astype(np.int64)
     rowc = get("rowc", np.int32).astype(np.int64)
     qrows = get("qrows", np.int8, (B, rb)).astype(np.int64)
@@ -197,14 +198,14 @@ def test_int8_list_anchors(gpu, k, metric, stride, d):
     assert off[0] == 0 and off[-1] == size and (np.diff(off) >= 0).all()
     assert ((lists >= 0) & (lists < 64)).all()
     assert all(len(set(r)) == p for r in lists.tolist()), "a list twice among a query's nearest"
-    n_anchor = (np.diff(off) + stride - 1) // stride
+    n_anchor = (np.diff(off) + ls - 1) // ls
     assert (n_anchor[lists] >= 32).all(), "a list of fewer than 32 anchors among the nearest"
     gmax = get("gmax", np.int32, (B, 64 * p)).astype(np.int64)
     want = np.full((B, 64 * p), np.iinfo(np.int32).min, np.int64)
     for q in range(B):
         for t in range(p):
             j = lists[q, t]
-            rows = np.arange(off[j], off[j + 1], stride)
+            rows = np.arange(off[j], off[j + 1], ls)
             np.maximum.at(want[q], t * 64 + np.arange(len(rows)) % 64, acc[q, rows])
     assert np.array_equal(gmax, want), "list anchor group maxima"
 
