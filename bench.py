@@ -9,7 +9,7 @@ rounded half-to-even and clipped to [0, 255]; drawn with torch generators seeded
 (base) and 3 (queries). The index stores its rows in the order of 4,096 k-means lists (built
 with the index; --lists 0 keeps id order) and the searches probe none of them (--probe 0): every
 row is screened, and similar consecutive rows switch fewer bits in the MFMA (about 3% faster
-screen, measured). Prints one JSON line with the roofline of the dominant kernel (the int8
+screen, measured); the thresholds come from the anchors of each query's 8 nearest lists. Prints one JSON line with the roofline of the dominant kernel (the int8
 MFMA screen, timed with HIP events inside the library over the timed steps) and the CPU oracle's
 exhaustive fp64 search timed on the first queries against the full base.
 """
@@ -761,7 +761,8 @@ def main():
             "n_lists": n_lists,
             "probe_lists": args.probe if n_lists else 0,
             "row_order": ("k-means list order" if n_lists else "id order")
-            + (" (the lists only order the stored rows; every row is screened)" if n_lists and not args.probe else ""),
+            + (" (every row is screened; the lists order the stored rows, and the anchors of each query's"
+               " 8 nearest lists bound its threshold)" if n_lists and not args.probe else ""),
             "build_s": round(t_build, 2),
             "screen": "int8 MFMA (exact), re-rank fp64",
             "phase_ms_per_step": phase_ms,
