@@ -375,8 +375,9 @@ def bench_config5(args):
     resident in HBM), 10,000 queries; while the timed searches run, another thread extends the
     index by 1,000,000 rows and removes 1,000,000 random ids. Afterwards 16 queries are checked
     against a GPU fp64 brute force over the live set (exact for 8-bit data). The config's 4,096
-    k-means lists (a speed option: the rows stored in list order, each query's nearest lists probed
-    first) need the whole base in one build: it is generated into host memory (128 GB) and built
+    k-means lists (a speed option: the rows stored in list order, the anchors of each query's 8
+    nearest lists bounding its threshold; --probe 2 probes the 2 nearest lists' rows instead) need
+    the whole base in one build: it is generated into host memory (128 GB) and built
     from there; --lists 0 builds by chunks without lists instead."""
     import threading
 
@@ -392,7 +393,7 @@ def bench_config5(args):
         return mixture_u8(m, d, 1000, centres, 100 + i if i >= 0 else 99, dev)
 
     n_lists = 4096 if args.lists < 0 else args.lists
-    args.probe = 2 if args.probe < 0 else args.probe
+    args.probe = 0 if args.probe < 0 else args.probe
     idx = certex.Index(d, metric="l2", capacity=n + n_new, n_lists=n_lists)
     t_build = time.perf_counter()
     if n_lists > 0:
@@ -606,7 +607,7 @@ def main():
     ap.add_argument("--stride", type=int, default=0,
                     help="configs 2 and 3: the index's anchor stride (default: the API's, 16)")
     ap.add_argument("--probe", type=int, default=-1,
-                    help="lists probed per query (default: the config's, 0 for config 2, 2 for config 5)")
+                    help="lists probed per query (default 0: the anchors of each query's 8 nearest lists set its threshold)")
     ap.add_argument("--summarize", nargs="+", metavar="DIR",
                     help="print a summary of the rocprofv3 CSV output under DIR (of a run with the "
                     "same --warmup and --steps) and exit; needs no GPU")

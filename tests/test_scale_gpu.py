@@ -84,8 +84,9 @@ def test_config5_workload_lists_during_updates(gpu):
     def reader():
         try:
             with torch.cuda.stream(torch.cuda.Stream()):
-                while not done.is_set() or len(results) < 3:
-                    D, I = idx.search(Q[:256], k=K, probe_lists=2)
+                while not done.is_set() or len(results) < 4:
+                    # the list anchors (no probe, config 5's default) and the probe in turn
+                    D, I = idx.search(Q[:256], k=K, probe_lists=(0, 2)[len(results) % 2])
                     torch.cuda.current_stream().synchronize()
                     results.append((D, I))
         except Exception as e:  # noqa: BLE001
