@@ -1586,10 +1586,11 @@ struct threshold_f_regs_launch {
  * the k survivors with the largest screen values are scored, which bounds the k-th neighbour's
  * score by U; then only the survivors whose screen lower bound does not exceed U are scored
  * (U tightens as better rows arrive). Scores use one wave per row; the best k by (score, row)
- * stay in LDS.
+ * stay in LDS. With 64-lane slots (d above 256) eight waves per SIMD, as many blocks as the LDS of a
+ * CU holds at config 3 (18 spilled registers; against six waves per SIMD, verify 0.82 -> 0.79 ms).
  */
 template <int L>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(L == 64 ? 6 : 4)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(L == 64 ? 8 : 4)))
 void verify_topk_f_kernel(verify_f_args a, int cap)
 {
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn[];
@@ -1604,8 +1605,8 @@ void verify_topk_f_kernel(verify_f_args a, int cap)
   __shared__ int sel_count;
   __shared__ int fill;
   // survivors whose screen values phase A selects in registers, 24 per thread; not with 64-lane
-  // slots (d above 256), whose six waves per SIMD leave no registers to spare (16 per thread
-  // there measured 4% slower than the streaming select, config 3)
+  // slots (d above 256), whose waves leave no registers to spare (16 per thread at six waves per
+  // SIMD measured 4% slower than the streaming select, config 3)
   constexpr bool REGS = L != 64;
   constexpr int RV    = 24;
 
