@@ -47,6 +47,8 @@ def test_integer_lists(gpu, dtype, n_lists):
         check(X, Q, 10, "l2", D, I)
     D, I = search(idx, Q, 100, probe_lists=2, batch=250)
     check(X, Q, 100, "l2", D, I)
+    D, I = search(idx, Q, 100, probe_lists=0, batch=250)  # k above 64: the anchors of every row
+    check(X, Q, 100, "l2", D, I)
 
 
 def test_integer_lists_host_source(gpu):
@@ -122,12 +124,17 @@ def test_lists_save_load(gpu, tmp_path):
     idx.add(torch.from_numpy(data.mixture_u8(5_000, seed=102)).cuda())
     idx.remove(torch.arange(0, 25_000, 11))
     D0, I0 = search(idx, Q, 10)
+    L0 = search(idx, Q, 10, probe_lists=0)  # the list anchors: the loaded lists' offsets
     idx.save(tmp_path / "lists.idx")
     back = certex.Index.load(tmp_path / "lists.idx")
     assert back.core.lists == (100, 20_000)
     D1, I1 = search(back, Q, 10)
     np.testing.assert_array_equal(I0, I1)
     np.testing.assert_array_equal(D0, D1)
+    L1 = search(back, Q, 10, probe_lists=0)
+    np.testing.assert_array_equal(L0[1], L1[1])
+    np.testing.assert_array_equal(L0[0], L1[0])
+    np.testing.assert_array_equal(L1[1], I1)
     Xf = data.powerlaw_unit(10_000, 96, seed=103)
     fidx = certex.Index(96, n_lists=40)
     fidx.add(torch.from_numpy(Xf).cuda())

@@ -20,12 +20,12 @@ from tests import data
 pytestmark = pytest.mark.gpu
 
 
-def c_search(idx, Q, k, entry, batch=2048, mask=None):
+def c_search(idx, Q, k, entry, batch=2048, mask=None, probe=2):
     """One call of `entry` (cuvsCertexSearch or cuvsCertexSearchNoAlloc) on torch's stream."""
     Q = Q.contiguous()
     I = torch.full((Q.shape[0], k), -7, dtype=torch.int64, device="cuda")
     D = torch.full((Q.shape[0], k), -7.0, dtype=torch.float32, device="cuda")
-    sp = C.SearchParams(128, int(batch), 2)
+    sp = C.SearchParams(128, int(batch), int(probe))
     qb, ib, db = C.Borrowed(Q), C.Borrowed(I), C.Borrowed(D)
     f, wb = C.Filter(0, C.NO_FILTER), None
     if mask is not None:
@@ -54,6 +54,17 @@ def test_uint8_two_calls(gpu):
     idx.add(torch.from_numpy(X).cuda())
     same(idx, Q, 10, batch=3000)
     same(idx, Q[:500], 10, batch=3000)  # the second call, smaller
+
+
+def test_uint8_lists_without_probe_two_calls(gpu):
+    """An index stored in k-means lists, searched without a probe: the thresholds come from the
+    anchors of each query's nearest lists (their scratch carved from the array as well)."""
+    X = data.mixture_u8(200_000, seed=146)
+    Q = torch.from_numpy(data.mixture_u8(2_000, seed=147)).cuda()
+    idx = certex.Index(128, n_lists=64)
+    idx.add(torch.from_numpy(X).cuda())
+    same(idx, Q, 10, batch=2000, probe=0)
+    same(idx, Q[:300], 64, batch=2000, probe=0)  # the second call, smaller
 
 
 def test_float_filtered_two_calls(gpu):
