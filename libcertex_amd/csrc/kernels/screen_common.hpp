@@ -316,6 +316,17 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
   uint32_t base    = 0;
   if (lane == leader) { base = atomicAdd(n_hits, total); }
   uint32_t pos = uint32_t(__builtin_amdgcn_readlane(int(base), leader)) + excl;
+  // the screen values pass through an empty asm statement, and no select below reads an array:
+  // selects between array elements are otherwise folded into one load at a computed index, which
+  // puts the values in scratch memory
+  const auto L = [](float f) {
+    if constexpr (VALS) { asm("" : "+v"(f)); }
+    return f;
+  };
+  const float x0 = L(float(v[0])), x1 = L(float(v[1])), x2 = L(float(v[2])), x3 = L(float(v[3]));
+  const float x4 = L(float(v[4])), x5 = L(float(v[5])), x6 = L(float(v[6])), x7 = L(float(v[7]));
+  const float x8 = L(float(v[8])), x9 = L(float(v[9])), x10 = L(float(v[10])), x11 = L(float(v[11]));
+  const float x12 = L(float(v[12])), x13 = L(float(v[13])), x14 = L(float(v[14])), x15 = L(float(v[15]));
   // each lane writes its survivors at pos, pos + 1, ...: the list, then the workgroup's spill
   // region (plain stores, moved to the buckets by the flush), then, when both are full (or no pool
   // was provided), straight into the global bucket with one atomic each
@@ -325,8 +336,13 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
     const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
     float val          = 0.0f;
     if constexpr (VALS) {
-#pragma unroll
-      for (int t = 0; t < 16; ++t) { val = t == j ? float(v[t]) : val; }
+      // value j of the lane's 16: a select tree on the 4 bits of j (15 selects on 4 masks)
+      const bool b0 = (j & 1) != 0, b1 = (j & 2) != 0, b2 = (j & 4) != 0, b3 = (j & 8) != 0;
+      const float a0 = b0 ? x1 : x0, a1 = b0 ? x3 : x2, a2 = b0 ? x5 : x4, a3 = b0 ? x7 : x6;
+      const float a4 = b0 ? x9 : x8, a5 = b0 ? x11 : x10, a6 = b0 ? x13 : x12, a7 = b0 ? x15 : x14;
+      const float c0 = b1 ? a1 : a0, c1 = b1 ? a3 : a2, c2 = b1 ? a5 : a4, c3 = b1 ? a7 : a6;
+      const float d0 = b2 ? c1 : c0, d1 = b2 ? c3 : c2;
+      val            = b3 ? d1 : d0;
     }
     if (pos < cap) {
       hit_q[pos]   = qloc;
