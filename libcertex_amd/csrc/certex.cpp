@@ -541,15 +541,12 @@ bool screen_into_buckets(cuvs::resources const& res, int64_t B, int64_t nq_pad, 
     }
     // survivors past the workgroups' LDS lists: a pool of the buckets' size, once a search of
     // these resources has overflowed them (the first such search took the slower atomic path)
-    sa.spill_q = nullptr, sa.spill_row = nullptr, sa.spill_val = nullptr, sa.spill_pool = 0;
+    sa.spill = nullptr, sa.spill_pool = 0;
     if (rs.spill_pool) {
       const size_t e = size_t(nq_pad) * size_t(cap);
-      sa.spill_q     = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_spill_q, e * 4));
-      sa.spill_row   = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_spill_row, e * 4));
-      if (vals != nullptr) {
-        sa.spill_val = static_cast<float*>(rs.get(cuvs::detail::ws_spill_val, e * 4));
-      }
-      sa.spill_pool = int64_t(e);
+      const size_t w = size_t(certex_amd::spill_words(vals != nullptr));
+      sa.spill       = static_cast<uint32_t*>(rs.get(cuvs::detail::ws_spill, e * 4 * w));
+      sa.spill_pool  = int64_t(e);
     }
     certex_amd::fill_u32(count, nq_pad, 0, stream);
     certex_amd::fill_u32(small, 2, 0, stream);

@@ -106,9 +106,7 @@ enum ws_slot : int {
   ws_probe_dist,  // list probe: center distances of the batch's queries
   ws_probe,       // list probe: nearest lists, pair tables
   ws_probe_rows,  // list probe: the query row of every (query, list) pair
-  ws_spill_q,     // screen spill pool: query of each entry
-  ws_spill_row,   // screen spill pool: row of each entry
-  ws_spill_val,   // screen spill pool: screen value of each entry (fp16 rows)
+  ws_spill,       // screen spill pool: packed query and row of each entry (+ value, fp16 rows)
   ws_qpaired,     // the batch's fp16 query rows in the paired layout (the tiled screen)
   ws_qlabels,     // query labels given in host memory, copied for the label filter
   ws_n_slots

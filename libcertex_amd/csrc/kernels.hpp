@@ -27,6 +27,11 @@ constexpr int32_t kKeepNone = 0x7fffffff;
 
 /** Rows of one screen step. */
 constexpr int kStepRows  = 64;
+/** Spill pool entries: the low kSpillRowBits bits of an entry's first word hold its row's offset
+ *  from the workgroup's first row, the bits above its query within the workgroup. */
+constexpr int kSpillRowBits = 20;
+/** Words of a spill entry: the packed query and row, then the screen value for fp16 rows. */
+constexpr int spill_words(bool values) { return values ? 2 : 1; }
 /** Widest integer row (bytes) that the MFMA screen instantiates. */
 constexpr int kMaxIntDim = 4096;
 
@@ -202,14 +207,13 @@ struct screen_args {
   float* cand_vals     = nullptr;  // [nq_pad, cap] screen values (fp16 rows only)
   int64_t cap          = 0;
   // screen: survivors past a workgroup's LDS list go to the workgroup's own region of a pool of
-  // spill_pool entries (query within the block, row, and screen value for fp16 rows), with plain
-  // stores; the launcher splits the pool evenly among its workgroups (spill_cap each), and the
-  // workgroup's flush moves its region into the buckets. Survivors past the region take a global
-  // atomic each. spill_need (device word) gets the largest count past the LDS list of any
-  // workgroup, so that the host knows whether to provide a pool.
-  uint32_t* spill_q   = nullptr;
-  uint32_t* spill_row = nullptr;
-  float* spill_val    = nullptr;
+  // spill_pool entries, with plain stores; the launcher splits the pool evenly among its
+  // workgroups (spill_cap each), and the workgroup's flush moves its region into the buckets.
+  // An entry is one word, (query within the block) << kSpillRowBits | (row - the workgroup's first
+  // row), followed for fp16 rows by the screen value's bits (kSpillWords). Survivors past the
+  // region take a global atomic each. spill_need (device word) gets the largest count past the
+  // LDS list of any workgroup, so that the host knows whether to provide a pool.
+  uint32_t* spill     = nullptr;
   int64_t spill_pool  = 0;
   int64_t spill_cap   = 0;  // set by the launcher
   uint32_t* spill_need = nullptr;

@@ -39,6 +39,7 @@
 
 #include "screen_common.hpp"
 
+#include <stdexcept>
 #include <type_traits>
 
 namespace certex_amd {
@@ -118,6 +119,8 @@ void screen_kernel(screen_args a)
   const int64_t quarter = a.chunk_steps / 4;
   const int64_t w0      = w.chunk * a.chunk_steps + wave * quarter;
   const int64_t w1      = w0 + quarter < n_steps ? w0 + quarter : n_steps;
+  // the workgroup's first row: its spill entries hold rows as offsets from it
+  const int64_t rbase   = w.base + w.chunk * a.chunk_steps * kStepRows;
   // coarse anchor groups of one group per wave: each wave's group maxima wait in LDS, and the
   // workgroup writes each query's 4 consecutive columns together at its end (one 16-byte run per
   // query instead of four 4-byte stores to four lines of the table)
@@ -275,7 +278,7 @@ void screen_kernel(screen_args a)
               for (int r = 0; r < 4; ++r) { v16[bt * 4 + r] = acc[bt][qt][r]; }
             }
           }
-          push_hits<BT * 4, FILT, R::kValues>(bits, qloc, w.base + row0, q0, a, hit_q, hit_row,
+          push_hits<BT * 4, FILT, R::kValues>(bits, qloc, w.base + row0, rbase, q0, a, hit_q, hit_row,
                                               hit_val, &n_hits, uint32_t(kHitCap), v16);
         }
       }
@@ -395,7 +398,7 @@ void screen_kernel(screen_args a)
   }
   if constexpr (!ANCHORS) {
     __syncthreads();
-    flush_hits<R::kValues>(q0, QB, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(kHitCap),
+    flush_hits<R::kValues>(q0, rbase, QB, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(kHitCap),
                            reinterpret_cast<uint32_t*>(qlds));
     clk.stop(a);
   }
@@ -421,7 +424,10 @@ void launch(const screen_args& a, hipStream_t stream)
   const dim3 grid{unsigned(blocks)};
   const int ks  = a.row_bytes / 64;
   screen_args b = a;
-  b.spill_cap   = !ANCHORS && a.spill_q != nullptr ? a.spill_pool / blocks : 0;
+  b.spill_cap   = !ANCHORS && a.spill != nullptr ? a.spill_pool / blocks : 0;
+  if (b.spill_cap > 0 && b.chunk_steps * kStepRows > (int64_t(1) << kSpillRowBits)) {
+    throw std::logic_error("certex: a screen chunk has more rows than a spill entry can address");
+  }
   if constexpr (ANCHORS) {
     if (a.fine) {
       launch_other<R, ANCHORS, FILT, true>(b, grid, ks, qb_size, stream);

@@ -267,6 +267,21 @@ __device__ __forceinline__ uint32_t filter_mask(const screen_args& a, const scre
   return keep;
 }
 
+/** Writes spill pool entry e (an index into the launch's pool): query qloc of the workgroup, row
+ *  roff past the workgroup's first row (below 2^kSpillRowBits), and the screen value for fp16 rows
+ *  (one 8-byte store). */
+template <bool VALS>
+__device__ __forceinline__ void spill_put(const screen_args& a, int64_t e, uint32_t qloc, uint32_t roff,
+                                          float val)
+{
+  const uint32_t w0 = (qloc << kSpillRowBits) | roff;
+  if constexpr (VALS) {
+    reinterpret_cast<uint2*>(a.spill)[e] = make_uint2(w0, __float_as_uint(val));
+  } else {
+    a.spill[e] = w0;
+  }
+}
+
 /**
  * LDS survivor list of a workgroup: hit_q / hit_row / hit_val (the screen values, when the rows
  * carry them) of `cap` entries (kHitCap, or what the K-loop screen's LDS leaves) and the count
@@ -277,15 +292,15 @@ __device__ __forceinline__ uint32_t filter_mask(const screen_args& a, const scre
 /**
  * Appends the survivors of one 16-query tile of a step to the workgroup's list: `bits` is this
  * lane's survivor mask over NB = 16 or 32 rows (4 or 8 row tiles), `qloc` its query within the
- * workgroup, row0 the stored row of its bit 0, v the screen values of bits 0..15 (used when VALS,
- * NB = 16). The wave reserves all of its survivors with one LDS atomic: each lane's offset is the
+ * workgroup, row0 the stored row of its bit 0, rbase the workgroup's first row (spill entries hold
+ * rows as offsets from it), v the screen values of bits 0..15 (used when VALS, NB = 16). The wave reserves all of its survivors with one LDS atomic: each lane's offset is the
  * exclusive prefix of the survivor counts, summed from one ballot per bit of the count. The lanes
  * then write their survivors in as many rounds as the busiest lane has survivors, with no vote or
  * atomic per round. Every lane of the wave must call it.
  */
 template <int NB, bool FILT, bool VALS, typename V>
-__device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t row0, int64_t q0,
-                                          const screen_args& a, uint32_t* hit_q,
+__device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t row0, int64_t rbase,
+                                          int64_t q0, const screen_args& a, uint32_t* hit_q,
                                           uint32_t* hit_row, float* hit_val, uint32_t* n_hits,
                                           uint32_t cap, const V (&v)[16])
 {
@@ -349,10 +364,8 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
       hit_row[pos] = row;
       if constexpr (VALS) { hit_val[pos] = val; }
     } else if (int64_t(pos - cap) < a.spill_cap) {
-      const int64_t e = int64_t(blockIdx.x) * a.spill_cap + int64_t(pos - cap);
-      a.spill_q[e]    = qloc;
-      a.spill_row[e]  = row;
-      if constexpr (VALS) { a.spill_val[e] = val; }
+      spill_put<VALS>(a, int64_t(blockIdx.x) * a.spill_cap + int64_t(pos - cap), qloc,
+                      uint32_t(row0 - rbase) + uint32_t((j >> 2) * 16 + (j & 3)), val);
     } else {
       const int64_t q   = q0 + qloc;
       const uint32_t at = atomicAdd(a.cand_count + q, 1u);
@@ -371,10 +384,11 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
  * region past it. Each LDS entry's rank among its query's survivors comes from an LDS counter
  * (cnt), the region's entries follow the query's LDS entries (cursor cur); then one global atomic
  * per query reserves the query's slots. `scratch` holds 2 qb + cap words of LDS (the query rows'
- * space). Records the workgroup's count past the LDS list in spill_need.
+ * space); rbase is the workgroup's first row (spill_put). Records the workgroup's count past the
+ * LDS list in spill_need.
  */
 template <bool VALS>
-__device__ inline void flush_hits(int64_t q0, int qb, const screen_args& a, const uint32_t* hit_q,
+__device__ inline void flush_hits(int64_t q0, int64_t rbase, int qb, const screen_args& a, const uint32_t* hit_q,
                                   const uint32_t* hit_row, const float* hit_val,
                                   const uint32_t* n_hits, uint32_t cap, uint32_t* scratch)
 {
@@ -393,7 +407,10 @@ __device__ inline void flush_hits(int64_t q0, int qb, const screen_args& a, cons
   __syncthreads();
   for (int e = threadIdx.x; e < qb; e += blockDim.x) { cur[e] = cnt[e]; }
   __syncthreads();
-  for (uint32_t e = threadIdx.x; e < ns; e += blockDim.x) { atomicAdd(&cnt[a.spill_q[region + e]], 1u); }
+  const uint32_t* sp   = a.spill + region * spill_words(VALS);
+  for (uint32_t e = threadIdx.x; e < ns; e += blockDim.x) {
+    atomicAdd(&cnt[sp[e * spill_words(VALS)] >> kSpillRowBits], 1u);
+  }
   __syncthreads();
   for (int e = threadIdx.x; e < qb; e += blockDim.x) {
     if (cnt[e] != 0) { cnt[e] = atomicAdd(a.cand_count + q0 + e, cnt[e]); }
@@ -409,12 +426,19 @@ __device__ inline void flush_hits(int64_t q0, int qb, const screen_args& a, cons
     }
   }
   for (uint32_t e = threadIdx.x; e < ns; e += blockDim.x) {
-    const uint32_t ql    = a.spill_q[region + e];
+    uint32_t w0 = 0, w1 = 0;
+    if constexpr (VALS) {
+      const uint2 v = reinterpret_cast<const uint2*>(sp)[e];
+      w0 = v.x, w1 = v.y;
+    } else {
+      w0 = sp[e];
+    }
+    const uint32_t ql    = w0 >> kSpillRowBits;
     const uint32_t bslot = cnt[ql] + atomicAdd(&cur[ql], 1u);
     if (bslot < a.cap) {
       const int64_t q                = q0 + ql;
-      a.cand_rows[q * a.cap + bslot] = a.spill_row[region + e];
-      if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = a.spill_val[region + e]; }
+      a.cand_rows[q * a.cap + bslot] = uint32_t(rbase + (w0 & ((1u << kSpillRowBits) - 1)));
+      if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = __uint_as_float(w1); }
     }
   }
 }

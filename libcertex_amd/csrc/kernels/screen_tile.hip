@@ -63,6 +63,7 @@ constexpr int kTileRows  = 256;              // stored rows of a tile (4 steps o
 constexpr int kStageB    = 64;               // bytes of a row per stage (32 halves)
 constexpr int kBufs      = 3;                // stage buffers
 constexpr int kTileSteps = kTileRows / kStepRows;
+static_assert(kTileRows <= (1 << kSpillRowBits), "spill entries address a tile's rows");
 
 typedef const __attribute__((address_space(1))) void* gptr;
 typedef __attribute__((address_space(3))) void* lptr;
@@ -361,7 +362,8 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
   // per wave 8 KB: a lane's 4 RT screen values of one query tile, 16-byte slot bt ^ (lane & 7) of
   // its 128 bytes, so that the survivor loop reads a value by its bit index
   uint8_t* vals      = lds + tile_lds(TQ) - kTileWaves * 8192 + wave * 8192 + lane * 128;
-  const int64_t row0 = w.base + scan0 + wr * 16 * RT + (lane >> 4) * 4;  // stored row of bit 0
+  const int64_t row_t = w.base + scan0;  // the tile's first row: spill entries are offsets from it
+  const int64_t row0  = row_t + wr * 16 * RT + (lane >> 4) * 4;  // stored row of bit 0
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int qloc = wq * 16 * QT + qt * 16 + frow;
@@ -416,10 +418,8 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
         hit_row[pos] = row;
         if constexpr (R::kValues) { hit_val[pos] = val; }
       } else if (int64_t(pos - CAP) < a.spill_cap) {
-        const int64_t e = int64_t(blockIdx.x) * a.spill_cap + int64_t(pos - CAP);
-        a.spill_q[e]    = uint32_t(qloc);
-        a.spill_row[e]  = row;
-        if constexpr (R::kValues) { a.spill_val[e] = val; }
+        spill_put<R::kValues>(a, int64_t(blockIdx.x) * a.spill_cap + int64_t(pos - CAP), uint32_t(qloc),
+                              uint32_t(row0 - row_t) + uint32_t((j >> 2) * 16 + (j & 3)), val);
       } else {
         const int64_t q   = w.q0 + qloc;
         const uint32_t at = atomicAdd(a.cand_count + q, 1u);
@@ -432,7 +432,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
     }
   }
   __syncthreads();
-  flush_hits<R::kValues>(w.q0, TQ, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(CAP), scratch);
+  flush_hits<R::kValues>(w.q0, row_t, TQ, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(CAP), scratch);
   clk.stop(a);
 }
 
@@ -460,7 +460,7 @@ void launch_shape(const screen_args& a, hipStream_t stream)
       "fine groups, no filter)");
   }
   screen_args b = a;
-  b.spill_cap   = !ANCH && a.spill_q != nullptr ? a.spill_pool / blocks : 0;
+  b.spill_cap   = !ANCH && a.spill != nullptr ? a.spill_pool / blocks : 0;
   auto* k       = &screen_tile_kernel<R, RT, QT, FILT, ANCH>;
   const int lds = tile_lds_total(TQ);
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(k),
