@@ -194,9 +194,10 @@ def test_config3_shape_labels(gpu):
 
 @pytest.mark.parametrize("d", [100, 300])
 def test_many_survivors_spill(gpu, d):
-    """A quarter of the rows repeat one row near every query (narrow screen at d = 100, K-loop
+    """A quarter of the rows repeat one row near every query (narrow screen at d = 100, tiled
     screen at d = 300): thousands of survivors per workgroup pass its LDS list. Repeated searches
-    (the later ones with the spill pool) must equal the oracle."""
+    (the later ones with the spill pool, whose entries pack query, row offset and value) must equal
+    the oracle."""
     rng = np.random.default_rng(d)
     X = rng.standard_normal((30_000, d)).astype(np.float32)
     base = rng.standard_normal(d).astype(np.float32)

@@ -56,6 +56,24 @@ def test_int_wide(gpu, dtype, metric, d):
         check(X, Q, k, metric, D, I)
 
 
+def test_int_wide_many_survivors_spill(gpu):
+    """d = 384 (the tiled int8 screen): a quarter of the rows repeat one row near every query, so a
+    tile of 256 rows keeps thousands of survivors, past its LDS list. The first search moves them
+    with a global atomic each and asks for a spill pool; the later ones write the tiles' spill
+    regions (entries of one word: query and row offset). Every search must equal the oracle."""
+    rng = np.random.default_rng(384)
+    X = rng.integers(0, 256, (40_000, 384)).astype(np.uint8)
+    base = rng.integers(0, 256, 384).astype(np.uint8)
+    X[rng.permutation(40_000)[:10_000]] = base
+    Q = np.clip(base.astype(np.int32) + rng.integers(-2, 3, (64, 384)), 0, 255).astype(np.uint8)
+    idx = certex.Index(384, metric="l2")
+    idx.add(torch.from_numpy(X).cuda())
+    for _ in range(3):
+        D, I = idx.search(torch.from_numpy(Q).cuda(), k=100)
+        torch.cuda.synchronize()
+        check(X, Q, 100, "l2", D, I)
+
+
 def test_int_wide_updates_filters_labels(gpu):
     """d = 960: extend from host memory, removals, a bitset, a bitmap, labels through the filter
     and through the paired label partition (the routed tiled screen and anchor pass)."""
