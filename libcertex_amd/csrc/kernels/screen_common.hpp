@@ -330,7 +330,8 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
   const int leader = __builtin_ctzll(__ballot(1));
   uint32_t base    = 0;
   if (lane == leader) { base = atomicAdd(n_hits, total); }
-  uint32_t pos = uint32_t(__builtin_amdgcn_readlane(int(base), leader)) + excl;
+  const uint32_t first = uint32_t(__builtin_amdgcn_readlane(int(base), leader));
+  uint32_t pos         = first + excl;
   // the screen values pass through an empty asm statement, and no select below reads an array:
   // selects between array elements are otherwise folded into one load at a computed index, which
   // puts the values in scratch memory
@@ -344,38 +345,56 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
   const float x12 = L(float(v[12])), x13 = L(float(v[13])), x14 = L(float(v[14])), x15 = L(float(v[15]));
   // each lane writes its survivors at pos, pos + 1, ...: the list, then the workgroup's spill
   // region (plain stores, moved to the buckets by the flush), then, when both are full (or no pool
-  // was provided), straight into the global bucket with one atomic each
-  while (bits != 0) {
-    const int j        = __builtin_ctz(bits);
-    bits &= bits - 1;
-    const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
-    float val          = 0.0f;
-    if constexpr (VALS) {
-      // value j of the lane's 16: a select tree on the 4 bits of j (15 selects on 4 masks)
-      const bool b0 = (j & 1) != 0, b1 = (j & 2) != 0, b2 = (j & 4) != 0, b3 = (j & 8) != 0;
-      const float a0 = b0 ? x1 : x0, a1 = b0 ? x3 : x2, a2 = b0 ? x5 : x4, a3 = b0 ? x7 : x6;
-      const float a4 = b0 ? x9 : x8, a5 = b0 ? x11 : x10, a6 = b0 ? x13 : x12, a7 = b0 ? x15 : x14;
-      const float c0 = b1 ? a1 : a0, c1 = b1 ? a3 : a2, c2 = b1 ? a5 : a4, c3 = b1 ? a7 : a6;
-      const float d0 = b2 ? c1 : c0, d1 = b2 ? c3 : c2;
-      val            = b3 ? d1 : d0;
+  // was provided), straight into the global bucket with one atomic each. A wave whose survivors all
+  // go to the list, or all to the region, takes a loop without the per-survivor choice
+  const auto each = [&](auto put) {
+    while (bits != 0) {
+      const int j = __builtin_ctz(bits);
+      bits &= bits - 1;
+      float val   = 0.0f;
+      if constexpr (VALS) {
+        // value j of the lane's 16: a select tree on the 4 bits of j (15 selects on 4 masks)
+        const bool b0 = (j & 1) != 0, b1 = (j & 2) != 0, b2 = (j & 4) != 0, b3 = (j & 8) != 0;
+        const float a0 = b0 ? x1 : x0, a1 = b0 ? x3 : x2, a2 = b0 ? x5 : x4, a3 = b0 ? x7 : x6;
+        const float a4 = b0 ? x9 : x8, a5 = b0 ? x11 : x10, a6 = b0 ? x13 : x12, a7 = b0 ? x15 : x14;
+        const float c0 = b1 ? a1 : a0, c1 = b1 ? a3 : a2, c2 = b1 ? a5 : a4, c3 = b1 ? a7 : a6;
+        const float d0 = b2 ? c1 : c0, d1 = b2 ? c3 : c2;
+        val            = b3 ? d1 : d0;
+      }
+      put(uint32_t((j >> 2) * 16 + (j & 3)), val);
+      ++pos;
     }
+  };
+  const uint32_t roff0 = uint32_t(row0 - rbase);
+  if (first + total <= cap) {
+    each([&](uint32_t d, float val) {
+      hit_q[pos]   = qloc;
+      hit_row[pos] = uint32_t(row0) + d;
+      if constexpr (VALS) { hit_val[pos] = val; }
+    });
+    return;
+  }
+  const int64_t e0 = int64_t(blockIdx.x) * a.spill_cap - int64_t(cap);
+  if (first >= cap && int64_t(first - cap) + total <= a.spill_cap) {
+    each([&](uint32_t d, float val) { spill_put<VALS>(a, e0 + pos, qloc, roff0 + d, val); });
+    return;
+  }
+  each([&](uint32_t d, float val) {
     if (pos < cap) {
       hit_q[pos]   = qloc;
-      hit_row[pos] = row;
+      hit_row[pos] = uint32_t(row0) + d;
       if constexpr (VALS) { hit_val[pos] = val; }
     } else if (int64_t(pos - cap) < a.spill_cap) {
-      spill_put<VALS>(a, int64_t(blockIdx.x) * a.spill_cap + int64_t(pos - cap), qloc,
-                      uint32_t(row0 - rbase) + uint32_t((j >> 2) * 16 + (j & 3)), val);
+      spill_put<VALS>(a, e0 + pos, qloc, roff0 + d, val);
     } else {
       const int64_t q   = q0 + qloc;
       const uint32_t at = atomicAdd(a.cand_count + q, 1u);
       if (at < a.cap) {
-        a.cand_rows[q * a.cap + at] = row;
+        a.cand_rows[q * a.cap + at] = uint32_t(row0) + d;
         if constexpr (VALS) { a.cand_vals[q * a.cap + at] = val; }
       }
     }
-    ++pos;
-  }
+  });
 }
 
 /**
