@@ -404,22 +404,39 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
     const int leader = __builtin_ctzll(__ballot(1));
     uint32_t base    = 0;
     if (lane == leader) { base = atomicAdd(&n_hits, total); }
-    uint32_t pos = uint32_t(__builtin_amdgcn_readlane(int(base), leader)) + excl;
-    while (bits != 0) {
-      const int j        = __builtin_ctz(bits);
-      bits &= bits - 1;
-      const uint32_t row = uint32_t(row0 + (j >> 2) * 16 + (j & 3));
-      float val          = 0;
-      if constexpr (R::kValues) {
-        val = *reinterpret_cast<const float*>(vals + ((((j >> 2) ^ (lane & 7)) << 4) | ((j & 3) << 2)));
+    const uint32_t first = uint32_t(__builtin_amdgcn_readlane(int(base), leader));
+    uint32_t pos         = first + excl;
+    // each survivor with its value (read back from the parked values by bit index); a wave whose
+    // survivors all fit the list takes a loop without the choice between list, region and bucket
+    const auto each = [&](auto put) {
+      while (bits != 0) {
+        const int j = __builtin_ctz(bits);
+        bits &= bits - 1;
+        float val   = 0;
+        if constexpr (R::kValues) {
+          val = *reinterpret_cast<const float*>(vals + ((((j >> 2) ^ (lane & 7)) << 4) | ((j & 3) << 2)));
+        }
+        put(uint32_t((j >> 2) * 16 + (j & 3)), val);
+        ++pos;
       }
+    };
+    if (first + total <= uint32_t(CAP)) {
+      each([&](uint32_t d, float val) {
+        hit_q[pos]   = uint32_t(qloc);
+        hit_row[pos] = uint32_t(row0) + d;
+        if constexpr (R::kValues) { hit_val[pos] = val; }
+      });
+      continue;
+    }
+    each([&](uint32_t d, float val) {
+      const uint32_t row = uint32_t(row0) + d;
       if (pos < uint32_t(CAP)) {
         hit_q[pos]   = uint32_t(qloc);
         hit_row[pos] = row;
         if constexpr (R::kValues) { hit_val[pos] = val; }
       } else if (int64_t(pos - CAP) < a.spill_cap) {
         spill_put<R::kValues>(a, int64_t(blockIdx.x) * a.spill_cap + int64_t(pos - CAP), uint32_t(qloc),
-                              uint32_t(row0 - row_t) + uint32_t((j >> 2) * 16 + (j & 3)), val);
+                              uint32_t(row0 - row_t) + d, val);
       } else {
         const int64_t q   = w.q0 + qloc;
         const uint32_t at = atomicAdd(a.cand_count + q, 1u);
@@ -428,8 +445,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
           if constexpr (R::kValues) { a.cand_vals[q * a.cap + at] = val; }
         }
       }
-      ++pos;
-    }
+    });
   }
   __syncthreads();
   flush_hits<R::kValues>(w.q0, row_t, TQ, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(CAP), scratch);
