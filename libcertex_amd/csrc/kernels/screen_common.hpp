@@ -427,9 +427,31 @@ __device__ inline void flush_hits(int64_t q0, int64_t rbase, int qb, const scree
   for (int e = threadIdx.x; e < qb; e += blockDim.x) { cur[e] = cnt[e]; }
   __syncthreads();
   const uint32_t* sp   = a.spill + region * spill_words(VALS);
-  for (uint32_t e = threadIdx.x; e < ns; e += blockDim.x) {
-    atomicAdd(&cnt[sp[e * spill_words(VALS)] >> kSpillRowBits], 1u);
-  }
+  // the region's entries, SB per thread and round: their loads are in flight together
+  constexpr int SB      = 8;
+  const auto region_rounds = [&](auto f) {
+    for (uint32_t e0 = threadIdx.x; e0 < ns; e0 += SB * blockDim.x) {
+      uint32_t w0[SB], w1[SB];
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        const uint32_t e = e0 + uint32_t(i) * blockDim.x;
+        w0[i] = 0, w1[i] = 0;
+        if (e < ns) {
+          if constexpr (VALS) {
+            const uint2 v = reinterpret_cast<const uint2*>(sp)[e];
+            w0[i] = v.x, w1[i] = v.y;
+          } else {
+            w0[i] = sp[e];
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        if (e0 + uint32_t(i) * blockDim.x < ns) { f(w0[i], w1[i]); }
+      }
+    }
+  };
+  region_rounds([&](uint32_t w0, uint32_t) { atomicAdd(&cnt[w0 >> kSpillRowBits], 1u); });
   __syncthreads();
   for (int e = threadIdx.x; e < qb; e += blockDim.x) {
     if (cnt[e] != 0) { cnt[e] = atomicAdd(a.cand_count + q0 + e, cnt[e]); }
@@ -444,14 +466,7 @@ __device__ inline void flush_hits(int64_t q0, int64_t rbase, int qb, const scree
       if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = hit_val[e]; }
     }
   }
-  for (uint32_t e = threadIdx.x; e < ns; e += blockDim.x) {
-    uint32_t w0 = 0, w1 = 0;
-    if constexpr (VALS) {
-      const uint2 v = reinterpret_cast<const uint2*>(sp)[e];
-      w0 = v.x, w1 = v.y;
-    } else {
-      w0 = sp[e];
-    }
+  region_rounds([&](uint32_t w0, uint32_t w1) {
     const uint32_t ql    = w0 >> kSpillRowBits;
     const uint32_t bslot = cnt[ql] + atomicAdd(&cur[ql], 1u);
     if (bslot < a.cap) {
@@ -459,7 +474,7 @@ __device__ inline void flush_hits(int64_t q0, int64_t rbase, int qb, const scree
       a.cand_rows[q * a.cap + bslot] = uint32_t(rbase + (w0 & ((1u << kSpillRowBits) - 1)));
       if constexpr (VALS) { a.cand_vals[q * a.cap + bslot] = __uint_as_float(w1); }
     }
-  }
+  });
 }
 
 /** A workgroup's life by the shader clock and by the constant 100 MHz counter, added to
