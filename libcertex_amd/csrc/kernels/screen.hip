@@ -95,6 +95,7 @@ void screen_kernel(screen_args a)
   __shared__ uint32_t hit_row[ANCHORS ? 1 : kHitCap];
   __shared__ float hit_val[ANCHORS || !R::kValues ? 1 : kHitCap];
   __shared__ uint32_t n_hits;
+  __shared__ uint32_t spill_n[ANCHORS ? 1 : QB];  // entries of each query in the spill region
 
   const val_t* rowc  = static_cast<const val_t*>(a.rowc);
   const val_t* theta = static_cast<const val_t*>(a.theta);
@@ -140,6 +141,7 @@ void screen_kernel(screen_args a)
     for (int e = tid; e < qlive; e += 256) {
       thl[e] = q0 + e < w.q_end ? theta[q0 + e] : R::keep_none();
     }
+    for (int e = tid; e < QB; e += 256) { spill_n[e] = 0; }
   }
   __syncthreads();
 
@@ -279,7 +281,7 @@ void screen_kernel(screen_args a)
             }
           }
           push_hits<BT * 4, FILT, R::kValues>(bits, qloc, w.base + row0, rbase, q0, a, hit_q, hit_row,
-                                              hit_val, &n_hits, uint32_t(kHitCap), v16);
+                                              hit_val, &n_hits, spill_n, uint32_t(kHitCap), v16);
         }
       }
     }
@@ -399,7 +401,7 @@ void screen_kernel(screen_args a)
   if constexpr (!ANCHORS) {
     __syncthreads();
     flush_hits<R::kValues>(q0, rbase, QB, a, hit_q, hit_row, hit_val, &n_hits, uint32_t(kHitCap),
-                           reinterpret_cast<uint32_t*>(qlds));
+                           reinterpret_cast<uint32_t*>(qlds), spill_n);
     clk.stop(a);
   }
 }

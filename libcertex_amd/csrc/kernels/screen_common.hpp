@@ -293,16 +293,18 @@ __device__ __forceinline__ void spill_put(const screen_args& a, int64_t e, uint3
  * Appends the survivors of one 16-query tile of a step to the workgroup's list: `bits` is this
  * lane's survivor mask over NB = 16 or 32 rows (4 or 8 row tiles), `qloc` its query within the
  * workgroup, row0 the stored row of its bit 0, rbase the workgroup's first row (spill entries hold
- * rows as offsets from it), v the screen values of bits 0..15 (used when VALS, NB = 16). The wave reserves all of its survivors with one LDS atomic: each lane's offset is the
- * exclusive prefix of the survivor counts, summed from one ballot per bit of the count. The lanes
- * then write their survivors in as many rounds as the busiest lane has survivors, with no vote or
- * atomic per round. Every lane of the wave must call it.
+ * rows as offsets from it), v the screen values of bits 0..15 (used when VALS, NB = 16), spill_n
+ * (LDS, per query of the workgroup) the count of each query's entries in the spill region. The
+ * wave reserves all of its survivors with one LDS atomic: each lane's offset is the exclusive
+ * prefix of the survivor counts, summed from one ballot per bit of the count. The lanes then write
+ * their survivors in as many rounds as the busiest lane has survivors, with no vote or atomic per
+ * round. Every lane of the wave must call it.
  */
 template <int NB, bool FILT, bool VALS, typename V>
 __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t row0, int64_t rbase,
                                           int64_t q0, const screen_args& a, uint32_t* hit_q,
                                           uint32_t* hit_row, float* hit_val, uint32_t* n_hits,
-                                          uint32_t cap, const V (&v)[16])
+                                          uint32_t* spill_n, uint32_t cap, const V (&v)[16])
 {
   static_assert(NB == 16 || NB == 32, "16 or 32 rows per lane");
   static_assert(!VALS || NB == 16, "screen values come with 4 row tiles");
@@ -376,6 +378,7 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
   }
   const int64_t e0 = int64_t(blockIdx.x) * a.spill_cap - int64_t(cap);
   if (first >= cap && int64_t(first - cap) + total <= a.spill_cap) {
+    if (cnt != 0) { atomicAdd(&spill_n[qloc], cnt); }
     each([&](uint32_t d, float val) { spill_put<VALS>(a, e0 + pos, qloc, roff0 + d, val); });
     return;
   }
@@ -385,6 +388,7 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
       hit_row[pos] = uint32_t(row0) + d;
       if constexpr (VALS) { hit_val[pos] = val; }
     } else if (int64_t(pos - cap) < a.spill_cap) {
+      atomicAdd(&spill_n[qloc], 1u);
       spill_put<VALS>(a, e0 + pos, qloc, roff0 + d, val);
     } else {
       const int64_t q   = q0 + qloc;
@@ -403,13 +407,15 @@ __device__ __forceinline__ void push_hits(uint32_t bits, uint32_t qloc, int64_t 
  * region past it. Each LDS entry's rank among its query's survivors comes from an LDS counter
  * (cnt), the region's entries follow the query's LDS entries (cursor cur); then one global atomic
  * per query reserves the query's slots. `scratch` holds 2 qb + cap words of LDS (the query rows'
- * space); rbase is the workgroup's first row (spill_put). Records the workgroup's count past the
- * LDS list in spill_need.
+ * space); rbase is the workgroup's first row (spill_put); spill_n, when given, the count of each
+ * query's region entries (push_hits), so that the region is read once. Records the workgroup's
+ * count past the LDS list in spill_need.
  */
 template <bool VALS>
 __device__ inline void flush_hits(int64_t q0, int64_t rbase, int qb, const screen_args& a, const uint32_t* hit_q,
                                   const uint32_t* hit_row, const float* hit_val,
-                                  const uint32_t* n_hits, uint32_t cap, uint32_t* scratch)
+                                  const uint32_t* n_hits, uint32_t cap, uint32_t* scratch,
+                                  const uint32_t* spill_n = nullptr)
 {
   uint32_t* cnt        = scratch;           // [qb] survivors per query, then their first slot
   uint32_t* cur        = scratch + qb;      // [qb] the next rank of a region entry per query
@@ -424,7 +430,10 @@ __device__ inline void flush_hits(int64_t q0, int64_t rbase, int qb, const scree
   __syncthreads();
   for (uint32_t e = threadIdx.x; e < nh; e += blockDim.x) { rank[e] = atomicAdd(&cnt[hit_q[e]], 1u); }
   __syncthreads();
-  for (int e = threadIdx.x; e < qb; e += blockDim.x) { cur[e] = cnt[e]; }
+  for (int e = threadIdx.x; e < qb; e += blockDim.x) {
+    cur[e] = cnt[e];
+    if (spill_n != nullptr) { cnt[e] += spill_n[e]; }
+  }
   __syncthreads();
   const uint32_t* sp   = a.spill + region * spill_words(VALS);
   // the region's entries, SB per thread and round: their loads are in flight together
@@ -451,8 +460,10 @@ __device__ inline void flush_hits(int64_t q0, int64_t rbase, int qb, const scree
       }
     }
   };
-  region_rounds([&](uint32_t w0, uint32_t) { atomicAdd(&cnt[w0 >> kSpillRowBits], 1u); });
-  __syncthreads();
+  if (spill_n == nullptr) {
+    region_rounds([&](uint32_t w0, uint32_t) { atomicAdd(&cnt[w0 >> kSpillRowBits], 1u); });
+    __syncthreads();
+  }
   for (int e = threadIdx.x; e < qb; e += blockDim.x) {
     if (cnt[e] != 0) { cnt[e] = atomicAdd(a.cand_count + q0 + e, cnt[e]); }
   }
