@@ -87,6 +87,7 @@ void screen_kernel(screen_args a)
   static_assert(BT * 4 <= 32, "a lane's survivor mask of one query tile is 32 bits");
   static_assert(!ANCHORS || BT == 4, "the anchor pass runs 64-row steps");
   static_assert(!R::kValues || BT == 4, "screen values travel for 16 rows per query tile");
+  static_assert(QB <= (1 << (32 - kSpillRowBits)), "a spill entry holds the query within the block");
   __shared__ __attribute__((aligned(16))) uint8_t qlds[QB * ROWB];
   __shared__ val_t thl[ANCHORS ? 1 : QB];
   __shared__ val_t gml[ANCHORS ? 4 * QB : 1];

@@ -143,6 +143,7 @@ __global__ __launch_bounds__(64 * kTileWaves, 2) void screen_tile_kernel(screen_
   using S           = tile_shape<RT, QT>;
   static_assert(sizeof(frag_t) == 16 && sizeof(val_t) == 4, "16-byte operands, 4-byte values");
   constexpr int TQ  = S::TQ;
+  static_assert(TQ <= (1 << (32 - kSpillRowBits)), "a spill entry holds the query within the tile");
   constexpr int CA  = kTileRows / 16 / kTileWaves;  // row copies per wave and stage
   constexpr int CB  = TQ / 16 / kTileWaves;         // query copies per wave and stage
   constexpr int NC  = CA + CB;                      // copies per wave and stage
